@@ -1,0 +1,252 @@
+/*
+ * tsk.h — C ABI of the MI355X (gfx950) MM-DiT hot path.
+ *
+ * The entry points mirror the ggml operator nodes that thinksound.cpp's MM-DiT
+ * graph builder emits, so a ggml backend (or any C caller) can hand those nodes
+ * to these kernels 1:1:
+ *
+ *   tsk_mul_mat         <- ggml_mul_mat(ctx, W, x)            src/mmdit.cpp:13, :24
+ *                          (+ the ggml_add bias node of lin()  src/mmdit.cpp:14)
+ *   tsk_flash_attn_ext  <- ggml_flash_attn_ext(ctx,q,k,v,mask,scale,max_bias,softcap)
+ *                          + ggml_flash_attn_ext_set_prec     src/mmdit.cpp:91-92
+ *   tsk_rms_norm_mul    <- ggml_mul(ggml_rms_norm(x, eps), w)  src/mmdit.cpp:78-80
+ *   tsk_rope_ext        <- ggml_rope_ext(..., GGML_ROPE_TYPE_NORMAL, ...) src/mmdit.cpp:96-99
+ *   tsk_qk_norm_rope    <- the chain rms_norm -> mul(w) -> rope_ext of
+ *                          pre_attn                             src/mmdit.cpp:221-223
+ *   tsk_norm            <- ggml_norm(x, eps)                   src/mmdit.cpp:59
+ *   tsk_dit_*           <- ts_dit::load / forward / sample     src/mmdit.h:9-42
+ *
+ * Conventions (all follow ggml):
+ *   - tensors are non-owning views: ne[] = extents with ne[0] fastest,
+ *     nb[] = byte strides, data = DEVICE pointer (tsk_dit_* host entry points
+ *     say so explicitly where they take host memory);
+ *   - type ids use ggml's enum ggml_type numbering;
+ *   - every entry point validates shapes, types, strides and pointers on the
+ *     host BEFORE any launch and returns a negative tsk_status instead of
+ *     aborting (ggml would GGML_ASSERT);
+ *   - kernels are enqueued on the given stream (a hipStream_t; NULL = the
+ *     null stream) and are not synchronised; entry points are reentrant per
+ *     stream.
+ */
+#ifndef TSK_TSK_H
+#define TSK_TSK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (values of ggml's enum ggml_type). */
+enum tsk_type {
+    TSK_TYPE_F32  = 0,
+    TSK_TYPE_F16  = 1,
+    TSK_TYPE_Q8_0 = 8,   /* blocks of {fp16 d; int8 qs[32]} (34 bytes) along ne[0] */
+    TSK_TYPE_I32  = 26,
+    TSK_TYPE_BF16 = 30,
+    /* Extension (no ggml counterpart): Q8_0 weights repacked once for the GPU
+     * by tsk_q8_0_repack. Same values as TSK_TYPE_Q8_0, split into two planes:
+     * int8 qs[ne1][ne0] followed by fp16 d[ne1][ne0/32]; nb[] are ignored. */
+    TSK_TYPE_Q8_0_SPLIT = 0x1008
+};
+
+/* ggml_prec values (ggml_flash_attn_ext_set_prec). */
+enum tsk_prec {
+    TSK_PREC_DEFAULT = 0,
+    TSK_PREC_F32     = 10
+};
+
+/* ggml_rope_type: only NORMAL (adjacent pairs) is on the MM-DiT path. */
+enum tsk_rope_mode {
+    TSK_ROPE_TYPE_NORMAL = 0
+};
+
+enum tsk_status {
+    TSK_OK               = 0,
+    TSK_ERR_INVALID_ARG  = -1,  /* null pointer, bad scalar argument      */
+    TSK_ERR_TYPE         = -2,  /* element type not supported             */
+    TSK_ERR_SHAPE        = -3,  /* ne[] inconsistent between operands     */
+    TSK_ERR_STRIDE       = -4,  /* nb[] layout not supported              */
+    TSK_ERR_ALIGN        = -5,  /* pointer / row alignment not supported  */
+    TSK_ERR_UNSUPPORTED  = -6,  /* valid ggml node this library does not run */
+    TSK_ERR_NOT_INIT     = -7,  /* tsk_init was not called                */
+    TSK_ERR_HIP          = -8,  /* a HIP runtime call failed              */
+    TSK_ERR_NOMEM        = -9   /* device allocation failed               */
+};
+
+typedef struct tsk_tensor {
+    int32_t type;      /* enum tsk_type                          */
+    int64_t ne[4];     /* extents, ne[0] fastest                 */
+    size_t  nb[4];     /* byte strides (nb[0] = element/block size) */
+    void   *data;      /* device pointer                         */
+} tsk_tensor;
+
+typedef void *tsk_stream;   /* hipStream_t */
+
+/* ---- library ---------------------------------------------------------- */
+
+/* Select the HIP device and create per-device state. Idempotent. */
+int         tsk_init(int device);
+/* Release library-owned device memory (workspaces). */
+int         tsk_shutdown(void);
+/* Text for a tsk_status value. */
+const char *tsk_status_string(int status);
+/* Detail of the last error reported on the calling thread ("" if none). */
+const char *tsk_last_error(void);
+/* Library version string. */
+const char *tsk_version(void);
+
+/* ---- operators -------------------------------------------------------- */
+
+/*
+ * dst = a x b (+ bias), ggml_mul_mat semantics.
+ *   a    : weight, ne = [K, M, 1, 1]; F32, F16, BF16, Q8_0 or Q8_0_SPLIT.
+ *          Rows must be contiguous (nb[0] = element/block size).
+ *   b    : activations, ne = [K, N, n2, n3]; F32 (or BF16), rows contiguous.
+ *          As in ggml, b is first converted to a's vec_dot type: BF16 weights
+ *          round b to bf16 (RNE); Q8_0 weights quantize b per 32-block to Q8_0
+ *          (amax/127 scale, round-to-nearest-even); F16 weights round to fp16.
+ *   bias : nullable, F32 ne = [M]; fused ggml_add broadcast over N.
+ *   dst  : F32 (or BF16), ne = [M, N, n2, n3]; rows contiguous.
+ * K must be a multiple of 32 for Q8_0 (ggml block) and of 8 otherwise.
+ */
+int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias,
+                tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * ggml_flash_attn_ext semantics (non-causal, online softmax):
+ *   q    : ne = [D, Nq, H, B]   F32, F16 or BF16
+ *   k    : ne = [D, Nkv, Hkv, B] F32, F16 or BF16   (H % Hkv == 0)
+ *   v    : ne = [D, Nkv, Hkv, B] same type as k
+ *   mask : nullable, F16 (or F32) ne = [Nkv, >=Nq, m2, m3]; added as
+ *          slope*mask; broadcast over heads/batch when m2 | H, m3 | B.
+ *   dst  : F32 (or BF16) ne = [D, H, Nq, B]  (ggml's permuted result)
+ * D must be 64. Q is converted to K's type as ggml-cpu does (F16/BF16 K);
+ * products are exact, logits/softmax/accumulation are fp32; V of a 16-bit
+ * type is used as fp16 in the P.V product (the same cast mmdit.cpp:89-90
+ * applies before the node). With F32 K/V everything is fp32.
+ * prec: TSK_PREC_DEFAULT or TSK_PREC_F32 (both run fp32 softmax).
+ */
+int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
+                       const tsk_tensor *mask, float scale, float max_bias,
+                       float logit_softcap, int prec, tsk_tensor *dst,
+                       tsk_stream stream);
+
+/* dst = rms_norm(x, eps) * w   over ne[0] of x (F32/BF16 in, same type out);
+ * w F32 ne = [ne0]. */
+int tsk_rms_norm_mul(const tsk_tensor *x, const tsk_tensor *w, float eps,
+                     tsk_tensor *dst, tsk_stream stream);
+
+/* dst = layer norm (no affine) of x over ne[0], eps as ggml_norm. F32/BF16. */
+int tsk_norm(const tsk_tensor *x, float eps, tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * ggml_rope_ext, mode NORMAL, on x ne = [n_dims_total, n_head, S, B] F32/BF16
+ * with pos I32 ne = [S]. theta_i = pos * freq_base^(-2i/n_dims) built by the
+ * same running product as ggml-cpu's rope cache, times freq_scale.
+ * ext_factor must be 0 and attn_factor 1 (the MM-DiT call, mmdit.cpp:98).
+ */
+int tsk_rope_ext(const tsk_tensor *x, const tsk_tensor *pos, int n_dims, int mode,
+                 float freq_base, float freq_scale, float ext_factor,
+                 float attn_factor, tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * Fused pre_attn prologue: dst = rope_ext(rms_norm(x, eps) * w, pos) with
+ * pos == NULL meaning "no RoPE" (text stream, mmdit.cpp:223).
+ * x ne = [64, n_head, S, B] F32/BF16, w F32 [64]; dst F32/BF16 same shape.
+ */
+int tsk_qk_norm_rope(const tsk_tensor *x, const tsk_tensor *w, const tsk_tensor *pos,
+                     float eps, int n_dims, float freq_base, float freq_scale,
+                     tsk_tensor *dst, tsk_stream stream);
+
+/* Quantize F32 rows (ne0 % 32 == 0) to Q8_0 with ggml-cpu's x86 rounding
+ * (d = amax/127 stored fp16, q = rne(x*127/amax)). dst type Q8_0. */
+int tsk_q8_0_quantize(const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream);
+/* Dequantize Q8_0 or Q8_0_SPLIT to F32: y = fp32(d) * q (exact). */
+int tsk_q8_0_dequantize(const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream);
+/* Repack ggml Q8_0 blocks into the TSK_TYPE_Q8_0_SPLIT planes (bit-preserving).
+ * dst->data must hold ne1*ne0 + 2*ne1*(ne0/32) bytes. */
+int tsk_q8_0_repack(const tsk_tensor *src, tsk_tensor *dst, tsk_stream stream);
+/* Bytes a Q8_0_SPLIT tensor of ne = [K, M] occupies. */
+size_t tsk_q8_0_split_nbytes(int64_t K, int64_t M);
+
+/* ggml_op ids used by tsk_supports_op (values of ggml's enum ggml_op are not
+ * stable across ggml revisions, so these are this library's own). */
+enum tsk_op {
+    TSK_OP_MUL_MAT        = 1,
+    TSK_OP_FLASH_ATTN_EXT = 2,
+    TSK_OP_RMS_NORM_MUL   = 3,
+    TSK_OP_ROPE_EXT       = 4,
+    TSK_OP_NORM           = 5
+};
+/* Mirror of a ggml backend's supports_op: 1 if tsk would run the node with
+ * these operand descriptors (data pointers are not inspected), else 0.
+ * srcs follow the argument order of the matching entry point. */
+int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs,
+                    const tsk_tensor *dst);
+
+/* ---- MM-DiT step driver (counterpart of ts_dit, src/mmdit.h:9-42) ------ */
+
+typedef struct tsk_dit tsk_dit;
+
+enum tsk_mlp_kind {
+    TSK_MLP_GELU_TANH = 0   /* Linear(d, r*d) -> GELU(tanh) -> Linear(r*d, d) */
+};
+
+typedef struct tsk_dit_config {
+    int   hidden;        /* 1024 */
+    int   n_head;        /* 16   */
+    int   head_dim;      /* 64   */
+    int   depth;         /* 21 = joint + fused */
+    int   fused_depth;   /* 14   */
+    int   latent_dim;    /* 64   */
+    int   text_seq;      /* 77   */
+    int   mlp_hidden;    /* 4096 */
+    int   mlp_kind;      /* enum tsk_mlp_kind */
+    int   weight_type;   /* TSK_TYPE_BF16 (only weight type of the DiT driver) */
+    int   max_batch;     /* capacity: batch rows per forward (2 for CFG) */
+    int   max_latent;    /* capacity: latent tokens T                    */
+    float rope_theta;    /* 10000 */
+    float t_max_period;  /* 1     */
+    float ln_eps;        /* 1e-5  (mmdit.cpp:59)  */
+    float qk_eps;        /* 1e-6  (mmdit.cpp:10)  */
+} tsk_dit_config;
+
+/* Fill the 9 s / 30 s MM-DiT defaults above. */
+void tsk_dit_default_config(tsk_dit_config *cfg);
+/* Allocate device state for cfg (weights are zero until set). */
+int  tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out);
+void tsk_dit_destroy(tsk_dit *dit);
+/* Number of named weight tensors and the i-th name / ggml shape. */
+int  tsk_dit_n_tensors(const tsk_dit *dit);
+int  tsk_dit_tensor_info(const tsk_dit *dit, int i, const char **name, int64_t ne[4]);
+/* Upload one named weight from HOST f32 data (converted to the weight type). */
+int  tsk_dit_set_tensor(tsk_dit *dit, const char *name, const float *host_f32,
+                        int64_t n_elements);
+/*
+ * One flow evaluation for B (<= max_batch) rows, all pointers HOST:
+ *   latent [B, T, latent_dim], t [B], text [B, text_seq, hidden]
+ *   -> flow [B, T, latent_dim].
+ */
+int  tsk_dit_forward(tsk_dit *dit, int B, int T, const float *latent, const float *t,
+                     const float *text, float *flow, tsk_stream stream);
+/* Same with DEVICE pointers (f32), no host synchronisation. */
+int  tsk_dit_forward_device(tsk_dit *dit, int B, int T, const float *latent_d,
+                            const float *t_d, const float *text_d, float *flow_d,
+                            tsk_stream stream);
+/*
+ * Rectified-flow Euler sampler with CFG (ts_dit::sample, mmdit.cpp:344-376),
+ * cond/uncond batched as B=2 per step. HOST pointers:
+ *   noise [T, latent_dim], text_cond / text_uncond [text_seq, hidden]
+ *   -> out [T, latent_dim]; flow0 (nullable) = CFG velocity of step 0.
+ */
+int  tsk_dit_sample(tsk_dit *dit, int T, const float *noise, const float *text_cond,
+                    const float *text_uncond, int steps, float cfg_scale,
+                    float *out, float *flow0, tsk_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSK_TSK_H */

@@ -1,0 +1,290 @@
+"""ctypes front end of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker that the HIP path is compared against
+and the timed CPU baseline of bench.py. Nothing in the product imports it.
+
+Arrays follow numpy C order, i.e. the reverse of ggml's ne[]: a ggml tensor
+ne = [D, N, H, B] is a numpy array of shape (B, H, N, D). 16-bit float types
+are passed as numpy float16 (F16) or as uint16 bit patterns (BF16).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
+Q8_CPU_SIMD, Q8_CPU_REF, Q8_GGUF_PY = 0, 1, 2
+
+
+class TskTensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
+
+
+class DitConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq",
+        "mlp_hidden", "mlp_kind", "weight_type", "max_batch", "max_latent")] + \
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
+
+
+_lib = None
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER(TskTensor)
+        L.orc_mul_mat.argtypes = [P, P, P, P]
+        L.orc_flash_attn_ext.argtypes = [P, P, P, P, ctypes.c_float, ctypes.c_float,
+                                         ctypes.c_float, ctypes.c_int, P]
+        L.orc_rms_norm_mul.argtypes = [P, ctypes.c_void_p, ctypes.c_float, P]
+        L.orc_norm.argtypes = [P, ctypes.c_float, P]
+        L.orc_rope_ext.argtypes = [P, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
+                                   ctypes.c_float, P]
+        L.orc_quantize_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                        ctypes.c_int]
+        L.orc_dequantize_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.orc_fp32_to_fp16.restype = ctypes.c_uint16
+        L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.orc_fp16_to_fp32.restype = ctypes.c_float
+        L.orc_fp32_to_bf16.argtypes = [ctypes.c_float]
+        L.orc_fp32_to_bf16.restype = ctypes.c_uint16
+        for nm in ("orc_fp32_to_fp16_row", "orc_fp16_to_fp32_row",
+                   "orc_fp32_to_bf16_row", "orc_bf16_to_fp32_row"):
+            getattr(L, nm).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_dit_create.argtypes = [ctypes.POINTER(DitConfig)]
+        L.orc_dit_create.restype = ctypes.c_void_p
+        L.orc_dit_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_dit_set_tensor.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p,
+                                         ctypes.c_int64]
+        L.orc_dit_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        L.orc_dit_sample.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+# ---------------------------------------------------------------- conversions
+def f32_to_f16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_fp32_to_fp16_row(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def f16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().orc_fp16_to_fp32_row(h.ctypes.data, y.ctypes.data, h.size)
+    return y
+
+
+def f32_to_bf16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_fp32_to_bf16_row(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def bf16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().orc_bf16_to_fp32_row(h.ctypes.data, y.ctypes.data, h.size)
+    return y
+
+
+# ---------------------------------------------------------------- tensors
+def tensor(arr, ttype):
+    """tsk_tensor view of a C-contiguous numpy array (shape reversed to ne)."""
+    assert arr.flags["C_CONTIGUOUS"]
+    t = TskTensor()
+    t.type = ttype
+    shape = list(arr.shape)[::-1]
+    strides = list(arr.strides)[::-1]
+    if ttype == Q8_0:
+        # arr is (rows, K/32, 34) uint8 -> ne = [K, rows]
+        rows, nblk = arr.shape[0], arr.shape[1]
+        shape = [nblk * 32, rows]
+        strides = [34, nblk * 34]
+    while len(shape) < 4:
+        shape.append(1)
+        strides.append(strides[-1] * (shape[-2] if len(shape) > 1 else 1))
+    for i in range(4):
+        t.ne[i] = shape[i]
+        t.nb[i] = strides[i]
+    t.data = arr.ctypes.data
+    return t
+
+
+def _ttype(arr, bf16):
+    if arr.dtype == np.float32:
+        return F32
+    if arr.dtype == np.float16:
+        return F16
+    if arr.dtype == np.uint16 and bf16:
+        return BF16
+    raise TypeError(arr.dtype)
+
+
+# ---------------------------------------------------------------- Q8_0
+def quantize_q8_0(x, mode=Q8_CPU_SIMD):
+    """(..., K) float32 -> (rows, K/32, 34) uint8 ggml block_q8_0 bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    rows = x.size // K
+    out = np.empty((rows, K // 32, 34), dtype=np.uint8)
+    lib().orc_quantize_q8_0(x.ctypes.data, out.ctypes.data, x.size, mode)
+    return out
+
+
+def dequantize_q8_0(blocks):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    rows, nb = blocks.shape[0], blocks.shape[1]
+    y = np.empty((rows, nb * 32), dtype=np.float32)
+    lib().orc_dequantize_q8_0(blocks.ctypes.data, y.ctypes.data, rows * nb * 32)
+    return y
+
+
+# ---------------------------------------------------------------- ops
+def mul_mat(a, b, bias=None, a_type=None):
+    """ggml_mul_mat: a is (M, K) weights (F32/F16/BF16-bits or Q8_0 blocks),
+    b is (..., N, K) float32 -> (..., N, M) float32."""
+    a = np.ascontiguousarray(a)
+    if a_type is None:
+        a_type = _ttype(a, False)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    M = a.shape[0]
+    out = np.empty(b.shape[:-1] + (M,), dtype=np.float32)
+    ta, tb, td = tensor(a, a_type), tensor(b, F32), tensor(out, F32)
+    tbias = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        tbias = ctypes.byref(tensor(bias, F32))
+    rc = lib().orc_mul_mat(ctypes.byref(ta), ctypes.byref(tb), tbias, ctypes.byref(td))
+    assert rc == 0, rc
+    return out
+
+
+def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0,
+                   vacc_f16=False, kv_bf16=False, q_bf16=False):
+    """q (B,H,Nq,D), k/v (B,Hkv,Nkv,D) -> (B,Nq,H,D) float32 (ggml permuted)."""
+    # keep the contiguous copies alive: tensors hold raw pointers
+    q, k, v = (np.ascontiguousarray(a) for a in (q, k, v))
+    B, H, Nq, D = q.shape
+    out = np.empty((B, Nq, H, v.shape[-1]), dtype=np.float32)
+    tq = tensor(q, _ttype(q, q_bf16))
+    tk = tensor(k, _ttype(k, kv_bf16))
+    tv = tensor(v, _ttype(v, kv_bf16))
+    tm = None
+    if mask is not None:
+        mask = np.ascontiguousarray(mask)
+        tm = ctypes.byref(tensor(mask, _ttype(mask, False)))
+    td = tensor(out, F32)
+    rc = lib().orc_flash_attn_ext(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv), tm,
+                                  scale, max_bias, softcap, int(vacc_f16), ctypes.byref(td))
+    assert rc == 0, rc
+    return out
+
+
+def rms_norm_mul(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    wp = None
+    if w is not None:
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        wp = w.ctypes.data
+    rc = lib().orc_rms_norm_mul(ctypes.byref(tensor(x, F32)), wp, eps, ctypes.byref(tensor(out, F32)))
+    assert rc == 0
+    return out
+
+
+def norm(x, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    rc = lib().orc_norm(ctypes.byref(tensor(x, F32)), eps, ctypes.byref(tensor(out, F32)))
+    assert rc == 0
+    return out
+
+
+def rope_ext(x, pos, n_dims, freq_base=10000.0, freq_scale=1.0):
+    """x (B, S, H, D) float32 (ggml ne [D, H, S, B]), pos int32 (S,)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    out = np.empty_like(x)
+    rc = lib().orc_rope_ext(ctypes.byref(tensor(x, F32)), pos.ctypes.data, n_dims, freq_base,
+                            freq_scale, ctypes.byref(tensor(out, F32)))
+    assert rc == 0
+    return out
+
+
+# ---------------------------------------------------------------- MM-DiT
+def dit_config(**kw):
+    c = DitConfig(hidden=1024, n_head=16, head_dim=64, depth=21, fused_depth=14, latent_dim=64,
+                  text_seq=77, mlp_hidden=4096, mlp_kind=0, weight_type=BF16, max_batch=2,
+                  max_latent=646, rope_theta=10000.0, t_max_period=1.0, ln_eps=1e-5, qk_eps=1e-6)
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+class OracleDiT:
+    def __init__(self, cfg):
+        self.cfg = cfg
+        self.h = lib().orc_dit_create(ctypes.byref(cfg))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_dit_destroy(self.h)
+            self.h = None
+
+    def set_tensor(self, name, arr):
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        rc = lib().orc_dit_set_tensor(self.h, name.encode(), arr.ctypes.data, arr.size)
+        assert rc == 0, (name, rc)
+
+    def forward(self, latent, t, text, act_bf16=True, kv_f16=True):
+        latent = np.ascontiguousarray(latent, dtype=np.float32)
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        text = np.ascontiguousarray(text, dtype=np.float32)
+        B, T, L = latent.shape
+        flow = np.empty((B, T, L), dtype=np.float32)
+        rc = lib().orc_dit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data,
+                                   text.ctypes.data, flow.ctypes.data, int(act_bf16), int(kv_f16))
+        assert rc == 0
+        return flow
+
+    def sample(self, noise, text_cond, text_uncond, steps=24, cfg_scale=5.0, act_bf16=True,
+               kv_f16=True):
+        noise = np.ascontiguousarray(noise, dtype=np.float32)
+        text_cond = np.ascontiguousarray(text_cond, dtype=np.float32)
+        text_uncond = np.ascontiguousarray(text_uncond, dtype=np.float32)
+        T, L = noise.shape
+        out = np.empty((T, L), dtype=np.float32)
+        flow0 = np.empty((T, L), dtype=np.float32)
+        rc = lib().orc_dit_sample(self.h, T, noise.ctypes.data, text_cond.ctypes.data,
+                                  text_uncond.ctypes.data, steps, cfg_scale, out.ctypes.data,
+                                  flow0.ctypes.data, int(act_bf16), int(kv_f16))
+        assert rc == 0
+        return out, flow0

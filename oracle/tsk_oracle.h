@@ -1,0 +1,93 @@
+/*
+ * tsk_oracle.h — CPU restatement of the ggml-cpu arithmetic behind the
+ * thinksound.cpp MM-DiT hot path.  TEST INFRASTRUCTURE ONLY: this is the
+ * checker the HIP path is compared against (and the timed CPU baseline). The
+ * product library never links or calls it.
+ *
+ * The arithmetic being restated lives in ggml (github.com/ggml-org/ggml), an
+ * un-vendored submodule of the reference (.gitmodules:1-3); the published
+ * numbers were made with the ggml of llama.cpp commit 911b67a60
+ * (docs/PROGRESS.md:17). ggml is absent from this container, so each function
+ * restates ggml's published algorithm and cites the reference call site that
+ * emits the node. Tensors use ggml's ne/nb conventions (tsk_tensor) with HOST
+ * data pointers.
+ */
+#ifndef TSK_ORACLE_H
+#define TSK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "../include/tsk/tsk.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* threads used by the parallel loops below (default 1) */
+void     orc_set_threads(int n);
+int      orc_get_threads(void);
+
+/* scalar conversions, round-to-nearest-even (ggml GGML_FP32_TO_FP16 / _BF16) */
+uint16_t orc_fp32_to_fp16(float f);
+float    orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_bf16(float f);
+float    orc_bf16_to_fp32(uint16_t h);
+void     orc_fp32_to_fp16_row(const float *x, uint16_t *y, int64_t n);
+void     orc_fp16_to_fp32_row(const uint16_t *x, float *y, int64_t n);
+void     orc_fp32_to_bf16_row(const float *x, uint16_t *y, int64_t n);
+void     orc_bf16_to_fp32_row(const uint16_t *x, float *y, int64_t n);
+
+/* Q8_0 (34-byte blocks {fp16 d; int8 qs[32]}) */
+enum orc_q8_mode {
+    ORC_Q8_CPU_SIMD = 0,  /* ggml-cpu x86 quantize_row_q8_0: d=amax/127, q=rne(x*127/amax) */
+    ORC_Q8_CPU_REF  = 1,  /* quantize_row_q8_0_ref: q=roundf(x*(1/d)) (half away)        */
+    ORC_Q8_GGUF_PY  = 2   /* gguf-py quants.Q8_0: q=roundf(x/d) (half away)               */
+};
+void     orc_quantize_q8_0(const float *x, void *blocks, int64_t n, int mode);
+void     orc_dequantize_q8_0(const void *blocks, float *y, int64_t n);
+
+/* ggml_mul_mat: dst[M,N,..] = a[K,M] x b[K,N,..] (+bias[M]); dst F32. */
+int      orc_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias,
+                     tsk_tensor *dst);
+
+/* ggml_flash_attn_ext (ggml-cpu one-row-at-a-time online softmax).
+ * vacc_f16 = 1 reproduces ggml-cpu's fp16 V accumulator for F16 V; 0 keeps
+ * the accumulator in fp64 (exact reference for the same rounded inputs). */
+int      orc_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
+                            const tsk_tensor *mask, float scale, float max_bias,
+                            float logit_softcap, int vacc_f16, tsk_tensor *dst);
+
+/* ggml_rms_norm followed by ggml_mul with w (w may be NULL). F32 only. */
+int      orc_rms_norm_mul(const tsk_tensor *x, const float *w, float eps, tsk_tensor *dst);
+/* ggml_norm (no affine). F32 only. */
+int      orc_norm(const tsk_tensor *x, float eps, tsk_tensor *dst);
+/* ggml_rope_ext NORMAL mode, ext_factor 0, attn_factor 1. F32 only. */
+int      orc_rope_ext(const tsk_tensor *x, const int32_t *pos, int n_dims, float freq_base,
+                      float freq_scale, tsk_tensor *dst);
+
+/* elementwise helpers used by the DiT restatement */
+float    orc_silu(float x);
+float    orc_gelu_tanh(float x);
+
+/* ---- MM-DiT flow step (BASELINE textbook configuration) ------------------
+ * Structure of ts_dit::forward (src/mmdit.cpp:119-342) with the benchmarked
+ * block shape: linear layers, GELU(tanh) MLP, two streams (latent, text),
+ * adaLN from the timestep embedding. Weights are given by name as host F32
+ * arrays (already rounded the way the device holds them). */
+typedef struct orc_dit orc_dit;
+orc_dit *orc_dit_create(const tsk_dit_config *cfg);
+void     orc_dit_destroy(orc_dit *d);
+int      orc_dit_set_tensor(orc_dit *d, const char *name, const float *src, int64_t n);
+/* act_bf16 = 1 rounds every mul_mat activation to bf16 (ggml's BF16-weight
+ * path); 0 keeps activations F32 (the "GGML F32 path").  kv_f16 = 1 casts K/V
+ * to F16 before attention as mmdit.cpp:89-90 does. */
+int      orc_dit_forward(orc_dit *d, int B, int T, const float *latent, const float *t,
+                         const float *text, float *flow, int act_bf16, int kv_f16);
+int      orc_dit_sample(orc_dit *d, int T, const float *noise, const float *text_cond,
+                        const float *text_uncond, int steps, float cfg_scale, float *out,
+                        float *flow0, int act_bf16, int kv_f16);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
