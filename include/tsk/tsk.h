@@ -231,9 +231,11 @@ int  tsk_dit_set_tensor(tsk_dit *dit, const char *name, const float *host_f32,
  */
 int  tsk_dit_forward(tsk_dit *dit, int B, int T, const float *latent, const float *t,
                      const float *text, float *flow, tsk_stream stream);
-/* Same with DEVICE pointers (f32), no host synchronisation. */
+/* Same with DEVICE pointers for latent / text / flow (f32) and the B
+ * timesteps on the HOST (the t-embedding is built on the host in fp32 as
+ * mmdit.cpp:305-314 does); no host synchronisation. */
 int  tsk_dit_forward_device(tsk_dit *dit, int B, int T, const float *latent_d,
-                            const float *t_d, const float *text_d, float *flow_d,
+                            const float *t_host, const float *text_d, float *flow_d,
                             tsk_stream stream);
 /*
  * Rectified-flow Euler sampler with CFG (ts_dit::sample, mmdit.cpp:344-376),

@@ -1,0 +1,405 @@
+// gemm.hip — weight GEMMs of the MM-DiT projections for gfx950
+// (ggml_mul_mat nodes of lin() / conv1d_f32(), src/mmdit.cpp:12-25).
+//
+//   Y[n, m] = epi( sum_k X[n, k] * W[m, k] + bias[m] )
+//
+// BF16 weights: bf16 MFMA 16x16x32, fp32 accumulation; f32 activations are
+// rounded to bf16 (RNE) while staged, which is ggml's conversion of src1 to
+// the weight's vec_dot type.
+// Q8_0 weights: int8 MFMA 16x16x32 = exactly one 32-element Q8_0 block per
+// instruction, so each MFMA yields the exact integer block sum of ggml's
+// vec_dot_q8_0_q8_0; it is scaled by fp32(d_w) * fp32(d_x) into fp32
+// accumulators. Activations were quantized per 32-block beforehand.
+//
+// Tiling: workgroup = WM x WN waves; a wave owns TM x TN 16x16 tiles with
+// A = W rows (output features) and B = X rows (tokens), so each lane ends up
+// with 4 consecutive output features of one token (16-B stores). Operand
+// tiles are double buffered through LDS with one barrier per K step.
+#include "tsk_common.h"
+#include "tsk_internal.h"
+
+namespace tsk {
+
+namespace {
+
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+    // 0.5 x (1 + tanh(u)), tanh(u) = 1 - 2 / (exp(2u) + 1)
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    const float t = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
+    return 0.5f * x * (1.0f + t);
+}
+
+template <int EPI, bool YBF16>
+__device__ __forceinline__ void epilogue4(const GemmParams &p, int m0, int n, f32x4 v) {
+    if (n >= p.N || m0 >= p.M) return;
+    const bool full = m0 + 3 < p.M;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+        if (full) { f32x4 t = *(const f32x4 *) (p.bias + m0); bv[0] = t[0]; bv[1] = t[1]; bv[2] = t[2]; bv[3] = t[3]; }
+        else for (int r = 0; r < 4 && m0 + r < p.M; ++r) bv[r] = p.bias[m0 + r];
+    }
+    float o[4];
+    for (int r = 0; r < 4; ++r) o[r] = v[r] + bv[r];
+    if constexpr (EPI == EPI_GELU)
+        for (int r = 0; r < 4; ++r) o[r] = gelu_tanh_f(o[r]);
+    if constexpr (EPI == EPI_GATE_RES) {
+        const float *g = p.gate + (int64_t) (n / p.rows_per_gate) * p.ld_gate + m0;
+        float *rr = p.res + (int64_t) n * p.ld_res + m0;
+        if (full) {
+            f32x4 gg = *(const f32x4 *) g;
+            f32x4 cur = *(f32x4 *) rr;
+            for (int r = 0; r < 4; ++r) cur[r] += gg[r] * o[r];
+            *(f32x4 *) rr = cur;
+        } else {
+            for (int r = 0; r < 4 && m0 + r < p.M; ++r) rr[r] += g[r] * o[r];
+        }
+        return;
+    }
+    if constexpr (YBF16) {
+        uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
+        if (full) {
+            uint16_t t4[4];
+            for (int r = 0; r < 4; ++r) t4[r] = f32_to_bf16_bits(o[r]);
+            u32x2 w;
+            __builtin_memcpy(&w, t4, 8);
+            *(u32x2 *) yr = w;
+        } else {
+            for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+        }
+    } else {
+        float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
+        if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+        else for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+    }
+}
+
+// ------------------------------------------------------------------ BF16
+constexpr int BK = 64;
+constexpr int LDSB = BK + 8;   // bf16 elements per LDS row (144 B)
+
+template <int WM, int WN, int TM, int TN, bool XF32, int EPI, bool YBF16>
+__global__ __launch_bounds__(WM * WN * 64)
+void gemm_bf16_kernel(const GemmParams p) {
+    constexpr int NT = WM * WN * 64;
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int WCH = BM * (BK / 8), XCH = BN * (BK / 8);   // 16-B chunks (8 bf16)
+    constexpr int WPER = (WCH + NT - 1) / NT, XPER = (XCH + NT - 1) / NT;
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BM * LDSB];
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BN * LDSB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int wm = wave % WM, wn = wave / WM;
+    const int bm0 = blockIdx.x * BM, bn0 = blockIdx.y * BN;
+    const uint16_t *W = (const uint16_t *) p.w;
+
+    u32x4 wreg[WPER];
+    u32x4 xreg[XPER][XF32 ? 2 : 1];
+    const int nk = (p.K + BK - 1) / BK;
+
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            wreg[i] = u32x4{0, 0, 0, 0};
+            if (c < WCH) {
+                const int row = bm0 + c / (BK / 8), kk = k0 + (c % (BK / 8)) * 8;
+                if (row < p.M && kk < p.K) wreg[i] = *(const u32x4 *) (W + (int64_t) row * p.ld_w + kk);
+            }
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            xreg[i][0] = u32x4{0, 0, 0, 0};
+            if constexpr (XF32) xreg[i][1] = u32x4{0, 0, 0, 0};
+            if (c < XCH) {
+                const int row = bn0 + c / (BK / 8), kk = k0 + (c % (BK / 8)) * 8;
+                if (row < p.N && kk < p.K) {
+                    if constexpr (XF32) {
+                        const float *xr = (const float *) p.x + (int64_t) row * p.ld_x + kk;
+                        xreg[i][0] = *(const u32x4 *) xr;
+                        xreg[i][1] = *(const u32x4 *) (xr + 4);
+                    } else {
+                        xreg[i][0] = *(const u32x4 *) ((const uint16_t *) p.x + (int64_t) row * p.ld_x + kk);
+                    }
+                }
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            if (c < WCH) *(u32x4 *) &Ws[buf][(c / (BK / 8)) * LDSB + (c % (BK / 8)) * 8] = wreg[i];
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            if (c < XCH) {
+                u32x4 v;
+                if constexpr (XF32) {
+                    const float *f0 = (const float *) &xreg[i][0];
+                    const float *f1 = (const float *) &xreg[i][1];
+                    uint16_t t8[8];
+                    for (int j = 0; j < 4; ++j) { t8[j] = f32_to_bf16_bits(f0[j]); t8[4 + j] = f32_to_bf16_bits(f1[j]); }
+                    __builtin_memcpy(&v, t8, 16);
+                } else {
+                    v = xreg[i][0];
+                }
+                *(u32x4 *) &Xs[buf][(c / (BK / 8)) * LDSB + (c % (BK / 8)) * 8] = v;
+            }
+        }
+    };
+
+    f32x4 acc[TM][TN];
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            bf16x8 a[TM], b[TN];
+            for (int i = 0; i < TM; ++i)
+                a[i] = *(const bf16x8 *) &Ws[buf][((wm * TM + i) * 16 + lr) * LDSB + 32 * kk + 8 * lg];
+            for (int j = 0; j < TN; ++j)
+                b[j] = *(const bf16x8 *) &Xs[buf][((wn * TN + j) * 16 + lr) * LDSB + 32 * kk + 8 * lg];
+            for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) {
+            const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
+            const int n = bn0 + (wn * TN + j) * 16 + lr;
+            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
+        }
+}
+
+// ------------------------------------------------------------------ Q8_0
+constexpr int QBK = 128;            // 4 Q8_0 blocks per K step
+constexpr int LDSQ = QBK + 16;      // bytes per LDS row
+
+template <int WM, int WN, int TM, int TN, int EPI, bool YBF16>
+__global__ __launch_bounds__(WM * WN * 64)
+void gemm_q8_kernel(const GemmParams p) {
+    constexpr int NT = WM * WN * 64;
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int NBK = QBK / 32;
+    constexpr int WCH = BM * (QBK / 16), XCH = BN * (QBK / 16);   // 16-B chunks
+    constexpr int WPER = (WCH + NT - 1) / NT, XPER = (XCH + NT - 1) / NT;
+    __shared__ __attribute__((aligned(16))) int8_t Wq[2][BM * LDSQ];
+    __shared__ __attribute__((aligned(16))) int8_t Xq[2][BN * LDSQ];
+    __shared__ float Wd[2][BM * NBK];
+    __shared__ float Xd[2][BN * NBK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int wm = wave % WM, wn = wave / WM;
+    const int bm0 = blockIdx.x * BM, bn0 = blockIdx.y * BN;
+    const int KB = p.K / 32;
+
+    u32x4 wreg[WPER], xreg[XPER];
+    float wdreg[(BM * NBK + NT - 1) / NT], xdreg[(BN * NBK + NT - 1) / NT];
+    const int nk = (p.K + QBK - 1) / QBK;
+
+    auto gload = [&](int kt) {
+        const int k0 = kt * QBK;
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            wreg[i] = u32x4{0, 0, 0, 0};
+            if (c < WCH) {
+                const int row = bm0 + c / (QBK / 16), kk = k0 + (c % (QBK / 16)) * 16;
+                if (row < p.M && kk < p.K) wreg[i] = *(const u32x4 *) (p.qw + (int64_t) row * p.K + kk);
+            }
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            xreg[i] = u32x4{0, 0, 0, 0};
+            if (c < XCH) {
+                const int row = bn0 + c / (QBK / 16), kk = k0 + (c % (QBK / 16)) * 16;
+                if (row < p.N && kk < p.K) xreg[i] = *(const u32x4 *) (p.qx + (int64_t) row * p.K + kk);
+            }
+        }
+        for (int i = 0; i * NT < BM * NBK; ++i) {
+            const int c = tid + i * NT;
+            wdreg[i] = 0.0f;
+            if (c < BM * NBK) {
+                const int row = bm0 + c / NBK, kb = kt * NBK + c % NBK;
+                if (row < p.M && kb < KB) wdreg[i] = f16_bits_to_f32(p.dw[(int64_t) row * KB + kb]);
+            }
+        }
+        for (int i = 0; i * NT < BN * NBK; ++i) {
+            const int c = tid + i * NT;
+            xdreg[i] = 0.0f;
+            if (c < BN * NBK) {
+                const int row = bn0 + c / NBK, kb = kt * NBK + c % NBK;
+                if (row < p.N && kb < KB) xdreg[i] = p.dx[(int64_t) row * KB + kb];
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            if (c < WCH) *(u32x4 *) &Wq[buf][(c / (QBK / 16)) * LDSQ + (c % (QBK / 16)) * 16] = wreg[i];
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            if (c < XCH) *(u32x4 *) &Xq[buf][(c / (QBK / 16)) * LDSQ + (c % (QBK / 16)) * 16] = xreg[i];
+        }
+        for (int i = 0; i * NT < BM * NBK; ++i) {
+            const int c = tid + i * NT;
+            if (c < BM * NBK) Wd[buf][c] = wdreg[i];
+        }
+        for (int i = 0; i * NT < BN * NBK; ++i) {
+            const int c = tid + i * NT;
+            if (c < BN * NBK) Xd[buf][c] = xdreg[i];
+        }
+    };
+
+    f32x4 acc[TM][TN];
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        for (int kb = 0; kb < NBK; ++kb) {
+            long a[TM], b[TN];
+            f32x4 dwv[TM];
+            float dxv[TN];
+            for (int i = 0; i < TM; ++i) {
+                const int mr = (wm * TM + i) * 16;
+                a[i] = *(const long *) &Wq[buf][(mr + lr) * LDSQ + 32 * kb + 8 * lg];
+                for (int r = 0; r < 4; ++r) dwv[i][r] = Wd[buf][(mr + 4 * lg + r) * NBK + kb];
+            }
+            for (int j = 0; j < TN; ++j) {
+                const int nr = (wn * TN + j) * 16;
+                b[j] = *(const long *) &Xq[buf][(nr + lr) * LDSQ + 32 * kb + 8 * lg];
+                dxv[j] = Xd[buf][(nr + lr) * NBK + kb];
+            }
+            for (int i = 0; i < TM; ++i)
+                for (int j = 0; j < TN; ++j) {
+                    const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], i32x4{0, 0, 0, 0}, 0, 0, 0);
+                    for (int r = 0; r < 4; ++r)
+                        acc[i][j][r] += (float) isum[r] * (dwv[i][r] * dxv[j]);
+                }
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) {
+            const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
+            const int n = bn0 + (wn * TN + j) * 16 + lr;
+            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
+        }
+}
+
+// ------------------------------------------------------------------ activation quantization
+// One thread per 32-block: d = amax/127 (stored as the fp32 value of its fp16
+// rounding), q = rne(x * (127/amax)) — ggml-cpu's x86 quantize_row_q8_0.
+template <bool XF32>
+__global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int K, int8_t *qx, float *dx) {
+    const int KB = K / 32;
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= (int64_t) N * KB) return;
+    const int row = (int) (blk / KB), kb = (int) (blk % KB);
+    float v[32];
+    if constexpr (XF32) {
+        const float *xr = (const float *) x + (int64_t) row * ld_x + kb * 32;
+        for (int j = 0; j < 32; j += 4) {
+            f32x4 t = *(const f32x4 *) (xr + j);
+            v[j] = t[0]; v[j + 1] = t[1]; v[j + 2] = t[2]; v[j + 3] = t[3];
+        }
+    } else {
+        const uint16_t *xr = (const uint16_t *) x + (int64_t) row * ld_x + kb * 32;
+        for (int j = 0; j < 32; ++j) v[j] = bf16_bits_to_f32(xr[j]);
+    }
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    dx[(int64_t) row * KB + kb] = f16_bits_to_f32(f32_to_f16_bits(d));
+    int8_t q[32];
+    for (int j = 0; j < 32; ++j) q[j] = (int8_t) __builtin_rintf(v[j] * id);
+    int8_t *o = qx + (int64_t) row * K + kb * 32;
+    *(u32x4 *) o = *(const u32x4 *) q;
+    *(u32x4 *) (o + 16) = *(const u32x4 *) (q + 16);
+}
+
+// ------------------------------------------------------------------ dispatch
+template <int WM, int WN, int TM, int TN, bool XF32, bool YBF16>
+hipError_t gemm_bf16_epi(const GemmParams &p, hipStream_t s) {
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
+    dim3 block(WM * WN * 64);
+    switch (p.epi) {
+        case EPI_GELU:
+            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GELU, YBF16>), grid, block, 0, s, p);
+            break;
+        case EPI_GATE_RES:
+            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GATE_RES, false>), grid, block, 0, s, p);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_STORE, YBF16>), grid, block, 0, s, p);
+    }
+    return hipGetLastError();
+}
+
+template <bool XF32, bool YBF16>
+hipError_t gemm_bf16_tile(const GemmParams &p, hipStream_t s) {
+    // 64x64 tiles (4 waves of 32x32) unless that leaves most CUs idle
+    const int64_t big = (int64_t) ((p.M + 63) / 64) * ((p.N + 63) / 64);
+    if (big >= 200) return gemm_bf16_epi<2, 2, 2, 2, XF32, YBF16>(p, s);
+    return gemm_bf16_epi<2, 2, 1, 2, XF32, YBF16>(p, s);   // 32 x 64 tiles
+}
+
+template <int WM, int WN, int TM, int TN, bool YBF16>
+hipError_t gemm_q8_epi(const GemmParams &p, hipStream_t s) {
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
+    dim3 block(WM * WN * 64);
+    switch (p.epi) {
+        case EPI_GELU:
+            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_GELU, YBF16>), grid, block, 0, s, p);
+            break;
+        case EPI_GATE_RES:
+            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_GATE_RES, false>), grid, block, 0, s, p);
+            break;
+        default:
+            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_STORE, YBF16>), grid, block, 0, s, p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s) {
+    if (p.x_f32) return p.y_bf16 ? gemm_bf16_tile<true, true>(p, s) : gemm_bf16_tile<true, false>(p, s);
+    return p.y_bf16 ? gemm_bf16_tile<false, true>(p, s) : gemm_bf16_tile<false, false>(p, s);
+}
+
+hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
+    return p.y_bf16 ? gemm_q8_epi<2, 2, 2, 2, true>(p, s) : gemm_q8_epi<2, 2, 2, 2, false>(p, s);
+}
+
+hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K,
+                                   int8_t *qx, float *dx, hipStream_t s) {
+    const int64_t nblk = (int64_t) N * (K / 32);
+    const int threads = 256;
+    dim3 grid((unsigned) ((nblk + threads - 1) / threads));
+    if (x_f32) hipLaunchKernelGGL(quantize_rows_q8_kernel<true>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
+    else hipLaunchKernelGGL(quantize_rows_q8_kernel<false>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
+    return hipGetLastError();
+}
+
+}  // namespace tsk

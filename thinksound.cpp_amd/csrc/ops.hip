@@ -1,0 +1,412 @@
+// ops.hip — memory-bound kernels of the MM-DiT path for gfx950:
+//   rms_norm*w (src/mmdit.cpp:78-80), layer norm (:59), rope NORMAL (:96-99),
+//   the fused QK-RMSNorm+RoPE prologue (:221-223), Q8_0 (de)quantisation and
+//   repacking, and the DiT driver's glue (LN+modulate, QKV split, adaLN GEMV,
+//   CFG/Euler update).
+// One wave (64 lanes) or one 256-thread block per row; rows are streamed once.
+#include "tsk_common.h"
+#include "tsk_internal.h"
+
+namespace tsk {
+
+namespace {
+
+__device__ __forceinline__ float vload(const View4 &v, const char *row, int64_t i) {
+    return v.type == TSK_TYPE_F32 ? ((const float *) row)[i] : bf16_bits_to_f32(((const uint16_t *) row)[i]);
+}
+__device__ __forceinline__ void vstore(const View4 &v, char *row, int64_t i, float x) {
+    if (v.type == TSK_TYPE_F32) ((float *) row)[i] = x;
+    else ((uint16_t *) row)[i] = f32_to_bf16_bits(x);
+}
+__device__ __forceinline__ const char *vrow(const View4 &v, int64_t r) {
+    const int64_t i1 = r % v.ne[1], i2 = (r / v.ne[1]) % v.ne[2], i3 = r / (v.ne[1] * v.ne[2]);
+    return (const char *) v.data + i1 * v.nb[1] + i2 * v.nb[2] + i3 * v.nb[3];
+}
+
+// ggml-cpu's rope cache: theta = p; theta *= theta_scale per pair (running product)
+__device__ __forceinline__ float rope_theta(float p, float theta_scale, int pair) {
+    float th = p;
+    for (int j = 0; j < pair; ++j) th *= theta_scale;
+    return th;
+}
+
+// ---------------------------------------------------------------- rms_norm * w
+__global__ void rms_norm_mul_kernel(const View4 x, const float *w, float eps, const View4 y, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const char *xr = vrow(x, r);
+    char *yr = (char *) vrow(y, r);
+    const int64_t n = x.ne[0];
+    float ss = 0.0f;
+    for (int64_t i = lane; i < n; i += 64) { const float v = vload(x, xr, i); ss += v * v; }
+    ss = wave_sum(ss);
+    const float mean = ss / (float) n;
+    const float sc = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = lane; i < n; i += 64) {
+        float v = vload(x, xr, i) * sc;
+        if (w) v = v * w[i];
+        vstore(y, yr, i, v);
+    }
+}
+
+// ---------------------------------------------------------------- layer norm (no affine)
+__global__ void norm_kernel(const View4 x, float eps, const View4 y, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const char *xr = vrow(x, r);
+    char *yr = (char *) vrow(y, r);
+    const int64_t n = x.ne[0];
+    float s = 0.0f;
+    for (int64_t i = lane; i < n; i += 64) s += vload(x, xr, i);
+    const float mean = wave_sum(s) / (float) n;
+    float s2 = 0.0f;
+    for (int64_t i = lane; i < n; i += 64) { const float v = vload(x, xr, i) - mean; s2 += v * v; }
+    const float var = wave_sum(s2) / (float) n;
+    const float sc = 1.0f / sqrtf(var + eps);
+    for (int64_t i = lane; i < n; i += 64) vstore(y, yr, i, (vload(x, xr, i) - mean) * sc);
+}
+
+// ---------------------------------------------------------------- rope NORMAL
+// x ne = [ne0, n_head, S, B]; pos[i2]. One wave per (i1, i2, i3) row.
+__global__ void rope_kernel(const View4 x, const int32_t *pos, int n_dims, float theta_scale,
+                            float freq_scale, const View4 y, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const int64_t i2 = (r / x.ne[1]) % x.ne[2];
+    const char *xr = vrow(x, r);
+    char *yr = (char *) vrow(y, r);
+    const float p = (float) pos[i2];
+    for (int i = lane; 2 * i < n_dims; i += 64) {
+        const float th = freq_scale * rope_theta(p, theta_scale, i);
+        const float c = cosf(th), sn = sinf(th);
+        const float x0 = vload(x, xr, 2 * i), x1 = vload(x, xr, 2 * i + 1);
+        vstore(y, yr, 2 * i, x0 * c - x1 * sn);
+        vstore(y, yr, 2 * i + 1, x0 * sn + x1 * c);
+    }
+    for (int64_t i = n_dims + lane; i < x.ne[0]; i += 64) vstore(y, yr, i, vload(x, xr, i));
+}
+
+// ---------------------------------------------------------------- fused qk norm + rope
+// x ne = [64, n_head, S, B]; 32 lanes per head vector (one pair each).
+__global__ void qk_norm_rope_kernel(const View4 x, const float *w, const int32_t *pos, float eps,
+                                    int n_dims, float theta_scale, float freq_scale, const View4 y,
+                                    int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32;
+    const int i = threadIdx.x & 31;
+    if (r >= rows) return;
+    const char *xr = vrow(x, r);
+    char *yr = (char *) vrow(y, r);
+    float x0 = vload(x, xr, 2 * i), x1 = vload(x, xr, 2 * i + 1);
+    float ss = x0 * x0 + x1 * x1;
+    for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+    const float sc = 1.0f / sqrtf(ss / 64.0f + eps);
+    x0 = x0 * sc * w[2 * i];
+    x1 = x1 * sc * w[2 * i + 1];
+    if (pos && 2 * i < n_dims) {
+        const int64_t i2 = (r / x.ne[1]) % x.ne[2];
+        const float th = freq_scale * rope_theta((float) pos[i2], theta_scale, i);
+        const float c = cosf(th), sn = sinf(th);
+        const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+        x0 = y0; x1 = y1;
+    }
+    vstore(y, yr, 2 * i, x0);
+    vstore(y, yr, 2 * i + 1, x1);
+}
+
+// ---------------------------------------------------------------- Q8_0 blocks
+struct __attribute__((packed)) BlockQ8 { uint16_t d; int8_t qs[32]; };
+
+__global__ void q8_quantize_blocks_kernel(const float *x, int64_t ld_x, int64_t rows, int64_t K,
+                                          char *blocks, int64_t ld_blocks) {
+    const int64_t KB = K / 32;
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= rows * KB) return;
+    const int64_t row = blk / KB, kb = blk % KB;
+    const float *xr = x + row * ld_x + kb * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(xr[j]));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    BlockQ8 *o = (BlockQ8 *) (blocks + row * ld_blocks) + kb;
+    o->d = f32_to_f16_bits(d);
+    for (int j = 0; j < 32; ++j) o->qs[j] = (int8_t) __builtin_rintf(xr[j] * id);
+}
+
+__global__ void q8_dequantize_kernel(const char *src, int split, int64_t rows, int64_t K, int64_t ld_src,
+                                     float *y, int64_t ld_y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * K) return;
+    const int64_t row = i / K, k = i % K;
+    float d;
+    int q;
+    if (split) {
+        const int8_t *qs = (const int8_t *) src;
+        const uint16_t *ds = (const uint16_t *) (src + rows * K);
+        q = qs[row * K + k];
+        d = f16_bits_to_f32(ds[row * (K / 32) + k / 32]);
+    } else {
+        const BlockQ8 *b = (const BlockQ8 *) (src + row * ld_src) + k / 32;
+        q = b->qs[k % 32];
+        d = f16_bits_to_f32(b->d);
+    }
+    y[row * ld_y + k] = d * (float) q;
+}
+
+__global__ void q8_repack_kernel(const char *src, int64_t ld_src, int64_t rows, int64_t K, char *dst) {
+    const int64_t KB = K / 32;
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= rows * KB) return;
+    const int64_t row = blk / KB, kb = blk % KB;
+    const BlockQ8 *b = (const BlockQ8 *) (src + row * ld_src) + kb;
+    int8_t *qs = (int8_t *) dst + row * K + kb * 32;
+    for (int j = 0; j < 32; ++j) qs[j] = b->qs[j];
+    uint16_t *ds = (uint16_t *) (dst + rows * K);
+    ds[row * KB + kb] = b->d;
+}
+
+__global__ void f32_to_bf16_kernel(const float *x, uint16_t *y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = f32_to_bf16_bits(x[i]);
+}
+
+// ---------------------------------------------------------------- DiT glue
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < (int) (blockDim.x >> 6); ++i) t += red[i];
+    return t;
+}
+
+// one 256-thread block per row; H % 4 == 0
+__global__ __launch_bounds__(256) void ln_modulate_kernel(const float *x, int64_t ld_x, int H, int rows_per_b,
+                                                          const float *shift, const float *scale,
+                                                          int64_t ld_mod, float eps, uint16_t *y, int64_t ld_y) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float *xr = x + (int64_t) r * ld_x;
+    float s = 0.0f;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+        f32x4 v = *(const f32x4 *) (xr + i);
+        s += v[0] + v[1] + v[2] + v[3];
+    }
+    const float mean = block_sum_256(s, red) / (float) H;
+    float s2 = 0.0f;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+        f32x4 v = *(const f32x4 *) (xr + i);
+        for (int j = 0; j < 4; ++j) { const float d = v[j] - mean; s2 += d * d; }
+    }
+    const float var = block_sum_256(s2, red) / (float) H;
+    const float rs = 1.0f / sqrtf(var + eps);
+    const int b = r / rows_per_b;
+    const float *sh = shift + (int64_t) b * ld_mod, *sc = scale + (int64_t) b * ld_mod;
+    uint16_t *yr = y + (int64_t) r * ld_y;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+        f32x4 v = *(const f32x4 *) (xr + i);
+        uint16_t o[4];
+        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits((v[j] - mean) * rs * (sc[i + j] + 1.0f) + sh[i + j]);
+        u32x2 w;
+        __builtin_memcpy(&w, o, 8);
+        *(u32x2 *) (yr + i) = w;
+    }
+}
+
+// qkv row (bf16, [q | k | v] each head-major nh x 64) -> q/k/v [B, nh, Ntot, 64] bf16
+// one 256-thread block per row (nh <= 16 per pass of 8 heads x 32 pairs)
+__global__ __launch_bounds__(256) void qkv_prologue_kernel(const uint16_t *qkv, int S, int nh, const float *qn_w,
+                                                           const float *kn_w, float eps, int rope, float theta_scale,
+                                                           float freq_scale, uint16_t *q, uint16_t *k, uint16_t *v,
+                                                           int Ntot, int tok_off) {
+    const int r = blockIdx.x;
+    const int b = r / S, s = r % S;
+    const int H = nh * 64;
+    const uint16_t *row = qkv + (int64_t) r * 3 * H;
+    const int pair = threadIdx.x & 31, hsub = threadIdx.x >> 5;     // 8 heads per pass
+    float c = 1.0f, sn = 0.0f;
+    if (rope) {
+        const float th = freq_scale * rope_theta((float) s, theta_scale, pair);
+        c = cosf(th);
+        sn = sinf(th);
+    }
+    for (int which = 0; which < 2; ++which) {
+        const uint16_t *src = row + which * H;
+        const float *w = which ? kn_w : qn_w;
+        uint16_t *dst = which ? k : q;
+        for (int h0 = 0; h0 < nh; h0 += 8) {
+            const int h = h0 + hsub;
+            float x0 = 0.0f, x1 = 0.0f;
+            if (h < nh) {
+                const uint32_t two = *(const uint32_t *) (src + h * 64 + 2 * pair);
+                x0 = bf16_bits_to_f32((uint16_t) (two & 0xffff));
+                x1 = bf16_bits_to_f32((uint16_t) (two >> 16));
+            }
+            float ss = x0 * x0 + x1 * x1;
+            for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+            const float sc = 1.0f / sqrtf(ss / 64.0f + eps);
+            x0 = x0 * sc * w[2 * pair];
+            x1 = x1 * sc * w[2 * pair + 1];
+            if (rope) {
+                const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+                x0 = y0; x1 = y1;
+            }
+            if (h < nh) {
+                uint16_t *o = dst + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + 2 * pair;
+                *(uint32_t *) o = (uint32_t) f32_to_bf16_bits(x0) | ((uint32_t) f32_to_bf16_bits(x1) << 16);
+            }
+        }
+    }
+    // v: plain copy, 4 elements per thread
+    const uint16_t *vs = row + 2 * H;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+        const int h = i / 64, d = i % 64;
+        *(u32x2 *) (v + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + d) = *(const u32x2 *) (vs + i);
+    }
+}
+
+// adaLN GEMV list: one wave per output row; c already holds silu(cond), [B][K] f32
+template <int MAXB>
+__global__ __launch_bounds__(256) void adaln_gemv_kernel(const GemvJob *jobs, const float *c, int B, int K) {
+    const GemvJob jb = jobs[blockIdx.y];
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (j >= jb.M) return;
+    const uint16_t *wr = jb.w + (int64_t) j * K;
+    float acc[MAXB];
+    for (int b = 0; b < MAXB; ++b) acc[b] = 0.0f;
+    for (int k = lane * 8; k < K; k += 512) {
+        const u32x4 raw = *(const u32x4 *) (wr + k);
+        const uint16_t *h = (const uint16_t *) &raw;
+        float wv[8];
+        for (int e = 0; e < 8; ++e) wv[e] = bf16_bits_to_f32(h[e]);
+        for (int b = 0; b < MAXB; ++b) {
+            if (b >= B) break;
+            const float *cr = c + (int64_t) b * K + k;
+            const f32x4 c0 = *(const f32x4 *) cr, c1 = *(const f32x4 *) (cr + 4);
+            acc[b] += wv[0] * c0[0] + wv[1] * c0[1] + wv[2] * c0[2] + wv[3] * c0[3] +
+                      wv[4] * c1[0] + wv[5] * c1[1] + wv[6] * c1[2] + wv[7] * c1[3];
+        }
+    }
+    for (int b = 0; b < MAXB; ++b) {
+        if (b >= B) break;
+        const float s = wave_sum(acc[b]);
+        if (lane == 0) jb.out[(int64_t) b * jb.ld_out + j] = s + (jb.bias ? jb.bias[j] : 0.0f);
+    }
+}
+
+__global__ void silu_kernel(float *x, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
+}
+
+__global__ void cfg_euler_kernel(const float *flow2, int64_t n, float cfg, float dt, float *x, float *x2,
+                                 float *flow0) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float fc = flow2[i], fu = flow2[n + i];
+    const float v = fu + (fc - fu) * cfg;
+    if (flow0) flow0[i] = v;
+    const float nx = x[i] + dt * v;
+    x[i] = nx;
+    if (x2) { x2[i] = nx; x2[n + i] = nx; }
+}
+
+inline unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_rms_norm_mul(const View4 &x, const float *w, float eps, const View4 &y, hipStream_t s) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    hipLaunchKernelGGL(rms_norm_mul_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, w, eps, y, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm(const View4 &x, float eps, const View4 &y, hipStream_t s) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    hipLaunchKernelGGL(norm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, eps, y, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const View4 &x, const int32_t *pos, int n_dims, float theta_scale, float freq_scale,
+                       const View4 &y, hipStream_t s) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, pos, n_dims, theta_scale,
+                       freq_scale, y, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(const View4 &x, const float *w, const int32_t *pos, float eps, int n_dims,
+                               float theta_scale, float freq_scale, const View4 &y, hipStream_t s) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(blocks_for(rows, 8)), dim3(256), 0, s, x, w, pos, eps, n_dims,
+                       theta_scale, freq_scale, y, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_quantize_blocks(const float *x, int64_t ld_x, int64_t rows, int64_t K, void *blocks,
+                                     int64_t ld_blocks, hipStream_t s) {
+    hipLaunchKernelGGL(q8_quantize_blocks_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, x, ld_x,
+                       rows, K, (char *) blocks, ld_blocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_dequantize(const void *src, int split, int64_t rows, int64_t K, int64_t ld_src, float *y,
+                                int64_t ld_y, hipStream_t s) {
+    hipLaunchKernelGGL(q8_dequantize_kernel, dim3(blocks_for(rows * K, 256)), dim3(256), 0, s, (const char *) src,
+                       split, rows, K, ld_src, y, ld_y);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_repack(const void *src, int64_t ld_src, int64_t rows, int64_t K, void *dst, hipStream_t s) {
+    hipLaunchKernelGGL(q8_repack_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, (const char *) src,
+                       ld_src, rows, K, (char *) dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_modulate(const float *x, int64_t ld_x, int rows, int H, int rows_per_b, const float *shift,
+                              const float *scale, int64_t ld_mod, float eps, uint16_t *y, int64_t ld_y,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(ln_modulate_kernel, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
+                       ld_mod, eps, y, ld_y);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_prologue(const uint16_t *qkv, int rows, int S, int nh, const float *qn_w, const float *kn_w,
+                               float eps, int rope, float theta_scale, float freq_scale, uint16_t *q, uint16_t *k,
+                               uint16_t *v, int Ntot, int tok_off, hipStream_t s) {
+    hipLaunchKernelGGL(qkv_prologue_kernel, dim3(rows), dim3(256), 0, s, qkv, S, nh, qn_w, kn_w, eps, rope,
+                       theta_scale, freq_scale, q, k, v, Ntot, tok_off);
+    return hipGetLastError();
+}
+
+hipError_t launch_adaln_gemv(const GemvJob *jobs_dev, int njobs, int max_m, const float *c, int B, int K,
+                             hipStream_t s) {
+    dim3 grid(blocks_for(max_m, 4), njobs);
+    if (B <= 2) hipLaunchKernelGGL(adaln_gemv_kernel<2>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
+    else if (B <= 8) hipLaunchKernelGGL(adaln_gemv_kernel<8>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
+    else hipLaunchKernelGGL(adaln_gemv_kernel<32>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_cfg_euler(const float *flow2, int64_t n, float cfg, float dt, float *x, float *x2, float *flow0,
+                            hipStream_t s) {
+    hipLaunchKernelGGL(cfg_euler_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, flow2, n, cfg, dt, x, x2, flow0);
+    return hipGetLastError();
+}
+
+}  // namespace tsk

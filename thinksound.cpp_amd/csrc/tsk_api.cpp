@@ -1,0 +1,536 @@
+// tsk_api.cpp — C ABI of the gfx950 MM-DiT hot path (include/tsk/tsk.h).
+// Every entry point validates its operands on the host and returns a
+// tsk_status; nothing aborts. Kernels are enqueued on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/tsk/tsk.h"
+#include "tsk_internal.h"
+#include "tsk_runtime.h"
+
+using namespace tsk;
+
+namespace tsk {
+
+static thread_local char g_err[512];
+
+int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(TSK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---- per-process device state: one workspace per device, grown on demand
+namespace {
+std::mutex g_mu;
+int g_device = -1;
+struct Workspace { void *ptr = nullptr; size_t size = 0; };
+Workspace g_ws[64];
+}  // namespace
+
+int require_init() {
+    if (g_device < 0) return fail(TSK_ERR_NOT_INIT, "tsk_init() has not been called");
+    return TSK_OK;
+}
+
+int workspace(size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(TSK_ERR_INVALID_ARG, "device id %d out of range", dev);
+    Workspace &w = g_ws[dev];
+    if (w.size < bytes) {
+        // the old buffer may still be read by queued kernels of any stream
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+        if (w.ptr) (void) hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.size = 0;
+        const size_t sz = (bytes + 0xfffff) & ~(size_t) 0xfffff;
+        e = hipMalloc(&w.ptr, sz);
+        if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", sz, hipGetErrorString(e));
+        w.size = sz;
+    }
+    *out = w.ptr;
+    return TSK_OK;
+}
+
+}  // namespace tsk
+
+// ------------------------------------------------------------------ helpers
+namespace {
+
+int elt_size(int type) {
+    switch (type) {
+        case TSK_TYPE_F32: case TSK_TYPE_I32: return 4;
+        case TSK_TYPE_F16: case TSK_TYPE_BF16: return 2;
+        default: return 0;
+    }
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t) p % a) == 0; }
+
+int check_tensor(const tsk_tensor *t, const char *name) {
+    if (!t) return fail(TSK_ERR_INVALID_ARG, "%s is NULL", name);
+    if (!t->data) return fail(TSK_ERR_INVALID_ARG, "%s->data is NULL", name);
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] < 1) return fail(TSK_ERR_SHAPE, "%s->ne[%d] = %lld < 1", name, i, (long long) t->ne[i]);
+    return TSK_OK;
+}
+
+// rows of ne[0] contiguous elements, row stride aligned to `row_align` bytes
+int check_rows(const tsk_tensor *t, const char *name, size_t row_align) {
+    const int es = elt_size(t->type);
+    if (!es) return fail(TSK_ERR_TYPE, "%s: type %d not supported here", name, t->type);
+    if (t->nb[0] != (size_t) es) return fail(TSK_ERR_STRIDE, "%s: nb[0] = %zu, rows must be contiguous", name, t->nb[0]);
+    for (int i = 1; i < 4; ++i)
+        if (t->ne[i] > 1 && t->nb[i] % row_align)
+            return fail(TSK_ERR_ALIGN, "%s: nb[%d] = %zu not a multiple of %zu", name, i, t->nb[i], row_align);
+    if (!aligned(t->data, row_align)) return fail(TSK_ERR_ALIGN, "%s: data not %zu-byte aligned", name, row_align);
+    return TSK_OK;
+}
+
+View4 view(const tsk_tensor *t) {
+    View4 v;
+    v.data = t->data;
+    v.type = t->type;
+    for (int i = 0; i < 4; ++i) { v.ne[i] = t->ne[i]; v.nb[i] = (int64_t) t->nb[i]; }
+    return v;
+}
+
+bool same_shape(const tsk_tensor *a, const tsk_tensor *b) {
+    for (int i = 0; i < 4; ++i) if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+// b rows are uniformly strided over (ne1, ne2, ne3) -> one GEMM with N = ne1*ne2*ne3
+bool rows_uniform(const tsk_tensor *t) {
+    return (t->ne[2] == 1 || t->nb[2] == t->nb[1] * (size_t) t->ne[1]) &&
+           (t->ne[3] == 1 || t->nb[3] == t->nb[2] * (size_t) t->ne[2]);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ library
+extern "C" int tsk_init(int device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(TSK_ERR_INVALID_ARG, "device %d of %d", device, n);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_device = device;
+    return TSK_OK;
+}
+
+extern "C" int tsk_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_device < 0) return TSK_OK;
+    (void) hipDeviceSynchronize();
+    for (auto &w : g_ws) {
+        if (w.ptr) (void) hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.size = 0;
+    }
+    g_device = -1;
+    return TSK_OK;
+}
+
+extern "C" const char *tsk_status_string(int s) {
+    switch (s) {
+        case TSK_OK: return "ok";
+        case TSK_ERR_INVALID_ARG: return "invalid argument";
+        case TSK_ERR_TYPE: return "unsupported type";
+        case TSK_ERR_SHAPE: return "shape mismatch";
+        case TSK_ERR_STRIDE: return "unsupported strides";
+        case TSK_ERR_ALIGN: return "misaligned operand";
+        case TSK_ERR_UNSUPPORTED: return "unsupported operation";
+        case TSK_ERR_NOT_INIT: return "library not initialised";
+        case TSK_ERR_HIP: return "HIP runtime error";
+        case TSK_ERR_NOMEM: return "out of device memory";
+        default: return "unknown status";
+    }
+}
+
+extern "C" const char *tsk_last_error(void) { return g_err; }
+extern "C" const char *tsk_version(void) { return "tsk 0.1 gfx950"; }
+
+// ------------------------------------------------------------------ mul_mat
+namespace {
+
+int validate_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, const tsk_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(a, "a")) || (rc = check_tensor(b, "b")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (bias && (rc = check_tensor(bias, "bias"))) return rc;
+    const int64_t K = a->ne[0], M = a->ne[1];
+    if (a->ne[2] != 1 || a->ne[3] != 1) return fail(TSK_ERR_UNSUPPORTED, "a must be 2-D (weights), got ne2=%lld ne3=%lld", (long long) a->ne[2], (long long) a->ne[3]);
+    if (b->ne[0] != K) return fail(TSK_ERR_SHAPE, "b->ne[0]=%lld != K=%lld", (long long) b->ne[0], (long long) K);
+    if (dst->ne[0] != M || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3])
+        return fail(TSK_ERR_SHAPE, "dst must be [M=%lld, %lld, %lld, %lld]", (long long) M, (long long) b->ne[1], (long long) b->ne[2], (long long) b->ne[3]);
+    if (b->type != TSK_TYPE_F32 && b->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "b must be F32 or BF16");
+    if (dst->type != TSK_TYPE_F32 && dst->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "dst must be F32 or BF16");
+    if ((rc = check_rows(b, "b", 16)) || (rc = check_rows(dst, "dst", 16))) return rc;
+    if (bias) {
+        if (bias->type != TSK_TYPE_F32 || bias->ne[0] != M || bias->ne[1] * bias->ne[2] * bias->ne[3] != 1)
+            return fail(TSK_ERR_SHAPE, "bias must be F32 [M]");
+        if (bias->nb[0] != 4 || !aligned(bias->data, 16)) return fail(TSK_ERR_ALIGN, "bias must be contiguous, 16-byte aligned");
+    }
+    switch (a->type) {
+        case TSK_TYPE_BF16:
+            if (K % 8) return fail(TSK_ERR_SHAPE, "K=%lld must be a multiple of 8 for BF16", (long long) K);
+            if ((rc = check_rows(a, "a", 16))) return rc;
+            break;
+        case TSK_TYPE_Q8_0:
+            if (K % 32) return fail(TSK_ERR_SHAPE, "K=%lld must be a multiple of 32 for Q8_0", (long long) K);
+            if (a->nb[0] != 34) return fail(TSK_ERR_STRIDE, "Q8_0 a->nb[0] must be 34 (block size)");
+            if (a->nb[1] < (size_t) (K / 32) * 34) return fail(TSK_ERR_STRIDE, "Q8_0 rows overlap");
+            if (b->type != TSK_TYPE_F32 && b->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "b type");
+            break;
+        case TSK_TYPE_Q8_0_SPLIT:
+            if (K % 32) return fail(TSK_ERR_SHAPE, "K=%lld must be a multiple of 32 for Q8_0", (long long) K);
+            if (!aligned(a->data, 16)) return fail(TSK_ERR_ALIGN, "Q8_0_SPLIT data must be 16-byte aligned");
+            break;
+        case TSK_TYPE_F32:
+        case TSK_TYPE_F16:
+            return fail(TSK_ERR_UNSUPPORTED, "mul_mat with %s weights is not implemented on gfx950 (BF16, Q8_0 only)",
+                        a->type == TSK_TYPE_F32 ? "F32" : "F16");
+        default:
+            return fail(TSK_ERR_TYPE, "weight type %d", a->type);
+    }
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, tsk_tensor *dst,
+                           tsk_stream stream) {
+    int rc = validate_mul_mat(a, b, bias, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    const int64_t K = a->ne[0], M = a->ne[1];
+    const int es_b = elt_size(b->type), es_d = elt_size(dst->type);
+
+    // slices of uniformly strided rows: one launch per (i2, i3) unless rows are uniform
+    const bool uni = rows_uniform(b) && rows_uniform(dst);
+    const int64_t nslices = uni ? 1 : b->ne[2] * b->ne[3];
+    const int64_t Nslice = uni ? b->ne[1] * b->ne[2] * b->ne[3] : b->ne[1];
+
+    // Q8_0 weights: repack raw ggml blocks into planes in the workspace
+    const int8_t *qw = nullptr;
+    const uint16_t *dw = nullptr;
+    char *ws = nullptr;
+    size_t wbytes = 0;
+    if (a->type == TSK_TYPE_Q8_0 || a->type == TSK_TYPE_Q8_0_SPLIT) {
+        const size_t act = (size_t) (Nslice * K) + sizeof(float) * (size_t) (Nslice * (K / 32));
+        wbytes = a->type == TSK_TYPE_Q8_0 ? tsk_q8_0_split_nbytes(K, M) : 0;
+        const size_t total = ((wbytes + 255) & ~(size_t) 255) + act + 256;
+        if ((rc = workspace(total, (void **) &ws))) return rc;
+        if (a->type == TSK_TYPE_Q8_0) {
+            hipError_t e = launch_q8_repack(a->data, (int64_t) a->nb[1], M, K, ws, s);
+            if (e != hipSuccess) return hip_fail(e, "q8 repack");
+            qw = (const int8_t *) ws;
+        } else {
+            qw = (const int8_t *) a->data;
+        }
+        dw = (const uint16_t *) ((const char *) qw + (size_t) (M * K));
+    }
+
+    for (int64_t sl = 0; sl < nslices; ++sl) {
+        const int64_t i2 = sl % b->ne[2], i3 = sl / b->ne[2];
+        GemmParams p;
+        memset(&p, 0, sizeof(p));
+        p.x = (const char *) b->data + i2 * b->nb[2] + i3 * b->nb[3];
+        p.y = (char *) dst->data + i2 * dst->nb[2] + i3 * dst->nb[3];
+        p.bias = bias ? (const float *) bias->data : nullptr;
+        p.ld_x = (int64_t) (b->nb[1] / es_b);
+        p.ld_y = (int64_t) (dst->nb[1] / es_d);
+        p.M = (int) M;
+        p.N = (int) Nslice;
+        p.K = (int) K;
+        p.x_f32 = b->type == TSK_TYPE_F32;
+        p.y_bf16 = dst->type == TSK_TYPE_BF16;
+        p.epi = EPI_STORE;
+        p.rows_per_gate = 1;
+        hipError_t e;
+        if (a->type == TSK_TYPE_BF16) {
+            p.w = a->data;
+            p.ld_w = (int64_t) (a->nb[1] / 2);
+            e = launch_gemm_bf16(p, s);
+        } else {
+            char *act = ws + ((wbytes + 255) & ~(size_t) 255);
+            int8_t *qx = (int8_t *) act;
+            float *dx = (float *) (act + (((size_t) (Nslice * K) + 15) & ~(size_t) 15));
+            e = launch_quantize_rows_q8(p.x, p.x_f32, p.ld_x, p.N, p.K, qx, dx, s);
+            if (e != hipSuccess) return hip_fail(e, "q8 activation quantize");
+            p.qw = qw;
+            p.dw = dw;
+            p.qx = qx;
+            p.dx = dx;
+            e = launch_gemm_q8(p, s);
+        }
+        if (e != hipSuccess) return hip_fail(e, "mul_mat launch");
+    }
+    return TSK_OK;
+}
+
+// ------------------------------------------------------------------ flash_attn_ext
+namespace {
+
+int validate_fa(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v, const tsk_tensor *mask,
+                float scale, float max_bias, float softcap, int prec, const tsk_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(q, "q")) || (rc = check_tensor(k, "k")) || (rc = check_tensor(v, "v")) ||
+        (rc = check_tensor(dst, "dst")))
+        return rc;
+    if (mask && (rc = check_tensor(mask, "mask"))) return rc;
+    if (q->ne[0] != 64 || k->ne[0] != 64 || v->ne[0] != 64)
+        return fail(TSK_ERR_UNSUPPORTED, "head dim must be 64 (got q %lld, k %lld, v %lld)", (long long) q->ne[0], (long long) k->ne[0], (long long) v->ne[0]);
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3])
+        return fail(TSK_ERR_SHAPE, "k and v shapes differ");
+    if (q->ne[3] != k->ne[3]) return fail(TSK_ERR_SHAPE, "batch of q and k differ");
+    if (q->ne[2] % k->ne[2]) return fail(TSK_ERR_SHAPE, "q heads %lld not a multiple of kv heads %lld", (long long) q->ne[2], (long long) k->ne[2]);
+    if (dst->ne[0] != 64 || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != q->ne[3])
+        return fail(TSK_ERR_SHAPE, "dst must be [64, H, Nq, B] (ggml permuted result)");
+    for (const tsk_tensor *t : {q, k, v})
+        if (t->type != TSK_TYPE_F32 && t->type != TSK_TYPE_F16 && t->type != TSK_TYPE_BF16)
+            return fail(TSK_ERR_TYPE, "q/k/v type %d", t->type);
+    if (k->type != v->type) return fail(TSK_ERR_TYPE, "k and v must have the same type");
+    if (dst->type != TSK_TYPE_F32 && dst->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "dst type");
+    if ((rc = check_rows(q, "q", 16)) || (rc = check_rows(k, "k", 16)) || (rc = check_rows(v, "v", 16)) ||
+        (rc = check_rows(dst, "dst", 16)))
+        return rc;
+    if (mask) {
+        if (mask->type != TSK_TYPE_F16 && mask->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "mask must be F16 or F32");
+        if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1])
+            return fail(TSK_ERR_SHAPE, "mask must cover [Nkv, Nq]");
+        if (q->ne[2] % mask->ne[2] || q->ne[3] % mask->ne[3]) return fail(TSK_ERR_SHAPE, "mask broadcast");
+        if (mask->nb[0] != (size_t) elt_size(mask->type)) return fail(TSK_ERR_STRIDE, "mask rows must be contiguous");
+        if (!aligned(mask->data, elt_size(mask->type))) return fail(TSK_ERR_ALIGN, "mask data alignment");
+    }
+    if (!(scale > 0.0f) || !(max_bias >= 0.0f) || !(softcap >= 0.0f) || softcap != softcap)
+        return fail(TSK_ERR_INVALID_ARG, "scale must be > 0, max_bias and softcap >= 0");
+    if (prec != TSK_PREC_DEFAULT && prec != TSK_PREC_F32) return fail(TSK_ERR_INVALID_ARG, "prec %d", prec);
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
+                                  const tsk_tensor *mask, float scale, float max_bias, float logit_softcap, int prec,
+                                  tsk_tensor *dst, tsk_stream stream) {
+    int rc = validate_fa(q, k, v, mask, scale, max_bias, logit_softcap, prec, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.q = q->data; p.k = k->data; p.v = v->data; p.o = dst->data;
+    p.mask = mask ? mask->data : nullptr;
+    p.q_type = q->type; p.kv_type = k->type;
+    p.out_bf16 = dst->type == TSK_TYPE_BF16;
+    p.mask_f16 = mask ? mask->type == TSK_TYPE_F16 : 1;
+    p.Nq = (int) q->ne[1]; p.Nkv = (int) k->ne[1]; p.H = (int) q->ne[2]; p.Hkv = (int) k->ne[2]; p.B = (int) q->ne[3];
+    p.q_nb1 = q->nb[1]; p.q_nb2 = q->nb[2]; p.q_nb3 = q->nb[3];
+    p.k_nb1 = k->nb[1]; p.k_nb2 = k->nb[2]; p.k_nb3 = k->nb[3];
+    p.v_nb1 = v->nb[1]; p.v_nb2 = v->nb[2]; p.v_nb3 = v->nb[3];
+    if (mask) {
+        p.m_nb1 = mask->nb[1]; p.m_nb2 = mask->nb[2]; p.m_nb3 = mask->nb[3];
+        p.m_ne2 = (int) mask->ne[2]; p.m_ne3 = (int) mask->ne[3];
+    } else {
+        p.m_ne2 = p.m_ne3 = 1;
+    }
+    p.o_nb1 = dst->nb[1]; p.o_nb2 = dst->nb[2]; p.o_nb3 = dst->nb[3];
+    p.softcap = logit_softcap;
+    p.scale = logit_softcap != 0.0f ? scale / logit_softcap : scale;
+    p.max_bias = max_bias;
+    p.n_head_log2 = 1u << (uint32_t) floorf(log2f((float) p.H));
+    p.m0 = powf(2.0f, -(max_bias) / (float) p.n_head_log2);
+    p.m1 = powf(2.0f, -(max_bias / 2.0f) / (float) p.n_head_log2);
+    hipError_t e = launch_attention(p, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "flash_attn_ext launch");
+    return TSK_OK;
+}
+
+// ------------------------------------------------------------------ norms / rope
+namespace {
+
+int check_unary(const tsk_tensor *x, const tsk_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (!same_shape(x, dst)) return fail(TSK_ERR_SHAPE, "x and dst shapes differ");
+    for (const tsk_tensor *t : {x, dst})
+        if (t->type != TSK_TYPE_F32 && t->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "F32 or BF16 only");
+    if ((rc = check_rows(x, "x", elt_size(x->type))) || (rc = check_rows(dst, "dst", elt_size(dst->type)))) return rc;
+    return TSK_OK;
+}
+
+int check_w(const tsk_tensor *w, int64_t n) {
+    int rc;
+    if ((rc = check_tensor(w, "w"))) return rc;
+    if (w->type != TSK_TYPE_F32 || w->ne[0] != n || w->ne[1] * w->ne[2] * w->ne[3] != 1 || w->nb[0] != 4)
+        return fail(TSK_ERR_SHAPE, "w must be contiguous F32 [%lld]", (long long) n);
+    return TSK_OK;
+}
+
+int check_pos(const tsk_tensor *pos, const tsk_tensor *x) {
+    int rc;
+    if ((rc = check_tensor(pos, "pos"))) return rc;
+    if (pos->type != TSK_TYPE_I32 || pos->ne[0] != x->ne[2] || pos->nb[0] != 4)
+        return fail(TSK_ERR_SHAPE, "pos must be contiguous I32 [ne2 of x = %lld]", (long long) x->ne[2]);
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_rms_norm_mul(const tsk_tensor *x, const tsk_tensor *w, float eps, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_unary(x, dst))) return rc;
+    if (w && (rc = check_w(w, x->ne[0]))) return rc;
+    if (!(eps >= 0.0f)) return fail(TSK_ERR_INVALID_ARG, "eps");
+    if ((rc = require_init())) return rc;
+    hipError_t e = launch_rms_norm_mul(view(x), w ? (const float *) w->data : nullptr, eps, view(dst), (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "rms_norm launch");
+}
+
+extern "C" int tsk_norm(const tsk_tensor *x, float eps, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_unary(x, dst))) return rc;
+    if (!(eps >= 0.0f)) return fail(TSK_ERR_INVALID_ARG, "eps");
+    if ((rc = require_init())) return rc;
+    hipError_t e = launch_norm(view(x), eps, view(dst), (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "norm launch");
+}
+
+extern "C" int tsk_rope_ext(const tsk_tensor *x, const tsk_tensor *pos, int n_dims, int mode, float freq_base,
+                            float freq_scale, float ext_factor, float attn_factor, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_unary(x, dst)) || (rc = check_pos(pos, x))) return rc;
+    if (mode != TSK_ROPE_TYPE_NORMAL) return fail(TSK_ERR_UNSUPPORTED, "rope mode %d (NORMAL only)", mode);
+    if (ext_factor != 0.0f || attn_factor != 1.0f) return fail(TSK_ERR_UNSUPPORTED, "ext_factor must be 0, attn_factor 1");
+    if (n_dims <= 0 || (n_dims & 1) || n_dims > x->ne[0] || n_dims > 128) return fail(TSK_ERR_INVALID_ARG, "n_dims %d", n_dims);
+    if (!(freq_base > 0.0f)) return fail(TSK_ERR_INVALID_ARG, "freq_base");
+    if ((rc = require_init())) return rc;
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    hipError_t e = launch_rope(view(x), (const int32_t *) pos->data, n_dims, theta_scale, freq_scale, view(dst),
+                               (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "rope launch");
+}
+
+extern "C" int tsk_qk_norm_rope(const tsk_tensor *x, const tsk_tensor *w, const tsk_tensor *pos, float eps, int n_dims,
+                                float freq_base, float freq_scale, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_unary(x, dst)) || (rc = check_w(w, 64))) return rc;
+    if (x->ne[0] != 64) return fail(TSK_ERR_UNSUPPORTED, "head dim must be 64");
+    if (pos && (rc = check_pos(pos, x))) return rc;
+    if (pos && (n_dims <= 0 || (n_dims & 1) || n_dims > 64)) return fail(TSK_ERR_INVALID_ARG, "n_dims %d", n_dims);
+    if (!(eps >= 0.0f) || (pos && !(freq_base > 0.0f))) return fail(TSK_ERR_INVALID_ARG, "eps / freq_base");
+    if ((rc = require_init())) return rc;
+    const float theta_scale = pos ? powf(freq_base, -2.0f / (float) n_dims) : 1.0f;
+    hipError_t e = launch_qk_norm_rope(view(x), (const float *) w->data, pos ? (const int32_t *) pos->data : nullptr,
+                                       eps, n_dims, theta_scale, freq_scale, view(dst), (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "qk_norm_rope launch");
+}
+
+// ------------------------------------------------------------------ Q8_0
+extern "C" size_t tsk_q8_0_split_nbytes(int64_t K, int64_t M) {
+    if (K <= 0 || M <= 0 || K % 32) return 0;
+    return (size_t) (K * M) + 2 * (size_t) (M * (K / 32));
+}
+
+extern "C" int tsk_q8_0_quantize(const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (x->type != TSK_TYPE_F32 || dst->type != TSK_TYPE_Q8_0) return fail(TSK_ERR_TYPE, "x F32 -> dst Q8_0");
+    if (!same_shape(x, dst)) return fail(TSK_ERR_SHAPE, "shapes differ");
+    if (x->ne[0] % 32) return fail(TSK_ERR_SHAPE, "ne0 %% 32 != 0");
+    if ((rc = check_rows(x, "x", 4))) return rc;
+    if (dst->nb[0] != 34) return fail(TSK_ERR_STRIDE, "dst nb[0] must be 34");
+    if (!rows_uniform(x) || !rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "rows must be uniformly strided");
+    if ((rc = require_init())) return rc;
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    hipError_t e = launch_q8_quantize_blocks((const float *) x->data, (int64_t) (x->nb[1] / 4), rows, x->ne[0],
+                                             dst->data, (int64_t) dst->nb[1], (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "q8 quantize launch");
+}
+
+extern "C" int tsk_q8_0_dequantize(const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if ((x->type != TSK_TYPE_Q8_0 && x->type != TSK_TYPE_Q8_0_SPLIT) || dst->type != TSK_TYPE_F32)
+        return fail(TSK_ERR_TYPE, "x Q8_0/Q8_0_SPLIT -> dst F32");
+    if (!same_shape(x, dst)) return fail(TSK_ERR_SHAPE, "shapes differ");
+    if (x->ne[0] % 32) return fail(TSK_ERR_SHAPE, "ne0 %% 32 != 0");
+    if ((rc = check_rows(dst, "dst", 4))) return rc;
+    if (!rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "dst rows must be uniformly strided");
+    const bool split = x->type == TSK_TYPE_Q8_0_SPLIT;
+    if (!split && (x->nb[0] != 34 || !rows_uniform(x))) return fail(TSK_ERR_STRIDE, "Q8_0 strides");
+    if ((rc = require_init())) return rc;
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    hipError_t e = launch_q8_dequantize(x->data, split, rows, x->ne[0], split ? 0 : (int64_t) x->nb[1],
+                                        (float *) dst->data, (int64_t) (dst->nb[1] / 4), (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "q8 dequantize launch");
+}
+
+extern "C" int tsk_q8_0_repack(const tsk_tensor *src, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(src, "src")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (src->type != TSK_TYPE_Q8_0 || dst->type != TSK_TYPE_Q8_0_SPLIT) return fail(TSK_ERR_TYPE, "Q8_0 -> Q8_0_SPLIT");
+    if (!same_shape(src, dst) || src->ne[2] * src->ne[3] != 1) return fail(TSK_ERR_SHAPE, "2-D Q8_0 of equal shape");
+    if (src->ne[0] % 32 || src->nb[0] != 34) return fail(TSK_ERR_STRIDE, "Q8_0 layout");
+    if (!aligned(dst->data, 16)) return fail(TSK_ERR_ALIGN, "dst 16-byte alignment");
+    if ((rc = require_init())) return rc;
+    hipError_t e = launch_q8_repack(src->data, (int64_t) src->nb[1], src->ne[1], src->ne[0], dst->data, (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "q8 repack launch");
+}
+
+// ------------------------------------------------------------------ supports_op
+extern "C" int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs, const tsk_tensor *dst) {
+    // validation only: swap data pointers for a dummy aligned address
+    static char dummy[64] __attribute__((aligned(64)));
+    tsk_tensor t[6], d;
+    if (!srcs || !dst || n_srcs < 1 || n_srcs > 5) return 0;
+    for (int i = 0; i < n_srcs; ++i) {
+        if (!srcs[i]) { t[i].type = -1; continue; }
+        t[i] = *srcs[i];
+        t[i].data = dummy;
+    }
+    d = *dst;
+    d.data = dummy;
+    auto opt = [&](int i) -> const tsk_tensor * { return i < n_srcs && srcs[i] ? &t[i] : nullptr; };
+    int rc;
+    switch (op) {
+        case TSK_OP_MUL_MAT:
+            rc = n_srcs >= 2 ? validate_mul_mat(&t[0], &t[1], opt(2), &d) : TSK_ERR_INVALID_ARG;
+            break;
+        case TSK_OP_FLASH_ATTN_EXT:
+            rc = n_srcs >= 3 ? validate_fa(&t[0], &t[1], &t[2], opt(3), 0.125f, 0.0f, 0.0f, TSK_PREC_F32, &d)
+                             : TSK_ERR_INVALID_ARG;
+            break;
+        case TSK_OP_RMS_NORM_MUL:
+            rc = check_unary(&t[0], &d);
+            if (!rc && opt(1)) rc = check_w(&t[1], t[0].ne[0]);
+            break;
+        case TSK_OP_ROPE_EXT:
+            rc = check_unary(&t[0], &d);
+            if (!rc) rc = n_srcs >= 2 ? check_pos(&t[1], &t[0]) : TSK_ERR_INVALID_ARG;
+            break;
+        case TSK_OP_NORM:
+            rc = check_unary(&t[0], &d);
+            break;
+        default:
+            rc = TSK_ERR_UNSUPPORTED;
+    }
+    return rc == TSK_OK ? 1 : 0;
+}

@@ -1,0 +1,66 @@
+// tsk_common.h — shared device types and helpers for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tsk/tsk.h"
+
+namespace tsk {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+// ---- scalar conversions (round to nearest even) -------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+    return __uint_as_float((uint32_t) h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t) ((x >> 16) | 64u);
+    return (uint16_t) ((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16) f;              // v_cvt_f16_f32: RNE
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float) __builtin_bit_cast(_Float16, h);
+}
+
+// Element-type tags used by the kernels' templates.
+enum class Elt : int { F32 = 0, F16 = 1, BF16 = 30 };
+
+template <Elt E> struct EltInfo;
+template <> struct EltInfo<Elt::F32>  { typedef float    storage; static constexpr int bytes = 4; };
+template <> struct EltInfo<Elt::F16>  { typedef uint16_t storage; static constexpr int bytes = 2; };
+template <> struct EltInfo<Elt::BF16> { typedef uint16_t storage; static constexpr int bytes = 2; };
+
+template <Elt E> __device__ __forceinline__ float load_as_f32(const void *p, int64_t i) {
+    if constexpr (E == Elt::F32) return ((const float *) p)[i];
+    else if constexpr (E == Elt::F16) return f16_bits_to_f32(((const uint16_t *) p)[i]);
+    else return bf16_bits_to_f32(((const uint16_t *) p)[i]);
+}
+template <Elt E> __device__ __forceinline__ void store_from_f32(void *p, int64_t i, float v) {
+    if constexpr (E == Elt::F32) ((float *) p)[i] = v;
+    else if constexpr (E == Elt::F16) ((uint16_t *) p)[i] = f32_to_f16_bits(v);
+    else ((uint16_t *) p)[i] = f32_to_bf16_bits(v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace tsk

@@ -1,0 +1,348 @@
+"""Python front end of libtsk.so (ctypes over the C ABI in include/tsk/tsk.h).
+
+Mirrors the ggml operator surface that src/mmdit.cpp drives for the MM-DiT
+hot path -- mul_mat, flash_attn_ext, rms_norm*w, rope_ext, norm -- plus the
+ts_dit driver (load / forward / sample, src/mmdit.h:9-42). Tensors are torch
+tensors on the GPU; shapes are torch order, i.e. the reverse of ggml's ne[]
+(a ggml [D, N, H, B] tensor is a torch (B, H, N, D) tensor). Errors raise
+TskError with the library's status and message; nothing falls back to a CPU
+path: if libtsk.so is missing, load() raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtsk.so")
+
+F32, F16, Q8_0, I32, BF16, Q8_0_SPLIT = 0, 1, 8, 26, 30, 0x1008
+PREC_DEFAULT, PREC_F32 = 0, 10
+ROPE_NORMAL = 0
+OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_RMS_NORM_MUL, OP_ROPE_EXT, OP_NORM = 1, 2, 3, 4, 5
+STATUS = {0: "TSK_OK", -1: "TSK_ERR_INVALID_ARG", -2: "TSK_ERR_TYPE", -3: "TSK_ERR_SHAPE",
+          -4: "TSK_ERR_STRIDE", -5: "TSK_ERR_ALIGN", -6: "TSK_ERR_UNSUPPORTED",
+          -7: "TSK_ERR_NOT_INIT", -8: "TSK_ERR_HIP", -9: "TSK_ERR_NOMEM"}
+
+
+class TskError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class TskTensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
+
+
+class DitConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq",
+        "mlp_hidden", "mlp_kind", "weight_type", "max_batch", "max_latent")] + \
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
+
+
+_lib = None
+
+
+def load():
+    """Load libtsk.so (built by __graft_entry__.build()); raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.POINTER(TskTensor)
+    vp, f, i = ctypes.c_void_p, ctypes.c_float, ctypes.c_int
+    sig = {
+        "tsk_init": ([i], i), "tsk_shutdown": ([], i),
+        "tsk_status_string": ([i], ctypes.c_char_p), "tsk_last_error": ([], ctypes.c_char_p),
+        "tsk_version": ([], ctypes.c_char_p),
+        "tsk_mul_mat": ([P, P, P, P, vp], i),
+        "tsk_flash_attn_ext": ([P, P, P, P, f, f, f, i, P, vp], i),
+        "tsk_rms_norm_mul": ([P, P, f, P, vp], i),
+        "tsk_norm": ([P, f, P, vp], i),
+        "tsk_rope_ext": ([P, P, i, i, f, f, f, f, P, vp], i),
+        "tsk_qk_norm_rope": ([P, P, P, f, i, f, f, P, vp], i),
+        "tsk_q8_0_quantize": ([P, P, vp], i), "tsk_q8_0_dequantize": ([P, P, vp], i),
+        "tsk_q8_0_repack": ([P, P, vp], i),
+        "tsk_q8_0_split_nbytes": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
+        "tsk_supports_op": ([i, ctypes.POINTER(P), i, P], i),
+        "tsk_dit_default_config": ([ctypes.POINTER(DitConfig)], None),
+        "tsk_dit_create": ([ctypes.POINTER(DitConfig), ctypes.POINTER(vp)], i),
+        "tsk_dit_destroy": ([vp], None),
+        "tsk_dit_n_tensors": ([vp], i),
+        "tsk_dit_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p),
+                                 ctypes.POINTER(ctypes.c_int64)], i),
+        "tsk_dit_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_dit_forward": ([vp, i, i, vp, vp, vp, vp, vp], i),
+        "tsk_dit_forward_device": ([vp, i, i, vp, vp, vp, vp, vp], i),
+        "tsk_dit_sample": ([vp, i, vp, vp, vp, i, f, vp, vp, vp], i),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def check(rc):
+    if rc != 0:
+        raise TskError(rc, load().tsk_last_error().decode())
+    return rc
+
+
+_initialised = False
+
+
+def init(device=0):
+    global _initialised
+    if not _initialised:
+        check(load().tsk_init(device))
+        _initialised = True
+
+
+# ---------------------------------------------------------------- descriptors
+def _ttype(t):
+    import torch
+    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32}
+    if t.dtype not in m:
+        raise TypeError(f"no tsk type for {t.dtype}")
+    return m[t.dtype]
+
+
+def desc(t, ttype=None):
+    """tsk_tensor view of a torch tensor: ne = reversed shape, nb = reversed byte strides.
+    A Q8_0 tensor is a uint8 torch tensor of shape (rows, K/32, 34)."""
+    d = TskTensor()
+    ttype = _ttype(t) if ttype is None else ttype
+    d.type = ttype
+    if ttype == Q8_0:
+        rows, nblk = t.shape[0], t.shape[1]
+        ne = [nblk * 32, rows]
+        nb = [34, t.stride(0)]
+    elif ttype == Q8_0_SPLIT:
+        ne = list(t.logical_shape)
+        nb = [1, ne[0]]
+    else:
+        es = t.element_size()
+        ne = list(t.shape)[::-1]
+        nb = [s * es for s in t.stride()][::-1]
+    while len(ne) < 4:
+        nb.append(nb[-1] * ne[-1] if ne else 4)
+        ne.append(1)
+    for k in range(4):
+        d.ne[k] = int(ne[k])
+        d.nb[k] = int(nb[k])
+    d.data = t.data_ptr()
+    return d
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ref(x):
+    return ctypes.byref(x) if x is not None else None
+
+
+# ---------------------------------------------------------------- operators
+def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype=None):
+    """ggml_mul_mat(a, b) (+bias): a (M, K) weights, b (..., N, K) -> (..., N, M)."""
+    import torch
+    init()
+    at = a_type if a_type is not None else _ttype(a)
+    M = a.shape[0] if at != Q8_0_SPLIT else a.logical_shape[1]
+    if out is None:
+        out = torch.empty(b.shape[:-1] + (M,), dtype=out_dtype or torch.float32, device=b.device)
+    da, db, dd = desc(a, at), desc(b), desc(out)
+    dbias = desc(bias) if bias is not None else None
+    check(load().tsk_mul_mat(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd), _stream()))
+    return out
+
+
+def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0, prec=PREC_F32,
+                   out=None, out_dtype=None):
+    """q (B, H, Nq, D), k/v (B, Hkv, Nkv, D) -> (B, Nq, H, D) (ggml's permuted result)."""
+    import torch
+    init()
+    B, H, Nq, D = q.shape
+    if out is None:
+        out = torch.empty((B, Nq, H, v.shape[-1]), dtype=out_dtype or torch.float32, device=q.device)
+    dq, dk, dv, dd = desc(q), desc(k), desc(v), desc(out)
+    dm = desc(mask) if mask is not None else None
+    check(load().tsk_flash_attn_ext(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), _ref(dm),
+                                    scale, max_bias, softcap, prec, ctypes.byref(dd), _stream()))
+    return out
+
+
+def rms_norm_mul(x, w, eps, out=None):
+    import torch
+    init()
+    out = torch.empty_like(x) if out is None else out
+    dx, dd = desc(x), desc(out)
+    dw = desc(w) if w is not None else None
+    check(load().tsk_rms_norm_mul(ctypes.byref(dx), _ref(dw), eps, ctypes.byref(dd), _stream()))
+    return out
+
+
+def norm(x, eps, out=None):
+    import torch
+    init()
+    out = torch.empty_like(x) if out is None else out
+    dx, dd = desc(x), desc(out)
+    check(load().tsk_norm(ctypes.byref(dx), eps, ctypes.byref(dd), _stream()))
+    return out
+
+
+def rope_ext(x, pos, n_dims, freq_base=10000.0, freq_scale=1.0, mode=ROPE_NORMAL, out=None):
+    """x (B, S, H, D) i.e. ggml [D, H, S, B]; pos int32 (S,)."""
+    import torch
+    init()
+    out = torch.empty_like(x) if out is None else out
+    dx, dp, dd = desc(x), desc(pos), desc(out)
+    check(load().tsk_rope_ext(ctypes.byref(dx), ctypes.byref(dp), n_dims, mode, freq_base, freq_scale,
+                              0.0, 1.0, ctypes.byref(dd), _stream()))
+    return out
+
+
+def qk_norm_rope(x, w, pos, eps=1e-6, n_dims=64, freq_base=10000.0, freq_scale=1.0, out=None):
+    import torch
+    init()
+    out = torch.empty_like(x) if out is None else out
+    dx, dw, dd = desc(x), desc(w), desc(out)
+    dp = desc(pos) if pos is not None else None
+    check(load().tsk_qk_norm_rope(ctypes.byref(dx), ctypes.byref(dw), _ref(dp), eps, n_dims, freq_base,
+                                  freq_scale, ctypes.byref(dd), _stream()))
+    return out
+
+
+def q8_0_quantize(x):
+    """(rows, K) float32 -> (rows, K/32, 34) uint8 ggml block_q8_0 bytes."""
+    import torch
+    init()
+    rows, K = x.shape
+    out = torch.empty((rows, K // 32, 34), dtype=torch.uint8, device=x.device)
+    dx, dd = desc(x), desc(out, Q8_0)
+    check(load().tsk_q8_0_quantize(ctypes.byref(dx), ctypes.byref(dd), _stream()))
+    return out
+
+
+class SplitQ8:
+    """Q8_0 weights repacked into int8 / fp16 planes (TSK_TYPE_Q8_0_SPLIT)."""
+
+    def __init__(self, buf, K, M):
+        self.buf, self.logical_shape = buf, (K, M)
+
+    def data_ptr(self):
+        return self.buf.data_ptr()
+
+
+def q8_0_repack(blocks):
+    import torch
+    init()
+    rows, nb = blocks.shape[0], blocks.shape[1]
+    K = nb * 32
+    buf = torch.empty(load().tsk_q8_0_split_nbytes(K, rows), dtype=torch.uint8, device=blocks.device)
+    sp = SplitQ8(buf, K, rows)
+    ds, dd = desc(blocks, Q8_0), desc(sp, Q8_0_SPLIT)
+    check(load().tsk_q8_0_repack(ctypes.byref(ds), ctypes.byref(dd), _stream()))
+    return sp
+
+
+def q8_0_dequantize(x):
+    import torch
+    init()
+    if isinstance(x, SplitQ8):
+        K, rows = x.logical_shape
+        dx = desc(x, Q8_0_SPLIT)
+    else:
+        rows, K = x.shape[0], x.shape[1] * 32
+        dx = desc(x, Q8_0)
+    out = torch.empty((rows, K), dtype=torch.float32, device="cuda")
+    dd = desc(out)
+    check(load().tsk_q8_0_dequantize(ctypes.byref(dx), ctypes.byref(dd), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- MM-DiT driver
+def dit_config(**kw):
+    c = DitConfig()
+    load().tsk_dit_default_config(ctypes.byref(c))
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+class Dit:
+    """ts_dit counterpart: named BF16 weights on the GPU, forward() and sample()."""
+
+    def __init__(self, cfg=None):
+        init()
+        self.cfg = cfg if cfg is not None else dit_config()
+        h = ctypes.c_void_p()
+        check(load().tsk_dit_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().tsk_dit_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """[(name, ggml ne tuple)] of every weight the driver expects."""
+        L = load()
+        out = []
+        for k_ in range(L.tsk_dit_n_tensors(self.h)):
+            nm = ctypes.c_char_p()
+            ne = (ctypes.c_int64 * 4)()
+            check(L.tsk_dit_tensor_info(self.h, k_, ctypes.byref(nm), ne))
+            out.append((nm.value.decode(), tuple(ne)))
+        return out
+
+    def set_tensor(self, name, host_f32):
+        """host_f32: contiguous numpy float32 array."""
+        check(load().tsk_dit_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
+
+    def forward(self, latent, t, text):
+        """host numpy arrays: latent (B, T, L), t (B,), text (B, text_seq, hidden) -> flow (B, T, L)."""
+        import numpy as np
+        latent = np.ascontiguousarray(latent, dtype=np.float32)
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        text = np.ascontiguousarray(text, dtype=np.float32)
+        B, T, L = latent.shape
+        flow = np.empty_like(latent)
+        check(load().tsk_dit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data, text.ctypes.data,
+                                     flow.ctypes.data, _stream()))
+        return flow
+
+    def forward_device(self, latent, t, text, flow):
+        """torch GPU tensors latent (B, T, L), text (B, S, H), flow out; t host numpy (B,)."""
+        import numpy as np
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        B, T, _ = latent.shape
+        check(load().tsk_dit_forward_device(self.h, B, T, ctypes.c_void_p(latent.data_ptr()),
+                                            t.ctypes.data, ctypes.c_void_p(text.data_ptr()),
+                                            ctypes.c_void_p(flow.data_ptr()), _stream()))
+        return flow
+
+    def sample(self, noise, text_cond, text_uncond, steps=24, cfg_scale=5.0):
+        import numpy as np
+        noise = np.ascontiguousarray(noise, dtype=np.float32)
+        text_cond = np.ascontiguousarray(text_cond, dtype=np.float32)
+        text_uncond = np.ascontiguousarray(text_uncond, dtype=np.float32)
+        T, L = noise.shape
+        out = np.empty_like(noise)
+        flow0 = np.empty_like(noise)
+        check(load().tsk_dit_sample(self.h, T, noise.ctypes.data, text_cond.ctypes.data,
+                                    text_uncond.ctypes.data, steps, cfg_scale, out.ctypes.data,
+                                    flow0.ctypes.data, _stream()))
+        return out, flow0
