@@ -1,0 +1,168 @@
+#!/usr/bin/env python3
+"""MM-DiT flow-step benchmark on one MI355X.
+
+Workload (the configuration the metric is quoted on): one full MM-DiT flow
+step at 9 s -- 194 latent tokens + 77 text tokens, CFG batch 2, d = 1024,
+16 heads x 64, GELU(tanh) MLP 4x, 7 joint + 14 fused blocks, BF16 weights
+random-init N(0, 0.02) from seed 1234, latent/text N(0, 1) from seed 4242,
+t = 0.5. Inputs are resident in HBM before the timed region.
+
+Prints ONE JSON line: steps/s (value), the roofline of the dominant kernel
+class (measured with HIP events around its launches inside the timed steps),
+attention TFLOP/s at 9 s and 30 s, and the CPU baseline (the oracle's
+restatement of the same flow step on this host's cores).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def make_inputs(B, T, seed=4242):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lat = rng.standard_normal((B, T, 64), dtype=np.float32)
+    txt = rng.standard_normal((B, 77, 1024), dtype=np.float32)   # row 0 cond, row 1 uncond
+    return lat, np.full(B, 0.5, np.float32), txt
+
+
+def roofline(role, ms, launches, flop, nbytes):
+    """achieved rate of one launch class against the MI355X roof that bounds it."""
+    if launches == 0 or ms <= 0:
+        return None
+    avg_s = ms / 1e3 / launches
+    ai = flop / max(nbytes, 1.0)
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if ai >= ridge:
+        ach = flop / launches / avg_s / 1e12
+        return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "kernel": role, "launches_per_step": None, "avg_us": round(avg_s * 1e6, 3),
+                "flop_per_launch": flop / launches, "bytes_per_launch": nbytes / launches}
+    ach = nbytes / launches / avg_s / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": role,
+            "launches_per_step": None, "avg_us": round(avg_s * 1e6, 3),
+            "flop_per_launch": flop / launches, "bytes_per_launch": nbytes / launches}
+
+
+def cpu_baseline(weights, lat, t, txt, threads):
+    """The oracle's flow step (same weights and inputs) on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    oracle.set_threads(threads)
+    od = oracle.OracleDiT(oracle.dit_config())
+    for k, v in weights.items():
+        od.set_tensor(k, v)
+    t0 = time.perf_counter()
+    od.forward(lat, t, txt, act_bf16=True, kv_f16=True)
+    dt = time.perf_counter() - t0
+    return {"value": round(1.0 / dt, 4), "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"one full 21-block CFG-batched flow step at 9 s (B=2, 194+77 tokens), "
+                      f"oracle C restatement of ggml-cpu semantics, {threads} threads, {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the MM-DiT step on one GPU "
+              f"only (CFG/data sharding over several GPUs is a design note in DESIGN.md); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from __graft_entry__ import ensure_built, load_tsk
+
+    ensure_built()
+    tsk = load_tsk()
+    tsk.init(0)
+    dit = tsk.Dit(tsk.dit_config(max_batch=2, max_latent=646))
+    weights = tsk.synthetic_weights(dit.tensors(), seed=1234)
+    for k, v in weights.items():
+        dit.set_tensor(k, v)
+
+    def run(T, steps, warmup, timing):
+        lat, t, txt = make_inputs(2, T)
+        lat_d, txt_d = tsk.to_device(lat), tsk.to_device(txt)
+        flow = tsk.empty((2, T, 64))
+        for _ in range(warmup):
+            dit.forward_device(lat_d, t, txt_d, flow)
+        tsk.synchronize()
+        if timing:
+            dit.timing(True)
+        s, e = tsk.Event(), tsk.Event()
+        s.record()
+        for _ in range(steps):
+            dit.forward_device(lat_d, t, txt_d, flow)
+        e.record()
+        tsk.synchronize()
+        ms = s.elapsed_ms(e) / steps
+        roles = None
+        if timing:
+            dit.timing(False)
+            roles = dit.timing_read()
+        return ms, roles, (lat, t, txt)
+
+    # config 2 (9 s): timed steps; per-kernel HIP events around every launch inside them
+    ms_plain, _, inputs9 = run(194, args.steps, args.warmup, False)
+    ms_timed, roles9, _ = run(194, args.steps, 1, True)
+    # 30 s (646 latent + 77 text tokens): steps/s and attention at N = 723
+    ms30, roles30, _ = run(646, max(5, args.steps // 2), 2, True)
+
+    dom = max(roles9, key=lambda r: roles9[r][0])
+    rf = roofline(dom, *roles9[dom])
+    rf["launches_per_step"] = roles9[dom][1] // args.steps
+
+    def attn(roles, ms_steps):
+        ms, n, fl, by = roles["attn"]
+        tf = fl / (ms / 1e3) / 1e12
+        return {"tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                "avg_us": round(ms * 1e3 / n, 3), "launches_per_step": n // ms_steps}
+
+    breakdown = {r: {"ms_per_step": round(v[0] / args.steps, 4), "launches_per_step": v[1] // args.steps,
+                     "tflops": round(v[2] / (v[0] / 1e3) / 1e12, 2) if v[0] > 0 else None}
+                 for r, v in roles9.items()}
+    out = {
+        "metric": "DiT flow steps/s at 9 s (CFG b=2)",
+        "value": round(1000.0 / ms_plain, 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_plain, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, random-init N(0,0.02) BF16 weights)",
+        "config": {"workload": "MM-DiT flow step, 9 s: 194 latent + 77 text tokens, CFG batch 2, "
+                               "d=1024, 16x64 heads, GELU MLP 4x, 7 joint + 14 fused blocks, BF16 weights",
+                   "global_batch": 2, "seq_len": 271, "parallelism": "single GPU"},
+        "roofline": rf,
+        "attention": {"9s": attn(roles9, args.steps), "30s": attn(roles30, max(5, args.steps // 2))},
+        "steps_per_s_30s": round(1000.0 / ms30, 2),
+        "ms_per_step_with_kernel_events": round(ms_timed, 4),
+        "breakdown_9s": breakdown,
+    }
+    if not args.no_cpu_baseline:
+        lat, t, txt = inputs9
+        threads = min(16, os.cpu_count() or 1)
+        out["cpu_baseline"] = cpu_baseline(weights, lat, t, txt, threads)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

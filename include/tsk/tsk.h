@@ -247,6 +247,29 @@ int  tsk_dit_sample(tsk_dit *dit, int T, const float *noise, const float *text_c
                     const float *text_uncond, int steps, float cfg_scale,
                     float *out, float *flow0, tsk_stream stream);
 
+/*
+ * Kernel timing of the step driver (extension, no counterpart in the
+ * reference: ggml exposes no per-node timing). tsk_dit_timing(dit, 1) resets
+ * the accumulators and records a HIP event pair around every launch of the
+ * driver from then on (on the caller's stream); 0 stops recording.
+ * tsk_dit_timing_read synchronises on the last event of `role` and returns the
+ * summed kernel time, the number of launches and their algorithmic FLOPs and
+ * bytes (weights + activations read + outputs written, once each).
+ */
+enum tsk_dit_role {
+    TSK_ROLE_QKV = 0,        /* QKV projection GEMMs                      */
+    TSK_ROLE_OUT = 1,        /* attention output projection (linear1)     */
+    TSK_ROLE_FC1 = 2,        /* MLP up GEMM (+GELU)                       */
+    TSK_ROLE_FC2 = 3,        /* MLP down GEMM (+gate*residual)            */
+    TSK_ROLE_ATTN = 4,       /* flash attention                           */
+    TSK_ROLE_ADALN = 5,      /* t_embed MLP + adaLN GEMVs                 */
+    TSK_ROLE_OTHER = 6,      /* LN/modulate, QKV split, in/out projection */
+    TSK_ROLE_COUNT = 7
+};
+int  tsk_dit_timing(tsk_dit *dit, int enable);
+int  tsk_dit_timing_read(tsk_dit *dit, int role, double *ms, int64_t *launches,
+                         double *flop, double *bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,9 @@ def lib():
         L.orc_dit_create.argtypes = [ctypes.POINTER(DitConfig)]
         L.orc_dit_create.restype = ctypes.c_void_p
         L.orc_dit_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_dit_n_tensors.argtypes = [ctypes.c_void_p]
+        L.orc_dit_tensor_info.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+                                          ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
         L.orc_dit_set_tensor.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p,
                                          ctypes.c_int64]
         L.orc_dit_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
@@ -258,6 +261,14 @@ class OracleDiT:
         if getattr(self, "h", None):
             lib().orc_dit_destroy(self.h)
             self.h = None
+
+    def tensors(self):
+        out = []
+        for i in range(lib().orc_dit_n_tensors(self.h)):
+            nm, a, b = ctypes.c_char_p(), ctypes.c_int64(), ctypes.c_int64()
+            lib().orc_dit_tensor_info(self.h, i, ctypes.byref(nm), ctypes.byref(a), ctypes.byref(b))
+            out.append((nm.value.decode(), (a.value, b.value, 1, 1)))
+        return out
 
     def set_tensor(self, name, arr):
         arr = np.ascontiguousarray(arr, dtype=np.float32)

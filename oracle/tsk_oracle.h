@@ -78,9 +78,14 @@ typedef struct orc_dit orc_dit;
 orc_dit *orc_dit_create(const tsk_dit_config *cfg);
 void     orc_dit_destroy(orc_dit *d);
 int      orc_dit_set_tensor(orc_dit *d, const char *name, const float *src, int64_t n);
-/* act_bf16 = 1 rounds every mul_mat activation to bf16 (ggml's BF16-weight
- * path); 0 keeps activations F32 (the "GGML F32 path").  kv_f16 = 1 casts K/V
- * to F16 before attention as mmdit.cpp:89-90 does. */
+int      orc_dit_n_tensors(const orc_dit *d);
+/* name and ggml ne[0], ne[1] of the i-th weight */
+int      orc_dit_tensor_info(const orc_dit *d, int i, const char **name, int64_t *ne0, int64_t *ne1);
+/* act_bf16 = 1 rounds the activations of the per-block projections (qkv,
+ * linear1, fc1, fc2) to bf16 (ggml's BF16-weight mul_mat) and keeps F32
+ * activations for the conditioning, input and output projections (the device
+ * path's precision policy); 0 keeps all activations F32 (the "GGML F32
+ * path"). kv_f16 = 1 casts K/V to F16 before attention as mmdit.cpp:89-90. */
 int      orc_dit_forward(orc_dit *d, int B, int T, const float *latent, const float *t,
                          const float *text, float *flow, int act_bf16, int kv_f16);
 int      orc_dit_sample(orc_dit *d, int T, const float *noise, const float *text_cond,

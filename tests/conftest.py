@@ -24,5 +24,5 @@ def rel_l2(a, b):
 @pytest.fixture(scope="session")
 def orc():
     import oracle
-    oracle.set_threads(min(8, os.cpu_count() or 1))
+    oracle.set_threads(min(16, os.cpu_count() or 1))
     return oracle

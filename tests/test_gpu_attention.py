@@ -11,48 +11,42 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def env(orc):
-    import torch
     from __graft_entry__ import ensure_built, load_tsk
     ensure_built()
     tsk = load_tsk()
     tsk.init(0)
-    return tsk, torch, orc
-
-
-def bf16_dev(torch, bits):
-    return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+    return tsk, orc
 
 
 @pytest.mark.parametrize("B,H,N", [(2, 16, 271), (1, 16, 77), (2, 8, 1), (1, 2, 65), (2, 16, 194)])
 def test_f32_attention(env, B, H, N):
     """config 1: F32 joint attention, scale 1/8, no mask (rel-L2 <= 1e-5)."""
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(1234 + N)
     q, k, v = (rng.standard_normal((B, H, N, 64)).astype(np.float32) for _ in range(3))
-    o = tsk.flash_attn_ext(*(torch.from_numpy(a).cuda() for a in (q, k, v)), scale=0.125)
+    o = tsk.flash_attn_ext(*(tsk.to_device(a) for a in (q, k, v)), scale=0.125)
     ref = orc.flash_attn_ext(q, k, v, scale=0.125)
-    assert rel_l2(o.cpu().numpy(), ref) <= 1e-5
+    assert rel_l2(o.numpy(), ref) <= 1e-5
 
 
 @pytest.mark.parametrize("B,H,N", [(1, 16, 420), (1, 16, 1040), (1, 16, 194), (1, 16, 646),
                                    (2, 16, 271), (1, 8, 77)])
 def test_reference_types_f32q_f16kv(env, B, H, N):
     """the node mmdit.cpp:88-92 emits: Q F32, K/V cast to F16, prec F32."""
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(N)
     q = rng.standard_normal((B, H, N, 64)).astype(np.float32)
     k = rng.standard_normal((B, H, N, 64)).astype(np.float16)
     v = rng.standard_normal((B, H, N, 64)).astype(np.float16)
-    o = tsk.flash_attn_ext(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
-                           torch.from_numpy(v).cuda(), scale=0.125)
+    o = tsk.flash_attn_ext(tsk.to_device(q), tsk.to_device(k), tsk.to_device(v), scale=0.125)
     ref = orc.flash_attn_ext(q, k, v, scale=0.125)
-    assert rel_l2(o.cpu().numpy(), ref) <= 1e-3
+    assert rel_l2(o.numpy(), ref) <= 1e-3
 
 
 @pytest.mark.parametrize("N", [723, 271, 33])
 def test_bf16_attention_config3(env, N):
     """config 3: bf16 Q/K/V after QK-RMSNorm and RoPE on the 646 latent positions."""
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(99 + N)
     B, H = 2, 16
     x = [rng.standard_normal((B, N, H, 64)).astype(np.float32) for _ in range(3)]
@@ -65,16 +59,16 @@ def test_bf16_attention_config3(env, N):
         t[:, :nlat] = orc.rope_ext(np.ascontiguousarray(t[:, :nlat]), pos, 64)
         qk.append(t)
     bits = [orc.f32_to_bf16_bits(np.ascontiguousarray(t.transpose(0, 2, 1, 3))) for t in (qk[0], qk[1], x[2])]
-    o = tsk.flash_attn_ext(*(bf16_dev(torch, b) for b in bits), scale=0.125)
+    o = tsk.flash_attn_ext(*(tsk.bf16_to_device(b) for b in bits), scale=0.125)
     ref = orc.flash_attn_ext(*bits, scale=0.125, kv_bf16=True, q_bf16=True)
-    assert rel_l2(o.cpu().numpy(), ref) <= 1e-3
-    ob = tsk.flash_attn_ext(*(bf16_dev(torch, b) for b in bits), scale=0.125, out_dtype=torch.bfloat16)
-    assert rel_l2(ob.float().cpu().numpy(), ref) <= 5e-3
+    assert rel_l2(o.numpy(), ref) <= 1e-3
+    ob = tsk.flash_attn_ext(*(tsk.bf16_to_device(b) for b in bits), scale=0.125, out_dtype="bf16")
+    assert rel_l2(orc.bf16_bits_to_f32(ob.numpy()), ref) <= 5e-3
 
 
 def test_mask_gqa_softcap_alibi(env):
     """T5-style additive per-head bias + pad mask (config 4 path), GQA, softcap, ALiBi."""
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(4)
     B, H, Hkv, N = 1, 8, 4, 130
     q = rng.standard_normal((B, H, N, 64)).astype(np.float32)
@@ -82,25 +76,25 @@ def test_mask_gqa_softcap_alibi(env):
     v = rng.standard_normal((B, Hkv, N, 64)).astype(np.float16)
     mask = rng.standard_normal((1, H, N, N)).astype(np.float16)
     mask[..., N - 20:] = -np.inf                                   # padded keys
-    dev = lambda a: torch.from_numpy(a).cuda()
+    dev = tsk.to_device
     o = tsk.flash_attn_ext(dev(q), dev(k), dev(v), mask=dev(mask), scale=1.0)
     ref = orc.flash_attn_ext(q, k, v, mask=mask, scale=1.0)
-    assert rel_l2(o.cpu().numpy(), ref) <= 1e-3
+    assert rel_l2(o.numpy(), ref) <= 1e-3
     o = tsk.flash_attn_ext(dev(q), dev(k), dev(v), mask=dev(mask), scale=0.125, max_bias=8.0, softcap=30.0)
     ref = orc.flash_attn_ext(q, k, v, mask=mask, scale=0.125, max_bias=8.0, softcap=30.0)
-    assert rel_l2(o.cpu().numpy(), ref) <= 1e-3
+    assert rel_l2(o.numpy(), ref) <= 1e-3
 
 
 def test_fully_masked_rows_and_ragged_kv(env):
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(5)
     q = rng.standard_normal((1, 2, 20, 64)).astype(np.float32)
     k = rng.standard_normal((1, 2, 37, 64)).astype(np.float32)
     v = rng.standard_normal((1, 2, 37, 64)).astype(np.float32)
     mask = np.zeros((1, 1, 32, 37), np.float16)
     mask[0, 0, 3, :] = -np.inf
-    dev = lambda a: torch.from_numpy(a).cuda()
-    o = tsk.flash_attn_ext(dev(q), dev(k), dev(v), mask=dev(mask)).cpu().numpy()
+    dev = tsk.to_device
+    o = tsk.flash_attn_ext(dev(q), dev(k), dev(v), mask=dev(mask)).numpy()
     ref = orc.flash_attn_ext(q, k, v, mask=mask)
     assert np.all(np.isfinite(o)) and np.all(o[0, 3] == 0)
     assert rel_l2(o, ref) <= 1e-5
@@ -108,13 +102,13 @@ def test_fully_masked_rows_and_ragged_kv(env):
 
 def test_strided_views_and_determinism(env):
     """q/k/v as permuted views of one qkv buffer (no copies), run twice bit-equal."""
-    tsk, torch, orc = env
+    tsk, orc = env
     rng = np.random.default_rng(6)
     qkv = rng.standard_normal((2, 3, 16, 100, 64)).astype(np.float32)   # ggml ne [64,100,16,3,2]
-    t = torch.from_numpy(qkv).cuda()
-    q, k, v = t[:, 0], t[:, 1], t[:, 2]
-    o1 = tsk.flash_attn_ext(q, k, v).cpu().numpy()
-    o2 = tsk.flash_attn_ext(q, k, v).cpu().numpy()
+    t = tsk.to_device(qkv)
+    q, k, v = t.select(1, 0), t.select(1, 1), t.select(1, 2)
+    o1 = tsk.flash_attn_ext(q, k, v).numpy()
+    o2 = tsk.flash_attn_ext(q, k, v).numpy()
     assert np.array_equal(o1, o2)
     ref = orc.flash_attn_ext(qkv[:, 0], qkv[:, 1], qkv[:, 2])
     assert rel_l2(o1, ref) <= 1e-5

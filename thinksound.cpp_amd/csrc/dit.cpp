@@ -1,7 +1,212 @@
-// dit.cpp — MM-DiT step driver (placeholder entry points until the driver lands)
+// dit.cpp — MM-DiT flow-step driver and CFG sampler on gfx950 (counterpart of
+// ts_dit, src/mmdit.h:9-42 / src/mmdit.cpp:119-376).
+//
+// One forward() runs, for B batch rows (CFG cond/uncond as B = 2):
+//   host: t-embedding frequencies (mmdit.cpp:305-314), uploaded;
+//   t_embed MLP (:158-160) -> silu(cond);
+//   ONE launch for every block's adaLN GEMV (they only depend on cond);
+//   input projection; 7 joint blocks (latent + text streams, the last text
+//   stream pre_only, :238-271) and 14 fused blocks (:275-281), each:
+//     LN+modulate -> QKV GEMM -> split/RMSNorm/RoPE into the attention
+//     layout -> flash attention over the concatenated tokens ->
+//     out-proj GEMM with fused gate*residual -> LN+modulate ->
+//     fc1 GEMM with fused GELU -> fc2 GEMM with fused gate*residual;
+//   final adaLN/LN/modulate + output projection (:285-289).
+// Weights are stored once as bf16 (matrices) / f32 (biases, norm weights);
+// the QKV rows are permuted from the reference's interleaved (h d j) order
+// (split_qkv, mmdit.cpp:67-76) to [q | k | v] blocks at load, which is exact.
+// Activations live in preallocated device buffers sized for max_batch x
+// max_latent; nothing is allocated per forward.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
 #include "../../include/tsk/tsk.h"
+#include "tsk_internal.h"
 #include "tsk_runtime.h"
 
+using namespace tsk;
+
+namespace {
+
+struct WInfo {
+    std::string name;
+    int64_t ne0, ne1;      // ggml ne: [in, out] for matrices, [n] for vectors
+    bool matrix;           // stored bf16
+    bool qkv_perm;         // rows (or entries) permuted (h d j) -> [q | k | v]
+    size_t offset;         // bytes into the weight blob
+};
+
+struct RoleTiming {
+    std::vector<hipEvent_t> ev;   // start/stop pairs, reused across resets
+    size_t used = 0;
+    int64_t launches = 0;
+    double flop = 0.0, bytes = 0.0;
+};
+
+struct StreamW {           // one MMDitSingleBlock's weights
+    const uint16_t *ada_w, *qkv_w, *l1_w, *fc1_w, *fc2_w;
+    const float *ada_b, *qkv_b, *qn, *kn, *l1_b, *fc1_b, *fc2_b;
+    bool pre_only;
+    float *mod;            // [max_batch][nmod * H] adaLN output
+    int nmod;
+};
+
+}  // namespace
+
+struct tsk_dit {
+    tsk_dit_config cfg;
+    std::vector<WInfo> w;
+    std::unordered_map<std::string, int> idx;
+    char *blob = nullptr;
+    size_t blob_bytes = 0;
+    std::vector<StreamW> joint_lat, joint_txt, fused;
+    // activations
+    float *lat = nullptr, *txt = nullptr, *flow = nullptr, *xf = nullptr;
+    float *temb = nullptr, *tmp_c = nullptr, *cvec = nullptr;
+    float *mods = nullptr;
+    float *final_mod = nullptr;     // [max_batch][2H] final-layer adaLN output
+    float *qkv = nullptr;           // [rows][3H] f32 QKV projection
+    uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *h = nullptr;
+    GemvJob *jobs_dev = nullptr;    // [adaLN jobs..., t_embed.0, t_embed.2]
+    int njobs = 0, max_job_m = 0;
+    float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
+    bool timing = false;
+    RoleTiming rt[TSK_ROLE_COUNT];
+    // sampler buffers
+    float *s_x = nullptr, *s_x2 = nullptr, *s_text2 = nullptr, *s_flow2 = nullptr, *s_flow0 = nullptr;
+};
+
+namespace {
+
+int hipcheck(hipError_t e, const char *what) { return e == hipSuccess ? TSK_OK : hip_fail(e, what); }
+
+// Records an event pair around the launches made in its lifetime when the
+// driver's timing is enabled, and books their algorithmic FLOPs / bytes.
+struct Timed {
+    RoleTiming *r = nullptr;
+    hipEvent_t stop = nullptr;
+    hipStream_t st;
+    Timed(tsk_dit *d, int role, double flop, double bytes, hipStream_t s) : st(s) {
+        if (!d->timing) return;
+        r = &d->rt[role];
+        if (r->used + 2 > r->ev.size()) {
+            hipEvent_t a, b;
+            if (hipEventCreate(&a) != hipSuccess) { r = nullptr; return; }
+            if (hipEventCreate(&b) != hipSuccess) { (void) hipEventDestroy(a); r = nullptr; return; }
+            r->ev.push_back(a);
+            r->ev.push_back(b);
+        }
+        hipEvent_t start = r->ev[r->used];
+        stop = r->ev[r->used + 1];
+        r->used += 2;
+        r->launches += 1;
+        r->flop += flop;
+        r->bytes += bytes;
+        (void) hipEventRecord(start, st);
+    }
+    ~Timed() {
+        if (r) (void) hipEventRecord(stop, st);
+    }
+};
+
+void add(tsk_dit *d, const std::string &name, int64_t ne0, int64_t ne1, bool matrix, bool perm = false) {
+    WInfo wi;
+    wi.name = name;
+    wi.ne0 = ne0;
+    wi.ne1 = ne1;
+    wi.matrix = matrix;
+    wi.qkv_perm = perm;
+    wi.offset = 0;
+    d->idx[name] = (int) d->w.size();
+    d->w.push_back(wi);
+}
+
+void add_block(tsk_dit *d, const std::string &p, bool pre_only) {
+    const int H = d->cfg.hidden, F = d->cfg.mlp_hidden, hd = d->cfg.head_dim;
+    const int nmod = pre_only ? 2 : 6;
+    add(d, p + ".adaLN_modulation.1.weight", H, nmod * H, true);
+    add(d, p + ".adaLN_modulation.1.bias", nmod * H, 1, false);
+    add(d, p + ".attn.qkv.weight", H, 3 * H, true, true);
+    add(d, p + ".attn.qkv.bias", 3 * H, 1, false, true);
+    add(d, p + ".attn.q_norm.weight", hd, 1, false);
+    add(d, p + ".attn.k_norm.weight", hd, 1, false);
+    if (!pre_only) {
+        add(d, p + ".linear1.weight", H, H, true);
+        add(d, p + ".linear1.bias", H, 1, false);
+        add(d, p + ".ffn.fc1.weight", H, F, true);
+        add(d, p + ".ffn.fc1.bias", F, 1, false);
+        add(d, p + ".ffn.fc2.weight", F, H, true);
+        add(d, p + ".ffn.fc2.bias", H, 1, false);
+    }
+}
+
+template <class T> T *wptr(tsk_dit *d, const std::string &name) {
+    return (T *) (d->blob + d->w[d->idx.at(name)].offset);
+}
+
+StreamW stream_weights(tsk_dit *d, const std::string &p, bool pre_only) {
+    StreamW s;
+    memset(&s, 0, sizeof(s));
+    s.pre_only = pre_only;
+    s.nmod = pre_only ? 2 : 6;
+    s.ada_w = wptr<uint16_t>(d, p + ".adaLN_modulation.1.weight");
+    s.ada_b = wptr<float>(d, p + ".adaLN_modulation.1.bias");
+    s.qkv_w = wptr<uint16_t>(d, p + ".attn.qkv.weight");
+    s.qkv_b = wptr<float>(d, p + ".attn.qkv.bias");
+    s.qn = wptr<float>(d, p + ".attn.q_norm.weight");
+    s.kn = wptr<float>(d, p + ".attn.k_norm.weight");
+    if (!pre_only) {
+        s.l1_w = wptr<uint16_t>(d, p + ".linear1.weight");
+        s.l1_b = wptr<float>(d, p + ".linear1.bias");
+        s.fc1_w = wptr<uint16_t>(d, p + ".ffn.fc1.weight");
+        s.fc1_b = wptr<float>(d, p + ".ffn.fc1.bias");
+        s.fc2_w = wptr<uint16_t>(d, p + ".ffn.fc2.weight");
+        s.fc2_b = wptr<float>(d, p + ".ffn.fc2.bias");
+    }
+    return s;
+}
+
+int validate_cfg(const tsk_dit_config *c) {
+    if (!c) return fail(TSK_ERR_INVALID_ARG, "cfg is NULL");
+    if (c->head_dim != 64) return fail(TSK_ERR_UNSUPPORTED, "head_dim must be 64");
+    if (c->hidden != c->n_head * c->head_dim) return fail(TSK_ERR_SHAPE, "hidden != n_head * head_dim");
+    if (c->n_head < 1 || c->n_head > 64) return fail(TSK_ERR_SHAPE, "n_head %d", c->n_head);
+    if (c->depth < c->fused_depth || c->depth - c->fused_depth < 1 || c->fused_depth < 0)
+        return fail(TSK_ERR_SHAPE, "depth %d / fused_depth %d", c->depth, c->fused_depth);
+    if (c->mlp_kind != TSK_MLP_GELU_TANH) return fail(TSK_ERR_UNSUPPORTED, "mlp_kind %d", c->mlp_kind);
+    if (c->weight_type != TSK_TYPE_BF16) return fail(TSK_ERR_UNSUPPORTED, "DiT weights must be BF16");
+    if (c->mlp_hidden % 64 || c->latent_dim % 8 || c->latent_dim < 8 || c->text_seq < 1)
+        return fail(TSK_ERR_SHAPE, "mlp_hidden %% 64, latent_dim %% 8");
+    if (c->max_batch < 1 || c->max_batch > 32 || c->max_latent < 1) return fail(TSK_ERR_SHAPE, "capacity");
+    if (!(c->ln_eps > 0) || !(c->qk_eps > 0) || !(c->rope_theta > 0) || !(c->t_max_period > 0))
+        return fail(TSK_ERR_INVALID_ARG, "eps / theta / period");
+    return TSK_OK;
+}
+
+// GEMM helper: Y[n, m] for n < N rows of x
+int gemm(const uint16_t *W, const float *bias, const void *x, bool x_f32, int64_t ld_x, int N, int K, int M,
+         int epi, void *y, bool y_bf16, int64_t ld_y, float *res, const float *gate, int64_t ld_gate,
+         int rows_per_gate, hipStream_t s, int x_group_rows = 0, int64_t x_group_stride = 0, bool x_split = false) {
+    GemmParams p;
+    memset(&p, 0, sizeof(p));
+    p.x = x; p.w = W; p.bias = bias; p.y = y; p.res = res; p.gate = gate;
+    p.ld_x = ld_x; p.ld_w = K; p.ld_y = ld_y; p.ld_res = M; p.ld_gate = ld_gate;
+    p.x_group_rows = x_group_rows; p.x_group_stride = x_group_stride;
+    p.M = M; p.N = N; p.K = K;
+    p.rows_per_gate = rows_per_gate > 0 ? rows_per_gate : 1;
+    p.x_f32 = x_f32; p.y_bf16 = y_bf16; p.epi = epi; p.x_split = x_split;
+    return hipcheck(launch_gemm_bf16(p, s), "gemm");
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ config / lifecycle
 extern "C" void tsk_dit_default_config(tsk_dit_config *c) {
     if (!c) return;
     c->hidden = 1024; c->n_head = 16; c->head_dim = 64; c->depth = 21; c->fused_depth = 14;
@@ -9,11 +214,426 @@ extern "C" void tsk_dit_default_config(tsk_dit_config *c) {
     c->weight_type = TSK_TYPE_BF16; c->max_batch = 2; c->max_latent = 646;
     c->rope_theta = 10000.0f; c->t_max_period = 1.0f; c->ln_eps = 1e-5f; c->qk_eps = 1e-6f;
 }
-extern "C" int tsk_dit_create(const tsk_dit_config *, tsk_dit **out) { if (out) *out = nullptr; return tsk::fail(TSK_ERR_UNSUPPORTED, "dit driver not built"); }
-extern "C" void tsk_dit_destroy(tsk_dit *) {}
-extern "C" int tsk_dit_n_tensors(const tsk_dit *) { return 0; }
-extern "C" int tsk_dit_tensor_info(const tsk_dit *, int, const char **, int64_t *) { return TSK_ERR_UNSUPPORTED; }
-extern "C" int tsk_dit_set_tensor(tsk_dit *, const char *, const float *, int64_t) { return TSK_ERR_UNSUPPORTED; }
-extern "C" int tsk_dit_forward(tsk_dit *, int, int, const float *, const float *, const float *, float *, tsk_stream) { return TSK_ERR_UNSUPPORTED; }
-extern "C" int tsk_dit_forward_device(tsk_dit *, int, int, const float *, const float *, const float *, float *, tsk_stream) { return TSK_ERR_UNSUPPORTED; }
-extern "C" int tsk_dit_sample(tsk_dit *, int, const float *, const float *, const float *, int, float, float *, float *, tsk_stream) { return TSK_ERR_UNSUPPORTED; }
+
+extern "C" void tsk_dit_destroy(tsk_dit *d) {
+    if (!d) return;
+    (void) hipDeviceSynchronize();
+    for (auto &r : d->rt)
+        for (hipEvent_t e : r.ev) (void) hipEventDestroy(e);
+    void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->qkv,
+                    d->q, d->k, d->v, d->o, d->h, d->jobs_dev, d->freq,
+                    d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
+    for (void *b : bufs)
+        if (b) (void) hipFree(b);
+    delete d;
+}
+
+extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
+    if (!out) return fail(TSK_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    int rc = validate_cfg(cfg);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    tsk_dit *d = new tsk_dit();
+    d->cfg = *cfg;
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden, nj = c.depth - c.fused_depth;
+    add(d, "audio_input_proj.weight", c.latent_dim, H, true);
+    add(d, "audio_input_proj.bias", H, 1, false);
+    add(d, "t_embed.mlp.0.weight", H, H, true);
+    add(d, "t_embed.mlp.0.bias", H, 1, false);
+    add(d, "t_embed.mlp.2.weight", H, H, true);
+    add(d, "t_embed.mlp.2.bias", H, 1, false);
+    for (int i = 0; i < nj; ++i) {
+        add_block(d, "joint_blocks." + std::to_string(i) + ".latent_block", false);
+        add_block(d, "joint_blocks." + std::to_string(i) + ".text_block", i == nj - 1);
+    }
+    for (int i = 0; i < c.fused_depth; ++i) add_block(d, "fused_blocks." + std::to_string(i), false);
+    add(d, "final_layer.adaLN_modulation.1.weight", H, 2 * H, true);
+    add(d, "final_layer.adaLN_modulation.1.bias", 2 * H, 1, false);
+    add(d, "final_layer.linear.weight", H, c.latent_dim, true);
+    add(d, "final_layer.linear.bias", c.latent_dim, 1, false);
+    size_t off = 0;
+    for (auto &wi : d->w) {
+        wi.offset = off;
+        off += ((size_t) (wi.ne0 * wi.ne1) * (wi.matrix ? 2 : 4) + 255) & ~(size_t) 255;
+    }
+    d->blob_bytes = off;
+
+    const int B = c.max_batch, T = c.max_latent, St = c.text_seq, F = c.mlp_hidden;
+    const int64_t rows = (int64_t) B * (T + St);
+    auto alloc = [&](void **p, size_t bytes) -> int {
+        hipError_t e = hipMalloc(p, bytes);
+        if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return TSK_OK;
+    };
+    // adaLN outputs: one region per stream block + final layer
+    size_t mod_floats = 0;
+    const int nstreams = 2 * nj + c.fused_depth;
+    mod_floats = (size_t) B * 6 * H * nstreams + (size_t) B * 2 * H;
+    if ((rc = alloc((void **) &d->blob, d->blob_bytes)) ||
+        (rc = alloc((void **) &d->lat, sizeof(float) * B * T * H)) ||
+        (rc = alloc((void **) &d->txt, sizeof(float) * B * St * H)) ||
+        (rc = alloc((void **) &d->flow, sizeof(float) * B * T * c.latent_dim)) ||
+        (rc = alloc((void **) &d->xf, sizeof(float) * B * T * H)) ||
+        (rc = alloc((void **) &d->temb, sizeof(float) * B * H)) ||
+        (rc = alloc((void **) &d->tmp_c, sizeof(float) * B * H)) ||
+        (rc = alloc((void **) &d->cvec, sizeof(float) * B * H)) ||
+        (rc = alloc((void **) &d->mods, sizeof(float) * mod_floats)) ||
+        (rc = alloc((void **) &d->xn, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->qkv, 4 * rows * 3 * H)) ||
+        (rc = alloc((void **) &d->q, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->k, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->v, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->o, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->h, 2 * rows * F)) ||
+        (rc = alloc((void **) &d->jobs_dev, sizeof(GemvJob) * (nstreams + 3))) ||
+        (rc = alloc((void **) &d->freq, sizeof(float) * (H / 2)))) {
+        tsk_dit_destroy(d);
+        return rc;
+    }
+    // t-embedding frequencies exactly as the host code of mmdit.cpp:308-310
+    std::vector<float> fr(H / 2);
+    const float fscale_t = 10000.0f / c.t_max_period;
+    for (int kk = 0; kk < H / 2; ++kk) fr[kk] = fscale_t * powf(10000.0f, -2.0f * (float) kk / (float) H);
+    hipError_t e = hipMemcpy(d->freq, fr.data(), sizeof(float) * (H / 2), hipMemcpyHostToDevice);
+    if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemcpy freq"); }
+    e = hipMemset(d->blob, 0, d->blob_bytes);
+    if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemset"); }
+
+    // per-stream weights and adaLN job table
+    std::vector<GemvJob> jobs;
+    float *mp = d->mods;
+    auto mk = [&](StreamW s) {
+        s.mod = mp;
+        mp += (size_t) B * 6 * H;
+        GemvJob j;
+        j.w = s.ada_w; j.bias = s.ada_b; j.x = d->cvec; j.out = s.mod; j.M = s.nmod * H;
+        j.silu_out = 0; j.ld_out = (int64_t) s.nmod * H;
+        jobs.push_back(j);
+        return s;
+    };
+    for (int i = 0; i < nj; ++i) {
+        d->joint_lat.push_back(mk(stream_weights(d, "joint_blocks." + std::to_string(i) + ".latent_block", false)));
+        d->joint_txt.push_back(mk(stream_weights(d, "joint_blocks." + std::to_string(i) + ".text_block", i == nj - 1)));
+    }
+    for (int i = 0; i < c.fused_depth; ++i) d->fused.push_back(mk(stream_weights(d, "fused_blocks." + std::to_string(i), false)));
+    GemvJob fj;
+    fj.w = wptr<uint16_t>(d, "final_layer.adaLN_modulation.1.weight");
+    fj.bias = wptr<float>(d, "final_layer.adaLN_modulation.1.bias");
+    fj.x = d->cvec;
+    fj.out = mp;
+    d->final_mod = mp;
+    fj.M = 2 * H;
+    fj.silu_out = 0;
+    fj.ld_out = 2 * H;
+    jobs.push_back(fj);
+    d->njobs = (int) jobs.size();
+    // t_embed MLP (f32 activations): silu(W0 temb + b0) -> silu(W2 . + b2) = silu(cond)
+    GemvJob t0, t2;
+    t0.w = wptr<uint16_t>(d, "t_embed.mlp.0.weight"); t0.bias = wptr<float>(d, "t_embed.mlp.0.bias");
+    t0.x = d->temb; t0.out = d->tmp_c; t0.M = H; t0.silu_out = 1; t0.ld_out = H;
+    t2.w = wptr<uint16_t>(d, "t_embed.mlp.2.weight"); t2.bias = wptr<float>(d, "t_embed.mlp.2.bias");
+    t2.x = d->tmp_c; t2.out = d->cvec; t2.M = H; t2.silu_out = 1; t2.ld_out = H;
+    jobs.push_back(t0);
+    jobs.push_back(t2);
+    d->max_job_m = 6 * H;
+    e = hipMemcpy(d->jobs_dev, jobs.data(), sizeof(GemvJob) * jobs.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemcpy jobs"); }
+    *out = d;
+    return TSK_OK;
+}
+
+extern "C" int tsk_dit_n_tensors(const tsk_dit *d) { return d ? (int) d->w.size() : 0; }
+
+extern "C" int tsk_dit_tensor_info(const tsk_dit *d, int i, const char **name, int64_t ne[4]) {
+    if (!d || i < 0 || i >= (int) d->w.size()) return fail(TSK_ERR_INVALID_ARG, "tensor index %d", i);
+    if (name) *name = d->w[i].name.c_str();
+    if (ne) { ne[0] = d->w[i].ne0; ne[1] = d->w[i].ne1; ne[2] = 1; ne[3] = 1; }
+    return TSK_OK;
+}
+
+// host f32 -> device (bf16 for matrices), with the (h d j) -> [q|k|v] row permutation
+extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src, int64_t n) {
+    if (!d || !name || !src) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = d->idx.find(name);
+    if (it == d->idx.end()) return fail(TSK_ERR_INVALID_ARG, "unknown tensor '%s'", name);
+    const WInfo &wi = d->w[it->second];
+    if (n != wi.ne0 * wi.ne1) return fail(TSK_ERR_SHAPE, "'%s' has %lld elements, got %lld", name, (long long) (wi.ne0 * wi.ne1), (long long) n);
+    const int H = d->cfg.hidden;
+    std::vector<float> perm;
+    const float *s = src;
+    if (wi.qkv_perm) {
+        // source row r = 3*i + j (i = h*64 + d) -> destination row j*H + i
+        const int64_t rowlen = wi.matrix ? wi.ne0 : 1;
+        perm.resize((size_t) n);
+        for (int64_t i = 0; i < H; ++i)
+            for (int j = 0; j < 3; ++j)
+                memcpy(&perm[(size_t) ((j * H + i) * rowlen)], src + (3 * i + j) * rowlen, sizeof(float) * rowlen);
+        s = perm.data();
+    }
+    char *dst = d->blob + wi.offset;
+    hipError_t e;
+    if (wi.matrix) {
+        std::vector<uint16_t> bf((size_t) n);
+        for (int64_t i = 0; i < n; ++i) {
+            uint32_t x;
+            memcpy(&x, &s[i], 4);
+            if ((x & 0x7fffffffu) > 0x7f800000u) bf[i] = (uint16_t) ((x >> 16) | 64u);
+            else bf[i] = (uint16_t) ((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+        }
+        e = hipMemcpy(dst, bf.data(), 2 * (size_t) n, hipMemcpyHostToDevice);
+    } else {
+        e = hipMemcpy(dst, s, 4 * (size_t) n, hipMemcpyHostToDevice);
+    }
+    return hipcheck(e, "set_tensor copy");
+}
+
+// ------------------------------------------------------------------ forward
+namespace {
+
+int run_block_stream_pre(tsk_dit *d, const StreamW &sw, const float *x, int B, int S, int rope, uint16_t *xn,
+                         float *qkv, int Ntot, int tok_off, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden, rows = B * S;
+    const int64_t ldm = (int64_t) sw.nmod * H;
+    hipError_t e;
+    {
+        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * H, 6.0 * rows * H + 8.0 * B * H, st);
+        e = launch_ln_modulate(x, H, rows, H, S, sw.mod, sw.mod + H, ldm, c.ln_eps, xn, H, st);
+    }
+    if (e != hipSuccess) return hip_fail(e, "ln_modulate");
+    int rc;
+    {
+        Timed tm(d, TSK_ROLE_QKV, 2.0 * rows * H * 3 * H, 2.0 * 3 * H * H + 2.0 * rows * H + 4.0 * rows * 3 * H + 12.0 * H, st);
+        rc = gemm(sw.qkv_w, sw.qkv_b, xn, false, H, rows, H, 3 * H, EPI_STORE, qkv, false, 3 * H, nullptr, nullptr,
+                  0, 0, st);
+    }
+    if (rc) return rc;
+    const float theta_scale = powf(c.rope_theta, -2.0f / (float) c.head_dim);
+    {
+        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * 2 * H, 18.0 * rows * H, st);
+        e = launch_qkv_prologue(qkv, rows, S, c.n_head, sw.qn, sw.kn, c.qk_eps, rope, theta_scale, 1.0f, d->q, d->k,
+                                d->v, Ntot, tok_off, st);
+    }
+    return hipcheck(e, "qkv_prologue");
+}
+
+int run_block_stream_post(tsk_dit *d, const StreamW &sw, float *x, int B, int S, int Ntot, int tok_off,
+                          hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden, F = c.mlp_hidden, rows = B * S;
+    const int64_t ldm = (int64_t) sw.nmod * H;
+    // x += gate_msa * (linear1(o) + b); o rows of this stream: o[b][tok_off + s]
+    int rc;
+    {
+        Timed tm(d, TSK_ROLE_OUT, 2.0 * rows * H * H, 2.0 * H * H + 2.0 * rows * H + 8.0 * rows * H, st);
+        rc = gemm(sw.l1_w, sw.l1_b, d->o + (size_t) tok_off * H, false, H, rows, H, H, EPI_GATE_RES, nullptr, false,
+                  0, x, sw.mod + 2 * H, ldm, S, st, S, (int64_t) Ntot * H);
+    }
+    if (rc) return rc;
+    hipError_t e;
+    {
+        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * H, 6.0 * rows * H + 8.0 * B * H, st);
+        e = launch_ln_modulate(x, H, rows, H, S, sw.mod + 3 * H, sw.mod + 4 * H, ldm, c.ln_eps, d->xn, H, st);
+    }
+    if (e != hipSuccess) return hip_fail(e, "ln_modulate");
+    {
+        Timed tm(d, TSK_ROLE_FC1, 2.0 * rows * H * F, 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F, st);
+        rc = gemm(sw.fc1_w, sw.fc1_b, d->xn, false, H, rows, H, F, EPI_GELU, d->h, true, F, nullptr, nullptr, 0, 0, st);
+    }
+    if (rc) return rc;
+    Timed tm(d, TSK_ROLE_FC2, 2.0 * rows * F * H, 2.0 * H * F + 2.0 * rows * F + 8.0 * rows * H, st);
+    return gemm(sw.fc2_w, sw.fc2_b, d->h, false, F, rows, F, H, EPI_GATE_RES, nullptr, false, 0, x, sw.mod + 5 * H,
+                ldm, S, st);
+}
+
+int attention(tsk_dit *d, int B, int Ntot, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.q = d->q; p.k = d->k; p.v = d->v; p.o = d->o;
+    p.q_type = p.kv_type = TSK_TYPE_F16;
+    p.out_bf16 = 1;
+    p.mask_f16 = 1;
+    p.Nq = p.Nkv = Ntot; p.H = p.Hkv = c.n_head; p.B = B;
+    p.q_nb1 = p.k_nb1 = p.v_nb1 = 128;
+    p.q_nb2 = p.k_nb2 = p.v_nb2 = (int64_t) 128 * Ntot;
+    p.q_nb3 = p.k_nb3 = p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;
+    p.m_ne2 = p.m_ne3 = 1;
+    p.o_nb1 = 128; p.o_nb2 = (int64_t) 128 * c.n_head; p.o_nb3 = (int64_t) 128 * c.n_head * Ntot;
+    p.scale = 1.0f / sqrtf((float) c.head_dim);
+    p.n_head_log2 = 1;
+    const double nn = (double) Ntot * Ntot;
+    Timed tm(d, TSK_ROLE_ATTN, 4.0 * B * c.n_head * nn * c.head_dim, 4.0 * 2.0 * B * Ntot * c.hidden, st);
+    return hipcheck(launch_attention(p, st), "attention");
+}
+
+int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host, const float *text_d,
+                 float *flow_d, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden, St = c.text_seq, nj = c.depth - c.fused_depth;
+    // timestep frequency embedding [cos(t f), sin(t f)] (mmdit.cpp:305-314); t by value
+    TimeVals tv;
+    for (int b = 0; b < 32; ++b) tv.t[b] = b < B ? t_host[b] : 0.0f;
+    hipError_t e = launch_timestep_embed(d->freq, tv, B, H, d->temb, st);
+    if (e != hipSuccess) return hip_fail(e, "timestep embed");
+    int rc;
+    // t_embed MLP -> silu(cond) (mmdit.cpp:158-160, :209), f32 activations
+    {
+        Timed tm(d, TSK_ROLE_ADALN, 4.0 * B * H * H, 4.0 * H * H, st);
+        if ((e = launch_gemv_jobs(d->jobs_dev + d->njobs, 1, H, B, H, st)) != hipSuccess) return hip_fail(e, "t_embed.0");
+        if ((e = launch_gemv_jobs(d->jobs_dev + d->njobs + 1, 1, H, B, H, st)) != hipSuccess) return hip_fail(e, "t_embed.2");
+    }
+    // every adaLN modulation of the step in one launch
+    {
+        const double mtot = (double) H * (6.0 * (2 * nj + c.fused_depth) - 4.0 + 2.0);
+        Timed tm(d, TSK_ROLE_ADALN, 2.0 * B * mtot * H, 2.0 * mtot * H, st);
+        if ((e = launch_gemv_jobs(d->jobs_dev, d->njobs, d->max_job_m, B, H, st)) != hipSuccess)
+            return hip_fail(e, "adaln gemv");
+    }
+    // input projection (f32-accurate split activations), text stream copy
+    {
+        Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
+        rc = gemm(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d, true,
+                  c.latent_dim, B * T, c.latent_dim, H, EPI_STORE, d->lat, false, H, nullptr, nullptr, 0, 0, st, 0, 0, true);
+    }
+    if (rc) return rc;
+    if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
+        return hip_fail(e, "text copy");
+
+    const int Nj = T + St;
+    for (int i = 0; i < nj; ++i) {
+        const StreamW &L = d->joint_lat[i], &X = d->joint_txt[i];
+        if ((rc = run_block_stream_pre(d, L, d->lat, B, T, 1, d->xn, d->qkv, Nj, 0, st))) return rc;
+        if ((rc = run_block_stream_pre(d, X, d->txt, B, St, 0, d->xn, d->qkv, Nj, T, st))) return rc;
+        if ((rc = attention(d, B, Nj, st))) return rc;
+        if ((rc = run_block_stream_post(d, L, d->lat, B, T, Nj, 0, st))) return rc;
+        if (!X.pre_only && (rc = run_block_stream_post(d, X, d->txt, B, St, Nj, T, st))) return rc;
+    }
+    for (int i = 0; i < c.fused_depth; ++i) {
+        const StreamW &L = d->fused[i];
+        if ((rc = run_block_stream_pre(d, L, d->lat, B, T, 1, d->xn, d->qkv, T, 0, st))) return rc;
+        if ((rc = attention(d, B, T, st))) return rc;
+        if ((rc = run_block_stream_post(d, L, d->lat, B, T, T, 0, st))) return rc;
+    }
+    // final layer: adaLN (shift, scale) -> LN/modulate (f32) -> linear to latent_dim
+    const float *fmod = d->final_mod;
+    Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * H * c.latent_dim, 12.0 * B * T * H + 2.0 * H * c.latent_dim, st);
+    if ((e = launch_ln_modulate_f32(d->lat, H, B * T, H, T, fmod, fmod + H, 2 * H, c.ln_eps, d->xf, H, st)) != hipSuccess)
+        return hip_fail(e, "final ln_modulate");
+    return gemm(wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf,
+                true, H, B * T, H, c.latent_dim, EPI_STORE, flow_d, false, c.latent_dim, nullptr, nullptr, 0, 0, st,
+                0, 0, true);
+}
+
+int check_forward_args(tsk_dit *d, int B, int T, const void *a, const void *t, const void *b, const void *f) {
+    if (!d || !a || !t || !b || !f) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    if (B < 1 || B > d->cfg.max_batch) return fail(TSK_ERR_SHAPE, "B=%d outside [1, %d]", B, d->cfg.max_batch);
+    if (T < 1 || T > d->cfg.max_latent) return fail(TSK_ERR_SHAPE, "T=%d outside [1, %d]", T, d->cfg.max_latent);
+    return require_init();
+}
+
+}  // namespace
+
+extern "C" int tsk_dit_forward_device(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host,
+                                      const float *text_d, float *flow_d, tsk_stream stream) {
+    int rc = check_forward_args(d, B, T, latent_d, t_host, text_d, flow_d);
+    if (rc) return rc;
+    return forward_impl(d, B, T, latent_d, t_host, text_d, flow_d, (hipStream_t) stream);
+}
+
+extern "C" int tsk_dit_forward(tsk_dit *d, int B, int T, const float *latent, const float *t, const float *text,
+                               float *flow, tsk_stream stream) {
+    int rc = check_forward_args(d, B, T, latent, t, text, flow);
+    if (rc) return rc;
+    const tsk_dit_config &c = d->cfg;
+    hipStream_t st = (hipStream_t) stream;
+    float *lat_d = nullptr, *txt_d = nullptr;
+    const size_t nl = (size_t) B * T * c.latent_dim, nt = (size_t) B * c.text_seq * c.hidden;
+    hipError_t e = hipMalloc((void **) &lat_d, sizeof(float) * (nl + nt));
+    if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc: %s", hipGetErrorString(e));
+    txt_d = lat_d + nl;
+    rc = hipcheck(hipMemcpyAsync(lat_d, latent, sizeof(float) * nl, hipMemcpyHostToDevice, st), "latent upload");
+    if (!rc) rc = hipcheck(hipMemcpyAsync(txt_d, text, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text upload");
+    if (!rc) rc = forward_impl(d, B, T, lat_d, t, txt_d, d->flow, st);
+    if (!rc) rc = hipcheck(hipMemcpyAsync(flow, d->flow, sizeof(float) * nl, hipMemcpyDeviceToHost, st), "flow download");
+    if (!rc) rc = hipcheck(hipStreamSynchronize(st), "stream sync");
+    (void) hipStreamSynchronize(st);
+    (void) hipFree(lat_d);
+    return rc;
+}
+
+// ------------------------------------------------------------------ sampler
+extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float *text_cond,
+                              const float *text_uncond, int steps, float cfg_scale, float *out, float *flow0,
+                              tsk_stream stream) {
+    if (!d || !noise || !text_cond || !text_uncond || !out) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    if (d->cfg.max_batch < 2) return fail(TSK_ERR_SHAPE, "CFG needs max_batch >= 2");
+    if (T < 1 || T > d->cfg.max_latent) return fail(TSK_ERR_SHAPE, "T=%d", T);
+    if (steps < 1) return fail(TSK_ERR_INVALID_ARG, "steps=%d", steps);
+    int rc = require_init();
+    if (rc) return rc;
+    const tsk_dit_config &c = d->cfg;
+    hipStream_t st = (hipStream_t) stream;
+    const size_t n = (size_t) T * c.latent_dim, nt = (size_t) c.text_seq * c.hidden;
+    if (!d->s_x) {
+        const size_t cap = (size_t) c.max_latent * c.latent_dim;
+        hipError_t e = hipMalloc((void **) &d->s_x, sizeof(float) * cap * 6 + sizeof(float) * 2 * nt);
+        if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc sampler buffers");
+        d->s_x2 = d->s_x + cap;
+        d->s_flow2 = d->s_x + 3 * cap;
+        d->s_flow0 = d->s_x + 5 * cap;
+        d->s_text2 = d->s_x + 6 * cap;
+    }
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2 + n, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_text2, text_cond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_text2 + nt, text_uncond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
+    for (int s = 0; s < steps; ++s) {
+        // linspace(1, 0, steps + 1) (mmdit.cpp:360-362)
+        const float t_curr = 1.0f - (float) s / (float) steps;
+        const float t_prev = 1.0f - (float) (s + 1) / (float) steps;
+        const float tt[2] = {t_curr, t_curr};
+        if ((rc = forward_impl(d, 2, T, d->s_x2, tt, d->s_text2, d->s_flow2, st))) return rc;
+        hipError_t e = launch_cfg_euler(d->s_flow2, (int64_t) n, cfg_scale, t_prev - t_curr, d->s_x, d->s_x2,
+                                        s == 0 ? d->s_flow0 : nullptr, st);
+        if (e != hipSuccess) return hip_fail(e, "cfg_euler");
+    }
+    if ((rc = hipcheck(hipMemcpyAsync(out, d->s_x, sizeof(float) * n, hipMemcpyDeviceToHost, st), "out"))) return rc;
+    if (flow0 && (rc = hipcheck(hipMemcpyAsync(flow0, d->s_flow0, sizeof(float) * n, hipMemcpyDeviceToHost, st), "flow0")))
+        return rc;
+    return hipcheck(hipStreamSynchronize(st), "sync");
+}
+
+// ------------------------------------------------------------------ timing
+extern "C" int tsk_dit_timing(tsk_dit *d, int enable) {
+    if (!d) return fail(TSK_ERR_INVALID_ARG, "dit is NULL");
+    if (enable) {
+        for (auto &r : d->rt) { r.used = 0; r.launches = 0; r.flop = 0.0; r.bytes = 0.0; }
+    }
+    d->timing = enable != 0;
+    return TSK_OK;
+}
+
+extern "C" int tsk_dit_timing_read(tsk_dit *d, int role, double *ms, int64_t *launches, double *flop, double *bytes) {
+    if (!d || role < 0 || role >= TSK_ROLE_COUNT) return fail(TSK_ERR_INVALID_ARG, "role %d", role);
+    RoleTiming &r = d->rt[role];
+    double total = 0.0;
+    if (r.used) {
+        hipError_t e = hipEventSynchronize(r.ev[r.used - 1]);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        for (size_t i = 0; i + 1 < r.used; i += 2) {
+            float m = 0.0f;
+            e = hipEventElapsedTime(&m, r.ev[i], r.ev[i + 1]);
+            if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+            total += m;
+        }
+    }
+    if (ms) *ms = total;
+    if (launches) *launches = r.launches;
+    if (flop) *flop = r.flop;
+    if (bytes) *bytes = r.bytes;
+    return TSK_OK;
+}

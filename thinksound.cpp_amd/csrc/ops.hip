@@ -184,10 +184,11 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
     return t;
 }
 
-// one 256-thread block per row; H % 4 == 0
+// one 256-thread block per row; H % 4 == 0; bf16 or f32 output
+template <bool YF32>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(const float *x, int64_t ld_x, int H, int rows_per_b,
                                                           const float *shift, const float *scale,
-                                                          int64_t ld_mod, float eps, uint16_t *y, int64_t ld_y) {
+                                                          int64_t ld_mod, float eps, void *y, int64_t ld_y) {
     __shared__ float red[4];
     const int r = blockIdx.x;
     const float *xr = x + (int64_t) r * ld_x;
@@ -206,28 +207,35 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(const float *x, int64_
     const float rs = 1.0f / sqrtf(var + eps);
     const int b = r / rows_per_b;
     const float *sh = shift + (int64_t) b * ld_mod, *sc = scale + (int64_t) b * ld_mod;
-    uint16_t *yr = y + (int64_t) r * ld_y;
     for (int i = threadIdx.x * 4; i < H; i += 1024) {
         f32x4 v = *(const f32x4 *) (xr + i);
-        uint16_t o[4];
-        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits((v[j] - mean) * rs * (sc[i + j] + 1.0f) + sh[i + j]);
-        u32x2 w;
-        __builtin_memcpy(&w, o, 8);
-        *(u32x2 *) (yr + i) = w;
+        float o[4];
+        for (int j = 0; j < 4; ++j) o[j] = (v[j] - mean) * rs * (sc[i + j] + 1.0f) + sh[i + j];
+        if constexpr (YF32) {
+            *(f32x4 *) ((float *) y + (int64_t) r * ld_y + i) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+            uint16_t ob[4];
+            for (int j = 0; j < 4; ++j) ob[j] = f32_to_bf16_bits(o[j]);
+            u32x2 w;
+            __builtin_memcpy(&w, ob, 8);
+            *(u32x2 *) ((uint16_t *) y + (int64_t) r * ld_y + i) = w;
+        }
     }
 }
 
-// qkv row (bf16, [q | k | v] each head-major nh x 64) -> q/k/v [B, nh, Ntot, 64] bf16
-// one 256-thread block per row (nh <= 16 per pass of 8 heads x 32 pairs)
-__global__ __launch_bounds__(256) void qkv_prologue_kernel(const uint16_t *qkv, int S, int nh, const float *qn_w,
+// qkv row (f32, [q | k | v] each head-major nh x 64) -> q/k/v [B, nh, Ntot, 64] fp16:
+// RMSNorm*w on q and k, RoPE when rope != 0, and the F16 cast of Q/K/V that
+// attention() applies before flash_attn_ext (mmdit.cpp:88-90).
+// One 256-thread block per row (8 heads x 32 pairs per pass).
+__global__ __launch_bounds__(256) void qkv_prologue_kernel(const float *qkv, int S, int nh, const float *qn_w,
                                                            const float *kn_w, float eps, int rope, float theta_scale,
                                                            float freq_scale, uint16_t *q, uint16_t *k, uint16_t *v,
                                                            int Ntot, int tok_off) {
     const int r = blockIdx.x;
     const int b = r / S, s = r % S;
     const int H = nh * 64;
-    const uint16_t *row = qkv + (int64_t) r * 3 * H;
-    const int pair = threadIdx.x & 31, hsub = threadIdx.x >> 5;     // 8 heads per pass
+    const float *row = qkv + (int64_t) r * 3 * H;
+    const int pair = threadIdx.x & 31, hsub = threadIdx.x >> 5;
     float c = 1.0f, sn = 0.0f;
     if (rope) {
         const float th = freq_scale * rope_theta((float) s, theta_scale, pair);
@@ -235,16 +243,16 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(const uint16_t *qkv, 
         sn = sinf(th);
     }
     for (int which = 0; which < 2; ++which) {
-        const uint16_t *src = row + which * H;
+        const float *src = row + which * H;
         const float *w = which ? kn_w : qn_w;
         uint16_t *dst = which ? k : q;
         for (int h0 = 0; h0 < nh; h0 += 8) {
             const int h = h0 + hsub;
             float x0 = 0.0f, x1 = 0.0f;
             if (h < nh) {
-                const uint32_t two = *(const uint32_t *) (src + h * 64 + 2 * pair);
-                x0 = bf16_bits_to_f32((uint16_t) (two & 0xffff));
-                x1 = bf16_bits_to_f32((uint16_t) (two >> 16));
+                const f32x4 two = *(const f32x4 *) (src + h * 64 + 4 * (pair >> 1));
+                x0 = (pair & 1) ? two[2] : two[0];
+                x1 = (pair & 1) ? two[3] : two[1];
             }
             float ss = x0 * x0 + x1 * x1;
             for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
@@ -257,21 +265,25 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(const uint16_t *qkv, 
             }
             if (h < nh) {
                 uint16_t *o = dst + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + 2 * pair;
-                *(uint32_t *) o = (uint32_t) f32_to_bf16_bits(x0) | ((uint32_t) f32_to_bf16_bits(x1) << 16);
+                *(uint32_t *) o = (uint32_t) f32_to_f16_bits(x0) | ((uint32_t) f32_to_f16_bits(x1) << 16);
             }
         }
     }
-    // v: plain copy, 4 elements per thread
-    const uint16_t *vs = row + 2 * H;
+    // v: F16 cast, 4 elements per thread
+    const float *vs = row + 2 * H;
     for (int i = threadIdx.x * 4; i < H; i += 1024) {
         const int h = i / 64, d = i % 64;
-        *(u32x2 *) (v + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + d) = *(const u32x2 *) (vs + i);
+        const f32x4 x = *(const f32x4 *) (vs + i);
+        uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]), f32_to_f16_bits(x[3])};
+        u32x2 w2;
+        __builtin_memcpy(&w2, o4, 8);
+        *(u32x2 *) (v + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + d) = w2;
     }
 }
 
-// adaLN GEMV list: one wave per output row; c already holds silu(cond), [B][K] f32
+// GEMV list: one wave per output row; lane k-slices of 8, f32 activations
 template <int MAXB>
-__global__ __launch_bounds__(256) void adaln_gemv_kernel(const GemvJob *jobs, const float *c, int B, int K) {
+__global__ __launch_bounds__(256) void gemv_jobs_kernel(const GemvJob *jobs, int B, int K) {
     const GemvJob jb = jobs[blockIdx.y];
     const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -286,7 +298,7 @@ __global__ __launch_bounds__(256) void adaln_gemv_kernel(const GemvJob *jobs, co
         for (int e = 0; e < 8; ++e) wv[e] = bf16_bits_to_f32(h[e]);
         for (int b = 0; b < MAXB; ++b) {
             if (b >= B) break;
-            const float *cr = c + (int64_t) b * K + k;
+            const float *cr = jb.x + (int64_t) b * K + k;
             const f32x4 c0 = *(const f32x4 *) cr, c1 = *(const f32x4 *) (cr + 4);
             acc[b] += wv[0] * c0[0] + wv[1] * c0[1] + wv[2] * c0[2] + wv[3] * c0[3] +
                       wv[4] * c1[0] + wv[5] * c1[1] + wv[6] * c1[2] + wv[7] * c1[3];
@@ -295,13 +307,27 @@ __global__ __launch_bounds__(256) void adaln_gemv_kernel(const GemvJob *jobs, co
     for (int b = 0; b < MAXB; ++b) {
         if (b >= B) break;
         const float s = wave_sum(acc[b]);
-        if (lane == 0) jb.out[(int64_t) b * jb.ld_out + j] = s + (jb.bias ? jb.bias[j] : 0.0f);
+        if (lane == 0) {
+            float v = s + (jb.bias ? jb.bias[j] : 0.0f);
+            if (jb.silu_out) v = v / (1.0f + __expf(-v));
+            jb.out[(int64_t) b * jb.ld_out + j] = v;
+        }
     }
 }
 
 __global__ void silu_kernel(float *x, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
+}
+
+__global__ void timestep_embed_kernel(const float *freq, const TimeVals tv, int B, int H, float *temb) {
+    const int half = H / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * half) return;
+    const int b = i / half, k = i % half;
+    const float a = tv.t[b] * freq[k];
+    temb[(int64_t) b * H + k] = cosf(a);
+    temb[(int64_t) b * H + half + k] = sinf(a);
 }
 
 __global__ void cfg_euler_kernel(const float *flow2, int64_t n, float cfg, float dt, float *x, float *x2,
@@ -376,12 +402,19 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 hipError_t launch_ln_modulate(const float *x, int64_t ld_x, int rows, int H, int rows_per_b, const float *shift,
                               const float *scale, int64_t ld_mod, float eps, uint16_t *y, int64_t ld_y,
                               hipStream_t s) {
-    hipLaunchKernelGGL(ln_modulate_kernel, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
-                       ld_mod, eps, y, ld_y);
+    hipLaunchKernelGGL(ln_modulate_kernel<false>, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
+                       ld_mod, eps, (void *) y, ld_y);
     return hipGetLastError();
 }
 
-hipError_t launch_qkv_prologue(const uint16_t *qkv, int rows, int S, int nh, const float *qn_w, const float *kn_w,
+hipError_t launch_ln_modulate_f32(const float *x, int64_t ld_x, int rows, int H, int rows_per_b, const float *shift,
+                                  const float *scale, int64_t ld_mod, float eps, float *y, int64_t ld_y, hipStream_t s) {
+    hipLaunchKernelGGL(ln_modulate_kernel<true>, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
+                       ld_mod, eps, (void *) y, ld_y);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_prologue(const float *qkv, int rows, int S, int nh, const float *qn_w, const float *kn_w,
                                float eps, int rope, float theta_scale, float freq_scale, uint16_t *q, uint16_t *k,
                                uint16_t *v, int Ntot, int tok_off, hipStream_t s) {
     hipLaunchKernelGGL(qkv_prologue_kernel, dim3(rows), dim3(256), 0, s, qkv, S, nh, qn_w, kn_w, eps, rope,
@@ -389,17 +422,22 @@ hipError_t launch_qkv_prologue(const uint16_t *qkv, int rows, int S, int nh, con
     return hipGetLastError();
 }
 
-hipError_t launch_adaln_gemv(const GemvJob *jobs_dev, int njobs, int max_m, const float *c, int B, int K,
-                             hipStream_t s) {
+hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K, hipStream_t s) {
     dim3 grid(blocks_for(max_m, 4), njobs);
-    if (B <= 2) hipLaunchKernelGGL(adaln_gemv_kernel<2>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
-    else if (B <= 8) hipLaunchKernelGGL(adaln_gemv_kernel<8>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
-    else hipLaunchKernelGGL(adaln_gemv_kernel<32>, grid, dim3(256), 0, s, jobs_dev, c, B, K);
+    if (B <= 2) hipLaunchKernelGGL(gemv_jobs_kernel<2>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    else if (B <= 8) hipLaunchKernelGGL(gemv_jobs_kernel<8>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    else hipLaunchKernelGGL(gemv_jobs_kernel<32>, grid, dim3(256), 0, s, jobs_dev, B, K);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb, hipStream_t s) {
+    hipLaunchKernelGGL(timestep_embed_kernel, dim3(blocks_for((int64_t) B * (H / 2), 256)), dim3(256), 0, s, freq, tv,
+                       B, H, temb);
     return hipGetLastError();
 }
 

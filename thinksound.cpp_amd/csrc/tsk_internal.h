@@ -47,9 +47,15 @@ struct GemmParams {
     float *res;              // EPI_GATE_RES: f32 residual rows of M (in/out)
     const float *gate;       // EPI_GATE_RES: gate rows of M (row stride ld_gate)
     int64_t ld_x, ld_w, ld_y, ld_res, ld_gate;  // row strides in elements
+    // optional grouping of activation rows: row n of X starts at
+    // x + (n / x_group_rows) * x_group_stride + (n % x_group_rows) * ld_x
+    // (x_group_rows == 0: plain row stride)
+    int x_group_rows;
+    int64_t x_group_stride;
     int M, N, K;
     int rows_per_gate;
     int x_f32, y_bf16, epi;
+    int x_split;             // f32 activations as bf16 hi + lo (two MFMAs): f32-grade products
     // Q8_0: activations pre-quantized into planes qx [N][K] int8 and
     // dx [N][K/32] f32 (fp16-representable scales)
     const int8_t *qx;
@@ -94,27 +100,34 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 hipError_t launch_ln_modulate(const float *x, int64_t ld_x, int rows, int H, int rows_per_b,
                               const float *shift, const float *scale, int64_t ld_mod, float eps,
                               uint16_t *y, int64_t ld_y, hipStream_t s);
-// Split the QKV GEMM output (rows of [q | k | v], head-major, bf16) into the
-// attention layout [B, nh, Ntot, 64] at token offset tok_off, applying
+hipError_t launch_ln_modulate_f32(const float *x, int64_t ld_x, int rows, int H, int rows_per_b,
+                                  const float *shift, const float *scale, int64_t ld_mod, float eps,
+                                  float *y, int64_t ld_y, hipStream_t s);
+// Split the QKV GEMM output (f32 rows of [q | k | v], head-major) into the
+// fp16 attention layout [B, nh, Ntot, 64] at token offset tok_off, applying
 // RMSNorm*w to q and k and (if rope) RoPE with position = row % S.
-hipError_t launch_qkv_prologue(const uint16_t *qkv, int rows, int S, int nh,
+hipError_t launch_qkv_prologue(const float *qkv, int rows, int S, int nh,
                                const float *qn_w, const float *kn_w, float eps, int rope,
                                float theta_scale, float freq_scale, uint16_t *q, uint16_t *k,
                                uint16_t *v, int Ntot, int tok_off, hipStream_t s);
-// out[b, j] = sum_k W[j, k] * silu(c[b, k]) + bias[j] for a list of GEMVs
+// A list of small-batch GEMVs with f32 activations (products exact in fp32):
+// out[b, j] = act( sum_k W[j, k] * x[b, k] + bias[j] ), act = silu if silu_out
 struct GemvJob {
     const uint16_t *w;     // bf16 [M][K]
-    const float *bias;     // [M]
+    const float *bias;     // [M], nullable
+    const float *x;        // [B][K] f32
     float *out;            // [B][ld_out]
     int M;
+    int silu_out;
     int64_t ld_out;
 };
-hipError_t launch_adaln_gemv(const GemvJob *jobs_dev, int njobs, int max_m, const float *c,
-                             int B, int K, hipStream_t s);
-// Timestep embedding + t_embed MLP input: temb[b, :] = [cos(t f_k), sin(t f_k)]
-hipError_t launch_timestep_embed(const float *t, int B, int H, float t_max_period, float *temb,
-                                 hipStream_t s);
+hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K,
+                            hipStream_t s);
 hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s);
+// t-embedding: temb[b, k] = cos(t_b * freq[k]), temb[b, H/2 + k] = sin(t_b * freq[k])
+struct TimeVals { float t[32]; };
+hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb,
+                                 hipStream_t s);
 // CFG combine + Euler step: x[i] += dt * (fu + (fc - fu) * cfg); flow0 optional
 hipError_t launch_cfg_euler(const float *flow2, int64_t n, float cfg, float dt, float *x,
                             float *x2, float *flow0, hipStream_t s);

@@ -2,9 +2,10 @@
 
 Mirrors the ggml operator surface that src/mmdit.cpp drives for the MM-DiT
 hot path -- mul_mat, flash_attn_ext, rms_norm*w, rope_ext, norm -- plus the
-ts_dit driver (load / forward / sample, src/mmdit.h:9-42). Tensors are torch
-tensors on the GPU; shapes are torch order, i.e. the reverse of ggml's ne[]
-(a ggml [D, N, H, B] tensor is a torch (B, H, N, D) tensor). Errors raise
+ts_dit driver (load / forward / sample, src/mmdit.h:9-42). Device tensors are
+DeviceArrays allocated through the same HIP runtime libtsk.so links (no
+second runtime in the process); shapes are numpy order, i.e. the reverse of
+ggml's ne[] (a ggml [D, N, H, B] tensor has shape (B, H, N, D)). Errors raise
 TskError with the library's status and message; nothing falls back to a CPU
 path: if libtsk.so is missing, load() raises.
 """
@@ -78,6 +79,9 @@ def load():
         "tsk_dit_forward": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_forward_device": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_sample": ([vp, i, vp, vp, vp, i, f, vp, vp, vp], i),
+        "tsk_dit_timing": ([vp, i], i),
+        "tsk_dit_timing_read": ([vp, i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
+                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -103,20 +107,179 @@ def init(device=0):
         _initialised = True
 
 
+# ---------------------------------------------------------------- device memory
+# The HIP runtime libtsk.so links (resolved by soname once libtsk is loaded),
+# so buffers, streams and events all live in the same runtime as the kernels.
+_hip = None
+DTYPES = {"f32": (F32, 4, "float32"), "f16": (F16, 2, "float16"), "bf16": (BF16, 2, "uint16"),
+          "i32": (I32, 4, "int32"), "u8": (-1, 1, "uint8")}
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        load()
+        H = ctypes.CDLL("libamdhip64.so.7")
+        vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        for nm, args in {"hipMalloc": [ctypes.POINTER(vp), sz], "hipFree": [vp],
+                         "hipMemcpy": [vp, vp, sz, i], "hipMemcpyAsync": [vp, vp, sz, i, vp],
+                         "hipMemset": [vp, i, sz], "hipDeviceSynchronize": [],
+                         "hipStreamSynchronize": [vp], "hipEventCreate": [ctypes.POINTER(vp)],
+                         "hipEventDestroy": [vp], "hipEventRecord": [vp, vp],
+                         "hipEventSynchronize": [vp],
+                         "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp]}.items():
+            getattr(H, nm).argtypes = args
+            getattr(H, nm).restype = i
+        _hip = H
+    return _hip
+
+
+def _hipcheck(rc, what):
+    if rc != 0:
+        raise TskError(-8, f"{what} failed with hipError {rc}")
+
+
+class DeviceArray:
+    """A device buffer (or a strided view of one) of dtype f32/f16/bf16/i32/u8.
+    shape/strides are numpy-style (strides in elements), C-contiguous by default."""
+
+    def __init__(self, shape, dtype="f32", _base=None, _ptr=None, _strides=None):
+        self.shape = tuple(int(x) for x in shape)
+        self.dtype = dtype
+        self.ttype, self.itemsize, self.npdtype = DTYPES[dtype]
+        if _strides is None:
+            st, acc = [], 1
+            for d in reversed(self.shape):
+                st.append(acc)
+                acc *= d
+            _strides = tuple(reversed(st))
+        self.strides = tuple(int(x) for x in _strides)
+        self._base = _base
+        if _ptr is not None:
+            self.ptr = _ptr
+        else:
+            n = 1
+            for d in self.shape:
+                n *= d
+            p = ctypes.c_void_p()
+            _hipcheck(hip().hipMalloc(ctypes.byref(p), max(n * self.itemsize, 256)), "hipMalloc")
+            self.ptr = p.value
+            self._owner = True
+
+    def __del__(self):
+        if getattr(self, "_owner", False) and self.ptr:
+            try:
+                hip().hipFree(ctypes.c_void_p(self.ptr))
+            except Exception:
+                pass
+            self.ptr = None
+
+    # accessors used by desc()
+    def stride(self, dim=None):
+        return self.strides if dim is None else self.strides[dim]
+
+    def element_size(self):
+        return self.itemsize
+
+    def data_ptr(self):
+        return self.ptr
+
+    @property
+    def nbytes(self):
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n * self.itemsize
+
+    def contiguous(self):
+        exp = DeviceArray(self.shape, self.dtype, _ptr=0).strides
+        return self.strides == exp
+
+    @staticmethod
+    def from_numpy(a, dtype=None):
+        import numpy as np
+        if dtype is None:
+            dtype = {np.dtype("float32"): "f32", np.dtype("float16"): "f16", np.dtype("int32"): "i32",
+                     np.dtype("uint8"): "u8"}[a.dtype]
+        a = np.ascontiguousarray(a)
+        d = DeviceArray(a.shape, dtype)
+        _hipcheck(hip().hipMemcpy(ctypes.c_void_p(d.ptr), ctypes.c_void_p(a.ctypes.data), a.nbytes, 1),
+                  "hipMemcpy H2D")
+        return d
+
+    def numpy(self):
+        import numpy as np
+        if not self.contiguous():
+            raise ValueError("numpy() needs a contiguous array")
+        out = np.empty(self.shape, dtype=self.npdtype)
+        synchronize()
+        _hipcheck(hip().hipMemcpy(ctypes.c_void_p(out.ctypes.data), ctypes.c_void_p(self.ptr), out.nbytes, 2),
+                  "hipMemcpy D2H")
+        return out
+
+    def view(self, offset, shape, strides):
+        """strided view starting `offset` elements into this buffer"""
+        return DeviceArray(shape, self.dtype, _base=self, _ptr=self.ptr + offset * self.itemsize,
+                           _strides=strides)
+
+    def select(self, dim, index):
+        """view with dimension `dim` fixed at `index` (like a[:, index] for dim 1)"""
+        off = index * self.strides[dim]
+        shape = self.shape[:dim] + self.shape[dim + 1:]
+        strides = self.strides[:dim] + self.strides[dim + 1:]
+        return self.view(off, shape, strides)
+
+
+def synchronize():
+    _hipcheck(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _hipcheck(hip().hipEventCreate(ctypes.byref(p)), "hipEventCreate")
+        self.h = p
+
+    def record(self, stream=None):
+        _hipcheck(hip().hipEventRecord(self.h, stream), "hipEventRecord")
+
+    def elapsed_ms(self, end):
+        _hipcheck(hip().hipEventSynchronize(end.h), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        _hipcheck(hip().hipEventElapsedTime(ctypes.byref(ms), self.h, end.h), "hipEventElapsedTime")
+        return ms.value
+
+    def __del__(self):
+        try:
+            hip().hipEventDestroy(self.h)
+        except Exception:
+            pass
+
+
+def empty(shape, dtype="f32"):
+    return DeviceArray(shape, dtype)
+
+
+def to_device(a, dtype=None):
+    return DeviceArray.from_numpy(a, dtype)
+
+
+def bf16_to_device(bits):
+    """uint16 numpy array of bf16 bit patterns -> bf16 DeviceArray"""
+    import numpy as np
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    d = DeviceArray(bits.shape, "bf16")
+    _hipcheck(hip().hipMemcpy(ctypes.c_void_p(d.ptr), ctypes.c_void_p(bits.ctypes.data), bits.nbytes, 1),
+              "hipMemcpy H2D")
+    return d
+
+
 # ---------------------------------------------------------------- descriptors
-def _ttype(t):
-    import torch
-    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32}
-    if t.dtype not in m:
-        raise TypeError(f"no tsk type for {t.dtype}")
-    return m[t.dtype]
-
-
 def desc(t, ttype=None):
-    """tsk_tensor view of a torch tensor: ne = reversed shape, nb = reversed byte strides.
-    A Q8_0 tensor is a uint8 torch tensor of shape (rows, K/32, 34)."""
+    """tsk_tensor view of a DeviceArray: ne = reversed shape, nb = reversed byte strides.
+    A Q8_0 tensor is a u8 array of shape (rows, K/32, 34)."""
     d = TskTensor()
-    ttype = _ttype(t) if ttype is None else ttype
+    ttype = t.ttype if ttype is None else ttype
     d.type = ttype
     if ttype == Q8_0:
         rows, nblk = t.shape[0], t.shape[1]
@@ -140,8 +303,7 @@ def desc(t, ttype=None):
 
 
 def _stream():
-    import torch
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return None     # the null stream
 
 
 def _ref(x):
@@ -149,14 +311,13 @@ def _ref(x):
 
 
 # ---------------------------------------------------------------- operators
-def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype=None):
+def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype="f32"):
     """ggml_mul_mat(a, b) (+bias): a (M, K) weights, b (..., N, K) -> (..., N, M)."""
-    import torch
     init()
-    at = a_type if a_type is not None else _ttype(a)
+    at = a_type if a_type is not None else a.ttype
     M = a.shape[0] if at != Q8_0_SPLIT else a.logical_shape[1]
     if out is None:
-        out = torch.empty(b.shape[:-1] + (M,), dtype=out_dtype or torch.float32, device=b.device)
+        out = DeviceArray(tuple(b.shape[:-1]) + (M,), out_dtype)
     da, db, dd = desc(a, at), desc(b), desc(out)
     dbias = desc(bias) if bias is not None else None
     check(load().tsk_mul_mat(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd), _stream()))
@@ -164,13 +325,12 @@ def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype=None):
 
 
 def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0, prec=PREC_F32,
-                   out=None, out_dtype=None):
+                   out=None, out_dtype="f32"):
     """q (B, H, Nq, D), k/v (B, Hkv, Nkv, D) -> (B, Nq, H, D) (ggml's permuted result)."""
-    import torch
     init()
     B, H, Nq, D = q.shape
     if out is None:
-        out = torch.empty((B, Nq, H, v.shape[-1]), dtype=out_dtype or torch.float32, device=q.device)
+        out = DeviceArray((B, Nq, H, v.shape[-1]), out_dtype)
     dq, dk, dv, dd = desc(q), desc(k), desc(v), desc(out)
     dm = desc(mask) if mask is not None else None
     check(load().tsk_flash_attn_ext(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), _ref(dm),
@@ -179,9 +339,8 @@ def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0, p
 
 
 def rms_norm_mul(x, w, eps, out=None):
-    import torch
     init()
-    out = torch.empty_like(x) if out is None else out
+    out = DeviceArray(x.shape, x.dtype) if out is None else out
     dx, dd = desc(x), desc(out)
     dw = desc(w) if w is not None else None
     check(load().tsk_rms_norm_mul(ctypes.byref(dx), _ref(dw), eps, ctypes.byref(dd), _stream()))
@@ -189,9 +348,8 @@ def rms_norm_mul(x, w, eps, out=None):
 
 
 def norm(x, eps, out=None):
-    import torch
     init()
-    out = torch.empty_like(x) if out is None else out
+    out = DeviceArray(x.shape, x.dtype) if out is None else out
     dx, dd = desc(x), desc(out)
     check(load().tsk_norm(ctypes.byref(dx), eps, ctypes.byref(dd), _stream()))
     return out
@@ -199,9 +357,8 @@ def norm(x, eps, out=None):
 
 def rope_ext(x, pos, n_dims, freq_base=10000.0, freq_scale=1.0, mode=ROPE_NORMAL, out=None):
     """x (B, S, H, D) i.e. ggml [D, H, S, B]; pos int32 (S,)."""
-    import torch
     init()
-    out = torch.empty_like(x) if out is None else out
+    out = DeviceArray(x.shape, x.dtype) if out is None else out
     dx, dp, dd = desc(x), desc(pos), desc(out)
     check(load().tsk_rope_ext(ctypes.byref(dx), ctypes.byref(dp), n_dims, mode, freq_base, freq_scale,
                               0.0, 1.0, ctypes.byref(dd), _stream()))
@@ -209,9 +366,8 @@ def rope_ext(x, pos, n_dims, freq_base=10000.0, freq_scale=1.0, mode=ROPE_NORMAL
 
 
 def qk_norm_rope(x, w, pos, eps=1e-6, n_dims=64, freq_base=10000.0, freq_scale=1.0, out=None):
-    import torch
     init()
-    out = torch.empty_like(x) if out is None else out
+    out = DeviceArray(x.shape, x.dtype) if out is None else out
     dx, dw, dd = desc(x), desc(w), desc(out)
     dp = desc(pos) if pos is not None else None
     check(load().tsk_qk_norm_rope(ctypes.byref(dx), ctypes.byref(dw), _ref(dp), eps, n_dims, freq_base,
@@ -220,11 +376,10 @@ def qk_norm_rope(x, w, pos, eps=1e-6, n_dims=64, freq_base=10000.0, freq_scale=1
 
 
 def q8_0_quantize(x):
-    """(rows, K) float32 -> (rows, K/32, 34) uint8 ggml block_q8_0 bytes."""
-    import torch
+    """(rows, K) f32 -> (rows, K/32, 34) u8 ggml block_q8_0 bytes."""
     init()
     rows, K = x.shape
-    out = torch.empty((rows, K // 32, 34), dtype=torch.uint8, device=x.device)
+    out = DeviceArray((rows, K // 32, 34), "u8")
     dx, dd = desc(x), desc(out, Q8_0)
     check(load().tsk_q8_0_quantize(ctypes.byref(dx), ctypes.byref(dd), _stream()))
     return out
@@ -241,11 +396,10 @@ class SplitQ8:
 
 
 def q8_0_repack(blocks):
-    import torch
     init()
     rows, nb = blocks.shape[0], blocks.shape[1]
     K = nb * 32
-    buf = torch.empty(load().tsk_q8_0_split_nbytes(K, rows), dtype=torch.uint8, device=blocks.device)
+    buf = DeviceArray((load().tsk_q8_0_split_nbytes(K, rows),), "u8")
     sp = SplitQ8(buf, K, rows)
     ds, dd = desc(blocks, Q8_0), desc(sp, Q8_0_SPLIT)
     check(load().tsk_q8_0_repack(ctypes.byref(ds), ctypes.byref(dd), _stream()))
@@ -253,7 +407,6 @@ def q8_0_repack(blocks):
 
 
 def q8_0_dequantize(x):
-    import torch
     init()
     if isinstance(x, SplitQ8):
         K, rows = x.logical_shape
@@ -261,13 +414,36 @@ def q8_0_dequantize(x):
     else:
         rows, K = x.shape[0], x.shape[1] * 32
         dx = desc(x, Q8_0)
-    out = torch.empty((rows, K), dtype=torch.float32, device="cuda")
+    out = DeviceArray((rows, K), "f32")
     dd = desc(out)
     check(load().tsk_q8_0_dequantize(ctypes.byref(dx), ctypes.byref(dd), _stream()))
     return out
 
 
 # ---------------------------------------------------------------- MM-DiT driver
+def synthetic_weights(tensors, seed=1234, std=0.02):
+    """Seeded random-init weights {name: float32 array of shape (ne1, ne0)}.
+    Matrices (ne1 > 1) are N(0, std) rounded to bf16 (RNE) so every consumer
+    sees the values the device holds; biases are N(0, std); RMSNorm weights
+    are 1 + N(0, std). Each tensor has its own stream (seed, crc32(name))."""
+    import zlib
+
+    import numpy as np
+    out = {}
+    for name, ne in tensors:
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        n = int(ne[0]) * int(ne[1])
+        w = rng.standard_normal(n, dtype=np.float32) * np.float32(std)
+        if name.endswith("norm.weight"):
+            w += np.float32(1.0)
+        if ne[1] > 1:
+            u = w.view(np.uint32)
+            u = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+            w = u.view(np.float32)
+        out[name] = w.reshape(int(ne[1]), int(ne[0])) if ne[1] > 1 else w
+    return out
+
+
 def dit_config(**kw):
     c = DitConfig()
     load().tsk_dit_default_config(ctypes.byref(c))
@@ -325,7 +501,7 @@ class Dit:
         return flow
 
     def forward_device(self, latent, t, text, flow):
-        """torch GPU tensors latent (B, T, L), text (B, S, H), flow out; t host numpy (B,)."""
+        """DeviceArrays latent (B, T, L), text (B, S, H), flow out (f32); t host numpy (B,)."""
         import numpy as np
         t = np.ascontiguousarray(t, dtype=np.float32)
         B, T, _ = latent.shape
@@ -333,6 +509,21 @@ class Dit:
                                             t.ctypes.data, ctypes.c_void_p(text.data_ptr()),
                                             ctypes.c_void_p(flow.data_ptr()), _stream()))
         return flow
+
+    ROLES = ("qkv", "out", "fc1", "fc2", "attn", "adaln", "other")
+
+    def timing(self, enable=True):
+        check(load().tsk_dit_timing(self.h, int(bool(enable))))
+
+    def timing_read(self):
+        """{role: (ms_total, launches, flop, bytes)} since the last timing(True)."""
+        out = {}
+        for r, nm in enumerate(self.ROLES):
+            ms, n, fl, by = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+            check(load().tsk_dit_timing_read(self.h, r, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(fl),
+                                             ctypes.byref(by)))
+            out[nm] = (ms.value, n.value, fl.value, by.value)
+        return out
 
     def sample(self, noise, text_cond, text_uncond, steps=24, cfg_scale=5.0):
         import numpy as np
