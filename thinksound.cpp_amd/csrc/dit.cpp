@@ -190,7 +190,7 @@ int validate_cfg(const tsk_dit_config *c) {
 }
 
 // GEMM helper: Y[n, m] for n < N rows of x
-int gemm(const uint16_t *W, const float *bias, const void *x, bool x_f32, int64_t ld_x, int N, int K, int M,
+int gemm(tsk_dit *d, const uint16_t *W, const float *bias, const void *x, bool x_f32, int64_t ld_x, int N, int K, int M,
          int epi, void *y, bool y_bf16, int64_t ld_y, float *res, const float *gate, int64_t ld_gate,
          int rows_per_gate, hipStream_t s, int x_group_rows = 0, int64_t x_group_stride = 0, bool x_split = false) {
     GemmParams p;
@@ -406,7 +406,7 @@ int run_block_stream_pre(tsk_dit *d, const StreamW &sw, const float *x, int B, i
     int rc;
     {
         Timed tm(d, TSK_ROLE_QKV, 2.0 * rows * H * 3 * H, 2.0 * 3 * H * H + 2.0 * rows * H + 4.0 * rows * 3 * H + 12.0 * H, st);
-        rc = gemm(sw.qkv_w, sw.qkv_b, xn, false, H, rows, H, 3 * H, EPI_STORE, qkv, false, 3 * H, nullptr, nullptr,
+        rc = gemm(d, sw.qkv_w, sw.qkv_b, xn, false, H, rows, H, 3 * H, EPI_STORE, qkv, false, 3 * H, nullptr, nullptr,
                   0, 0, st);
     }
     if (rc) return rc;
@@ -428,7 +428,7 @@ int run_block_stream_post(tsk_dit *d, const StreamW &sw, float *x, int B, int S,
     int rc;
     {
         Timed tm(d, TSK_ROLE_OUT, 2.0 * rows * H * H, 2.0 * H * H + 2.0 * rows * H + 8.0 * rows * H, st);
-        rc = gemm(sw.l1_w, sw.l1_b, d->o + (size_t) tok_off * H, false, H, rows, H, H, EPI_GATE_RES, nullptr, false,
+        rc = gemm(d, sw.l1_w, sw.l1_b, d->o + (size_t) tok_off * H, false, H, rows, H, H, EPI_GATE_RES, nullptr, false,
                   0, x, sw.mod + 2 * H, ldm, S, st, S, (int64_t) Ntot * H);
     }
     if (rc) return rc;
@@ -440,11 +440,11 @@ int run_block_stream_post(tsk_dit *d, const StreamW &sw, float *x, int B, int S,
     if (e != hipSuccess) return hip_fail(e, "ln_modulate");
     {
         Timed tm(d, TSK_ROLE_FC1, 2.0 * rows * H * F, 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F, st);
-        rc = gemm(sw.fc1_w, sw.fc1_b, d->xn, false, H, rows, H, F, EPI_GELU, d->h, true, F, nullptr, nullptr, 0, 0, st);
+        rc = gemm(d, sw.fc1_w, sw.fc1_b, d->xn, false, H, rows, H, F, EPI_GELU, d->h, true, F, nullptr, nullptr, 0, 0, st);
     }
     if (rc) return rc;
     Timed tm(d, TSK_ROLE_FC2, 2.0 * rows * F * H, 2.0 * H * F + 2.0 * rows * F + 8.0 * rows * H, st);
-    return gemm(sw.fc2_w, sw.fc2_b, d->h, false, F, rows, F, H, EPI_GATE_RES, nullptr, false, 0, x, sw.mod + 5 * H,
+    return gemm(d, sw.fc2_w, sw.fc2_b, d->h, false, F, rows, F, H, EPI_GATE_RES, nullptr, false, 0, x, sw.mod + 5 * H,
                 ldm, S, st);
 }
 
@@ -495,7 +495,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // input projection (f32-accurate split activations), text stream copy
     {
         Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
-        rc = gemm(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d, true,
+        rc = gemm(d, wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d, true,
                   c.latent_dim, B * T, c.latent_dim, H, EPI_STORE, d->lat, false, H, nullptr, nullptr, 0, 0, st, 0, 0, true);
     }
     if (rc) return rc;
@@ -522,7 +522,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * H * c.latent_dim, 12.0 * B * T * H + 2.0 * H * c.latent_dim, st);
     if ((e = launch_ln_modulate_f32(d->lat, H, B * T, H, T, fmod, fmod + H, 2 * H, c.ln_eps, d->xf, H, st)) != hipSuccess)
         return hip_fail(e, "final ln_modulate");
-    return gemm(wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf,
+    return gemm(d, wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf,
                 true, H, B * T, H, c.latent_dim, EPI_STORE, flow_d, false, c.latent_dim, nullptr, nullptr, 0, 0, st,
                 0, 0, true);
 }
