@@ -39,6 +39,7 @@ struct WInfo {
     int64_t ne0, ne1;      // ggml ne: [in, out] for matrices, [n] for vectors
     bool matrix;           // stored bf16
     bool qkv_perm;         // rows (or entries) permuted (h d j) -> [q | k | v]
+    bool tiled;            // stored in the MFMA-tiled layout of the block GEMMs
     size_t offset;         // bytes into the weight blob
 };
 
@@ -48,6 +49,12 @@ struct RoleTiming {
     int64_t launches = 0;
     double flop = 0.0, bytes = 0.0;
 };
+
+// split-K slices of the two K-reducing block projections; fixed, so every
+// output element is summed in the same order whatever the batch or length
+constexpr int KSPLIT_OUT = 2;    // linear1 (K = hidden)
+constexpr int KSPLIT_FC2 = 4;    // ffn.fc2 (K = mlp_hidden)
+constexpr int KSPLIT_MAX = 4;
 
 struct StreamW {           // one MMDitSingleBlock's weights
     const uint16_t *ada_w, *qkv_w, *l1_w, *fc1_w, *fc2_w;
@@ -71,8 +78,11 @@ struct tsk_dit {
     float *temb = nullptr, *tmp_c = nullptr, *cvec = nullptr;
     float *mods = nullptr;
     float *final_mod = nullptr;     // [max_batch][2H] final-layer adaLN output
-    float *qkv = nullptr;           // [rows][3H] f32 QKV projection
+    // bf16 activations: xn [rows][H] (LN outputs), h [rows][F] (GELU outputs),
+    // latent rows first, text rows from the fixed offset max_batch * max_latent;
+    // fp16 attention operands q/k/v [B][n_head][Ntot][64]; o bf16 [B][Ntot][H]
     uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *h = nullptr;
+    float *part = nullptr;          // split-K partial sums [KSPLIT_MAX][rows][H], text at the same offset rule
     GemvJob *jobs_dev = nullptr;    // [adaLN jobs..., t_embed.0, t_embed.2]
     int njobs = 0, max_job_m = 0;
     float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
@@ -115,13 +125,15 @@ struct Timed {
     }
 };
 
-void add(tsk_dit *d, const std::string &name, int64_t ne0, int64_t ne1, bool matrix, bool perm = false) {
+void add(tsk_dit *d, const std::string &name, int64_t ne0, int64_t ne1, bool matrix, bool perm = false,
+         bool tiled = false) {
     WInfo wi;
     wi.name = name;
     wi.ne0 = ne0;
     wi.ne1 = ne1;
     wi.matrix = matrix;
     wi.qkv_perm = perm;
+    wi.tiled = tiled;
     wi.offset = 0;
     d->idx[name] = (int) d->w.size();
     d->w.push_back(wi);
@@ -132,16 +144,16 @@ void add_block(tsk_dit *d, const std::string &p, bool pre_only) {
     const int nmod = pre_only ? 2 : 6;
     add(d, p + ".adaLN_modulation.1.weight", H, nmod * H, true);
     add(d, p + ".adaLN_modulation.1.bias", nmod * H, 1, false);
-    add(d, p + ".attn.qkv.weight", H, 3 * H, true, true);
+    add(d, p + ".attn.qkv.weight", H, 3 * H, true, true, true);
     add(d, p + ".attn.qkv.bias", 3 * H, 1, false, true);
     add(d, p + ".attn.q_norm.weight", hd, 1, false);
     add(d, p + ".attn.k_norm.weight", hd, 1, false);
     if (!pre_only) {
-        add(d, p + ".linear1.weight", H, H, true);
+        add(d, p + ".linear1.weight", H, H, true, false, true);
         add(d, p + ".linear1.bias", H, 1, false);
-        add(d, p + ".ffn.fc1.weight", H, F, true);
+        add(d, p + ".ffn.fc1.weight", H, F, true, false, true);
         add(d, p + ".ffn.fc1.bias", F, 1, false);
-        add(d, p + ".ffn.fc2.weight", F, H, true);
+        add(d, p + ".ffn.fc2.weight", F, H, true, false, true);
         add(d, p + ".ffn.fc2.bias", H, 1, false);
     }
 }
@@ -220,7 +232,7 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     (void) hipDeviceSynchronize();
     for (auto &r : d->rt)
         for (hipEvent_t e : r.ev) (void) hipEventDestroy(e);
-    void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->qkv,
+    void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
                     d->q, d->k, d->v, d->o, d->h, d->jobs_dev, d->freq,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
     for (void *b : bufs)
@@ -281,7 +293,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->cvec, sizeof(float) * B * H)) ||
         (rc = alloc((void **) &d->mods, sizeof(float) * mod_floats)) ||
         (rc = alloc((void **) &d->xn, 2 * rows * H)) ||
-        (rc = alloc((void **) &d->qkv, 4 * rows * 3 * H)) ||
+        (rc = alloc((void **) &d->part, sizeof(float) * KSPLIT_MAX * rows * H)) ||
         (rc = alloc((void **) &d->q, 2 * rows * H)) ||
         (rc = alloc((void **) &d->k, 2 * rows * H)) ||
         (rc = alloc((void **) &d->v, 2 * rows * H)) ||
@@ -382,6 +394,15 @@ extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src
             if ((x & 0x7fffffffu) > 0x7f800000u) bf[i] = (uint16_t) ((x >> 16) | 64u);
             else bf[i] = (uint16_t) ((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
         }
+        if (wi.tiled) {
+            // rows of K = ne0 -> 16 x 32 MFMA tiles (tiled_index), 8 elements at a time
+            const int64_t K = wi.ne0, M = wi.ne1;
+            std::vector<uint16_t> t((size_t) n);
+            for (int64_t m = 0; m < M; ++m)
+                for (int64_t k = 0; k < K; k += 8)
+                    memcpy(&t[(size_t) tiled_index(m, k, K)], &bf[(size_t) (m * K + k)], 16);
+            bf.swap(t);
+        }
         e = hipMemcpy(dst, bf.data(), 2 * (size_t) n, hipMemcpyHostToDevice);
     } else {
         e = hipMemcpy(dst, s, 4 * (size_t) n, hipMemcpyHostToDevice);
@@ -392,60 +413,148 @@ extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src
 // ------------------------------------------------------------------ forward
 namespace {
 
-int run_block_stream_pre(tsk_dit *d, const StreamW &sw, const float *x, int B, int S, int rope, uint16_t *xn,
-                         float *qkv, int Ntot, int tok_off, hipStream_t st) {
-    const tsk_dit_config &c = d->cfg;
-    const int H = c.hidden, rows = B * S;
-    const int64_t ldm = (int64_t) sw.nmod * H;
-    hipError_t e;
-    {
-        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * H, 6.0 * rows * H + 8.0 * B * H, st);
-        e = launch_ln_modulate(x, H, rows, H, S, sw.mod, sw.mod + H, ldm, c.ln_eps, xn, H, st);
+// One stream (latent or text) of a block as seen by the grouped launches.
+struct StreamRun {
+    const StreamW *w;
+    float *x;               // f32 residual rows [B * S][H]
+    int S;                  // tokens per batch row
+    int tok_off;            // offset of this stream in the joint token order
+    int rope;               // RoPE on q/k (latent stream)
+    uint16_t *xn, *h;       // bf16 LN outputs / GELU outputs of this stream
+    float *part;            // split-K partials of this stream
+    // residual update still owed from the previous projection (split-K partials)
+    const float *pend_bias = nullptr, *pend_gate = nullptr;
+    int64_t pend_ld_gate = 0;   // row stride of the owing block's modulation
+    int pend_split = 0;
+};
+
+LnStream ln_stream(const StreamRun &r, int B, int H, int64_t ldm, const float *shift, const float *scale, void *y) {
+    LnStream l;
+    memset(&l, 0, sizeof(l));
+    l.x = r.x; l.ld_x = H;
+    if (r.pend_split) {
+        l.part = r.part; l.nsplit = r.pend_split; l.part_stride = (int64_t) B * r.S * H;
+        l.bias = r.pend_bias; l.gate = r.pend_gate; l.ld_gate = r.pend_ld_gate;
     }
-    if (e != hipSuccess) return hip_fail(e, "ln_modulate");
-    int rc;
-    {
-        Timed tm(d, TSK_ROLE_QKV, 2.0 * rows * H * 3 * H, 2.0 * 3 * H * H + 2.0 * rows * H + 4.0 * rows * 3 * H + 12.0 * H, st);
-        rc = gemm(d, sw.qkv_w, sw.qkv_b, xn, false, H, rows, H, 3 * H, EPI_STORE, qkv, false, 3 * H, nullptr, nullptr,
-                  0, 0, st);
-    }
-    if (rc) return rc;
-    const float theta_scale = powf(c.rope_theta, -2.0f / (float) c.head_dim);
-    {
-        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * 2 * H, 18.0 * rows * H, st);
-        e = launch_qkv_prologue(qkv, rows, S, c.n_head, sw.qn, sw.kn, c.qk_eps, rope, theta_scale, 1.0f, d->q, d->k,
-                                d->v, Ntot, tok_off, st);
-    }
-    return hipcheck(e, "qkv_prologue");
+    l.shift = shift; l.scale = scale; l.ld_mod = ldm;
+    l.y = y; l.ld_y = H;
+    l.rows = B * r.S; l.rows_per_b = r.S;
+    return l;
 }
 
-int run_block_stream_post(tsk_dit *d, const StreamW &sw, float *x, int B, int S, int Ntot, int tok_off,
-                          hipStream_t st) {
+GemmProblem gemm_problem(const void *x, int64_t ld_x, const uint16_t *w, const float *bias, void *y, int64_t ld_y,
+                         int N, int K, int M) {
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
+    q.x = x; q.w = w; q.w_tiled = 1; q.bias = bias; q.y = y;
+    q.ld_x = ld_x; q.ld_w = K; q.ld_y = ld_y;
+    q.M = M; q.N = N; q.K = K; q.splits = 1;
+    return q;
+}
+
+// LN + modulate of every stream (paying the residual updates they owe) into xn
+int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
-    const int H = c.hidden, F = c.mlp_hidden, rows = B * S;
-    const int64_t ldm = (int64_t) sw.nmod * H;
-    // x += gate_msa * (linear1(o) + b); o rows of this stream: o[b][tok_off + s]
+    const int H = c.hidden;
+    LnGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nstream = ns; g.H = H; g.eps = c.ln_eps; g.y_f32 = 0;
+    double rows = 0.0, pbytes = 0.0;
+    for (int i = 0; i < ns; ++i) {
+        const StreamW &w = *r[i].w;
+        const int64_t ldm = (int64_t) w.nmod * H;
+        // which = 0: shift_msa / scale_msa (mod 0, 1); 1: shift_mlp / scale_mlp (mod 3, 4)
+        const float *sh = w.mod + (which ? 3 : 0) * H, *sc = w.mod + (which ? 4 : 1) * H;
+        g.s[i] = ln_stream(r[i], B, H, ldm, sh, sc, r[i].xn);
+        rows += (double) B * r[i].S;
+        pbytes += 4.0 * r[i].pend_split * B * r[i].S * H;
+        r[i].pend_split = 0;
+    }
+    Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * H, 14.0 * rows * H + pbytes, st);
+    return hipcheck(launch_ln_group(g, st), "ln_group");
+}
+
+int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden;
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = ns;
+    double fl = 0.0, by = 0.0;
+    for (int i = 0; i < ns; ++i) {
+        const int rows = B * r[i].S;
+        GemmProblem &q = g.p[i];
+        q = gemm_problem(r[i].xn, H, r[i].w->qkv_w, r[i].w->qkv_b, nullptr, 0, rows, H, 3 * H);
+        q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
+        q.q = d->q; q.k = d->k; q.v = d->v;
+        q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope;
+        q.theta_scale = powf(c.rope_theta, -2.0f / (float) c.head_dim);
+        q.freq_scale = 1.0f;
+        q.eps = c.qk_eps;
+        fl += 2.0 * rows * H * 3.0 * H;
+        by += 2.0 * 3 * H * H + 2.0 * rows * H + 2.0 * rows * 3 * H + 12.0 * H;
+    }
+    Timed tm(d, TSK_ROLE_QKV, fl, by, st);
+    return hipcheck(launch_gemm_group(g, 0, EPI_QKV, st), "qkv gemm");
+}
+
+// linear1 on the attention output (o rows of each stream: o[b][tok_off + s]),
+// split-K partials; the residual update is paid by the next run_ln
+int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
+    const int H = d->cfg.hidden;
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    double fl = 0.0, by = 0.0;
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        const int rows = B * r[i].S;
+        GemmProblem &q = g.p[g.nprob++];
+        q = gemm_problem(d->o + (size_t) r[i].tok_off * H, H, r[i].w->l1_w, nullptr, r[i].part, H, rows, H, H);
+        q.x_group_rows = r[i].S;
+        q.x_group_stride = (int64_t) Ntot * H;
+        q.splits = KSPLIT_OUT;
+        r[i].pend_split = KSPLIT_OUT;
+        r[i].pend_bias = r[i].w->l1_b;
+        r[i].pend_gate = r[i].w->mod + 2 * H;   // gate_msa
+        r[i].pend_ld_gate = (int64_t) r[i].w->nmod * H;
+        fl += 2.0 * rows * H * H;
+        by += 2.0 * H * H + 2.0 * rows * H + 4.0 * KSPLIT_OUT * rows * H;
+    }
+    if (!g.nprob) return TSK_OK;
+    Timed tm(d, TSK_ROLE_OUT, fl, by, st);
+    return hipcheck(launch_gemm_group(g, 0, EPI_PARTIAL, st), "linear1 gemm");
+}
+
+int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
+    const int H = d->cfg.hidden, F = d->cfg.mlp_hidden;
+    GemmGroup g1, g2;
+    memset(&g1, 0, sizeof(g1));
+    memset(&g2, 0, sizeof(g2));
+    double fl = 0.0, by1 = 0.0, by2 = 0.0;
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        const int rows = B * r[i].S;
+        g1.p[g1.nprob++] = gemm_problem(r[i].xn, H, r[i].w->fc1_w, r[i].w->fc1_b, r[i].h, F, rows, H, F);
+        GemmProblem &q = g2.p[g2.nprob++];
+        q = gemm_problem(r[i].h, F, r[i].w->fc2_w, nullptr, r[i].part, H, rows, F, H);
+        q.splits = KSPLIT_FC2;
+        r[i].pend_split = KSPLIT_FC2;
+        r[i].pend_bias = r[i].w->fc2_b;
+        r[i].pend_gate = r[i].w->mod + 5 * H;   // gate_mlp
+        r[i].pend_ld_gate = (int64_t) r[i].w->nmod * H;
+        fl += 2.0 * rows * H * F;
+        by1 += 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F;
+        by2 += 2.0 * H * F + 2.0 * rows * F + 4.0 * KSPLIT_FC2 * rows * H;
+    }
+    if (!g1.nprob) return TSK_OK;
     int rc;
     {
-        Timed tm(d, TSK_ROLE_OUT, 2.0 * rows * H * H, 2.0 * H * H + 2.0 * rows * H + 8.0 * rows * H, st);
-        rc = gemm(d, sw.l1_w, sw.l1_b, d->o + (size_t) tok_off * H, false, H, rows, H, H, EPI_GATE_RES, nullptr, false,
-                  0, x, sw.mod + 2 * H, ldm, S, st, S, (int64_t) Ntot * H);
+        Timed tm(d, TSK_ROLE_FC1, fl, by1, st);
+        rc = hipcheck(launch_gemm_group(g1, 0, EPI_GELU_BF16, st), "fc1 gemm");
     }
     if (rc) return rc;
-    hipError_t e;
-    {
-        Timed tm(d, TSK_ROLE_OTHER, 8.0 * rows * H, 6.0 * rows * H + 8.0 * B * H, st);
-        e = launch_ln_modulate(x, H, rows, H, S, sw.mod + 3 * H, sw.mod + 4 * H, ldm, c.ln_eps, d->xn, H, st);
-    }
-    if (e != hipSuccess) return hip_fail(e, "ln_modulate");
-    {
-        Timed tm(d, TSK_ROLE_FC1, 2.0 * rows * H * F, 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F, st);
-        rc = gemm(d, sw.fc1_w, sw.fc1_b, d->xn, false, H, rows, H, F, EPI_GELU, d->h, true, F, nullptr, nullptr, 0, 0, st);
-    }
-    if (rc) return rc;
-    Timed tm(d, TSK_ROLE_FC2, 2.0 * rows * F * H, 2.0 * H * F + 2.0 * rows * F + 8.0 * rows * H, st);
-    return gemm(d, sw.fc2_w, sw.fc2_b, d->h, false, F, rows, F, H, EPI_GATE_RES, nullptr, false, 0, x, sw.mod + 5 * H,
-                ldm, S, st);
+    Timed tm(d, TSK_ROLE_FC2, fl, by2, st);
+    return hipcheck(launch_gemm_group(g2, 0, EPI_PARTIAL, st), "fc2 gemm");
 }
 
 int attention(tsk_dit *d, int B, int Ntot, hipStream_t st) {
@@ -502,26 +611,53 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
         return hip_fail(e, "text copy");
 
+    // streams: latent rows of this call first, text rows from the capacity offset
+    const size_t cap = (size_t) c.max_batch * c.max_latent;
+    StreamRun L, X;
+    L.w = nullptr; L.x = d->lat; L.S = T; L.tok_off = 0; L.rope = 1;
+    L.xn = d->xn; L.h = d->h; L.part = d->part;
+    X.w = nullptr; X.x = d->txt; X.S = St; X.tok_off = T; X.rope = 0;
+    X.xn = d->xn + cap * H; X.h = d->h + cap * c.mlp_hidden; X.part = d->part + (size_t) KSPLIT_MAX * cap * H;
+    // joint blocks: LN -> QKV (+RMSNorm/RoPE/F16 epilogue) -> attention over the
+    // concatenated tokens -> linear1 (split-K) -> residual + LN -> fc1 (+GELU)
+    // -> fc2 (split-K, residual paid by the next LN); both streams per launch
     const int Nj = T + St;
     for (int i = 0; i < nj; ++i) {
-        const StreamW &L = d->joint_lat[i], &X = d->joint_txt[i];
-        if ((rc = run_block_stream_pre(d, L, d->lat, B, T, 1, d->xn, d->qkv, Nj, 0, st))) return rc;
-        if ((rc = run_block_stream_pre(d, X, d->txt, B, St, 0, d->xn, d->qkv, Nj, T, st))) return rc;
+        L.w = &d->joint_lat[i];
+        X.w = &d->joint_txt[i];
+        StreamRun r2[2] = {L, X};
+        if ((rc = run_ln(d, r2, 2, B, 0, st))) return rc;
+        if ((rc = run_qkv(d, r2, 2, B, Nj, st))) return rc;
         if ((rc = attention(d, B, Nj, st))) return rc;
-        if ((rc = run_block_stream_post(d, L, d->lat, B, T, Nj, 0, st))) return rc;
-        if (!X.pre_only && (rc = run_block_stream_post(d, X, d->txt, B, St, Nj, T, st))) return rc;
+        if ((rc = run_out(d, r2, 2, B, Nj, st))) return rc;
+        const int ns = r2[1].w->pre_only ? 1 : 2;
+        if ((rc = run_ln(d, r2, ns, B, 1, st))) return rc;
+        if ((rc = run_mlp(d, r2, ns, B, st))) return rc;
+        L = r2[0];
+        X = r2[1];
     }
+    // fused blocks: the latent stream alone
     for (int i = 0; i < c.fused_depth; ++i) {
-        const StreamW &L = d->fused[i];
-        if ((rc = run_block_stream_pre(d, L, d->lat, B, T, 1, d->xn, d->qkv, T, 0, st))) return rc;
+        L.w = &d->fused[i];
+        if ((rc = run_ln(d, &L, 1, B, 0, st))) return rc;
+        if ((rc = run_qkv(d, &L, 1, B, T, st))) return rc;
         if ((rc = attention(d, B, T, st))) return rc;
-        if ((rc = run_block_stream_post(d, L, d->lat, B, T, T, 0, st))) return rc;
+        if ((rc = run_out(d, &L, 1, B, T, st))) return rc;
+        if ((rc = run_ln(d, &L, 1, B, 1, st))) return rc;
+        if ((rc = run_mlp(d, &L, 1, B, st))) return rc;
     }
-    // final layer: adaLN (shift, scale) -> LN/modulate (f32) -> linear to latent_dim
-    const float *fmod = d->final_mod;
-    Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * H * c.latent_dim, 12.0 * B * T * H + 2.0 * H * c.latent_dim, st);
-    if ((e = launch_ln_modulate_f32(d->lat, H, B * T, H, T, fmod, fmod + H, 2 * H, c.ln_eps, d->xf, H, st)) != hipSuccess)
-        return hip_fail(e, "final ln_modulate");
+    // final layer: last residual update + LN/modulate (f32, final adaLN shift/scale)
+    // -> linear to latent_dim with f32-accurate split activations
+    {
+        const float *fmod = d->final_mod;
+        LnGroup g;
+        memset(&g, 0, sizeof(g));
+        g.nstream = 1; g.H = H; g.eps = c.ln_eps; g.y_f32 = 1;
+        g.s[0] = ln_stream(L, B, H, 2 * H, fmod, fmod + H, d->xf);
+        Timed tm(d, TSK_ROLE_OTHER, 10.0 * B * T * H, 16.0 * B * T * H + 4.0 * L.pend_split * B * T * H, st);
+        if ((e = launch_ln_group(g, st)) != hipSuccess) return hip_fail(e, "final ln");
+    }
+    Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * H * c.latent_dim, 4.0 * B * T * H + 2.0 * H * c.latent_dim, st);
     return gemm(d, wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf,
                 true, H, B * T, H, c.latent_dim, EPI_STORE, flow_d, false, c.latent_dim, nullptr, nullptr, 0, 0, st,
                 0, 0, true);

@@ -18,16 +18,12 @@
 #include "tsk_common.h"
 #include "tsk_internal.h"
 
+#include <cstring>
+
 namespace tsk {
 
 namespace {
 
-__device__ __forceinline__ float gelu_tanh_f(float x) {
-    // 0.5 x (1 + tanh(u)), tanh(u) = 1 - 2 / (exp(2u) + 1)
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    const float t = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
-    return 0.5f * x * (1.0f + t);
-}
 
 template <int EPI, bool YBF16>
 __device__ __forceinline__ void epilogue4(const GemmParams &p, int m0, int n, f32x4 v) {
@@ -357,196 +353,6 @@ __global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int 
     *(u32x4 *) (o + 16) = *(const u32x4 *) (q + 16);
 }
 
-// ------------------------------------------------------------------ BF16, token-spanning tiles
-// Workgroup = 4 waves; wave w owns output features [bm0 + w*TM*16, +TM*16) for
-// ALL BN = TN*16 tokens of the tile, so the activation tile in LDS is shared by
-// the four waves and each weight row is read by one wave only. Token tiles of
-// 16*TN are picked per call to fit N (388 = 5 x 80 - 12). Global loads run
-// PF K-steps ahead of the MFMAs through registers (PF stages in flight), LDS
-// is double buffered with one barrier per K-step.
-constexpr int PF = 3;
-
-template <int TM, int TN, bool XF32, int EPI, bool YBF16>
-__global__ __launch_bounds__(256)
-void gemm_bf16_tok_kernel(const GemmParams p) {
-    constexpr int NT = 256;
-    constexpr int BM = 4 * TM * 16, BN = TN * 16;
-    constexpr int CPR = BK / 8;                                // 16-B chunks per row per K-step
-    constexpr int WCH = BM * CPR, XCH = BN * CPR;
-    constexpr int WPER = (WCH + NT - 1) / NT, XPER = (XCH + NT - 1) / NT;
-    constexpr int XW = XF32 ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BM * LDSB];
-    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BN * LDSB];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int bm0 = blockIdx.x * BM, bn0 = blockIdx.y * BN;
-    const int kb = 0, ke = (p.K + BK - 1) / BK;
-
-    // Per-thread source rows, fixed for the whole K loop. Out-of-range rows
-    // read row 0 and are zeroed by select, so every K-step issues the same
-    // loads unconditionally (static s_waitcnt counts keep PF stages in flight).
-    const uint16_t *wsrc[WPER];
-    bool wok[WPER];
-    int wcol[WPER];
-    for (int i = 0; i < WPER; ++i) {
-        const int c = min(tid + i * NT, WCH - 1);
-        const int row = bm0 + c / CPR;
-        wok[i] = row < p.M && tid + i * NT < WCH;
-        wsrc[i] = (const uint16_t *) p.w + (int64_t) (wok[i] ? row : 0) * p.ld_w;
-        wcol[i] = (c % CPR) * 8;
-    }
-    const char *xsrc[XPER];
-    bool xok[XPER];
-    int xcol[XPER];
-    for (int i = 0; i < XPER; ++i) {
-        const int c = min(tid + i * NT, XCH - 1);
-        const int row = bn0 + c / CPR;
-        xok[i] = row < p.N && tid + i * NT < XCH;
-        const int r = xok[i] ? row : 0;
-        const int64_t xoff = p.x_group_rows
-            ? (int64_t) (r / p.x_group_rows) * p.x_group_stride + (int64_t) (r % p.x_group_rows) * p.ld_x
-            : (int64_t) r * p.ld_x;
-        xsrc[i] = (const char *) p.x + xoff * (XF32 ? 4 : 2);
-        xcol[i] = (c % CPR) * 8;
-    }
-
-    u32x4 wreg[PF][WPER];
-    u32x4 xreg[PF][XPER][XW];
-
-    auto gload = [&](int st, int kt) {
-        const int k0 = kt * BK;
-        for (int i = 0; i < WPER; ++i) {
-            const int kk = k0 + wcol[i];
-            const bool ok = wok[i] && kk < p.K;
-            const u32x4 v = *(const u32x4 *) (wsrc[i] + (ok ? kk : 0));
-            wreg[st][i] = ok ? v : u32x4{0, 0, 0, 0};
-        }
-        for (int i = 0; i < XPER; ++i) {
-            const int kk = k0 + xcol[i];
-            const bool ok = xok[i] && kk < p.K;
-            const int kc = ok ? kk : 0;
-            if constexpr (XF32) {
-                const float *xr = (const float *) xsrc[i] + kc;
-                const u32x4 v0 = *(const u32x4 *) xr, v1 = *(const u32x4 *) (xr + 4);
-                xreg[st][i][0] = ok ? v0 : u32x4{0, 0, 0, 0};
-                xreg[st][i][1] = ok ? v1 : u32x4{0, 0, 0, 0};
-            } else {
-                const u32x4 v = *(const u32x4 *) ((const uint16_t *) xsrc[i] + kc);
-                xreg[st][i][0] = ok ? v : u32x4{0, 0, 0, 0};
-            }
-        }
-    };
-    auto lstore = [&](int st, int buf) {
-        for (int i = 0; i < WPER; ++i) {
-            const int c = tid + i * NT;
-            if (c < WCH) *(u32x4 *) &Ws[buf][(c / CPR) * LDSB + (c % CPR) * 8] = wreg[st][i];
-        }
-        for (int i = 0; i < XPER; ++i) {
-            const int c = tid + i * NT;
-            if (c < XCH) {
-                u32x4 v;
-                if constexpr (XF32) {
-                    const float *f0 = (const float *) &xreg[st][i][0];
-                    const float *f1 = (const float *) &xreg[st][i][1];
-                    uint16_t t8[8];
-                    for (int j = 0; j < 4; ++j) { t8[j] = f32_to_bf16_bits(f0[j]); t8[4 + j] = f32_to_bf16_bits(f1[j]); }
-                    __builtin_memcpy(&v, t8, 16);
-                } else {
-                    v = xreg[st][i][0];
-                }
-                *(u32x4 *) &Xs[buf][(c / CPR) * LDSB + (c % CPR) * 8] = v;
-            }
-        }
-    };
-
-    f32x4 acc[TM][TN];
-    for (int i = 0; i < TM; ++i)
-        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
-
-    auto compute = [&](int buf) {
-        for (int kk = 0; kk < BK / 32; ++kk) {
-            bf16x8 a[TM], b[TN];
-            for (int i = 0; i < TM; ++i)
-                a[i] = *(const bf16x8 *) &Ws[buf][((wave * TM + i) * 16 + lr) * LDSB + 32 * kk + 8 * lg];
-            for (int j = 0; j < TN; ++j)
-                b[j] = *(const bf16x8 *) &Xs[buf][(j * 16 + lr) * LDSB + 32 * kk + 8 * lg];
-            for (int i = 0; i < TM; ++i)
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    // prologue: PF K-steps in flight (indices past the split are clamped and unused)
-    const int klast = ke > kb ? ke - 1 : kb;
-    for (int st = 0; st < PF; ++st) gload(st, min(kb + st, klast));
-    int kt = kb;
-    // full trips: every iteration stores one stage, re-issues it PF steps ahead, computes
-    for (; kt + PF <= ke; kt += PF) {
-#pragma unroll
-        for (int st = 0; st < PF; ++st) {
-            const int buf = (kt + st - kb) & 1;
-            lstore(st, buf);
-            __syncthreads();
-            gload(st, min(kt + st + PF, klast));
-            compute(buf);
-        }
-    }
-    // tail: fewer than PF K-steps left, already in flight
-#pragma unroll
-    for (int st = 0; st < PF; ++st) {
-        if (kt + st < ke) {
-            const int buf = (kt + st - kb) & 1;
-            lstore(st, buf);
-            __syncthreads();
-            compute(buf);
-        }
-    }
-
-    for (int i = 0; i < TM; ++i)
-        for (int j = 0; j < TN; ++j) {
-            const int m0 = bm0 + (wave * TM + i) * 16 + 4 * lg;
-            const int n = bn0 + j * 16 + lr;
-            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
-        }
-}
-
-template <int TN, bool XF32>
-hipError_t gemm_tok_launch(const GemmParams &p, hipStream_t s) {
-    constexpr int BM = 128, BN = TN * 16;
-    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
-    dim3 block(256);
-    if constexpr (XF32) {
-        if (p.epi != EPI_STORE) return hipErrorInvalidValue;
-        if (p.y_bf16) hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, true, EPI_STORE, true>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, true, EPI_STORE, false>), grid, block, 0, s, p);
-    } else {
-        switch (p.epi) {
-            case EPI_GELU:
-                if (!p.y_bf16) return hipErrorInvalidValue;
-                hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, false, EPI_GELU, true>), grid, block, 0, s, p);
-                break;
-            case EPI_GATE_RES:
-                hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, false, EPI_GATE_RES, false>), grid, block, 0, s, p);
-                break;
-            default:
-                if (p.y_bf16) hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, false, EPI_STORE, true>), grid, block, 0, s, p);
-                else hipLaunchKernelGGL((gemm_bf16_tok_kernel<2, TN, false, EPI_STORE, false>), grid, block, 0, s, p);
-        }
-    }
-    return hipGetLastError();
-}
-
-template <bool XF32>
-hipError_t gemm_tok_dispatch(const GemmParams &p, int TN, hipStream_t s) {
-    switch (TN) {
-        case 1: return gemm_tok_launch<1, XF32>(p, s);
-        case 2: return gemm_tok_launch<2, XF32>(p, s);
-        case 3: return gemm_tok_launch<3, XF32>(p, s);
-        default: return gemm_tok_launch<4, XF32>(p, s);
-    }
-}
-
 // ------------------------------------------------------------------ dispatch
 template <int WM, int WN, int TM, int TN, bool XF32, bool YBF16>
 hipError_t gemm_bf16_epi(const GemmParams &p, hipStream_t s) {
@@ -595,10 +401,16 @@ hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s) {
         hipLaunchKernelGGL((gemm_bf16_kernel<2, 2, 1, 2, true, EPI_STORE, false, true>), grid, dim3(256), 0, s, p);
         return hipGetLastError();
     }
-    // 128 x 32 tiles: measured fastest across the DiT projection shapes
-    // (N = 154..1446 tokens, K = 1024 / 4096, M = 1024..4096) on MI355X
-    const int TN = p.N >= 32 ? 2 : 1;
-    return p.x_f32 ? gemm_tok_dispatch<true>(p, TN, s) : gemm_tok_dispatch<false>(p, TN, s);
+    if (p.epi != EPI_STORE) return hipErrorInvalidValue;
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = p.x; q.w = (const uint16_t *) p.w; q.bias = p.bias; q.y = p.y;
+    q.ld_x = p.ld_x; q.ld_w = p.ld_w; q.ld_y = p.ld_y;
+    q.x_group_rows = p.x_group_rows; q.x_group_stride = p.x_group_stride;
+    q.M = p.M; q.N = p.N; q.K = p.K; q.splits = 1;
+    return launch_gemm_group(g, p.x_f32 ? GEMM_X_F32 : 0, p.y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32, s);
 }
 
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {

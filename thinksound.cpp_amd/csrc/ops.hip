@@ -23,13 +23,6 @@ __device__ __forceinline__ const char *vrow(const View4 &v, int64_t r) {
     return (const char *) v.data + i1 * v.nb[1] + i2 * v.nb[2] + i3 * v.nb[3];
 }
 
-// ggml-cpu's rope cache: theta = p; theta *= theta_scale per pair (running product)
-__device__ __forceinline__ float rope_theta(float p, float theta_scale, int pair) {
-    float th = p;
-    for (int j = 0; j < pair; ++j) th *= theta_scale;
-    return th;
-}
-
 // ---------------------------------------------------------------- rms_norm * w
 __global__ void rms_norm_mul_kernel(const View4 x, const float *w, float eps, const View4 y, int64_t rows) {
     const int64_t r = (int64_t) blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -184,100 +177,69 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
     return t;
 }
 
-// one 256-thread block per row; H % 4 == 0; bf16 or f32 output
+// Residual update + LayerNorm + adaLN modulate, one 256-thread block per row
+// of up to two streams (mmdit.cpp:196-231: x = x + gate * y, then
+// modulate(LN(x), shift, scale) for the next projection):
+//   pending: x += gate[b] * (sum_s part[s][r] + bias)   (splits summed in order)
+//   y = LN(x, eps) * (1 + scale[b]) + shift[b]           (bf16, or f32)
+// A row of H <= 4096 floats stays in registers (4 per thread per 1024).
 template <bool YF32>
-__global__ __launch_bounds__(256) void ln_modulate_kernel(const float *x, int64_t ld_x, int H, int rows_per_b,
-                                                          const float *shift, const float *scale,
-                                                          int64_t ld_mod, float eps, void *y, int64_t ld_y) {
+__global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
     __shared__ float red[4];
-    const int r = blockIdx.x;
-    const float *xr = x + (int64_t) r * ld_x;
+    int r = blockIdx.x, si = 0;
+    if (g.nstream > 1 && r >= g.s[0].rows) { r -= g.s[0].rows; si = 1; }
+    const LnStream &st = g.s[si];
+    const int H = g.H, b = r / st.rows_per_b;
+    float *xr = st.x + (int64_t) r * st.ld_x;
+    constexpr int VMAX = 4;
+    f32x4 v[VMAX];
     float s = 0.0f;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) {
-        f32x4 v = *(const f32x4 *) (xr + i);
-        s += v[0] + v[1] + v[2] + v[3];
+#pragma unroll
+    for (int j = 0; j < VMAX; ++j) {
+        const int i = (threadIdx.x + 256 * j) * 4;
+        if (i >= H) break;
+        v[j] = *(const f32x4 *) (xr + i);
+        if (st.part) {
+            const float *pp = st.part + (int64_t) r * H + i;
+            f32x4 acc = *(const f32x4 *) pp;
+            for (int sp = 1; sp < st.nsplit; ++sp) {
+                const f32x4 t = *(const f32x4 *) (pp + sp * st.part_stride);
+                for (int e = 0; e < 4; ++e) acc[e] += t[e];
+            }
+            const f32x4 bv = st.bias ? *(const f32x4 *) (st.bias + i) : f32x4{0, 0, 0, 0};
+            const f32x4 gv = *(const f32x4 *) (st.gate + (int64_t) b * st.ld_gate + i);
+            for (int e = 0; e < 4; ++e) v[j][e] += gv[e] * (acc[e] + bv[e]);
+            *(f32x4 *) (xr + i) = v[j];
+        }
+        s += v[j][0] + v[j][1] + v[j][2] + v[j][3];
     }
     const float mean = block_sum_256(s, red) / (float) H;
     float s2 = 0.0f;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) {
-        f32x4 v = *(const f32x4 *) (xr + i);
-        for (int j = 0; j < 4; ++j) { const float d = v[j] - mean; s2 += d * d; }
+#pragma unroll
+    for (int j = 0; j < VMAX; ++j) {
+        const int i = (threadIdx.x + 256 * j) * 4;
+        if (i >= H) break;
+        for (int e = 0; e < 4; ++e) { const float d = v[j][e] - mean; s2 += d * d; }
     }
     const float var = block_sum_256(s2, red) / (float) H;
-    const float rs = 1.0f / sqrtf(var + eps);
-    const int b = r / rows_per_b;
-    const float *sh = shift + (int64_t) b * ld_mod, *sc = scale + (int64_t) b * ld_mod;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) {
-        f32x4 v = *(const f32x4 *) (xr + i);
+    const float rs = 1.0f / sqrtf(var + g.eps);
+    const float *sh = st.shift + (int64_t) b * st.ld_mod, *sc = st.scale + (int64_t) b * st.ld_mod;
+#pragma unroll
+    for (int j = 0; j < VMAX; ++j) {
+        const int i = (threadIdx.x + 256 * j) * 4;
+        if (i >= H) break;
+        const f32x4 shv = *(const f32x4 *) (sh + i), scv = *(const f32x4 *) (sc + i);
         float o[4];
-        for (int j = 0; j < 4; ++j) o[j] = (v[j] - mean) * rs * (sc[i + j] + 1.0f) + sh[i + j];
+        for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mean) * rs * (scv[e] + 1.0f) + shv[e];
         if constexpr (YF32) {
-            *(f32x4 *) ((float *) y + (int64_t) r * ld_y + i) = f32x4{o[0], o[1], o[2], o[3]};
+            *(f32x4 *) ((float *) st.y + (int64_t) r * st.ld_y + i) = f32x4{o[0], o[1], o[2], o[3]};
         } else {
             uint16_t ob[4];
-            for (int j = 0; j < 4; ++j) ob[j] = f32_to_bf16_bits(o[j]);
+            for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16_bits(o[e]);
             u32x2 w;
             __builtin_memcpy(&w, ob, 8);
-            *(u32x2 *) ((uint16_t *) y + (int64_t) r * ld_y + i) = w;
+            *(u32x2 *) ((uint16_t *) st.y + (int64_t) r * st.ld_y + i) = w;
         }
-    }
-}
-
-// qkv row (f32, [q | k | v] each head-major nh x 64) -> q/k/v [B, nh, Ntot, 64] fp16:
-// RMSNorm*w on q and k, RoPE when rope != 0, and the F16 cast of Q/K/V that
-// attention() applies before flash_attn_ext (mmdit.cpp:88-90).
-// One 256-thread block per row (8 heads x 32 pairs per pass).
-__global__ __launch_bounds__(256) void qkv_prologue_kernel(const float *qkv, int S, int nh, const float *qn_w,
-                                                           const float *kn_w, float eps, int rope, float theta_scale,
-                                                           float freq_scale, uint16_t *q, uint16_t *k, uint16_t *v,
-                                                           int Ntot, int tok_off) {
-    const int r = blockIdx.x;
-    const int b = r / S, s = r % S;
-    const int H = nh * 64;
-    const float *row = qkv + (int64_t) r * 3 * H;
-    const int pair = threadIdx.x & 31, hsub = threadIdx.x >> 5;
-    float c = 1.0f, sn = 0.0f;
-    if (rope) {
-        const float th = freq_scale * rope_theta((float) s, theta_scale, pair);
-        c = cosf(th);
-        sn = sinf(th);
-    }
-    for (int which = 0; which < 2; ++which) {
-        const float *src = row + which * H;
-        const float *w = which ? kn_w : qn_w;
-        uint16_t *dst = which ? k : q;
-        for (int h0 = 0; h0 < nh; h0 += 8) {
-            const int h = h0 + hsub;
-            float x0 = 0.0f, x1 = 0.0f;
-            if (h < nh) {
-                const f32x4 two = *(const f32x4 *) (src + h * 64 + 4 * (pair >> 1));
-                x0 = (pair & 1) ? two[2] : two[0];
-                x1 = (pair & 1) ? two[3] : two[1];
-            }
-            float ss = x0 * x0 + x1 * x1;
-            for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
-            const float sc = 1.0f / sqrtf(ss / 64.0f + eps);
-            x0 = x0 * sc * w[2 * pair];
-            x1 = x1 * sc * w[2 * pair + 1];
-            if (rope) {
-                const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
-                x0 = y0; x1 = y1;
-            }
-            if (h < nh) {
-                uint16_t *o = dst + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + 2 * pair;
-                *(uint32_t *) o = (uint32_t) f32_to_f16_bits(x0) | ((uint32_t) f32_to_f16_bits(x1) << 16);
-            }
-        }
-    }
-    // v: F16 cast, 4 elements per thread
-    const float *vs = row + 2 * H;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) {
-        const int h = i / 64, d = i % 64;
-        const f32x4 x = *(const f32x4 *) (vs + i);
-        uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]), f32_to_f16_bits(x[3])};
-        u32x2 w2;
-        __builtin_memcpy(&w2, o4, 8);
-        *(u32x2 *) (v + (((int64_t) b * nh + h) * Ntot + tok_off + s) * 64 + d) = w2;
     }
 }
 
@@ -399,26 +361,11 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
     return hipGetLastError();
 }
 
-hipError_t launch_ln_modulate(const float *x, int64_t ld_x, int rows, int H, int rows_per_b, const float *shift,
-                              const float *scale, int64_t ld_mod, float eps, uint16_t *y, int64_t ld_y,
-                              hipStream_t s) {
-    hipLaunchKernelGGL(ln_modulate_kernel<false>, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
-                       ld_mod, eps, (void *) y, ld_y);
-    return hipGetLastError();
-}
-
-hipError_t launch_ln_modulate_f32(const float *x, int64_t ld_x, int rows, int H, int rows_per_b, const float *shift,
-                                  const float *scale, int64_t ld_mod, float eps, float *y, int64_t ld_y, hipStream_t s) {
-    hipLaunchKernelGGL(ln_modulate_kernel<true>, dim3(rows), dim3(256), 0, s, x, ld_x, H, rows_per_b, shift, scale,
-                       ld_mod, eps, (void *) y, ld_y);
-    return hipGetLastError();
-}
-
-hipError_t launch_qkv_prologue(const float *qkv, int rows, int S, int nh, const float *qn_w, const float *kn_w,
-                               float eps, int rope, float theta_scale, float freq_scale, uint16_t *q, uint16_t *k,
-                               uint16_t *v, int Ntot, int tok_off, hipStream_t s) {
-    hipLaunchKernelGGL(qkv_prologue_kernel, dim3(rows), dim3(256), 0, s, qkv, S, nh, qn_w, kn_w, eps, rope,
-                       theta_scale, freq_scale, q, k, v, Ntot, tok_off);
+hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
+    if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
+    const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
+    if (g.y_f32) hipLaunchKernelGGL(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
+    else hipLaunchKernelGGL(ln_group_kernel<false>, dim3(rows), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 

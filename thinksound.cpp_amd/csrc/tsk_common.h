@@ -54,6 +54,22 @@ template <Elt E> __device__ __forceinline__ void store_from_f32(void *p, int64_t
     else ((uint16_t *) p)[i] = f32_to_bf16_bits(v);
 }
 
+// GELU, tanh form: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
+// tanh(u) = 1 - 2 / (exp(2u) + 1)
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    const float t = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
+    return 0.5f * x * (1.0f + t);
+}
+
+// RoPE angle of pair i at position p: p * theta_scale^i as a running product
+// (the order ggml's rope evaluates it in)
+__device__ __forceinline__ float rope_theta(float p, float theta_scale, int pair) {
+    float th = p;
+    for (int j = 0; j < pair; ++j) th *= theta_scale;
+    return th;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;

@@ -64,6 +64,52 @@ struct GemmParams {
     const uint16_t *dw;      // [M][K/32] fp16 bits
 };
 hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s);
+
+// ---------------------------------------------------------------- grouped GEMM
+// One launch runs up to two independent problems (the latent and text streams
+// of a joint block), Y[n, m] = sum_k X[n, k] W[m, k], with one of:
+enum GroupEpi : int {
+    EPI_STORE_F32 = 10,   // y f32 = acc + bias
+    EPI_STORE_BF16 = 11,  // y bf16 = acc + bias
+    EPI_GELU_BF16 = 12,   // y bf16 = gelu_tanh(acc + bias)
+    EPI_QKV = 13,         // acc + bias -> RMSNorm*w (q, k), RoPE, fp16 -> attention layout
+    EPI_PARTIAL = 14      // split-K: y f32 slice [split][N][M] = partial acc (no bias)
+};
+enum GemmFlags : int { GEMM_X_F32 = 1 };
+
+struct GemmProblem {
+    const void *x;                 // activations (bf16, or f32 with GEMM_X_F32)
+    const uint16_t *w;             // bf16 weights [M][K] row-major (ld_w), or tiled (w_tiled)
+    int w_tiled;                   // 1: MFMA-tiled layout of tile_bf16_weights() (M % 16 == 0, K % 32 == 0)
+    const float *bias;             // [M] nullable (ignored by EPI_PARTIAL)
+    void *y;                       // output (see GroupEpi)
+    int64_t ld_x, ld_w, ld_y;      // row strides in elements
+    int x_group_rows;              // see GemmParams
+    int64_t x_group_stride;
+    int M, N, K;
+    int splits;                    // K slices (EPI_PARTIAL), else 1
+    // EPI_QKV: M = 3 * n_head * 64 with [q | k | v] head-major
+    const float *qn_w, *kn_w;      // RMSNorm weights [64]
+    uint16_t *q, *k, *v;           // fp16 [B][n_head][Ntot][64]
+    int seq;                       // rows per batch item (row n -> b = n / seq, s = n % seq)
+    int Ntot, tok_off, rope;
+    float theta_scale, freq_scale, eps;
+    // filled by launch_gemm_group
+    int tiles_m, tiles_n, block_begin;
+};
+struct GemmGroup {
+    GemmProblem p[2];
+    int nprob;
+};
+hipError_t launch_gemm_group(GemmGroup &g, int flags, int epi, hipStream_t s);
+
+// MFMA-tiled weight layout: W[m][k] (M % 16 == 0, K % 32 == 0) is stored as
+// 16 x 32 tiles, tile (m / 16, k / 32) at element (m / 16 * (K / 32) + k / 32) * 512,
+// inside it lane l = m % 16 + 16 * (k % 32 / 8) holds k % 8 = 0..7 at l * 8 + k % 8.
+// One wave's A operand of a 16x16x32 MFMA is then 1 KiB of consecutive bytes.
+inline int64_t tiled_index(int64_t m, int64_t k, int64_t K) {
+    return ((m / 16) * (K / 32) + k / 32) * 512 + ((m % 16) + 16 * ((k % 32) / 8)) * 8 + (k % 8);
+}
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s);
 // Activation quantization to planes for launch_gemm_q8 (ggml-cpu x86 rounding).
 // x rows of K (f32 or bf16, row stride ld_x elements).
@@ -95,21 +141,31 @@ hipError_t launch_q8_repack(const void *src, int64_t ld_src, int64_t rows, int64
 hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s);
 
 // ---------------------------------------------------------------- DiT glue
-// y[r, :] = LN(x[r, :], eps) * (1 + scale[b, :]) + shift[b, :], b = r / rows_per_b;
-// x f32 (row stride ld_x), y bf16 (row stride ld_y).
-hipError_t launch_ln_modulate(const float *x, int64_t ld_x, int rows, int H, int rows_per_b,
-                              const float *shift, const float *scale, int64_t ld_mod, float eps,
-                              uint16_t *y, int64_t ld_y, hipStream_t s);
-hipError_t launch_ln_modulate_f32(const float *x, int64_t ld_x, int rows, int H, int rows_per_b,
-                                  const float *shift, const float *scale, int64_t ld_mod, float eps,
-                                  float *y, int64_t ld_y, hipStream_t s);
-// Split the QKV GEMM output (f32 rows of [q | k | v], head-major) into the
-// fp16 attention layout [B, nh, Ntot, 64] at token offset tok_off, applying
-// RMSNorm*w to q and k and (if rope) RoPE with position = row % S.
-hipError_t launch_qkv_prologue(const float *qkv, int rows, int S, int nh,
-                               const float *qn_w, const float *kn_w, float eps, int rope,
-                               float theta_scale, float freq_scale, uint16_t *q, uint16_t *k,
-                               uint16_t *v, int Ntot, int tok_off, hipStream_t s);
+// Residual update + LayerNorm + modulate for up to two streams in one launch.
+// Row r of a stream (b = r / rows_per_b):
+//   if part: x[r] += gate[b * ld_gate] * (sum_{s < nsplit} part[s * part_stride + r * H] + bias)
+//   y[r] = LN(x[r], eps) * (1 + scale[b]) + shift[b]   (bf16, or f32 when y_f32)
+struct LnStream {
+    float *x;                     // f32 rows of H (in/out), row stride ld_x
+    int64_t ld_x;
+    const float *part;            // split-K partial sums [nsplit][rows][H], or null
+    int nsplit;
+    int64_t part_stride;          // elements between split slices
+    const float *bias;            // [H] added to the partial sum, nullable
+    const float *gate;            // [B][ld_gate]
+    int64_t ld_gate;
+    const float *shift, *scale;   // [B][ld_mod]
+    int64_t ld_mod;
+    void *y;                      // output rows, row stride ld_y
+    int64_t ld_y;
+    int rows, rows_per_b;
+};
+struct LnGroup {
+    LnStream s[2];
+    int nstream, H, y_f32;
+    float eps;
+};
+hipError_t launch_ln_group(const LnGroup &g, hipStream_t s);
 // A list of small-batch GEMVs with f32 activations (products exact in fp32):
 // out[b, j] = act( sum_k W[j, k] * x[b, k] + bias[j] ), act = silu if silu_out
 struct GemvJob {
