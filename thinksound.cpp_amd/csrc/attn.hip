@@ -312,11 +312,11 @@ hipError_t launch_attn_t(const AttnParams &p, hipStream_t s) {
     const int64_t wgs_big = (int64_t) ((p.Nq + rows_per_wg_big - 1) / rows_per_wg_big) * p.H * p.B;
     if (KVE != Elt::F32 && wgs_big >= 256) {
         dim3 grid((p.Nq + rows_per_wg_big - 1) / rows_per_wg_big, p.H, p.B);
-        hipLaunchKernelGGL((attn_kernel<QE, KVE, OE, 4, 2>), grid, dim3(256), 0, s, p);
+        launch_kernel((attn_kernel<QE, KVE, OE, 4, 2>), grid, dim3(256), 0, s, p);
     } else {
         constexpr int rows = 4 * 1 * 16;
         dim3 grid((p.Nq + rows - 1) / rows, p.H, p.B);
-        hipLaunchKernelGGL((attn_kernel<QE, KVE, OE, 4, 1>), grid, dim3(256), 0, s, p);
+        launch_kernel((attn_kernel<QE, KVE, OE, 4, 1>), grid, dim3(256), 0, s, p);
     }
     return hipGetLastError();
 }

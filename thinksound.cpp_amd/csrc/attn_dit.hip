@@ -1,0 +1,436 @@
+// attn_dit.hip — flash attention of the MM-DiT blocks on gfx950: the
+// ggml_flash_attn_ext node of attention() (src/mmdit.cpp:85-95) for head_dim
+// 64, no mask, no softcap / ALiBi, one KV head per query head, 16-bit K and V
+// -- the configuration mmdit.cpp emits. The DiT step driver feeds it directly
+// (its QKV epilogue writes V already transposed); tsk_flash_attn_ext routes
+// matching nodes here after transposing V with vt_transpose_kernel.
+//
+// Work split: a workgroup owns QB blocks of 32 query rows of one (batch,
+// head) and splits the keys into KS contiguous ranges; wave (g, qb) runs
+// query block qb over key range g, so QB * KS waves share the CU. The waves
+// of one key range share its K / V^T tiles (64 keys), brought into LDS by
+// direct global->LDS loads (two or three buffers, one barrier per tile). At the end
+// the KS partial softmax states of a query block are merged through LDS.
+//
+// Per tile and wave (v_mfma_f32_32x32x16, fp32 accumulation):
+//   S^T = K . Q^T  (keys x queries): lane l owns query l % 32 and 32 of the 64
+//                  keys, so row max / sum are lane-local plus one xor-32 step;
+//   P^T = exp2(S^T * scale * log2(e) - m) in fp16. With fp16 K, Q is
+//                  pre-scaled by scale * log2(e) and the accumulators are
+//                  seeded with -m (the running max), so the MFMA itself yields
+//                  the exponent; with bf16 K (8-bit mantissa: pre-scaling
+//                  would add a visible rounding) Q stays unscaled, the seed is
+//                  -m / c and the logits are scaled after the product. The
+//                  S^T accumulators are already the B operand of the next
+//                  product;
+//   O^T += V^T . P^T.
+// V^T positions are permuted inside every group of 16 keys (bits 2 and 3 of
+// the key index swapped, an involution) so that each lane's A operand of
+// V^T . P^T is one 16-byte LDS read that matches the keys its P^T slots hold.
+// Softmax state is rescaled lazily: the running max only moves when a tile's
+// max exceeds it by more than 8 (a factor 256 in fp16 P), which is exact in
+// real arithmetic and keeps P <= 256.
+//
+// Numerics follow ggml's GPU F16 flash-attn path (mmdit.cpp:89-92 casts K/V
+// to F16 and sets GGML_PREC_F32; ggml's GPU kernels scale Q before its
+// 16-bit conversion): Q (times scale * log2(e) for fp16 K) rounded to K's
+// type, exact 16-bit
+// products, fp32 logits, softmax and accumulation; P and V enter P.V as fp16;
+// the row sum adds the same fp16 P values in fp32 (v_dot2).
+#include "tsk_common.h"
+#include "tsk_internal.h"
+
+namespace tsk {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+
+constexpr int KT = 64;                  // keys per tile
+constexpr int TILE_H = 2 * KT * 64;     // halves per tile buffer: K [64][64] then V^T [64][64]
+constexpr float RESCALE_T = 8.0f;       // lazy-rescale threshold (log2 domain)
+
+// LDS row of 64 halves (8 chunks of 16 B); chunk c of row r sits at slot
+// c ^ ((r / 2) % 8). A ds_read_b128 serves 16 lanes per cycle over 256 B (two
+// rows): lanes reading rows r .. r + 15 then hit 16 distinct 16-B slots.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
+// K/V^T tile buffers per key range: 3 (two tiles in flight) when they fit
+// and every wave issues the same number of loads per tile, else 2
+constexpr int nbuf(int KS, int QB) { return (KS <= 2 && 16 % QB == 0) ? 3 : 2; }
+
+template <bool KBF16>
+__device__ __forceinline__ uint16_t to_k_type(float x) {
+    return KBF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+}
+
+// 8 consecutive Q elements times c, rounded to K's 16-bit type
+template <bool KBF16>
+__device__ __forceinline__ u32x4 load_q8(const char *row, int d0, int q_type, float c) {
+    float f[8];
+    if (q_type == TSK_TYPE_F32) {
+        const f32x4 a = *(const f32x4 *) (row + 4 * d0), b = *(const f32x4 *) (row + 4 * d0 + 16);
+        for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
+    } else {
+        const u32x4 r = *(const u32x4 *) (row + 2 * d0);
+        uint16_t h[8];
+        __builtin_memcpy(h, &r, 16);
+        for (int i = 0; i < 8; ++i) f[i] = q_type == TSK_TYPE_F16 ? f16_bits_to_f32(h[i]) : bf16_bits_to_f32(h[i]);
+    }
+    uint16_t o[8];
+    for (int i = 0; i < 8; ++i) o[i] = to_k_type<KBF16>(f[i] * c);
+    u32x4 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
+}
+
+template <bool KBF16, bool BOUNDED, int KS, int QB>
+__global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    constexpr int NB = nbuf(KS, QB);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = wave / QB, qb = wave % QB;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    // workgroup L runs on XCD L % 8; the units of one (batch, head) are
+    // consecutive within an XCD so its K / V^T stay in that XCD's L2
+    const int W = p.qtiles * p.H * p.B;
+    const int per = (int) (gridDim.x >> 3);
+    const int u = (int) (blockIdx.x & 7) * per + (int) (blockIdx.x >> 3);
+    if (u >= W) return;
+    const int bh = u / p.qtiles, qt = u % p.qtiles;
+    const int b = bh / p.H, h = bh % p.H;
+
+    const int ntiles = (p.Nkv + KT - 1) / KT;
+    const int tpg = (ntiles + KS - 1) / KS;
+    const int t0 = g * tpg, tend = min(ntiles, t0 + tpg);
+
+    const char *qp = (const char *) p.q + (int64_t) h * p.q_nb2 + (int64_t) b * p.q_nb3;
+    const char *kp = (const char *) p.k + (int64_t) h * p.k_nb2 + (int64_t) b * p.k_nb3;
+    const uint16_t *vp = p.vt + (int64_t) bh * p.vt_bh;
+
+    // Q^T fragments (B operand): lane holds Q[q0 + l32][16 ks + 8 hi + 0..7]
+    const int q0 = qt * (QB * 32) + qb * 32;
+    const char *qrow = qp + (int64_t) min(q0 + l32, p.Nq - 1) * p.q_nb1;
+    u32x4 qraw[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        qraw[ks] = p.q_prescaled ? *(const u32x4 *) (qrow + 2 * (16 * ks + 8 * hi))
+                                 : load_q8<KBF16>(qrow, 16 * ks + 8 * hi, p.q_type, KBF16 ? 1.0f : p.c);
+    const float c = p.c;
+
+    uint16_t *gb = lds + g * NB * TILE_H;
+    // one tile of this key range into buffer `buf`: 16 wave-loads of 1 KiB
+    // (8 for K rows, 8 for V^T rows), spread over the range's QB waves; lane
+    // i of wave-load j fills slot i % 8 of row R = 8 (j % 8) + i / 8, i.e.
+    // chunk (i % 8) ^ ((R / 2) % 8) of that row (the swizzle of swz()), where
+    // (R / 2) % 8 = 4 (j % 2) + i / 16. K rows are clamped to Nkv - 1 on the
+    // last tile only.
+    constexpr int NJ = (16 - 1) / QB + 1;       // wave-loads of wave qb: j = qb + QB * i < 16
+    const int r8 = lane >> 3;
+    const int ch0 = (lane & 7) ^ (lane >> 4), ch1 = (lane & 7) ^ (4 | (lane >> 4));
+    const char *krow0 = kp + (int64_t) r8 * p.k_nb1;
+    const uint16_t *vrow0 = vp + (int64_t) r8 * p.ldv;
+    auto issue = [&](int tile, int buf) {
+        uint16_t *dst = gb + buf * TILE_H;
+        const int key0 = tile * KT;
+        const bool last = tile == ntiles - 1;
+#pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+            const int j = qb + QB * i;
+            if (j >= 16) break;
+            const int ch = (j & 1) ? ch1 : ch0;
+            const void *src;
+            if (j < 8) {
+                const int rowu = key0 + (j & 7) * 8;                 // wave-uniform part of the key row
+                src = last ? (const void *) (kp + (int64_t) min(rowu + r8, p.Nkv - 1) * p.k_nb1 + ch * 16)
+                           : (const void *) (krow0 + (int64_t) rowu * p.k_nb1 + ch * 16);
+            } else {
+                src = vrow0 + (int64_t) ((j & 7) * 8) * p.ldv + key0 + ch * 8;
+            }
+            __builtin_amdgcn_global_load_lds(src, (lds_void *) (dst + j * 512), 16, 0, 0);
+        }
+    };
+
+    f32x16 o[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] = 0.0f;
+    // running max m (log2 domain, scaled logits); cm = -m (-m / c for bf16 K)
+    // seeds the S^T accumulators. Before the first tile m is unset: cm = 0
+    // and the first 32 keys set m to their own max. BOUNDED: the caller has
+    // shown |logit * scale * log2(e)| <= ATTN_LOGIT_BOUND for every pair, so
+    // m stays 0: P <= 2^ATTN_LOGIT_BOUND fits fp16 and no max is needed.
+    float m_run = BOUNDED ? 0.0f : -INFINITY, l_run = 0.0f;
+    f32x16 cm;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) cm[e] = 0.0f;
+    const f16x2 one = {(_Float16) 1.0f, (_Float16) 1.0f};
+
+    // NB - 1 tiles in flight ahead of the one being read
+    if (t0 < tend) issue(t0, 0);
+    if constexpr (NB == 3) {
+        if (t0 + 1 < tend) {
+            issue(t0 + 1, 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 / QB) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+
+    int buf = 0;
+    for (int it = 0; it < tpg; ++it) {
+        const int tile = t0 + it;
+        const uint16_t *kb = gb + buf * TILE_H;
+        const uint16_t *vb = kb + KT * 64;
+        const int nbuf_next = buf + (NB - 1) >= NB ? buf - 1 : buf + (NB - 1);   // (buf + NB - 1) % NB
+        if (tile < tend) {
+            // all fragments of this tile first, then the loads NB - 1 tiles ahead
+            u32x4 kf[2][4];
+            f16x8 vf[2][4];
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) kf[mb][ks] = *(const u32x4 *) (kb + swz(32 * mb + l32, 2 * ks + hi));
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) vf[db][cc] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
+            if (tile + NB - 1 < tend) issue(tile + NB - 1, nbuf_next);
+
+            // S^T - m = K . Q^T + cm: s[mb][4 r + jj] for key 32 mb + 8 r + 4 hi + jj, query l32
+            f32x16 s[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+                if constexpr (BOUNDED) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) s[mb][e] = 0.0f;
+                } else {
+                    s[mb] = cm;
+                }
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if constexpr (KBF16)
+                        s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kf[mb][ks]),
+                                                                         __builtin_bit_cast(bf16x8, qraw[ks]), s[mb], 0, 0, 0);
+                    else
+                        s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[mb][ks]),
+                                                                        __builtin_bit_cast(f16x8, qraw[ks]), s[mb], 0, 0, 0);
+                }
+            }
+            const int lim = tile == ntiles - 1 ? p.Nkv - tile * KT : KT;
+            // softmax and P.V per 32-key half: the second half's MFMAs overlap
+            // the first half's exponentials, the first half's P.V the second's
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+                if constexpr (KBF16) s[mb] *= c;
+                if (lim < KT) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (32 * mb + 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) s[mb][e] = -INFINITY;
+                }
+                if constexpr (!BOUNDED) {
+                float mx = s[mb][0];
+#pragma unroll
+                for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[mb][e]);
+                {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // both halves of the wave: same query
+                }
+                // lazy rescale: m moves only when these keys exceed it by more
+                // than RESCALE_T (or when it is unset, on the first keys)
+                if (__any(!(m_run > -INFINITY) || mx > RESCALE_T)) {
+                    const bool set = m_run > -INFINITY;
+                    const float dm = set ? fmaxf(mx, 0.0f) : mx;                    // new m = m + dm
+                    const float alpha = set ? __builtin_amdgcn_exp2f(-dm) : 0.0f;   // o, l are 0 before
+                    l_run *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 2; ++db) o[db] *= alpha;
+                    m_run = set ? m_run + dm : mx;
+                    s[mb] -= dm;
+                    if (mb == 0) s[1] -= KBF16 ? dm / c : dm;     // s[1] still holds K.Q^T - old m (unscaled for bf16)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) cm[e] = KBF16 ? -m_run / c : -m_run;
+                }
+                }
+                // P^T (B operand) for keys 16 cc .. 16 cc + 15, cc = 2 mb + h2:
+                // accumulator slots 8 h2 + 0..7 of s[mb]
+                f16x8 pf[2];
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) pf[h2][t] = (_Float16) __builtin_amdgcn_exp2f(s[mb][8 * h2 + t]);
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) {
+                        const f16x2 pr = {pf[h2][t], pf[h2][t + 1]};
+                        l_run = __builtin_amdgcn_fdot2(pr, one, l_run, false);
+                    }
+                // O^T += V^T . P^T
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2)
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[db][2 * mb + h2], pf[h2], o[db], 0, 0, 0);
+            }
+        }
+        // the next tile has landed (this wave's loads; the barrier covers the others')
+        if constexpr (NB == 3) {
+            if (tile + 2 < tend) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 / QB) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        buf = buf + 1 == NB ? 0 : buf + 1;
+    }
+
+    // ---- merge the KS key ranges of each query block (LDS reused)
+    if constexpr (KS > 1) {
+        float *mo = (float *) lds;                        // [KS-1][QB][32][64] partial O^T
+        float *ml = mo + (KS - 1) * QB * 32 * 64;         // [KS-1][QB][2][64]  m, l
+        if (g > 0) {
+            float *dst = mo + ((g - 1) * QB + qb) * 32 * 64;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) dst[(16 * db + e) * 64 + lane] = o[db][e];
+            float *dl = ml + ((g - 1) * QB + qb) * 128;
+            dl[lane] = m_run;
+            dl[64 + lane] = l_run;
+        }
+        __syncthreads();
+        if (g > 0) return;
+        for (int g2 = 1; g2 < KS; ++g2) {
+            const float *src = mo + ((g2 - 1) * QB + qb) * 32 * 64;
+            const float *sl = ml + ((g2 - 1) * QB + qb) * 128;
+            const float m2 = sl[lane], l2 = sl[64 + lane];
+            const float mn = fmaxf(m_run, m2);
+            if (mn == -INFINITY) continue;                // neither side saw a key
+            const float a1 = __builtin_amdgcn_exp2f(m_run - mn), a2 = __builtin_amdgcn_exp2f(m2 - mn);
+            l_run = l_run * a1 + l2 * a2;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[db][e] = o[db][e] * a1 + src[(16 * db + e) * 64 + lane] * a2;
+            m_run = mn;
+        }
+    }
+
+    // ---- O = O^T / l; lane writes dims 32 db + 8 r + 4 hi + 0..3 of query q0 + l32
+    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int q = q0 + l32;
+    if (q >= p.Nq) return;
+    char *orow = (char *) p.o + (int64_t) b * p.o_nb3 + (int64_t) q * p.o_nb2 + (int64_t) h * p.o_nb1;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d0 = 32 * db + 8 * r + 4 * hi;
+            if (p.out_bf16) {
+                uint16_t t4[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) t4[jj] = f32_to_bf16_bits(o[db][4 * r + jj] * inv);
+                u32x2 w;
+                __builtin_memcpy(&w, t4, 8);
+                *(u32x2 *) (orow + 2 * d0) = w;
+            } else {
+                *(f32x4 *) (orow + 4 * d0) = f32x4{o[db][4 * r] * inv, o[db][4 * r + 1] * inv,
+                                                  o[db][4 * r + 2] * inv, o[db][4 * r + 3] * inv};
+            }
+        }
+}
+
+template <bool KBF16, bool BOUNDED, int KS, int QB>
+hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
+    AttnFastParams p = p0;
+    p.qtiles = (p.Nq + QB * 32 - 1) / (QB * 32);
+    const int W = p.qtiles * p.H * p.B;
+    const int grid = (W + 7) / 8 * 8;
+    size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
+    if (KS > 1) lds = max(lds, (size_t) (KS - 1) * QB * (32 * 64 + 128) * 4);
+    auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB>;
+    static size_t attr = 0;
+    if (lds > attr) {
+        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
+            hipSuccess)
+            (void) hipGetLastError();
+        attr = lds;
+    }
+    launch_kernel(kern, dim3(grid), dim3(64 * KS * QB), lds, s, p);
+    return hipGetLastError();
+}
+
+template <bool KBF16, bool BOUNDED>
+hipError_t launch_cfg(const AttnFastParams &p, int cfg, hipStream_t s) {
+    switch (cfg) {
+        case 41: return launch_ks_qb<KBF16, BOUNDED, 4, 1>(p, s);
+        case 42: return launch_ks_qb<KBF16, BOUNDED, 4, 2>(p, s);
+        case 43: return launch_ks_qb<KBF16, BOUNDED, 4, 3>(p, s);
+        case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1>(p, s);
+        case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2>(p, s);
+        case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4>(p, s);
+        case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4>(p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// V [rows of 64] (F16 or BF16, ggml strides) -> V^T fp16 [B*H][64][ldv] at
+// positions vt_pos(key), zero from Nkv to ldv. One workgroup per 64 keys.
+__global__ __launch_bounds__(256) void vt_transpose_kernel(const void *v, int v_bf16, int64_t nb1, int64_t nb2,
+                                                           int64_t nb3, int Nkv, int H, uint16_t *vt, int ldv) {
+    __shared__ uint16_t t[64][66];
+    const int bh = blockIdx.y, b = bh / H, h = bh % H, k0 = blockIdx.x * 64;
+    const char *vb = (const char *) v + (int64_t) h * nb2 + (int64_t) b * nb3;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int kk = i / 64, d = i % 64;
+        uint16_t x = 0;
+        if (k0 + kk < Nkv) {
+            x = *(const uint16_t *) (vb + (int64_t) (k0 + kk) * nb1 + 2 * d);
+            if (v_bf16) x = f32_to_f16_bits(bf16_bits_to_f32(x));
+        }
+        t[kk][d] = x;
+    }
+    __syncthreads();
+    uint16_t *dst = vt + (int64_t) bh * 64 * ldv + k0;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int d = i / 64, pos = i % 64;
+        dst[(int64_t) d * ldv + pos] = t[vt_pos(pos)][d];
+    }
+}
+
+}  // namespace
+
+// (key ranges, query blocks) per workgroup, from MI355X sweeps over the
+// MM-DiT shapes (B=2, 16 heads, N = 194 .. 1040): 32-row query blocks of all
+// (batch, head) pairs spread over the 256 CUs with 2-3 waves per SIMD
+int attn_fast_default_cfg(int Nq, int H, int B, int bounded) {
+    const int qblocks = (Nq + 31) / 32 * H * B;
+    if (qblocks >= 640) return bounded ? 43 : 24;
+    if (qblocks >= 256) return 42;
+    return 41;
+}
+
+hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
+    if (p.Nq < 1 || p.Nkv < 1 || p.H < 1 || p.B < 1 || p.ldv < (p.Nkv + KT - 1) / KT * KT) return hipErrorInvalidValue;
+    const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.bounded && !p.k_bf16);
+    if (p.bounded && !p.k_bf16) return launch_cfg<false, true>(p, cfg, s);
+    return p.k_bf16 ? launch_cfg<true, false>(p, cfg, s) : launch_cfg<false, false>(p, cfg, s);
+}
+
+hipError_t launch_vt_transpose(const void *v, int v_bf16, int64_t nb1, int64_t nb2, int64_t nb3, int Nkv, int H, int B,
+                               uint16_t *vt, int ldv, hipStream_t s) {
+    launch_kernel(vt_transpose_kernel, dim3(ldv / 64, H * B), dim3(256), 0, s, v, v_bf16, nb1, nb2, nb3, Nkv, H,
+                       vt, ldv);
+    return hipGetLastError();
+}
+
+}  // namespace tsk

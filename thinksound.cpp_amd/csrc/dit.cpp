@@ -21,6 +21,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -41,6 +42,7 @@ struct WInfo {
     bool qkv_perm;         // rows (or entries) permuted (h d j) -> [q | k | v]
     bool tiled;            // stored in the MFMA-tiled layout of the block GEMMs
     size_t offset;         // bytes into the weight blob
+    float amax;            // max |value| of a vector as last set (0 until then)
 };
 
 struct RoleTiming {
@@ -62,6 +64,7 @@ struct StreamW {           // one MMDitSingleBlock's weights
     bool pre_only;
     float *mod;            // [max_batch][nmod * H] adaLN output
     int nmod;
+    int qn_idx, kn_idx;    // tensor indices of the q / k RMSNorm weights
 };
 
 }  // namespace
@@ -80,13 +83,16 @@ struct tsk_dit {
     float *final_mod = nullptr;     // [max_batch][2H] final-layer adaLN output
     // bf16 activations: xn [rows][H] (LN outputs), h [rows][F] (GELU outputs),
     // latent rows first, text rows from the fixed offset max_batch * max_latent;
-    // fp16 attention operands q/k/v [B][n_head][Ntot][64]; o bf16 [B][Ntot][H]
-    uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *h = nullptr;
+    // fp16 attention operands q/k [B][n_head][Ntot][64], V transposed
+    // vt [B][n_head][64][ldv] (key positions vt_pos()); o bf16 [B][Ntot][H]
+    uint16_t *xn = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr, *o = nullptr, *h = nullptr;
+    int ldv = 0;
     float *part = nullptr;          // split-K partial sums [KSPLIT_MAX][rows][H], text at the same offset rule
     GemvJob *jobs_dev = nullptr;    // [adaLN jobs..., t_embed.0, t_embed.2]
     int njobs = 0, max_job_m = 0;
     float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
     bool timing = false;
+    int attn_cfg = 0;               // attention launch shape override (0: automatic)
     RoleTiming rt[TSK_ROLE_COUNT];
     // sampler buffers
     float *s_x = nullptr, *s_x2 = nullptr, *s_text2 = nullptr, *s_flow2 = nullptr, *s_flow0 = nullptr;
@@ -96,8 +102,9 @@ namespace {
 
 int hipcheck(hipError_t e, const char *what) { return e == hipSuccess ? TSK_OK : hip_fail(e, what); }
 
-// Records an event pair around the launches made in its lifetime when the
-// driver's timing is enabled, and books their algorithmic FLOPs / bytes.
+// Makes the launches in its lifetime stamp an event pair with their own
+// execution start / end (launch_kernel) when the driver's timing is enabled,
+// and books their algorithmic FLOPs / bytes.
 struct Timed {
     RoleTiming *r = nullptr;
     hipEvent_t stop = nullptr;
@@ -118,10 +125,10 @@ struct Timed {
         r->launches += 1;
         r->flop += flop;
         r->bytes += bytes;
-        (void) hipEventRecord(start, st);
+        launch_events() = LaunchEvents{start, stop};
     }
     ~Timed() {
-        if (r) (void) hipEventRecord(stop, st);
+        if (r) launch_events() = LaunchEvents{nullptr, nullptr};
     }
 };
 
@@ -135,6 +142,7 @@ void add(tsk_dit *d, const std::string &name, int64_t ne0, int64_t ne1, bool mat
     wi.qkv_perm = perm;
     wi.tiled = tiled;
     wi.offset = 0;
+    wi.amax = 0.0f;
     d->idx[name] = (int) d->w.size();
     d->w.push_back(wi);
 }
@@ -173,6 +181,8 @@ StreamW stream_weights(tsk_dit *d, const std::string &p, bool pre_only) {
     s.qkv_b = wptr<float>(d, p + ".attn.qkv.bias");
     s.qn = wptr<float>(d, p + ".attn.q_norm.weight");
     s.kn = wptr<float>(d, p + ".attn.k_norm.weight");
+    s.qn_idx = d->idx.at(p + ".attn.q_norm.weight");
+    s.kn_idx = d->idx.at(p + ".attn.k_norm.weight");
     if (!pre_only) {
         s.l1_w = wptr<uint16_t>(d, p + ".linear1.weight");
         s.l1_b = wptr<float>(d, p + ".linear1.bias");
@@ -233,7 +243,7 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     for (auto &r : d->rt)
         for (hipEvent_t e : r.ev) (void) hipEventDestroy(e);
     void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
-                    d->q, d->k, d->v, d->o, d->h, d->jobs_dev, d->freq,
+                    d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
@@ -248,6 +258,8 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     if ((rc = require_init())) return rc;
     tsk_dit *d = new tsk_dit();
     d->cfg = *cfg;
+    // attention launch shape override for tuning sweeps: 10 * key ranges + query blocks
+    if (const char *ac = getenv("TSK_ATTN_CFG")) d->attn_cfg = atoi(ac);
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -274,6 +286,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
 
     const int B = c.max_batch, T = c.max_latent, St = c.text_seq, F = c.mlp_hidden;
     const int64_t rows = (int64_t) B * (T + St);
+    d->ldv = (T + St + 63) / 64 * 64;
     auto alloc = [&](void **p, size_t bytes) -> int {
         hipError_t e = hipMalloc(p, bytes);
         if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -296,7 +309,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->part, sizeof(float) * KSPLIT_MAX * rows * H)) ||
         (rc = alloc((void **) &d->q, 2 * rows * H)) ||
         (rc = alloc((void **) &d->k, 2 * rows * H)) ||
-        (rc = alloc((void **) &d->v, 2 * rows * H)) ||
+        (rc = alloc((void **) &d->vt, 2 * (size_t) B * H * d->ldv)) ||
         (rc = alloc((void **) &d->o, 2 * rows * H)) ||
         (rc = alloc((void **) &d->h, 2 * rows * F)) ||
         (rc = alloc((void **) &d->jobs_dev, sizeof(GemvJob) * (nstreams + 3))) ||
@@ -311,6 +324,10 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     hipError_t e = hipMemcpy(d->freq, fr.data(), sizeof(float) * (H / 2), hipMemcpyHostToDevice);
     if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemcpy freq"); }
     e = hipMemset(d->blob, 0, d->blob_bytes);
+    if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemset"); }
+    // V^T key positions past a call's token count are read (and multiplied by
+    // P = 0) by the attention kernel: they must hold finite values
+    e = hipMemset(d->vt, 0, 2 * (size_t) B * H * d->ldv);
     if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemset"); }
 
     // per-stream weights and adaLN job table
@@ -385,6 +402,11 @@ extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src
         s = perm.data();
     }
     char *dst = d->blob + wi.offset;
+    if (!wi.matrix) {
+        float a = 0.0f;
+        for (int64_t i = 0; i < n; ++i) a = fmaxf(a, fabsf(src[i]));
+        d->w[it->second].amax = a;
+    }
     hipError_t e;
     if (wi.matrix) {
         std::vector<uint16_t> bf((size_t) n);
@@ -486,11 +508,12 @@ int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         GemmProblem &q = g.p[i];
         q = gemm_problem(r[i].xn, H, r[i].w->qkv_w, r[i].w->qkv_b, nullptr, 0, rows, H, 3 * H);
         q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
-        q.q = d->q; q.k = d->k; q.v = d->v;
+        q.q = d->q; q.k = d->k; q.vt = d->vt; q.ldv = d->ldv;
         q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope;
         q.theta_scale = powf(c.rope_theta, -2.0f / (float) c.head_dim);
         q.freq_scale = 1.0f;
         q.eps = c.qk_eps;
+        q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), see attention()
         fl += 2.0 * rows * H * 3.0 * H;
         by += 2.0 * 3 * H * H + 2.0 * rows * H + 2.0 * rows * 3 * H + 12.0 * H;
     }
@@ -557,25 +580,38 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     return hipcheck(launch_gemm_group(g2, 0, EPI_PARTIAL, st), "fc2 gemm");
 }
 
-int attention(tsk_dit *d, int B, int Ntot, hipStream_t st) {
+// Attention over the concatenated q/k/vt of the streams in r[0..ns). q was
+// written pre-multiplied by scale * log2(e) (run_qkv). q and k are RMS-normed
+// (|x / rms(x)| = 8 for 64 dims) times w, and RoPE is a rotation, so every
+// logit obeys |q.k| * scale * log2(e) <= 64 * scale * log2(e) * max|w_q| *
+// max|w_k| over the streams: under ATTN_LOGIT_BOUND the kernel needs no
+// running max.
+int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
-    AttnParams p;
+    AttnFastParams p;
     memset(&p, 0, sizeof(p));
-    p.q = d->q; p.k = d->k; p.v = d->v; p.o = d->o;
-    p.q_type = p.kv_type = TSK_TYPE_F16;
-    p.out_bf16 = 1;
-    p.mask_f16 = 1;
-    p.Nq = p.Nkv = Ntot; p.H = p.Hkv = c.n_head; p.B = B;
-    p.q_nb1 = p.k_nb1 = p.v_nb1 = 128;
-    p.q_nb2 = p.k_nb2 = p.v_nb2 = (int64_t) 128 * Ntot;
-    p.q_nb3 = p.k_nb3 = p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;
-    p.m_ne2 = p.m_ne3 = 1;
-    p.o_nb1 = 128; p.o_nb2 = (int64_t) 128 * c.n_head; p.o_nb3 = (int64_t) 128 * c.n_head * Ntot;
-    p.scale = 1.0f / sqrtf((float) c.head_dim);
-    p.n_head_log2 = 1;
+    p.q = d->q; p.k = d->k; p.vt = d->vt; p.o = d->o;
+    p.q_type = TSK_TYPE_F16; p.k_bf16 = 0; p.out_bf16 = 1;
+    p.Nq = p.Nkv = Ntot; p.H = c.n_head; p.B = B;
+    p.q_nb1 = p.k_nb1 = 128;
+    p.q_nb2 = p.k_nb2 = (int64_t) 128 * Ntot;
+    p.q_nb3 = p.k_nb3 = (int64_t) 128 * Ntot * c.n_head;
+    p.vt_bh = (int64_t) 64 * d->ldv;
+    p.ldv = d->ldv;
+    p.o_nb1 = 128; p.o_nb2 = (int64_t) 2 * c.hidden; p.o_nb3 = (int64_t) 2 * c.hidden * Ntot;
+    p.c = 1.4426950408889634f / sqrtf((float) c.head_dim);
+    p.q_prescaled = 1;
+    float aq = 0.0f, ak = 0.0f;
+    for (int i = 0; i < ns; ++i) {
+        aq = fmaxf(aq, d->w[r[i].w->qn_idx].amax);
+        ak = fmaxf(ak, d->w[r[i].w->kn_idx].amax);
+    }
+    // 1 % margin for the fp16 rounding of q and k
+    p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
+    p.force_cfg = d->attn_cfg;
     const double nn = (double) Ntot * Ntot;
     Timed tm(d, TSK_ROLE_ATTN, 4.0 * B * c.n_head * nn * c.head_dim, 4.0 * 2.0 * B * Ntot * c.hidden, st);
-    return hipcheck(launch_attention(p, st), "attention");
+    return hipcheck(launch_attn_fast(p, st), "attention");
 }
 
 int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host, const float *text_d,
@@ -628,7 +664,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         StreamRun r2[2] = {L, X};
         if ((rc = run_ln(d, r2, 2, B, 0, st))) return rc;
         if ((rc = run_qkv(d, r2, 2, B, Nj, st))) return rc;
-        if ((rc = attention(d, B, Nj, st))) return rc;
+        if ((rc = attention(d, r2, 2, B, Nj, st))) return rc;
         if ((rc = run_out(d, r2, 2, B, Nj, st))) return rc;
         const int ns = r2[1].w->pre_only ? 1 : 2;
         if ((rc = run_ln(d, r2, ns, B, 1, st))) return rc;
@@ -641,7 +677,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         L.w = &d->fused[i];
         if ((rc = run_ln(d, &L, 1, B, 0, st))) return rc;
         if ((rc = run_qkv(d, &L, 1, B, T, st))) return rc;
-        if ((rc = attention(d, B, T, st))) return rc;
+        if ((rc = attention(d, &L, 1, B, T, st))) return rc;
         if ((rc = run_out(d, &L, 1, B, T, st))) return rc;
         if ((rc = run_ln(d, &L, 1, B, 1, st))) return rc;
         if ((rc = run_mlp(d, &L, 1, B, st))) return rc;

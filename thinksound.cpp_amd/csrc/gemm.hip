@@ -361,13 +361,13 @@ hipError_t gemm_bf16_epi(const GemmParams &p, hipStream_t s) {
     dim3 block(WM * WN * 64);
     switch (p.epi) {
         case EPI_GELU:
-            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GELU, YBF16>), grid, block, 0, s, p);
+            launch_kernel((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GELU, YBF16>), grid, block, 0, s, p);
             break;
         case EPI_GATE_RES:
-            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GATE_RES, false>), grid, block, 0, s, p);
+            launch_kernel((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_GATE_RES, false>), grid, block, 0, s, p);
             break;
         default:
-            hipLaunchKernelGGL((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_STORE, YBF16>), grid, block, 0, s, p);
+            launch_kernel((gemm_bf16_kernel<WM, WN, TM, TN, XF32, EPI_STORE, YBF16>), grid, block, 0, s, p);
     }
     return hipGetLastError();
 }
@@ -380,13 +380,13 @@ hipError_t gemm_q8_epi(const GemmParams &p, hipStream_t s) {
     dim3 block(WM * WN * 64);
     switch (p.epi) {
         case EPI_GELU:
-            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_GELU, YBF16>), grid, block, 0, s, p);
+            launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_GELU, YBF16>), grid, block, 0, s, p);
             break;
         case EPI_GATE_RES:
-            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_GATE_RES, false>), grid, block, 0, s, p);
+            launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_GATE_RES, false>), grid, block, 0, s, p);
             break;
         default:
-            hipLaunchKernelGGL((gemm_q8_kernel<WM, WN, TM, TN, EPI_STORE, YBF16>), grid, block, 0, s, p);
+            launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_STORE, YBF16>), grid, block, 0, s, p);
     }
     return hipGetLastError();
 }
@@ -398,7 +398,7 @@ hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s) {
         // thin f32-accurate projections (input / output of the DiT): 32 x 64 tiles, plain store
         if (!p.x_f32 || p.epi != EPI_STORE || p.y_bf16) return hipErrorInvalidValue;
         dim3 grid((p.M + 31) / 32, (p.N + 63) / 64);
-        hipLaunchKernelGGL((gemm_bf16_kernel<2, 2, 1, 2, true, EPI_STORE, false, true>), grid, dim3(256), 0, s, p);
+        launch_kernel((gemm_bf16_kernel<2, 2, 1, 2, true, EPI_STORE, false, true>), grid, dim3(256), 0, s, p);
         return hipGetLastError();
     }
     if (p.epi != EPI_STORE) return hipErrorInvalidValue;
@@ -422,8 +422,8 @@ hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N
     const int64_t nblk = (int64_t) N * (K / 32);
     const int threads = 256;
     dim3 grid((unsigned) ((nblk + threads - 1) / threads));
-    if (x_f32) hipLaunchKernelGGL(quantize_rows_q8_kernel<true>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
-    else hipLaunchKernelGGL(quantize_rows_q8_kernel<false>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
+    if (x_f32) launch_kernel(quantize_rows_q8_kernel<true>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
+    else launch_kernel(quantize_rows_q8_kernel<false>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
     return hipGetLastError();
 }
 

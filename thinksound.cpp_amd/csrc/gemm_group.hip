@@ -276,11 +276,17 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
                 }
             }
             if (live) {
-                uint16_t *dst = sec == 0 ? p.q : sec == 1 ? p.k : p.v;
+                if (sec == 0)
+                    for (int e = 0; e < 4; ++e) x[e] *= p.q_scale;     // the attention's softmax scale
                 uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]), f32_to_f16_bits(x[3])};
-                u32x2 w2;
-                __builtin_memcpy(&w2, o4, 8);
-                *(u32x2 *) (dst + (((int64_t) b * nh + head) * p.Ntot + p.tok_off + spos) * 64 + 4 * sl) = w2;
+                if (sec < 2) {
+                    u32x2 w2;
+                    __builtin_memcpy(&w2, o4, 8);
+                    *(u32x2 *) ((sec ? p.k : p.q) + (((int64_t) b * nh + head) * p.Ntot + p.tok_off + spos) * 64 + 4 * sl) = w2;
+                } else {
+                    uint16_t *vcol = p.vt + (((int64_t) b * nh + head) * 64 + 4 * sl) * p.ldv + vt_pos(p.tok_off + spos);
+                    for (int e = 0; e < 4; ++e) vcol[(int64_t) e * p.ldv] = o4[e];
+                }
             }
         }
         return;
@@ -333,7 +339,7 @@ hipError_t launch_cfg(const GemmGroup &g, int KC, int nblocks, size_t lds, hipSt
             (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
         attr = lds;
     }
-    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(NT), lds, s, g, KC);
+    launch_kernel(kern, dim3(nblocks), dim3(NT), lds, s, g, KC);
     return hipGetLastError();
 }
 

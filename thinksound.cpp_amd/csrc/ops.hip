@@ -310,20 +310,20 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1
 
 hipError_t launch_rms_norm_mul(const View4 &x, const float *w, float eps, const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
-    hipLaunchKernelGGL(rms_norm_mul_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, w, eps, y, rows);
+    launch_kernel(rms_norm_mul_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, w, eps, y, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_norm(const View4 &x, float eps, const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
-    hipLaunchKernelGGL(norm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, eps, y, rows);
+    launch_kernel(norm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, eps, y, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_rope(const View4 &x, const int32_t *pos, int n_dims, float theta_scale, float freq_scale,
                        const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
-    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, pos, n_dims, theta_scale,
+    launch_kernel(rope_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, pos, n_dims, theta_scale,
                        freq_scale, y, rows);
     return hipGetLastError();
 }
@@ -331,66 +331,66 @@ hipError_t launch_rope(const View4 &x, const int32_t *pos, int n_dims, float the
 hipError_t launch_qk_norm_rope(const View4 &x, const float *w, const int32_t *pos, float eps, int n_dims,
                                float theta_scale, float freq_scale, const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(blocks_for(rows, 8)), dim3(256), 0, s, x, w, pos, eps, n_dims,
+    launch_kernel(qk_norm_rope_kernel, dim3(blocks_for(rows, 8)), dim3(256), 0, s, x, w, pos, eps, n_dims,
                        theta_scale, freq_scale, y, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_quantize_blocks(const float *x, int64_t ld_x, int64_t rows, int64_t K, void *blocks,
                                      int64_t ld_blocks, hipStream_t s) {
-    hipLaunchKernelGGL(q8_quantize_blocks_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, x, ld_x,
+    launch_kernel(q8_quantize_blocks_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, x, ld_x,
                        rows, K, (char *) blocks, ld_blocks);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_dequantize(const void *src, int split, int64_t rows, int64_t K, int64_t ld_src, float *y,
                                 int64_t ld_y, hipStream_t s) {
-    hipLaunchKernelGGL(q8_dequantize_kernel, dim3(blocks_for(rows * K, 256)), dim3(256), 0, s, (const char *) src,
+    launch_kernel(q8_dequantize_kernel, dim3(blocks_for(rows * K, 256)), dim3(256), 0, s, (const char *) src,
                        split, rows, K, ld_src, y, ld_y);
     return hipGetLastError();
 }
 
 hipError_t launch_q8_repack(const void *src, int64_t ld_src, int64_t rows, int64_t K, void *dst, hipStream_t s) {
-    hipLaunchKernelGGL(q8_repack_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, (const char *) src,
+    launch_kernel(q8_repack_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, (const char *) src,
                        ld_src, rows, K, (char *) dst);
     return hipGetLastError();
 }
 
 hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+    launch_kernel(f32_to_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
     return hipGetLastError();
 }
 
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
-    if (g.y_f32) hipLaunchKernelGGL(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
-    else hipLaunchKernelGGL(ln_group_kernel<false>, dim3(rows), dim3(256), 0, s, g);
+    if (g.y_f32) launch_kernel(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
+    else launch_kernel(ln_group_kernel<false>, dim3(rows), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K, hipStream_t s) {
     dim3 grid(blocks_for(max_m, 4), njobs);
-    if (B <= 2) hipLaunchKernelGGL(gemv_jobs_kernel<2>, grid, dim3(256), 0, s, jobs_dev, B, K);
-    else if (B <= 8) hipLaunchKernelGGL(gemv_jobs_kernel<8>, grid, dim3(256), 0, s, jobs_dev, B, K);
-    else hipLaunchKernelGGL(gemv_jobs_kernel<32>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    if (B <= 2) launch_kernel(gemv_jobs_kernel<2>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    else if (B <= 8) launch_kernel(gemv_jobs_kernel<8>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    else launch_kernel(gemv_jobs_kernel<32>, grid, dim3(256), 0, s, jobs_dev, B, K);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n);
+    launch_kernel(silu_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n);
     return hipGetLastError();
 }
 
 hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb, hipStream_t s) {
-    hipLaunchKernelGGL(timestep_embed_kernel, dim3(blocks_for((int64_t) B * (H / 2), 256)), dim3(256), 0, s, freq, tv,
+    launch_kernel(timestep_embed_kernel, dim3(blocks_for((int64_t) B * (H / 2), 256)), dim3(256), 0, s, freq, tv,
                        B, H, temb);
     return hipGetLastError();
 }
 
 hipError_t launch_cfg_euler(const float *flow2, int64_t n, float cfg, float dt, float *x, float *x2, float *flow0,
                             hipStream_t s) {
-    hipLaunchKernelGGL(cfg_euler_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, flow2, n, cfg, dt, x, x2, flow0);
+    launch_kernel(cfg_euler_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, flow2, n, cfg, dt, x, x2, flow0);
     return hipGetLastError();
 }
 

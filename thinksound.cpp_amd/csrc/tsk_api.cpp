@@ -17,6 +17,9 @@ using namespace tsk;
 namespace tsk {
 
 static thread_local char g_err[512];
+static thread_local LaunchEvents g_launch_events = {nullptr, nullptr};
+
+LaunchEvents &launch_events() { return g_launch_events; }
 
 int fail(int status, const char *fmt, ...) {
     va_list ap;
@@ -326,6 +329,25 @@ int validate_fa(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v, c
     return TSK_OK;
 }
 
+// Nodes the MFMA 32x32 kernel of attn_dit.hip runs: head_dim 64 (checked by
+// validate_fa), 16-bit K/V, one KV head per head, no mask / softcap / ALiBi,
+// 16-byte aligned rows.
+bool fa_fast_eligible(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v, const tsk_tensor *mask,
+                      float max_bias, float softcap, const tsk_tensor *dst) {
+    if (mask || max_bias != 0.0f || softcap != 0.0f) return false;
+    if (k->type != TSK_TYPE_F16 && k->type != TSK_TYPE_BF16) return false;
+    if (v->type != TSK_TYPE_F16 && v->type != TSK_TYPE_BF16) return false;
+    if (k->ne[2] != q->ne[2] || k->ne[3] != q->ne[3]) return false;
+    if (q->ne[1] > (1 << 24) || k->ne[1] > (1 << 24)) return false;
+    const tsk_tensor *rows16[3] = {q, k, dst};
+    for (const tsk_tensor *t : rows16) {
+        if (!aligned(t->data, 16)) return false;
+        for (int i = 1; i < 4; ++i)
+            if (t->nb[i] % 16) return false;
+    }
+    return true;
+}
+
 }  // namespace
 
 extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
@@ -334,6 +356,31 @@ extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, cons
     int rc = validate_fa(q, k, v, mask, scale, max_bias, logit_softcap, prec, dst);
     if (rc) return rc;
     if ((rc = require_init())) return rc;
+    if (fa_fast_eligible(q, k, v, mask, max_bias, logit_softcap, dst)) {
+        // transposed fp16 V in the workspace, then the MFMA 32x32 kernel
+        const int Nkv = (int) k->ne[1], H = (int) q->ne[2], B = (int) q->ne[3];
+        const int ldv = (Nkv + 63) / 64 * 64;
+        void *ws = nullptr;
+        if ((rc = workspace((size_t) 2 * B * H * 64 * ldv, &ws))) return rc;
+        hipStream_t st = (hipStream_t) stream;
+        hipError_t e = launch_vt_transpose(v->data, v->type == TSK_TYPE_BF16, (int64_t) v->nb[1], (int64_t) v->nb[2],
+                                           (int64_t) v->nb[3], Nkv, H, B, (uint16_t *) ws, ldv, st);
+        if (e != hipSuccess) return hip_fail(e, "flash_attn_ext V transpose");
+        AttnFastParams f;
+        memset(&f, 0, sizeof(f));
+        f.q = q->data; f.k = k->data; f.vt = (const uint16_t *) ws; f.o = dst->data;
+        f.q_type = q->type; f.k_bf16 = k->type == TSK_TYPE_BF16; f.out_bf16 = dst->type == TSK_TYPE_BF16;
+        f.Nq = (int) q->ne[1]; f.Nkv = Nkv; f.H = H; f.B = B;
+        f.q_nb1 = q->nb[1]; f.q_nb2 = q->nb[2]; f.q_nb3 = q->nb[3];
+        f.k_nb1 = k->nb[1]; f.k_nb2 = k->nb[2]; f.k_nb3 = k->nb[3];
+        f.vt_bh = (int64_t) 64 * ldv;
+        f.ldv = ldv;
+        f.o_nb1 = dst->nb[1]; f.o_nb2 = dst->nb[2]; f.o_nb3 = dst->nb[3];
+        f.c = scale * 1.4426950408889634f;
+        e = launch_attn_fast(f, st);
+        if (e != hipSuccess) return hip_fail(e, "flash_attn_ext launch");
+        return TSK_OK;
+    }
     AttnParams p;
     memset(&p, 0, sizeof(p));
     p.q = q->data; p.k = k->data; p.v = v->data; p.o = dst->data;

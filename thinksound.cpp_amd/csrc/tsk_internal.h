@@ -3,12 +3,32 @@
 // already happened when a launcher is called.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/tsk/tsk.h"
 
 namespace tsk {
+
+// Kernel timing of the step driver: while `stop` is set on the calling
+// thread, launch_kernel() launches with hipExtLaunchKernelGGL so that the
+// dispatch packets themselves stamp `start` (first launch) and `stop` (every
+// launch; the last one stands): the events then bracket kernel execution only.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+LaunchEvents &launch_events();
+template <typename F, typename... Args>
+inline void launch_kernel(F kern, const dim3 &grid, const dim3 &block, size_t shm, hipStream_t s, Args... args) {
+    LaunchEvents &ev = launch_events();
+    if (ev.stop) {
+        hipExtLaunchKernelGGL(kern, grid, block, (uint32_t) shm, s, ev.start, ev.stop, 0u, args...);
+        ev.start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kern, grid, block, shm, s, args...);
+    }
+}
 
 // ---------------------------------------------------------------- attention
 struct AttnParams {
@@ -30,6 +50,41 @@ struct AttnParams {
     uint32_t n_head_log2;
 };
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+
+// Fast path of ggml_flash_attn_ext for head_dim 64, H == Hkv, no mask /
+// softcap / ALiBi, 16-bit K (attn_dit.hip): q rows (F32/F16/BF16) and k rows
+// (F16/BF16) with ggml byte strides (rows 16-byte aligned), V given
+// transposed as fp16 vt [B*H][64][ldv] (slice stride vt_bh elements) with the
+// key positions of every 16-key group permuted by vt_pos() (ldv >= Nkv rounded
+// up to 64; the positions past Nkv hold finite values), output F32/BF16 in
+// ggml's permuted [D, H, Nq, B] byte strides. c = scale * log2(e).
+struct AttnFastParams {
+    const void *q, *k;
+    const uint16_t *vt;
+    void *o;
+    int q_type, k_bf16, out_bf16;
+    int Nq, Nkv, H, B;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t vt_bh;
+    int ldv;
+    int64_t o_nb1, o_nb2, o_nb3;
+    float c;
+    int q_prescaled;     // q is fp16 (K's type) already multiplied by c: loaded as is
+    int bounded;         // fp16 K only: every |q.k| * c <= ATTN_LOGIT_BOUND (no running max)
+    int qtiles;          // set by the launcher
+    int force_cfg;       // 0: launcher picks; else 10 * key ranges + query blocks
+};
+// Logit bound (log2 units) under which softmax runs without a running max:
+// exp2 of it (~6e3) and sums of it over 2^14 keys stay far inside fp16 / fp32.
+constexpr float ATTN_LOGIT_BOUND = 14.0f;
+hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s);
+int attn_fast_default_cfg(int Nq, int H, int B, int bounded);
+// V (F16/BF16 rows of 64, ggml strides) -> the transposed fp16 layout above
+hipError_t launch_vt_transpose(const void *v, int v_bf16, int64_t nb1, int64_t nb2, int64_t nb3, int Nkv, int H,
+                               int B, uint16_t *vt, int ldv, hipStream_t s);
+// position of key k in a V^T row: bits 2 and 3 swapped
+__host__ __device__ inline int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 // ---------------------------------------------------------------- GEMM
 // Y[n, m] = epi( sum_k X[n, k] * W[m, k] + bias[m] ), n < N tokens, m < M.
@@ -90,10 +145,13 @@ struct GemmProblem {
     int splits;                    // K slices (EPI_PARTIAL), else 1
     // EPI_QKV: M = 3 * n_head * 64 with [q | k | v] head-major
     const float *qn_w, *kn_w;      // RMSNorm weights [64]
-    uint16_t *q, *k, *v;           // fp16 [B][n_head][Ntot][64]
+    uint16_t *q, *k;               // fp16 [B][n_head][Ntot][64]
+    uint16_t *vt;                  // fp16 [B][n_head][64][ldv], key positions vt_pos()
+    int ldv;
     int seq;                       // rows per batch item (row n -> b = n / seq, s = n % seq)
     int Ntot, tok_off, rope;
     float theta_scale, freq_scale, eps;
+    float q_scale;                 // q is multiplied by this before its fp16 cast
     // filled by launch_gemm_group
     int tiles_m, tiles_n, block_begin;
 };
