@@ -69,13 +69,30 @@ def cpu_baseline(weights, lat, t, txt, threads):
                       f"oracle C restatement of ggml-cpu semantics, {threads} threads, {dt:.2f} s"}
 
 
+def copy_calibration(nbytes=256 << 20, reps=5):
+    """A plain device-to-device copy of known size: each launch reads and writes nbytes."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (the reference kernel of known "
+                         "traffic that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the MM-DiT step on one GPU "
               f"only (CFG/data sharding over several GPUs is a design note in DESIGN.md); use --gpus 1",
@@ -117,8 +134,9 @@ def main():
     # config 2 (9 s): timed steps; per-kernel HIP events around every launch inside them
     ms_plain, _, inputs9 = run(194, args.steps, args.warmup, False)
     ms_timed, roles9, _ = run(194, args.steps, 1, True)
-    # 30 s (646 latent + 77 text tokens): steps/s and attention at N = 723
-    ms30, roles30, _ = run(646, max(5, args.steps // 2), 2, True)
+    # 30 s (646 latent + 77 text tokens): steps/s (plain), attention at N = 723 (timed)
+    ms30, _, _ = run(646, max(5, args.steps // 2), 2, False)
+    _, roles30, _ = run(646, max(5, args.steps // 2), 1, True)
 
     dom = max(roles9, key=lambda r: roles9[r][0])
     rf = roofline(dom, *roles9[dom])

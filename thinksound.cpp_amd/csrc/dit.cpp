@@ -91,6 +91,11 @@ struct tsk_dit {
     GemvJob *jobs_dev = nullptr;    // [adaLN jobs..., t_embed.0, t_embed.2]
     int njobs = 0, max_job_m = 0;
     float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
+    float *rope_cs = nullptr;       // RoPE (cos, sin) [max_latent][head_dim] of the latent positions
+    // block GEMM tile shape per projection (qkv, out, fc1, fc2), launch_gemm_ks cfg:
+    // 64 x 64 register-prefetch tiles for the QKV and out projections, 128 x 64
+    // LDS-ring tiles for the MLP, measured on MI355X at 194 .. 646 latent tokens
+    int gemm_cfg[4] = {8, 8, 4, 4};
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
     RoleTiming rt[TSK_ROLE_COUNT];
@@ -243,7 +248,7 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     for (auto &r : d->rt)
         for (hipEvent_t e : r.ev) (void) hipEventDestroy(e);
     void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
-                    d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq,
+                    d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
@@ -260,6 +265,11 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     d->cfg = *cfg;
     // attention launch shape override for tuning sweeps: 10 * key ranges + query blocks
     if (const char *ac = getenv("TSK_ATTN_CFG")) d->attn_cfg = atoi(ac);
+    // block GEMM tile shapes for tuning sweeps: one digit per projection (qkv, out, fc1, fc2)
+    // (one hex digit each, 0 = the launcher's choice)
+    if (const char *gc = getenv("TSK_GEMM_CFG"))
+        for (int i = 0; i < 4 && gc[i]; ++i)
+            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'f' ? gc[i] - 'a' + 10 : 0;
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -313,7 +323,8 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->o, 2 * rows * H)) ||
         (rc = alloc((void **) &d->h, 2 * rows * F)) ||
         (rc = alloc((void **) &d->jobs_dev, sizeof(GemvJob) * (nstreams + 3))) ||
-        (rc = alloc((void **) &d->freq, sizeof(float) * (H / 2)))) {
+        (rc = alloc((void **) &d->freq, sizeof(float) * (H / 2))) ||
+        (rc = alloc((void **) &d->rope_cs, sizeof(float) * T * c.head_dim))) {
         tsk_dit_destroy(d);
         return rc;
     }
@@ -323,6 +334,10 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     for (int kk = 0; kk < H / 2; ++kk) fr[kk] = fscale_t * powf(10000.0f, -2.0f * (float) kk / (float) H);
     hipError_t e = hipMemcpy(d->freq, fr.data(), sizeof(float) * (H / 2), hipMemcpyHostToDevice);
     if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemcpy freq"); }
+    // latent positions 0 .. max_latent - 1, freq_scale 1 (mmdit.cpp:96-99, :316-318)
+    e = launch_rope_table(d->rope_cs, T, c.head_dim, powf(c.rope_theta, -2.0f / (float) c.head_dim), 1.0f, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "rope table"); }
     e = hipMemset(d->blob, 0, d->blob_bytes);
     if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemset"); }
     // V^T key positions past a call's token count are read (and multiplied by
@@ -514,11 +529,12 @@ int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         q.freq_scale = 1.0f;
         q.eps = c.qk_eps;
         q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), see attention()
+        q.rope_cs = r[i].rope ? d->rope_cs : nullptr;
         fl += 2.0 * rows * H * 3.0 * H;
         by += 2.0 * 3 * H * H + 2.0 * rows * H + 2.0 * rows * 3 * H + 12.0 * H;
     }
     Timed tm(d, TSK_ROLE_QKV, fl, by, st);
-    return hipcheck(launch_gemm_group(g, 0, EPI_QKV, st), "qkv gemm");
+    return hipcheck(launch_gemm_ks(g, EPI_QKV, d->gemm_cfg[0], st), "qkv gemm");
 }
 
 // linear1 on the attention output (o rows of each stream: o[b][tok_off + s]),
@@ -545,7 +561,7 @@ int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     }
     if (!g.nprob) return TSK_OK;
     Timed tm(d, TSK_ROLE_OUT, fl, by, st);
-    return hipcheck(launch_gemm_group(g, 0, EPI_PARTIAL, st), "linear1 gemm");
+    return hipcheck(launch_gemm_ks(g, EPI_PARTIAL, d->gemm_cfg[1], st), "linear1 gemm");
 }
 
 int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
@@ -573,11 +589,11 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     int rc;
     {
         Timed tm(d, TSK_ROLE_FC1, fl, by1, st);
-        rc = hipcheck(launch_gemm_group(g1, 0, EPI_GELU_BF16, st), "fc1 gemm");
+        rc = hipcheck(launch_gemm_ks(g1, EPI_GELU_BF16, d->gemm_cfg[2], st), "fc1 gemm");
     }
     if (rc) return rc;
     Timed tm(d, TSK_ROLE_FC2, fl, by2, st);
-    return hipcheck(launch_gemm_group(g2, 0, EPI_PARTIAL, st), "fc2 gemm");
+    return hipcheck(launch_gemm_ks(g2, EPI_PARTIAL, d->gemm_cfg[3], st), "fc2 gemm");
 }
 
 // Attention over the concatenated q/k/vt of the streams in r[0..ns). q was

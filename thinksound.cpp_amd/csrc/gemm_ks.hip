@@ -1,0 +1,413 @@
+// gemm_ks.hip — BF16 weight GEMMs of the MM-DiT block projections on gfx950
+// (the ggml_mul_mat nodes of lin(), src/mmdit.cpp:12-25), one launch for up
+// to two independent problems (the latent and text streams of a joint block):
+//
+//   Y[n, m] = epi( sum_k X[n, k] * W[m, k] + bias[m] )
+//
+// Work split. A workgroup of four waves owns a BM x BN output tile (BM
+// weight rows, BN tokens) over its K range (a K slice when the caller asks
+// for split-K partials). The K range is cut into 32-wide stages and wave w
+// takes stages w, w + 4, w + 8, ...: the four waves compute the same tile on
+// disjoint K, so no wave ever reads another wave's operands. Each wave
+// streams its stages into a private LDS ring (R stages deep) with direct
+// global->LDS loads and waits only on its own load counter: the main loop
+// has no barrier, and R stages of every wave (up to 144 KiB per CU) are in
+// flight at once, which is what hides L2 / HBM latency at these thin shapes.
+//
+// Operand layout. A stage holds TM A fragments (16 weight rows x 32 k each,
+// 1 KiB, read as is from the MFMA-tiled weight layout of tiled_index()) and
+// TN B fragments (16 tokens x 32 k: lane l fetches token l % 16, k 8 (l / 16)
+// + 0..7, 16 bytes of a bf16 activation row). Both land in LDS in the lane
+// order of the v_mfma_f32_16x16x32_bf16 operands, so every fragment is one
+// conflict-free ds_read_b128 at lane * 16.
+//
+// The four partial tiles are summed through LDS in wave order 0, 1, 2, 3:
+// every output element is summed in the same order whatever the launch
+// shape, the token count or its tile position, so batch rows are
+// independent bit for bit. The epilogue runs on the summed tile: f32 / bf16
+// store (+bias), GELU(tanh) -> bf16, split-K partial slices (summed in fixed
+// order by their consumer), or the QKV epilogue (RMSNorm * w on q and k,
+// RoPE from a cos/sin table on the latent stream, the fp16 cast into the
+// attention layout [B][n_head][Ntot][64] and V^T, mmdit.cpp:78-90).
+#include "tsk_common.h"
+#include "tsk_internal.h"
+
+namespace tsk {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int NT = 256;   // 4 waves
+
+// 16 bytes per lane from global memory straight into LDS at lds_base + lane * 16
+__device__ __forceinline__ void g2l16(const void *src, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void *) lds_base, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait until at most `rem` stages of L loads each are still in flight
+template <int L, int R>
+__device__ __forceinline__ void wait_stages(int rem) {
+    if constexpr (R >= 4) {
+        if (rem >= 3) { wait_vm<3 * L>(); return; }
+    }
+    if constexpr (R >= 3) {
+        if (rem >= 2) { wait_vm<2 * L>(); return; }
+    }
+    if (rem >= 1) { wait_vm<L>(); return; }
+    wait_vm<0>();
+}
+
+struct Coord {
+    int pi, tm, tn, split;
+};
+
+// Workgroup -> (problem, m tile, n tile, split). Problems start at multiples of
+// 8 so that bid % 8 (the XCD the workgroup lands on) is the same in both
+// numberings; when the m tiles split evenly over the 8 XCDs, every workgroup
+// reading one weight tile runs on the same XCD and shares its L2.
+__device__ __forceinline__ bool decode(const GemmGroup &g, Coord &c) {
+    const int bid = blockIdx.x;
+    c.pi = (g.nprob > 1 && bid >= g.p[1].block_begin) ? 1 : 0;
+    const GemmProblem &p = g.p[c.pi];
+    const int li = bid - p.block_begin;
+    const int cols = p.tiles_n * p.splits;
+    if (li >= p.tiles_m * cols) return false;
+    int col;
+    if ((p.tiles_m & 7) == 0) {
+        const int s = li >> 3;
+        c.tm = (li & 7) + 8 * (s / cols);
+        col = s % cols;
+    } else {
+        c.tm = li % p.tiles_m;
+        col = li / p.tiles_m;
+    }
+    c.tn = col % p.tiles_n;
+    c.split = col / p.tiles_n;
+    return true;
+}
+
+__device__ __forceinline__ int64_t x_row(const GemmProblem &p, int n) {
+    return p.x_group_rows ? (int64_t) (n / p.x_group_rows) * p.x_group_stride + (int64_t) (n % p.x_group_rows) * p.ld_x
+                          : (int64_t) n * p.ld_x;
+}
+
+template <int TM, int TN, int R, bool DIRECT>
+constexpr size_t lds_bytes() {
+    constexpr size_t ring = DIRECT ? 0 : (size_t) 4 * R * (TM + TN) * 1024;
+    constexpr size_t red = (size_t) 4 * (16 * (TN < 4 ? TN : 4)) * (16 * TM + 4) * 4;
+    return ring > red ? ring : red;
+}
+
+template <int TM, int TN, int R, bool DIRECT, int EPI>
+__global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = L * 1024;
+
+    Coord tc;
+    if (!decode(g, tc)) return;
+    const GemmProblem &p = g.p[tc.pi];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bm0 = tc.tm * BM, bn0 = tc.tn * BN;
+    const int KT = p.K >> 5;                                  // 32-wide k tiles
+    const int kt0 = tc.split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
+    const int nst = kt1 - kt0;
+    const int my_n = nst > wave ? (nst - wave + 3) >> 2 : 0;  // stages of this wave
+
+    // A: tile (rb, kt) of the tiled weights at (rb * KT + kt) * 512 elements,
+    // this lane's 16 bytes at lane * 8. Row blocks past M read the last one
+    // (their outputs are never stored).
+    const uint16_t *wl = p.w + lane * 8;
+    int64_t aoff[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) aoff[i] = (int64_t) min((bm0 >> 4) + i, (p.M >> 4) - 1) * KT * 512;
+    // B: token bn0 + 16 j + l % 16 (tokens past N read row N - 1), k 8 (l / 16)
+    const uint16_t *bsrc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = min(bn0 + 16 * j + (lane & 15), p.N - 1);
+        bsrc[j] = (const uint16_t *) p.x + x_row(p, n) + 8 * (lane >> 4);
+    }
+    uint8_t *ring = lds + wave * (R * STAGE);
+    auto issue = [&](int t, int slot) {
+        const int kt = kt0 + wave + 4 * t;
+        uint8_t *dst = ring + slot * STAGE;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            g2l16(wl + aoff[i] + (int64_t) kt * 512, dst + i * 1024);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            g2l16(bsrc[j] + kt * 32, dst + (TM + j) * 1024);
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    if constexpr (DIRECT) {
+        // operands straight into registers, R stages in flight. The stage
+        // count of every wave is a multiple of R (checked by the launcher), so
+        // every refill below is a real stage and the loads are unconditional:
+        // the compiler's load counter then waits for exactly one stage.
+        u32x4 ra[R][TM], rb[R][TN];
+        auto dload = [&](int t, int set) {
+            const int kt = kt0 + wave + 4 * t;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) ra[set][i] = *(const u32x4 *) (wl + aoff[i] + (int64_t) kt * 512);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) rb[set][j] = *(const u32x4 *) (bsrc[j] + kt * 32);
+        };
+        auto consume = [&](int set) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, ra[set][i]), __builtin_bit_cast(bf16x8, rb[set][j]), acc[i][j], 0, 0, 0);
+        };
+        if (my_n > 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) dload(r, r);
+            for (int t0 = 0; t0 < my_n - R; t0 += R) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    consume(r);
+                    dload(t0 + r + R, r);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) consume(r);
+        }
+    } else {
+#pragma unroll
+    for (int s = 0; s < R; ++s)
+        if (s < my_n) issue(s, s);
+    int slot = 0;
+    for (int t = 0; t < my_n; ++t) {
+        wait_stages<L, R>(min(my_n - 1 - t, R - 1));
+        const uint8_t *src = ring + slot * STAGE + lane * 16;
+        bf16x8 a[TM], b[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = *(const bf16x8 *) (src + i * 1024);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[j] = *(const bf16x8 *) (src + (TM + j) * 1024);
+        // the slot is refilled next: its reads must have returned
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (t + R < my_n) issue(t + R, slot);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        slot = slot + 1 == R ? 0 : slot + 1;
+    }
+    }
+
+    // ---- sum the four waves' partial tiles, 64 tokens at a time: red[w][token][feature]
+    constexpr int LDY = BM + 4;
+    constexpr int TNC = TN < 4 ? TN : 4, BNC = 16 * TNC;
+    float *red = (float *) lds;
+#pragma unroll
+    for (int c = 0; c < TN / TNC; ++c) {
+    const int bn0c = bn0 + c * BNC;
+    __syncthreads();                                          // rings drained / previous chunk consumed
+    {
+        float *mine = red + wave * (BNC * LDY);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TNC; ++j)
+                *(f32x4 *) &mine[(16 * j + (lane & 15)) * LDY + 16 * i + 4 * (lane >> 4)] = acc[i][c * TNC + j];
+    }
+    __syncthreads();
+    auto sum4 = [&](int nl, int ml) -> f32x4 {
+        const float *r0 = red + nl * LDY + ml;
+        f32x4 v = *(const f32x4 *) r0;
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const f32x4 u = *(const f32x4 *) (r0 + w * (BNC * LDY));
+            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+        }
+        return v;
+    };
+
+    if constexpr (EPI == EPI_QKV) {
+        // one 16-lane group per (token, head): lane sl holds dims 4 sl .. 4 sl + 3
+        const int H = p.M / 3, nh = H / 64;
+        const int grp = tid >> 4, sl = tid & 15;
+        constexpr int HPT = BM / 64;                 // heads per tile
+        for (int pp = grp; pp < BNC * HPT; pp += NT / 16) {
+            const int nl = pp / HPT, hl = pp % HPT;
+            const int n = bn0c + nl, f0 = bm0 + hl * 64;
+            const bool live = n < p.N;
+            f32x4 x = sum4(nl, hl * 64 + 4 * sl);
+            if (p.bias) {
+                const f32x4 bv = *(const f32x4 *) (p.bias + f0 + 4 * sl);
+                x = f32x4{x[0] + bv[0], x[1] + bv[1], x[2] + bv[2], x[3] + bv[3]};
+            }
+            const int sec = f0 / H, head = (f0 % H) / 64;
+            const int nn = live ? n : 0;
+            const int b = nn / p.seq, spos = nn % p.seq;
+            if (sec < 2) {
+                float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+                for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+                const float sc = 1.0f / sqrtf(ss / 64.0f + p.eps);
+                const float *w = sec ? p.kn_w : p.qn_w;
+                const f32x4 wv = *(const f32x4 *) (w + 4 * sl);
+                for (int e = 0; e < 4; ++e) x[e] = x[e] * sc * wv[e];
+                if (p.rope) {
+                    // (cos, sin) of pairs 2 sl, 2 sl + 1 at position spos
+                    const f32x4 cs = *(const f32x4 *) (p.rope_cs + (int64_t) spos * 64 + 4 * sl);
+                    for (int q2 = 0; q2 < 2; ++q2) {
+                        const float c = cs[2 * q2], sn = cs[2 * q2 + 1];
+                        const float x0 = x[2 * q2], x1 = x[2 * q2 + 1];
+                        x[2 * q2] = x0 * c - x1 * sn;
+                        x[2 * q2 + 1] = x0 * sn + x1 * c;
+                    }
+                }
+            }
+            if (live) {
+                if (sec == 0)
+                    for (int e = 0; e < 4; ++e) x[e] *= p.q_scale;     // the attention's softmax scale
+                uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]),
+                                  f32_to_f16_bits(x[3])};
+                if (sec < 2) {
+                    u32x2 w2;
+                    __builtin_memcpy(&w2, o4, 8);
+                    *(u32x2 *) ((sec ? p.k : p.q) + (((int64_t) b * nh + head) * p.Ntot + p.tok_off + spos) * 64 +
+                                4 * sl) = w2;
+                } else {
+                    uint16_t *vcol = p.vt + (((int64_t) b * nh + head) * 64 + 4 * sl) * p.ldv + vt_pos(p.tok_off + spos);
+                    for (int e = 0; e < 4; ++e) vcol[(int64_t) e * p.ldv] = o4[e];
+                }
+            }
+        }
+    } else {
+        // 8 consecutive features of one token per thread
+        constexpr int G = BM / 8;
+        for (int it = tid; it < BNC * G; it += NT) {
+            const int nl = it / G, ml = (it % G) * 8;
+            const int n = bn0c + nl, m = bm0 + ml;
+            if (n >= p.N || m >= p.M) continue;
+            const f32x4 v0 = sum4(nl, ml), v1 = sum4(nl, ml + 4);
+            float o[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            if (EPI != EPI_PARTIAL && p.bias) {
+                const f32x4 b0 = *(const f32x4 *) (p.bias + m), b1 = *(const f32x4 *) (p.bias + m + 4);
+                for (int e = 0; e < 4; ++e) { o[e] += b0[e]; o[4 + e] += b1[e]; }
+            }
+            if constexpr (EPI == EPI_GELU_BF16)
+                for (int e = 0; e < 8; ++e) o[e] = gelu_tanh_f(o[e]);
+            if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_GELU_BF16) {
+                uint16_t t8[8];
+                for (int e = 0; e < 8; ++e) t8[e] = f32_to_bf16_bits(o[e]);
+                u32x4 w;
+                __builtin_memcpy(&w, t8, 16);
+                *(u32x4 *) ((uint16_t *) p.y + (int64_t) n * p.ld_y + m) = w;
+            } else {
+                float *yr = (float *) p.y + (EPI == EPI_PARTIAL ? (int64_t) tc.split * p.N * p.ld_y : 0) +
+                            (int64_t) n * p.ld_y + m;
+                *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                *(f32x4 *) (yr + 4) = f32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+    }   // token chunk
+}
+
+template <int TM, int TN, int R, bool DIRECT, int EPI>
+hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
+    constexpr int BM = 16 * TM, BN = 16 * TN;
+    int nblocks = 0;
+    for (int i = 0; i < g.nprob; ++i) {
+        GemmProblem &p = g.p[i];
+        p.tiles_m = (p.M + BM - 1) / BM;
+        p.tiles_n = (p.N + BN - 1) / BN;
+        p.kt_split = (p.K / 32 + p.splits - 1) / p.splits;
+        p.block_begin = (nblocks + 7) & ~7;
+        nblocks = p.block_begin + p.tiles_m * p.tiles_n * p.splits;
+    }
+    constexpr size_t lds = lds_bytes<TM, TN, R, DIRECT>();
+    static_assert(lds <= 160 * 1024, "LDS");
+    auto kern = gemm_ks_kernel<TM, TN, R, DIRECT, EPI>;
+    static bool attr = false;   // dynamic LDS above 64 KiB is opted in once per kernel
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
+            hipSuccess)
+            (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
+        attr = true;
+    }
+    launch_kernel(kern, dim3(nblocks), dim3(NT), lds, s, g);
+    return hipGetLastError();
+}
+
+template <int TM, int TN, int R, bool DIRECT = false>
+hipError_t ks_epi(GemmGroup &g, int epi, hipStream_t s) {
+    switch (epi) {
+        case EPI_STORE_F32: return ks_launch<TM, TN, R, DIRECT, EPI_STORE_F32>(g, s);
+        case EPI_STORE_BF16: return ks_launch<TM, TN, R, DIRECT, EPI_STORE_BF16>(g, s);
+        case EPI_GELU_BF16: return ks_launch<TM, TN, R, DIRECT, EPI_GELU_BF16>(g, s);
+        case EPI_QKV: return ks_launch<TM, TN, R, DIRECT, EPI_QKV>(g, s);
+        case EPI_PARTIAL: return ks_launch<TM, TN, R, DIRECT, EPI_PARTIAL>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+int gemm_ks_tiles(const GemmGroup &g, int bm, int bn) {
+    int n = 0;
+    for (int i = 0; i < g.nprob; ++i) {
+        const GemmProblem &p = g.p[i];
+        n = ((n + 7) & ~7) + ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * max(p.splits, 1);
+    }
+    return n;
+}
+
+hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
+    if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
+    for (int i = 0; i < g.nprob; ++i) {
+        const GemmProblem &p = g.p[i];
+        if (!p.w_tiled || p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits < 1 ||
+            p.splits > p.K / 32)
+            return hipErrorInvalidValue;
+        if (epi != EPI_PARTIAL && p.splits != 1) return hipErrorInvalidValue;
+        if (epi == EPI_QKV && (p.M % 192 || p.seq < 1 || (p.rope && !p.rope_cs))) return hipErrorInvalidValue;
+    }
+    // 128 x 64 tiles by default; 64 x 64 when that leaves most CUs idle
+    if (!cfg) cfg = gemm_ks_tiles(g, 128, 64) >= 160 ? 1 : 2;
+    if (cfg >= 6) {
+        // register prefetch: every wave's stage count a multiple of the depth
+        const int depth = cfg == 7 || cfg == 8 || cfg == 10 ? 2 : 4;
+        for (int i = 0; i < g.nprob; ++i) {
+            const GemmProblem &p = g.p[i];
+            const int kts = (p.K / 32 + p.splits - 1) / p.splits;
+            if (kts % (4 * depth) || (p.K / 32) % p.splits) return hipErrorInvalidValue;
+        }
+    }
+    for (int i = 0; i < g.nprob; ++i)
+        if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 ? 64 : 128) && epi == EPI_QKV)
+            return hipErrorInvalidValue;
+    switch (cfg) {
+        case 1: return ks_epi<8, 4, 3>(g, epi, s);   // 128 x 64, 3 stages
+        case 2: return ks_epi<4, 4, 3>(g, epi, s);   // 64 x 64, 3 stages
+        case 3: return ks_epi<4, 8, 2>(g, epi, s);   // 64 x 128, 2 stages
+        case 4: return ks_epi<8, 4, 2>(g, epi, s);   // 128 x 64, 2 stages
+        case 5: return ks_epi<4, 4, 4>(g, epi, s);   // 64 x 64, 4 stages
+        case 6: return ks_epi<4, 4, 4, true>(g, epi, s);   // 64 x 64, register prefetch 4 stages
+        case 7: return ks_epi<8, 4, 2, true>(g, epi, s);   // 128 x 64, register prefetch 2 stages
+        case 8: return ks_epi<4, 4, 2, true>(g, epi, s);   // 64 x 64, register prefetch 2 stages
+        case 9: return ks_epi<8, 4, 4, true>(g, epi, s);   // 128 x 64, register prefetch 4 stages
+        case 10: return ks_epi<8, 8, 2, true>(g, epi, s);  // 128 x 128, register prefetch 2 stages
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace tsk

@@ -82,6 +82,16 @@ __global__ void rope_kernel(const View4 x, const int32_t *pos, int n_dims, float
     for (int64_t i = n_dims + lane; i < x.ne[0]; i += 64) vstore(y, yr, i, vload(x, xr, i));
 }
 
+__global__ void rope_table_kernel(float *cs, int npos, int n_dims, float theta_scale, float freq_scale) {
+    const int half = n_dims / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npos * half) return;
+    const int p = i / half, pr = i % half;
+    const float th = freq_scale * rope_theta((float) p, theta_scale, pr);
+    cs[(int64_t) p * n_dims + 2 * pr] = cosf(th);
+    cs[(int64_t) p * n_dims + 2 * pr + 1] = sinf(th);
+}
+
 // ---------------------------------------------------------------- fused qk norm + rope
 // x ne = [64, n_head, S, B]; 32 lanes per head vector (one pair each).
 __global__ void qk_norm_rope_kernel(const View4 x, const float *w, const int32_t *pos, float eps,
@@ -325,6 +335,13 @@ hipError_t launch_rope(const View4 &x, const int32_t *pos, int n_dims, float the
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
     launch_kernel(rope_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, pos, n_dims, theta_scale,
                        freq_scale, y, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_table(float *cs, int npos, int n_dims, float theta_scale, float freq_scale, hipStream_t s) {
+    if (npos < 1 || n_dims < 2 || n_dims % 2) return hipErrorInvalidValue;
+    launch_kernel(rope_table_kernel, dim3(blocks_for((int64_t) npos * (n_dims / 2), 256)), dim3(256), 0, s, cs, npos,
+                  n_dims, theta_scale, freq_scale);
     return hipGetLastError();
 }
 

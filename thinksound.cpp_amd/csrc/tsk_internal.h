@@ -152,14 +152,25 @@ struct GemmProblem {
     int Ntot, tok_off, rope;
     float theta_scale, freq_scale, eps;
     float q_scale;                 // q is multiplied by this before its fp16 cast
-    // filled by launch_gemm_group
+    const float *rope_cs;          // launch_gemm_ks: (cos, sin) of pair i at position s: [s * 64 + 2 i]
+    // filled by the launchers
     int tiles_m, tiles_n, block_begin;
+    int kt_split;                  // 32-wide k tiles per split (launch_gemm_ks)
 };
 struct GemmGroup {
     GemmProblem p[2];
     int nprob;
 };
 hipError_t launch_gemm_group(GemmGroup &g, int flags, int epi, hipStream_t s);
+// The DiT block projections (gemm_ks.hip): bf16 activations, MFMA-tiled
+// weights (w_tiled, M % 16 == 0, K % 32 == 0). cfg 0 picks the tile shape;
+// 1..5 force one (128x64 / 64x64 / 64x128 / 128x64 2-stage / 64x64 4-stage).
+hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s);
+int gemm_ks_tiles(const GemmGroup &g, int bm, int bn);
+// RoPE (cos, sin) table for positions 0 .. npos-1 and n_dims / 2 pairs, the
+// angle freq_scale * p * theta_scale^i evaluated as rope_theta() does:
+// cs[p * n_dims + 2 i] = cos, [.. + 1] = sin
+hipError_t launch_rope_table(float *cs, int npos, int n_dims, float theta_scale, float freq_scale, hipStream_t s);
 
 // MFMA-tiled weight layout: W[m][k] (M % 16 == 0, K % 32 == 0) is stored as
 // 16 x 32 tiles, tile (m / 16, k / 32) at element (m / 16 * (K / 32) + k / 32) * 512,
