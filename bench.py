@@ -138,6 +138,25 @@ def main():
     ms30, _, _ = run(646, max(5, args.steps // 2), 2, False)
     _, roles30, _ = run(646, max(5, args.steps // 2), 1, True)
 
+    # config 5: the full 24-step rectified-flow Euler sampler with CFG 5 at 30 s
+    # (646 latent + 77 text tokens, cond/uncond batched as B = 2 per step),
+    # noise N(0, 1) from seed 4242; wall clock around tsk_dit_sample (one
+    # warm-up sample, median of 3)
+    import numpy as np
+    rng = np.random.default_rng(4242)
+    noise = rng.standard_normal((646, 64), dtype=np.float32)
+    tc = rng.standard_normal((77, 1024), dtype=np.float32)
+    tu = rng.standard_normal((77, 1024), dtype=np.float32)
+    dit.sample(noise, tc, tu, steps=24, cfg_scale=5.0)
+    walls = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        dit.sample(noise, tc, tu, steps=24, cfg_scale=5.0)
+        walls.append(time.perf_counter() - t0)
+    wall = sorted(walls)[1]
+    sample30 = {"steps": 24, "cfg_scale": 5.0, "latent_tokens": 646, "seconds": round(wall, 5),
+                "sampler_steps_per_s": round(24 / wall, 2), "ms_per_step": round(wall / 24 * 1e3, 4)}
+
     dom = max(roles9, key=lambda r: roles9[r][0])
     rf = roofline(dom, *roles9[dom])
     rf["launches_per_step"] = roles9[dom][1] // args.steps
@@ -170,6 +189,7 @@ def main():
         "roofline": rf,
         "attention": {"9s": attn(roles9, args.steps), "30s": attn(roles30, max(5, args.steps // 2))},
         "steps_per_s_30s": round(1000.0 / ms30, 2),
+        "sample_24_steps_30s": sample30,
         "ms_per_step_with_kernel_events": round(ms_timed, 4),
         "breakdown_9s": breakdown,
     }

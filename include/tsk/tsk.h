@@ -186,6 +186,59 @@ enum tsk_op {
 int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs,
                     const tsk_tensor *dst);
 
+/* ---- T5 encoder stack (counterpart of ts_t5, src/t5_encoder.cpp:28-104) -- */
+
+typedef struct tsk_t5 tsk_t5;
+
+typedef struct tsk_t5_config {
+    int   d_model;       /* 2048 (GGUF t5.d_model, t5_encoder.cpp:32)      */
+    int   d_ff;          /* 5120 (t5.d_ff)                                 */
+    int   n_layers;      /* 24   (t5.n_layers, :33)                        */
+    int   n_heads;       /* 32   (t5.n_heads)                              */
+    int   d_kv;          /* 64   (t5.d_kv, :34; must be 64)                */
+    int   rel_buckets;   /* 32   (t5.rel_buckets, :35)                     */
+    int   rel_max_dist;  /* 128  (t5.rel_max_dist)                         */
+    int   weight_type;   /* TSK_TYPE_Q8_0: every matrix a ggml Q8_0 tensor */
+    int   max_tokens;    /* capacity: tokens per encode                    */
+    float eps;           /* 1e-6 (t5.eps, :36)                             */
+} tsk_t5_config;
+
+/* Fill the T5-v1.1-xl defaults above (max_tokens 512). */
+void tsk_t5_default_config(tsk_t5_config *cfg);
+int  tsk_t5_create(const tsk_t5_config *cfg, tsk_t5 **out);
+void tsk_t5_destroy(tsk_t5 *t5);
+/* Named weights (the converter's names: rel_bias, blk.<i>.attn_norm, .q, .k,
+ * .v, .o, .ffn_norm, .wi_0, .wi_1, .wo, out_norm) with their ggml shape and
+ * type (TSK_TYPE_Q8_0 matrices, TSK_TYPE_F32 vectors and rel_bias). */
+int  tsk_t5_n_tensors(const tsk_t5 *t5);
+int  tsk_t5_tensor_info(const tsk_t5 *t5, int i, const char **name, int64_t ne[4], int *type);
+/* Upload one weight from HOST memory in its stored form: ggml Q8_0 blocks
+ * (34 bytes per 32 values along ne[0]) or F32; nbytes must match exactly. */
+int  tsk_t5_set_tensor(tsk_t5 *t5, const char *name, const void *host_data, size_t nbytes);
+/*
+ * The encoder layers of ts_t5::encode (t5_encoder.cpp:56-88) on n <= max_tokens
+ * embedded tokens (the tok_emb row gather, :46, stays with the caller), all
+ * pointers HOST: x [n, d_model] f32, ids [n] (id 0 marks a padded key, :97)
+ * -> out [n, d_model] f32 (after out_norm). Attention runs as
+ * flash_attn_ext with the per-head relative-position bias + padding as its
+ * additive F32 mask, scale 1 (the reference's mul_mat/add/soft_max/mul_mat
+ * chain, :68-73).
+ */
+int  tsk_t5_encode(tsk_t5 *t5, int n, const float *x, const int32_t *ids, float *out,
+                   tsk_stream stream);
+/* Same with DEVICE x / out (f32) and HOST ids; no host synchronisation. */
+int  tsk_t5_encode_device(tsk_t5 *t5, int n, const float *x_d, const int32_t *ids_host,
+                          float *out_d, tsk_stream stream);
+/* Layers [layer_begin, layer_end) only, then out_norm if final_norm (else the
+ * residual stream itself): a stack split into stages, e.g. to check or
+ * pipeline it layer by layer. HOST (encode_range) or DEVICE (encode_layers)
+ * x / out; ids always HOST. */
+int  tsk_t5_encode_range(tsk_t5 *t5, int n, const float *x, const int32_t *ids, int layer_begin,
+                         int layer_end, int final_norm, float *out, tsk_stream stream);
+int  tsk_t5_encode_layers(tsk_t5 *t5, int n, const float *x_d, const int32_t *ids_host,
+                          int layer_begin, int layer_end, int final_norm, float *out_d,
+                          tsk_stream stream);
+
 /* ---- MM-DiT step driver (counterpart of ts_dit, src/mmdit.h:9-42) ------ */
 
 typedef struct tsk_dit tsk_dit;

@@ -25,6 +25,12 @@ class TskTensor(ctypes.Structure):
                 ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
 
 
+class T5Config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "d_model", "d_ff", "n_layers", "n_heads", "d_kv", "rel_buckets", "rel_max_dist",
+        "weight_type", "max_tokens")] + [("eps", ctypes.c_float)]
+
+
 class DitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq",
@@ -81,6 +87,20 @@ def lib():
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                      ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_int, ctypes.c_int]
+        vp = ctypes.c_void_p
+        L.orc_t5_bucket.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_t5_attention.argtypes = [vp, vp, vp, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, vp]
+        L.orc_t5_create.argtypes = [ctypes.POINTER(T5Config)]
+        L.orc_t5_create.restype = vp
+        L.orc_t5_destroy.argtypes = [vp]
+        L.orc_t5_n_tensors.argtypes = [vp]
+        L.orc_t5_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+                                         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.POINTER(ctypes.c_int)]
+        L.orc_t5_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
+        L.orc_t5_encode.argtypes = [vp, ctypes.c_int, vp, vp, vp]
+        L.orc_t5_encode_range.argtypes = [vp, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
         _lib = L
     return _lib
 
@@ -299,3 +319,77 @@ class OracleDiT:
                                   flow0.ctypes.data, int(act_bf16), int(kv_f16))
         assert rc == 0
         return out, flow0
+
+
+# ---------------------------------------------------------------- T5 encoder (config 4)
+def t5_config(**kw):
+    c = T5Config(d_model=2048, d_ff=5120, n_layers=24, n_heads=32, d_kv=64, rel_buckets=32,
+                 rel_max_dist=128, weight_type=Q8_0, max_tokens=512, eps=1e-6)
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+def t5_bucket(rel, num_buckets=32, max_dist=128):
+    """relative-position bucket of src/t5_encoder.cpp:14-26"""
+    return lib().orc_t5_bucket(int(rel), int(num_buckets), int(max_dist))
+
+
+def t5_attention_mask(rel_bias, ids, num_buckets=32, max_dist=128):
+    """[H][n][n] f32 additive mask: rel_bias[bucket(k - q)][h] + (-inf where ids[k] == 0)."""
+    rel_bias = np.asarray(rel_bias, dtype=np.float32)       # (buckets, H)
+    n = len(ids)
+    table = np.array([t5_bucket(r, num_buckets, max_dist) for r in range(-(n - 1), n)], dtype=np.int64)
+    rel = np.arange(n)[None, :] - np.arange(n)[:, None]    # k - q
+    bk = table[rel + (n - 1)]                               # (q, k)
+    m = rel_bias[bk].transpose(2, 0, 1).astype(np.float32)  # (H, q, k)
+    pad = np.where(np.asarray(ids) != 0, 0.0, -np.inf).astype(np.float32)
+    return np.ascontiguousarray(m + pad[None, None, :])
+
+
+def t5_attention(q, k, v, mask):
+    """q/k/v (n, H, D) f32 rows, mask (H, n, n) -> (n, H, D): the reference's
+    mul_mat / add / soft_max / mul_mat chain (src/t5_encoder.cpp:68-75)."""
+    q, k, v, mask = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, mask))
+    n, H, D = q.shape
+    out = np.empty((n, H, D), np.float32)
+    rc = lib().orc_t5_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, H * D, mask.ctypes.data,
+                                n, H, D, out.ctypes.data)
+    assert rc == 0
+    return out
+
+
+class OracleT5:
+    def __init__(self, cfg):
+        self.cfg = cfg
+        self.h = lib().orc_t5_create(ctypes.byref(cfg))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_t5_destroy(self.h)
+            self.h = None
+
+    def tensors(self):
+        out = []
+        for i in range(lib().orc_t5_n_tensors(self.h)):
+            nm, a, b, t = ctypes.c_char_p(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+            lib().orc_t5_tensor_info(self.h, i, ctypes.byref(nm), ctypes.byref(a), ctypes.byref(b),
+                                     ctypes.byref(t))
+            out.append((nm.value.decode(), (a.value, b.value, 1, 1), t.value))
+        return out
+
+    def set_tensor(self, name, data):
+        data = np.ascontiguousarray(data)
+        rc = lib().orc_t5_set_tensor(self.h, name.encode(), data.ctypes.data, data.nbytes)
+        assert rc == 0, (name, rc)
+
+    def encode(self, x, ids, layers=None, final_norm=True):
+        """layers = (begin, end) runs only those layers (default: all)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty_like(x)
+        b, e = layers if layers is not None else (0, self.cfg.n_layers)
+        rc = lib().orc_t5_encode_range(self.h, x.shape[0], x.ctypes.data, ids.ctypes.data, b, e,
+                                       int(final_norm), out.ctypes.data)
+        assert rc == 0
+        return out

@@ -25,7 +25,6 @@ static int g_threads = 1;
 void orc_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 256 ? 256 : n); }
 int  orc_get_threads(void) { return g_threads; }
 
-typedef void (*orc_range_fn)(void *ctx, int64_t lo, int64_t hi);
 typedef struct { orc_range_fn fn; void *ctx; int64_t lo, hi; } orc_job;
 
 static void *orc_job_run(void *p) {
@@ -35,7 +34,7 @@ static void *orc_job_run(void *p) {
 }
 
 /* Run fn over [0, n) split in contiguous chunks over g_threads threads. */
-static void orc_parallel(int64_t n, orc_range_fn fn, void *ctx) {
+void orc_parallel(int64_t n, orc_range_fn fn, void *ctx) {
     int nt = g_threads;
     if (nt > n) nt = (int) (n > 0 ? n : 1);
     if (nt <= 1) { if (n > 0) fn(ctx, 0, n); return; }

@@ -26,6 +26,9 @@ extern "C" {
 /* threads used by the parallel loops below (default 1) */
 void     orc_set_threads(int n);
 int      orc_get_threads(void);
+/* run fn over [0, n) in contiguous chunks on those threads */
+typedef void (*orc_range_fn)(void *ctx, int64_t lo, int64_t hi);
+void     orc_parallel(int64_t n, orc_range_fn fn, void *ctx);
 
 /* scalar conversions, round-to-nearest-even (ggml GGML_FP32_TO_FP16 / _BF16) */
 uint16_t orc_fp32_to_fp16(float f);
@@ -91,6 +94,32 @@ int      orc_dit_forward(orc_dit *d, int B, int T, const float *latent, const fl
 int      orc_dit_sample(orc_dit *d, int T, const float *noise, const float *text_cond,
                         const float *text_uncond, int steps, float cfg_scale, float *out,
                         float *flow0, int act_bf16, int kv_f16);
+
+/* ---- T5 encoder stack (ts_t5::encode, src/t5_encoder.cpp:40-104) ---------
+ * Relative-position bucket of t5_encoder.cpp:14-26 (bidirectional). */
+int      orc_t5_bucket(int rel, int num_buckets, int max_dist);
+/* The attention of one T5 layer as the reference graph computes it
+ * (t5_encoder.cpp:68-75): per head h, s[q][k] = sum_d k[k][d] q[q][d] (no
+ * scale) + mask[h][q][k]; soft_max over k (ggml-cpu: max subtracted, expf,
+ * sum in double, scaled by 1/sum); o[q][d] = sum_k v[k][d] p[q][k].
+ * q, k, v: rows of n tokens with H heads of D values at row stride ld
+ * (floats); mask [H][n][n]; out [n][H][D]. */
+int      orc_t5_attention(const float *q, const float *k, const float *v, int64_t ld, const float *mask,
+                          int n, int H, int D, float *out);
+/* Whole encoder stack on embedded tokens x [n][d_model] with key padding from
+ * ids (id 0 = padded key, t5_encoder.cpp:97): weights by the converter's
+ * names, matrices as ggml Q8_0 blocks (or F32), vectors F32. */
+typedef struct orc_t5 orc_t5;
+orc_t5  *orc_t5_create(const tsk_t5_config *cfg);
+void     orc_t5_destroy(orc_t5 *t);
+int      orc_t5_n_tensors(const orc_t5 *t);
+int      orc_t5_tensor_info(const orc_t5 *t, int i, const char **name, int64_t *ne0, int64_t *ne1, int *type);
+/* data: Q8_0 blocks (type Q8_0) or floats (type F32), nbytes checked */
+int      orc_t5_set_tensor(orc_t5 *t, const char *name, const void *data, size_t nbytes);
+int      orc_t5_encode(orc_t5 *t, int n, const float *x, const int32_t *ids, float *out);
+/* layers [layer_begin, layer_end), then out_norm if final_norm */
+int      orc_t5_encode_range(orc_t5 *t, int n, const float *x, const int32_t *ids, int layer_begin,
+                             int layer_end, int final_norm, float *out);
 
 #ifdef __cplusplus
 }

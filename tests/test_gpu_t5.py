@@ -1,0 +1,144 @@
+"""T5 encoder path on gfx950 (configuration 4) vs the oracle's restatement of
+ts_t5::encode (src/t5_encoder.cpp:40-104).
+
+Attention with the per-head relative-position bias + key padding as an F32
+additive mask, scale 1: fp32 attention, rel-L2 <= 1e-5 against the
+reference's explicit scores / soft_max / P.V chain.
+
+The encoder stack re-quantizes its activations to Q8_0 before each of the
+four GEMMs of a layer, as ggml's mul_mat does. A 1e-7 relative change of a
+layer's input (one ulp) flips the rounding of some of those values, and the
+oracle's own one-layer output then moves by ~3e-3 (measured below on every
+case). The device and the oracle differ by fp32 summation order, so each
+layer is checked from the device's own input (teacher forcing) against
+max(1e-3, 2 x that one-ulp sensitivity), and the whole stack end to end
+against 2 x the oracle's end-to-end sensitivity to a one-ulp input change."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env(orc):
+    from __graft_entry__ import ensure_built, load_tsk
+    ensure_built()
+    tsk = load_tsk()
+    tsk.init(0)
+    return tsk, orc
+
+
+def test_t5_attention_config4(env):
+    """config 4 attention: N = 512 tokens, 32 heads x 64, rel-bias table N(0, 1),
+    the last 64 keys padded; flash_attn_ext with the bias as its F32 mask."""
+    tsk, orc = env
+    rng = np.random.default_rng(4096)
+    n, H, D = 512, 32, 64
+    q, k, v = (rng.standard_normal((n, H, D)).astype(np.float32) * 0.35 for _ in range(3))
+    rel_bias = rng.standard_normal((32, H)).astype(np.float32)
+    ids = np.arange(1, n + 1, dtype=np.int32)
+    ids[-64:] = 0
+    mask = orc.t5_attention_mask(rel_bias, ids)                      # (H, n, n)
+    dev = tsk.to_device
+    qb, kb, vb = (np.ascontiguousarray(a.transpose(1, 0, 2))[None] for a in (q, k, v))   # (1, H, n, D)
+    o = tsk.flash_attn_ext(dev(qb), dev(kb), dev(vb), mask=dev(mask[None]), scale=1.0).numpy()[0]
+    ref = orc.t5_attention(q, k, v, mask)
+    e = rel_l2(o, ref)
+    print(f"T5 attention n=512 H=32: rel-L2 {e:.2e}", flush=True)
+    assert e <= 1e-5
+
+
+def q8_random(rng, K, M, scale):
+    """ggml Q8_0 blocks of a [K, M] weight: int8 U[-127, 127], fp16 d = scale"""
+    qs = rng.integers(-127, 128, size=(M, K // 32, 32), dtype=np.int8)
+    d = np.full((M, K // 32, 1), np.float16(scale)).view(np.uint8)
+    return np.ascontiguousarray(np.concatenate([d.reshape(M, K // 32, 2), qs.view(np.uint8)], axis=2))
+
+
+def t5_weights(names, rng, d):
+    """(name, data) one at a time (the 24-layer set is 1.2 GB of Q8_0 blocks).
+    Q8_0 scales keep activations at unit variance; q and k are scaled down by
+    8^(1/2) so that logits (64-term dot products, no softmax scale in T5) are
+    about N(0, 1) as in a trained T5 -- with unit-variance q and k the logits
+    are N(0, 64) and the random network is chaotic: a 1e-4 difference at one
+    layer grows to decorrelation within 24 layers."""
+    for name, ne, ty in names:
+        if ty == 8:      # Q8_0 [K, M]
+            K = ne[0]
+            s = 1.0 / np.sqrt(K * 127.0 * 127.0 / 3.0)
+            if name.endswith(".q") or name.endswith(".k"):
+                s /= np.sqrt(8.0)
+            yield name, q8_random(rng, K, ne[1], s)
+        elif name == "rel_bias":
+            yield name, rng.standard_normal((ne[1], ne[0])).astype(np.float32)
+        else:
+            yield name, (1.0 + 0.1 * rng.standard_normal(ne[0])).astype(np.float32)
+
+
+def ulp_perturbed(x, seed=1):
+    """x times (1 + 1e-7 N(0, 1)): about one ulp of float32"""
+    return (x * (1.0 + 1e-7 * np.random.default_rng(seed).standard_normal(x.shape))).astype(np.float32)
+
+
+def check_stack(t5, ot, x, ids, layers):
+    y = t5.encode(x, ids)
+    ref = ot.encode(x, ids)
+    e = rel_l2(y, ref)
+    e_floor = rel_l2(ot.encode(ulp_perturbed(x), ids), ref)
+    xg, rows = x, []
+    for L in range(layers):
+        a = t5.encode(xg, ids, layers=(L, L + 1), final_norm=False)
+        b = ot.encode(xg, ids, layers=(L, L + 1), final_norm=False)
+        floor = rel_l2(ot.encode(ulp_perturbed(xg, L + 2), ids, layers=(L, L + 1), final_norm=False), b)
+        rows.append((rel_l2(a, b), floor))
+        xg = a
+    print(f"T5 stack {layers} layers n={len(ids)}: end-to-end rel-L2 {e:.2e} (oracle one-ulp sensitivity "
+          f"{e_floor:.2e}); per layer device / one-ulp sensitivity: "
+          + " ".join(f"{a:.1e}/{f:.1e}" for a, f in rows), flush=True)
+    assert np.all(np.isfinite(y))
+    for a, f in rows:
+        assert a <= max(1e-3, 2.0 * f)
+    assert e <= max(1e-3, 2.0 * e_floor)
+    return y
+
+
+@pytest.mark.parametrize("layers,n,pad", [(2, 512, 64), (1, 77, 0), (3, 130, 13)])
+def test_t5_encoder_stack(env, layers, n, pad):
+    tsk, orc = env
+    cfg = tsk.t5_config(n_layers=layers, max_tokens=512)
+    t5 = tsk.T5(cfg)
+    ot = orc.OracleT5(orc.t5_config(n_layers=layers, max_tokens=512))
+    names = t5.tensors()
+    assert [(a, b[:2]) for a, b, _ in names] == [(a, b[:2]) for a, b, _ in ot.tensors()]
+    rng = np.random.default_rng(1234 + n)
+    for k_, v_ in t5_weights(names, rng, cfg.d_model):
+        t5.set_tensor(k_, v_)
+        ot.set_tensor(k_, v_)
+    x = rng.standard_normal((n, cfg.d_model)).astype(np.float32)
+    ids = np.arange(1, n + 1, dtype=np.int32)
+    if pad:
+        ids[-pad:] = 0
+    y = check_stack(t5, ot, x, ids, layers)
+    # deterministic, and bad arguments are errors, not faults
+    np.testing.assert_array_equal(t5.encode(x, ids), y)
+    with pytest.raises(tsk.TskError):
+        t5.encode(np.zeros((600, cfg.d_model), np.float32), np.ones(600, np.int32))
+    t5.close()
+
+
+def test_t5_config4_full_stack(env):
+    """configuration 4 as specified: 24 layers, 512 tokens, last 64 padded."""
+    tsk, orc = env
+    t5 = tsk.T5(tsk.t5_config())
+    ot = orc.OracleT5(orc.t5_config())
+    rng = np.random.default_rng(44)
+    for k_, v_ in t5_weights(t5.tensors(), rng, 2048):
+        t5.set_tensor(k_, v_)
+        ot.set_tensor(k_, v_)
+    x = rng.standard_normal((512, 2048)).astype(np.float32)
+    ids = np.arange(1, 513, dtype=np.int32)
+    ids[-64:] = 0
+    check_stack(t5, ot, x, ids, 24)
+    t5.close()

@@ -219,3 +219,56 @@ def test_gelu_closed_form():
     # fixed points of GELU(tanh): 0 -> 0; large x -> x; the value at 1 is known
     assert refmath.gelu_tanh(0.0) == 0.0
     assert abs(refmath.gelu_tanh(1.0) - 0.8411919906082768) < 1e-12
+
+
+# ---------------------------------------------------------------- T5 (config 4)
+def test_t5_bucket_closed_forms(orc):
+    """src/t5_encoder.cpp:14-26 with 32 buckets, max distance 128: exact
+    buckets below 8, one bucket per sign half, log-spaced above, clamped."""
+    assert orc.t5_bucket(0) == 0
+    for n in range(1, 8):
+        assert orc.t5_bucket(-n) == n and orc.t5_bucket(n) == 16 + n
+    # |rel| = 8 * 2^j lies exactly on bucket 8 + 2j (log(2^j) / log(16) = j / 4)
+    for j in range(4):
+        n = 8 << j
+        assert orc.t5_bucket(-n) == 8 + 2 * j and orc.t5_bucket(n) == 24 + 2 * j
+    for n in (128, 129, 1000, 10 ** 6):
+        assert orc.t5_bucket(-n) == 15 and orc.t5_bucket(n) == 31
+
+
+def test_t5_bucket_exact_integer_brute_force(orc):
+    """for 8 <= n < 128 the log bucket is 8 + max{j : 16^j <= (n / 8)^8},
+    decided here in exact integer arithmetic"""
+    for n in range(8, 400):
+        j = 0
+        while 16 ** (j + 1) * 8 ** 8 <= n ** 8:
+            j += 1
+        want = min(8 + j, 15)
+        assert orc.t5_bucket(-n) == want, n
+        assert orc.t5_bucket(n) == 16 + want, n
+
+
+def test_t5_attention_explicit_path_vs_fp64(orc):
+    """the reference's scores / add / soft_max / P.V chain (t5_encoder.cpp:68-75)
+    against an fp64 softmax with the same additive mask; padded keys get no weight"""
+    rng = np.random.default_rng(44)
+    n, H, D = 37, 3, 64
+    q, k, v = (rng.standard_normal((n, H, D)).astype(np.float32) * 0.3 for _ in range(3))
+    rel_bias = rng.standard_normal((32, H)).astype(np.float32)
+    ids = np.ones(n, np.int32)
+    ids[-5:] = 0
+    mask = orc.t5_attention_mask(rel_bias, ids)
+    # mask structure: bias depends only on k - q, padded keys are -inf
+    assert np.all(np.isneginf(mask[:, :, -5:]))
+    assert mask[1, 3, 7] == rel_bias[orc.t5_bucket(4), 1] and mask[2, 10, 2] == rel_bias[orc.t5_bucket(-8), 2]
+    o = orc.t5_attention(q, k, v, mask)
+    s = np.einsum("qhd,khd->hqk", q.astype(np.float64), k.astype(np.float64)) + mask.astype(np.float64)
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("hqk,khd->qhd", p, v.astype(np.float64))
+    assert rel_l2(o, ref) <= 1e-6
+    # keys past the padding never contribute: changing them changes nothing
+    v2 = v.copy()
+    v2[-5:] = 1e3
+    np.testing.assert_array_equal(orc.t5_attention(q, k, v2, mask), o)

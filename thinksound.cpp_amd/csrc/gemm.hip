@@ -36,6 +36,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams &p, int m0, int n, f3
     }
     float o[4];
     for (int r = 0; r < 4; ++r) o[r] = v[r] + bv[r];
+    if constexpr (EPI == EPI_GEGLU) {
+        // features m0 .. m0 + 3 are (a_j, b_j, a_j+1, b_j+1), j = m0 / 2 (M % 4 == 0)
+        float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0 / 2;
+        *(f32x2 *) yr = f32x2{gelu_tanh_f(o[0]) * o[1], gelu_tanh_f(o[2]) * o[3]};
+        return;
+    }
     if constexpr (EPI == EPI_GELU)
         for (int r = 0; r < 4; ++r) o[r] = gelu_tanh_f(o[r]);
     if constexpr (EPI == EPI_GATE_RES) {
@@ -384,6 +390,10 @@ hipError_t gemm_q8_epi(const GemmParams &p, hipStream_t s) {
             break;
         case EPI_GATE_RES:
             launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_GATE_RES, false>), grid, block, 0, s, p);
+            break;
+        case EPI_GEGLU:
+            if (p.M % 4 || p.y_bf16) return hipErrorInvalidValue;
+            launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_GEGLU, false>), grid, block, 0, s, p);
             break;
         default:
             launch_kernel((gemm_q8_kernel<WM, WN, TM, TN, EPI_STORE, YBF16>), grid, block, 0, s, p);

@@ -91,7 +91,8 @@ __host__ __device__ inline int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1)
 enum GemmEpi : int {
     EPI_STORE = 0,      // Y = acc (+bias)
     EPI_GELU = 1,       // Y = gelu_tanh(acc + bias)
-    EPI_GATE_RES = 2    // R[n, m] += gate[n / rows_per_gate, m] * (acc + bias); Y unused
+    EPI_GATE_RES = 2,   // R[n, m] += gate[n / rows_per_gate, m] * (acc + bias); Y unused
+    EPI_GEGLU = 3       // rows interleaved (a_j, b_j): Y[n, j] = gelu_tanh(a_j) * b_j, M even (Q8_0 only)
 };
 
 struct GemmParams {

@@ -35,6 +35,12 @@ class TskTensor(ctypes.Structure):
                 ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
 
 
+class T5Config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "d_model", "d_ff", "n_layers", "n_heads", "d_kv", "rel_buckets", "rel_max_dist",
+        "weight_type", "max_tokens")] + [("eps", ctypes.c_float)]
+
+
 class DitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq",
@@ -69,6 +75,17 @@ def load():
         "tsk_q8_0_repack": ([P, P, vp], i),
         "tsk_q8_0_split_nbytes": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
         "tsk_supports_op": ([i, ctypes.POINTER(P), i, P], i),
+        "tsk_t5_default_config": ([ctypes.POINTER(T5Config)], None),
+        "tsk_t5_create": ([ctypes.POINTER(T5Config), ctypes.POINTER(vp)], i),
+        "tsk_t5_destroy": ([vp], None),
+        "tsk_t5_n_tensors": ([vp], i),
+        "tsk_t5_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64),
+                                ctypes.POINTER(ctypes.c_int)], i),
+        "tsk_t5_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_size_t], i),
+        "tsk_t5_encode": ([vp, i, vp, vp, vp, vp], i),
+        "tsk_t5_encode_device": ([vp, i, vp, vp, vp, vp], i),
+        "tsk_t5_encode_range": ([vp, i, vp, vp, i, i, i, vp, vp], i),
+        "tsk_t5_encode_layers": ([vp, i, vp, vp, i, i, i, vp, vp], i),
         "tsk_dit_default_config": ([ctypes.POINTER(DitConfig)], None),
         "tsk_dit_create": ([ctypes.POINTER(DitConfig), ctypes.POINTER(vp)], i),
         "tsk_dit_destroy": ([vp], None),
@@ -537,3 +554,63 @@ class Dit:
                                     text_uncond.ctypes.data, steps, cfg_scale, out.ctypes.data,
                                     flow0.ctypes.data, _stream()))
         return out, flow0
+
+
+# ---------------------------------------------------------------- T5 encoder (ts_t5)
+def t5_config(**kw):
+    c = T5Config()
+    load().tsk_t5_default_config(ctypes.byref(c))
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+class T5:
+    """ts_t5 counterpart (src/t5_encoder.cpp:28-104): named Q8_0 / F32 weights on
+    the GPU and the encoder layers on embedded tokens."""
+
+    def __init__(self, cfg=None):
+        init()
+        self.cfg = cfg if cfg is not None else t5_config()
+        h = ctypes.c_void_p()
+        check(load().tsk_t5_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().tsk_t5_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """[(name, ggml ne tuple, type)]"""
+        L = load()
+        out = []
+        for k_ in range(L.tsk_t5_n_tensors(self.h)):
+            nm, ne, ty = ctypes.c_char_p(), (ctypes.c_int64 * 4)(), ctypes.c_int()
+            check(L.tsk_t5_tensor_info(self.h, k_, ctypes.byref(nm), ne, ctypes.byref(ty)))
+            out.append((nm.value.decode(), tuple(ne), ty.value))
+        return out
+
+    def set_tensor(self, name, data):
+        """data: numpy Q8_0 blocks (uint8, 34 bytes per 32 values) or float32."""
+        import numpy as np
+        data = np.ascontiguousarray(data)
+        check(load().tsk_t5_set_tensor(self.h, name.encode(), data.ctypes.data, data.nbytes))
+
+    def encode(self, x, ids, layers=None, final_norm=True):
+        """x (n, d_model) float32 embedded tokens, ids (n,) int32 (0 = padded key) -> (n, d_model);
+        layers = (begin, end) runs only those layers (default: all)."""
+        import numpy as np
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty_like(x)
+        b, e = layers if layers is not None else (0, self.cfg.n_layers)
+        check(load().tsk_t5_encode_range(self.h, x.shape[0], x.ctypes.data, ids.ctypes.data, b, e,
+                                         int(final_norm), out.ctypes.data, _stream()))
+        return out
