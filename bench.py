@@ -53,6 +53,18 @@ def roofline(role, ms, launches, flop, nbytes):
             "flop_per_launch": flop / launches, "bytes_per_launch": nbytes / launches}
 
 
+def measured_traffic(role):
+    """HBM bytes per launch of `role` at 9 s from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/hbm_traffic_flow_step_9s.md, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_flow_step_9s.md")
+    try:
+        lines = open(path).read().split("traffic_bytes_per_launch_9s", 1)[1].split("```")[0].split()
+    except (OSError, IndexError):
+        return None
+    table = dict(zip(lines[0::2], lines[1::2]))
+    return float(table[role]) if role in table else None
+
+
 def cpu_baseline(weights, lat, t, txt, threads):
     """The oracle's flow step (same weights and inputs) on this host's cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -160,6 +172,7 @@ def main():
     dom = max(roles9, key=lambda r: roles9[r][0])
     rf = roofline(dom, *roles9[dom])
     rf["launches_per_step"] = roles9[dom][1] // args.steps
+    rf["traffic"] = measured_traffic(dom)
 
     def attn(roles, ms_steps):
         ms, n, fl, by = roles["attn"]

@@ -69,8 +69,11 @@ struct Coord {
 
 // Workgroup -> (problem, m tile, n tile, split). Problems start at multiples of
 // 8 so that bid % 8 (the XCD the workgroup lands on) is the same in both
-// numberings; when the m tiles split evenly over the 8 XCDs, every workgroup
-// reading one weight tile runs on the same XCD and shares its L2.
+// numberings. When the (m tile, split) pairs divide evenly over the 8 XCDs,
+// XCD x owns the pairs c = x, x + 8, ... with c = m tile * splits + split and
+// runs every token tile of each: a weight tile is fetched into one XCD's L2
+// only, and with splits dividing 8 an XCD reads a single K slice of the
+// activations instead of all of them.
 __device__ __forceinline__ bool decode(const GemmGroup &g, Coord &c) {
     const int bid = blockIdx.x;
     c.pi = (g.nprob > 1 && bid >= g.p[1].block_begin) ? 1 : 0;
@@ -78,17 +81,18 @@ __device__ __forceinline__ bool decode(const GemmGroup &g, Coord &c) {
     const int li = bid - p.block_begin;
     const int cols = p.tiles_n * p.splits;
     if (li >= p.tiles_m * cols) return false;
-    int col;
-    if ((p.tiles_m & 7) == 0) {
+    if (((p.tiles_m * p.splits) & 7) == 0) {
         const int s = li >> 3;
-        c.tm = (li & 7) + 8 * (s / cols);
-        col = s % cols;
+        const int pair = (li & 7) + 8 * (s / p.tiles_n);
+        c.tn = s % p.tiles_n;
+        c.tm = pair / p.splits;
+        c.split = pair % p.splits;
     } else {
         c.tm = li % p.tiles_m;
-        col = li / p.tiles_m;
+        const int col = li / p.tiles_m;
+        c.tn = col % p.tiles_n;
+        c.split = col / p.tiles_n;
     }
-    c.tn = col % p.tiles_n;
-    c.split = col / p.tiles_n;
     return true;
 }
 
