@@ -98,6 +98,10 @@ struct tsk_dit {
     int gemm_cfg[4] = {8, 8, 4, 4};
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
+    // second stream for the adaLN GEMVs of the later blocks (HBM-bound) while
+    // the first blocks compute; fork / join events
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     RoleTiming rt[TSK_ROLE_COUNT];
     // sampler buffers
     float *s_x = nullptr, *s_x2 = nullptr, *s_text2 = nullptr, *s_flow2 = nullptr, *s_flow0 = nullptr;
@@ -216,21 +220,6 @@ int validate_cfg(const tsk_dit_config *c) {
     return TSK_OK;
 }
 
-// GEMM helper: Y[n, m] for n < N rows of x
-int gemm(tsk_dit *d, const uint16_t *W, const float *bias, const void *x, bool x_f32, int64_t ld_x, int N, int K, int M,
-         int epi, void *y, bool y_bf16, int64_t ld_y, float *res, const float *gate, int64_t ld_gate,
-         int rows_per_gate, hipStream_t s, int x_group_rows = 0, int64_t x_group_stride = 0, bool x_split = false) {
-    GemmParams p;
-    memset(&p, 0, sizeof(p));
-    p.x = x; p.w = W; p.bias = bias; p.y = y; p.res = res; p.gate = gate;
-    p.ld_x = ld_x; p.ld_w = K; p.ld_y = ld_y; p.ld_res = M; p.ld_gate = ld_gate;
-    p.x_group_rows = x_group_rows; p.x_group_stride = x_group_stride;
-    p.M = M; p.N = N; p.K = K;
-    p.rows_per_gate = rows_per_gate > 0 ? rows_per_gate : 1;
-    p.x_f32 = x_f32; p.y_bf16 = y_bf16; p.epi = epi; p.x_split = x_split;
-    return hipcheck(launch_gemm_bf16(p, s), "gemm");
-}
-
 }  // namespace
 
 // ------------------------------------------------------------------ config / lifecycle
@@ -247,6 +236,9 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     (void) hipDeviceSynchronize();
     for (auto &r : d->rt)
         for (hipEvent_t e : r.ev) (void) hipEventDestroy(e);
+    if (d->ev_fork) (void) hipEventDestroy(d->ev_fork);
+    if (d->ev_join) (void) hipEventDestroy(d->ev_join);
+    if (d->side) (void) hipStreamDestroy(d->side);
     void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
                     d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
@@ -327,6 +319,12 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->rope_cs, sizeof(float) * T * c.head_dim))) {
         tsk_dit_destroy(d);
         return rc;
+    }
+    {
+        hipError_t se = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
+        if (se == hipSuccess) se = hipEventCreateWithFlags(&d->ev_fork, hipEventDisableTiming);
+        if (se == hipSuccess) se = hipEventCreateWithFlags(&d->ev_join, hipEventDisableTiming);
+        if (se != hipSuccess) { tsk_dit_destroy(d); return hip_fail(se, "side stream"); }
     }
     // t-embedding frequencies exactly as the host code of mmdit.cpp:308-310
     std::vector<float> fr(H / 2);
@@ -646,20 +644,40 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         if ((e = launch_gemv_jobs(d->jobs_dev + d->njobs, 1, H, B, H, st)) != hipSuccess) return hip_fail(e, "t_embed.0");
         if ((e = launch_gemv_jobs(d->jobs_dev + d->njobs + 1, 1, H, B, H, st)) != hipSuccess) return hip_fail(e, "t_embed.2");
     }
-    // every adaLN modulation of the step in one launch
+    // every adaLN modulation of the step: the jobs of the first two joint blocks
+    // on the caller's stream, all later ones (the bulk of the 352 MB of adaLN
+    // weights at d = 1024, HBM-bound) on the side stream, where they overlap
+    // the first blocks; the caller's stream joins them before the first block
+    // that needs one
+    const int jmain = 2 * (nj < 2 ? nj : 2);
     {
-        const double mtot = (double) H * (6.0 * (2 * nj + c.fused_depth) - 4.0 + 2.0);
-        Timed tm(d, TSK_ROLE_ADALN, 2.0 * B * mtot * H, 2.0 * mtot * H, st);
-        if ((e = launch_gemv_jobs(d->jobs_dev, d->njobs, d->max_job_m, B, H, st)) != hipSuccess)
+        const double per = 6.0 * H * H;   // weight elements of one 6H-output job
+        Timed tm(d, TSK_ROLE_ADALN, 2.0 * B * per * jmain, 2.0 * per * jmain, st);
+        if ((e = launch_gemv_jobs(d->jobs_dev, jmain, d->max_job_m, B, H, st)) != hipSuccess)
             return hip_fail(e, "adaln gemv");
     }
-    // input projection (f32-accurate split activations), text stream copy
+    if ((e = hipEventRecord(d->ev_fork, st)) != hipSuccess) return hip_fail(e, "fork");
+    if ((e = hipStreamWaitEvent(d->side, d->ev_fork, 0)) != hipSuccess) return hip_fail(e, "fork");
+    {
+        const double mtot = (double) H * (6.0 * (2 * nj + c.fused_depth) - 4.0 + 2.0) - 6.0 * H * jmain;
+        Timed tm(d, TSK_ROLE_ADALN, 2.0 * B * mtot * H, 2.0 * mtot * H, d->side);
+        if ((e = launch_gemv_jobs(d->jobs_dev + jmain, d->njobs - jmain, d->max_job_m, B, H, d->side)) != hipSuccess)
+            return hip_fail(e, "adaln gemv");
+    }
+    if ((e = hipEventRecord(d->ev_join, d->side)) != hipSuccess) return hip_fail(e, "join");
+    bool joined = false;
+    auto join = [&]() -> int {
+        if (joined) return TSK_OK;
+        joined = true;
+        return hipcheck(hipStreamWaitEvent(st, d->ev_join, 0), "join");
+    };
+    // input projection (f32 activations, fp32 accumulation), text stream copy
     {
         Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
-        rc = gemm(d, wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d, true,
-                  c.latent_dim, B * T, c.latent_dim, H, EPI_STORE, d->lat, false, H, nullptr, nullptr, 0, 0, st, 0, 0, true);
+        e = launch_proj_f32(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d,
+                            c.latent_dim, B * T, c.latent_dim, H, d->lat, H, st);
+        if (e != hipSuccess) return hip_fail(e, "input projection");
     }
-    if (rc) return rc;
     if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
         return hip_fail(e, "text copy");
 
@@ -675,6 +693,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // -> fc2 (split-K, residual paid by the next LN); both streams per launch
     const int Nj = T + St;
     for (int i = 0; i < nj; ++i) {
+        if (2 * i >= jmain && (rc = join())) return rc;
         L.w = &d->joint_lat[i];
         X.w = &d->joint_txt[i];
         StreamRun r2[2] = {L, X};
@@ -689,6 +708,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         X = r2[1];
     }
     // fused blocks: the latent stream alone
+    if ((rc = join())) return rc;
     for (int i = 0; i < c.fused_depth; ++i) {
         L.w = &d->fused[i];
         if ((rc = run_ln(d, &L, 1, B, 0, st))) return rc;
@@ -699,7 +719,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         if ((rc = run_mlp(d, &L, 1, B, st))) return rc;
     }
     // final layer: last residual update + LN/modulate (f32, final adaLN shift/scale)
-    // -> linear to latent_dim with f32-accurate split activations
+    // -> linear to latent_dim (f32 activations, fp32 accumulation)
     {
         const float *fmod = d->final_mod;
         LnGroup g;
@@ -710,9 +730,9 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         if ((e = launch_ln_group(g, st)) != hipSuccess) return hip_fail(e, "final ln");
     }
     Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * H * c.latent_dim, 4.0 * B * T * H + 2.0 * H * c.latent_dim, st);
-    return gemm(d, wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf,
-                true, H, B * T, H, c.latent_dim, EPI_STORE, flow_d, false, c.latent_dim, nullptr, nullptr, 0, 0, st,
-                0, 0, true);
+    e = launch_proj_f32(wptr<uint16_t>(d, "final_layer.linear.weight"), wptr<float>(d, "final_layer.linear.bias"), d->xf, H,
+                        B * T, H, c.latent_dim, flow_d, c.latent_dim, st);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "final projection");
 }
 
 int check_forward_args(tsk_dit *d, int B, int T, const void *a, const void *t, const void *b, const void *f) {

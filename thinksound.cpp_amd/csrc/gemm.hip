@@ -79,18 +79,15 @@ __device__ __forceinline__ void epilogue4(const GemmParams &p, int m0, int n, f3
 constexpr int BK = 64;
 constexpr int LDSB = BK + 8;   // bf16 elements per LDS row (144 B)
 
-template <int WM, int WN, int TM, int TN, bool XF32, int EPI, bool YBF16, bool XSPLIT = false>
+template <int WM, int WN, int TM, int TN, bool XF32, int EPI, bool YBF16>
 __global__ __launch_bounds__(WM * WN * 64)
 void gemm_bf16_kernel(const GemmParams p) {
-    static_assert(!XSPLIT || XF32, "split activations come from f32");
     constexpr int NT = WM * WN * 64;
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     constexpr int WCH = BM * (BK / 8), XCH = BN * (BK / 8);   // 16-B chunks (8 bf16)
     constexpr int WPER = (WCH + NT - 1) / NT, XPER = (XCH + NT - 1) / NT;
     __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BM * LDSB];
     __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BN * LDSB];
-    // low halves of split activations (x - bf16(x), rounded to bf16)
-    __shared__ __attribute__((aligned(16))) uint16_t Xl[XSPLIT ? 2 : 1][XSPLIT ? BN * LDSB : 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -148,14 +145,6 @@ void gemm_bf16_kernel(const GemmParams p) {
                     uint16_t t8[8];
                     for (int j = 0; j < 4; ++j) { t8[j] = f32_to_bf16_bits(f0[j]); t8[4 + j] = f32_to_bf16_bits(f1[j]); }
                     __builtin_memcpy(&v, t8, 16);
-                    if constexpr (XSPLIT) {
-                        uint16_t l8[8];
-                        for (int j = 0; j < 4; ++j) {
-                            l8[j] = f32_to_bf16_bits(f0[j] - bf16_bits_to_f32(t8[j]));
-                            l8[4 + j] = f32_to_bf16_bits(f1[j] - bf16_bits_to_f32(t8[4 + j]));
-                        }
-                        *(u32x4 *) &Xl[buf][(c / (BK / 8)) * LDSB + (c % (BK / 8)) * 8] = *(const u32x4 *) l8;
-                    }
                 } else {
                     v = xreg[i][0];
                 }
@@ -183,13 +172,6 @@ void gemm_bf16_kernel(const GemmParams p) {
             for (int i = 0; i < TM; ++i)
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-            if constexpr (XSPLIT) {
-                for (int j = 0; j < TN; ++j)
-                    b[j] = *(const bf16x8 *) &Xl[buf][((wn * TN + j) * 16 + lr) * LDSB + 32 * kk + 8 * lg];
-                for (int i = 0; i < TM; ++i)
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-            }
         }
         if (kt + 1 < nk) lstore(buf ^ 1);
         __syncthreads();
@@ -404,13 +386,6 @@ hipError_t gemm_q8_epi(const GemmParams &p, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s) {
-    if (p.x_split) {
-        // thin f32-accurate projections (input / output of the DiT): 32 x 64 tiles, plain store
-        if (!p.x_f32 || p.epi != EPI_STORE || p.y_bf16) return hipErrorInvalidValue;
-        dim3 grid((p.M + 31) / 32, (p.N + 63) / 64);
-        launch_kernel((gemm_bf16_kernel<2, 2, 1, 2, true, EPI_STORE, false, true>), grid, dim3(256), 0, s, p);
-        return hipGetLastError();
-    }
     if (p.epi != EPI_STORE) return hipErrorInvalidValue;
     GemmGroup g;
     memset(&g, 0, sizeof(g));

@@ -287,6 +287,73 @@ __global__ __launch_bounds__(256) void gemv_jobs_kernel(const GemvJob *jobs, int
     }
 }
 
+// Thin f32-accurate projection y[n, m] = sum_k W[m, k] x[n, k] + b[m] with bf16
+// W (row-major) and f32 x: one wave per (token, 64 outputs), lane = output.
+// Four fp32 accumulators over k mod 4 (fixed order, fma per element: the
+// bf16 x f32 products are exact inside the fma), summed in order at the end.
+__global__ __launch_bounds__(256) void proj_f32_kernel(const uint16_t *w, const float *bias, const float *x,
+                                                       int64_t ld_x, int N, int K, int M, float *y, int64_t ld_y) {
+    const int lane = threadIdx.x & 63;
+    const int chunks = (M + 63) / 64;
+    const int64_t wv = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wv >= (int64_t) N * chunks) return;
+    const int n = (int) (wv / chunks), m = (int) (wv % chunks) * 64 + lane;
+    const float *xr = x + (int64_t) n * ld_x;
+    const uint16_t *wr = w + (int64_t) (m < M ? m : M - 1) * K;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < K; k += 8) {
+        const u32x4 w8 = *(const u32x4 *) (wr + k);
+        const f32x4 x0 = *(const f32x4 *) (xr + k), x1 = *(const f32x4 *) (xr + k + 4);
+        const uint16_t *h = (const uint16_t *) &w8;
+        for (int j = 0; j < 4; ++j) a[j] = fmaf(bf16_bits_to_f32(h[j]), x0[j], a[j]);
+        for (int j = 0; j < 4; ++j) a[j] = fmaf(bf16_bits_to_f32(h[4 + j]), x1[j], a[j]);
+    }
+    if (m < M) y[(int64_t) n * ld_y + m] = ((a[0] + a[1]) + (a[2] + a[3])) + (bias ? bias[m] : 0.0f);
+}
+
+// Same projection for long K and few outputs (the DiT's final layer, K = 1024,
+// M = 64): one 256-thread workgroup per (token, 64 outputs), the token's row
+// staged in LDS; wave w owns outputs 16 w .. 16 w + 15 and its lanes split K
+// (lane l: k = (K / 64) l .. +K / 64), so all 16 weight-row slices of a lane
+// are in flight at once; each output is one fixed-order wave sum.
+template <int KPL>
+__global__ __launch_bounds__(256) void proj_f32_kt_kernel(const uint16_t *w, const float *bias, const float *x,
+                                                          int64_t ld_x, int N, int M, float *y, int64_t ld_y) {
+    constexpr int K = KPL * 8 * 64;
+    __shared__ __attribute__((aligned(16))) float xs[K];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunks = (M + 63) / 64;
+    const int n = blockIdx.x / chunks, m0 = (blockIdx.x % chunks) * 64 + wave * 16;
+    const float *xr = x + (int64_t) n * ld_x;
+    for (int i = threadIdx.x * 4; i < K; i += 256 * 4) *(f32x4 *) &xs[i] = *(const f32x4 *) (xr + i);
+    u32x4 wv[16][KPL];
+#pragma unroll
+    for (int o = 0; o < 16; ++o) {
+        const int m = m0 + o < M ? m0 + o : M - 1;
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) wv[o][j] = *(const u32x4 *) (w + (int64_t) m * K + lane * KPL * 8 + 8 * j);
+    }
+    __syncthreads();
+    float xv[KPL * 8];
+#pragma unroll
+    for (int j = 0; j < KPL * 8; j += 4) {
+        const f32x4 t = *(const f32x4 *) &xs[lane * KPL * 8 + j];
+        xv[j] = t[0]; xv[j + 1] = t[1]; xv[j + 2] = t[2]; xv[j + 3] = t[3];
+    }
+#pragma unroll
+    for (int o = 0; o < 16; ++o) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) {
+            const uint16_t *h = (const uint16_t *) &wv[o][j];
+            for (int e = 0; e < 8; ++e) a = fmaf(bf16_bits_to_f32(h[e]), xv[8 * j + e], a);
+        }
+        a = wave_sum(a);
+        const int m = m0 + o;
+        if (lane == 0 && m < M) y[(int64_t) n * ld_y + m] = a + (bias ? bias[m] : 0.0f);
+    }
+}
+
 __global__ void silu_kernel(float *x, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
@@ -391,6 +458,19 @@ hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B
     if (B <= 2) launch_kernel(gemv_jobs_kernel<2>, grid, dim3(256), 0, s, jobs_dev, B, K);
     else if (B <= 8) launch_kernel(gemv_jobs_kernel<8>, grid, dim3(256), 0, s, jobs_dev, B, K);
     else launch_kernel(gemv_jobs_kernel<32>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,
+                           float *y, int64_t ld_y, hipStream_t s) {
+    if (N < 1 || M < 1 || K < 8 || K % 8 || ld_x % 4) return hipErrorInvalidValue;
+    if (K == 1024) {   // long rows: lanes split K (final layer)
+        launch_kernel(proj_f32_kt_kernel<2>, dim3((unsigned) ((int64_t) N * ((M + 63) / 64))), dim3(256), 0, s, w,
+                      bias, x, ld_x, N, M, y, ld_y);
+        return hipGetLastError();
+    }
+    const int64_t waves = (int64_t) N * ((M + 63) / 64);
+    launch_kernel(proj_f32_kernel, dim3(blocks_for(waves, 4)), dim3(256), 0, s, w, bias, x, ld_x, N, K, M, y, ld_y);
     return hipGetLastError();
 }
 

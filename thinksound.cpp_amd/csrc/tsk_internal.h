@@ -111,7 +111,6 @@ struct GemmParams {
     int M, N, K;
     int rows_per_gate;
     int x_f32, y_bf16, epi;
-    int x_split;             // f32 activations as bf16 hi + lo (two MFMAs): f32-grade products
     // Q8_0: activations pre-quantized into planes qx [N][K] int8 and
     // dx [N][K/32] f32 (fp16-representable scales)
     const int8_t *qx;
@@ -250,6 +249,10 @@ struct GemvJob {
 hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K,
                             hipStream_t s);
 hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s);
+// y[n, m] = sum_k W[m, k] x[n, k] + bias[m]: bf16 row-major W, f32 x and y,
+// fp32 fma accumulation (the DiT's input and output projections)
+hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,
+                           float *y, int64_t ld_y, hipStream_t s);
 // t-embedding: temb[b, k] = cos(t_b * freq[k]), temb[b, H/2 + k] = sin(t_b * freq[k])
 struct TimeVals { float t[32]; };
 hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb,
