@@ -186,6 +186,28 @@ enum tsk_op {
 int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs,
                     const tsk_tensor *dst);
 
+/* ---- GGUF ingestion (ts_model::load_backend, src/common/ts_model.cpp:13-41) --
+ * A host-side reader of the GGUF v2/v3 files the converters write
+ * (convert/convert_thinksound.py, convert/convert_t5.py, convert/quantize_gguf.py)
+ * and loaders that hand their tensors to the drivers by name. Tensor types
+ * read: F32, F16, BF16, Q8_0 (others give TSK_ERR_TYPE). No GPU work except
+ * inside the *_load_gguf calls (through the drivers' set_tensor). */
+typedef struct tsk_gguf tsk_gguf;
+int  tsk_gguf_open(const char *path, tsk_gguf **out);
+void tsk_gguf_close(tsk_gguf *g);
+int  tsk_gguf_n_tensors(const tsk_gguf *g);
+int  tsk_gguf_tensor_info(const tsk_gguf *g, int i, const char **name, int64_t ne[4], int *type);
+/* index of the tensor (>= 0) and its ggml ne / type, or a negative status */
+int  tsk_gguf_find_tensor(const tsk_gguf *g, const char *name, int64_t ne[4], int *type);
+/* the tensor's bytes as stored (as_f32 = 0) or converted to f32 (as_f32 = 1:
+ * F16 / BF16 exactly, Q8_0 as fp32(d) * q); dst_bytes must match exactly */
+int  tsk_gguf_read_tensor(const tsk_gguf *g, const char *name, int as_f32, void *dst, size_t dst_bytes);
+/* metadata: integers / bools as u32, numbers as f32, strings (pointer valid
+ * until tsk_gguf_close) */
+int  tsk_gguf_get_u32(const tsk_gguf *g, const char *key, uint32_t *out);
+int  tsk_gguf_get_f32(const tsk_gguf *g, const char *key, float *out);
+int  tsk_gguf_get_str(const tsk_gguf *g, const char *key, const char **out);
+
 /* ---- T5 encoder stack (counterpart of ts_t5, src/t5_encoder.cpp:28-104) -- */
 
 typedef struct tsk_t5 tsk_t5;
@@ -238,6 +260,10 @@ int  tsk_t5_encode_range(tsk_t5 *t5, int n, const float *x, const int32_t *ids, 
 int  tsk_t5_encode_layers(tsk_t5 *t5, int n, const float *x_d, const int32_t *ids_host,
                           int layer_begin, int layer_end, int final_norm, float *out_d,
                           tsk_stream stream);
+/* t5.* metadata (t5_encoder.cpp:31-36) over the values already in cfg */
+int  tsk_t5_config_from_gguf(const tsk_gguf *g, tsk_t5_config *cfg);
+/* every weight by name from a GGUF file, in its stored type (Q8_0 / F32) */
+int  tsk_t5_load_gguf(tsk_t5 *t5, const tsk_gguf *g);
 
 /* ---- MM-DiT step driver (counterpart of ts_dit, src/mmdit.h:9-42) ------ */
 
@@ -299,6 +325,12 @@ int  tsk_dit_forward_device(tsk_dit *dit, int B, int T, const float *latent_d,
 int  tsk_dit_sample(tsk_dit *dit, int T, const float *noise, const float *text_cond,
                     const float *text_uncond, int steps, float cfg_scale,
                     float *out, float *flow0, tsk_stream stream);
+/* dit.* metadata of convert_thinksound.py:38-45 over the values already in cfg */
+int  tsk_dit_config_from_gguf(const tsk_gguf *g, tsk_dit_config *cfg);
+/* every weight by name from a GGUF file: F32 / F16 / BF16 / Q8_0 tensors,
+ * converted to f32 and set as tsk_dit_set_tensor does (matrices rounded to
+ * the driver's BF16, so a Q8_0 file loads as bf16(fp32(d) * q)) */
+int  tsk_dit_load_gguf(tsk_dit *dit, const tsk_gguf *g);
 
 /*
  * Kernel timing of the step driver (extension, no counterpart in the

@@ -86,6 +86,20 @@ def load():
         "tsk_t5_encode_device": ([vp, i, vp, vp, vp, vp], i),
         "tsk_t5_encode_range": ([vp, i, vp, vp, i, i, i, vp, vp], i),
         "tsk_t5_encode_layers": ([vp, i, vp, vp, i, i, i, vp, vp], i),
+        "tsk_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(vp)], i),
+        "tsk_gguf_close": ([vp], None),
+        "tsk_gguf_n_tensors": ([vp], i),
+        "tsk_gguf_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64),
+                                  ctypes.POINTER(ctypes.c_int)], i),
+        "tsk_gguf_find_tensor": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int)], i),
+        "tsk_gguf_read_tensor": ([vp, ctypes.c_char_p, i, vp, ctypes.c_size_t], i),
+        "tsk_gguf_get_u32": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)], i),
+        "tsk_gguf_get_f32": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)], i),
+        "tsk_gguf_get_str": ([vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)], i),
+        "tsk_dit_config_from_gguf": ([vp, ctypes.POINTER(DitConfig)], i),
+        "tsk_dit_load_gguf": ([vp, vp], i),
+        "tsk_t5_config_from_gguf": ([vp, ctypes.POINTER(T5Config)], i),
+        "tsk_t5_load_gguf": ([vp, vp], i),
         "tsk_dit_default_config": ([ctypes.POINTER(DitConfig)], None),
         "tsk_dit_create": ([ctypes.POINTER(DitConfig), ctypes.POINTER(vp)], i),
         "tsk_dit_destroy": ([vp], None),
@@ -614,3 +628,86 @@ class T5:
         check(load().tsk_t5_encode_range(self.h, x.shape[0], x.ctypes.data, ids.ctypes.data, b, e,
                                          int(final_norm), out.ctypes.data, _stream()))
         return out
+
+
+# ---------------------------------------------------------------- GGUF files
+class Gguf:
+    """A GGUF file opened by the library's reader (host only; no GPU needed)."""
+
+    TYPES = {0: "f32", 1: "f16", 8: "q8_0", 30: "bf16"}
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        check(load().tsk_gguf_open(str(path).encode(), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().tsk_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """[(name, ggml ne tuple, ggml type)]"""
+        out = []
+        for k_ in range(load().tsk_gguf_n_tensors(self.h)):
+            nm, ne, ty = ctypes.c_char_p(), (ctypes.c_int64 * 4)(), ctypes.c_int()
+            check(load().tsk_gguf_tensor_info(self.h, k_, ctypes.byref(nm), ne, ctypes.byref(ty)))
+            out.append((nm.value.decode(), tuple(ne), ty.value))
+        return out
+
+    def read(self, name, as_f32=True):
+        """the tensor as f32 (numpy, shape = reversed ggml ne) or its stored bytes (uint8)"""
+        import numpy as np
+        ne, ty = (ctypes.c_int64 * 4)(), ctypes.c_int()
+        rc = load().tsk_gguf_find_tensor(self.h, name.encode(), ne, ctypes.byref(ty))
+        if rc < 0:
+            check(rc)
+        n = ne[0] * ne[1] * ne[2] * ne[3]
+        if as_f32:
+            out = np.empty(n, np.float32)
+        else:
+            nb = {0: 4 * n, 1: 2 * n, 30: 2 * n, 8: 34 * (n // 32)}.get(ty.value, 0)
+            out = np.empty(nb, np.uint8)
+        check(load().tsk_gguf_read_tensor(self.h, name.encode(), int(as_f32), out.ctypes.data, out.nbytes))
+        if not as_f32:
+            return out
+        dims = list(ne)
+        while len(dims) > 1 and dims[-1] == 1:
+            dims.pop()
+        return out.reshape(tuple(reversed(dims)))
+
+    def u32(self, key):
+        v = ctypes.c_uint32()
+        check(load().tsk_gguf_get_u32(self.h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def f32(self, key):
+        v = ctypes.c_float()
+        check(load().tsk_gguf_get_f32(self.h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def str(self, key):
+        v = ctypes.c_char_p()
+        check(load().tsk_gguf_get_str(self.h, key.encode(), ctypes.byref(v)))
+        return v.value.decode()
+
+    def dit_config(self, **kw):
+        c = dit_config(**kw)
+        check(load().tsk_dit_config_from_gguf(self.h, ctypes.byref(c)))
+        return c
+
+    def t5_config(self, **kw):
+        c = t5_config(**kw)
+        check(load().tsk_t5_config_from_gguf(self.h, ctypes.byref(c)))
+        return c
+
+    def load_into(self, model):
+        """all weights of a Dit or T5 driver from this file"""
+        fn = load().tsk_dit_load_gguf if isinstance(model, Dit) else load().tsk_t5_load_gguf
+        check(fn(model.h, self.h))
