@@ -14,6 +14,11 @@
  *   tsk_qk_norm_rope    <- the chain rms_norm -> mul(w) -> rope_ext of
  *                          pre_attn                             src/mmdit.cpp:221-223
  *   tsk_norm            <- ggml_norm(x, eps)                   src/mmdit.cpp:59
+ *   tsk_im2col_1d       <- ggml_im2col(w, x, s0,0,p0,0,d0,0, false, type) src/mmdit.cpp:21
+ *   tsk_conv1d          <- conv_cl / conv1d_f32                src/mmdit.cpp:20-34
+ *   tsk_swiglu          <- ggml_mul(ggml_silu(h1), h3)         src/mmdit.cpp:42, :50
+ *   tsk_conv_mlp_swiglu <- convmlp                             src/mmdit.cpp:39-44
+ *   tsk_mlp_swiglu      <- mlp                                 src/mmdit.cpp:47-52
  *   tsk_dit_*           <- ts_dit::load / forward / sample     src/mmdit.h:9-42
  *
  * Conventions (all follow ggml):
@@ -171,6 +176,77 @@ int tsk_q8_0_repack(const tsk_tensor *src, tsk_tensor *dst, tsk_stream stream);
 /* Bytes a Q8_0_SPLIT tensor of ne = [K, M] occupies. */
 size_t tsk_q8_0_split_nbytes(int64_t K, int64_t M);
 
+/* ---- convolution and SwiGLU glue (src/mmdit.cpp:20-52) -------------------
+ * The reference graph's latent / clip streams run kernel-3 convolutions
+ * (conv1d_f32 = ggml_im2col + ggml_mul_mat, conv_cl, convmlp) and its text
+ * stream SwiGLU linear MLPs (mlp). Convolutions here are one GEMM with
+ * K = KW * IC over an implicit im2col (the GEMM gathers shifted input rows
+ * while staging them; no im2col buffer), which needs the kernel's K in
+ * kw-major order: tsk_conv1d_pack_weight writes that layout once at load,
+ * and other layouts are permuted into library scratch on every call. Type
+ * rules are ggml_mul_mat's: BF16 kernels round the input to bf16 (RNE) and
+ * sum exact products in fp32; F32 kernels (the Q8_0 DiT keeps its 3-D
+ * kernels in F32) run all-fp32. Only the fp32 summation order differs from
+ * the ggml graph. */
+
+/*
+ * ggml_im2col(kernel, x, s0, 0, p0, 0, d0, 0, false, dst type), 1-D
+ * (conv1d_f32, src/mmdit.cpp:21):
+ *   kernel : ne = [KW, IC, ...]; only its shape is read
+ *   x      : F32 ne = [IW, IC, N, 1], any element strides (a ggml_transpose
+ *            view of a channels-fastest [IC, IW] tensor included)
+ *   dst    : ne = [IC * KW, OW, N, 1] F32, F16 or BF16, rows contiguous,
+ *            OW = (IW + 2 p0 - d0 (KW - 1) - 1) / s0 + 1
+ *   dst[n][ow][ic * KW + kw] = x[n][ic][ow * s0 + kw * d0 - p0], 0 outside [0, IW).
+ */
+int tsk_im2col_1d(const tsk_tensor *kernel, const tsk_tensor *x, int s0, int p0, int d0,
+                  tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * conv_cl (src/mmdit.cpp:28-34): channels-last 1-D convolution,
+ *   dst[b][ow][oc] = bias[oc] + sum_{ic,kw} w[oc][ic][kw] x[b][ow s0 + kw d0 - p0][ic]
+ *   w    : ne = [KW, IC, OC] BF16 or F32, any element strides; the kw-major
+ *          storage nb = [IC es, es, >= KW IC es (16-B multiple)] is read in
+ *          place (tsk_conv1d_pack_weight), other layouts are permuted into
+ *          scratch per call
+ *   bias : nullable F32 [OC], contiguous, 16-B aligned
+ *   x    : ne = [IC, IW, B, 1] F32, or BF16 with BF16 w (the canonical
+ *          channels-fastest layout: the reference's transpose is implicit);
+ *          rows contiguous, nb[1], nb[2] and data 16-B aligned; IC % 8 == 0
+ *   dst  : ne = [OC, OW, B, 1] F32 or BF16, rows contiguous and uniformly
+ *          strided (nb[2] = OW nb[1])
+ */
+int tsk_conv1d(const tsk_tensor *w, const tsk_tensor *bias, const tsk_tensor *x, int s0,
+               int p0, int d0, tsk_tensor *dst, tsk_stream stream);
+
+/* Copy a conv kernel ne = [KW, IC, OC] (any strides, BF16 or F32) into dst of
+ * the same type and shape laid out kw-major: nb = [IC es, es, KW IC es, ...]
+ * (a load-time permutation, like tsk_q8_0_repack; bit-preserving). */
+int tsk_conv1d_pack_weight(const tsk_tensor *w, tsk_tensor *dst, tsk_stream stream);
+
+/* dst = ggml_mul(ggml_silu(a), b) (src/mmdit.cpp:42, :50), F32, all three
+ * contiguous and of one shape; silu(a) = a / (1 + exp(-a)). */
+int tsk_swiglu(const tsk_tensor *a, const tsk_tensor *b, tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * convmlp (src/mmdit.cpp:39-44): dst = conv(w2, silu(conv(w1, x)) * conv(w3, x)),
+ * every conv stride 1, padding 1, dilation 1, no bias. w1, w3: [KW, IC, HID],
+ * w2: [KW, HID, OC], all BF16 or all F32 (layouts as tsk_conv1d); x and dst
+ * as tsk_conv1d; HID % 8 == 0. BF16: w1 and w3 run as ONE GEMM whose epilogue
+ * writes silu(h1) * h3 rounded to bf16 -- the conversion ggml_mul_mat applies
+ * to it before w2 -- so the hidden state is written once; F32: two GEMMs and
+ * tsk_swiglu. The hidden state lives in library scratch.
+ */
+int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                        const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream);
+
+/* mlp (src/mmdit.cpp:47-52): dst = w2 (silu(w1 x) * w3 x), linear layers
+ * without bias: w1, w3 ne = [IC, HID], w2 ne = [HID, OC], all BF16 or all
+ * F32, rows contiguous; x ne = [IC, N, n2, n3] F32 (or BF16 with BF16 weights),
+ * dst [OC, N, n2, n3] F32 or BF16, rows of both uniformly strided. */
+int tsk_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                   const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream);
+
 /* ggml_op ids used by tsk_supports_op (values of ggml's enum ggml_op are not
  * stable across ggml revisions, so these are this library's own). */
 enum tsk_op {
@@ -178,7 +254,9 @@ enum tsk_op {
     TSK_OP_FLASH_ATTN_EXT = 2,
     TSK_OP_RMS_NORM_MUL   = 3,
     TSK_OP_ROPE_EXT       = 4,
-    TSK_OP_NORM           = 5
+    TSK_OP_NORM           = 5,
+    TSK_OP_IM2COL         = 6,   /* srcs: kernel, x; fixed s0 = 1, p0 = 1, d0 = 1 */
+    TSK_OP_CONV1D         = 7    /* srcs: w, x, bias; fixed s0 = 1, p0 = 1, d0 = 1 */
 };
 /* Mirror of a ggml backend's supports_op: 1 if tsk would run the node with
  * these operand descriptors (data pointers are not inspected), else 0.

@@ -101,6 +101,11 @@ def lib():
         L.orc_t5_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
         L.orc_t5_encode.argtypes = [vp, ctypes.c_int, vp, vp, vp]
         L.orc_t5_encode_range.argtypes = [vp, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
+        L.orc_im2col_1d.argtypes = [ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
+        L.orc_conv1d.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
+        L.orc_swiglu.argtypes = [vp, vp, vp, ctypes.c_int64]
+        L.orc_conv_mlp_swiglu.argtypes = [P, P, P, P, P]
+        L.orc_mlp_swiglu.argtypes = [P, P, P, P, P]
         _lib = L
     return _lib
 
@@ -260,6 +265,77 @@ def rope_ext(x, pos, n_dims, freq_base=10000.0, freq_scale=1.0):
                             freq_scale, ctypes.byref(tensor(out, F32)))
     assert rc == 0
     return out
+
+
+# ---------------------------------------------------------------- convolution / SwiGLU
+def conv_len(iw, kw, s0=1, p0=1, d0=1):
+    return (iw + 2 * p0 - d0 * (kw - 1) - 1) // s0 + 1
+
+
+def im2col_1d(x, kw, s0=1, p0=1, d0=1):
+    """ggml_im2col 1-D: x (N, IC, IW) float32 -> (N, OW, IC*KW) float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N, IC, IW = x.shape
+    out = np.empty((N, conv_len(IW, kw, s0, p0, d0), IC * kw), dtype=np.float32)
+    rc = lib().orc_im2col_1d(kw, ctypes.byref(tensor(x, F32)), s0, p0, d0, ctypes.byref(tensor(out, F32)))
+    assert rc == 0, rc
+    return out
+
+
+def _kernel(w, w_type):
+    """(OC, IC, KW) kernel values (float32, float16 or bf16 bits) -> tsk view."""
+    w = np.ascontiguousarray(w)
+    return w, tensor(w, w_type if w_type is not None else _ttype(w, False))
+
+
+def conv1d(w, x, bias=None, s0=1, p0=1, d0=1, w_type=None):
+    """conv_cl: w (OC, IC, KW) (ggml ne [KW, IC, OC]), x (B, IW, IC) float32
+    channels fastest -> (B, OW, OC) float32."""
+    w, tw = _kernel(w, w_type)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, IW, _ = x.shape
+    out = np.empty((B, conv_len(IW, w.shape[2], s0, p0, d0), w.shape[0]), dtype=np.float32)
+    tb = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        tb = ctypes.byref(tensor(bias, F32))
+    rc = lib().orc_conv1d(ctypes.byref(tw), tb, ctypes.byref(tensor(x, F32)), s0, p0, d0,
+                          ctypes.byref(tensor(out, F32)))
+    assert rc == 0, rc
+    return out
+
+
+def swiglu(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().orc_swiglu(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size)
+    return out
+
+
+def conv_mlp_swiglu(w1, w3, w2, x, w_type=None):
+    """convmlp: kernels (HID, IC, KW), (HID, IC, KW), (OC, HID, KW); x (B, IW, IC)."""
+    (w1, t1), (w3, t3), (w2, t2) = (_kernel(w, w_type) for w in (w1, w3, w2))
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, IW, _ = x.shape
+    ow = conv_len(conv_len(IW, w1.shape[2]), w2.shape[2])
+    out = np.empty((B, ow, w2.shape[0]), dtype=np.float32)
+    rc = lib().orc_conv_mlp_swiglu(ctypes.byref(t1), ctypes.byref(t3), ctypes.byref(t2),
+                                   ctypes.byref(tensor(x, F32)), ctypes.byref(tensor(out, F32)))
+    assert rc == 0, rc
+    return out
+
+
+def mlp_swiglu(w1, w3, w2, x, w_type=None):
+    """mlp: weights (HID, IC), (HID, IC), (OC, HID); x (..., IC) -> (..., OC)."""
+    (w1, t1), (w3, t3), (w2, t2) = (_kernel(w, w_type) for w in (w1, w3, w2))
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    out = np.empty((x2.shape[0], w2.shape[0]), dtype=np.float32)
+    rc = lib().orc_mlp_swiglu(ctypes.byref(t1), ctypes.byref(t3), ctypes.byref(t2),
+                              ctypes.byref(tensor(x2, F32)), ctypes.byref(tensor(out, F32)))
+    assert rc == 0, rc
+    return out.reshape(x.shape[:-1] + (w2.shape[0],))
 
 
 # ---------------------------------------------------------------- MM-DiT

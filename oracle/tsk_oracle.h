@@ -70,6 +70,16 @@ int      orc_rope_ext(const tsk_tensor *x, const int32_t *pos, int n_dims, float
 
 /* elementwise helpers used by the DiT restatement */
 float    orc_silu(float x);
+
+/* convolution / SwiGLU nodes (tsk_oracle_conv.c, src/mmdit.cpp:20-52) */
+int      orc_im2col_1d(int KW, const tsk_tensor *x, int s0, int p0, int d0, tsk_tensor *dst);
+int      orc_conv1d(const tsk_tensor *w, const tsk_tensor *bias, const tsk_tensor *x, int s0, int p0,
+                    int d0, tsk_tensor *dst);
+void     orc_swiglu(const float *a, const float *b, float *y, int64_t n);
+int      orc_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                             const tsk_tensor *x, tsk_tensor *dst);
+int      orc_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                        const tsk_tensor *x, tsk_tensor *dst);
 float    orc_gelu_tanh(float x);
 
 /* ---- MM-DiT flow step (BASELINE textbook configuration) ------------------

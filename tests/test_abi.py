@@ -73,7 +73,9 @@ def test_mul_mat_validation(tsk):
     assert call_mm(T, a, bad_b, dst) == -3                       # K mismatch
     bad_dst = fake(T, T.F32, (388, 3000), 4)
     assert call_mm(T, a, b, bad_dst) == -3                       # M mismatch
-    assert call_mm(T, fake(T, T.F32, (3072, 1024), 4), b, dst) == -6   # F32 weights unsupported
+    assert call_mm(T, fake(T, T.F32, (3072, 1024), 4), b, dst) == -7   # F32 weights: all-fp32 GEMM
+    assert call_mm(T, fake(T, T.F16, (3072, 1024), 2), b, dst) == -6   # F16 weights unsupported
+    assert call_mm(T, fake(T, T.F32, (3072, 1024), 4), fake(T, T.BF16, (388, 1024), 2), dst) == -2
     q = T.TskTensor()
     q.type = T.Q8_0
     q.ne[:] = [1000, 64, 1, 1]
@@ -150,9 +152,73 @@ def test_supports_op(tsk):
     b = fake(T, T.F32, (154, 1024), 4)
     d = fake(T, T.F32, (154, 1024), 4)
     assert sup(T.OP_MUL_MAT, [a, b], d) == 1
-    assert sup(T.OP_MUL_MAT, [fake(T, T.F32, (1024, 1024), 4), b], d) == 0
+    assert sup(T.OP_MUL_MAT, [fake(T, T.F32, (1024, 1024), 4), b], d) == 1
+    assert sup(T.OP_MUL_MAT, [fake(T, T.F16, (1024, 1024), 2), b], d) == 0
     q = fake(T, T.F32, (1, 16, 77, 64), 4)
     kv = fake(T, T.F16, (1, 16, 77, 64), 2)
     o = fake(T, T.F32, (1, 77, 16, 64), 4)
     assert sup(T.OP_FLASH_ATTN_EXT, [q, kv, kv], o) == 1
     assert sup(T.OP_FLASH_ATTN_EXT, [fake(T, T.F32, (1, 8, 77, 80), 4), kv, kv], o) == 0
+
+
+def kernel_desc(T, ttype, oc, ic, kw, es, kw_major=False):
+    """ggml conv kernel ne = [KW, IC, OC]; ggml layout or the kw-major one"""
+    d = fake(T, ttype, (oc, ic, kw), es)
+    if kw_major:
+        d.nb[0], d.nb[1], d.nb[2] = ic * es, es, kw * ic * es
+    return d
+
+
+def test_conv_validation(tsk):
+    T = tsk
+    lib = T.load()
+    w = kernel_desc(T, T.BF16, 2816, 1024, 3, 2)
+    x = fake(T, T.F32, (2, 646, 1024), 4)          # ne [IC, IW, B]
+    y = fake(T, T.F32, (2, 646, 2816), 4)
+    conv = lambda w_, x_, y_, s0=1, p0=1, d0=1, b_=None: lib.tsk_conv1d(
+        ctypes.byref(w_), ctypes.byref(b_) if b_ else None, ctypes.byref(x_), s0, p0, d0, ctypes.byref(y_), None)
+    assert conv(w, x, y) == -7
+    assert conv(kernel_desc(T, T.BF16, 2816, 1024, 3, 2, True), x, y) == -7
+    assert conv(kernel_desc(T, T.F32, 2816, 1024, 3, 4), x, y) == -7
+    assert conv(kernel_desc(T, T.Q8_0, 2816, 1024, 3, 1), x, y) == -2        # 3-D kernels are BF16 / F32
+    assert conv(w, x, fake(T, T.F32, (2, 645, 2816), 4)) == -3              # OW mismatch
+    assert conv(w, x, fake(T, T.F32, (2, 323, 2816), 4), s0=2) == -7        # stride 2: OW = 323
+    assert conv(w, x, y, p0=-1) == -1
+    assert conv(kernel_desc(T, T.BF16, 64, 20, 3, 2), fake(T, T.F32, (1, 30, 20), 4),
+                fake(T, T.F32, (1, 30, 64), 4)) == -3                        # IC % 8
+    assert conv(kernel_desc(T, T.F32, 64, 16, 3, 4), fake(T, T.BF16, (1, 30, 16), 2),
+                fake(T, T.F32, (1, 30, 64), 4)) == -2                        # F32 kernel, BF16 x
+    assert conv(w, x, y, b_=fake(T, T.F32, (2816,), 4)) == -7
+    assert conv(w, x, y, b_=fake(T, T.F32, (2815,), 4)) == -3
+    # im2col node: x ne [IW, IC, N] any strides, dst [IC*KW, OW, N]
+    xi = fake(T, T.F32, (1, 1024, 646), 4)
+    ci = fake(T, T.F32, (1, 646, 3072), 4)
+    im = lambda x_, d_, s0=1, p0=1, d0=1: lib.tsk_im2col_1d(ctypes.byref(w), ctypes.byref(x_), s0, p0, d0,
+                                                            ctypes.byref(d_), None)
+    assert im(xi, ci) == -7
+    assert im(xi, fake(T, T.F16, (1, 646, 3072), 2)) == -7
+    assert im(xi, fake(T, T.F32, (1, 646, 3000), 4)) == -3
+    assert im(fake(T, T.F16, (1, 1024, 646), 2), ci) == -2
+    # SwiGLU MLPs
+    w2 = kernel_desc(T, T.BF16, 1024, 2816, 3, 2)
+    out = fake(T, T.F32, (2, 646, 1024), 4)
+    cm = lambda a, b_, c, x_, d_: lib.tsk_conv_mlp_swiglu(ctypes.byref(a), ctypes.byref(b_), ctypes.byref(c),
+                                                          ctypes.byref(x_), ctypes.byref(d_), None)
+    assert cm(w, w, w2, x, out) == -7
+    assert cm(w, w, kernel_desc(T, T.F32, 1024, 2816, 3, 4), x, out) == -2    # mixed kernel types
+    assert cm(w, w, kernel_desc(T, T.BF16, 1024, 2000, 3, 2), x, out) == -3   # w2 IC != HID
+    l1 = fake(T, T.BF16, (2816, 1024), 2)
+    l2 = fake(T, T.BF16, (1024, 2816), 2)
+    xt = fake(T, T.F32, (154, 1024), 4)
+    ml = lambda a, b_, c, x_, d_: lib.tsk_mlp_swiglu(ctypes.byref(a), ctypes.byref(b_), ctypes.byref(c),
+                                                     ctypes.byref(x_), ctypes.byref(d_), None)
+    assert ml(l1, l1, l2, xt, fake(T, T.F32, (154, 1024), 4)) == -7
+    assert ml(l1, l1, l2, xt, fake(T, T.F32, (154, 1000), 4)) == -3
+    a = fake(T, T.F32, (646, 2816), 4)
+    assert lib.tsk_swiglu(ctypes.byref(a), ctypes.byref(a), ctypes.byref(a), None) == -7
+    assert lib.tsk_swiglu(ctypes.byref(a), ctypes.byref(fake(T, T.F32, (646, 2815), 4)), ctypes.byref(a),
+                          None) == -3
+    # kw-major pack: dst strides must be the kw-major ones
+    pk = kernel_desc(T, T.BF16, 2816, 1024, 3, 2, True)
+    assert lib.tsk_conv1d_pack_weight(ctypes.byref(w), ctypes.byref(pk), None) == -7
+    assert lib.tsk_conv1d_pack_weight(ctypes.byref(w), ctypes.byref(w), None) == -4

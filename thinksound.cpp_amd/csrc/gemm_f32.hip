@@ -1,0 +1,170 @@
+// gemm_f32.hip — F32-weight GEMMs on gfx950: ggml_mul_mat with an F32 src0,
+// whose vec_dot type is F32, so activations stay fp32 and every product and
+// sum is fp32 (src/mmdit.cpp:13, :24 — the Q8_0 DiT keeps its 3-D
+// convolution kernels in F32).
+//
+//   Y[n, m] = sum_k X[n, k] * W[m, k] + bias[m]
+//
+// fp32 MFMA 16x16x4: A = 16 weight rows, B = 16 tokens; lane l supplies row /
+// token l % 16 at k-lane l / 16 and ends with 4 consecutive output features
+// of one token. A 16-B LDS read gives each lane four k values
+// (4 * (l / 16) + t, t = 0..3), consumed by four MFMAs, so one K block of 16
+// costs TM + TN LDS reads for 4 * TM * TN MFMAs.
+//
+// Workgroup = 2 x 2 waves, each TM x TN 16x16 tiles; operand tiles are
+// double buffered through LDS (global -> registers -> LDS, one barrier per
+// 32-wide K step). The activation rows may be an implicit im2col of a
+// channels-fastest input (GemmProblem::conv_ic, as in gemm_group.hip).
+#include "tsk_common.h"
+#include "tsk_internal.h"
+
+namespace tsk {
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int BK = 32;
+constexpr int LDK = BK + 4;   // floats per LDS row: 16-B aligned, the 16 rows of a read hit distinct banks
+
+template <int TM, int TN, bool YBF16>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
+    constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
+    constexpr int WCH = BM * (BK / 4), XCH = BN * (BK / 4);   // 16-B chunks per tile
+    constexpr int WPER = WCH / NT, XPER = XCH / NT;
+    static_assert(WCH % NT == 0 && XCH % NT == 0, "tile chunks");
+    __shared__ __attribute__((aligned(16))) float Ws[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) float Xs[2][BN * LDK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int bm0 = blockIdx.x * BM, bn0 = blockIdx.y * BN;
+    const float *W = p.wf;
+    const float *X = (const float *) p.x;
+
+    // per-chunk source rows, fixed over K: weight row, and for X the row
+    // offset (plain) or batch offset + first input position (convolution)
+    int64_t xbase[XPER];
+    int xiw0[XPER];
+    bool xrow_ok[XPER];
+    for (int i = 0; i < XPER; ++i) {
+        const int c = tid + i * NT;
+        const int n = bn0 + c / (BK / 4);
+        xrow_ok[i] = n < p.N;
+        const int nn = xrow_ok[i] ? n : 0;
+        if (p.conv_ic) {
+            const int b = nn / p.conv_ow, ow = nn - b * p.conv_ow;
+            xbase[i] = (int64_t) b * p.x_group_stride;
+            xiw0[i] = ow * p.conv_s - p.conv_p;
+        } else {
+            xbase[i] = p.x_group_rows ? (int64_t) (nn / p.x_group_rows) * p.x_group_stride +
+                                            (int64_t) (nn % p.x_group_rows) * p.ld_x
+                                      : (int64_t) nn * p.ld_x;
+            xiw0[i] = 0;
+        }
+    }
+
+    f32x4 wreg[WPER], xreg[XPER];
+    const int nk = (p.K + BK - 1) / BK;
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            const int row = bm0 + c / (BK / 4), k = k0 + (c % (BK / 4)) * 4;
+            wreg[i] = f32x4{0, 0, 0, 0};
+            if (row < p.M && k < p.K) wreg[i] = *(const f32x4 *) (W + (int64_t) row * p.ld_w + k);
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            const int k = k0 + (c % (BK / 4)) * 4;
+            bool ok = xrow_ok[i] && k < p.K;
+            int64_t off = 0;
+            if (p.conv_ic) {
+                const int kw = k / p.conv_ic, ic = k - kw * p.conv_ic;
+                const int iw = xiw0[i] + kw * p.conv_d;
+                ok = ok && iw >= 0 && iw < p.conv_iw;
+                off = xbase[i] + (int64_t) iw * p.ld_x + ic;
+            } else {
+                off = xbase[i] + k;
+            }
+            xreg[i] = f32x4{0, 0, 0, 0};
+            if (ok) xreg[i] = *(const f32x4 *) (X + off);
+        }
+    };
+    auto lstore = [&](int buf) {
+        for (int i = 0; i < WPER; ++i) {
+            const int c = tid + i * NT;
+            *(f32x4 *) &Ws[buf][(c / (BK / 4)) * LDK + (c % (BK / 4)) * 4] = wreg[i];
+        }
+        for (int i = 0; i < XPER; ++i) {
+            const int c = tid + i * NT;
+            *(f32x4 *) &Xs[buf][(c / (BK / 4)) * LDK + (c % (BK / 4)) * 4] = xreg[i];
+        }
+    };
+
+    f32x4 acc[TM][TN];
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int kb = 0; kb < BK / 16; ++kb) {
+            f32x4 a[TM], b[TN];
+            for (int i = 0; i < TM; ++i)
+                a[i] = *(const f32x4 *) &Ws[buf][((wm * TM + i) * 16 + lr) * LDK + 16 * kb + 4 * lg];
+            for (int j = 0; j < TN; ++j)
+                b[j] = *(const f32x4 *) &Xs[buf][((wn * TN + j) * 16 + lr) * LDK + 16 * kb + 4 * lg];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                for (int i = 0; i < TM; ++i)
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    for (int i = 0; i < TM; ++i) {
+        const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
+        if (m0 >= p.M) continue;
+        const bool full = m0 + 3 < p.M;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias)
+            for (int r = 0; r < 4 && m0 + r < p.M; ++r) bv[r] = p.bias[m0 + r];
+        for (int j = 0; j < TN; ++j) {
+            const int n = bn0 + (wn * TN + j) * 16 + lr;
+            if (n >= p.N) continue;
+            float o[4];
+            for (int r = 0; r < 4; ++r) o[r] = acc[i][j][r] + bv[r];
+            if constexpr (YBF16) {
+                uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
+                for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+            } else {
+                float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
+                if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                else for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s) {
+    constexpr int TM = 4, TN = 2, BM = 2 * TM * 16, BN = 2 * TN * 16;
+    if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf) return hipErrorInvalidValue;
+    if (p.conv_ic && (p.conv_ic % 4 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
+                      p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
+        return hipErrorInvalidValue;
+    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
+    if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true>), grid, dim3(NT), 0, s, p);
+    else launch_kernel((gemm_f32_kernel<TM, TN, false>), grid, dim3(NT), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace tsk

@@ -18,9 +18,20 @@
 //
 // Epilogues: f32 / bf16 store (+bias), GELU(tanh) -> bf16, split-K partial
 // slices (summed in fixed order by the consumer, so results do not depend on
-// the launch shape), and the QKV epilogue that applies RMSNorm*w to q and k,
+// the launch shape), the QKV epilogue that applies RMSNorm*w to q and k,
 // RoPE on the latent stream and the F16 cast into the attention layout
-// [B][n_head][Ntot][64] (mmdit.cpp:80-90), through an LDS transpose.
+// [B][n_head][Ntot][64] (mmdit.cpp:80-90), through an LDS transpose, and
+// SwiGLU: half of a wave's weight tiles stream W1 rows, the other half the
+// same rows of W3, so each lane holds h1 and h3 of the same (feature, token)
+// and writes silu(h1) * h3 (convmlp / mlp, mmdit.cpp:39-52).
+//
+// Convolutions (conv1d_f32 / conv_cl, mmdit.cpp:20-34) run as this GEMM with
+// K = KW * IC over an implicit im2col: the activation tile is gathered from
+// shifted position rows of the channels-fastest input while it is staged
+// into LDS, so no im2col buffer exists. This needs the weight's K in
+// kw-major order (k = kw * IC + ic), a load-time permutation of ggml's
+// [KW, IC, OC] kernel (k = ic * KW + kw); only the order of the fp32
+// accumulation differs from the ggml graph.
 #include "tsk_common.h"
 #include "tsk_internal.h"
 
@@ -71,18 +82,24 @@ __device__ __forceinline__ int64_t x_row_offset(const GemmProblem &p, int n) {
                           : (int64_t) n * p.ld_x;
 }
 
+constexpr bool is_swiglu(int epi) { return epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_BF16; }
+
 template <int TM, int TN, int PF, bool XF32, int EPI>
 __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int KC) {
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
     constexpr int BM = Tile<TM, TN>::BM, BN = Tile<TM, TN>::BN;
+    constexpr bool SWIGLU = is_swiglu(EPI);
+    constexpr int TMO = SWIGLU ? TM / 2 : TM;     // output row tiles per wave
+    constexpr int BMO = 4 * TMO * 16;             // output features per workgroup
     static_assert(PF * TM * 2 <= 48, "vmcnt range");
+    static_assert(!SWIGLU || TM % 2 == 0, "SwiGLU pairs weight tiles");
 
     TileCoord tc;
     if (!decode(g, tc)) return;
     const GemmProblem &p = g.p[tc.pi];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int bm0 = tc.tm * BM, bn0 = tc.tn * BN;
+    const int bm0 = tc.tm * BMO, bn0 = tc.tn * BN;
     const int LDX = KC + 8;                       // bf16 per LDS row: 16-B pad against bank conflicts
     const int kspl = ((p.K + p.splits - 1) / p.splits + KS - 1) / KS * KS;
     const int kbeg = tc.split * kspl, kend = min(p.K, kbeg + kspl);
@@ -95,14 +112,16 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
     // piece 1 at +32; tiled weights: the lane's 16 B of tile (rb, k / 32) at
     // wrow + (k / 32) * 512 (lane offset folded into wrow), piece 1 at +512.
     // Pieces outside [c0, c1) load offset 0 instead (a valid address).
+    // SwiGLU: tiles [0, TMO) are W1's row blocks, [TMO, TM) the same of W3.
     const uint16_t *wrow[TM];
     for (int i = 0; i < TM; ++i) {
-        const int rb = (bm0 >> 4) + wave * TM + i;
+        const int rb = (bm0 >> 4) + wave * TMO + i % TMO;
+        const uint16_t *wb = SWIGLU && i >= TMO ? p.w3 : p.w;
         if (p.w_tiled) {
-            wrow[i] = p.w + (int64_t) min(rb, p.M / 16 - 1) * (p.K / 32) * 512 + lane * 8;
+            wrow[i] = wb + (int64_t) min(rb, p.M / 16 - 1) * (p.K / 32) * 512 + lane * 8;
         } else {
             const int row = rb * 16 + lr;
-            wrow[i] = p.w + (int64_t) (row < p.M ? row : 0) * p.ld_w;
+            wrow[i] = wb + (int64_t) (row < p.M ? row : 0) * p.ld_w;
         }
     }
     const int wstep = p.w_tiled ? 1024 : 64, wpiece = p.w_tiled ? 512 : 32;
@@ -162,19 +181,43 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
         // loads are issued before the first PF weight steps (bf16 activations),
         // so the stores wait only for them (vmcnt retires in order).
         constexpr int RPW = BN / 4;                   // rows per wave
+        static_assert(2 * RPW <= 32, "piece mask");
         const int kcr = nst * KS;
         const int wv = __builtin_amdgcn_readfirstlane(wave);
         u32x4 xv[RPW][2][XF32 ? 2 : 1];
+        uint32_t xok = 0;                             // bit 2 g2 + h: the piece holds data
         auto xload = [&]() {
 #pragma unroll
             for (int g2 = 0; g2 < RPW; ++g2) {
                 const int r = wv + 4 * g2;
                 const bool rok = bn0 + r < p.N;
-                const int64_t roff = x_row_offset(p, rok ? bn0 + r : 0);
+                const int n = rok ? bn0 + r : 0;
+                int64_t roff;
+                int iw0 = 0;
+                if (p.conv_ic) {
+                    // output position ow of batch item b reads input positions
+                    // ow * s + kw * d - p
+                    const int b = n / p.conv_ow, ow = n - b * p.conv_ow;
+                    roff = (int64_t) b * p.x_group_stride;
+                    iw0 = ow * p.conv_s - p.conv_p;
+                } else {
+                    roff = x_row_offset(p, n);
+                }
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int col = lane * 8 + 512 * h;
-                    const int64_t off = roff + (rok && c0 + col < c1 ? c0 + col : 0);
+                    const int k = c0 + col;
+                    bool ok = rok && k < c1;
+                    int64_t off;
+                    if (p.conv_ic) {
+                        const int kw = k / p.conv_ic, ic = k - kw * p.conv_ic;
+                        const int iw = iw0 + kw * p.conv_d;
+                        ok = ok && iw >= 0 && iw < p.conv_iw;
+                        off = ok ? roff + (int64_t) iw * p.ld_x + ic : 0;
+                    } else {
+                        off = roff + (ok ? k : 0);
+                    }
+                    xok |= (uint32_t) ok << (2 * g2 + h);
                     if constexpr (XF32) {
                         const float *xf = (const float *) p.x + off;
                         xv[g2][h][0] = *(const u32x4 *) xf;
@@ -189,11 +232,10 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
 #pragma unroll
             for (int g2 = 0; g2 < RPW; ++g2) {
                 const int r = wv + 4 * g2;
-                const bool rok = bn0 + r < p.N;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int col = lane * 8 + 512 * h;
-                    const bool ok = rok && c0 + col < c1;
+                    const bool ok = (xok >> (2 * g2 + h)) & 1;
                     u32x4 t;
                     if constexpr (XF32) {
                         const float *f0 = (const float *) &xv[g2][h][0], *f1 = (const float *) &xv[g2][h][1];
@@ -207,6 +249,7 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
                 }
             }
         };
+        xok = 0;
         xload();
         if constexpr (XF32) {
             xstore();     // f32 tiles hold twice the registers: store before the weights go out
@@ -290,6 +333,37 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
             }
         }
         return;
+    } else if constexpr (SWIGLU) {
+        for (int i = 0; i < TMO; ++i) {
+            const int m0 = bm0 + (wave * TMO + i) * 16 + 4 * lg;
+            if (m0 >= p.M) continue;
+            const bool full = m0 + 3 < p.M;
+            for (int j = 0; j < TN; ++j) {
+                const int n = bn0 + j * 16 + lr;
+                if (n >= p.N) continue;
+                float o[4];
+                for (int r = 0; r < 4; ++r) {
+                    const float h1 = acc[i][j][r], h3 = acc[i + TMO][j][r];
+                    o[r] = h1 / (1.0f + expf(-h1)) * h3;
+                }
+                if constexpr (EPI == EPI_SWIGLU_BF16) {
+                    uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
+                    if (full) {
+                        uint16_t t4[4];
+                        for (int r = 0; r < 4; ++r) t4[r] = f32_to_bf16_bits(o[r]);
+                        u32x2 w;
+                        __builtin_memcpy(&w, t4, 8);
+                        *(u32x2 *) yr = w;
+                    } else {
+                        for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+                    }
+                } else {
+                    float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
+                    if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                    else for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+                }
+            }
+        }
     } else {
         for (int i = 0; i < TM; ++i) {
             const int m0 = bm0 + (wave * TM + i) * 16 + 4 * lg;
@@ -348,7 +422,9 @@ hipError_t group_launch(GemmGroup &g, int flags, int epi, hipStream_t s) {
     constexpr int BM = Tile<TM, TN>::BM, BN = Tile<TM, TN>::BN;
     if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
     const bool xf32 = (flags & GEMM_X_F32) != 0;
-    if (xf32 && epi != EPI_STORE_F32 && epi != EPI_STORE_BF16) return hipErrorInvalidValue;
+    const bool swiglu = is_swiglu(epi);
+    if (xf32 && epi != EPI_STORE_F32 && epi != EPI_STORE_BF16 && !swiglu) return hipErrorInvalidValue;
+    const int bmo = swiglu ? BM / 2 : BM;
     // K held in LDS per chunk: up to KCMAX, within the device's LDS per workgroup
     static int kc_dev = 0;
     if (!kc_dev) {
@@ -366,7 +442,14 @@ hipError_t group_launch(GemmGroup &g, int flags, int epi, hipStream_t s) {
         if (epi != EPI_PARTIAL && p.splits != 1) return hipErrorInvalidValue;
         if (epi == EPI_QKV && (p.M % 192 || p.seq < 1)) return hipErrorInvalidValue;
         if (p.w_tiled && (p.M % 16 || p.K % 32)) return hipErrorInvalidValue;
-        p.tiles_m = (p.M + BM - 1) / BM;
+        if (swiglu && (!p.w3 || p.bias)) return hipErrorInvalidValue;
+        if (p.conv_ic) {
+            // every 16-B piece of a K step lies inside one kw slice
+            if (p.conv_ic % 8 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
+                p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow)
+                return hipErrorInvalidValue;
+        }
+        p.tiles_m = (p.M + bmo - 1) / bmo;
         p.tiles_n = (p.N + BN - 1) / BN;
         p.block_begin = (nblocks + 7) & ~7;
         nblocks = p.block_begin + p.tiles_m * p.tiles_n * p.splits;
@@ -385,6 +468,12 @@ hipError_t group_launch(GemmGroup &g, int flags, int epi, hipStream_t s) {
         case EPI_GELU_BF16: return launch_cfg<TM, TN, PF, false, EPI_GELU_BF16>(g, kc, nblocks, lds, s);
         case EPI_QKV: return launch_cfg<TM, TN, PF, false, EPI_QKV>(g, kc, nblocks, lds, s);
         case EPI_PARTIAL: return launch_cfg<TM, TN, PF, false, EPI_PARTIAL>(g, kc, nblocks, lds, s);
+        case EPI_SWIGLU_F32:
+            return xf32 ? launch_cfg<TM, TN, PF, true, EPI_SWIGLU_F32>(g, kc, nblocks, lds, s)
+                        : launch_cfg<TM, TN, PF, false, EPI_SWIGLU_F32>(g, kc, nblocks, lds, s);
+        case EPI_SWIGLU_BF16:
+            return xf32 ? launch_cfg<TM, TN, PF, true, EPI_SWIGLU_BF16>(g, kc, nblocks, lds, s)
+                        : launch_cfg<TM, TN, PF, false, EPI_SWIGLU_BF16>(g, kc, nblocks, lds, s);
         default: return hipErrorInvalidValue;
     }
 }

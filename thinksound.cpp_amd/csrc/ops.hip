@@ -354,6 +354,42 @@ __global__ __launch_bounds__(256) void proj_f32_kt_kernel(const uint16_t *w, con
     }
 }
 
+// ggml_im2col, 1-D (conv1d_f32, src/mmdit.cpp:20-25): dst[n][ow][ic * KW + kw]
+// = x(iw = ow * s0 + kw * d0 - p0, ic, n), 0 outside [0, IW). x addressed by
+// element strides of position, channel and batch (so a channels-fastest
+// [IC, S] input needs no transpose first).
+template <Elt E>
+__global__ void im2col_1d_kernel(const float *x, int64_t sp, int64_t sc, int64_t sn, int IW, int IC, int KW, int OW,
+                                 int N, int s0, int p0, int d0, void *dst, int64_t ld) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t K = (int64_t) IC * KW;
+    if (i >= K * OW * N) return;
+    const int64_t kk = i % K, row = i / K;
+    const int ow = (int) (row % OW), n = (int) (row / OW);
+    const int ic = (int) (kk / KW), kw = (int) (kk % KW);
+    const int iw = ow * s0 + kw * d0 - p0;
+    const float v = iw >= 0 && iw < IW ? x[(int64_t) iw * sp + (int64_t) ic * sc + (int64_t) n * sn] : 0.0f;
+    store_from_f32<E>(dst, row * ld + kk, v);
+}
+
+// conv kernel [KW, IC, OC] (element strides s0, s1, s2) -> kw-major rows
+// dst[oc][kw * IC + ic], a bit copy
+template <typename T>
+__global__ void conv_pack_kernel(const T *w, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, T *dst) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t) KW * IC * OC) return;
+    const int ic = (int) (i % IC);
+    const int64_t r = i / IC;
+    const int kw = (int) (r % KW), oc = (int) (r / KW);
+    dst[i] = w[kw * s0 + ic * s1 + oc * s2];
+}
+
+// ggml_mul(ggml_silu(a), b) (convmlp / mlp, src/mmdit.cpp:39-52): y = a / (1 + e^-a) * b
+__global__ void silu_mul_kernel(const float *a, const float *b, float *y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float v = a[i]; y[i] = v / (1.0f + expf(-v)) * b[i]; }
+}
+
 __global__ void silu_kernel(float *x, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
@@ -471,6 +507,48 @@ hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x,
     }
     const int64_t waves = (int64_t) N * ((M + 63) / 64);
     launch_kernel(proj_f32_kernel, dim3(blocks_for(waves, 4)), dim3(256), 0, s, w, bias, x, ld_x, N, K, M, y, ld_y);
+    return hipGetLastError();
+}
+
+hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, int IW, int IC, int KW, int OW, int N,
+                           int s0, int p0, int d0, void *dst, int dst_type, int64_t ld, hipStream_t s) {
+    const int64_t total = (int64_t) IC * KW * OW * N;
+    if (total < 1) return hipErrorInvalidValue;
+    const dim3 grid(blocks_for(total, 256)), block(256);
+    switch (dst_type) {
+        case (int) Elt::F32:
+            launch_kernel(im2col_1d_kernel<Elt::F32>, grid, block, 0, s, x, sp, sc, sn, IW, IC, KW, OW, N, s0, p0, d0, dst, ld);
+            break;
+        case (int) Elt::F16:
+            launch_kernel(im2col_1d_kernel<Elt::F16>, grid, block, 0, s, x, sp, sc, sn, IW, IC, KW, OW, N, s0, p0, d0, dst, ld);
+            break;
+        case (int) Elt::BF16:
+            launch_kernel(im2col_1d_kernel<Elt::BF16>, grid, block, 0, s, x, sp, sc, sn, IW, IC, KW, OW, N, s0, p0, d0, dst, ld);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
+                            hipStream_t s) {
+    const int64_t total = (int64_t) KW * IC * OC;
+    if (total < 1) return hipErrorInvalidValue;
+    const dim3 grid(blocks_for(total, 256)), block(256);
+    if (es == 4)
+        launch_kernel(conv_pack_kernel<uint32_t>, grid, block, 0, s, (const uint32_t *) w, s0, s1, s2, KW, IC, OC,
+                      (uint32_t *) dst);
+    else if (es == 2)
+        launch_kernel(conv_pack_kernel<uint16_t>, grid, block, 0, s, (const uint16_t *) w, s0, s1, s2, KW, IC, OC,
+                      (uint16_t *) dst);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s) {
+    launch_kernel(silu_mul_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, a, b, y, n);
     return hipGetLastError();
 }
 

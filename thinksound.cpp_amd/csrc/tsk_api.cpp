@@ -38,7 +38,7 @@ namespace {
 std::mutex g_mu;
 int g_device = -1;
 struct Workspace { void *ptr = nullptr; size_t size = 0; };
-Workspace g_ws[64];
+Workspace g_ws[64][2];
 }  // namespace
 
 int require_init() {
@@ -46,13 +46,14 @@ int require_init() {
     return TSK_OK;
 }
 
-int workspace(size_t bytes, void **out) {
+int workspace(size_t bytes, void **out, int slot) {
     std::lock_guard<std::mutex> lk(g_mu);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev < 0 || dev >= 64) return fail(TSK_ERR_INVALID_ARG, "device id %d out of range", dev);
-    Workspace &w = g_ws[dev];
+    if (slot < 0 || slot > 1) return fail(TSK_ERR_INVALID_ARG, "workspace slot %d", slot);
+    Workspace &w = g_ws[dev][slot];
     if (w.size < bytes) {
         // the old buffer may still be read by queued kernels of any stream
         e = hipDeviceSynchronize();
@@ -142,11 +143,12 @@ extern "C" int tsk_shutdown(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_device < 0) return TSK_OK;
     (void) hipDeviceSynchronize();
-    for (auto &w : g_ws) {
-        if (w.ptr) (void) hipFree(w.ptr);
-        w.ptr = nullptr;
-        w.size = 0;
-    }
+    for (auto &dev : g_ws)
+        for (auto &w : dev) {
+            if (w.ptr) (void) hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.size = 0;
+        }
     g_device = -1;
     return TSK_OK;
 }
@@ -206,9 +208,13 @@ int validate_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor 
             if (!aligned(a->data, 16)) return fail(TSK_ERR_ALIGN, "Q8_0_SPLIT data must be 16-byte aligned");
             break;
         case TSK_TYPE_F32:
+            // vec_dot type F32: the activations stay fp32
+            if (b->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "F32 weights need F32 b");
+            if (K % 8) return fail(TSK_ERR_SHAPE, "K=%lld must be a multiple of 8 for F32", (long long) K);
+            if ((rc = check_rows(a, "a", 16))) return rc;
+            break;
         case TSK_TYPE_F16:
-            return fail(TSK_ERR_UNSUPPORTED, "mul_mat with %s weights is not implemented on gfx950 (BF16, Q8_0 only)",
-                        a->type == TSK_TYPE_F32 ? "F32" : "F16");
+            return fail(TSK_ERR_UNSUPPORTED, "mul_mat with F16 weights is not implemented on gfx950 (F32, BF16, Q8_0)");
         default:
             return fail(TSK_ERR_TYPE, "weight type %d", a->type);
     }
@@ -272,6 +278,13 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
             p.w = a->data;
             p.ld_w = (int64_t) (a->nb[1] / 2);
             e = launch_gemm_bf16(p, s);
+        } else if (a->type == TSK_TYPE_F32) {
+            GemmProblem q;
+            memset(&q, 0, sizeof(q));
+            q.x = p.x; q.wf = (const float *) a->data; q.bias = p.bias; q.y = p.y;
+            q.ld_x = p.ld_x; q.ld_w = (int64_t) (a->nb[1] / 4); q.ld_y = p.ld_y;
+            q.M = p.M; q.N = p.N; q.K = p.K; q.splits = 1;
+            e = launch_gemm_f32(q, p.y_bf16, s);
         } else {
             char *act = ws + ((wbytes + 255) & ~(size_t) 255);
             int8_t *qx = (int8_t *) act;
@@ -542,6 +555,355 @@ extern "C" int tsk_q8_0_repack(const tsk_tensor *src, tsk_tensor *dst, tsk_strea
     return e == hipSuccess ? TSK_OK : hip_fail(e, "q8 repack launch");
 }
 
+// ------------------------------------------------------------------ convolution / SwiGLU
+namespace {
+
+int64_t conv_out_len(int64_t IW, int64_t KW, int s0, int p0, int d0) {
+    return (IW + 2 * (int64_t) p0 - (int64_t) d0 * (KW - 1) - 1) / s0 + 1;
+}
+
+bool contiguous(const tsk_tensor *t) {
+    size_t nb = (size_t) elt_size(t->type);
+    for (int i = 0; i < 4; ++i) {
+        if (t->ne[i] > 1 && t->nb[i] != nb) return false;
+        nb *= (size_t) t->ne[i];
+    }
+    return true;
+}
+
+// conv kernel [KW, IC, OC] read in place by the GEMM: rows of K = KW * IC in
+// kw-major order, 16-B aligned
+bool kw_major(const tsk_tensor *w) {
+    const size_t es = (size_t) elt_size(w->type);
+    return (w->ne[0] == 1 || w->nb[0] == (size_t) w->ne[1] * es) && (w->ne[1] == 1 || w->nb[1] == es) &&
+           (w->ne[2] == 1 || (w->nb[2] % 16 == 0 && w->nb[2] >= (size_t) (w->ne[0] * w->ne[1]) * es)) &&
+           aligned(w->data, 16);
+}
+
+int check_conv_weight(const tsk_tensor *w, const char *name) {
+    int rc;
+    if ((rc = check_tensor(w, name))) return rc;
+    if (w->type != TSK_TYPE_BF16 && w->type != TSK_TYPE_F32)
+        return fail(TSK_ERR_TYPE, "%s: conv kernels are BF16 or F32 (type %d)", name, w->type);
+    if (w->ne[3] != 1) return fail(TSK_ERR_SHAPE, "%s must be [KW, IC, OC]", name);
+    const size_t es = (size_t) elt_size(w->type);
+    for (int i = 0; i < 3; ++i)
+        if (w->nb[i] % es) return fail(TSK_ERR_STRIDE, "%s: nb[%d] not a multiple of the element size", name, i);
+    if (!aligned(w->data, es)) return fail(TSK_ERR_ALIGN, "%s: data alignment", name);
+    return TSK_OK;
+}
+
+// channels-fastest activations [C, S, B, 1]
+int check_conv_act(const tsk_tensor *t, const char *name) {
+    int rc;
+    if ((rc = check_tensor(t, name))) return rc;
+    if (t->type != TSK_TYPE_F32 && t->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "%s: F32 or BF16", name);
+    if (t->ne[3] != 1) return fail(TSK_ERR_SHAPE, "%s must be [C, S, B, 1]", name);
+    return check_rows(t, name, 16);
+}
+
+int validate_conv(const tsk_tensor *w, const tsk_tensor *bias, const tsk_tensor *x, int s0, int p0, int d0,
+                  const tsk_tensor *dst) {
+    int rc;
+    if ((rc = check_conv_weight(w, "w")) || (rc = check_conv_act(x, "x")) || (rc = check_conv_act(dst, "dst")))
+        return rc;
+    if (bias && (rc = check_tensor(bias, "bias"))) return rc;
+    const int64_t KW = w->ne[0], IC = w->ne[1], OC = w->ne[2];
+    if (x->ne[0] != IC) return fail(TSK_ERR_SHAPE, "x->ne[0]=%lld != IC=%lld", (long long) x->ne[0], (long long) IC);
+    if (IC % 8) return fail(TSK_ERR_SHAPE, "IC=%lld must be a multiple of 8", (long long) IC);
+    if (w->type == TSK_TYPE_F32 && x->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "F32 kernels need F32 x");
+    if (s0 < 1 || d0 < 1 || p0 < 0) return fail(TSK_ERR_INVALID_ARG, "stride %d, padding %d, dilation %d", s0, p0, d0);
+    const int64_t OW = conv_out_len(x->ne[1], KW, s0, p0, d0);
+    if (OW < 1) return fail(TSK_ERR_SHAPE, "output length %lld < 1", (long long) OW);
+    if (dst->ne[0] != OC || dst->ne[1] != OW || dst->ne[2] != x->ne[2])
+        return fail(TSK_ERR_SHAPE, "dst must be [OC=%lld, OW=%lld, B=%lld, 1]", (long long) OC, (long long) OW,
+                    (long long) x->ne[2]);
+    if (!rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "dst rows must be uniformly strided");
+    if (KW * IC > (1 << 30) || OW * x->ne[2] > (1 << 30) || x->ne[1] > (1 << 30))
+        return fail(TSK_ERR_SHAPE, "conv too large");
+    if (bias) {
+        if (bias->type != TSK_TYPE_F32 || bias->ne[0] != OC || bias->ne[1] * bias->ne[2] * bias->ne[3] != 1)
+            return fail(TSK_ERR_SHAPE, "bias must be F32 [OC]");
+        if (bias->nb[0] != 4 || !aligned(bias->data, 16)) return fail(TSK_ERR_ALIGN, "bias must be contiguous, 16-byte aligned");
+    }
+    return TSK_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t) 255; }
+
+// bytes a kw-major copy of w needs in scratch (0 if w is used in place)
+size_t conv_pack_bytes(const tsk_tensor *w) {
+    return kw_major(w) ? 0 : align256((size_t) (w->ne[0] * w->ne[1] * w->ne[2]) * (size_t) elt_size(w->type));
+}
+
+// the kw-major rows of w: in place, or packed into *scratch (advanced)
+int conv_weight_rows(const tsk_tensor *w, char **scratch, const void **rows, int64_t *ld, hipStream_t s) {
+    const int es = elt_size(w->type);
+    if (kw_major(w)) {
+        *rows = w->data;
+        *ld = w->ne[2] > 1 ? (int64_t) (w->nb[2] / es) : w->ne[0] * w->ne[1];
+        return TSK_OK;
+    }
+    hipError_t e = launch_conv_pack(w->data, es, (int64_t) (w->nb[0] / es), (int64_t) (w->nb[1] / es),
+                                    (int64_t) (w->nb[2] / es), (int) w->ne[0], (int) w->ne[1], (int) w->ne[2], *scratch, s);
+    if (e != hipSuccess) return hip_fail(e, "conv kernel pack");
+    *rows = *scratch;
+    *ld = w->ne[0] * w->ne[1];
+    *scratch += conv_pack_bytes(w);
+    return TSK_OK;
+}
+
+// one convolution GEMM (validated operands): x rows [B][IW][IC] (ld_x, batch
+// stride xb in elements), y rows [B * OW][OC] (ld_y); kw-major weight rows.
+// swiglu: w3 rows given -> y = silu(x * w) * (x * w3) (BF16 kernels only)
+int conv_gemm(int wtype, const void *wrows, const void *w3rows, int64_t ld_w, const float *bias, int KW, int IC, int OC,
+              const void *x, int x_f32, int64_t ld_x, int64_t xb, int IW, int B, int s0, int p0, int d0, void *y,
+              int y_bf16, int64_t ld_y, hipStream_t s) {
+    const int OW = (int) conv_out_len(IW, KW, s0, p0, d0);
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
+    q.x = x; q.bias = bias; q.y = y;
+    q.ld_x = ld_x; q.ld_w = ld_w; q.ld_y = ld_y;
+    q.x_group_stride = xb;
+    q.M = OC; q.N = B * OW; q.K = KW * IC; q.splits = 1;
+    q.conv_ic = IC; q.conv_iw = IW; q.conv_ow = OW; q.conv_s = s0; q.conv_p = p0; q.conv_d = d0;
+    hipError_t e;
+    if (wtype == TSK_TYPE_F32) {
+        if (w3rows) return fail(TSK_ERR_UNSUPPORTED, "fused SwiGLU needs BF16 kernels");
+        q.wf = (const float *) wrows;
+        e = launch_gemm_f32(q, y_bf16, s);
+    } else {
+        GemmGroup g;
+        memset(&g, 0, sizeof(g));
+        g.nprob = 1;
+        q.w = (const uint16_t *) wrows;
+        q.w3 = (const uint16_t *) w3rows;
+        g.p[0] = q;
+        const int epi = w3rows ? (y_bf16 ? EPI_SWIGLU_BF16 : EPI_SWIGLU_F32) : (y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32);
+        e = launch_gemm_group(g, x_f32 ? GEMM_X_F32 : 0, epi, s);
+    }
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "conv GEMM launch");
+}
+
+int validate_im2col(const tsk_tensor *kernel, const tsk_tensor *x, int s0, int p0, int d0, const tsk_tensor *dst) {
+    int rc;
+    if (!kernel) return fail(TSK_ERR_INVALID_ARG, "kernel is NULL");
+    for (int i = 0; i < 2; ++i)
+        if (kernel->ne[i] < 1) return fail(TSK_ERR_SHAPE, "kernel->ne[%d] < 1", i);
+    if ((rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (x->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "x must be F32");
+    if (dst->type != TSK_TYPE_F32 && dst->type != TSK_TYPE_F16 && dst->type != TSK_TYPE_BF16)
+        return fail(TSK_ERR_TYPE, "dst must be F32, F16 or BF16");
+    const int64_t KW = kernel->ne[0], IC = kernel->ne[1];
+    if (x->ne[1] != IC || x->ne[3] != 1) return fail(TSK_ERR_SHAPE, "x must be [IW, IC=%lld, N, 1]", (long long) IC);
+    if (s0 < 1 || d0 < 1 || p0 < 0) return fail(TSK_ERR_INVALID_ARG, "stride %d, padding %d, dilation %d", s0, p0, d0);
+    const int64_t OW = conv_out_len(x->ne[0], KW, s0, p0, d0);
+    if (OW < 1) return fail(TSK_ERR_SHAPE, "output length %lld < 1", (long long) OW);
+    if (dst->ne[0] != IC * KW || dst->ne[1] != OW || dst->ne[2] != x->ne[2] || dst->ne[3] != 1)
+        return fail(TSK_ERR_SHAPE, "dst must be [IC*KW=%lld, OW=%lld, N=%lld, 1]", (long long) (IC * KW), (long long) OW,
+                    (long long) x->ne[2]);
+    for (int i = 0; i < 3; ++i)
+        if (x->nb[i] % 4) return fail(TSK_ERR_STRIDE, "x->nb[%d] not a multiple of 4", i);
+    if (!aligned(x->data, 4)) return fail(TSK_ERR_ALIGN, "x data alignment");
+    const size_t es = (size_t) elt_size(dst->type);
+    if (dst->nb[0] != es) return fail(TSK_ERR_STRIDE, "dst rows must be contiguous");
+    if (!rows_uniform(dst) || dst->nb[1] % es) return fail(TSK_ERR_STRIDE, "dst rows must be uniformly strided");
+    if (!aligned(dst->data, es)) return fail(TSK_ERR_ALIGN, "dst data alignment");
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_im2col_1d(const tsk_tensor *kernel, const tsk_tensor *x, int s0, int p0, int d0, tsk_tensor *dst,
+                             tsk_stream stream) {
+    int rc = validate_im2col(kernel, x, s0, p0, d0, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    const int es = elt_size(dst->type);
+    const int et = dst->type;   // the kernel's element codes are the ggml type ids
+    const int64_t OW = dst->ne[1];
+    hipError_t e = launch_im2col_1d((const float *) x->data, (int64_t) (x->nb[0] / 4), (int64_t) (x->nb[1] / 4),
+                                    (int64_t) (x->nb[2] / 4), (int) x->ne[0], (int) x->ne[1], (int) kernel->ne[0],
+                                    (int) OW, (int) x->ne[2], s0, p0, d0, dst->data, et, (int64_t) (dst->nb[1] / es),
+                                    (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "im2col launch");
+}
+
+extern "C" int tsk_conv1d_pack_weight(const tsk_tensor *w, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_conv_weight(w, "w")) || (rc = check_conv_weight(dst, "dst"))) return rc;
+    if (!same_shape(w, dst) || dst->type != w->type) return fail(TSK_ERR_SHAPE, "dst must have w's shape and type");
+    const size_t es = (size_t) elt_size(w->type);
+    const int64_t KW = w->ne[0], IC = w->ne[1];
+    if ((KW > 1 && dst->nb[0] != (size_t) IC * es) || (IC > 1 && dst->nb[1] != es) ||
+        (w->ne[2] > 1 && dst->nb[2] != (size_t) (KW * IC) * es))
+        return fail(TSK_ERR_STRIDE, "dst must be kw-major: nb = [IC*es, es, KW*IC*es]");
+    if (!aligned(dst->data, 16)) return fail(TSK_ERR_ALIGN, "dst data must be 16-byte aligned");
+    if ((rc = require_init())) return rc;
+    hipError_t e = launch_conv_pack(w->data, (int) es, (int64_t) (w->nb[0] / es), (int64_t) (w->nb[1] / es),
+                                    (int64_t) (w->nb[2] / es), (int) KW, (int) IC, (int) w->ne[2], dst->data,
+                                    (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "conv kernel pack");
+}
+
+extern "C" int tsk_conv1d(const tsk_tensor *w, const tsk_tensor *bias, const tsk_tensor *x, int s0, int p0, int d0,
+                          tsk_tensor *dst, tsk_stream stream) {
+    int rc = validate_conv(w, bias, x, s0, p0, d0, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    char *ws = nullptr;
+    const size_t need = conv_pack_bytes(w);
+    if (need && (rc = workspace(need, (void **) &ws, 1))) return rc;
+    const void *wr = nullptr;
+    int64_t ld_w = 0;
+    if ((rc = conv_weight_rows(w, &ws, &wr, &ld_w, s))) return rc;
+    const int esx = elt_size(x->type), esy = elt_size(dst->type);
+    return conv_gemm(w->type, wr, nullptr, ld_w, bias ? (const float *) bias->data : nullptr, (int) w->ne[0],
+                     (int) w->ne[1], (int) w->ne[2], x->data, x->type == TSK_TYPE_F32, (int64_t) (x->nb[1] / esx),
+                     (int64_t) (x->nb[2] / esx), (int) x->ne[1], (int) x->ne[2], s0, p0, d0, dst->data,
+                     dst->type == TSK_TYPE_BF16, (int64_t) (dst->nb[1] / esy), s);
+}
+
+extern "C" int tsk_swiglu(const tsk_tensor *a, const tsk_tensor *b, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(a, "a")) || (rc = check_tensor(b, "b")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if (a->type != TSK_TYPE_F32 || b->type != TSK_TYPE_F32 || dst->type != TSK_TYPE_F32)
+        return fail(TSK_ERR_TYPE, "a, b and dst must be F32");
+    if (!same_shape(a, b) || !same_shape(a, dst)) return fail(TSK_ERR_SHAPE, "a, b and dst shapes differ");
+    if (!contiguous(a) || !contiguous(b) || !contiguous(dst)) return fail(TSK_ERR_STRIDE, "a, b and dst must be contiguous");
+    if ((rc = require_init())) return rc;
+    const int64_t n = a->ne[0] * a->ne[1] * a->ne[2] * a->ne[3];
+    hipError_t e = launch_silu_mul((const float *) a->data, (const float *) b->data, (float *) dst->data, n,
+                                   (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "swiglu launch");
+}
+
+namespace {
+
+// convmlp / mlp on validated operands: geometry of the two convolutions
+// (KW = 1, p = 0 for mlp), x rows [B][IW][IC], dst rows [B * OW2][OC]
+int swiglu_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, int KW1, int IC, int HID, int KW2,
+               int OC, int pad, const void *x, int x_f32, int64_t ld_x, int64_t xb, int IW, int B, void *y, int y_bf16,
+               int64_t ld_y, hipStream_t s) {
+    const int OW1 = (int) conv_out_len(IW, KW1, 1, pad, 1);
+    const int OW2 = (int) conv_out_len(OW1, KW2, 1, pad, 1);
+    if (OW1 < 1 || OW2 < 1) return fail(TSK_ERR_SHAPE, "output length < 1");
+    const bool bf16 = w1->type == TSK_TYPE_BF16;
+    // scratch: hidden [B * OW1][HID] (bf16 for BF16 kernels: the conversion
+    // w2's mul_mat applies), f32 h3 for F32 kernels, then packed kernels
+    const size_t nh = (size_t) B * OW1 * HID;
+    const size_t hbytes = align256(nh * (bf16 ? 2 : 4)), h3bytes = bf16 ? 0 : align256(nh * 4);
+    const size_t total = hbytes + h3bytes + conv_pack_bytes(w1) + conv_pack_bytes(w3) + conv_pack_bytes(w2);
+    char *ws = nullptr;
+    int rc;
+    if ((rc = workspace(total, (void **) &ws, 1))) return rc;
+    void *h = ws;
+    float *h3 = bf16 ? nullptr : (float *) (ws + hbytes);
+    char *pk = ws + hbytes + h3bytes;
+    const void *r1, *r3, *r2;
+    int64_t ld1, ld3, ld2;
+    if ((rc = conv_weight_rows(w1, &pk, &r1, &ld1, s)) || (rc = conv_weight_rows(w3, &pk, &r3, &ld3, s)) ||
+        (rc = conv_weight_rows(w2, &pk, &r2, &ld2, s)))
+        return rc;
+    if (ld1 != ld3) return fail(TSK_ERR_STRIDE, "w1 and w3 row strides differ");
+    if (bf16) {
+        if ((rc = conv_gemm(TSK_TYPE_BF16, r1, r3, ld1, nullptr, KW1, IC, HID, x, x_f32, ld_x, xb, IW, B, 1, pad, 1, h,
+                            1, HID, s)))
+            return rc;
+    } else {
+        if ((rc = conv_gemm(TSK_TYPE_F32, r1, nullptr, ld1, nullptr, KW1, IC, HID, x, 1, ld_x, xb, IW, B, 1, pad, 1, h,
+                            0, HID, s)) ||
+            (rc = conv_gemm(TSK_TYPE_F32, r3, nullptr, ld3, nullptr, KW1, IC, HID, x, 1, ld_x, xb, IW, B, 1, pad, 1, h3,
+                            0, HID, s)))
+            return rc;
+        hipError_t e = launch_silu_mul((const float *) h, h3, (float *) h, (int64_t) nh, s);
+        if (e != hipSuccess) return hip_fail(e, "swiglu launch");
+    }
+    return conv_gemm(w2->type, r2, nullptr, ld2, nullptr, KW2, HID, OC, h, !bf16, HID, (int64_t) OW1 * HID, OW1, B, 1,
+                     pad, 1, y, y_bf16, ld_y, s);
+}
+
+int check_mlp_types(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x) {
+    if (w1->type != w3->type || w1->type != w2->type) return fail(TSK_ERR_TYPE, "w1, w3 and w2 must share one type");
+    if (w1->type == TSK_TYPE_F32 && x->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "F32 kernels need F32 x");
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                                   const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_conv_weight(w1, "w1")) || (rc = check_conv_weight(w3, "w3")) || (rc = check_conv_weight(w2, "w2")) ||
+        (rc = check_conv_act(x, "x")) || (rc = check_conv_act(dst, "dst")))
+        return rc;
+    if ((rc = check_mlp_types(w1, w3, w2, x))) return rc;
+    if (!same_shape(w1, w3)) return fail(TSK_ERR_SHAPE, "w1 and w3 shapes differ");
+    const int64_t KW1 = w1->ne[0], IC = w1->ne[1], HID = w1->ne[2], KW2 = w2->ne[0], OC = w2->ne[2];
+    if (x->ne[0] != IC) return fail(TSK_ERR_SHAPE, "x->ne[0] != IC=%lld", (long long) IC);
+    if (w2->ne[1] != HID) return fail(TSK_ERR_SHAPE, "w2 must be [KW, HID=%lld, OC]", (long long) HID);
+    if (IC % 8 || HID % 8) return fail(TSK_ERR_SHAPE, "IC and HID must be multiples of 8");
+    const int64_t OW1 = conv_out_len(x->ne[1], KW1, 1, 1, 1), OW2 = conv_out_len(OW1, KW2, 1, 1, 1);
+    if (OW1 < 1 || OW2 < 1) return fail(TSK_ERR_SHAPE, "output length < 1");
+    if (dst->ne[0] != OC || dst->ne[1] != OW2 || dst->ne[2] != x->ne[2])
+        return fail(TSK_ERR_SHAPE, "dst must be [OC=%lld, OW=%lld, B=%lld, 1]", (long long) OC, (long long) OW2,
+                    (long long) x->ne[2]);
+    if (!rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "dst rows must be uniformly strided");
+    if (KW1 * IC > (1 << 30) || KW2 * HID > (1 << 30) || OW1 * x->ne[2] * HID > ((int64_t) 1 << 40))
+        return fail(TSK_ERR_SHAPE, "convmlp too large");
+    if ((rc = require_init())) return rc;
+    const int esx = elt_size(x->type), esy = elt_size(dst->type);
+    return swiglu_mlp(w1, w3, w2, (int) KW1, (int) IC, (int) HID, (int) KW2, (int) OC, 1, x->data,
+                      x->type == TSK_TYPE_F32, (int64_t) (x->nb[1] / esx), (int64_t) (x->nb[2] / esx), (int) x->ne[1],
+                      (int) x->ne[2], dst->data, dst->type == TSK_TYPE_BF16, (int64_t) (dst->nb[1] / esy),
+                      (hipStream_t) stream);
+}
+
+extern "C" int tsk_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x,
+                              tsk_tensor *dst, tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(w1, "w1")) || (rc = check_tensor(w3, "w3")) || (rc = check_tensor(w2, "w2")) ||
+        (rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst")))
+        return rc;
+    if ((rc = check_mlp_types(w1, w3, w2, x))) return rc;
+    for (const tsk_tensor *w : {w1, w3, w2}) {
+        if (w->type != TSK_TYPE_BF16 && w->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "weights must be BF16 or F32");
+        if (w->ne[2] != 1 || w->ne[3] != 1) return fail(TSK_ERR_SHAPE, "weights must be 2-D");
+        if ((rc = check_rows(w, "w", 16))) return rc;
+    }
+    if (!same_shape(w1, w3)) return fail(TSK_ERR_SHAPE, "w1 and w3 shapes differ");
+    const int64_t IC = w1->ne[0], HID = w1->ne[1], OC = w2->ne[1];
+    if (w2->ne[0] != HID) return fail(TSK_ERR_SHAPE, "w2 must be [HID=%lld, OC]", (long long) HID);
+    if (x->ne[0] != IC) return fail(TSK_ERR_SHAPE, "x->ne[0] != IC=%lld", (long long) IC);
+    if (IC % 8 || HID % 8) return fail(TSK_ERR_SHAPE, "IC and HID must be multiples of 8");
+    if (x->type != TSK_TYPE_F32 && x->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "x must be F32 or BF16");
+    if (dst->type != TSK_TYPE_F32 && dst->type != TSK_TYPE_BF16) return fail(TSK_ERR_TYPE, "dst must be F32 or BF16");
+    if (dst->ne[0] != OC || dst->ne[1] != x->ne[1] || dst->ne[2] != x->ne[2] || dst->ne[3] != x->ne[3])
+        return fail(TSK_ERR_SHAPE, "dst must be [OC=%lld, N, n2, n3] of x", (long long) OC);
+    if ((rc = check_rows(x, "x", 16)) || (rc = check_rows(dst, "dst", 16))) return rc;
+    if (!rows_uniform(x) || !rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "x and dst rows must be uniformly strided");
+    const int64_t N = x->ne[1] * x->ne[2] * x->ne[3];
+    if (N > (1 << 30)) return fail(TSK_ERR_SHAPE, "too many rows");
+    if ((rc = require_init())) return rc;
+    // a linear layer is the KW = 1, padding 0 convolution over one sequence of N rows
+    const int esx = elt_size(x->type), esy = elt_size(dst->type);
+    auto as_kernel = [](const tsk_tensor *w) {
+        // [K, M] rows -> the kw-major conv kernel [1, K, M]
+        const size_t es = (size_t) elt_size(w->type);
+        tsk_tensor k;
+        k.type = w->type;
+        k.ne[0] = 1; k.ne[1] = w->ne[0]; k.ne[2] = w->ne[1]; k.ne[3] = 1;
+        k.nb[0] = (size_t) w->ne[0] * es; k.nb[1] = es; k.nb[2] = w->nb[1]; k.nb[3] = w->nb[1] * (size_t) w->ne[1];
+        k.data = w->data;
+        return k;
+    };
+    const tsk_tensor k1 = as_kernel(w1), k3 = as_kernel(w3), k2 = as_kernel(w2);
+    return swiglu_mlp(&k1, &k3, &k2, 1, (int) IC, (int) HID, 1, (int) OC, 0, x->data, x->type == TSK_TYPE_F32,
+                      (int64_t) (x->nb[1] / esx), 0, (int) N, 1, dst->data, dst->type == TSK_TYPE_BF16,
+                      (int64_t) (dst->nb[1] / esy), (hipStream_t) stream);
+}
+
 // ------------------------------------------------------------------ supports_op
 extern "C" int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs, const tsk_tensor *dst) {
     // validation only: swap data pointers for a dummy aligned address
@@ -575,6 +937,12 @@ extern "C" int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs
             break;
         case TSK_OP_NORM:
             rc = check_unary(&t[0], &d);
+            break;
+        case TSK_OP_IM2COL:
+            rc = n_srcs >= 2 ? validate_im2col(&t[0], &t[1], 1, 1, 1, &d) : TSK_ERR_INVALID_ARG;
+            break;
+        case TSK_OP_CONV1D:
+            rc = n_srcs >= 2 ? validate_conv(&t[0], opt(2), &t[1], 1, 1, 1, &d) : TSK_ERR_INVALID_ARG;
             break;
         default:
             rc = TSK_ERR_UNSUPPORTED;

@@ -128,7 +128,11 @@ enum GroupEpi : int {
     EPI_STORE_BF16 = 11,  // y bf16 = acc + bias
     EPI_GELU_BF16 = 12,   // y bf16 = gelu_tanh(acc + bias)
     EPI_QKV = 13,         // acc + bias -> RMSNorm*w (q, k), RoPE, fp16 -> attention layout
-    EPI_PARTIAL = 14      // split-K: y f32 slice [split][N][M] = partial acc (no bias)
+    EPI_PARTIAL = 14,     // split-K: y f32 slice [split][N][M] = partial acc (no bias)
+    // SwiGLU over two weights sharing X: y[n, m] = silu(X W[m]) * (X W3[m]),
+    // no bias (convmlp / mlp, src/mmdit.cpp:39-52)
+    EPI_SWIGLU_F32 = 15,
+    EPI_SWIGLU_BF16 = 16
 };
 enum GemmFlags : int { GEMM_X_F32 = 1 };
 
@@ -143,6 +147,13 @@ struct GemmProblem {
     int64_t x_group_stride;
     int M, N, K;
     int splits;                    // K slices (EPI_PARTIAL), else 1
+    const uint16_t *w3;            // EPI_SWIGLU_*: the second weight (same layout as w)
+    const float *wf;               // launch_gemm_f32: f32 weights [M][K] row-major (ld_w)
+    // implicit im2col (conv_ic > 0): row n of X is output position ow = n % conv_ow
+    // of batch item b = n / conv_ow, and column k = kw * conv_ic + ic reads
+    // x[b * x_group_stride + (ow * conv_s + kw * conv_d - conv_p) * ld_x + ic],
+    // zero outside [0, conv_iw) (x_group_rows must be 0, conv_ic % 8 == 0)
+    int conv_ic, conv_iw, conv_ow, conv_s, conv_p, conv_d;
     // EPI_QKV: M = 3 * n_head * 64 with [q | k | v] head-major
     const float *qn_w, *kn_w;      // RMSNorm weights [64]
     uint16_t *q, *k;               // fp16 [B][n_head][Ntot][64]
@@ -249,6 +260,20 @@ struct GemvJob {
 hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K,
                             hipStream_t s);
 hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s);
+// ggml_im2col 1-D: dst row (n * OW + ow), column ic * KW + kw; dst_type an
+// Elt value (F32 / F16 / BF16); x element strides sp (position), sc
+// (channel), sn (batch)
+hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, int IW, int IC, int KW, int OW, int N,
+                           int s0, int p0, int d0, void *dst, int dst_type, int64_t ld, hipStream_t s);
+// conv kernel [KW, IC, OC] of es-byte elements (element strides s0..s2) ->
+// kw-major rows dst[oc][kw * IC + ic]
+hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
+                            hipStream_t s);
+// F32-weight GEMM (gemm_f32.hip): p.wf [M][K] (ld_w), f32 activations p.x
+// (plain rows or implicit im2col), y f32 or bf16 (+bias)
+hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s);
+// y = silu(a) * b, f32, n elements
+hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
 // y[n, m] = sum_k W[m, k] x[n, k] + bias[m]: bf16 row-major W, f32 x and y,
 // fp32 fma accumulation (the DiT's input and output projections)
 hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,

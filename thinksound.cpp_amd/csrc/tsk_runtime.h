@@ -11,8 +11,9 @@ int fail(int status, const char *fmt, ...);
 int hip_fail(hipError_t e, const char *what);
 // TSK_OK if tsk_init() was called
 int require_init();
-// device scratch of at least `bytes`, owned by the library (one per device);
-// growing it synchronises the device
-int workspace(size_t bytes, void **out);
+// device scratch of at least `bytes`, owned by the library (one per device and
+// slot: slot 0 serves single operators, slot 1 the composite entry points that
+// call them); growing it synchronises the device
+int workspace(size_t bytes, void **out, int slot = 0);
 
 }  // namespace tsk

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libtsk.so")
 F32, F16, Q8_0, I32, BF16, Q8_0_SPLIT = 0, 1, 8, 26, 30, 0x1008
 PREC_DEFAULT, PREC_F32 = 0, 10
 ROPE_NORMAL = 0
-OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_RMS_NORM_MUL, OP_ROPE_EXT, OP_NORM = 1, 2, 3, 4, 5
+OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_RMS_NORM_MUL, OP_ROPE_EXT, OP_NORM, OP_IM2COL, OP_CONV1D = 1, 2, 3, 4, 5, 6, 7
 STATUS = {0: "TSK_OK", -1: "TSK_ERR_INVALID_ARG", -2: "TSK_ERR_TYPE", -3: "TSK_ERR_SHAPE",
           -4: "TSK_ERR_STRIDE", -5: "TSK_ERR_ALIGN", -6: "TSK_ERR_UNSUPPORTED",
           -7: "TSK_ERR_NOT_INIT", -8: "TSK_ERR_HIP", -9: "TSK_ERR_NOMEM"}
@@ -75,6 +75,12 @@ def load():
         "tsk_q8_0_repack": ([P, P, vp], i),
         "tsk_q8_0_split_nbytes": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
         "tsk_supports_op": ([i, ctypes.POINTER(P), i, P], i),
+        "tsk_im2col_1d": ([P, P, i, i, i, P, vp], i),
+        "tsk_conv1d": ([P, P, P, i, i, i, P, vp], i),
+        "tsk_conv1d_pack_weight": ([P, P, vp], i),
+        "tsk_swiglu": ([P, P, P, vp], i),
+        "tsk_conv_mlp_swiglu": ([P, P, P, P, P, vp], i),
+        "tsk_mlp_swiglu": ([P, P, P, P, P, vp], i),
         "tsk_t5_default_config": ([ctypes.POINTER(T5Config)], None),
         "tsk_t5_create": ([ctypes.POINTER(T5Config), ctypes.POINTER(vp)], i),
         "tsk_t5_destroy": ([vp], None),
@@ -448,6 +454,84 @@ def q8_0_dequantize(x):
     out = DeviceArray((rows, K), "f32")
     dd = desc(out)
     check(load().tsk_q8_0_dequantize(ctypes.byref(dx), ctypes.byref(dd), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- convolution / SwiGLU
+def conv_len(iw, kw, s0=1, p0=1, d0=1):
+    return (iw + 2 * p0 - d0 * (kw - 1) - 1) // s0 + 1
+
+
+def im2col_1d(kernel_shape, x, s0=1, p0=1, d0=1, out_dtype="f32"):
+    """ggml_im2col 1-D: kernel_shape (OC, IC, KW); x (N, IC, IW) f32 (any
+    strides, e.g. a transposed view) -> (N, OW, IC*KW)."""
+    init()
+    OC, IC, KW = kernel_shape
+    N, _, IW = x.shape
+    out = DeviceArray((N, conv_len(IW, KW, s0, p0, d0), IC * KW), out_dtype)
+    k = TskTensor()
+    k.type = F32
+    k.ne[0], k.ne[1], k.ne[2], k.ne[3] = KW, IC, OC, 1
+    dx, dd = desc(x), desc(out)
+    check(load().tsk_im2col_1d(ctypes.byref(k), ctypes.byref(dx), s0, p0, d0, ctypes.byref(dd), _stream()))
+    return out
+
+
+def conv1d_pack_weight(w):
+    """(OC, IC, KW) kernel (ggml ne [KW, IC, OC]) -> a copy laid out kw-major,
+    returned as an (OC, IC, KW) view with element strides (KW*IC, 1, IC)."""
+    init()
+    OC, IC, KW = w.shape
+    buf = DeviceArray((OC * KW * IC,), w.dtype)
+    out = buf.view(0, (OC, IC, KW), (KW * IC, 1, IC))
+    dw, dd = desc(w), desc(out)
+    check(load().tsk_conv1d_pack_weight(ctypes.byref(dw), ctypes.byref(dd), _stream()))
+    return out
+
+
+def conv1d(w, x, bias=None, s0=1, p0=1, d0=1, out=None, out_dtype="f32"):
+    """conv_cl: w (OC, IC, KW) kernel, x (B, IW, IC) channels fastest -> (B, OW, OC)."""
+    init()
+    OC, IC, KW = w.shape
+    B, IW, _ = x.shape
+    if out is None:
+        out = DeviceArray((B, conv_len(IW, KW, s0, p0, d0), OC), out_dtype)
+    dw, dx, dd = desc(w), desc(x), desc(out)
+    db = desc(bias) if bias is not None else None
+    check(load().tsk_conv1d(ctypes.byref(dw), _ref(db), ctypes.byref(dx), s0, p0, d0, ctypes.byref(dd), _stream()))
+    return out
+
+
+def swiglu(a, b, out=None):
+    """ggml_mul(ggml_silu(a), b), f32."""
+    init()
+    out = DeviceArray(a.shape, "f32") if out is None else out
+    da, db, dd = desc(a), desc(b), desc(out)
+    check(load().tsk_swiglu(ctypes.byref(da), ctypes.byref(db), ctypes.byref(dd), _stream()))
+    return out
+
+
+def conv_mlp_swiglu(w1, w3, w2, x, out=None, out_dtype="f32"):
+    """convmlp: kernels (HID, IC, KW), (HID, IC, KW), (OC, HID, KW); x (B, IW, IC) -> (B, OW, OC)."""
+    init()
+    B, IW, _ = x.shape
+    if out is None:
+        ow = conv_len(conv_len(IW, w1.shape[2]), w2.shape[2])
+        out = DeviceArray((B, ow, w2.shape[0]), out_dtype)
+    d1, d3, d2, dx, dd = desc(w1), desc(w3), desc(w2), desc(x), desc(out)
+    check(load().tsk_conv_mlp_swiglu(ctypes.byref(d1), ctypes.byref(d3), ctypes.byref(d2), ctypes.byref(dx),
+                                     ctypes.byref(dd), _stream()))
+    return out
+
+
+def mlp_swiglu(w1, w3, w2, x, out=None, out_dtype="f32"):
+    """mlp: weights (HID, IC), (HID, IC), (OC, HID); x (..., IC) -> (..., OC)."""
+    init()
+    if out is None:
+        out = DeviceArray(tuple(x.shape[:-1]) + (w2.shape[0],), out_dtype)
+    d1, d3, d2, dx, dd = desc(w1), desc(w3), desc(w2), desc(x), desc(out)
+    check(load().tsk_mlp_swiglu(ctypes.byref(d1), ctypes.byref(d3), ctypes.byref(d2), ctypes.byref(dx),
+                                ctypes.byref(dd), _stream()))
     return out
 
 
