@@ -180,9 +180,10 @@ def main():
         return {"tflops": round(tf, 2), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                 "avg_us": round(ms * 1e3 / n, 3), "launches_per_step": n // ms_steps}
 
-    breakdown = {r: {"ms_per_step": round(v[0] / args.steps, 4), "launches_per_step": v[1] // args.steps,
-                     "tflops": round(v[2] / (v[0] / 1e3) / 1e12, 2) if v[0] > 0 else None}
-                 for r, v in roles9.items()}
+    def breakdown(roles, steps):
+        return {r: {"ms_per_step": round(v[0] / steps, 4), "launches_per_step": v[1] // steps,
+                    "tflops": round(v[2] / (v[0] / 1e3) / 1e12, 2) if v[0] > 0 else None}
+                for r, v in roles.items()}
     out = {
         "metric": "DiT flow steps/s at 9 s (CFG b=2)",
         "value": round(1000.0 / ms_plain, 2),
@@ -204,7 +205,8 @@ def main():
         "steps_per_s_30s": round(1000.0 / ms30, 2),
         "sample_24_steps_30s": sample30,
         "ms_per_step_with_kernel_events": round(ms_timed, 4),
-        "breakdown_9s": breakdown,
+        "breakdown_9s": breakdown(roles9, args.steps),
+        "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9

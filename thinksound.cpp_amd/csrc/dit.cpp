@@ -92,10 +92,9 @@ struct tsk_dit {
     int njobs = 0, max_job_m = 0;
     float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
     float *rope_cs = nullptr;       // RoPE (cos, sin) [max_latent][head_dim] of the latent positions
-    // block GEMM tile shape per projection (qkv, out, fc1, fc2), launch_gemm_ks cfg:
-    // 64 x 64 register-prefetch tiles for the QKV and out projections, 128 x 64
-    // LDS-ring tiles for the MLP, measured on MI355X at 194 .. 646 latent tokens
-    int gemm_cfg[4] = {8, 8, 4, 4};
+    // block GEMM tile shape per projection (qkv, out, fc1, fc2): a launch_gemm_ks
+    // cfg, or 0 for the shape rule of gemm_cfg_for() (TSK_GEMM_CFG overrides)
+    int gemm_cfg[4] = {0, 0, 0, 0};
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
     // second stream for the adaLN GEMVs of the later blocks (HBM-bound) while
@@ -261,7 +260,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     // (one hex digit each, 0 = the launcher's choice)
     if (const char *gc = getenv("TSK_GEMM_CFG"))
         for (int i = 0; i < 4 && gc[i]; ++i)
-            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'f' ? gc[i] - 'a' + 10 : 0;
+            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10 : 0;
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -509,6 +508,19 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
     return hipcheck(launch_ln_group(g, st), "ln_group");
 }
 
+// Block GEMM tile shape by projection and activation rows of the larger
+// stream, measured on MI355X over 194 .. 646 latent tokens (B = 2): 64 x 64
+// cooperative tiles (cfg 22) while the token count leaves 128-row tiles too
+// few, 128 x 64 cooperative tiles (cfg 12) beyond; fc2 below that keeps the
+// 128 x 64 K-split LDS-ring tiles (cfg 4). The tile shape does not change
+// any summation order.
+int gemm_cfg_for(const tsk_dit *d, int role, int rows) {
+    if (d->gemm_cfg[role]) return d->gemm_cfg[role];
+    const int big = role <= 1 ? 1100 : 550;   // qkv, out : fc1, fc2
+    if (rows >= big) return 12;
+    return role == 3 ? 4 : 22;
+}
+
 int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden;
@@ -532,7 +544,7 @@ int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         by += 2.0 * 3 * H * H + 2.0 * rows * H + 2.0 * rows * 3 * H + 12.0 * H;
     }
     Timed tm(d, TSK_ROLE_QKV, fl, by, st);
-    return hipcheck(launch_gemm_ks(g, EPI_QKV, d->gemm_cfg[0], st), "qkv gemm");
+    return hipcheck(launch_gemm_ks(g, EPI_QKV, gemm_cfg_for(d, 0, B * r[0].S), st), "qkv gemm");
 }
 
 // linear1 on the attention output (o rows of each stream: o[b][tok_off + s]),
@@ -559,7 +571,7 @@ int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     }
     if (!g.nprob) return TSK_OK;
     Timed tm(d, TSK_ROLE_OUT, fl, by, st);
-    return hipcheck(launch_gemm_ks(g, EPI_PARTIAL, d->gemm_cfg[1], st), "linear1 gemm");
+    return hipcheck(launch_gemm_ks(g, EPI_PARTIAL, gemm_cfg_for(d, 1, B * r[0].S), st), "linear1 gemm");
 }
 
 int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
@@ -587,11 +599,11 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     int rc;
     {
         Timed tm(d, TSK_ROLE_FC1, fl, by1, st);
-        rc = hipcheck(launch_gemm_ks(g1, EPI_GELU_BF16, d->gemm_cfg[2], st), "fc1 gemm");
+        rc = hipcheck(launch_gemm_ks(g1, EPI_GELU_BF16, gemm_cfg_for(d, 2, B * r[0].S), st), "fc1 gemm");
     }
     if (rc) return rc;
     Timed tm(d, TSK_ROLE_FC2, fl, by2, st);
-    return hipcheck(launch_gemm_ks(g2, EPI_PARTIAL, d->gemm_cfg[3], st), "fc2 gemm");
+    return hipcheck(launch_gemm_ks(g2, EPI_PARTIAL, gemm_cfg_for(d, 3, B * r[0].S), st), "fc2 gemm");
 }
 
 // Attention over the concatenated q/k/vt of the streams in r[0..ns). q was

@@ -21,6 +21,14 @@
 // order of the v_mfma_f32_16x16x32_bf16 operands, so every fragment is one
 // conflict-free ds_read_b128 at lane * 16.
 //
+// Cooperative tiles (MODE_COOP, for token counts that fill the chip with
+// 128-token tiles): the four waves split the output tile 2 x 2 instead and
+// share one LDS ring of 32-wide stages, each wave loading a quarter of every
+// stage's fragments; a stage is consumed after every wave's loads of it have
+// landed (own load counter, then one barrier per stage). Each wave then
+// reads (TM + TN) / 2 fragments for TM * TN / 4 MFMAs, half the LDS traffic
+// per MFMA of the K-split tiles, and no partial tiles need summing.
+//
 // The four partial tiles are summed through LDS in wave order 0, 1, 2, 3:
 // every output element is summed in the same order whatever the launch
 // shape, the token count or its tile position, so batch rows are
@@ -101,17 +109,31 @@ __device__ __forceinline__ int64_t x_row(const GemmProblem &p, int n) {
                           : (int64_t) n * p.ld_x;
 }
 
-template <int TM, int TN, int R, bool DIRECT>
+// main-loop modes
+enum : int {
+    MODE_RING = 0,     // K-split waves, private LDS rings of direct global->LDS loads
+    MODE_DIRECT = 1,   // K-split waves, operands straight into registers
+    MODE_COOP = 2      // 2 x 2 waves over the tile, one shared LDS ring
+};
+
+template <int TM, int TN, int R, int MODE, int KH = 1>
 constexpr size_t lds_bytes() {
-    constexpr size_t ring = DIRECT ? 0 : (size_t) 4 * R * (TM + TN) * 1024;
-    constexpr size_t red = (size_t) 4 * (16 * (TN < 4 ? TN : 4)) * (16 * TM + 4) * 4;
+    constexpr size_t ring = MODE == MODE_DIRECT ? 0
+                          : MODE == MODE_COOP   ? (size_t) R * KH * (TM + TN) * 1024
+                                                : (size_t) 4 * R * (TM + TN) * 1024;
+    constexpr size_t red = MODE == MODE_COOP ? (size_t) (16 * TN) * (16 * TM + 4) * 4
+                                             : (size_t) 4 * (16 * (TN < 4 ? TN : 4)) * (16 * TM + 4) * 4;
     return ring > red ? ring : red;
 }
 
-template <int TM, int TN, int R, bool DIRECT, int EPI>
+template <int TM, int TN, int R, int MODE, int EPI, int KH = 1>
 __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = L * 1024;
+    constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = KH * L * 1024;
+    constexpr bool COOP = MODE == MODE_COOP, DIRECT = MODE == MODE_DIRECT;
+    static_assert(!COOP || (TM % 2 == 0 && TN % 2 == 0 && L % 4 == 0), "cooperative tile shape");
+    static_assert(COOP || KH == 1, "KH: 32-wide k tiles per cooperative stage");
+    constexpr int TMW = COOP ? TM / 2 : TM, TNW = COOP ? TN / 2 : TN;   // 16x16 tiles per wave
 
     Coord tc;
     if (!decode(g, tc)) return;
@@ -122,7 +144,8 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     const int KT = p.K >> 5;                                  // 32-wide k tiles
     const int kt0 = tc.split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
     const int nst = kt1 - kt0;
-    const int my_n = nst > wave ? (nst - wave + 3) >> 2 : 0;  // stages of this wave
+    const int my_n = COOP ? nst / KH : nst > wave ? (nst - wave + 3) >> 2 : 0;   // stages this wave computes
+    const int wm = COOP ? (wave & 1) : 0, wn = COOP ? (wave >> 1) : 0;       // cooperative quadrant
 
     // A: tile (rb, kt) of the tiled weights at (rb * KT + kt) * 512 elements,
     // this lane's 16 bytes at lane * 8. Row blocks past M read the last one
@@ -150,13 +173,57 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
             g2l16(bsrc[j] + kt * 32, dst + (TM + j) * 1024);
     };
 
-    f32x4 acc[TM][TN];
+    f32x4 acc[TMW][TNW];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TMW; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+        for (int j = 0; j < TNW; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-    if constexpr (DIRECT) {
+    if constexpr (COOP) {
+        // shared ring of R stages of KH 32-wide k tiles (the launcher checks
+        // that KH divides the tiles of every K range); wave w loads fragments
+        // w, w + 4, ... of each stage, fragment h * L + f being tile h's A
+        // fragment f (f < TM) or B fragment f - TM
+        constexpr int LW = KH * L / 4;
+        const int ns = my_n;
+        auto cissue = [&](int t, int slot) {
+            uint8_t *dst = lds + slot * STAGE;
+#pragma unroll
+            for (int q = 0; q < LW; ++q) {
+                const int fq = wave + 4 * q, h = fq / L, f = fq % L;
+                const int kt = kt0 + t * KH + h;
+                if (f < TM) g2l16(wl + aoff[f] + (int64_t) kt * 512, dst + fq * 1024);
+                else g2l16(bsrc[f - TM] + kt * 32, dst + fq * 1024);
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < R - 1; ++s)
+            if (s < ns) cissue(s, s);
+        int slot = 0;
+        for (int t = 0; t < ns; ++t) {
+            // this wave's loads of stage t have landed; the barrier makes every
+            // wave's visible and ends every wave's reads of stage t - 1, whose
+            // slot is refilled next
+            wait_stages<LW, R - 1>(min(ns - 1 - t, R - 2));
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (t + R - 1 < ns) cissue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
+#pragma unroll
+            for (int h = 0; h < KH; ++h) {
+                const uint8_t *src = lds + slot * STAGE + h * (L * 1024) + lane * 16;
+                bf16x8 a[TMW], b[TNW];
+#pragma unroll
+                for (int i = 0; i < TMW; ++i) a[i] = *(const bf16x8 *) (src + (wm * TMW + i) * 1024);
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) b[j] = *(const bf16x8 *) (src + (TM + wn * TNW + j) * 1024);
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TNW; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+            slot = slot + 1 == R ? 0 : slot + 1;
+        }
+    } else if constexpr (DIRECT) {
         // operands straight into registers, R stages in flight. The stage
         // count of every wave is a multiple of R (checked by the launcher), so
         // every refill below is a real stage and the loads are unconditional:
@@ -216,14 +283,22 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     }
 
     // ---- sum the four waves' partial tiles, 64 tokens at a time: red[w][token][feature]
+    // (cooperative tiles: each wave stores its quadrant of one [token][feature] tile)
     constexpr int LDY = BM + 4;
-    constexpr int TNC = TN < 4 ? TN : 4, BNC = 16 * TNC;
+    constexpr int TNC = COOP ? TN : TN < 4 ? TN : 4, BNC = 16 * TNC;
     float *red = (float *) lds;
 #pragma unroll
     for (int c = 0; c < TN / TNC; ++c) {
     const int bn0c = bn0 + c * BNC;
     __syncthreads();                                          // rings drained / previous chunk consumed
-    {
+    if constexpr (COOP) {
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+                *(f32x4 *) &red[(16 * (wn * TNW + j) + (lane & 15)) * LDY + 16 * (wm * TMW + i) + 4 * (lane >> 4)] =
+                    acc[i][j];
+    } else {
         float *mine = red + wave * (BNC * LDY);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -235,10 +310,12 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     auto sum4 = [&](int nl, int ml) -> f32x4 {
         const float *r0 = red + nl * LDY + ml;
         f32x4 v = *(const f32x4 *) r0;
+        if constexpr (!COOP) {
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            const f32x4 u = *(const f32x4 *) (r0 + w * (BNC * LDY));
-            v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+            for (int w = 1; w < 4; ++w) {
+                const f32x4 u = *(const f32x4 *) (r0 + w * (BNC * LDY));
+                v = f32x4{v[0] + u[0], v[1] + u[1], v[2] + u[2], v[3] + u[3]};
+            }
         }
         return v;
     };
@@ -326,7 +403,7 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     }   // token chunk
 }
 
-template <int TM, int TN, int R, bool DIRECT, int EPI>
+template <int TM, int TN, int R, int MODE, int EPI, int KH>
 hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     constexpr int BM = 16 * TM, BN = 16 * TN;
     int nblocks = 0;
@@ -335,12 +412,13 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
         p.tiles_m = (p.M + BM - 1) / BM;
         p.tiles_n = (p.N + BN - 1) / BN;
         p.kt_split = (p.K / 32 + p.splits - 1) / p.splits;
+        if (KH > 1 && ((p.K / 32) % p.splits || p.kt_split % KH)) return hipErrorInvalidValue;
         p.block_begin = (nblocks + 7) & ~7;
         nblocks = p.block_begin + p.tiles_m * p.tiles_n * p.splits;
     }
-    constexpr size_t lds = lds_bytes<TM, TN, R, DIRECT>();
+    constexpr size_t lds = lds_bytes<TM, TN, R, MODE, KH>();
     static_assert(lds <= 160 * 1024, "LDS");
-    auto kern = gemm_ks_kernel<TM, TN, R, DIRECT, EPI>;
+    auto kern = gemm_ks_kernel<TM, TN, R, MODE, EPI, KH>;
     static bool attr = false;   // dynamic LDS above 64 KiB is opted in once per kernel
     if (!attr) {
         if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
@@ -352,14 +430,14 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int TM, int TN, int R, bool DIRECT = false>
+template <int TM, int TN, int R, int MODE = MODE_RING, int KH = 1>
 hipError_t ks_epi(GemmGroup &g, int epi, hipStream_t s) {
     switch (epi) {
-        case EPI_STORE_F32: return ks_launch<TM, TN, R, DIRECT, EPI_STORE_F32>(g, s);
-        case EPI_STORE_BF16: return ks_launch<TM, TN, R, DIRECT, EPI_STORE_BF16>(g, s);
-        case EPI_GELU_BF16: return ks_launch<TM, TN, R, DIRECT, EPI_GELU_BF16>(g, s);
-        case EPI_QKV: return ks_launch<TM, TN, R, DIRECT, EPI_QKV>(g, s);
-        case EPI_PARTIAL: return ks_launch<TM, TN, R, DIRECT, EPI_PARTIAL>(g, s);
+        case EPI_STORE_F32: return ks_launch<TM, TN, R, MODE, EPI_STORE_F32, KH>(g, s);
+        case EPI_STORE_BF16: return ks_launch<TM, TN, R, MODE, EPI_STORE_BF16, KH>(g, s);
+        case EPI_GELU_BF16: return ks_launch<TM, TN, R, MODE, EPI_GELU_BF16, KH>(g, s);
+        case EPI_QKV: return ks_launch<TM, TN, R, MODE, EPI_QKV, KH>(g, s);
+        case EPI_PARTIAL: return ks_launch<TM, TN, R, MODE, EPI_PARTIAL, KH>(g, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -387,7 +465,7 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     }
     // 128 x 64 tiles by default; 64 x 64 when that leaves most CUs idle
     if (!cfg) cfg = gemm_ks_tiles(g, 128, 64) >= 160 ? 1 : 2;
-    if (cfg >= 6) {
+    if (cfg >= 6 && cfg <= 10) {
         // register prefetch: every wave's stage count a multiple of the depth
         const int depth = cfg == 7 || cfg == 8 || cfg == 10 ? 2 : 4;
         for (int i = 0; i < g.nprob; ++i) {
@@ -397,7 +475,11 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         }
     }
     for (int i = 0; i < g.nprob; ++i)
-        if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 ? 64 : 128) && epi == EPI_QKV)
+        if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
+                                cfg == 22 || cfg == 23
+                            ? 64
+                            : 128) &&
+            epi == EPI_QKV)
             return hipErrorInvalidValue;
     switch (cfg) {
         case 1: return ks_epi<8, 4, 3>(g, epi, s);   // 128 x 64, 3 stages
@@ -405,11 +487,24 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         case 3: return ks_epi<4, 8, 2>(g, epi, s);   // 64 x 128, 2 stages
         case 4: return ks_epi<8, 4, 2>(g, epi, s);   // 128 x 64, 2 stages
         case 5: return ks_epi<4, 4, 4>(g, epi, s);   // 64 x 64, 4 stages
-        case 6: return ks_epi<4, 4, 4, true>(g, epi, s);   // 64 x 64, register prefetch 4 stages
-        case 7: return ks_epi<8, 4, 2, true>(g, epi, s);   // 128 x 64, register prefetch 2 stages
-        case 8: return ks_epi<4, 4, 2, true>(g, epi, s);   // 64 x 64, register prefetch 2 stages
-        case 9: return ks_epi<8, 4, 4, true>(g, epi, s);   // 128 x 64, register prefetch 4 stages
-        case 10: return ks_epi<8, 8, 2, true>(g, epi, s);  // 128 x 128, register prefetch 2 stages
+        case 6: return ks_epi<4, 4, 4, MODE_DIRECT>(g, epi, s);   // 64 x 64, register prefetch 4 stages
+        case 7: return ks_epi<8, 4, 2, MODE_DIRECT>(g, epi, s);   // 128 x 64, register prefetch 2 stages
+        case 8: return ks_epi<4, 4, 2, MODE_DIRECT>(g, epi, s);   // 64 x 64, register prefetch 2 stages
+        case 9: return ks_epi<8, 4, 4, MODE_DIRECT>(g, epi, s);   // 128 x 64, register prefetch 4 stages
+        case 10: return ks_epi<8, 8, 2, MODE_DIRECT>(g, epi, s);  // 128 x 128, register prefetch 2 stages
+        case 11: return ks_epi<8, 8, 4, MODE_COOP>(g, epi, s);    // 128 x 128 cooperative, 4 stages
+        case 12: return ks_epi<8, 4, 4, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 4 stages
+        case 13: return ks_epi<4, 8, 4, MODE_COOP>(g, epi, s);    // 64 x 128 cooperative, 4 stages
+        case 14: return ks_epi<8, 8, 3, MODE_COOP>(g, epi, s);    // 128 x 128 cooperative, 3 stages
+        case 15: return ks_epi<8, 4, 3, MODE_COOP, 2>(g, epi, s); // 128 x 64 cooperative, 3 stages of 64 k
+        case 16: return ks_epi<8, 4, 2, MODE_COOP, 2>(g, epi, s); // 128 x 64 cooperative, 2 stages of 64 k
+        case 17: return ks_epi<8, 8, 2, MODE_COOP, 2>(g, epi, s); // 128 x 128 cooperative, 2 stages of 64 k
+        case 18: return ks_epi<4, 8, 3, MODE_COOP, 2>(g, epi, s); // 64 x 128 cooperative, 3 stages of 64 k
+        case 19: return ks_epi<8, 4, 6, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 6 stages
+        case 20: return ks_epi<8, 4, 3, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 3 stages
+        case 21: return ks_epi<8, 4, 2, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 2 stages
+        case 22: return ks_epi<4, 4, 4, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 4 stages
+        case 23: return ks_epi<4, 4, 3, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 3 stages
         default: return hipErrorInvalidValue;
     }
 }
