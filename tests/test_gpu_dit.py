@@ -107,3 +107,32 @@ def test_sampler_cfg(env):
     print(f"sampler: flow0 {e0:.3e}, latent {ex:.3e}", flush=True)
     assert e0 <= 5e-3 and ex <= 5e-3
     dit.close()
+
+
+@pytest.mark.parametrize("steps", [4, 40])
+def test_sampler_schedule_is_bit_exact(env, steps):
+    """The conditioning schedule (every step's adaLN outputs computed before the
+    first step, 32 steps per batched pass) changes no bit against computing
+    them inside each step as the reference does (TSK_DIT_SCHED=0); 40 steps
+    span two 32-step passes."""
+    import os
+    tsk, orc = env
+    cfg = tsk.dit_config(depth=2, fused_depth=1, max_latent=64)
+    dit = tsk.Dit(cfg)
+    for k, v in tsk.synthetic_weights(dit.tensors(), seed=77).items():
+        dit.set_tensor(k, v)
+    rng = np.random.default_rng(5)
+    noise = rng.standard_normal((33, 64), dtype=np.float32)
+    tc = rng.standard_normal((77, 1024), dtype=np.float32)
+    tu = rng.standard_normal((77, 1024), dtype=np.float32)
+    x1, f1 = dit.sample(noise, tc, tu, steps=steps, cfg_scale=4.0)
+    os.environ["TSK_DIT_SCHED"] = "0"
+    try:
+        x0, f0 = dit.sample(noise, tc, tu, steps=steps, cfg_scale=4.0)
+    finally:
+        del os.environ["TSK_DIT_SCHED"]
+    assert np.array_equal(f1, f0) and np.array_equal(x1, x0)
+    # and the schedule is rebuilt for a different step count on the same model
+    x2, _ = dit.sample(noise, tc, tu, steps=3, cfg_scale=4.0)
+    assert np.isfinite(x2).all() and not np.array_equal(x2, x1)
+    dit.close()

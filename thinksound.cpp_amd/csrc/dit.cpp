@@ -64,6 +64,7 @@ struct StreamW {           // one MMDitSingleBlock's weights
     bool pre_only;
     float *mod;            // [max_batch][nmod * H] adaLN output
     int nmod;
+    size_t sched_off;      // offset of this block's modulations in a schedule row
     int qn_idx, kn_idx;    // tensor indices of the q / k RMSNorm weights
 };
 
@@ -81,6 +82,17 @@ struct tsk_dit {
     float *temb = nullptr, *tmp_c = nullptr, *cvec = nullptr;
     float *mods = nullptr;
     float *final_mod = nullptr;     // [max_batch][2H] final-layer adaLN output
+    // sampler conditioning schedule: every step's adaLN outputs, one row of
+    // sched_row floats per step (blocks at StreamW::sched_off, final layer at
+    // sched_final), computed in one batched pass before the first step
+    float *sched = nullptr;
+    size_t sched_cap = 0, sched_row = 0, sched_final = 0;
+    float *sched_act = nullptr;       // [3][32][H]: temb, t_embed hidden, silu(cond) of 32 steps
+    GemvJob *sched_jobs = nullptr;    // device job tables, one per 32-step chunk
+    int sched_jobs_cap = 0;
+    std::vector<GemvJob> jobs_host;   // the adaLN job table (blocks, final layer, t_embed.0, .2)
+    std::vector<size_t> jobs_sched_off;   // schedule-row offset of each adaLN job's output
+    const float *cur_sched = nullptr; // the schedule row of the running step (nullptr: computed per call)
     // bf16 activations: xn [rows][H] (LN outputs), h [rows][F] (GELU outputs),
     // latent rows first, text rows from the fixed offset max_batch * max_latent;
     // fp16 attention operands q/k [B][n_head][Ntot][64], V transposed
@@ -238,7 +250,8 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     if (d->ev_fork) (void) hipEventDestroy(d->ev_fork);
     if (d->ev_join) (void) hipEventDestroy(d->ev_join);
     if (d->side) (void) hipStreamDestroy(d->side);
-    void *bufs[] = {d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
+    void *bufs[] = {d->sched, d->sched_act, d->sched_jobs,
+                    d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
                     d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
     for (void *b : bufs)
@@ -345,9 +358,13 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     // per-stream weights and adaLN job table
     std::vector<GemvJob> jobs;
     float *mp = d->mods;
+    size_t soff = 0;
     auto mk = [&](StreamW s) {
         s.mod = mp;
         mp += (size_t) B * 6 * H;
+        s.sched_off = soff;
+        d->jobs_sched_off.push_back(soff);
+        soff += (size_t) 6 * H;
         GemvJob j;
         j.w = s.ada_w; j.bias = s.ada_b; j.x = d->cvec; j.out = s.mod; j.M = s.nmod * H;
         j.silu_out = 0; j.ld_out = (int64_t) s.nmod * H;
@@ -365,6 +382,9 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     fj.x = d->cvec;
     fj.out = mp;
     d->final_mod = mp;
+    d->sched_final = soff;
+    d->sched_row = soff + (size_t) 2 * H;
+    d->jobs_sched_off.push_back(soff);
     fj.M = 2 * H;
     fj.silu_out = 0;
     fj.ld_out = 2 * H;
@@ -379,6 +399,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     jobs.push_back(t0);
     jobs.push_back(t2);
     d->max_job_m = 6 * H;
+    d->jobs_host = jobs;
     e = hipMemcpy(d->jobs_dev, jobs.data(), sizeof(GemvJob) * jobs.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) { tsk_dit_destroy(d); return hip_fail(e, "hipMemcpy jobs"); }
     *out = d;
@@ -462,6 +483,11 @@ struct StreamRun {
     int pend_split = 0;
 };
 
+// adaLN outputs of a block for the running call: its own [B][nmod * H] rows,
+// or one schedule row shared by the batch (row stride 0)
+const float *mod_of(const tsk_dit *d, const StreamW &w) { return d->cur_sched ? d->cur_sched + w.sched_off : w.mod; }
+int64_t mod_ld(const tsk_dit *d, const StreamW &w) { return d->cur_sched ? 0 : (int64_t) w.nmod * d->cfg.hidden; }
+
 LnStream ln_stream(const StreamRun &r, int B, int H, int64_t ldm, const float *shift, const float *scale, void *y) {
     LnStream l;
     memset(&l, 0, sizeof(l));
@@ -496,9 +522,10 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
     double rows = 0.0, pbytes = 0.0;
     for (int i = 0; i < ns; ++i) {
         const StreamW &w = *r[i].w;
-        const int64_t ldm = (int64_t) w.nmod * H;
+        const int64_t ldm = mod_ld(d, w);
         // which = 0: shift_msa / scale_msa (mod 0, 1); 1: shift_mlp / scale_mlp (mod 3, 4)
-        const float *sh = w.mod + (which ? 3 : 0) * H, *sc = w.mod + (which ? 4 : 1) * H;
+        const float *m = mod_of(d, w);
+        const float *sh = m + (which ? 3 : 0) * H, *sc = m + (which ? 4 : 1) * H;
         g.s[i] = ln_stream(r[i], B, H, ldm, sh, sc, r[i].xn);
         rows += (double) B * r[i].S;
         pbytes += 4.0 * r[i].pend_split * B * r[i].S * H;
@@ -564,8 +591,8 @@ int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         q.splits = KSPLIT_OUT;
         r[i].pend_split = KSPLIT_OUT;
         r[i].pend_bias = r[i].w->l1_b;
-        r[i].pend_gate = r[i].w->mod + 2 * H;   // gate_msa
-        r[i].pend_ld_gate = (int64_t) r[i].w->nmod * H;
+        r[i].pend_gate = mod_of(d, *r[i].w) + 2 * H;   // gate_msa
+        r[i].pend_ld_gate = mod_ld(d, *r[i].w);
         fl += 2.0 * rows * H * H;
         by += 2.0 * H * H + 2.0 * rows * H + 4.0 * KSPLIT_OUT * rows * H;
     }
@@ -589,8 +616,8 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
         q.splits = KSPLIT_FC2;
         r[i].pend_split = KSPLIT_FC2;
         r[i].pend_bias = r[i].w->fc2_b;
-        r[i].pend_gate = r[i].w->mod + 5 * H;   // gate_mlp
-        r[i].pend_ld_gate = (int64_t) r[i].w->nmod * H;
+        r[i].pend_gate = mod_of(d, *r[i].w) + 5 * H;   // gate_mlp
+        r[i].pend_ld_gate = mod_ld(d, *r[i].w);
         fl += 2.0 * rows * H * F;
         by1 += 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F;
         by2 += 2.0 * H * F + 2.0 * rows * F + 4.0 * KSPLIT_FC2 * rows * H;
@@ -640,16 +667,20 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     return hipcheck(launch_attn_fast(p, st), "attention");
 }
 
-int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host, const float *text_d,
-                 float *flow_d, hipStream_t st) {
+// The adaLN conditioning of one forward call: timestep embedding, t_embed MLP
+// and every block's modulations for the call's B rows of t. The jobs of the
+// first jmain streams run on the caller's stream, the rest on the side stream
+// (the caller's stream waits on d->ev_join before the first block that needs
+// them).
+int run_conditioning(tsk_dit *d, int B, const float *t_host, int jmain, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
-    const int H = c.hidden, St = c.text_seq, nj = c.depth - c.fused_depth;
+    const int H = c.hidden, nj = c.depth - c.fused_depth;
+    hipError_t e;
     // timestep frequency embedding [cos(t f), sin(t f)] (mmdit.cpp:305-314); t by value
     TimeVals tv;
     for (int b = 0; b < 32; ++b) tv.t[b] = b < B ? t_host[b] : 0.0f;
-    hipError_t e = launch_timestep_embed(d->freq, tv, B, H, d->temb, st);
+    e = launch_timestep_embed(d->freq, tv, B, H, d->temb, st);
     if (e != hipSuccess) return hip_fail(e, "timestep embed");
-    int rc;
     // t_embed MLP -> silu(cond) (mmdit.cpp:158-160, :209), f32 activations
     {
         Timed tm(d, TSK_ROLE_ADALN, 4.0 * B * H * H, 4.0 * H * H, st);
@@ -659,9 +690,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // every adaLN modulation of the step: the jobs of the first two joint blocks
     // on the caller's stream, all later ones (the bulk of the 352 MB of adaLN
     // weights at d = 1024, HBM-bound) on the side stream, where they overlap
-    // the first blocks; the caller's stream joins them before the first block
-    // that needs one
-    const int jmain = 2 * (nj < 2 ? nj : 2);
+    // the first blocks
     {
         const double per = 6.0 * H * H;   // weight elements of one 6H-output job
         Timed tm(d, TSK_ROLE_ADALN, 2.0 * B * per * jmain, 2.0 * per * jmain, st);
@@ -677,7 +706,23 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
             return hip_fail(e, "adaln gemv");
     }
     if ((e = hipEventRecord(d->ev_join, d->side)) != hipSuccess) return hip_fail(e, "join");
-    bool joined = false;
+    return TSK_OK;
+}
+
+int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host, const float *text_d,
+                 float *flow_d, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden, St = c.text_seq, nj = c.depth - c.fused_depth;
+    hipError_t e;
+    int rc;
+    // a sampler step with a conditioning schedule reads its modulations from
+    // the schedule row (d->cur_sched); otherwise they are computed here
+    const int jmain = 2 * (nj < 2 ? nj : 2);
+    bool joined = true;
+    if (!d->cur_sched) {
+        if ((rc = run_conditioning(d, B, t_host, jmain, st))) return rc;
+        joined = false;
+    }
     auto join = [&]() -> int {
         if (joined) return TSK_OK;
         joined = true;
@@ -733,11 +778,11 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // final layer: last residual update + LN/modulate (f32, final adaLN shift/scale)
     // -> linear to latent_dim (f32 activations, fp32 accumulation)
     {
-        const float *fmod = d->final_mod;
+        const float *fmod = d->cur_sched ? d->cur_sched + d->sched_final : d->final_mod;
         LnGroup g;
         memset(&g, 0, sizeof(g));
         g.nstream = 1; g.H = H; g.eps = c.ln_eps; g.y_f32 = 1;
-        g.s[0] = ln_stream(L, B, H, 2 * H, fmod, fmod + H, d->xf);
+        g.s[0] = ln_stream(L, B, H, d->cur_sched ? 0 : 2 * H, fmod, fmod + H, d->xf);
         Timed tm(d, TSK_ROLE_OTHER, 10.0 * B * T * H, 16.0 * B * T * H + 4.0 * L.pend_split * B * T * H, st);
         if ((e = launch_ln_group(g, st)) != hipSuccess) return hip_fail(e, "final ln");
     }
@@ -785,6 +830,79 @@ extern "C" int tsk_dit_forward(tsk_dit *d, int B, int T, const float *latent, co
 }
 
 // ------------------------------------------------------------------ sampler
+namespace {
+
+// The sampler's t values are fixed by its step count (linspace(1, 0, steps + 1),
+// mmdit.cpp:360-362) and the adaLN modulations depend on t alone, identically
+// for the conditional and the unconditional row. They are computed for every
+// step before the first one, 32 steps per batched pass, so each adaLN weight
+// matrix is read once per 32 steps instead of once per step; every output is
+// summed exactly as the per-call path sums it (the GEMV's summation order does
+// not depend on its batch), so the schedule changes no result bit.
+int build_schedule(tsk_dit *d, int steps, hipStream_t st) {
+    const int H = d->cfg.hidden;
+    const size_t R = d->sched_row;
+    const int nchunk = (steps + 31) / 32;
+    const int nj = d->njobs;                  // block + final-layer jobs; t_embed.0 / .2 follow
+    const int per = nj + 2;
+    hipError_t e;
+    if (d->sched_cap < (size_t) steps * R) {
+        if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "sync");
+        if (d->sched) (void) hipFree(d->sched);
+        d->sched = nullptr;
+        d->sched_cap = 0;
+        if (hipMalloc((void **) &d->sched, sizeof(float) * (size_t) steps * R) != hipSuccess)
+            return fail(TSK_ERR_NOMEM, "hipMalloc conditioning schedule (%d steps)", steps);
+        d->sched_cap = (size_t) steps * R;
+    }
+    if (!d->sched_act && hipMalloc((void **) &d->sched_act, sizeof(float) * 3 * 32 * H) != hipSuccess)
+        return fail(TSK_ERR_NOMEM, "hipMalloc schedule activations");
+    if (d->sched_jobs_cap < nchunk * per) {
+        if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "sync");
+        if (d->sched_jobs) (void) hipFree(d->sched_jobs);
+        d->sched_jobs = nullptr;
+        d->sched_jobs_cap = 0;
+        if (hipMalloc((void **) &d->sched_jobs, sizeof(GemvJob) * nchunk * per) != hipSuccess)
+            return fail(TSK_ERR_NOMEM, "hipMalloc schedule jobs");
+        d->sched_jobs_cap = nchunk * per;
+    }
+    float *temb = d->sched_act, *hid = temb + 32 * H, *cvec = hid + 32 * H;
+    std::vector<GemvJob> tab((size_t) nchunk * per);
+    for (int ck = 0; ck < nchunk; ++ck) {
+        GemvJob *t = tab.data() + (size_t) ck * per;
+        float *row0 = d->sched + (size_t) ck * 32 * R;
+        for (int j = 0; j < nj; ++j) {
+            t[j] = d->jobs_host[j];
+            t[j].x = cvec;
+            t[j].out = row0 + d->jobs_sched_off[j];
+            t[j].ld_out = (int64_t) R;
+        }
+        t[nj] = d->jobs_host[nj];
+        t[nj].x = temb; t[nj].out = hid; t[nj].ld_out = H;
+        t[nj + 1] = d->jobs_host[nj + 1];
+        t[nj + 1].x = hid; t[nj + 1].out = cvec; t[nj + 1].ld_out = H;
+    }
+    // the table is read by kernels queued on st: copy it before any of them
+    if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "sync");
+    if ((e = hipMemcpy(d->sched_jobs, tab.data(), sizeof(GemvJob) * tab.size(), hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(e, "hipMemcpy schedule jobs");
+    const double wel = (double) R * H;   // adaLN weight elements
+    Timed tm(d, TSK_ROLE_ADALN, 2.0 * steps * (wel + 2.0 * H * H), 2.0 * nchunk * (wel + 2.0 * H * H), st);
+    for (int ck = 0; ck < nchunk; ++ck) {
+        const int Bc = std::min(32, steps - 32 * ck);
+        TimeVals tv;
+        for (int b = 0; b < 32; ++b) tv.t[b] = b < Bc ? 1.0f - (float) (32 * ck + b) / (float) steps : 0.0f;
+        const GemvJob *t = d->sched_jobs + (size_t) ck * per;
+        if ((e = launch_timestep_embed(d->freq, tv, Bc, H, temb, st)) != hipSuccess) return hip_fail(e, "timestep embed");
+        if ((e = launch_gemv_jobs(t + nj, 1, H, Bc, H, st)) != hipSuccess) return hip_fail(e, "t_embed.0");
+        if ((e = launch_gemv_jobs(t + nj + 1, 1, H, Bc, H, st)) != hipSuccess) return hip_fail(e, "t_embed.2");
+        if ((e = launch_gemv_jobs(t, nj, d->max_job_m, Bc, H, st)) != hipSuccess) return hip_fail(e, "adaln schedule");
+    }
+    return TSK_OK;
+}
+
+}  // namespace
+
 extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float *text_cond,
                               const float *text_uncond, int steps, float cfg_scale, float *out, float *flow0,
                               tsk_stream stream) {
@@ -811,11 +929,20 @@ extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float
     if ((rc = hipcheck(hipMemcpyAsync(d->s_x2 + n, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2, text_cond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2 + nt, text_uncond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
+    // TSK_DIT_SCHED=0 computes the conditioning inside every step instead
+    const char *sched_env = getenv("TSK_DIT_SCHED");
+    const bool use_sched = !(sched_env && sched_env[0] == '0');
+    if (use_sched && (rc = build_schedule(d, steps, st))) return rc;
+    struct SchedGuard {
+        tsk_dit *d;
+        ~SchedGuard() { d->cur_sched = nullptr; }
+    } guard{d};
     for (int s = 0; s < steps; ++s) {
         // linspace(1, 0, steps + 1) (mmdit.cpp:360-362)
         const float t_curr = 1.0f - (float) s / (float) steps;
         const float t_prev = 1.0f - (float) (s + 1) / (float) steps;
         const float tt[2] = {t_curr, t_curr};
+        d->cur_sched = use_sched ? d->sched + (size_t) s * d->sched_row : nullptr;
         if ((rc = forward_impl(d, 2, T, d->s_x2, tt, d->s_text2, d->s_flow2, st))) return rc;
         hipError_t e = launch_cfg_euler(d->s_flow2, (int64_t) n, cfg_scale, t_prev - t_curr, d->s_x, d->s_x2,
                                         s == 0 ? d->s_flow0 : nullptr, st);
