@@ -126,21 +126,31 @@ constexpr size_t lds_bytes() {
     return ring > red ? ring : red;
 }
 
-template <int TM, int TN, int R, int MODE, int EPI, int KH = 1>
+// read by fragments of the implicit im2col that fall into the zero padding
+__device__ __attribute__((aligned(16))) uint16_t g_zero_row[32];
+
+constexpr bool epi_swiglu(int epi) { return epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_BF16; }
+
+template <int TM, int TN, int R, int MODE, int EPI, int KH = 1, bool CONV = false>
 __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = KH * L * 1024;
     constexpr bool COOP = MODE == MODE_COOP, DIRECT = MODE == MODE_DIRECT;
     static_assert(!COOP || (TM % 2 == 0 && TN % 2 == 0 && L % 4 == 0), "cooperative tile shape");
     static_assert(COOP || KH == 1, "KH: 32-wide k tiles per cooperative stage");
+    static_assert(COOP || (!CONV && !epi_swiglu(EPI)), "convolutions and SwiGLU run cooperative tiles");
     constexpr int TMW = COOP ? TM / 2 : TM, TNW = COOP ? TN / 2 : TN;   // 16x16 tiles per wave
+    // SwiGLU: row blocks [0, TM / 2) of the tile are W's, [TM / 2, TM) the
+    // same rows of W3, so the tile holds BM / 2 output features
+    constexpr bool SWIGLU = epi_swiglu(EPI);
+    constexpr int BMO = SWIGLU ? BM / 2 : BM;
 
     Coord tc;
     if (!decode(g, tc)) return;
     const GemmProblem &p = g.p[tc.pi];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bm0 = tc.tm * BM, bn0 = tc.tn * BN;
+    const int bm0 = tc.tm * BMO, bn0 = tc.tn * BN;
     const int KT = p.K >> 5;                                  // 32-wide k tiles
     const int kt0 = tc.split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
     const int nst = kt1 - kt0;
@@ -148,29 +158,54 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     const int wm = COOP ? (wave & 1) : 0, wn = COOP ? (wave >> 1) : 0;       // cooperative quadrant
 
     // A: tile (rb, kt) of the tiled weights at (rb * KT + kt) * 512 elements,
-    // this lane's 16 bytes at lane * 8. Row blocks past M read the last one
-    // (their outputs are never stored).
-    const uint16_t *wl = p.w + lane * 8;
-    int64_t aoff[TM];
+    // this lane's 16 bytes at lane * 8; row-major weights (cooperative tiles
+    // only): row 16 rb + l % 16, k 32 kt + 8 (l / 16). Row blocks past M read
+    // the last one (their outputs are never stored).
+    const uint16_t *abase[TM];
+    const int astep = p.w_tiled ? 512 : 32;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) aoff[i] = (int64_t) min((bm0 >> 4) + i, (p.M >> 4) - 1) * KT * 512;
-    // B: token bn0 + 16 j + l % 16 (tokens past N read row N - 1), k 8 (l / 16)
+    for (int i = 0; i < TM; ++i) {
+        const int rb = min((bm0 >> 4) + (SWIGLU ? i % (TM / 2) : i), (p.M >> 4) - 1);
+        const uint16_t *wsrc = SWIGLU && i >= TM / 2 ? p.w3 : p.w;
+        abase[i] = p.w_tiled ? wsrc + (int64_t) rb * KT * 512 + lane * 8
+                             : wsrc + (int64_t) (rb * 16 + (lane & 15)) * p.ld_w + 8 * (lane >> 4);
+    }
+    // B: token bn0 + 16 j + l % 16 (tokens past N read row N - 1), k 8 (l / 16);
+    // implicit im2col: the token is output position ow of batch item b, and
+    // k tile kt reads input position ow s + kw d - p (kw = 32 kt / IC), or a
+    // zero row in the padding
     const uint16_t *bsrc[TN];
+    int biw[CONV ? TN : 1];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = min(bn0 + 16 * j + (lane & 15), p.N - 1);
-        bsrc[j] = (const uint16_t *) p.x + x_row(p, n) + 8 * (lane >> 4);
+        if constexpr (CONV) {
+            const int b = n / p.conv_ow, ow = n - b * p.conv_ow;
+            bsrc[j] = (const uint16_t *) p.x + (int64_t) b * p.x_group_stride + 8 * (lane >> 4);
+            biw[j] = ow * p.conv_s - p.conv_p;
+        } else {
+            bsrc[j] = (const uint16_t *) p.x + x_row(p, n) + 8 * (lane >> 4);
+        }
     }
+    auto bfrag = [&](int j, int kt) -> const uint16_t * {
+        if constexpr (CONV) {
+            const int k = kt * 32, kw = k / p.conv_ic, ic0 = k - kw * p.conv_ic;
+            const int iw = biw[j] + kw * p.conv_d;
+            return iw >= 0 && iw < p.conv_iw ? bsrc[j] + (int64_t) iw * p.ld_x + ic0 : g_zero_row + 8 * (lane >> 4);
+        } else {
+            return bsrc[j] + kt * 32;
+        }
+    };
     uint8_t *ring = lds + wave * (R * STAGE);
     auto issue = [&](int t, int slot) {
         const int kt = kt0 + wave + 4 * t;
         uint8_t *dst = ring + slot * STAGE;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-            g2l16(wl + aoff[i] + (int64_t) kt * 512, dst + i * 1024);
+            g2l16(abase[i] + (int64_t) kt * astep, dst + i * 1024);
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-            g2l16(bsrc[j] + kt * 32, dst + (TM + j) * 1024);
+            g2l16(bfrag(j, kt), dst + (TM + j) * 1024);
     };
 
     f32x4 acc[TMW][TNW];
@@ -192,8 +227,8 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
             for (int q = 0; q < LW; ++q) {
                 const int fq = wave + 4 * q, h = fq / L, f = fq % L;
                 const int kt = kt0 + t * KH + h;
-                if (f < TM) g2l16(wl + aoff[f] + (int64_t) kt * 512, dst + fq * 1024);
-                else g2l16(bsrc[f - TM] + kt * 32, dst + fq * 1024);
+                if (f < TM) g2l16(abase[f] + (int64_t) kt * astep, dst + fq * 1024);
+                else g2l16(bfrag(f - TM, kt), dst + fq * 1024);
             }
         };
 #pragma unroll
@@ -232,9 +267,9 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
         auto dload = [&](int t, int set) {
             const int kt = kt0 + wave + 4 * t;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) ra[set][i] = *(const u32x4 *) (wl + aoff[i] + (int64_t) kt * 512);
+            for (int i = 0; i < TM; ++i) ra[set][i] = *(const u32x4 *) (abase[i] + (int64_t) kt * astep);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) rb[set][j] = *(const u32x4 *) (bsrc[j] + kt * 32);
+            for (int j = 0; j < TN; ++j) rb[set][j] = *(const u32x4 *) bfrag(j, kt);
         };
         auto consume = [&](int set) {
 #pragma unroll
@@ -371,6 +406,31 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
                 }
             }
         }
+    } else if constexpr (SWIGLU) {
+        // 8 consecutive features of one token per thread: silu(W x) * (W3 x)
+        constexpr int G = BMO / 8;
+        for (int it = tid; it < BNC * G; it += NT) {
+            const int nl = it / G, ml = (it % G) * 8;
+            const int n = bn0c + nl, m = bm0 + ml;
+            if (n >= p.N || m >= p.M) continue;
+            const f32x4 a0 = sum4(nl, ml), a1 = sum4(nl, ml + 4);
+            const f32x4 c0 = sum4(nl, BMO + ml), c1 = sum4(nl, BMO + ml + 4);
+            const float h1[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const float h3[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+            float o[8];
+            for (int e = 0; e < 8; ++e) o[e] = h1[e] / (1.0f + expf(-h1[e])) * h3[e];
+            if constexpr (EPI == EPI_SWIGLU_BF16) {
+                uint16_t t8[8];
+                for (int e = 0; e < 8; ++e) t8[e] = f32_to_bf16_bits(o[e]);
+                u32x4 w;
+                __builtin_memcpy(&w, t8, 16);
+                *(u32x4 *) ((uint16_t *) p.y + (int64_t) n * p.ld_y + m) = w;
+            } else {
+                float *yr = (float *) p.y + (int64_t) n * p.ld_y + m;
+                *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                *(f32x4 *) (yr + 4) = f32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
     } else {
         // 8 consecutive features of one token per thread
         constexpr int G = BM / 8;
@@ -403,9 +463,9 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     }   // token chunk
 }
 
-template <int TM, int TN, int R, int MODE, int EPI, int KH>
+template <int TM, int TN, int R, int MODE, int EPI, int KH, bool CONV = false>
 hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
-    constexpr int BM = 16 * TM, BN = 16 * TN;
+    constexpr int BM = 16 * TM / (epi_swiglu(EPI) ? 2 : 1), BN = 16 * TN;
     int nblocks = 0;
     for (int i = 0; i < g.nprob; ++i) {
         GemmProblem &p = g.p[i];
@@ -418,7 +478,7 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     }
     constexpr size_t lds = lds_bytes<TM, TN, R, MODE, KH>();
     static_assert(lds <= 160 * 1024, "LDS");
-    auto kern = gemm_ks_kernel<TM, TN, R, MODE, EPI, KH>;
+    auto kern = gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV>;
     static bool attr = false;   // dynamic LDS above 64 KiB is opted in once per kernel
     if (!attr) {
         if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
@@ -442,7 +502,43 @@ hipError_t ks_epi(GemmGroup &g, int epi, hipStream_t s) {
     }
 }
 
+template <int TM, int TN, int R, bool CONV>
+hipError_t conv_epi(GemmGroup &g, int epi, hipStream_t s) {
+    switch (epi) {
+        case EPI_STORE_F32: return ks_launch<TM, TN, R, MODE_COOP, EPI_STORE_F32, 1, CONV>(g, s);
+        case EPI_STORE_BF16: return ks_launch<TM, TN, R, MODE_COOP, EPI_STORE_BF16, 1, CONV>(g, s);
+        case EPI_SWIGLU_F32: return ks_launch<TM, TN, R, MODE_COOP, EPI_SWIGLU_F32, 1, CONV>(g, s);
+        case EPI_SWIGLU_BF16: return ks_launch<TM, TN, R, MODE_COOP, EPI_SWIGLU_BF16, 1, CONV>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
+    if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
+    const bool conv = g.p[0].conv_ic != 0;
+    int64_t tiles = 0;   // 128 x 64 tiles (64 x 64 output features for SwiGLU)
+    for (int i = 0; i < g.nprob; ++i) {
+        const GemmProblem &p = g.p[i];
+        if (p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits != 1 || (p.conv_ic != 0) != conv)
+            return hipErrorInvalidValue;
+        if (!p.w_tiled && (p.ld_w % 8 || ((uintptr_t) p.w & 15) || (p.w3 && ((uintptr_t) p.w3 & 15))))
+            return hipErrorInvalidValue;
+        if (p.w_tiled && epi_swiglu(epi)) return hipErrorInvalidValue;
+        if (epi_swiglu(epi) && (!p.w3 || p.bias || p.M % 8)) return hipErrorInvalidValue;
+        if (p.ld_x % 8 || ((uintptr_t) p.x & 15)) return hipErrorInvalidValue;
+        if (conv && (p.conv_ic % 32 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
+                     p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow || p.x_group_stride % 8))
+            return hipErrorInvalidValue;
+        tiles += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 63) / 64);
+    }
+    // 128 x 64 tiles once they fill the 256 CUs about twice, 64 x 64 below
+    // (the crossover measured on the DiT projections)
+    if (tiles >= 512)
+        return conv ? conv_epi<8, 4, 4, true>(g, epi, s) : conv_epi<8, 4, 4, false>(g, epi, s);
+    return conv ? conv_epi<4, 4, 4, true>(g, epi, s) : conv_epi<4, 4, 4, false>(g, epi, s);
+}
 
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn) {
     int n = 0;

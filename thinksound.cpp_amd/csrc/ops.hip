@@ -372,6 +372,23 @@ __global__ void im2col_1d_kernel(const float *x, int64_t sp, int64_t sc, int64_t
     store_from_f32<E>(dst, row * ld + kk, v);
 }
 
+// f32 rows -> bf16 (RNE), 4 elements per thread: row r = b * rows_per_b + i of
+// x at b * ld_b + i * ld_x, y contiguous rows of `cols`
+__global__ void cast_rows_bf16_kernel(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows,
+                                      int cols, uint16_t *y) {
+    const int64_t q = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int cq = cols / 4;
+    if (q >= rows * cq) return;
+    const int64_t r = q / cq;
+    const int c = (int) (q - r * cq) * 4;
+    const int64_t b = r / rows_per_b, i = r - b * rows_per_b;
+    const f32x4 v = *(const f32x4 *) (x + b * ld_b + i * ld_x + c);
+    uint16_t t4[4] = {f32_to_bf16_bits(v[0]), f32_to_bf16_bits(v[1]), f32_to_bf16_bits(v[2]), f32_to_bf16_bits(v[3])};
+    u32x2 w;
+    __builtin_memcpy(&w, t4, 8);
+    *(u32x2 *) (y + r * cols + c) = w;
+}
+
 // conv kernel [KW, IC, OC] (element strides s0, s1, s2) -> kw-major rows
 // dst[oc][kw * IC + ic], a bit copy
 template <typename T>
@@ -528,6 +545,14 @@ hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, 
         default:
             return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_cast_rows_bf16(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows, int cols,
+                                 uint16_t *y, hipStream_t s) {
+    if (rows < 1 || cols < 4 || cols % 4 || rows_per_b < 1 || ld_x % 4 || ld_b % 4) return hipErrorInvalidValue;
+    const int64_t n = rows * (cols / 4);
+    launch_kernel(cast_rows_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, ld_x, ld_b, rows_per_b, rows, cols, y);
     return hipGetLastError();
 }
 

@@ -3,6 +3,7 @@
 // tsk_status; nothing aborts. Kernels are enqueued on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -236,6 +237,35 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
     const bool uni = rows_uniform(b) && rows_uniform(dst);
     const int64_t nslices = uni ? 1 : b->ne[2] * b->ne[3];
     const int64_t Nslice = uni ? b->ne[1] * b->ne[2] * b->ne[3] : b->ne[1];
+
+    // BF16 weights with M % 16 == 0, K % 32 == 0 and uniformly strided rows:
+    // the cooperative tiles of gemm_ks.hip on bf16 activation rows (f32 b is
+    // rounded to bf16 into the workspace first: ggml's conversion of src1)
+    if (a->type == TSK_TYPE_BF16 && uni && M % 16 == 0 && K % 32 == 0 && a->nb[1] % 16 == 0) {
+        uint16_t *xb = nullptr;
+        const int64_t N = Nslice;
+        const int64_t ld_b = (int64_t) (b->nb[1] / es_b);
+        if (b->type == TSK_TYPE_F32) {
+            if ((rc = workspace((size_t) (N * K) * 2, (void **) &xb))) return rc;
+            hipError_t e = launch_cast_rows_bf16((const float *) b->data, ld_b, 0, (int) std::min<int64_t>(N, 1 << 30), N,
+                                                 (int) K, xb, s);
+            if (e != hipSuccess) return hip_fail(e, "mul_mat input cast");
+        }
+        GemmGroup g;
+        memset(&g, 0, sizeof(g));
+        g.nprob = 1;
+        GemmProblem &q = g.p[0];
+        q.x = xb ? (const void *) xb : b->data;
+        q.ld_x = xb ? K : ld_b;
+        q.w = (const uint16_t *) a->data;
+        q.ld_w = (int64_t) (a->nb[1] / 2);
+        q.bias = bias ? (const float *) bias->data : nullptr;
+        q.y = dst->data;
+        q.ld_y = (int64_t) (dst->nb[1] / es_d);
+        q.M = (int) M; q.N = (int) N; q.K = (int) K; q.splits = 1;
+        hipError_t e = launch_gemm_coop(g, dst->type == TSK_TYPE_BF16 ? EPI_STORE_BF16 : EPI_STORE_F32, s);
+        return e == hipSuccess ? TSK_OK : hip_fail(e, "mul_mat launch");
+    }
 
     // Q8_0 weights: repack raw ggml blocks into planes in the workspace
     const int8_t *qw = nullptr;
@@ -653,13 +683,33 @@ int conv_weight_rows(const tsk_tensor *w, char **scratch, const void **rows, int
     return TSK_OK;
 }
 
+// BF16 convolutions with IC % 32 == 0 and OC % 16 == 0 run the cooperative
+// tiles of gemm_ks.hip on bf16 input rows (f32 inputs are rounded to bf16
+// first -- the conversion ggml_mul_mat applies to its src1 -- into
+// B * IW * IC bf16 of scratch); others the grouped GEMM of gemm_group.hip
+bool conv_coop(int wtype, int IC, int OC) { return wtype == TSK_TYPE_BF16 && IC % 32 == 0 && OC % 16 == 0; }
+size_t conv_cast_bytes(int wtype, int x_f32, int64_t IC, int64_t IW, int64_t B, int64_t OC) {
+    return conv_coop(wtype, (int) IC, (int) OC) && x_f32 ? align256((size_t) (B * IW * IC) * 2) : 0;
+}
+
 // one convolution GEMM (validated operands): x rows [B][IW][IC] (ld_x, batch
 // stride xb in elements), y rows [B * OW][OC] (ld_y); kw-major weight rows.
-// swiglu: w3 rows given -> y = silu(x * w) * (x * w3) (BF16 kernels only)
+// swiglu: w3 rows given -> y = silu(x * w) * (x * w3) (BF16 kernels only).
+// xcast: conv_cast_bytes() of scratch, or nullptr when that is 0.
 int conv_gemm(int wtype, const void *wrows, const void *w3rows, int64_t ld_w, const float *bias, int KW, int IC, int OC,
               const void *x, int x_f32, int64_t ld_x, int64_t xb, int IW, int B, int s0, int p0, int d0, void *y,
-              int y_bf16, int64_t ld_y, hipStream_t s) {
+              int y_bf16, int64_t ld_y, uint16_t *xcast, hipStream_t s) {
     const int OW = (int) conv_out_len(IW, KW, s0, p0, d0);
+    const bool coop = conv_coop(wtype, IC, OC) && (!x_f32 || xcast) && ld_w % 8 == 0 &&
+                      ((uintptr_t) wrows & 15) == 0 && ((uintptr_t) w3rows & 15) == 0;
+    if (coop && x_f32) {
+        hipError_t e = launch_cast_rows_bf16((const float *) x, ld_x, xb, IW, (int64_t) B * IW, IC, xcast, s);
+        if (e != hipSuccess) return hip_fail(e, "conv input cast");
+        x = xcast;
+        x_f32 = 0;
+        ld_x = IC;
+        xb = (int64_t) IW * IC;
+    }
     GemmProblem q;
     memset(&q, 0, sizeof(q));
     q.x = x; q.bias = bias; q.y = y;
@@ -680,7 +730,7 @@ int conv_gemm(int wtype, const void *wrows, const void *w3rows, int64_t ld_w, co
         q.w3 = (const uint16_t *) w3rows;
         g.p[0] = q;
         const int epi = w3rows ? (y_bf16 ? EPI_SWIGLU_BF16 : EPI_SWIGLU_F32) : (y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32);
-        e = launch_gemm_group(g, x_f32 ? GEMM_X_F32 : 0, epi, s);
+        e = coop ? launch_gemm_coop(g, epi, s) : launch_gemm_group(g, x_f32 ? GEMM_X_F32 : 0, epi, s);
     }
     return e == hipSuccess ? TSK_OK : hip_fail(e, "conv GEMM launch");
 }
@@ -753,16 +803,20 @@ extern "C" int tsk_conv1d(const tsk_tensor *w, const tsk_tensor *bias, const tsk
     if ((rc = require_init())) return rc;
     hipStream_t s = (hipStream_t) stream;
     char *ws = nullptr;
-    const size_t need = conv_pack_bytes(w);
+    const int x_f32 = x->type == TSK_TYPE_F32;
+    const size_t cast = conv_cast_bytes(w->type, x_f32, w->ne[1], x->ne[1], x->ne[2], w->ne[2]);
+    const size_t need = conv_pack_bytes(w) + cast;
     if (need && (rc = workspace(need, (void **) &ws, 1))) return rc;
+    uint16_t *xcast = cast ? (uint16_t *) ws : nullptr;
+    char *pk = ws + cast;
     const void *wr = nullptr;
     int64_t ld_w = 0;
-    if ((rc = conv_weight_rows(w, &ws, &wr, &ld_w, s))) return rc;
+    if ((rc = conv_weight_rows(w, &pk, &wr, &ld_w, s))) return rc;
     const int esx = elt_size(x->type), esy = elt_size(dst->type);
     return conv_gemm(w->type, wr, nullptr, ld_w, bias ? (const float *) bias->data : nullptr, (int) w->ne[0],
-                     (int) w->ne[1], (int) w->ne[2], x->data, x->type == TSK_TYPE_F32, (int64_t) (x->nb[1] / esx),
+                     (int) w->ne[1], (int) w->ne[2], x->data, x_f32, (int64_t) (x->nb[1] / esx),
                      (int64_t) (x->nb[2] / esx), (int) x->ne[1], (int) x->ne[2], s0, p0, d0, dst->data,
-                     dst->type == TSK_TYPE_BF16, (int64_t) (dst->nb[1] / esy), s);
+                     dst->type == TSK_TYPE_BF16, (int64_t) (dst->nb[1] / esy), xcast, s);
 }
 
 extern "C" int tsk_swiglu(const tsk_tensor *a, const tsk_tensor *b, tsk_tensor *dst, tsk_stream stream) {
@@ -794,13 +848,15 @@ int swiglu_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
     // w2's mul_mat applies), f32 h3 for F32 kernels, then packed kernels
     const size_t nh = (size_t) B * OW1 * HID;
     const size_t hbytes = align256(nh * (bf16 ? 2 : 4)), h3bytes = bf16 ? 0 : align256(nh * 4);
-    const size_t total = hbytes + h3bytes + conv_pack_bytes(w1) + conv_pack_bytes(w3) + conv_pack_bytes(w2);
+    const size_t cast = conv_cast_bytes(w1->type, x_f32, IC, IW, B, HID);
+    const size_t total = hbytes + h3bytes + cast + conv_pack_bytes(w1) + conv_pack_bytes(w3) + conv_pack_bytes(w2);
     char *ws = nullptr;
     int rc;
     if ((rc = workspace(total, (void **) &ws, 1))) return rc;
     void *h = ws;
     float *h3 = bf16 ? nullptr : (float *) (ws + hbytes);
-    char *pk = ws + hbytes + h3bytes;
+    uint16_t *xcast = cast ? (uint16_t *) (ws + hbytes + h3bytes) : nullptr;
+    char *pk = ws + hbytes + h3bytes + cast;
     const void *r1, *r3, *r2;
     int64_t ld1, ld3, ld2;
     if ((rc = conv_weight_rows(w1, &pk, &r1, &ld1, s)) || (rc = conv_weight_rows(w3, &pk, &r3, &ld3, s)) ||
@@ -809,19 +865,19 @@ int swiglu_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
     if (ld1 != ld3) return fail(TSK_ERR_STRIDE, "w1 and w3 row strides differ");
     if (bf16) {
         if ((rc = conv_gemm(TSK_TYPE_BF16, r1, r3, ld1, nullptr, KW1, IC, HID, x, x_f32, ld_x, xb, IW, B, 1, pad, 1, h,
-                            1, HID, s)))
+                            1, HID, xcast, s)))
             return rc;
     } else {
         if ((rc = conv_gemm(TSK_TYPE_F32, r1, nullptr, ld1, nullptr, KW1, IC, HID, x, 1, ld_x, xb, IW, B, 1, pad, 1, h,
-                            0, HID, s)) ||
+                            0, HID, nullptr, s)) ||
             (rc = conv_gemm(TSK_TYPE_F32, r3, nullptr, ld3, nullptr, KW1, IC, HID, x, 1, ld_x, xb, IW, B, 1, pad, 1, h3,
-                            0, HID, s)))
+                            0, HID, nullptr, s)))
             return rc;
         hipError_t e = launch_silu_mul((const float *) h, h3, (float *) h, (int64_t) nh, s);
         if (e != hipSuccess) return hip_fail(e, "swiglu launch");
     }
     return conv_gemm(w2->type, r2, nullptr, ld2, nullptr, KW2, HID, OC, h, !bf16, HID, (int64_t) OW1 * HID, OW1, B, 1,
-                     pad, 1, y, y_bf16, ld_y, s);
+                     pad, 1, y, y_bf16, ld_y, nullptr, s);
 }
 
 int check_mlp_types(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x) {

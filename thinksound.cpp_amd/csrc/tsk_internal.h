@@ -178,6 +178,11 @@ hipError_t launch_gemm_group(GemmGroup &g, int flags, int epi, hipStream_t s);
 // 1..5 force one (128x64 / 64x64 / 64x128 / 128x64 2-stage / 64x64 4-stage).
 hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s);
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn);
+// Cooperative-tile GEMM of gemm_ks.hip over row-major (or tiled) bf16 weights
+// and bf16 activation rows, optionally an implicit im2col (conv_ic % 32 == 0)
+// and the SwiGLU epilogue: EPI_STORE_F32 / _BF16, EPI_SWIGLU_F32 / _BF16.
+// M % 16 == 0, K % 32 == 0, 16-byte aligned rows.
+hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s);
 // RoPE (cos, sin) table for positions 0 .. npos-1 and n_dims / 2 pairs, the
 // angle freq_scale * p * theta_scale^i evaluated as rope_theta() does:
 // cs[p * n_dims + 2 i] = cos, [.. + 1] = sin
@@ -265,6 +270,10 @@ hipError_t launch_silu_inplace(float *x, int64_t n, hipStream_t s);
 // (channel), sn (batch)
 hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, int IW, int IC, int KW, int OW, int N,
                            int s0, int p0, int d0, void *dst, int dst_type, int64_t ld, hipStream_t s);
+// f32 rows -> contiguous bf16 rows (RNE): row b * rows_per_b + i read at
+// x + b * ld_b + i * ld_x (element strides, multiples of 4; cols % 4 == 0)
+hipError_t launch_cast_rows_bf16(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows, int cols,
+                                 uint16_t *y, hipStream_t s);
 // conv kernel [KW, IC, OC] of es-byte elements (element strides s0..s2) ->
 // kw-major rows dst[oc][kw * IC + ic]
 hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
