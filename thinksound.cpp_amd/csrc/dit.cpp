@@ -273,7 +273,9 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     // (one hex digit each, 0 = the launcher's choice)
     if (const char *gc = getenv("TSK_GEMM_CFG"))
         for (int i = 0; i < 4 && gc[i]; ++i)
-            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10 : 0;
+            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0'
+                           : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10
+                           : gc[i] >= 'A' && gc[i] <= 'Z' ? gc[i] - 'A' + 36 : 0;
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -536,16 +538,18 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
 }
 
 // Block GEMM tile shape by projection and activation rows of the larger
-// stream, measured on MI355X over 194 .. 646 latent tokens (B = 2): 64 x 64
-// cooperative tiles (cfg 22) while the token count leaves 128-row tiles too
-// few, 128 x 64 cooperative tiles (cfg 12) beyond; fc2 below that keeps the
-// 128 x 64 K-split LDS-ring tiles (cfg 4). The tile shape does not change
-// any summation order.
+// stream, measured on MI355X over 194 .. 646 latent tokens (B = 2): below
+// 550 rows 64 x 64 cooperative tiles of 64-wide stages (cfg 30); up to 1100
+// rows the same for qkv, 64 x 64 tiles of 32-wide stages for out (cfg 22)
+// and 128 x 64 tiles of 64-wide stages for the MLP (cfg 28); beyond, 128 x 64
+// cooperative tiles of 32-wide stages (cfg 12). The tile shape does not
+// change any summation order.
 int gemm_cfg_for(const tsk_dit *d, int role, int rows) {
     if (d->gemm_cfg[role]) return d->gemm_cfg[role];
-    const int big = role <= 1 ? 1100 : 550;   // qkv, out : fc1, fc2
-    if (rows >= big) return 12;
-    return role == 3 ? 4 : 22;
+    if (rows >= 1100) return 12;
+    if (rows < 550) return 30;
+    static const int mid[4] = {30, 22, 28, 28};   // qkv, out, fc1, fc2
+    return mid[role];
 }
 
 int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {

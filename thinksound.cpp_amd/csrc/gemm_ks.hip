@@ -37,6 +37,8 @@
 // order by their consumer), or the QKV epilogue (RMSNorm * w on q and k,
 // RoPE from a cos/sin table on the latent stream, the fp16 cast into the
 // attention layout [B][n_head][Ntot][64] and V^T, mmdit.cpp:78-90).
+#include <cstdlib>
+
 #include "tsk_common.h"
 #include "tsk_internal.h"
 
@@ -56,6 +58,29 @@ __device__ __forceinline__ void g2l16(const void *src, void *lds_base) {
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The same waits as s_waitcnt instructions the compiler sees (its own
+// counter bookkeeping then knows what has completed): vmcnt(N) only, and
+// lgkmcnt(0) only (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8; a field at its maximum does not wait).
+template <int N>
+__device__ __forceinline__ void wait_vm_seen() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkm0_seen() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+template <int L, int R>
+__device__ __forceinline__ void wait_stages_seen(int rem) {
+    if constexpr (R >= 4) {
+        if (rem >= 3) { wait_vm_seen<3 * L>(); return; }
+    }
+    if constexpr (R >= 3) {
+        if (rem >= 2) { wait_vm_seen<2 * L>(); return; }
+    }
+    if (rem >= 1) { wait_vm_seen<L>(); return; }
+    wait_vm_seen<0>();
 }
 
 // wait until at most `rem` stages of L loads each are still in flight
@@ -113,21 +138,25 @@ __device__ __forceinline__ int64_t x_row(const GemmProblem &p, int n) {
 enum : int {
     MODE_RING = 0,     // K-split waves, private LDS rings of direct global->LDS loads
     MODE_DIRECT = 1,   // K-split waves, operands straight into registers
-    MODE_COOP = 2      // 2 x 2 waves over the tile, one shared LDS ring
+    MODE_COOP = 2,     // 2 x 2 waves over the tile, one shared LDS ring
+    MODE_COOP_PIPE = 3,// MODE_COOP with the next stage's fragments read from LDS during this stage's MFMAs
+    MODE_COOP64 = 4    // MODE_COOP with 64-wide k stages of whole 128-byte rows (swizzled in LDS)
 };
 
 template <int TM, int TN, int R, int MODE, int KH = 1>
 constexpr size_t lds_bytes() {
+    constexpr bool coop = MODE == MODE_COOP || MODE == MODE_COOP_PIPE || MODE == MODE_COOP64;
     constexpr size_t ring = MODE == MODE_DIRECT ? 0
-                          : MODE == MODE_COOP   ? (size_t) R * KH * (TM + TN) * 1024
+                          : MODE == MODE_COOP64 ? (size_t) R * 2 * (TM + TN) * 1024
+                          : coop                ? (size_t) R * KH * (TM + TN) * 1024
                                                 : (size_t) 4 * R * (TM + TN) * 1024;
-    constexpr size_t red = MODE == MODE_COOP ? (size_t) (16 * TN) * (16 * TM + 4) * 4
-                                             : (size_t) 4 * (16 * (TN < 4 ? TN : 4)) * (16 * TM + 4) * 4;
+    constexpr size_t red = coop ? (size_t) (16 * TN) * (16 * TM + 4) * 4
+                                : (size_t) 4 * (16 * (TN < 4 ? TN : 4)) * (16 * TM + 4) * 4;
     return ring > red ? ring : red;
 }
 
 // read by fragments of the implicit im2col that fall into the zero padding
-__device__ __attribute__((aligned(16))) uint16_t g_zero_row[32];
+__device__ __attribute__((aligned(16))) uint16_t g_zero_row[64];
 
 constexpr bool epi_swiglu(int epi) { return epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_BF16; }
 
@@ -135,9 +164,11 @@ template <int TM, int TN, int R, int MODE, int EPI, int KH = 1, bool CONV = fals
 __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = KH * L * 1024;
-    constexpr bool COOP = MODE == MODE_COOP, DIRECT = MODE == MODE_DIRECT;
+    constexpr bool PIPE = MODE == MODE_COOP_PIPE, C64 = MODE == MODE_COOP64;
+    constexpr bool COOP = MODE == MODE_COOP || PIPE || C64, DIRECT = MODE == MODE_DIRECT;
     static_assert(!COOP || (TM % 2 == 0 && TN % 2 == 0 && L % 4 == 0), "cooperative tile shape");
-    static_assert(COOP || KH == 1, "KH: 32-wide k tiles per cooperative stage");
+    static_assert((COOP && !PIPE && !C64) || KH == 1, "KH: 32-wide k tiles per cooperative stage");
+    static_assert(!PIPE || R >= 3, "pipelined fragments need three ring slots");
     static_assert(COOP || (!CONV && !epi_swiglu(EPI)), "convolutions and SwiGLU run cooperative tiles");
     constexpr int TMW = COOP ? TM / 2 : TM, TNW = COOP ? TN / 2 : TN;   // 16x16 tiles per wave
     // SwiGLU: row blocks [0, TM / 2) of the tile are W's, [TM / 2, TM) the
@@ -154,7 +185,7 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     const int KT = p.K >> 5;                                  // 32-wide k tiles
     const int kt0 = tc.split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
     const int nst = kt1 - kt0;
-    const int my_n = COOP ? nst / KH : nst > wave ? (nst - wave + 3) >> 2 : 0;   // stages this wave computes
+    const int my_n = C64 ? nst / 2 : COOP ? nst / KH : nst > wave ? (nst - wave + 3) >> 2 : 0;   // stages this wave computes
     const int wm = COOP ? (wave & 1) : 0, wn = COOP ? (wave >> 1) : 0;       // cooperative quadrant
 
     // A: tile (rb, kt) of the tiled weights at (rb * KT + kt) * 512 elements,
@@ -214,7 +245,199 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
 #pragma unroll
         for (int j = 0; j < TNW; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-    if constexpr (COOP) {
+    if constexpr (C64) {
+        // Stages of 64 k (k tiles kt0 + 2 t, + 1; the launcher checks that
+        // every K range holds an even number of tiles). A stage holds TM + TN
+        // units of 2 KiB: tiled weights as two 1 KiB MFMA fragments (k tile
+        // 2 t, 2 t + 1); row-major weights and activations as 16 rows x 128
+        // bytes, loaded as two blocks of 8 rows in which lane i fetches row
+        // 8 h + i / 8, 16-byte chunk (i % 8) ^ key, key = (i / 8) ^ 4 h: each
+        // row is one whole 128-byte line, and the MFMA read of chunk c of
+        // row t at block t / 8, row t % 8, slot c ^ key hits 16 distinct
+        // 16-byte bank groups over the 16 rows.
+        constexpr int U = TM + TN, LW = 2 * U / 4;
+        constexpr int USZ = 2048, STG = U * USZ;
+        const int ns = my_n;
+        const int r8 = lane >> 3;
+        // row-major operands: this lane's element offset inside a 16-row block, per block half h
+        int64_t aoff_l[2];
+        int chk[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            chk[h] = ((lane & 7) ^ r8 ^ (4 * h)) * 8;                 // bf16 elements
+            aoff_l[h] = (int64_t) (8 * h + r8) * p.ld_w + chk[h];
+        }
+        // B: token rows of this lane per (token block j, half h)
+        const uint16_t *bp[TN][2];
+        int bw[CONV ? TN : 1][2];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int n = min(bn0 + 16 * j + 8 * h + r8, p.N - 1);
+                if constexpr (CONV) {
+                    const int b = n / p.conv_ow, ow = n - b * p.conv_ow;
+                    bp[j][h] = (const uint16_t *) p.x + (int64_t) b * p.x_group_stride + chk[h];
+                    bw[j][h] = ow * p.conv_s - p.conv_p;
+                } else {
+                    bp[j][h] = (const uint16_t *) p.x + x_row(p, n) + chk[h];
+                }
+            }
+        // MFMA read offsets of this lane (token / row t = lane % 16, chunk 4 kh + lane / 16)
+        int roff[2];
+        {
+            const int tq = lane & 15, kc = lane >> 4;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+                roff[kh] = (tq >> 3) * 1024 + (tq & 7) * 128 + (((4 * kh + kc) ^ (tq & 7) ^ (4 * (tq >> 3))) * 16);
+        }
+        // this wave's loads, fixed per q for the whole K range: fragment
+        // f = wave + 4 q is unit f / 2, half f % 2; its source advances by
+        // `step` elements per stage (1024 for tiled weights, 64 otherwise)
+        const uint16_t *qsrc[LW];
+        int qlds[LW], qstep[LW], qconv[CONV ? LW : 1];
+#pragma unroll
+        for (int q = 0; q < LW; ++q) {
+            const int f = wave + 4 * q, u = f >> 1, h = f & 1;
+            qlds[q] = u * USZ + h * 1024;
+            if (CONV) qconv[CONV ? q : 0] = 0;
+            if (u < TM) {
+                if (p.w_tiled) {
+                    qsrc[q] = abase[u] + (int64_t) (kt0 + h) * 512;
+                    qstep[q] = 1024;
+                } else {
+                    const int rb = min((bm0 >> 4) + (SWIGLU ? u % (TM / 2) : u), (p.M >> 4) - 1);
+                    const uint16_t *wsrc = SWIGLU && u >= TM / 2 ? p.w3 : p.w;
+                    qsrc[q] = wsrc + (int64_t) rb * 16 * p.ld_w + aoff_l[h] + kt0 * 32;
+                    qstep[q] = 64;
+                }
+            } else {
+                const int j = u - TM;
+                if constexpr (CONV) {
+                    // implicit im2col: the row base (batch item) and first input position
+                    qsrc[q] = bp[j][h];
+                    qconv[q] = bw[j][h];
+                    qstep[q] = 0;
+                } else {
+                    qsrc[q] = bp[j][h] + kt0 * 32;
+                    qstep[q] = 64;
+                }
+            }
+        }
+        const bool qisb[4] = {(wave + 0) / 2 >= TM, (wave + 4) / 2 >= TM, (wave + 8) / 2 >= TM, (wave + 12) / 2 >= TM};
+        auto cissue = [&](int t, int slot) {
+            uint8_t *dst = lds + slot * STG;
+#pragma unroll
+            for (int q = 0; q < LW; ++q) {
+                if constexpr (CONV) {
+                    const bool isb = q < 4 ? qisb[q] : (wave + 4 * q) / 2 >= TM;
+                    if (isb) {
+                        const int k = (kt0 + 2 * t) * 32, kw = k / p.conv_ic, ic0 = k - kw * p.conv_ic;
+                        const int iw = qconv[q] + kw * p.conv_d;
+                        const int h = (wave + 4 * q) & 1;
+                        g2l16(iw >= 0 && iw < p.conv_iw ? qsrc[q] + (int64_t) iw * p.ld_x + ic0 : g_zero_row + chk[h],
+                              dst + qlds[q]);
+                        continue;
+                    }
+                }
+                g2l16(qsrc[q] + (int64_t) t * qstep[q], dst + qlds[q]);
+            }
+        };
+        // A fragment read offsets: tiled (lane order) or swizzled rows
+        int aro[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) aro[kh] = p.w_tiled ? kh * 1024 + lane * 16 : roff[kh];
+#pragma unroll
+        for (int s = 0; s < R - 1; ++s)
+            if (s < ns) cissue(s, s);
+        int slot = 0;
+        for (int t = 0; t < ns; ++t) {
+            wait_stages<LW, R - 1>(min(ns - 1 - t, R - 2));
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (t + R - 1 < ns) cissue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
+            const uint8_t *src = lds + slot * STG;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                bf16x8 a[TMW], b[TNW];
+#pragma unroll
+                for (int i = 0; i < TMW; ++i) a[i] = *(const bf16x8 *) (src + (wm * TMW + i) * USZ + aro[kh]);
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) b[j] = *(const bf16x8 *) (src + (TM + wn * TNW + j) * USZ + roff[kh]);
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TNW; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+            slot = slot + 1 == R ? 0 : slot + 1;
+        }
+    } else if constexpr (PIPE) {
+        // shared ring as below (KH = 1); the fragments of stage t + 1 are read
+        // into a second register set while stage t's MFMAs run, so the LDS
+        // latency overlaps the MFMAs. Slot of stage t - 1 (read during
+        // iteration t - 2) is refilled at iteration t.
+        constexpr int LW = L / 4;
+        const int ns = my_n;
+        auto cissue = [&](int t, int slot) {
+            uint8_t *dst = lds + slot * STAGE;
+            const int kt = kt0 + t;
+#pragma unroll
+            for (int q = 0; q < LW; ++q) {
+                const int f = wave + 4 * q;
+                if (f < TM) g2l16(abase[f] + (int64_t) kt * astep, dst + f * 1024);
+                else g2l16(bfrag(f - TM, kt), dst + f * 1024);
+            }
+        };
+        bf16x8 a0[TMW], b0[TNW], a1[TMW], b1[TNW];
+        auto cread = [&](int slot, bf16x8 (&a)[TMW], bf16x8 (&b)[TNW]) {
+            const uint8_t *src = lds + slot * STAGE + lane * 16;
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) a[i] = *(const bf16x8 *) (src + (wm * TMW + i) * 1024);
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) b[j] = *(const bf16x8 *) (src + (TM + wn * TNW + j) * 1024);
+        };
+#pragma unroll
+        for (int s = 0; s < R - 1; ++s)
+            if (s < ns) cissue(s, s);
+        if (ns > 0) {
+            wait_stages_seen<LW, R - 1>(min(ns - 1, R - 2));
+            wait_lgkm0_seen();
+            asm volatile("s_barrier" ::: "memory");
+            cread(0, a0, b0);
+        }
+        int slot = 0;
+        // the two register sets alternate (two iterations per loop trip), so
+        // the fragments being read are never the MFMAs' operands and the
+        // compiler's counter waits let the reads stay in flight
+        auto step = [&](int t, const bf16x8 (&ac)[TMW], const bf16x8 (&bc)[TNW], bf16x8 (&an)[TMW],
+                        bf16x8 (&bn)[TNW]) {
+            const int nslot = slot + 1 == R ? 0 : slot + 1;
+            if (t + 1 < ns) {
+                // stage t + 1 has landed for every wave, and every wave is
+                // done with iteration t - 1 (its reads of stage t)
+                wait_stages_seen<LW, R - 1>(min(ns - 2 - t, R - 3));
+                wait_lgkm0_seen();
+                asm volatile("s_barrier" ::: "memory");
+                cread(nslot, an, bn);
+                if (t + R - 1 < ns) cissue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
+            }
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[i], bc[j], acc[i][j], 0, 0, 0);
+            slot = nslot;
+        };
+        // in the loop both steps read ahead (provably, so the compiler's
+        // waits stay exact); the last one or two steps follow it
+        int t = 0;
+        for (; t + 2 < ns; t += 2) {
+            step(t, a0, b0, a1, b1);
+            step(t + 1, a1, b1, a0, b0);
+        }
+        if (t < ns) step(t, a0, b0, a1, b1);
+        if (t + 1 < ns) step(t + 1, a1, b1, a0, b0);
+    } else if constexpr (COOP) {
         // shared ring of R stages of KH 32-wide k tiles (the launcher checks
         // that KH divides the tiles of every K range); wave w loads fragments
         // w, w + 4, ... of each stage, fragment h * L + f being tile h's A
@@ -473,6 +696,8 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
         p.tiles_n = (p.N + BN - 1) / BN;
         p.kt_split = (p.K / 32 + p.splits - 1) / p.splits;
         if (KH > 1 && ((p.K / 32) % p.splits || p.kt_split % KH)) return hipErrorInvalidValue;
+        if (MODE == MODE_COOP64 && ((p.K / 32) % p.splits || p.kt_split % 2 || (CONV && p.conv_ic % 64)))
+            return hipErrorInvalidValue;
         p.block_begin = (nblocks + 7) & ~7;
         nblocks = p.block_begin + p.tiles_m * p.tiles_n * p.splits;
     }
@@ -502,13 +727,13 @@ hipError_t ks_epi(GemmGroup &g, int epi, hipStream_t s) {
     }
 }
 
-template <int TM, int TN, int R, bool CONV>
+template <int TM, int TN, int R, bool CONV, int MODE = MODE_COOP>
 hipError_t conv_epi(GemmGroup &g, int epi, hipStream_t s) {
     switch (epi) {
-        case EPI_STORE_F32: return ks_launch<TM, TN, R, MODE_COOP, EPI_STORE_F32, 1, CONV>(g, s);
-        case EPI_STORE_BF16: return ks_launch<TM, TN, R, MODE_COOP, EPI_STORE_BF16, 1, CONV>(g, s);
-        case EPI_SWIGLU_F32: return ks_launch<TM, TN, R, MODE_COOP, EPI_SWIGLU_F32, 1, CONV>(g, s);
-        case EPI_SWIGLU_BF16: return ks_launch<TM, TN, R, MODE_COOP, EPI_SWIGLU_BF16, 1, CONV>(g, s);
+        case EPI_STORE_F32: return ks_launch<TM, TN, R, MODE, EPI_STORE_F32, 1, CONV>(g, s);
+        case EPI_STORE_BF16: return ks_launch<TM, TN, R, MODE, EPI_STORE_BF16, 1, CONV>(g, s);
+        case EPI_SWIGLU_F32: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_F32, 1, CONV>(g, s);
+        case EPI_SWIGLU_BF16: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_BF16, 1, CONV>(g, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -533,11 +758,24 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
             return hipErrorInvalidValue;
         tiles += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 63) / 64);
     }
-    // 128 x 64 tiles once they fill the 256 CUs about twice, 64 x 64 below
-    // (the crossover measured on the DiT projections)
-    if (tiles >= 512)
-        return conv ? conv_epi<8, 4, 4, true>(g, epi, s) : conv_epi<8, 4, 4, false>(g, epi, s);
-    return conv ? conv_epi<4, 4, 4, true>(g, epi, s) : conv_epi<4, 4, 4, false>(g, epi, s);
+    // Tile shape, measured on MI355X over the convolution / MLP / DiT shapes:
+    // with K % 64 == 0 (and IC % 64 == 0 for convolutions) the 64-wide row
+    // stages, 128 x 64 tiles (2 stages) from ~400 such tiles, 64 x 64 tiles
+    // (3 stages) below; otherwise the 32-wide stages, 128 x 64 from ~512
+    // tiles. TSK_COOP_CFG forces a shape (12, 22, 28, 29, 30, 32) for sweeps.
+    bool k64 = true;
+    for (int i = 0; i < g.nprob; ++i) k64 = k64 && g.p[i].K % 64 == 0 && (!conv || g.p[i].conv_ic % 64 == 0);
+    int cfg = k64 ? (tiles >= 400 ? 29 : 30) : (tiles >= 512 ? 12 : 22);
+    if (const char *e = getenv("TSK_COOP_CFG")) cfg = atoi(e);
+    if (!k64 && cfg >= 28) cfg = tiles >= 512 ? 12 : 22;
+    switch (cfg) {
+        case 12: return conv ? conv_epi<8, 4, 4, true>(g, epi, s) : conv_epi<8, 4, 4, false>(g, epi, s);
+        case 28: return conv ? conv_epi<8, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 3, false, MODE_COOP64>(g, epi, s);
+        case 29: return conv ? conv_epi<8, 4, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 2, false, MODE_COOP64>(g, epi, s);
+        case 30: return conv ? conv_epi<4, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<4, 4, 3, false, MODE_COOP64>(g, epi, s);
+        case 32: return conv ? conv_epi<8, 8, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 8, 2, false, MODE_COOP64>(g, epi, s);
+        default: return conv ? conv_epi<4, 4, 4, true>(g, epi, s) : conv_epi<4, 4, 4, false>(g, epi, s);
+    }
 }
 
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn) {
@@ -572,7 +810,7 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     }
     for (int i = 0; i < g.nprob; ++i)
         if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
-                                cfg == 22 || cfg == 23
+                                cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33
                             ? 64
                             : 128) &&
             epi == EPI_QKV)
@@ -601,6 +839,16 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         case 21: return ks_epi<8, 4, 2, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 2 stages
         case 22: return ks_epi<4, 4, 4, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 4 stages
         case 23: return ks_epi<4, 4, 3, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 3 stages
+        case 24: return ks_epi<8, 4, 4, MODE_COOP_PIPE>(g, epi, s);   // 128 x 64 cooperative, pipelined, 4 stages
+        case 25: return ks_epi<4, 4, 4, MODE_COOP_PIPE>(g, epi, s);   // 64 x 64 cooperative, pipelined, 4 stages
+        case 26: return ks_epi<8, 4, 5, MODE_COOP_PIPE>(g, epi, s);   // 128 x 64 cooperative, pipelined, 5 stages
+        case 27: return ks_epi<8, 8, 4, MODE_COOP_PIPE>(g, epi, s);   // 128 x 128 cooperative, pipelined, 4 stages
+        case 28: return ks_epi<8, 4, 3, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 3 stages of 64 k rows
+        case 29: return ks_epi<8, 4, 2, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 2 stages of 64 k rows
+        case 30: return ks_epi<4, 4, 3, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 3 stages of 64 k rows
+        case 31: return ks_epi<4, 4, 2, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 2 stages of 64 k rows
+        case 32: return ks_epi<8, 8, 2, MODE_COOP64>(g, epi, s);   // 128 x 128 cooperative, 2 stages of 64 k rows
+        case 33: return ks_epi<4, 4, 4, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 4 stages of 64 k rows
         default: return hipErrorInvalidValue;
     }
 }
