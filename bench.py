@@ -9,8 +9,9 @@ t = 0.5. Inputs are resident in HBM before the timed region.
 
 Prints ONE JSON line: steps/s (value), the roofline of the dominant kernel
 class (measured with HIP events around its launches inside the timed steps),
-attention TFLOP/s at 9 s and 30 s, and the CPU baseline (the oracle's
-restatement of the same flow step on this host's cores).
+attention TFLOP/s at 9 s and 30 s, the reference graph's SwiGLU conv MLP and
+k3 convolution at 30 s, and the CPU baseline (the oracle's restatement of the
+same flow step on this host's cores).
 """
 import argparse
 import json
@@ -79,6 +80,41 @@ def cpu_baseline(weights, lat, t, txt, threads):
     return {"value": round(1.0 / dt, 4), "unit": "steps/s", "cores": threads, "kind": "port",
             "sample": f"one full 21-block CFG-batched flow step at 9 s (B=2, 194+77 tokens), "
                       f"oracle C restatement of ggml-cpu semantics, {threads} threads, {dt:.2f} s"}
+
+
+def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
+    """convmlp and conv_cl (src/mmdit.cpp:28-44) on device-resident operands:
+    us per call (HIP events around `reps` back-to-back calls) and TFLOP/s."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+
+    def kernel(oc, ic):
+        w = (rng.standard_normal((oc, ic, 3)) * 0.02).astype(np.float32)
+        u = w.view(np.uint32)
+        bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)   # RNE to bf16
+        return tsk.conv1d_pack_weight(tsk.bf16_to_device(bits))
+
+    w1, w3, w2, wl = kernel(F, H), kernel(F, H), kernel(H, F), kernel(H, H)
+    x = tsk.to_device(rng.standard_normal((B, S, H)).astype(np.float32))
+    y = tsk.empty((B, S, H))
+    out = {}
+    for name, fn, flop in (
+            ("conv_mlp_swiglu", lambda: tsk.conv_mlp_swiglu(w1, w3, w2, x, out=y), 3 * 2.0 * B * S * 3 * H * F),
+            ("conv1d_linear1", lambda: tsk.conv1d(wl, x, out=y), 2.0 * B * S * 3 * H * H)):
+        for _ in range(3):
+            fn()
+        tsk.synchronize()
+        s, e = tsk.Event(), tsk.Event()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        tsk.synchronize()
+        us = s.elapsed_ms(e) / reps * 1e3
+        tf = flop / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 2), "tflops": round(tf, 1), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "shape": f"B={B} S={S} {H}->{F}->{H} k3" if name == "conv_mlp_swiglu" else f"B={B} S={S} {H}->{H} k3"}
+    return out
 
 
 def copy_calibration(nbytes=256 << 20, reps=5):
@@ -169,6 +205,11 @@ def main():
     sample30 = {"steps": 24, "cfg_scale": 5.0, "latent_tokens": 646, "seconds": round(wall, 5),
                 "sampler_steps_per_s": round(24 / wall, 2), "ms_per_step": round(wall / 24 * 1e3, 4)}
 
+    # the reference graph's convolution glue at 30 s (B = 2, 646 positions):
+    # convmlp 1024 -> 2816 -> 1024 (k3, padding 1, SwiGLU) and a conv_cl
+    # linear1 1024 -> 1024 (k3), BF16 kernels packed kw-major once, f32 input
+    conv30 = conv_bench(tsk, reps=max(5, args.steps))
+
     dom = max(roles9, key=lambda r: roles9[r][0])
     rf = roofline(dom, *roles9[dom])
     rf["launches_per_step"] = roles9[dom][1] // args.steps
@@ -207,6 +248,7 @@ def main():
         "ms_per_step_with_kernel_events": round(ms_timed, 4),
         "breakdown_9s": breakdown(roles9, args.steps),
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
+        "conv_30s": conv30,
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9
