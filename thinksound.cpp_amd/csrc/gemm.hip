@@ -18,6 +18,7 @@
 #include "tsk_common.h"
 #include "tsk_internal.h"
 
+#include <cstdlib>
 #include <cstring>
 
 namespace tsk {
@@ -309,6 +310,174 @@ void gemm_q8_kernel(const GemmParams p) {
         }
 }
 
+// ------------------------------------------------------------------ Q8_0, cooperative tiles
+// Four waves split a BM x BN tile 2 x 2 and share an LDS ring of 128-k stages
+// (four Q8_0 blocks): each 16-row operand unit is 16 rows x 128 int8, fetched
+// by direct global->LDS loads as two blocks of 8 whole 128-byte rows with the
+// XOR-swizzled chunk order of the cooperative bf16 tiles (lane i: row i / 8,
+// chunk (i % 8) ^ (i / 8) ^ 4 h), so the MFMA reads are conflict-free and
+// every fetched line is used whole. The tile's block scales are staged once
+// into LDS as f32 [block][row] (weights) and [block][token] (activations).
+// Per block: one int8 MFMA 16x16x32 gives the exact integer block dot, then
+// acc += float(isum) * (d_w * d_x) -- the same expression, in the same block
+// order, as gemm_q8_kernel, so both produce the same bits.
+namespace {
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void q8_g2l16(const void *src, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *) lds_base, 16, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void q8_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+}  // namespace
+
+template <int TM, int TN, int R, int EPI, bool YBF16>
+__global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int tiles_m, int tiles_n) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int BM = 16 * TM, BN = 16 * TN, TMW = TM / 2, TNW = TN / 2;
+    constexpr int U = TM + TN, USZ = 2048, STG = U * USZ, LW = 2 * U / 4;
+    static_assert(TM % 2 == 0 && TN % 2 == 0 && (2 * U) % 4 == 0 && R >= 2 && R <= 4, "tile shape");
+    const int KB = p.K / 32, ns = p.K / 128;
+    const int li = blockIdx.x;
+    int tm, tn;
+    if ((tiles_m & 7) == 0) {
+        // XCD x (= workgroup id mod 8) owns m tiles x, x + 8, ... and every token tile of each
+        const int sidx = li >> 3;
+        tm = (li & 7) + 8 * (sidx / tiles_n);
+        tn = sidx % tiles_n;
+    } else {
+        tm = li % tiles_m;
+        tn = li / tiles_m;
+    }
+    if (tm >= tiles_m || tn >= tiles_n) return;
+    const int bm0 = tm * BM, bn0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    // block scales of the tile, f32: dws[kb][row], dxs[kb][token]
+    float *dws = (float *) (lds + R * STG);
+    float *dxs = dws + KB * BM;
+    // lane = row (token): four blocks per load, LDS writes of consecutive rows
+    // for one block (conflict-free)
+    for (int e = tid; e < (KB / 4) * BM; e += 256) {
+        const int row = e % BM, q4 = e / BM;
+        const u32x2 v = *(const u32x2 *) (p.dw + (int64_t) min(bm0 + row, p.M - 1) * KB + 4 * q4);
+        const uint16_t *h = (const uint16_t *) &v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dws[(4 * q4 + c) * BM + row] = f16_bits_to_f32(h[c]);
+    }
+    for (int e = tid; e < (KB / 4) * BN; e += 256) {
+        const int tok = e % BN, q4 = e / BN;
+        const f32x4 v = *(const f32x4 *) (p.dx + (int64_t) min(bn0 + tok, p.N - 1) * KB + 4 * q4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dxs[(4 * q4 + c) * BN + tok] = v[c];
+    }
+    __syncthreads();
+
+    // this wave's loads: fragment f = wave + 4 q is unit f / 2 (A units first), half f % 2
+    const int r8 = lane >> 3;
+    const int8_t *qsrc[LW];
+    int qlds[LW];
+#pragma unroll
+    for (int q = 0; q < LW; ++q) {
+        const int f = wave + 4 * q, u = f >> 1, h = f & 1;
+        const int chunk = ((lane & 7) ^ r8 ^ (4 * h)) * 16;
+        qlds[q] = u * USZ + h * 1024;
+        if (u < TM) {
+            const int rb = min((bm0 >> 4) + u, (p.M >> 4) - 1);
+            qsrc[q] = p.qw + (int64_t) (rb * 16 + 8 * h + r8) * p.K + chunk;
+        } else {
+            const int n = min(bn0 + 16 * (u - TM) + 8 * h + r8, p.N - 1);
+            qsrc[q] = p.qx + (int64_t) n * p.K + chunk;
+        }
+    }
+    auto issue = [&](int t, int slot) {
+        uint8_t *dst = lds + slot * STG;
+#pragma unroll
+        for (int q = 0; q < LW; ++q) q8_g2l16(qsrc[q] + (int64_t) t * 128, dst + qlds[q]);
+    };
+    // MFMA operand read offsets: row t = lane % 16, bytes 32 b + 8 (lane / 16) of the row
+    int roff[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int c = 2 * b + (lg >> 1);
+        roff[b] = (lr >> 3) * 1024 + (lr & 7) * 128 + ((c ^ (lr & 7) ^ (4 * (lr >> 3))) * 16) + (lg & 1) * 8;
+    }
+
+    f32x4 acc[TMW][TNW];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+#pragma unroll
+    for (int st = 0; st < R - 1; ++st)
+        if (st < ns) issue(st, st);
+    int slot = 0;
+    for (int t = 0; t < ns; ++t) {
+        // own loads of stage t landed (at most min(ns - 1 - t, R - 2) later stages in flight)
+        const int rem = min(ns - 1 - t, R - 2);
+        if constexpr (R >= 4) {
+            if (rem >= 2) q8_wait_vm<2 * LW>();
+            else if (rem == 1) q8_wait_vm<LW>();
+            else q8_wait_vm<0>();
+        } else if constexpr (R == 3) {
+            if (rem >= 1) q8_wait_vm<LW>();
+            else q8_wait_vm<0>();
+        } else {
+            q8_wait_vm<0>();
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + R - 1 < ns) issue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
+        const uint8_t *src = lds + slot * STG;
+        // all block MFMAs of the stage first (independent results), then the
+        // rescales in block order, so no MFMA waits on the previous one's read-out
+        i32x4 isum[4][TMW][TNW];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            long a[TMW], bq[TNW];
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) a[i] = *(const long *) (src + (wm * TMW + i) * USZ + roff[b]);
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) bq[j] = *(const long *) (src + (TM + wn * TNW + j) * USZ + roff[b]);
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+                    isum[b][i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bq[j], i32x4{0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int kb = 4 * t + b;
+            f32x4 dwv[TMW];
+            float dxv[TNW];
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) dwv[i] = *(const f32x4 *) &dws[kb * BM + 16 * (wm * TMW + i) + 4 * lg];
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) dxv[j] = dxs[kb * BN + 16 * (wn * TNW + j) + lr];
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] += (float) isum[b][i][j][r] * (dwv[i][r] * dxv[j]);
+        }
+        slot = slot + 1 == R ? 0 : slot + 1;
+    }
+
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+            const int m0 = bm0 + 16 * (wm * TMW + i) + 4 * lg;
+            const int n = bn0 + 16 * (wn * TNW + j) + lr;
+            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
+        }
+}
+
 // ------------------------------------------------------------------ activation quantization
 // One thread per 32-block: d = amax/127 (stored as the fp32 value of its fp16
 // rounding), q = rne(x * (127/amax)) — ggml-cpu's x86 quantize_row_q8_0.
@@ -398,7 +567,61 @@ hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s) {
     return launch_gemm_group(g, p.x_f32 ? GEMM_X_F32 : 0, p.y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32, s);
 }
 
+namespace {
+
+template <int TM, int TN, int R, int EPI, bool YBF16>
+hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
+    constexpr int BM = 16 * TM, BN = 16 * TN;
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) (p.K / 32) * (BM + BN) * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    auto kern = gemm_q8c_kernel<TM, TN, R, EPI, YBF16>;
+    static size_t attr = 0;   // dynamic LDS opted in so far for this kernel
+    if (lds > attr) {
+        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
+            (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
+        attr = lds;
+    }
+    launch_kernel(kern, dim3(tiles_m * tiles_n), dim3(256), lds, s, p, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+template <int TM, int TN, int R, bool YBF16>
+hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
+    switch (p.epi) {
+        case EPI_GELU: return q8c_launch<TM, TN, R, EPI_GELU, YBF16>(p, s);
+        case EPI_GATE_RES: return q8c_launch<TM, TN, R, EPI_GATE_RES, false>(p, s);
+        case EPI_GEGLU:
+            if (p.M % 4 || p.y_bf16) return hipErrorInvalidValue;
+            return q8c_launch<TM, TN, R, EPI_GEGLU, false>(p, s);
+        default: return q8c_launch<TM, TN, R, EPI_STORE, YBF16>(p, s);
+    }
+}
+
+}  // namespace
+
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
+    // cooperative tiles when the planes allow them: K % 128 (four-block
+    // stages), M % 16, 16-byte aligned rows and block scales that fit in LDS.
+    // Measured on MI355X at 1446 rows: 64 x 64 tiles with a 2-stage ring win
+    // for K <= 2048 (1024 -> 3072: 51.5 -> 36.0 us); at K = 4096 the 2 x 2-wave
+    // kernel below stays faster (its K loop needs no staged scales).
+    const bool coop = p.K % 128 == 0 && p.K <= 2048 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
+                      ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
+                      (size_t) 3 * 8 * 2048 + (size_t) (p.K / 32) * 128 * 4 <= 160 * 1024;
+    if (coop) {
+        // TSK_Q8_CFG picks a tile shape for sweeps: 1 = 64 x 64 / 3 stages,
+        // 2 = 64 x 64 / 2 stages (default), 3 = 128 x 64 / 2 stages, 4 = 64 x 128 / 2 stages
+        int cfg = 2;
+        if (const char *e = getenv("TSK_Q8_CFG")) cfg = atoi(e);
+        if ((cfg == 3 || cfg == 4) && (size_t) 2 * 12 * 2048 + (size_t) (p.K / 32) * 192 * 4 > 160 * 1024) cfg = 1;
+        switch (cfg) {
+            case 2: return p.y_bf16 ? q8c_epi<4, 4, 2, true>(p, s) : q8c_epi<4, 4, 2, false>(p, s);
+            case 3: return p.y_bf16 ? q8c_epi<8, 4, 2, true>(p, s) : q8c_epi<8, 4, 2, false>(p, s);
+            case 4: return p.y_bf16 ? q8c_epi<4, 8, 2, true>(p, s) : q8c_epi<4, 8, 2, false>(p, s);
+            default: return p.y_bf16 ? q8c_epi<4, 4, 3, true>(p, s) : q8c_epi<4, 4, 3, false>(p, s);
+        }
+    }
     return p.y_bf16 ? gemm_q8_epi<2, 2, 2, 2, true>(p, s) : gemm_q8_epi<2, 2, 2, 2, false>(p, s);
 }
 
