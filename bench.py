@@ -10,7 +10,8 @@ t = 0.5. Inputs are resident in HBM before the timed region.
 Prints ONE JSON line: steps/s (value), the roofline of the dominant kernel
 class (measured with HIP events around its launches inside the timed steps),
 attention TFLOP/s at 9 s and 30 s, the reference graph's SwiGLU conv MLP and
-k3 convolution at 30 s, and the CPU baseline (the oracle's restatement of the
+k3 convolution at 30 s, the Q8_0 projection GEMMs at 30 s, the 24-layer T5
+encoder stack, and the CPU baseline (the oracle's restatement of the
 same flow step on this host's cores).
 """
 import argparse
@@ -24,6 +25,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
 
 
 def make_inputs(B, T, seed=4242):
@@ -115,6 +117,81 @@ def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
         out[name] = {"us": round(us, 2), "tflops": round(tf, 1), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                      "shape": f"B={B} S={S} {H}->{F}->{H} k3" if name == "conv_mlp_swiglu" else f"B={B} S={S} {H}->{H} k3"}
     return out
+
+
+def q8_blocks(rng, M, K, scale):
+    """ggml Q8_0 blocks (M, K/32, 34) uint8: fp16 scale then int8 values uniform in [-127, 127]."""
+    import numpy as np
+    qs = rng.integers(-127, 128, size=(M, K // 32, 32), dtype=np.int8)
+    d = np.full((M, K // 32, 1), np.float16(scale)).view(np.uint8)
+    return np.ascontiguousarray(np.concatenate([d.reshape(M, K // 32, 2), qs.view(np.uint8)], axis=2))
+
+
+def q8_bench(tsk, reps=10, N=1446, seed=5):
+    """The four Q8_0 projection GEMMs at 30 s (2 x 723 rows), weights repacked
+    once, activations quantized per call (ggml's conversion of src1)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    rows, tot_us, tot_ops = {}, 0.0, 0.0
+    for K, M in ((1024, 3072), (1024, 1024), (1024, 4096), (4096, 1024)):
+        w = tsk.q8_0_repack(tsk.to_device(q8_blocks(rng, M, K, 1.0 / (127.0 * np.sqrt(K)))))
+        x = tsk.to_device(rng.standard_normal((N, K)).astype(np.float32))
+        y = tsk.empty((N, M))
+        fn = lambda: tsk.mul_mat(w, x, out=y, a_type=tsk.Q8_0_SPLIT)
+        for _ in range(3):
+            fn()
+        tsk.synchronize()
+        s, e = tsk.Event(), tsk.Event()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        tsk.synchronize()
+        us = s.elapsed_ms(e) / reps * 1e3
+        ops = 2.0 * N * K * M
+        rows[f"{K}->{M}"] = {"us": round(us, 2), "tops": round(ops / us / 1e6, 1)}
+        tot_us += us
+        tot_ops += ops
+    return {"rows": N, "gemms": rows, "total_us": round(tot_us, 2), "tops": round(tot_ops / tot_us / 1e6, 1),
+            "frac_of_int8_peak": round(tot_ops / tot_us / 1e6 / PEAK_INT8_TOPS, 4)}
+
+
+def t5_bench(tsk, seed=44, reps=3):
+    """Configuration 4: the 24-layer T5 encoder stack on 512 tokens (last 64
+    padded), random Q8_0 weights; wall time of one encode with the operands
+    resident (median of reps)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    t5 = tsk.T5(tsk.t5_config())
+    for name, ne, ty in t5.tensors():
+        if ty == 8:
+            s = 1.0 / np.sqrt(ne[0] * 127.0 * 127.0 / 3.0)
+            if name.endswith(".q") or name.endswith(".k"):
+                s /= np.sqrt(8.0)
+            t5.set_tensor(name, q8_blocks(rng, ne[1], ne[0], s))
+        elif name == "rel_bias":
+            t5.set_tensor(name, rng.standard_normal((ne[1], ne[0])).astype(np.float32))
+        else:
+            t5.set_tensor(name, (1.0 + 0.1 * rng.standard_normal(ne[0])).astype(np.float32))
+    c = t5.cfg
+    x = tsk.to_device(rng.standard_normal((512, c.d_model)).astype(np.float32))
+    ids = np.arange(1, 513, dtype=np.int32)
+    ids[-64:] = 0
+    out = tsk.empty((512, c.d_model))
+    t5.encode_device(x, ids, out)
+    tsk.synchronize()
+    walls = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        t5.encode_device(x, ids, out)
+        tsk.synchronize()
+        walls.append(time.perf_counter() - t0)
+    wall = sorted(walls)[len(walls) // 2]
+    per_layer = 2.0 * 512 * c.d_model * (3 * c.n_heads * c.d_kv + c.n_heads * c.d_kv + 2 * c.d_ff) + \
+        2.0 * 512 * c.d_ff * c.d_model + 4.0 * c.n_heads * 512 * 512 * c.d_kv
+    t5.close()
+    return {"layers": c.n_layers, "tokens": 512, "ms": round(wall * 1e3, 3),
+            "tops": round(per_layer * c.n_layers / wall / 1e12, 1)}
 
 
 def copy_calibration(nbytes=256 << 20, reps=5):
@@ -209,6 +286,9 @@ def main():
     # convmlp 1024 -> 2816 -> 1024 (k3, padding 1, SwiGLU) and a conv_cl
     # linear1 1024 -> 1024 (k3), BF16 kernels packed kw-major once, f32 input
     conv30 = conv_bench(tsk, reps=max(5, args.steps))
+    # configuration 3's Q8_0 projection GEMMs at 30 s and configuration 4's T5 stack
+    q8 = q8_bench(tsk)
+    t5 = t5_bench(tsk)
 
     dom = max(roles9, key=lambda r: roles9[r][0])
     rf = roofline(dom, *roles9[dom])
@@ -249,6 +329,8 @@ def main():
         "breakdown_9s": breakdown(roles9, args.steps),
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
         "conv_30s": conv30,
+        "q8_0_projections_30s": q8,
+        "t5_encoder_config4": t5,
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9

@@ -713,6 +713,15 @@ class T5:
                                          int(final_norm), out.ctypes.data, _stream()))
         return out
 
+    def encode_device(self, x, ids, out=None):
+        """x: (n, d_model) f32 DeviceArray, ids: (n,) int32 host array -> (n, d_model) DeviceArray."""
+        import numpy as np
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = DeviceArray(x.shape, "f32") if out is None else out
+        check(load().tsk_t5_encode_device(self.h, x.shape[0], x.data_ptr(), ids.ctypes.data, out.data_ptr(),
+                                          _stream()))
+        return out
+
 
 # ---------------------------------------------------------------- GGUF files
 class Gguf:
