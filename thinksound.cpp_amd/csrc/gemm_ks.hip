@@ -578,20 +578,103 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
         return v;
     };
 
+    auto sum1 = [&](int nl, int ml) -> float {
+        const float *r0 = red + nl * LDY + ml;
+        float v = *r0;
+        if constexpr (!COOP) {
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += r0[w * (BNC * LDY)];
+        }
+        return v;
+    };
+
     if constexpr (EPI == EPI_QKV) {
-        // one 16-lane group per (token, head): lane sl holds dims 4 sl .. 4 sl + 3
+        // one 16-lane group per (token, head): lane sl holds dims 4 sl .. 4 sl + 3.
+        // Every global load of the epilogue (bias, norm weights, RoPE table) is
+        // issued before its first store: loads and stores share one counter, so
+        // a load behind a store would also wait for that store.
         const int H = p.M / 3, nh = H / 64;
         const int grp = tid >> 4, sl = tid & 15;
         constexpr int HPT = BM / 64;                 // heads per tile
-        for (int pp = grp; pp < BNC * HPT; pp += NT / 16) {
+        constexpr int U = BNC * HPT / (NT / 16);     // (token, head) pairs per lane group
+        if (bm0 >= 2 * H && p.seq >= BNC) {
+            // V tile -> V^T rows: lane (row ml, 4-position chunk) writes 4 consecutive
+            // key slots of one V^T row (vt_pos keeps aligned 4-runs together), so a
+            // row's 128 bytes leave as whole runs instead of 2-byte scatters. The
+            // tile's tokens span at most two batch items (seq >= BNC); part 0 is
+            // batch item b0 from s0, part 1 the next item from position 0.
+            const int n0 = bn0c, n1 = min(bn0c + BNC, p.N);
+            if (n0 < n1) {
+                const int b0 = n0 / p.seq, s0 = n0 - b0 * p.seq;
+                const int e0 = min(p.seq, s0 + (n1 - n0));
+                const int ca0 = (p.tok_off + s0) >> 2, cnt0 = ((p.tok_off + e0 - 1) >> 2) - ca0 + 1;
+                const int r1 = n1 - (b0 + 1) * p.seq;                   // tokens of item b0 + 1
+                const int ca1 = p.tok_off >> 2, cnt1 = r1 > 0 ? ((p.tok_off + r1 - 1) >> 2) - ca1 + 1 : 0;
+                constexpr int KR = BM / 64, CS = (BNC / 4 + 3 + 3) / 4;  // rows, chunk slots per lane
+                float bv[KR];
+#pragma unroll
+                for (int k = 0; k < KR; ++k) bv[k] = p.bias ? p.bias[bm0 + 16 * (wave + 4 * k) + (lane & 15)] : 0.0f;
+#pragma unroll
+                for (int k = 0; k < KR; ++k) {
+                    const int ml = 16 * (wave + 4 * k) + (lane & 15);
+                    const int f = bm0 + ml - 2 * H, head = f / 64, d = f % 64;
+#pragma unroll
+                    for (int i = 0; i < CS; ++i) {
+                        const int cj = (lane >> 4) + 4 * i;
+                        if (cj >= cnt0 + cnt1) continue;
+                        const int b = cj < cnt0 ? b0 : b0 + 1;
+                        const int gc = cj < cnt0 ? ca0 + cj : ca1 + cj - cnt0;
+                        float v[4];
+                        bool all = true;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int spos = 4 * gc + e - p.tok_off, n = b * p.seq + spos;
+                            const bool ok = spos >= 0 && spos < p.seq && n >= n0 && n < n1;
+                            v[e] = ok ? sum1(n - n0, ml) + bv[k] : 0.0f;
+                            all = all && ok;
+                        }
+                        uint16_t *row = p.vt + (((int64_t) b * nh + head) * 64 + d) * p.ldv + vt_pos(4 * gc);
+                        if (all) {
+                            const uint16_t o4[4] = {f32_to_f16_bits(v[0]), f32_to_f16_bits(v[1]),
+                                                    f32_to_f16_bits(v[2]), f32_to_f16_bits(v[3])};
+                            u32x2 w2;
+                            __builtin_memcpy(&w2, o4, 8);
+                            *(u32x2 *) row = w2;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int spos = 4 * gc + e - p.tok_off, n = b * p.seq + spos;
+                                if (spos >= 0 && spos < p.seq && n >= n0 && n < n1) row[e] = f32_to_f16_bits(v[e]);
+                            }
+                        }
+                    }
+                }
+            }
+        } else {
+        static_assert(U * (NT / 16) == BNC * HPT, "QKV epilogue pairs");
+        f32x4 xs[U], wvs[U], css[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int pp = grp + u * (NT / 16);
+            const int nl = pp / HPT, hl = pp % HPT;
+            const int n = bn0c + nl, f0 = bm0 + hl * 64;
+            const int sec = f0 / H, spos = (n < p.N ? n : 0) % p.seq;
+            xs[u] = sum4(nl, hl * 64 + 4 * sl);
+            if (p.bias) {
+                const f32x4 bv = *(const f32x4 *) (p.bias + f0 + 4 * sl);
+                xs[u] = f32x4{xs[u][0] + bv[0], xs[u][1] + bv[1], xs[u][2] + bv[2], xs[u][3] + bv[3]};
+            }
+            wvs[u] = sec < 2 ? *(const f32x4 *) ((sec ? p.kn_w : p.qn_w) + 4 * sl) : f32x4{0, 0, 0, 0};
+            css[u] = sec < 2 && p.rope ? *(const f32x4 *) (p.rope_cs + (int64_t) spos * 64 + 4 * sl)
+                                       : f32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int pp = grp + u * (NT / 16);
             const int nl = pp / HPT, hl = pp % HPT;
             const int n = bn0c + nl, f0 = bm0 + hl * 64;
             const bool live = n < p.N;
-            f32x4 x = sum4(nl, hl * 64 + 4 * sl);
-            if (p.bias) {
-                const f32x4 bv = *(const f32x4 *) (p.bias + f0 + 4 * sl);
-                x = f32x4{x[0] + bv[0], x[1] + bv[1], x[2] + bv[2], x[3] + bv[3]};
-            }
+            f32x4 x = xs[u];
             const int sec = f0 / H, head = (f0 % H) / 64;
             const int nn = live ? n : 0;
             const int b = nn / p.seq, spos = nn % p.seq;
@@ -599,12 +682,11 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
                 float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
                 for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
                 const float sc = 1.0f / sqrtf(ss / 64.0f + p.eps);
-                const float *w = sec ? p.kn_w : p.qn_w;
-                const f32x4 wv = *(const f32x4 *) (w + 4 * sl);
+                const f32x4 wv = wvs[u];
                 for (int e = 0; e < 4; ++e) x[e] = x[e] * sc * wv[e];
                 if (p.rope) {
                     // (cos, sin) of pairs 2 sl, 2 sl + 1 at position spos
-                    const f32x4 cs = *(const f32x4 *) (p.rope_cs + (int64_t) spos * 64 + 4 * sl);
+                    const f32x4 cs = css[u];
                     for (int q2 = 0; q2 < 2; ++q2) {
                         const float c = cs[2 * q2], sn = cs[2 * q2 + 1];
                         const float x0 = x[2 * q2], x1 = x[2 * q2 + 1];
@@ -628,6 +710,7 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
                     for (int e = 0; e < 4; ++e) vcol[(int64_t) e * p.ldv] = o4[e];
                 }
             }
+        }
         }
     } else if constexpr (SWIGLU) {
         // 8 consecutive features of one token per thread: silu(W x) * (W3 x)
@@ -810,7 +893,8 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     }
     for (int i = 0; i < g.nprob; ++i)
         if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
-                                cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33
+                                cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33 ||
+                                cfg == 34 || cfg == 35
                             ? 64
                             : 128) &&
             epi == EPI_QKV)
@@ -849,6 +933,8 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         case 31: return ks_epi<4, 4, 2, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 2 stages of 64 k rows
         case 32: return ks_epi<8, 8, 2, MODE_COOP64>(g, epi, s);   // 128 x 128 cooperative, 2 stages of 64 k rows
         case 33: return ks_epi<4, 4, 4, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 4 stages of 64 k rows
+        case 34: return ks_epi<4, 4, 5, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 5 stages of 64 k rows
+        case 35: return ks_epi<4, 4, 6, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 6 stages of 64 k rows
         default: return hipErrorInvalidValue;
     }
 }

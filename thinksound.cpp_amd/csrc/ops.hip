@@ -4,6 +4,8 @@
 //   repacking, and the DiT driver's glue (LN+modulate, QKV split, adaLN GEMV,
 //   CFG/Euler update).
 // One wave (64 lanes) or one 256-thread block per row; rows are streamed once.
+#include <cstdlib>
+
 #include "tsk_common.h"
 #include "tsk_internal.h"
 
@@ -253,36 +255,119 @@ __global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
     }
 }
 
+// The same row update with one wave per row and H = 256 NV: every load of the
+// row (residual, split slices, bias, gate, shift, scale) is issued before the
+// first reduction, and both reductions stay inside the wave (no LDS, no
+// barrier).
+template <bool YF32, int NV>
+__global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
+    int r = blockIdx.x, si = 0;
+    if (g.nstream > 1 && r >= g.s[0].rows) { r -= g.s[0].rows; si = 1; }
+    const LnStream &st = g.s[si];
+    constexpr int H = 256 * NV;
+    const int lane = threadIdx.x, b = r / st.rows_per_b;
+    float *xr = st.x + (int64_t) r * st.ld_x;
+    const float *sh = st.shift + (int64_t) b * st.ld_mod, *sc = st.scale + (int64_t) b * st.ld_mod;
+    f32x4 v[NV], shv[NV], scv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = (lane + 64 * j) * 4;
+        v[j] = *(const f32x4 *) (xr + i);
+        shv[j] = *(const f32x4 *) (sh + i);
+        scv[j] = *(const f32x4 *) (sc + i);
+    }
+    if (st.part) {
+        f32x4 acc[NV], gv[NV], bv[NV];
+        const float *gr = st.gate + (int64_t) b * st.ld_gate;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int i = (lane + 64 * j) * 4;
+            acc[j] = *(const f32x4 *) (st.part + (int64_t) r * H + i);
+            gv[j] = *(const f32x4 *) (gr + i);
+            bv[j] = st.bias ? *(const f32x4 *) (st.bias + i) : f32x4{0, 0, 0, 0};
+        }
+        for (int sp = 1; sp < st.nsplit; ++sp) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const f32x4 t = *(const f32x4 *) (st.part + sp * st.part_stride + (int64_t) r * H + (lane + 64 * j) * 4);
+                for (int e = 0; e < 4; ++e) acc[j][e] += t[e];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            for (int e = 0; e < 4; ++e) v[j][e] += gv[j][e] * (acc[j][e] + bv[j][e]);
+            *(f32x4 *) (xr + (lane + 64 * j) * 4) = v[j];
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) s += v[j][0] + v[j][1] + v[j][2] + v[j][3];
+    const float mean = wave_sum(s) / (float) H;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        for (int e = 0; e < 4; ++e) { const float d = v[j][e] - mean; s2 += d * d; }
+    const float rs = 1.0f / sqrtf(wave_sum(s2) / (float) H + g.eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = (lane + 64 * j) * 4;
+        float o[4];
+        for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mean) * rs * (scv[j][e] + 1.0f) + shv[j][e];
+        if constexpr (YF32) {
+            *(f32x4 *) ((float *) st.y + (int64_t) r * st.ld_y + i) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+            uint16_t ob[4];
+            for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16_bits(o[e]);
+            u32x2 w;
+            __builtin_memcpy(&w, ob, 8);
+            *(u32x2 *) ((uint16_t *) st.y + (int64_t) r * st.ld_y + i) = w;
+        }
+    }
+}
+
 // GEMV list: one wave per output row; lane k-slices of 8, f32 activations
-template <int MAXB>
+template <int MAXB, int RW>
 __global__ __launch_bounds__(256) void gemv_jobs_kernel(const GemvJob *jobs, int B, int K) {
+    // RW rows per wave: their weight loads are issued together and each
+    // activation slice is loaded once for all of them; every row is summed
+    // in the same order whatever RW (lane partials over k, then the wave sum)
     const GemvJob jb = jobs[blockIdx.y];
-    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int j0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
     const int lane = threadIdx.x & 63;
-    if (j >= jb.M) return;
-    const uint16_t *wr = jb.w + (int64_t) j * K;
-    float acc[MAXB];
-    for (int b = 0; b < MAXB; ++b) acc[b] = 0.0f;
+    if (j0 >= jb.M) return;
+    float acc[RW][MAXB];
+    for (int r = 0; r < RW; ++r)
+        for (int b = 0; b < MAXB; ++b) acc[r][b] = 0.0f;
     for (int k = lane * 8; k < K; k += 512) {
-        const u32x4 raw = *(const u32x4 *) (wr + k);
-        const uint16_t *h = (const uint16_t *) &raw;
-        float wv[8];
-        for (int e = 0; e < 8; ++e) wv[e] = bf16_bits_to_f32(h[e]);
+        u32x4 raw[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            raw[r] = j0 + r < jb.M ? *(const u32x4 *) (jb.w + (int64_t) (j0 + r) * K + k) : u32x4{0, 0, 0, 0};
         for (int b = 0; b < MAXB; ++b) {
             if (b >= B) break;
             const float *cr = jb.x + (int64_t) b * K + k;
             const f32x4 c0 = *(const f32x4 *) cr, c1 = *(const f32x4 *) (cr + 4);
-            acc[b] += wv[0] * c0[0] + wv[1] * c0[1] + wv[2] * c0[2] + wv[3] * c0[3] +
-                      wv[4] * c1[0] + wv[5] * c1[1] + wv[6] * c1[2] + wv[7] * c1[3];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const uint16_t *h = (const uint16_t *) &raw[r];
+                float wv[8];
+                for (int e = 0; e < 8; ++e) wv[e] = bf16_bits_to_f32(h[e]);
+                acc[r][b] += wv[0] * c0[0] + wv[1] * c0[1] + wv[2] * c0[2] + wv[3] * c0[3] +
+                             wv[4] * c1[0] + wv[5] * c1[1] + wv[6] * c1[2] + wv[7] * c1[3];
+            }
         }
     }
-    for (int b = 0; b < MAXB; ++b) {
-        if (b >= B) break;
-        const float s = wave_sum(acc[b]);
-        if (lane == 0) {
-            float v = s + (jb.bias ? jb.bias[j] : 0.0f);
-            if (jb.silu_out) v = v / (1.0f + __expf(-v));
-            jb.out[(int64_t) b * jb.ld_out + j] = v;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int j = j0 + r;
+        for (int b = 0; b < MAXB; ++b) {
+            if (b >= B) break;
+            const float s = wave_sum(acc[r][b]);
+            if (lane == 0 && j < jb.M) {
+                float v = s + (jb.bias ? jb.bias[j] : 0.0f);
+                if (jb.silu_out) v = v / (1.0f + __expf(-v));
+                jb.out[(int64_t) b * jb.ld_out + j] = v;
+            }
         }
     }
 }
@@ -501,16 +586,30 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
+    static const bool block_rows = std::getenv("TSK_LN_BLOCK") != nullptr;   // A/B against the block kernel
+    if (g.H == 1024 && !block_rows) {
+        if (g.y_f32) launch_kernel(ln_wave_kernel<true, 4>, dim3(rows), dim3(64), 0, s, g);
+        else launch_kernel(ln_wave_kernel<false, 4>, dim3(rows), dim3(64), 0, s, g);
+        return hipGetLastError();
+    }
     if (g.y_f32) launch_kernel(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
     else launch_kernel(ln_group_kernel<false>, dim3(rows), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K, hipStream_t s) {
-    dim3 grid(blocks_for(max_m, 4), njobs);
-    if (B <= 2) launch_kernel(gemv_jobs_kernel<2>, grid, dim3(256), 0, s, jobs_dev, B, K);
-    else if (B <= 8) launch_kernel(gemv_jobs_kernel<8>, grid, dim3(256), 0, s, jobs_dev, B, K);
-    else launch_kernel(gemv_jobs_kernel<32>, grid, dim3(256), 0, s, jobs_dev, B, K);
+    // rows per wave at B <= 2 (TSK_GEMV_RW = 1, 2, 4 for sweeps; 2 measured best on the adaLN lists)
+    static const int rw_env = std::getenv("TSK_GEMV_RW") ? std::atoi(std::getenv("TSK_GEMV_RW")) : 2;
+    if (B <= 2 && rw_env == 4)
+        launch_kernel(gemv_jobs_kernel<2, 4>, dim3(blocks_for(max_m, 16), njobs), dim3(256), 0, s, jobs_dev, B, K);
+    else if (B <= 2 && rw_env == 2)
+        launch_kernel(gemv_jobs_kernel<2, 2>, dim3(blocks_for(max_m, 8), njobs), dim3(256), 0, s, jobs_dev, B, K);
+    else if (B <= 2)
+        launch_kernel(gemv_jobs_kernel<2, 1>, dim3(blocks_for(max_m, 4), njobs), dim3(256), 0, s, jobs_dev, B, K);
+    else if (B <= 8)
+        launch_kernel(gemv_jobs_kernel<8, 2>, dim3(blocks_for(max_m, 8), njobs), dim3(256), 0, s, jobs_dev, B, K);
+    else
+        launch_kernel(gemv_jobs_kernel<32, 1>, dim3(blocks_for(max_m, 4), njobs), dim3(256), 0, s, jobs_dev, B, K);
     return hipGetLastError();
 }
 
