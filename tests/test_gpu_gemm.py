@@ -113,3 +113,23 @@ def test_q8_0_dequant_and_quant_bit_exact(env):
     g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "q8_0.npz"))
     kat = tsk.q8_0_dequantize(tsk.to_device(np.ascontiguousarray(g["kat_blocks"][:, None, :])))
     assert np.array_equal(kat.numpy(), g["kat_deq"])
+
+
+@pytest.mark.parametrize("N,K,M", [(512, 5120, 2048), (300, 4096, 1024), (77, 2176, 256)])
+def test_q8_0_cooperative_matches_2x2_wave_kernel(env, N, K, M, monkeypatch):
+    """The cooperative Q8_0 tiles stage block scales in 2048-k segments for long
+    K; each output still sums its blocks in block order, so it equals the
+    2 x 2-wave kernel bit for bit."""
+    tsk, orc = env
+    rng = np.random.default_rng(K + M)
+    blocks = np.zeros((M, K // 32, 34), np.uint8)
+    qs = rng.integers(-127, 128, size=(M, K // 32, 32)).astype(np.int8)
+    d = (np.abs(rng.standard_normal((M, K // 32))) * 0.02 / 127 + 1e-5).astype(np.float16)
+    blocks[..., :2] = d.view(np.uint8).reshape(M, K // 32, 2)
+    blocks[..., 2:] = qs.view(np.uint8)
+    x = tsk.to_device(rng.standard_normal((N, K)).astype(np.float32))
+    sp = tsk.q8_0_repack(tsk.to_device(blocks))
+    y = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
+    monkeypatch.setenv("TSK_Q8_OLD", "1")
+    y_old = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
+    assert np.array_equal(y, y_old)

@@ -357,24 +357,50 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     const int wm = wave & 1, wn = wave >> 1;
     const int lr = lane & 15, lg = lane >> 4;
 
-    // block scales of the tile, f32: dws[kb][row], dxs[kb][token]
+    // block scales of one segment of up to SEG blocks, f32: dws[kb][row],
+    // dxs[kb][token]. Lane = row (token): four blocks per load, LDS writes of
+    // consecutive rows for one block (conflict-free). A segment's scales are
+    // loaded into registers during the last stage of the previous segment and
+    // written to LDS at the next segment's first stage, between two barriers.
+    constexpr int SEG = 64, PW = (SEG / 4 * BM + 255) / 256, PX = (SEG / 4 * BN + 255) / 256;
+    constexpr int SPS = SEG / 4;                       // stages per segment
     float *dws = (float *) (lds + R * STG);
-    float *dxs = dws + KB * BM;
-    // lane = row (token): four blocks per load, LDS writes of consecutive rows
-    // for one block (conflict-free)
-    for (int e = tid; e < (KB / 4) * BM; e += 256) {
-        const int row = e % BM, q4 = e / BM;
-        const u32x2 v = *(const u32x2 *) (p.dw + (int64_t) min(bm0 + row, p.M - 1) * KB + 4 * q4);
-        const uint16_t *h = (const uint16_t *) &v;
+    float *dxs = dws + min(KB, SEG) * BM;
+    u32x2 pw[PW];
+    f32x4 px[PX];
+    auto load_scales = [&](int seg) {
+        const int kb0 = seg * SEG, nq = min(KB - kb0, SEG) / 4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dws[(4 * q4 + c) * BM + row] = f16_bits_to_f32(h[c]);
-    }
-    for (int e = tid; e < (KB / 4) * BN; e += 256) {
-        const int tok = e % BN, q4 = e / BN;
-        const f32x4 v = *(const f32x4 *) (p.dx + (int64_t) min(bn0 + tok, p.N - 1) * KB + 4 * q4);
+        for (int i = 0; i < PW; ++i) {
+            const int e = tid + 256 * i, row = e % BM, q4 = e / BM;
+            if (q4 < nq) pw[i] = *(const u32x2 *) (p.dw + (int64_t) min(bm0 + row, p.M - 1) * KB + kb0 + 4 * q4);
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dxs[(4 * q4 + c) * BN + tok] = v[c];
-    }
+        for (int i = 0; i < PX; ++i) {
+            const int e = tid + 256 * i, tok = e % BN, q4 = e / BN;
+            if (q4 < nq) px[i] = *(const f32x4 *) (p.dx + (int64_t) min(bn0 + tok, p.N - 1) * KB + kb0 + 4 * q4);
+        }
+    };
+    auto store_scales = [&](int seg) {
+        const int nq = min(KB - seg * SEG, SEG) / 4;
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            const int e = tid + 256 * i, row = e % BM, q4 = e / BM;
+            const uint16_t *h = (const uint16_t *) &pw[i];
+            if (q4 < nq)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) dws[(4 * q4 + c) * BM + row] = f16_bits_to_f32(h[c]);
+        }
+#pragma unroll
+        for (int i = 0; i < PX; ++i) {
+            const int e = tid + 256 * i, tok = e % BN, q4 = e / BN;
+            if (q4 < nq)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) dxs[(4 * q4 + c) * BN + tok] = px[i][c];
+        }
+    };
+    load_scales(0);
+    store_scales(0);
     __syncthreads();
 
     // this wave's loads: fragment f = wave + 4 q is unit f / 2 (A units first), half f % 2
@@ -420,7 +446,10 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     for (int t = 0; t < ns; ++t) {
         // own loads of stage t landed (at most min(ns - 1 - t, R - 2) later stages in flight)
         const int rem = min(ns - 1 - t, R - 2);
-        if constexpr (R >= 4) {
+        const bool seg_start = t > 0 && t % SPS == 0;
+        if (seg_start) {
+            q8_wait_vm<0>();                     // the segment's scale loads are the youngest
+        } else if constexpr (R >= 4) {
             if (rem >= 2) q8_wait_vm<2 * LW>();
             else if (rem == 1) q8_wait_vm<LW>();
             else q8_wait_vm<0>();
@@ -431,7 +460,13 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
             q8_wait_vm<0>();
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (seg_start) {
+            // every wave's reads of the previous segment's scales are done
+            store_scales(t / SPS);
+            __syncthreads();
+        }
         if (t + R - 1 < ns) issue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
+        if (t % SPS == SPS - 1 && t + 1 < ns) load_scales(t / SPS + 1);
         const uint8_t *src = lds + slot * STG;
         // all block MFMAs of the stage first (independent results), then the
         // rescales in block order, so no MFMA waits on the previous one's read-out
@@ -451,7 +486,7 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
         }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const int kb = 4 * t + b;
+            const int kb = 4 * (t % SPS) + b;
             f32x4 dwv[TMW];
             float dxv[TNW];
 #pragma unroll
@@ -573,7 +608,7 @@ template <int TM, int TN, int R, int EPI, bool YBF16>
 hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
     constexpr int BM = 16 * TM, BN = 16 * TN;
     const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
-    const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) (p.K / 32) * (BM + BN) * 4;
+    const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) std::min(p.K / 32, 64) * (BM + BN) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto kern = gemm_q8c_kernel<TM, TN, R, EPI, YBF16>;
     static size_t attr = 0;   // dynamic LDS opted in so far for this kernel
@@ -602,19 +637,18 @@ hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
 
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // cooperative tiles when the planes allow them: K % 128 (four-block
-    // stages), M % 16, 16-byte aligned rows and block scales that fit in LDS.
-    // Measured on MI355X at 1446 rows: 64 x 64 tiles with a 2-stage ring win
-    // for K <= 2048 (1024 -> 3072: 51.5 -> 36.0 us); at K = 4096 the 2 x 2-wave
-    // kernel below stays faster (its K loop needs no staged scales).
-    const bool coop = p.K % 128 == 0 && p.K <= 2048 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
+    // stages), M % 16, 16-byte aligned rows; block scales staged in segments
+    // of 2048 k. Measured on MI355X at 1446 rows: 64 x 64 tiles with a 2-stage
+    // ring (1024 -> 3072: 51.5 -> 36.0 us against the 2 x 2-wave kernel below,
+    // which stays for other shapes; TSK_Q8_OLD forces it for comparisons).
+    const bool coop = p.K % 128 == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
                       ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
-                      (size_t) 3 * 8 * 2048 + (size_t) (p.K / 32) * 128 * 4 <= 160 * 1024;
+                      !std::getenv("TSK_Q8_OLD");
     if (coop) {
         // TSK_Q8_CFG picks a tile shape for sweeps: 1 = 64 x 64 / 3 stages,
         // 2 = 64 x 64 / 2 stages (default), 3 = 128 x 64 / 2 stages, 4 = 64 x 128 / 2 stages
         int cfg = 2;
         if (const char *e = getenv("TSK_Q8_CFG")) cfg = atoi(e);
-        if ((cfg == 3 || cfg == 4) && (size_t) 2 * 12 * 2048 + (size_t) (p.K / 32) * 192 * 4 > 160 * 1024) cfg = 1;
         switch (cfg) {
             case 2: return p.y_bf16 ? q8c_epi<4, 4, 2, true>(p, s) : q8c_epi<4, 4, 2, false>(p, s);
             case 3: return p.y_bf16 ? q8c_epi<8, 4, 2, true>(p, s) : q8c_epi<8, 4, 2, false>(p, s);

@@ -63,6 +63,76 @@ __global__ void norm_kernel(const View4 x, float eps, const View4 y, int64_t row
     for (int64_t i = lane; i < n; i += 64) vstore(y, yr, i, (vload(x, xr, i) - mean) * sc);
 }
 
+// ---------------------------------------------------------------- rows held in registers
+// F32 rows of n = 256 NV contiguous floats, 16-byte aligned: one wave per row
+// loads the whole row (and w) before its reductions and stores after them, so
+// no load waits behind a store of the same wave. RMS: y = x / sqrt(mean(x^2) +
+// eps) * w; NORM: y = (x - mean) / sqrt(mean((x - mean)^2) + eps).
+template <bool RMS, int NV>
+__global__ __launch_bounds__(256) void norm_rows_kernel(const float *x, int64_t ldx, const float *w, float eps,
+                                                        float *y, int64_t ldy, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    constexpr int n = 256 * NV;
+    const float *xr = x + r * ldx;
+    f32x4 v[NV], wv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        v[j] = *(const f32x4 *) (xr + (lane + 64 * j) * 4);
+        wv[j] = RMS && w ? *(const f32x4 *) (w + (lane + 64 * j) * 4) : f32x4{1, 1, 1, 1};
+    }
+    float mean = 0.0f;
+    if constexpr (!RMS) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) s += v[j][0] + v[j][1] + v[j][2] + v[j][3];
+        mean = wave_sum(s) / (float) n;
+    }
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        for (int e = 0; e < 4; ++e) { const float d = v[j][e] - mean; s2 += d * d; }
+    const float sc = 1.0f / sqrtf(wave_sum(s2) / (float) n + eps);
+    float *yr = y + r * ldy;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        f32x4 o;
+        for (int e = 0; e < 4; ++e) o[e] = RMS && w ? v[j][e] * sc * wv[j][e] : (v[j][e] - mean) * sc;
+        *(f32x4 *) (yr + (lane + 64 * j) * 4) = o;
+    }
+}
+
+// rows of x and y uniformly strided F32 with n = 256 NV, NV in {1, 2, 4, 8, 16}
+bool rows_fit(const View4 &x, const View4 &y, int64_t *ldx, int64_t *ldy) {
+    const int64_t n = x.ne[0];
+    if (x.type != TSK_TYPE_F32 || y.type != TSK_TYPE_F32 || n % 256 || n > 4096 || (n / 256) & (n / 256 - 1))
+        return false;
+    for (const View4 *v : {&x, &y}) {
+        if (v->nb[0] != 4 || v->nb[1] % 16 || ((uintptr_t) v->data & 15) || v->nb[2] != v->ne[1] * v->nb[1] ||
+            v->nb[3] != v->ne[2] * v->nb[2])
+            return false;
+    }
+    for (int d = 0; d < 4; ++d)
+        if (x.ne[d] != y.ne[d]) return false;
+    *ldx = x.nb[1] / 4;
+    *ldy = y.nb[1] / 4;
+    return true;
+}
+
+template <bool RMS>
+void launch_norm_rows(const float *x, int64_t ldx, const float *w, float eps, float *y, int64_t ldy, int64_t rows,
+                      int n, hipStream_t s) {
+    const dim3 grid((unsigned) ((rows + 3) / 4)), blk(256);
+    switch (n / 256) {
+        case 1: launch_kernel(norm_rows_kernel<RMS, 1>, grid, blk, 0, s, x, ldx, w, eps, y, ldy, rows); break;
+        case 2: launch_kernel(norm_rows_kernel<RMS, 2>, grid, blk, 0, s, x, ldx, w, eps, y, ldy, rows); break;
+        case 4: launch_kernel(norm_rows_kernel<RMS, 4>, grid, blk, 0, s, x, ldx, w, eps, y, ldy, rows); break;
+        case 8: launch_kernel(norm_rows_kernel<RMS, 8>, grid, blk, 0, s, x, ldx, w, eps, y, ldy, rows); break;
+        default: launch_kernel(norm_rows_kernel<RMS, 16>, grid, blk, 0, s, x, ldx, w, eps, y, ldy, rows); break;
+    }
+}
+
 // ---------------------------------------------------------------- rope NORMAL
 // x ne = [ne0, n_head, S, B]; pos[i2]. One wave per (i1, i2, i3) row.
 __global__ void rope_kernel(const View4 x, const int32_t *pos, int n_dims, float theta_scale,
@@ -525,12 +595,22 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1
 
 hipError_t launch_rms_norm_mul(const View4 &x, const float *w, float eps, const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    int64_t ldx, ldy;
+    if (rows_fit(x, y, &ldx, &ldy) && !((uintptr_t) w & 15)) {
+        launch_norm_rows<true>((const float *) x.data, ldx, w, eps, (float *) y.data, ldy, rows, (int) x.ne[0], s);
+        return hipGetLastError();
+    }
     launch_kernel(rms_norm_mul_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, w, eps, y, rows);
     return hipGetLastError();
 }
 
 hipError_t launch_norm(const View4 &x, float eps, const View4 &y, hipStream_t s) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    int64_t ldx, ldy;
+    if (rows_fit(x, y, &ldx, &ldy)) {
+        launch_norm_rows<false>((const float *) x.data, ldx, nullptr, eps, (float *) y.data, ldy, rows, (int) x.ne[0], s);
+        return hipGetLastError();
+    }
     launch_kernel(norm_kernel, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, eps, y, rows);
     return hipGetLastError();
 }
