@@ -259,30 +259,6 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
         constexpr int USZ = 2048, STG = U * USZ;
         const int ns = my_n;
         const int r8 = lane >> 3;
-        // row-major operands: this lane's element offset inside a 16-row block, per block half h
-        int64_t aoff_l[2];
-        int chk[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            chk[h] = ((lane & 7) ^ r8 ^ (4 * h)) * 8;                 // bf16 elements
-            aoff_l[h] = (int64_t) (8 * h + r8) * p.ld_w + chk[h];
-        }
-        // B: token rows of this lane per (token block j, half h)
-        const uint16_t *bp[TN][2];
-        int bw[CONV ? TN : 1][2];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int n = min(bn0 + 16 * j + 8 * h + r8, p.N - 1);
-                if constexpr (CONV) {
-                    const int b = n / p.conv_ow, ow = n - b * p.conv_ow;
-                    bp[j][h] = (const uint16_t *) p.x + (int64_t) b * p.x_group_stride + chk[h];
-                    bw[j][h] = ow * p.conv_s - p.conv_p;
-                } else {
-                    bp[j][h] = (const uint16_t *) p.x + x_row(p, n) + chk[h];
-                }
-            }
         // MFMA read offsets of this lane (token / row t = lane % 16, chunk 4 kh + lane / 16)
         int roff[2];
         {
@@ -293,33 +269,42 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
         }
         // this wave's loads, fixed per q for the whole K range: fragment
         // f = wave + 4 q is unit f / 2, half f % 2; its source advances by
-        // `step` elements per stage (1024 for tiled weights, 64 otherwise)
+        // `step` elements per stage (1024 for tiled weights, 64 otherwise).
+        // Row-major operands: lane i of half h fetches row 8 h + i / 8 of its
+        // 16-row block, bf16 chunk qchk = (i % 8) ^ (i / 8) ^ 4 h. Every source
+        // is computed from (u, h) directly: the unit and half depend on the
+        // wave, and arrays indexed by them would live in scratch memory.
         const uint16_t *qsrc[LW];
-        int qlds[LW], qstep[LW], qconv[CONV ? LW : 1];
+        int qlds[LW], qstep[LW], qconv[CONV ? LW : 1], qchk[CONV ? LW : 1];
 #pragma unroll
         for (int q = 0; q < LW; ++q) {
             const int f = wave + 4 * q, u = f >> 1, h = f & 1;
+            const int chk = ((lane & 7) ^ r8 ^ (4 * h)) * 8;            // bf16 elements
             qlds[q] = u * USZ + h * 1024;
-            if (CONV) qconv[CONV ? q : 0] = 0;
+            if constexpr (CONV) {
+                qconv[q] = 0;
+                qchk[q] = chk;
+            }
             if (u < TM) {
+                const int rb = min((bm0 >> 4) + (SWIGLU ? u % (TM / 2) : u), (p.M >> 4) - 1);
+                const uint16_t *wsrc = SWIGLU && u >= TM / 2 ? p.w3 : p.w;
                 if (p.w_tiled) {
-                    qsrc[q] = abase[u] + (int64_t) (kt0 + h) * 512;
+                    qsrc[q] = wsrc + (int64_t) rb * KT * 512 + lane * 8 + (int64_t) (kt0 + h) * 512;
                     qstep[q] = 1024;
                 } else {
-                    const int rb = min((bm0 >> 4) + (SWIGLU ? u % (TM / 2) : u), (p.M >> 4) - 1);
-                    const uint16_t *wsrc = SWIGLU && u >= TM / 2 ? p.w3 : p.w;
-                    qsrc[q] = wsrc + (int64_t) rb * 16 * p.ld_w + aoff_l[h] + kt0 * 32;
+                    qsrc[q] = wsrc + (int64_t) (rb * 16 + 8 * h + r8) * p.ld_w + chk + kt0 * 32;
                     qstep[q] = 64;
                 }
             } else {
-                const int j = u - TM;
+                const int n = min(bn0 + 16 * (u - TM) + 8 * h + r8, p.N - 1);
                 if constexpr (CONV) {
                     // implicit im2col: the row base (batch item) and first input position
-                    qsrc[q] = bp[j][h];
-                    qconv[q] = bw[j][h];
+                    const int b = n / p.conv_ow, ow = n - b * p.conv_ow;
+                    qsrc[q] = (const uint16_t *) p.x + (int64_t) b * p.x_group_stride + chk;
+                    qconv[q] = ow * p.conv_s - p.conv_p;
                     qstep[q] = 0;
                 } else {
-                    qsrc[q] = bp[j][h] + kt0 * 32;
+                    qsrc[q] = (const uint16_t *) p.x + x_row(p, n) + chk + kt0 * 32;
                     qstep[q] = 64;
                 }
             }
@@ -334,8 +319,7 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
                     if (isb) {
                         const int k = (kt0 + 2 * t) * 32, kw = k / p.conv_ic, ic0 = k - kw * p.conv_ic;
                         const int iw = qconv[q] + kw * p.conv_d;
-                        const int h = (wave + 4 * q) & 1;
-                        g2l16(iw >= 0 && iw < p.conv_iw ? qsrc[q] + (int64_t) iw * p.ld_x + ic0 : g_zero_row + chk[h],
+                        g2l16(iw >= 0 && iw < p.conv_iw ? qsrc[q] + (int64_t) iw * p.ld_x + ic0 : g_zero_row + qchk[q],
                               dst + qlds[q]);
                         continue;
                     }
