@@ -190,17 +190,15 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const uint16_t *vb = kb + KT * 64;
         const int nbuf_next = buf + (NB - 1) >= NB ? buf - 1 : buf + (NB - 1);   // (buf + NB - 1) % NB
         if (tile < tend) {
-            // all fragments of this tile first, then the loads NB - 1 tiles ahead
+            // K fragments of this tile first, then the loads NB - 1 tiles ahead
+            // (into another buffer); the V^T fragments are read after the
+            // K . Q^T products, so they take the K fragments' registers
             u32x4 kf[2][4];
             f16x8 vf[2][4];
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) kf[mb][ks] = *(const u32x4 *) (kb + swz(32 * mb + l32, 2 * ks + hi));
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) vf[db][cc] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
             if (tile + NB - 1 < tend) issue(tile + NB - 1, nbuf_next);
 
             // S^T - m = K . Q^T + cm: s[mb][4 r + jj] for key 32 mb + 8 r + 4 hi + jj, query l32
@@ -223,6 +221,10 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
                                                                         __builtin_bit_cast(f16x8, qraw[ks]), s[mb], 0, 0, 0);
                 }
             }
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) vf[db][cc] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
             const int lim = tile == ntiles - 1 ? p.Nkv - tile * KT : KT;
             // softmax and P.V per 32-key half: the second half's MFMAs overlap
             // the first half's exponentials, the first half's P.V the second's

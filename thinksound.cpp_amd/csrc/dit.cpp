@@ -542,11 +542,11 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
 // 550 rows 64 x 64 cooperative tiles of 64-wide stages (cfg 30); up to 1100
 // rows the same for qkv, 64 x 64 tiles of 32-wide stages for out (cfg 22)
 // and 128 x 64 tiles of 64-wide stages for the MLP (cfg 28); beyond, 128 x 64
-// cooperative tiles of 32-wide stages (cfg 12). The tile shape does not
-// change any summation order.
+// tiles of two 64-wide stages (cfg 29), 64 x 64 for out (cfg 30). The tile
+// shape does not change any summation order.
 int gemm_cfg_for(const tsk_dit *d, int role, int rows) {
     if (d->gemm_cfg[role]) return d->gemm_cfg[role];
-    if (rows >= 1100) return 12;
+    if (rows >= 1100) return role == 1 ? 30 : 29;
     if (rows < 550) return 30;
     static const int mid[4] = {30, 22, 28, 28};   // qkv, out, fc1, fc2
     return mid[role];
