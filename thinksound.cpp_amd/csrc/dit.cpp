@@ -722,6 +722,17 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // a sampler step with a conditioning schedule reads its modulations from
     // the schedule row (d->cur_sched); otherwise they are computed here
     const int jmain = 2 * (nj < 2 ? nj : 2);
+    // input projection (f32 activations, fp32 accumulation) and text stream
+    // copy first: the conditioning's later adaLN GEMVs fill the chip from the
+    // side stream, and these small launches would wait behind them
+    {
+        Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
+        e = launch_proj_f32(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d,
+                            c.latent_dim, B * T, c.latent_dim, H, d->lat, H, st);
+        if (e != hipSuccess) return hip_fail(e, "input projection");
+    }
+    if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
+        return hip_fail(e, "text copy");
     bool joined = true;
     if (!d->cur_sched) {
         if ((rc = run_conditioning(d, B, t_host, jmain, st))) return rc;
@@ -732,15 +743,6 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
         joined = true;
         return hipcheck(hipStreamWaitEvent(st, d->ev_join, 0), "join");
     };
-    // input projection (f32 activations, fp32 accumulation), text stream copy
-    {
-        Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
-        e = launch_proj_f32(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d,
-                            c.latent_dim, B * T, c.latent_dim, H, d->lat, H, st);
-        if (e != hipSuccess) return hip_fail(e, "input projection");
-    }
-    if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
-        return hip_fail(e, "text copy");
 
     // streams: latent rows of this call first, text rows from the capacity offset
     const size_t cap = (size_t) c.max_batch * c.max_latent;

@@ -471,16 +471,22 @@ __global__ __launch_bounds__(256) void proj_f32_kernel(const uint16_t *w, const 
 // staged in LDS; wave w owns outputs 16 w .. 16 w + 15 and its lanes split K
 // (lane l: k = (K / 64) l .. +K / 64), so all 16 weight-row slices of a lane
 // are in flight at once; each output is one fixed-order wave sum.
-template <int KPL>
+template <int KPL, int TOK>
 __global__ __launch_bounds__(256) void proj_f32_kt_kernel(const uint16_t *w, const float *bias, const float *x,
                                                           int64_t ld_x, int N, int M, float *y, int64_t ld_y) {
+    // a workgroup: 64 outputs (16 per wave) of TOK consecutive tokens; lane l
+    // holds k slice [l * KPL * 8, +KPL * 8) of its wave's 16 weight rows in
+    // registers for all TOK tokens; each output is its lane partials summed in
+    // k order, then the wave sum -- the same order for any TOK
     constexpr int K = KPL * 8 * 64;
-    __shared__ __attribute__((aligned(16))) float xs[K];
+    __shared__ __attribute__((aligned(16))) float xs[TOK][K];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int chunks = (M + 63) / 64;
-    const int n = blockIdx.x / chunks, m0 = (blockIdx.x % chunks) * 64 + wave * 16;
-    const float *xr = x + (int64_t) n * ld_x;
-    for (int i = threadIdx.x * 4; i < K; i += 256 * 4) *(f32x4 *) &xs[i] = *(const f32x4 *) (xr + i);
+    const int m0 = blockIdx.x * 64 + wave * 16, n0 = blockIdx.y * TOK;
+    for (int i = threadIdx.x * 4; i < TOK * K; i += 256 * 4) {
+        const int t = i / K, c = i - t * K;
+        const int n = min(n0 + t, N - 1);
+        *(f32x4 *) &xs[t][c] = *(const f32x4 *) (x + (int64_t) n * ld_x + c);
+    }
     u32x4 wv[16][KPL];
 #pragma unroll
     for (int o = 0; o < 16; ++o) {
@@ -489,23 +495,68 @@ __global__ __launch_bounds__(256) void proj_f32_kt_kernel(const uint16_t *w, con
         for (int j = 0; j < KPL; ++j) wv[o][j] = *(const u32x4 *) (w + (int64_t) m * K + lane * KPL * 8 + 8 * j);
     }
     __syncthreads();
-    float xv[KPL * 8];
+    for (int t = 0; t < TOK; ++t) {
+        const int n = n0 + t;
+        if (n >= N) break;
+        float xv[KPL * 8];
 #pragma unroll
-    for (int j = 0; j < KPL * 8; j += 4) {
-        const f32x4 t = *(const f32x4 *) &xs[lane * KPL * 8 + j];
-        xv[j] = t[0]; xv[j + 1] = t[1]; xv[j + 2] = t[2]; xv[j + 3] = t[3];
-    }
-#pragma unroll
-    for (int o = 0; o < 16; ++o) {
-        float a = 0.0f;
-#pragma unroll
-        for (int j = 0; j < KPL; ++j) {
-            const uint16_t *h = (const uint16_t *) &wv[o][j];
-            for (int e = 0; e < 8; ++e) a = fmaf(bf16_bits_to_f32(h[e]), xv[8 * j + e], a);
+        for (int j = 0; j < KPL * 8; j += 4) {
+            const f32x4 v = *(const f32x4 *) &xs[t][lane * KPL * 8 + j];
+            xv[j] = v[0]; xv[j + 1] = v[1]; xv[j + 2] = v[2]; xv[j + 3] = v[3];
         }
-        a = wave_sum(a);
-        const int m = m0 + o;
-        if (lane == 0 && m < M) y[(int64_t) n * ld_y + m] = a + (bias ? bias[m] : 0.0f);
+#pragma unroll
+        for (int o = 0; o < 16; ++o) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) {
+                const uint16_t *h = (const uint16_t *) &wv[o][j];
+                for (int e = 0; e < 8; ++e) a = fmaf(bf16_bits_to_f32(h[e]), xv[8 * j + e], a);
+            }
+            a = wave_sum(a);
+            const int m = m0 + o;
+            if (lane == 0 && m < M) y[(int64_t) n * ld_y + m] = a + (bias ? bias[m] : 0.0f);
+        }
+    }
+}
+
+// Short-K projection (the 64-channel latent input): lane l holds output
+// m0 + l's K weights in registers, a workgroup runs TT tokens whose rows are
+// staged in LDS (float4 broadcasts); k is summed as in proj_f32_kernel
+// (a[k % 4] in k order, then ((a0 + a1) + (a2 + a3)) + bias).
+template <int K, int TT>
+__global__ __launch_bounds__(256) void proj_f32_rows_kernel(const uint16_t *w, const float *bias, const float *x,
+                                                            int64_t ld_x, int N, int M, float *y, int64_t ld_y) {
+    __shared__ __attribute__((aligned(16))) float xs[TT][K];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m0 = blockIdx.x * 64, n0 = blockIdx.y * TT;
+    for (int i = threadIdx.x; i < TT * (K / 4); i += 256) {
+        const int t = i / (K / 4), c = (i - t * (K / 4)) * 4;
+        const int n = min(n0 + t, N - 1);
+        *(f32x4 *) &xs[t][c] = *(const f32x4 *) (x + (int64_t) n * ld_x + c);
+    }
+    const int m = m0 + lane;
+    const uint16_t *wr = w + (int64_t) (m < M ? m : M - 1) * K;
+    float wv[K];
+#pragma unroll
+    for (int k = 0; k < K; k += 8) {
+        const u32x4 w8 = *(const u32x4 *) (wr + k);
+        const uint16_t *h = (const uint16_t *) &w8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[k + e] = bf16_bits_to_f32(h[e]);
+    }
+    const float bv = bias && m < M ? bias[m] : 0.0f;
+    __syncthreads();
+    for (int t = wave; t < TT; t += 4) {
+        const int n = n0 + t;
+        if (n >= N) break;
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < K; k += 4) {
+            const f32x4 xv = *(const f32x4 *) &xs[t][k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = fmaf(wv[k + e], xv[e], a[e]);
+        }
+        if (m < M) y[(int64_t) n * ld_y + m] = ((a[0] + a[1]) + (a[2] + a[3])) + bv;
     }
 }
 
@@ -696,9 +747,14 @@ hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B
 hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,
                            float *y, int64_t ld_y, hipStream_t s) {
     if (N < 1 || M < 1 || K < 8 || K % 8 || ld_x % 4) return hipErrorInvalidValue;
-    if (K == 1024) {   // long rows: lanes split K (final layer)
-        launch_kernel(proj_f32_kt_kernel<2>, dim3((unsigned) ((int64_t) N * ((M + 63) / 64))), dim3(256), 0, s, w,
-                      bias, x, ld_x, N, M, y, ld_y);
+    if (K == 1024) {   // long rows: lanes split K (final layer), 4 tokens per workgroup
+        launch_kernel(proj_f32_kt_kernel<2, 4>, dim3((unsigned) ((M + 63) / 64), (unsigned) ((N + 3) / 4)), dim3(256), 0,
+                      s, w, bias, x, ld_x, N, M, y, ld_y);
+        return hipGetLastError();
+    }
+    if (K == 64) {     // the latent input: weights in registers, 16 tokens per workgroup
+        launch_kernel(proj_f32_rows_kernel<64, 16>, dim3((unsigned) ((M + 63) / 64), (unsigned) ((N + 15) / 16)),
+                      dim3(256), 0, s, w, bias, x, ld_x, N, M, y, ld_y);
         return hipGetLastError();
     }
     const int64_t waves = (int64_t) N * ((M + 63) / 64);
