@@ -106,12 +106,8 @@ struct Coord {
 // XCD x owns the pairs c = x, x + 8, ... with c = m tile * splits + split and
 // runs every token tile of each: a weight tile is fetched into one XCD's L2
 // only, and with splits dividing 8 an XCD reads a single K slice of the
-// activations instead of all of them.
-__device__ __forceinline__ bool decode(const GemmGroup &g, Coord &c) {
-    const int bid = blockIdx.x;
-    c.pi = (g.nprob > 1 && bid >= g.p[1].block_begin) ? 1 : 0;
-    const GemmProblem &p = g.p[c.pi];
-    const int li = bid - p.block_begin;
+// activations instead of all of them. `li` counts the problem's workgroups.
+__device__ __forceinline__ bool decode(const GemmProblem &p, int li, Coord &c) {
     const int cols = p.tiles_n * p.splits;
     if (li >= p.tiles_m * cols) return false;
     if (((p.tiles_m * p.splits) & 7) == 0) {
@@ -160,9 +156,11 @@ __device__ __attribute__((aligned(16))) uint16_t g_zero_row[64];
 
 constexpr bool epi_swiglu(int epi) { return epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_BF16; }
 
-template <int TM, int TN, int R, int MODE, int EPI, int KH = 1, bool CONV = false>
-__global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+// The tile of one problem; `p` is the kernel argument itself (g.p[0] or
+// g.p[1] by name, never by a runtime index), so every field is read at a fixed
+// kernel-argument offset and all of them can be requested at kernel entry.
+template <int TM, int TN, int R, int MODE, int EPI, int KH, bool CONV>
+__device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord tc, uint8_t *lds) {
     constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = KH * L * 1024;
     constexpr bool PIPE = MODE == MODE_COOP_PIPE, C64 = MODE == MODE_COOP64;
     constexpr bool COOP = MODE == MODE_COOP || PIPE || C64, DIRECT = MODE == MODE_DIRECT;
@@ -176,9 +174,6 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     constexpr bool SWIGLU = epi_swiglu(EPI);
     constexpr int BMO = SWIGLU ? BM / 2 : BM;
 
-    Coord tc;
-    if (!decode(g, tc)) return;
-    const GemmProblem &p = g.p[tc.pi];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bm0 = tc.tm * BMO, bn0 = tc.tn * BN;
@@ -753,6 +748,24 @@ __global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
     }   // token chunk
 }
 
+// NPROB = 1: one problem (g.p[0]); NPROB = 2: workgroups from
+// g.p[1].block_begin on run the second problem
+template <int TM, int TN, int R, int MODE, int EPI, int KH, bool CONV, int NPROB>
+__global__ __launch_bounds__(NT) void gemm_ks_kernel(const GemmGroup g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bid = blockIdx.x;
+    Coord tc;
+    if (NPROB == 2 && bid >= g.p[1].block_begin) {
+        tc.pi = 1;
+        if (!decode(g.p[1], bid - g.p[1].block_begin, tc)) return;
+        gemm_ks_tile<TM, TN, R, MODE, EPI, KH, CONV>(g.p[1], tc, lds);
+    } else {
+        tc.pi = 0;
+        if (!decode(g.p[0], bid, tc)) return;
+        gemm_ks_tile<TM, TN, R, MODE, EPI, KH, CONV>(g.p[0], tc, lds);
+    }
+}
+
 template <int TM, int TN, int R, int MODE, int EPI, int KH, bool CONV = false>
 hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     constexpr int BM = 16 * TM / (epi_swiglu(EPI) ? 2 : 1), BN = 16 * TN;
@@ -770,13 +783,14 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     }
     constexpr size_t lds = lds_bytes<TM, TN, R, MODE, KH>();
     static_assert(lds <= 160 * 1024, "LDS");
-    auto kern = gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV>;
-    static bool attr = false;   // dynamic LDS above 64 KiB is opted in once per kernel
-    if (!attr) {
+    auto kern = g.nprob == 2 ? gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV, 2>
+                             : gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV, 1>;
+    static bool attr[2] = {false, false};   // dynamic LDS above 64 KiB is opted in once per kernel
+    if (!attr[g.nprob - 1]) {
         if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
             hipSuccess)
             (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
-        attr = true;
+        attr[g.nprob - 1] = true;
     }
     launch_kernel(kern, dim3(nblocks), dim3(NT), lds, s, g);
     return hipGetLastError();
