@@ -631,37 +631,38 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
             }
         } else {
         static_assert(U * (NT / 16) == BNC * HPT, "QKV epilogue pairs");
-        f32x4 xs[U], wvs[U], css[U];
+        static_assert((NT / 16) % HPT == 0, "a lane group keeps one head");
+        // lane group grp runs pairs pp = grp + 16 u: token pp / HPT, head pp % HPT
+        // = grp % HPT for every u, so the bias and norm weights are one load
+        const int hl = grp % HPT, f0 = bm0 + hl * 64;
+        const int sec = f0 / H, head = (f0 % H) / 64;
+        const f32x4 bv = p.bias ? *(const f32x4 *) (p.bias + f0 + 4 * sl) : f32x4{0, 0, 0, 0};
+        const f32x4 wv = sec < 2 ? *(const f32x4 *) ((sec ? p.kn_w : p.qn_w) + 4 * sl) : f32x4{0, 0, 0, 0};
+        f32x4 xs[U], css[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int pp = grp + u * (NT / 16);
-            const int nl = pp / HPT, hl = pp % HPT;
-            const int n = bn0c + nl, f0 = bm0 + hl * 64;
-            const int sec = f0 / H, spos = (n < p.N ? n : 0) % p.seq;
+            const int nl = (grp + u * (NT / 16)) / HPT;
+            const int n = bn0c + nl, spos = (n < p.N ? n : 0) % p.seq;
             xs[u] = sum4(nl, hl * 64 + 4 * sl);
-            if (p.bias) {
-                const f32x4 bv = *(const f32x4 *) (p.bias + f0 + 4 * sl);
-                xs[u] = f32x4{xs[u][0] + bv[0], xs[u][1] + bv[1], xs[u][2] + bv[2], xs[u][3] + bv[3]};
-            }
-            wvs[u] = sec < 2 ? *(const f32x4 *) ((sec ? p.kn_w : p.qn_w) + 4 * sl) : f32x4{0, 0, 0, 0};
             css[u] = sec < 2 && p.rope ? *(const f32x4 *) (p.rope_cs + (int64_t) spos * 64 + 4 * sl)
                                        : f32x4{0, 0, 0, 0};
         }
+        // every load of the epilogue has landed before the first store (a wait
+        // the compiler sees, so no per-pair wait then also waits for the
+        // previous pairs' stores, which share the counter)
+        __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int pp = grp + u * (NT / 16);
-            const int nl = pp / HPT, hl = pp % HPT;
-            const int n = bn0c + nl, f0 = bm0 + hl * 64;
+            const int nl = (grp + u * (NT / 16)) / HPT;
+            const int n = bn0c + nl;
             const bool live = n < p.N;
-            f32x4 x = xs[u];
-            const int sec = f0 / H, head = (f0 % H) / 64;
+            f32x4 x = f32x4{xs[u][0] + bv[0], xs[u][1] + bv[1], xs[u][2] + bv[2], xs[u][3] + bv[3]};
             const int nn = live ? n : 0;
             const int b = nn / p.seq, spos = nn % p.seq;
             if (sec < 2) {
-                float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-                for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+                // the 16 lanes of this (token, head) pair form one DPP row
+                const float ss = row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
                 const float sc = 1.0f / sqrtf(ss / 64.0f + p.eps);
-                const f32x4 wv = wvs[u];
                 for (int e = 0; e < 4; ++e) x[e] = x[e] * sc * wv[e];
                 if (p.rope) {
                     // (cos, sin) of pairs 2 sl, 2 sl + 1 at position spos

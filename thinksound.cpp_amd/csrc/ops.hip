@@ -265,13 +265,12 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 //   pending: x += gate[b] * (sum_s part[s][r] + bias)   (splits summed in order)
 //   y = LN(x, eps) * (1 + scale[b]) + shift[b]           (bf16, or f32)
 // A row of H <= 4096 floats stays in registers (4 per thread per 1024).
+// One row of stream `st` (the kernel argument g.s[0] or g.s[1] by name, so
+// every field is read at a fixed kernel-argument offset).
 template <bool YF32>
-__global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
+__device__ __forceinline__ void ln_group_row(const LnStream &st, int r, int H, float eps) {
     __shared__ float red[4];
-    int r = blockIdx.x, si = 0;
-    if (g.nstream > 1 && r >= g.s[0].rows) { r -= g.s[0].rows; si = 1; }
-    const LnStream &st = g.s[si];
-    const int H = g.H, b = r / st.rows_per_b;
+    const int b = r / st.rows_per_b;
     float *xr = st.x + (int64_t) r * st.ld_x;
     constexpr int VMAX = 4;
     f32x4 v[VMAX];
@@ -304,7 +303,7 @@ __global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
         for (int e = 0; e < 4; ++e) { const float d = v[j][e] - mean; s2 += d * d; }
     }
     const float var = block_sum_256(s2, red) / (float) H;
-    const float rs = 1.0f / sqrtf(var + g.eps);
+    const float rs = 1.0f / sqrtf(var + eps);
     const float *sh = st.shift + (int64_t) b * st.ld_mod, *sc = st.scale + (int64_t) b * st.ld_mod;
 #pragma unroll
     for (int j = 0; j < VMAX; ++j) {
@@ -325,15 +324,19 @@ __global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
     }
 }
 
+template <bool YF32>
+__global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
+    const int r = blockIdx.x;
+    if (g.nstream > 1 && r >= g.s[0].rows) ln_group_row<YF32>(g.s[1], r - g.s[0].rows, g.H, g.eps);
+    else ln_group_row<YF32>(g.s[0], r, g.H, g.eps);
+}
+
 // The same row update with one wave per row and H = 256 NV: every load of the
 // row (residual, split slices, bias, gate, shift, scale) is issued before the
 // first reduction, and both reductions stay inside the wave (no LDS, no
 // barrier).
 template <bool YF32, int NV>
-__global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
-    int r = blockIdx.x, si = 0;
-    if (g.nstream > 1 && r >= g.s[0].rows) { r -= g.s[0].rows; si = 1; }
-    const LnStream &st = g.s[si];
+__device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps) {
     constexpr int H = 256 * NV;
     const int lane = threadIdx.x, b = r / st.rows_per_b;
     float *xr = st.x + (int64_t) r * st.ld_x;
@@ -377,7 +380,7 @@ __global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
 #pragma unroll
     for (int j = 0; j < NV; ++j)
         for (int e = 0; e < 4; ++e) { const float d = v[j][e] - mean; s2 += d * d; }
-    const float rs = 1.0f / sqrtf(wave_sum(s2) / (float) H + g.eps);
+    const float rs = 1.0f / sqrtf(wave_sum(s2) / (float) H + eps);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int i = (lane + 64 * j) * 4;
@@ -393,6 +396,13 @@ __global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
             *(u32x2 *) ((uint16_t *) st.y + (int64_t) r * st.ld_y + i) = w;
         }
     }
+}
+
+template <bool YF32, int NV>
+__global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
+    const int r = blockIdx.x;
+    if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YF32, NV>(g.s[1], r - g.s[0].rows, g.eps);
+    else ln_wave_row<YF32, NV>(g.s[0], r, g.eps);
 }
 
 // GEMV list: one wave per output row; lane k-slices of 8, f32 activations
