@@ -26,54 +26,78 @@ namespace tsk {
 namespace {
 
 
-template <int EPI, bool YBF16>
-__device__ __forceinline__ void epilogue4(const GemmParams &p, int m0, int n, f32x4 v) {
-    if (n >= p.N || m0 >= p.M) return;
-    const bool full = m0 + 3 < p.M;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias) {
-        if (full) { f32x4 t = *(const f32x4 *) (p.bias + m0); bv[0] = t[0]; bv[1] = t[1]; bv[2] = t[2]; bv[3] = t[3]; }
-        else for (int r = 0; r < 4 && m0 + r < p.M; ++r) bv[r] = p.bias[m0 + r];
-    }
-    float o[4];
-    for (int r = 0; r < 4; ++r) o[r] = v[r] + bv[r];
-    if constexpr (EPI == EPI_GEGLU) {
-        // features m0 .. m0 + 3 are (a_j, b_j, a_j+1, b_j+1), j = m0 / 2 (M % 4 == 0)
-        float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0 / 2;
-        *(f32x2 *) yr = f32x2{gelu_tanh_f(o[0]) * o[1], gelu_tanh_f(o[2]) * o[3]};
-        return;
-    }
-    if constexpr (EPI == EPI_GELU)
-        for (int r = 0; r < 4; ++r) o[r] = gelu_tanh_f(o[r]);
+// 4 floats of row `row` at columns m0 .. m0 + 3 (zeros past M)
+__device__ __forceinline__ f32x4 load4_guard(const float *row, int m0, int M) {
+    if (m0 + 3 < M) return *(const f32x4 *) (row + m0);
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 4 && m0 + r < M; ++r) v[r] = row[m0 + r];
+    return v;
+}
+
+// Epilogue of a wave's TI x TJ output fragments (lane: features m0[i] .. + 3
+// of token n[j]): every load (bias, gate, residual) of all fragments first,
+// then one wait the compiler sees, then the stores -- loads and stores share
+// one counter, so a load issued behind a store would also wait for it.
+template <int EPI, bool YBF16, int TI, int TJ>
+__device__ __forceinline__ void epilogue_frags(const GemmParams &p, const int (&m0)[TI], const int (&n)[TJ],
+                                               const f32x4 (&acc)[TI][TJ]) {
+    f32x4 bv[TI], gv[TI][TJ], rv[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) bv[i] = p.bias && m0[i] < p.M ? load4_guard(p.bias, m0[i], p.M) : f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (EPI == EPI_GATE_RES) {
-        const float *g = p.gate + (int64_t) (n / p.rows_per_gate) * p.ld_gate + m0;
-        float *rr = p.res + (int64_t) n * p.ld_res + m0;
-        if (full) {
-            f32x4 gg = *(const f32x4 *) g;
-            f32x4 cur = *(f32x4 *) rr;
-            for (int r = 0; r < 4; ++r) cur[r] += gg[r] * o[r];
-            *(f32x4 *) rr = cur;
-        } else {
-            for (int r = 0; r < 4 && m0 + r < p.M; ++r) rr[r] += g[r] * o[r];
-        }
-        return;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const bool ok = n[j] < p.N && m0[i] < p.M;
+                gv[i][j] = ok ? load4_guard(p.gate + (int64_t) (n[j] / p.rows_per_gate) * p.ld_gate, m0[i], p.M)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+                rv[i][j] = ok ? load4_guard(p.res + (int64_t) n[j] * p.ld_res, m0[i], p.M) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
     }
-    if constexpr (YBF16) {
-        uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
-        if (full) {
-            uint16_t t4[4];
-            for (int r = 0; r < 4; ++r) t4[r] = f32_to_bf16_bits(o[r]);
-            u32x2 w;
-            __builtin_memcpy(&w, t4, 8);
-            *(u32x2 *) yr = w;
-        } else {
-            for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int mm = m0[i], nn = n[j];
+            if (nn >= p.N || mm >= p.M) continue;
+            const bool full = mm + 3 < p.M;
+            float o[4];
+            for (int r = 0; r < 4; ++r) o[r] = acc[i][j][r] + bv[i][r];
+            if constexpr (EPI == EPI_GEGLU) {
+                // features mm .. mm + 3 are (a_j, b_j, a_j+1, b_j+1), j = mm / 2 (M % 4 == 0)
+                float *yr = (float *) p.y + (int64_t) nn * p.ld_y + mm / 2;
+                *(f32x2 *) yr = f32x2{gelu_tanh_f(o[0]) * o[1], gelu_tanh_f(o[2]) * o[3]};
+                continue;
+            }
+            if constexpr (EPI == EPI_GELU)
+                for (int r = 0; r < 4; ++r) o[r] = gelu_tanh_f(o[r]);
+            if constexpr (EPI == EPI_GATE_RES) {
+                float *rr = p.res + (int64_t) nn * p.ld_res + mm;
+                f32x4 cur = rv[i][j];
+                for (int r = 0; r < 4; ++r) cur[r] += gv[i][j][r] * o[r];
+                if (full) *(f32x4 *) rr = cur;
+                else for (int r = 0; r < 4 && mm + r < p.M; ++r) rr[r] = cur[r];
+                continue;
+            }
+            if constexpr (YBF16) {
+                uint16_t *yr = (uint16_t *) p.y + (int64_t) nn * p.ld_y + mm;
+                if (full) {
+                    uint16_t t4[4];
+                    for (int r = 0; r < 4; ++r) t4[r] = f32_to_bf16_bits(o[r]);
+                    u32x2 w;
+                    __builtin_memcpy(&w, t4, 8);
+                    *(u32x2 *) yr = w;
+                } else {
+                    for (int r = 0; r < 4 && mm + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+                }
+            } else {
+                float *yr = (float *) p.y + (int64_t) nn * p.ld_y + mm;
+                if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                else for (int r = 0; r < 4 && mm + r < p.M; ++r) yr[r] = o[r];
+            }
         }
-    } else {
-        float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
-        if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
-        else for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
-    }
 }
 
 // ------------------------------------------------------------------ BF16
@@ -178,12 +202,12 @@ void gemm_bf16_kernel(const GemmParams p) {
         __syncthreads();
     }
 
-    for (int i = 0; i < TM; ++i)
-        for (int j = 0; j < TN; ++j) {
-            const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
-            const int n = bn0 + (wn * TN + j) * 16 + lr;
-            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
-        }
+    int m0[TM], nn[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) m0[i] = bm0 + (wm * TM + i) * 16 + 4 * lg;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) nn[j] = bn0 + (wn * TN + j) * 16 + lr;
+    epilogue_frags<EPI, YBF16, TM, TN>(p, m0, nn, acc);
 }
 
 // ------------------------------------------------------------------ Q8_0
@@ -302,12 +326,12 @@ void gemm_q8_kernel(const GemmParams p) {
         __syncthreads();
     }
 
-    for (int i = 0; i < TM; ++i)
-        for (int j = 0; j < TN; ++j) {
-            const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
-            const int n = bn0 + (wn * TN + j) * 16 + lr;
-            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
-        }
+    int m0[TM], nn[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) m0[i] = bm0 + (wm * TM + i) * 16 + 4 * lg;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) nn[j] = bn0 + (wn * TN + j) * 16 + lr;
+    epilogue_frags<EPI, YBF16, TM, TN>(p, m0, nn, acc);
 }
 
 // ------------------------------------------------------------------ Q8_0, cooperative tiles
@@ -503,14 +527,12 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
         slot = slot + 1 == R ? 0 : slot + 1;
     }
 
+    int m0[TMW], nn[TNW];
 #pragma unroll
-    for (int i = 0; i < TMW; ++i)
+    for (int i = 0; i < TMW; ++i) m0[i] = bm0 + 16 * (wm * TMW + i) + 4 * lg;
 #pragma unroll
-        for (int j = 0; j < TNW; ++j) {
-            const int m0 = bm0 + 16 * (wm * TMW + i) + 4 * lg;
-            const int n = bn0 + 16 * (wn * TNW + j) + lr;
-            epilogue4<EPI, YBF16>(p, m0, n, acc[i][j]);
-        }
+    for (int j = 0; j < TNW; ++j) nn[j] = bn0 + 16 * (wn * TNW + j) + lr;
+    epilogue_frags<EPI, YBF16, TMW, TNW>(p, m0, nn, acc);
 }
 
 // ------------------------------------------------------------------ activation quantization

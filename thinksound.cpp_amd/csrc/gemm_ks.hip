@@ -718,18 +718,24 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
             }
         }
     } else {
-        // 8 consecutive features of one token per thread
+        // 8 consecutive features of one token per thread; the features are
+        // the same on every iteration (NT is a multiple of G), so the bias is
+        // one load ahead of the loop and no store waits behind a load
         constexpr int G = BM / 8;
+        static_assert(NT % G == 0, "one feature group per thread");
+        f32x4 b0 = f32x4{0, 0, 0, 0}, b1 = f32x4{0, 0, 0, 0};
+        if (EPI != EPI_PARTIAL && p.bias && bm0 + (tid % G) * 8 < p.M) {
+            b0 = *(const f32x4 *) (p.bias + bm0 + (tid % G) * 8);
+            b1 = *(const f32x4 *) (p.bias + bm0 + (tid % G) * 8 + 4);
+        }
         for (int it = tid; it < BNC * G; it += NT) {
             const int nl = it / G, ml = (it % G) * 8;
             const int n = bn0c + nl, m = bm0 + ml;
             if (n >= p.N || m >= p.M) continue;
             const f32x4 v0 = sum4(nl, ml), v1 = sum4(nl, ml + 4);
             float o[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            if (EPI != EPI_PARTIAL && p.bias) {
-                const f32x4 b0 = *(const f32x4 *) (p.bias + m), b1 = *(const f32x4 *) (p.bias + m + 4);
+            if (EPI != EPI_PARTIAL && p.bias)
                 for (int e = 0; e < 4; ++e) { o[e] += b0[e]; o[4 + e] += b1[e]; }
-            }
             if constexpr (EPI == EPI_GELU_BF16)
                 for (int e = 0; e < 8; ++e) o[e] = gelu_tanh_f(o[e]);
             if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_GELU_BF16) {
