@@ -71,24 +71,40 @@ __device__ __forceinline__ float rope_theta(float p, float theta_scale, int pair
     return th;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// 64-lane reductions without LDS: DPP steps inside each 16-lane row (swaps
+// within quads, the half-row and the row mirrors), then v_permlane16_swap and
+// v_permlane32_swap pair the rows. Each step combines the same two values in
+// either order, so every lane ends with the same bits. The whole wave must be
+// active.
+__device__ __forceinline__ float dpp_f(float v, int ctrl_id) {
+    switch (ctrl_id) {
+        case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+        case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+        case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
+    }
+}
+// sum over each 16-lane row (every lane of the row gets the sum); all 16
+// lanes of a row must be active
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v += dpp_f(v, i);
     return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = row16_sum(v);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
 }
-// Sum over each 16-lane row of the wave with DPP moves (no LDS): swaps within
-// quads, then the half-row and the row mirrors. Every lane of a row gets the
-// same bits (each step adds the same two values in either order). All 16
-// lanes of a row must be active.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
-    return v;
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v = fmaxf(v, dpp_f(v, i));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
 }
 
 }  // namespace tsk
