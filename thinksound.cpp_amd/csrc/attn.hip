@@ -231,8 +231,7 @@ void attn_kernel(const AttnParams p) {
                     pv[qb][t][r] = x;
                     mloc = fmaxf(mloc, x);
                 }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            mloc = half_pair_max(row_pair_max(mloc));       // lanes l ^ 16, l ^ 32 (no LDS)
             const float m_new = fmaxf(m_run[qb], mloc);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
@@ -283,8 +282,7 @@ void attn_kernel(const AttnParams p) {
     // ---------------- epilogue: O = O^T / l, dst ne = [D, H, Nq, B]
     for (int qb = 0; qb < QB; ++qb) {
         float l = l_run[qb];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        l = half_pair_sum(row_pair_sum(l));
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int qrow = qbase + qb * 16 + lr;
         if (qrow >= p.Nq) continue;

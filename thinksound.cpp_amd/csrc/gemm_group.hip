@@ -302,8 +302,7 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
             const int sec = f0 / H, head = (f0 % H) / 64;
             const int b = (live ? n : 0) / p.seq, spos = (live ? n : 0) % p.seq;
             if (sec < 2) {
-                float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-                for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+                const float ss = row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);   // one DPP row
                 const float sc = 1.0f / sqrtf(ss / 64.0f + p.eps);
                 const float *w = sec ? p.kn_w : p.qn_w;
                 const f32x4 wv = *(const f32x4 *) (w + 4 * sl);

@@ -175,8 +175,7 @@ __global__ void qk_norm_rope_kernel(const View4 x, const float *w, const int32_t
     const char *xr = vrow(x, r);
     char *yr = (char *) vrow(y, r);
     float x0 = vload(x, xr, 2 * i), x1 = vload(x, xr, 2 * i + 1);
-    float ss = x0 * x0 + x1 * x1;
-    for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+    const float ss = row_pair_sum(row16_sum(x0 * x0 + x1 * x1));   // 32 lanes of one 32-lane half
     const float sc = 1.0f / sqrtf(ss / 64.0f + eps);
     x0 = x0 * sc * w[2 * i];
     x1 = x1 * sc * w[2 * i + 1];

@@ -91,6 +91,24 @@ __device__ __forceinline__ float row16_sum(float v) {
     for (int i = 0; i < 4; ++i) v += dpp_f(v, i);
     return v;
 }
+// the other 16-lane row of the same 32-lane half (rows 0 <-> 1, 2 <-> 3): {own, other} in either order
+__device__ __forceinline__ float row_pair_sum(float v) {
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+}
+__device__ __forceinline__ float row_pair_max(float v) {
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+}
+// the same lane of the other 32-lane half
+__device__ __forceinline__ float half_pair_sum(float v) {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+}
+__device__ __forceinline__ float half_pair_max(float v) {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);
     const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
