@@ -293,62 +293,82 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         buf = buf + 1 == NB ? 0 : buf + 1;
     }
 
-    // ---- merge the KS key ranges of each query block (LDS reused)
+    // ---- O = O^T / l; lane writes dims 32 db + 8 r + 4 hi + 0..3 of query q0 + l32:
+    // values vals[4 * k .. 4 * k + 3] are o[k / 4][4 * (k % 4) ..] (k = 4 db + r)
+    const int q = q0 + l32;
+    auto store4 = [&](int k, const float *vals, float inv) {
+        char *orow = (char *) p.o + (int64_t) b * p.o_nb3 + (int64_t) q * p.o_nb2 + (int64_t) h * p.o_nb1;
+        const int d0 = 32 * (k >> 2) + 8 * (k & 3) + 4 * hi;
+        if (p.out_bf16) {
+            uint16_t t4[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) t4[jj] = f32_to_bf16_bits(vals[jj] * inv);
+            u32x2 w;
+            __builtin_memcpy(&w, t4, 8);
+            *(u32x2 *) (orow + 2 * d0) = w;
+        } else {
+            *(f32x4 *) (orow + 4 * d0) = f32x4{vals[0] * inv, vals[1] * inv, vals[2] * inv, vals[3] * inv};
+        }
+    };
     if constexpr (KS > 1) {
-        float *mo = (float *) lds;                        // [KS-1][QB][32][64] partial O^T
-        float *ml = mo + (KS - 1) * QB * 32 * 64;         // [KS-1][QB][2][64]  m, l
-        if (g > 0) {
-            float *dst = mo + ((g - 1) * QB + qb) * 32 * 64;
+        // ---- merge the KS key ranges of each query block (LDS reused): every
+        // wave writes its partial O^T, running max and row sum; wave g then
+        // merges and stores values [g * JW, (g + 1) * JW) of the 32 per lane,
+        // each range weighted by exp2(m_range - m_max)
+        constexpr int JW = 32 / KS;
+        static_assert(JW % 4 == 0, "whole 4-dim groups per wave");
+        float *mo = (float *) lds;                        // [KS][QB][32][64] partial O^T
+        float *ml = mo + KS * QB * 32 * 64;               // [KS][QB][2][64]  m, l
+        {
+            float *dst = mo + (g * QB + qb) * 32 * 64;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) dst[(16 * db + e) * 64 + lane] = o[db][e];
-            float *dl = ml + ((g - 1) * QB + qb) * 128;
+            float *dl = ml + (g * QB + qb) * 128;
             dl[lane] = m_run;
             dl[64 + lane] = l_run;
         }
         __syncthreads();
-        if (g > 0) return;
-        for (int g2 = 1; g2 < KS; ++g2) {
-            const float *src = mo + ((g2 - 1) * QB + qb) * 32 * 64;
-            const float *sl = ml + ((g2 - 1) * QB + qb) * 128;
-            const float m2 = sl[lane], l2 = sl[64 + lane];
-            const float mn = fmaxf(m_run, m2);
-            if (mn == -INFINITY) continue;                // neither side saw a key
-            const float a1 = __builtin_amdgcn_exp2f(m_run - mn), a2 = __builtin_amdgcn_exp2f(m2 - mn);
-            l_run = l_run * a1 + l2 * a2;
+        float mg[KS], mx = -INFINITY;
 #pragma unroll
-            for (int db = 0; db < 2; ++db)
+        for (int g2 = 0; g2 < KS; ++g2) {
+            mg[g2] = ml[(g2 * QB + qb) * 128 + lane];
+            mx = fmaxf(mx, mg[g2]);
+        }
+        float lh = 0.0f, wt[KS];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[db][e] = o[db][e] * a1 + src[(16 * db + e) * 64 + lane] * a2;
-            m_run = mn;
+        for (int g2 = 0; g2 < KS; ++g2) {
+            wt[g2] = mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mg[g2] - mx);   // no range saw a key: 0
+            lh += ml[(g2 * QB + qb) * 128 + 64 + lane] * wt[g2];
+        }
+        float oj[JW];
+#pragma unroll
+        for (int jj = 0; jj < JW; ++jj) oj[jj] = 0.0f;
+#pragma unroll
+        for (int g2 = 0; g2 < KS; ++g2) {
+            const float *src = mo + (g2 * QB + qb) * 32 * 64 + g * JW * 64 + lane;
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj) oj[jj] += src[jj * 64] * wt[g2];
+        }
+        const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
+        const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (q >= p.Nq) return;
+#pragma unroll
+        for (int k = 0; k < JW / 4; ++k) store4(g * (JW / 4) + k, oj + 4 * k, inv);
+    } else {
+        const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+        const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (q >= p.Nq) return;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float vals[4] = {o[k >> 2][4 * (k & 3)], o[k >> 2][4 * (k & 3) + 1], o[k >> 2][4 * (k & 3) + 2],
+                                   o[k >> 2][4 * (k & 3) + 3]};
+            store4(k, vals, inv);
         }
     }
-
-    // ---- O = O^T / l; lane writes dims 32 db + 8 r + 4 hi + 0..3 of query q0 + l32
-    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-    const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const int q = q0 + l32;
-    if (q >= p.Nq) return;
-    char *orow = (char *) p.o + (int64_t) b * p.o_nb3 + (int64_t) q * p.o_nb2 + (int64_t) h * p.o_nb1;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int d0 = 32 * db + 8 * r + 4 * hi;
-            if (p.out_bf16) {
-                uint16_t t4[4];
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) t4[jj] = f32_to_bf16_bits(o[db][4 * r + jj] * inv);
-                u32x2 w;
-                __builtin_memcpy(&w, t4, 8);
-                *(u32x2 *) (orow + 2 * d0) = w;
-            } else {
-                *(f32x4 *) (orow + 4 * d0) = f32x4{o[db][4 * r] * inv, o[db][4 * r + 1] * inv,
-                                                  o[db][4 * r + 2] * inv, o[db][4 * r + 3] * inv};
-            }
-        }
 }
 
 template <bool KBF16, bool BOUNDED, int KS, int QB>
@@ -358,7 +378,7 @@ hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     const int W = p.qtiles * p.H * p.B;
     const int grid = (W + 7) / 8 * 8;
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
-    if (KS > 1) lds = max(lds, (size_t) (KS - 1) * QB * (32 * 64 + 128) * 4);
+    if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128) * 4);
     auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB>;
     static size_t attr = 0;
     if (lds > attr) {
