@@ -169,13 +169,16 @@ void attn_kernel(const AttnParams p) {
         }
     };
 
-    const bool has_mask = p.mask != nullptr;
+    const bool has_mask = p.mask != nullptr, has_rel = p.rel_lut != nullptr;
     const char *mrow[QB];
+    const float *rrow[QB];     // relative bias: rrow[qb][key] = lut value of (key - qrow)
     for (int qb = 0; qb < QB; ++qb) {
         const int qrow = qbase + qb * 16 + lr;
-        mrow[qb] = has_mask ? (const char *) p.mask + (int64_t) (qrow < p.Nq ? qrow : 0) * p.m_nb1 +
+        const int qr = qrow < p.Nq ? qrow : 0;
+        mrow[qb] = has_mask ? (const char *) p.mask + (int64_t) qr * p.m_nb1 +
                                   (int64_t) (h % p.m_ne2) * p.m_nb2 + (int64_t) (b % p.m_ne3) * p.m_nb3
                             : nullptr;
+        rrow[qb] = has_rel ? p.rel_lut + (int64_t) h * p.rel_nh + p.rel_off - qr : nullptr;
     }
 
     gload(0);
@@ -224,6 +227,9 @@ void attn_kernel(const AttnParams p) {
                     if (has_mask && key < p.Nkv) {
                         const float mv = p.mask_f16 ? f16_bits_to_f32(((const uint16_t *) mrow[qb])[key])
                                                     : ((const float *) mrow[qb])[key];
+                        x += slope * mv;
+                    } else if (has_rel && key < p.Nkv) {
+                        const float mv = rrow[qb][key] + (p.key_valid[key] ? 0.0f : -INFINITY);
                         x += slope * mv;
                     }
                     x *= 1.4426950408889634f;             // log2(e)

@@ -8,8 +8,10 @@
 //   q | k | v = Q8_0 mul_mat(W_qkv, h)                h quantized to Q8_0 once,
 //                                                     one int8-MFMA GEMM over the
 //                                                     three weights stacked
-//   o = flash_attn_ext(q, k, v, mask, scale 1)        per-head F32 mask =
-//                                                     rel_bias[bucket(k-q)] + pad
+//   o = flash_attn_ext(q, k, v, mask, scale 1)        mask[h][q][k] =
+//                                                     rel_bias[bucket(k-q)][h] + pad[k],
+//                                                     read from a per-head table
+//                                                     over k - q and the key padding
 //   x += Q8_0 mul_mat(W_o, o)                         residual in the epilogue
 //   h = rms_norm(x) * ffn_norm
 //   g = gelu(wi_0 h) * (wi_1 h)                       one GEMM over wi_0 / wi_1
@@ -17,9 +19,12 @@
 //   x += Q8_0 mul_mat(wo, g)
 // then out_norm. The reference adds the bias and the padding as two ggml_add
 // nodes before its soft_max (:69-71); the padding is 0 or -inf, so one
-// additive mask holds the same values. Bucket ids are computed on the host
-// in double precision exactly as the reference does (:95); the device only
-// gathers the bias table through them.
+// additive mask holds the same values. The attention adds, for key k of query
+// q, lut[h][k - q + max_tokens - 1] + (valid[k] ? 0 : -inf): the same float a
+// materialised [H][n][n] mask would hold, from a [H][2 max_tokens - 1] table
+// instead of 33.5 MB per layer at 512 tokens. Bucket ids are computed on the
+// host in double precision exactly as the reference does (:95); the device
+// only gathers the bias table through them.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -77,7 +82,7 @@ struct tsk_t5 {
     char *blob = nullptr;                    // every device weight
     float *rel_bias = nullptr, *out_norm = nullptr;
     // activations
-    float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *mask = nullptr, *ones = nullptr;
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *rel_lut = nullptr, *ones = nullptr;
     int8_t *qx = nullptr;
     float *dx = nullptr;
     int32_t *bkt = nullptr;                  // bucket of relative distance r at r + max_tokens - 1
@@ -87,14 +92,13 @@ struct tsk_t5 {
 
 namespace {
 
-// mask[h][q][k] = rel_bias[bkt[k - q]][h] + (valid[k] ? 0 : -inf)
-__global__ void t5_mask_kernel(const float *rel_bias, const int32_t *bkt, const uint8_t *valid, int n, int H,
-                               int maxn, float *mask) {
+// lut[h][r] = rel_bias[bkt[r]][h], r = k - q + maxn - 1 in [0, 2 maxn - 1)
+__global__ void t5_lut_kernel(const float *rel_bias, const int32_t *bkt, int H, int maxn, float *lut) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t) H * n * n) return;
-    const int k = (int) (i % n), q = (int) ((i / n) % n), h = (int) (i / ((int64_t) n * n));
-    const float b = rel_bias[(int64_t) bkt[k - q + maxn - 1] * H + h];
-    mask[i] = b + (valid[k] ? 0.0f : -INFINITY);
+    const int nr = 2 * maxn - 1;
+    if (i >= (int64_t) H * nr) return;
+    const int r = (int) (i % nr), h = (int) (i / nr);
+    lut[i] = rel_bias[(int64_t) bkt[r] * H + h];
 }
 
 __global__ void fill_kernel(float *p, int64_t n, float v) {
@@ -142,7 +146,7 @@ extern "C" void tsk_t5_default_config(tsk_t5_config *c) {
 extern "C" void tsk_t5_destroy(tsk_t5 *t) {
     if (!t) return;
     (void) hipDeviceSynchronize();
-    void *bufs[] = {t->blob, t->x, t->h, t->qkv, t->att, t->g, t->mask, t->ones, t->qx, t->dx, t->bkt, t->valid, t->io};
+    void *bufs[] = {t->blob, t->x, t->h, t->qkv, t->att, t->g, t->rel_lut, t->ones, t->qx, t->dx, t->bkt, t->valid, t->io};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
     delete t;
@@ -201,7 +205,7 @@ extern "C" int tsk_t5_create(const tsk_t5_config *cfg, tsk_t5 **out) {
         (rc = alloc((void **) &t->qkv, sizeof(float) * n * 3 * inner)) ||
         (rc = alloc((void **) &t->att, sizeof(float) * n * inner)) ||
         (rc = alloc((void **) &t->g, sizeof(float) * n * ff)) ||
-        (rc = alloc((void **) &t->mask, sizeof(float) * c.n_heads * n * n)) ||
+        (rc = alloc((void **) &t->rel_lut, sizeof(float) * c.n_heads * (2 * n - 1))) ||
         (rc = alloc((void **) &t->ones, sizeof(float) * d)) ||
         (rc = alloc((void **) &t->qx, (size_t) n * kmax)) ||
         (rc = alloc((void **) &t->dx, sizeof(float) * n * (kmax / 32))) ||
@@ -324,38 +328,36 @@ extern "C" int tsk_t5_encode_layers(tsk_t5 *t, int n, const float *x_d, const in
     for (int i = 0; i < n; ++i) valid[i] = ids[i] != 0;
     if ((rc = hipcheck(hipMemcpyAsync(t->valid, valid.data(), n, hipMemcpyHostToDevice, s), "ids"))) return rc;
     if ((rc = hipcheck(hipStreamSynchronize(s), "ids"))) return rc;    // `valid` is a host temporary
-    const int64_t nm = (int64_t) H * n * n;
-    launch_kernel(t5_mask_kernel, dim3((unsigned) ((nm + 255) / 256)), dim3(256), 0, s, (const float *) t->rel_bias,
-                  (const int32_t *) t->bkt, (const uint8_t *) t->valid, n, H, c.max_tokens, t->mask);
-    if ((rc = hipcheck(hipGetLastError(), "t5 mask"))) return rc;
+    const int64_t nl = (int64_t) H * (2 * c.max_tokens - 1);
+    launch_kernel(t5_lut_kernel, dim3((unsigned) ((nl + 255) / 256)), dim3(256), 0, s, (const float *) t->rel_bias,
+                  (const int32_t *) t->bkt, H, c.max_tokens, t->rel_lut);
+    if ((rc = hipcheck(hipGetLastError(), "t5 bias table"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(t->x, x_d, sizeof(float) * n * d, hipMemcpyDeviceToDevice, s), "x"))) return rc;
 
-    // attention views into the qkv rows [n][3 * inner] (ggml ne [64, n, H, 1])
-    tsk_tensor q, k, v, m, o;
-    auto view = [&](tsk_tensor &tv, void *data, int64_t row_bytes) {
-        memset(&tv, 0, sizeof(tv));
-        tv.type = TSK_TYPE_F32; tv.data = data;
-        tv.ne[0] = 64; tv.ne[1] = n; tv.ne[2] = H; tv.ne[3] = 1;
-        tv.nb[0] = 4; tv.nb[1] = (size_t) row_bytes; tv.nb[2] = 64 * 4; tv.nb[3] = (size_t) row_bytes * n;
-    };
-    view(q, t->qkv, (int64_t) 3 * inner * 4);
-    view(k, t->qkv + inner, (int64_t) 3 * inner * 4);
-    view(v, t->qkv + 2 * inner, (int64_t) 3 * inner * 4);
-    memset(&m, 0, sizeof(m));
-    m.type = TSK_TYPE_F32; m.data = t->mask;
-    m.ne[0] = n; m.ne[1] = n; m.ne[2] = H; m.ne[3] = 1;
-    m.nb[0] = 4; m.nb[1] = (size_t) n * 4; m.nb[2] = (size_t) n * n * 4; m.nb[3] = m.nb[2] * H;
-    memset(&o, 0, sizeof(o));                              // [64, H, n, 1]: rows of inner
-    o.type = TSK_TYPE_F32; o.data = t->att;
-    o.ne[0] = 64; o.ne[1] = H; o.ne[2] = n; o.ne[3] = 1;
-    o.nb[0] = 4; o.nb[1] = 64 * 4; o.nb[2] = (size_t) inner * 4; o.nb[3] = (size_t) inner * 4 * n;
+    // attention over the qkv rows [n][3 * inner] (ggml ne [64, n, H, 1]), F32
+    // q / k / v, scale 1, output rows of inner ([64, H, n, 1])
+    AttnParams ap;
+    memset(&ap, 0, sizeof(ap));
+    ap.q = t->qkv; ap.k = t->qkv + inner; ap.v = t->qkv + 2 * inner; ap.o = t->att;
+    ap.q_type = ap.kv_type = TSK_TYPE_F32;
+    ap.Nq = ap.Nkv = n; ap.H = ap.Hkv = H; ap.B = 1;
+    ap.q_nb1 = ap.k_nb1 = ap.v_nb1 = (int64_t) 3 * inner * 4;
+    ap.q_nb2 = ap.k_nb2 = ap.v_nb2 = 64 * 4;
+    ap.q_nb3 = ap.k_nb3 = ap.v_nb3 = (int64_t) 3 * inner * 4 * n;
+    ap.m_ne2 = ap.m_ne3 = 1;
+    ap.o_nb1 = 64 * 4; ap.o_nb2 = (int64_t) inner * 4; ap.o_nb3 = (int64_t) inner * 4 * n;
+    ap.scale = 1.0f;
+    ap.n_head_log2 = 1u << (uint32_t) floorf(log2f((float) H));
+    ap.m0 = ap.m1 = 1.0f;
+    ap.rel_lut = t->rel_lut; ap.rel_nh = 2 * c.max_tokens - 1; ap.rel_off = c.max_tokens - 1;
+    ap.key_valid = t->valid;
 
     for (int i = layer_begin; i < layer_end; ++i) {
         const Layer &ly = t->layers[i];
         if ((rc = rmsnorm(t->x, ly.attn_norm, c.eps, n, d, t->h, s))) return rc;
         if ((rc = quantize(t, t->h, n, d, s))) return rc;
         if ((rc = q8_gemm(t, ly.qkv_q, ly.qkv_d, n, d, 3 * inner, EPI_STORE, t->qkv, 3 * inner, nullptr, s))) return rc;
-        if ((rc = tsk_flash_attn_ext(&q, &k, &v, &m, 1.0f, 0.0f, 0.0f, TSK_PREC_F32, &o, stream))) return rc;
+        if ((rc = hipcheck(launch_attention(ap, s), "t5 attention"))) return rc;
         if ((rc = quantize(t, t->att, n, inner, s))) return rc;
         if ((rc = q8_gemm(t, ly.o_q, ly.o_d, n, inner, d, EPI_GATE_RES, nullptr, 0, t->x, s))) return rc;
         if ((rc = rmsnorm(t->x, ly.ffn_norm, c.eps, n, d, t->h, s))) return rc;

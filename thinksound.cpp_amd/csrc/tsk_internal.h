@@ -48,6 +48,13 @@ struct AttnParams {
     float softcap;
     float max_bias, m0, m1;
     uint32_t n_head_log2;
+    // relative-position bias in place of a mask (T5): key k of query q adds
+    // rel_lut[h * rel_nh + rel_off + k - q] + (key_valid[k] ? 0 : -inf) -- the
+    // value the materialised mask would hold; null: unused
+    const float *rel_lut;
+    int64_t rel_nh;
+    int rel_off;
+    const uint8_t *key_valid;
 };
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 
