@@ -212,6 +212,10 @@ void gemm_bf16_kernel(const GemmParams p) {
 
 // ------------------------------------------------------------------ Q8_0
 constexpr int QBK = 128;            // 4 Q8_0 blocks per K step
+// block scales of the cooperative Q8_0 tiles are staged in segments of this
+// many 32-element blocks (1024 k): 16 KiB of LDS at 64 x 64 tiles, so three
+// workgroups fit a CU next to their 2-stage ring
+constexpr int Q8_SEG = 32;
 constexpr int LDSQ = QBK + 16;      // bytes per LDS row
 
 template <int WM, int WN, int TM, int TN, int EPI, bool YBF16>
@@ -386,7 +390,7 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     // consecutive rows for one block (conflict-free). A segment's scales are
     // loaded into registers during the last stage of the previous segment and
     // written to LDS at the next segment's first stage, between two barriers.
-    constexpr int SEG = 64, PW = (SEG / 4 * BM + 255) / 256, PX = (SEG / 4 * BN + 255) / 256;
+    constexpr int SEG = Q8_SEG, PW = (SEG / 4 * BM + 255) / 256, PX = (SEG / 4 * BN + 255) / 256;
     constexpr int SPS = SEG / 4;                       // stages per segment
     float *dws = (float *) (lds + R * STG);
     float *dxs = dws + min(KB, SEG) * BM;
@@ -630,7 +634,7 @@ template <int TM, int TN, int R, int EPI, bool YBF16>
 hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
     constexpr int BM = 16 * TM, BN = 16 * TN;
     const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
-    const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) std::min(p.K / 32, 64) * (BM + BN) * 4;
+    const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) std::min(p.K / 32, Q8_SEG) * (BM + BN) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto kern = gemm_q8c_kernel<TM, TN, R, EPI, YBF16>;
     static size_t attr = 0;   // dynamic LDS opted in so far for this kernel
@@ -660,9 +664,10 @@ hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // cooperative tiles when the planes allow them: K % 128 (four-block
     // stages), M % 16, 16-byte aligned rows; block scales staged in segments
-    // of 2048 k. Measured on MI355X at 1446 rows: 64 x 64 tiles with a 2-stage
-    // ring (1024 -> 3072: 51.5 -> 36.0 us against the 2 x 2-wave kernel below,
-    // which stays for other shapes; TSK_Q8_OLD forces it for comparisons).
+    // of 1024 k (three 64 x 64 workgroups per CU). Measured on MI355X at 1446
+    // rows: 64 x 64 tiles with a 2-stage ring (1024 -> 3072: 51.5 -> 34.7 us
+    // against the 2 x 2-wave kernel below, which stays for other shapes;
+    // TSK_Q8_OLD forces it for comparisons).
     const bool coop = p.K % 128 == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
                       ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
                       !std::getenv("TSK_Q8_OLD");
