@@ -672,14 +672,20 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
                       ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
                       !std::getenv("TSK_Q8_OLD");
     if (coop) {
-        // TSK_Q8_CFG picks a tile shape for sweeps: 1 = 64 x 64 / 3 stages,
-        // 2 = 64 x 64 / 2 stages (default), 3 = 128 x 64 / 2 stages, 4 = 64 x 128 / 2 stages
-        int cfg = 2;
+        // 64 x 64 tiles with a 2-stage ring; 32 x 64 (weight rows x tokens)
+        // when the 64 x 64 grid would hold fewer than two tiles per CU
+        // (measured: 1446 x 1024 outputs at K = 1024 / 4096 19.8 -> 18.1 / 54.4
+        // -> 48.3 us; the T5 o / wo projections). TSK_Q8_CFG picks a shape for
+        // sweeps: 1 = 64 x 64 / 3 stages, 2 = 64 x 64 / 2 stages, 3 = 128 x 64,
+        // 4 = 64 x 128, 5 = 32 x 64 (2 stages)
+        const int64_t tiles64 = (int64_t) ((p.M + 63) / 64) * ((p.N + 63) / 64);
+        int cfg = tiles64 < 512 ? 5 : 2;
         if (const char *e = getenv("TSK_Q8_CFG")) cfg = atoi(e);
         switch (cfg) {
             case 2: return p.y_bf16 ? q8c_epi<4, 4, 2, true>(p, s) : q8c_epi<4, 4, 2, false>(p, s);
             case 3: return p.y_bf16 ? q8c_epi<8, 4, 2, true>(p, s) : q8c_epi<8, 4, 2, false>(p, s);
             case 4: return p.y_bf16 ? q8c_epi<4, 8, 2, true>(p, s) : q8c_epi<4, 8, 2, false>(p, s);
+            case 5: return p.y_bf16 ? q8c_epi<2, 4, 2, true>(p, s) : q8c_epi<2, 4, 2, false>(p, s);
             default: return p.y_bf16 ? q8c_epi<4, 4, 3, true>(p, s) : q8c_epi<4, 4, 3, false>(p, s);
         }
     }
