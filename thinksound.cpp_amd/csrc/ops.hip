@@ -649,6 +649,52 @@ __global__ void cfg_euler_kernel(const float *flow2, int64_t n, float cfg, float
     if (x2) { x2[i] = nx; x2[n + i] = nx; }
 }
 
+// RMS norm * w of norm_rows_kernel (RMS, one wave per row of 256 NV floats)
+// followed by the Q8_0 quantization of quantize_rows_q8_kernel, in one pass:
+// the 32-element block b of element (lane + 64 j) * 4 + e is held by lanes
+// 8 (b % 8) .. + 7 at register j = b / 8, so its amax is three DPP steps.
+// Same arithmetic as the two kernels in a row, so the same bits.
+template <int NV>
+__global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *x, int64_t ldx, const float *w, float eps,
+                                                         int8_t *qx, float *dx, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    constexpr int n = 256 * NV;
+    const float *xr = x + r * ldx;
+    f32x4 v[NV], wv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        v[j] = *(const f32x4 *) (xr + (lane + 64 * j) * 4);
+        wv[j] = *(const f32x4 *) (w + (lane + 64 * j) * 4);
+    }
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        for (int e = 0; e < 4; ++e) s2 += v[j][e] * v[j][e];
+    const float sc = 1.0f / sqrtf(wave_sum(s2) / (float) n + eps);
+    int8_t *qr = qx + r * n;
+    float *dr = dx + r * (n / 32);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        float o[4], amax = 0.0f;
+        for (int e = 0; e < 4; ++e) {
+            o[e] = v[j][e] * sc * wv[j][e];
+            amax = fmaxf(amax, fabsf(o[e]));
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) amax = fmaxf(amax, dpp_f(amax, i));   // the 8 lanes of the block
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        if ((lane & 7) == 0) dr[8 * j + (lane >> 3)] = f16_bits_to_f32(f32_to_f16_bits(d));
+        int8_t q[4];
+        for (int e = 0; e < 4; ++e) q[e] = (int8_t) __builtin_rintf(o[e] * id);
+        uint32_t w4;
+        __builtin_memcpy(&w4, q, 4);
+        *(uint32_t *) (qr + (lane + 64 * j) * 4) = w4;
+    }
+}
+
 inline unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1) / per); }
 
 }  // namespace
@@ -813,6 +859,20 @@ hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64
                       (uint16_t *) dst);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_q8(const float *x, int64_t ldx, const float *w, float eps, int8_t *qx, float *dx,
+                              int64_t rows, int n, hipStream_t s) {
+    if (rows < 1 || ldx % 4 || ((uintptr_t) x & 15) || ((uintptr_t) w & 15) || ((uintptr_t) qx & 3))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned) ((rows + 3) / 4)), blk(256);
+    switch (n) {
+        case 1024: launch_kernel(rms_norm_q8_kernel<4>, grid, blk, 0, s, x, ldx, w, eps, qx, dx, rows); break;
+        case 2048: launch_kernel(rms_norm_q8_kernel<8>, grid, blk, 0, s, x, ldx, w, eps, qx, dx, rows); break;
+        case 4096: launch_kernel(rms_norm_q8_kernel<16>, grid, blk, 0, s, x, ldx, w, eps, qx, dx, rows); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -123,6 +123,10 @@ int quantize(tsk_t5 *t, const float *x, int N, int K, hipStream_t s) {
     return hipcheck(launch_quantize_rows_q8(x, 1, K, N, K, t->qx, t->dx, s), "t5 quantize");
 }
 
+// rms_norm * w straight into the Q8_0 planes of the next GEMM's activations
+// (the two-launch path when the fused kernel does not take the width)
+int rmsnorm_q8(tsk_t5 *t, const float *x, const float *w, float eps, int N, int d, hipStream_t s);
+
 int rmsnorm(const float *x, const float *w, float eps, int N, int d, float *y, hipStream_t s) {
     View4 a;
     memset(&a, 0, sizeof(a));
@@ -132,6 +136,13 @@ int rmsnorm(const float *x, const float *w, float eps, int N, int d, float *y, h
     View4 o = a;
     o.data = y;
     return hipcheck(launch_rms_norm_mul(a, w, eps, o, s), "t5 rms_norm");
+}
+
+int rmsnorm_q8(tsk_t5 *t, const float *x, const float *w, float eps, int N, int d, hipStream_t s) {
+    if (d == 1024 || d == 2048 || d == 4096)
+        return hipcheck(launch_rms_norm_q8(x, d, w, eps, t->qx, t->dx, N, d, s), "t5 rms_norm + quantize");
+    int rc = rmsnorm(x, w, eps, N, d, t->h, s);
+    return rc ? rc : quantize(t, t->h, N, d, s);
 }
 
 }  // namespace
@@ -354,14 +365,12 @@ extern "C" int tsk_t5_encode_layers(tsk_t5 *t, int n, const float *x_d, const in
 
     for (int i = layer_begin; i < layer_end; ++i) {
         const Layer &ly = t->layers[i];
-        if ((rc = rmsnorm(t->x, ly.attn_norm, c.eps, n, d, t->h, s))) return rc;
-        if ((rc = quantize(t, t->h, n, d, s))) return rc;
+        if ((rc = rmsnorm_q8(t, t->x, ly.attn_norm, c.eps, n, d, s))) return rc;
         if ((rc = q8_gemm(t, ly.qkv_q, ly.qkv_d, n, d, 3 * inner, EPI_STORE, t->qkv, 3 * inner, nullptr, s))) return rc;
         if ((rc = hipcheck(launch_attention(ap, s), "t5 attention"))) return rc;
         if ((rc = quantize(t, t->att, n, inner, s))) return rc;
         if ((rc = q8_gemm(t, ly.o_q, ly.o_d, n, inner, d, EPI_GATE_RES, nullptr, 0, t->x, s))) return rc;
-        if ((rc = rmsnorm(t->x, ly.ffn_norm, c.eps, n, d, t->h, s))) return rc;
-        if ((rc = quantize(t, t->h, n, d, s))) return rc;
+        if ((rc = rmsnorm_q8(t, t->x, ly.ffn_norm, c.eps, n, d, s))) return rc;
         if ((rc = q8_gemm(t, ly.wi_q, ly.wi_d, n, d, 2 * ff, EPI_GEGLU, t->g, ff, nullptr, s))) return rc;
         if ((rc = quantize(t, t->g, n, ff, s))) return rc;
         if ((rc = q8_gemm(t, ly.wo_q, ly.wo_d, n, ff, d, EPI_GATE_RES, nullptr, 0, t->x, s))) return rc;

@@ -258,6 +258,11 @@ struct LnGroup {
     float eps;
 };
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s);
+// y = x / sqrt(mean(x^2) + eps) * w on F32 rows of n in {1024, 2048, 4096}
+// (16-byte aligned), quantized to Q8_0 planes qx [rows][n] / dx [rows][n/32]
+// as launch_quantize_rows_q8 does: the two launches' bits in one
+hipError_t launch_rms_norm_q8(const float *x, int64_t ldx, const float *w, float eps, int8_t *qx, float *dx,
+                              int64_t rows, int n, hipStream_t s);
 // A list of small-batch GEMVs with f32 activations (products exact in fp32):
 // out[b, j] = act( sum_k W[j, k] * x[b, k] + bias[j] ), act = silu if silu_out
 struct GemvJob {
