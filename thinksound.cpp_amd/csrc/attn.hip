@@ -28,14 +28,18 @@ constexpr int D = 64;           // head dim
 constexpr int LDS16 = D + 8;    // 16-bit row stride (elements): 144 B rows
 constexpr int LDS32 = D + 4;    // f32 row stride (elements)
 
-template <Elt QE, Elt KVE, Elt OE, int NW, int QB>
-__global__ __launch_bounds__(NW * 64)
+// KS key ranges per workgroup: the waves of range ks take key tiles
+// ks, ks + KS, ... for the same NW * QB * 16 query rows (their own LDS
+// buffers), and range 0 merges the others' running max / sum / output at the
+// end; KS = 2 puts two waves on each SIMD where the grid has one workgroup per CU
+template <Elt QE, Elt KVE, Elt OE, int NW, int QB, int KS = 1>
+__global__ __launch_bounds__(NW * 64 * KS)
 void attn_kernel(const AttnParams p) {
     constexpr bool F32 = (KVE == Elt::F32);
-    constexpr int NT = NW * 64;
+    constexpr int NT = NW * 64;      // threads of one key range
     constexpr int QROWS = NW * QB * 16;
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x % NT, ks = threadIdx.x / NT;
     const int lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int h = blockIdx.y, b = blockIdx.z;
@@ -57,8 +61,10 @@ void attn_kernel(const AttnParams p) {
     // ---------------- LDS
     typedef typename std::conditional<F32, float, uint16_t>::type lds_t;
     constexpr int LSTR = F32 ? LDS32 : LDS16;
-    __shared__ __attribute__((aligned(16))) lds_t Ks[2][KT * LSTR];
-    __shared__ __attribute__((aligned(16))) lds_t Vt[2][D * LSTR];
+    __shared__ __attribute__((aligned(16))) lds_t Ks_all[KS][2][KT * LSTR];
+    __shared__ __attribute__((aligned(16))) lds_t Vt_all[KS][2][D * LSTR];
+    lds_t (*Ks)[KT * LSTR] = Ks_all[ks];
+    lds_t (*Vt)[D * LSTR] = Vt_all[ks];
 
     // ---------------- Q fragments (B operand of S^T = K.Q^T)
     // 16-bit: lane holds Q[q = lr][32*kc + 8*lg + j], j < 8, kc < 2
@@ -111,6 +117,7 @@ void attn_kernel(const AttnParams p) {
     u32x4 vreg[VPER][2];
 
     const int ntiles = (p.Nkv + KT - 1) / KT;
+    const int niter = (ntiles + KS - 1) / KS;   // the same count in every key range
 
     auto gload = [&](int tile) {
         const int k0 = tile * KT;
@@ -181,14 +188,15 @@ void attn_kernel(const AttnParams p) {
         rrow[qb] = has_rel ? p.rel_lut + (int64_t) h * p.rel_nh + p.rel_off - qr : nullptr;
     }
 
-    gload(0);
+    // tiles past the last key load zeros and are masked like keys >= Nkv
+    gload(ks);
     lstore(0);
     __syncthreads();
 
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int buf = tile & 1;
-        if (tile + 1 < ntiles) gload(tile + 1);
-        const int k0 = tile * KT;
+    for (int it = 0; it < niter; ++it) {
+        const int buf = it & 1;
+        if (it + 1 < niter) gload((it + 1) * KS + ks);
+        const int k0 = (it * KS + ks) * KT;
 
         // ---- S^T = K . Q^T : s[qb][t][r] = S^T[key = k0+16t+4lg+r][q = lr]
         f32x4 s[QB][4];
@@ -281,8 +289,41 @@ void attn_kernel(const AttnParams p) {
                 }
         }
 
-        if (tile + 1 < ntiles) lstore(buf ^ 1);
+        if (it + 1 < niter) lstore(buf ^ 1);
         __syncthreads();
+    }
+
+    if constexpr (KS > 1) {
+        // ranges 1.. leave (m, l, O^T) per lane in their K buffers (every read
+        // of them ended at the loop's last barrier); range 0
+        // rescales both to the larger max and adds
+        constexpr int PER = QB * 18;
+        static_assert(NT * PER * sizeof(float) <= sizeof(Ks_all[0]), "merge buffer");
+        if (ks > 0) {
+            float *st = (float *) Ks_all[ks] + tid;
+            for (int qb = 0; qb < QB; ++qb) {
+                st[(qb * 18) * NT] = m_run[qb];
+                st[(qb * 18 + 1) * NT] = l_run[qb];
+                for (int dt = 0; dt < 4; ++dt)
+                    for (int r = 0; r < 4; ++r) st[(qb * 18 + 2 + 4 * dt + r) * NT] = oacc[qb][dt][r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
+        for (int o = 1; o < KS; ++o) {
+            const float *st = (const float *) Ks_all[o] + tid;
+            for (int qb = 0; qb < QB; ++qb) {
+                const float m1 = st[(qb * 18) * NT], l1 = st[(qb * 18 + 1) * NT];
+                const float m = fmaxf(m_run[qb], m1);
+                const float mu = m == -INFINITY ? 0.0f : m;
+                const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+                l_run[qb] = l_run[qb] * a0 + l1 * a1;
+                m_run[qb] = m;
+                for (int dt = 0; dt < 4; ++dt)
+                    for (int r = 0; r < 4; ++r)
+                        oacc[qb][dt][r] = oacc[qb][dt][r] * a0 + st[(qb * 18 + 2 + 4 * dt + r) * NT] * a1;
+            }
+        }
     }
 
     // ---------------- epilogue: O = O^T / l, dst ne = [D, H, Nq, B]
@@ -314,7 +355,13 @@ hipError_t launch_attn_t(const AttnParams &p, hipStream_t s) {
     // 4 waves x 1 block of 16 rows when few rows, else 4 waves x 2 blocks
     const int rows_per_wg_big = 4 * 2 * 16;
     const int64_t wgs_big = (int64_t) ((p.Nq + rows_per_wg_big - 1) / rows_per_wg_big) * p.H * p.B;
-    if (KVE != Elt::F32 && wgs_big >= 256) {
+    const int64_t wgs_small = (int64_t) ((p.Nq + 63) / 64) * p.H * p.B;
+    if (KVE == Elt::F32 && wgs_small <= 256) {
+        // F32 K/V on at most one workgroup per CU: two key ranges per
+        // workgroup (139 KiB of LDS), so two waves share each SIMD
+        dim3 grid((p.Nq + 63) / 64, p.H, p.B);
+        launch_kernel((attn_kernel<QE, KVE, OE, 4, 1, 2>), grid, dim3(512), 0, s, p);
+    } else if (KVE != Elt::F32 && wgs_big >= 256) {
         dim3 grid((p.Nq + rows_per_wg_big - 1) / rows_per_wg_big, p.H, p.B);
         launch_kernel((attn_kernel<QE, KVE, OE, 4, 2>), grid, dim3(256), 0, s, p);
     } else {
