@@ -68,20 +68,69 @@ def measured_traffic(role):
     return float(table[role]) if role in table else None
 
 
-def cpu_baseline(weights, lat, t, txt, threads):
-    """The oracle's flow step (same weights and inputs) on this host's cores."""
+def cpu_info():
+    """CPU model, the vector-ISA flags that matter to a GEMM, and core counts of this host."""
+    model, flags = None, []
+    try:
+        for line in open("/proc/cpuinfo"):
+            if model is None and line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+            if not flags and line.startswith("flags"):
+                have = set(line.split(":", 1)[1].split())
+                flags = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512_vnni", "avx512_bf16",
+                                     "amx_bf16", "amx_int8") if f in have]
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return {"model": model, "flags": flags, "logical_cpus": os.cpu_count(), "allowed_cpus": allowed}
+
+
+def cpu_baseline(weights, lat, t, txt, runs=5):
+    """The oracle's flow step (the same weights and inputs as the GPU step) on
+    this host: one warm-up, then the median of `runs` timed steps, at 4
+    threads (ggml-cpu's default thread count: the reference never sets
+    n_threads, src/common/ts_backend.h:10-16) and at every allowed core (at
+    most 16, the host share of one GPU); CFG as one B = 2 forward, and as the
+    reference's two B = 1 forwards per step (src/mmdit.cpp:363-364) on all
+    allowed cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    oracle.set_threads(threads)
+    info = cpu_info()
+    nthreads = max(1, min(16, info["allowed_cpus"]))
     od = oracle.OracleDiT(oracle.dit_config())
     for k, v in weights.items():
         od.set_tensor(k, v)
-    t0 = time.perf_counter()
-    od.forward(lat, t, txt, act_bf16=True, kv_f16=True)
-    dt = time.perf_counter() - t0
-    return {"value": round(1.0 / dt, 4), "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"one full 21-block CFG-batched flow step at 9 s (B=2, 194+77 tokens), "
-                      f"oracle C restatement of ggml-cpu semantics, {threads} threads, {dt:.2f} s"}
+
+    def timed(threads, fn):
+        oracle.set_threads(threads)
+        fn()
+        walls = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            walls.append(time.perf_counter() - t0)
+        return sorted(walls)[len(walls) // 2], [round(w, 3) for w in walls]
+
+    b2 = lambda: od.forward(lat, t, txt, act_bf16=True, kv_f16=True)
+
+    def two_b1():
+        od.forward(lat[:1], t[:1], txt[:1], act_bf16=True, kv_f16=True)
+        od.forward(lat[1:], t[1:], txt[1:], act_bf16=True, kv_f16=True)
+
+    med_all, walls_all = timed(nthreads, b2)
+    med_b1, walls_b1 = timed(nthreads, two_b1)
+    med_4, walls_4 = timed(4, b2)
+    return {"value": round(1.0 / med_all, 4), "unit": "steps/s", "cores": nthreads, "kind": "port",
+            "sample": f"one full 21-block CFG-batched flow step at 9 s (B=2, 194+77 tokens), the oracle's C "
+                      f"restatement of ggml-cpu semantics on {nthreads} threads; 1 warm-up, median of {runs}",
+            "cpu": info,
+            "median_s": round(med_all, 4), "runs_s": walls_all,
+            "threads_4": {"steps_per_s": round(1.0 / med_4, 4), "median_s": round(med_4, 4), "runs_s": walls_4},
+            "cfg_two_b1_forwards": {"threads": nthreads, "steps_per_s": round(1.0 / med_b1, 4),
+                                    "median_s": round(med_b1, 4), "runs_s": walls_b1}}
 
 
 def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
@@ -224,6 +273,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    import numpy as np
     from __graft_entry__ import ensure_built, load_tsk
 
     ensure_built()
@@ -236,7 +286,8 @@ def main():
 
     def run(T, steps, warmup, timing):
         lat, t, txt = make_inputs(2, T)
-        lat_d, txt_d = tsk.to_device(lat), tsk.to_device(txt)
+        # ts_dit::forward's latent layout ne = [T, 64, B]
+        lat_d, txt_d = tsk.to_device(np.ascontiguousarray(lat.transpose(0, 2, 1))), tsk.to_device(txt)
         flow = tsk.empty((2, T, 64))
         for _ in range(warmup):
             dit.forward_device(lat_d, t, txt_d, flow)
@@ -267,9 +318,8 @@ def main():
     # (646 latent + 77 text tokens, cond/uncond batched as B = 2 per step),
     # noise N(0, 1) from seed 4242; wall clock around tsk_dit_sample (one
     # warm-up sample, median of 3)
-    import numpy as np
     rng = np.random.default_rng(4242)
-    noise = rng.standard_normal((646, 64), dtype=np.float32)
+    noise = np.ascontiguousarray(rng.standard_normal((646, 64), dtype=np.float32).T)   # ne = [T, 64]
     tc = rng.standard_normal((77, 1024), dtype=np.float32)
     tu = rng.standard_normal((77, 1024), dtype=np.float32)
     dit.sample(noise, tc, tu, steps=24, cfg_scale=5.0)
@@ -334,8 +384,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9
-        threads = min(16, os.cpu_count() or 1)
-        out["cpu_baseline"] = cpu_baseline(weights, lat, t, txt, threads)
+        out["cpu_baseline"] = cpu_baseline(weights, lat, t, txt)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -20,6 +20,9 @@
  *   tsk_conv_mlp_swiglu <- convmlp                             src/mmdit.cpp:39-44
  *   tsk_mlp_swiglu      <- mlp                                 src/mmdit.cpp:47-52
  *   tsk_dit_*           <- ts_dit::load / forward / sample     src/mmdit.h:9-42
+ *   tsk_t5_attention    <- mul_mat(k,q) + bias + pad -> soft_max -> mul_mat
+ *                                                              src/t5_encoder.cpp:68-73
+ *   tsk_t5_*            <- ts_t5::load / encode                src/t5_encoder.cpp:28-104
  *
  * Conventions (all follow ggml):
  *   - tensors are non-owning views: ne[] = extents with ne[0] fastest,
@@ -31,7 +34,14 @@
  *     aborting (ggml would GGML_ASSERT);
  *   - kernels are enqueued on the given stream (a hipStream_t; NULL = the
  *     null stream) and are not synchronised; entry points are reentrant per
- *     stream.
+ *     stream: calls on different streams may run concurrently from different
+ *     host threads (one stream per caller thread, as a ggml backend uses it);
+ *   - operators that need device scratch take it from the workspace of their
+ *     stream: a buffer the caller binds with tsk_set_workspace (sized with
+ *     tsk_workspace_size; the library then never allocates), or else one the
+ *     library owns per (device, stream) and grows on first need (that growth
+ *     waits for the stream and reallocates; once every shape has been seen
+ *     no operator allocates or synchronises).
  */
 #ifndef TSK_TSK_H
 #define TSK_TSK_H
@@ -91,10 +101,24 @@ typedef void *tsk_stream;   /* hipStream_t */
 
 /* ---- library ---------------------------------------------------------- */
 
-/* Select the HIP device and create per-device state. Idempotent. */
+/* Select the HIP device, read its limits (CU count, LDS per workgroup) and
+ * the launch-shape overrides of tuning sweeps (TSK_* environment variables,
+ * read here and never on a launch). Idempotent; a later call re-reads them. */
 int         tsk_init(int device);
 /* Release library-owned device memory (workspaces). */
 int         tsk_shutdown(void);
+/*
+ * Bind a caller-owned device buffer (256-byte aligned) as the workspace of
+ * every operator enqueued on `stream` on the current device; ptr = NULL,
+ * bytes = 0 unbinds. An operator whose scratch exceeds `bytes` returns
+ * TSK_ERR_NOMEM. The buffer must stay valid while work queued on the stream
+ * may read it. No counterpart in ggml (whose backends keep scratch pools):
+ * for callers that cannot let a library allocate.
+ */
+int         tsk_set_workspace(tsk_stream stream, void *ptr, size_t bytes);
+/* Free the library-owned workspace of `stream` (call before destroying a
+ * stream that operators ran on; waits for it). */
+int         tsk_release_workspace(tsk_stream stream);
 /* Text for a tsk_status value. */
 const char *tsk_status_string(int status);
 /* Detail of the last error reported on the calling thread ("" if none). */
@@ -138,10 +162,38 @@ int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tenso
                        float logit_softcap, int prec, tsk_tensor *dst,
                        tsk_stream stream);
 
+/*
+ * The T5 encoder's self-attention chain (src/t5_encoder.cpp:68-73): scores =
+ * mul_mat(k, q) (no 1/sqrt(d): scale 1 there) + the relative-position bias
+ * rel_bias[bucket(k - q)][h] (:69, :95) + the padding mask (-inf on keys
+ * whose token id is 0, :70, :97) -> soft_max -> mul_mat(v^T, .), run as one
+ * flash attention whose bias comes from a per-head table over k - q:
+ *   q, k, v  : F32 ne = [64, n, H, 1], rows 16-byte aligned
+ *   rel_lut  : F32 ne = [2 n_max - 1, H], n_max >= n, rows contiguous:
+ *              rel_lut[h][n_max - 1 + k - q] is the bias of key k for query q
+ *   key_valid: DEVICE uint8 [n], 0 marks a padded key (its weight is 0)
+ *   dst      : F32 ne = [64, H, n, 1] (ggml's permuted result)
+ * A row whose keys are all padded gives 0 (ggml: 0/0 guarded as 0).
+ */
+int tsk_t5_attention(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
+                     const tsk_tensor *rel_lut, const uint8_t *key_valid, float scale,
+                     tsk_tensor *dst, tsk_stream stream);
+
 /* dst = rms_norm(x, eps) * w   over ne[0] of x (F32/BF16 in, same type out);
  * w F32 ne = [ne0]. */
 int tsk_rms_norm_mul(const tsk_tensor *x, const tsk_tensor *w, float eps,
                      tsk_tensor *dst, tsk_stream stream);
+
+/*
+ * T5's pre-projection norm and the conversion of the Q8_0 mul_mat that
+ * follows it (src/t5_encoder.cpp:58-61, :79-81): dst = Q8_0 quantization
+ * (tsk_q8_0_quantize's rounding) of rms_norm(x, eps) * w, in one pass over
+ * the row -- the same bits as tsk_rms_norm_mul followed by tsk_q8_0_quantize.
+ * x F32 ne = [n, rows] (n = 1024, 2048 or 4096; rows 16-byte aligned), w F32
+ * [n], dst Q8_0 of x's shape (nb[0] = 34). Scratch: the stream's workspace.
+ */
+int tsk_rms_norm_q8_0(const tsk_tensor *x, const tsk_tensor *w, float eps, tsk_tensor *dst,
+                      tsk_stream stream);
 
 /* dst = layer norm (no affine) of x over ne[0], eps as ggml_norm. F32/BF16. */
 int tsk_norm(const tsk_tensor *x, float eps, tsk_tensor *dst, tsk_stream stream);
@@ -256,13 +308,23 @@ enum tsk_op {
     TSK_OP_ROPE_EXT       = 4,
     TSK_OP_NORM           = 5,
     TSK_OP_IM2COL         = 6,   /* srcs: kernel, x; fixed s0 = 1, p0 = 1, d0 = 1 */
-    TSK_OP_CONV1D         = 7    /* srcs: w, x, bias; fixed s0 = 1, p0 = 1, d0 = 1 */
+    TSK_OP_CONV1D         = 7,   /* srcs: w, x, bias; fixed s0 = 1, p0 = 1, d0 = 1 */
+    TSK_OP_CONV_MLP_SWIGLU = 8,  /* srcs: w1, w3, w2, x */
+    TSK_OP_MLP_SWIGLU     = 9,   /* srcs: w1, w3, w2, x */
+    TSK_OP_RMS_NORM_Q8_0  = 10   /* srcs: x, w */
 };
 /* Mirror of a ggml backend's supports_op: 1 if tsk would run the node with
  * these operand descriptors (data pointers are not inspected), else 0.
  * srcs follow the argument order of the matching entry point. */
 int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs,
                     const tsk_tensor *dst);
+/* Device scratch (bytes) the node needs from its stream's workspace
+ * (tsk_set_workspace); 0 for operators that need none. Validates the
+ * descriptors like the entry point (data pointers are not inspected) and
+ * returns its status. Counterpart of a ggml backend's buffer sizing
+ * (ggml_backend_buft_get_alloc_size); srcs as for tsk_supports_op. */
+int tsk_workspace_size(int op, const tsk_tensor *const *srcs, int n_srcs,
+                       const tsk_tensor *dst, size_t *bytes);
 
 /* ---- GGUF ingestion (ts_model::load_backend, src/common/ts_model.cpp:13-41) --
  * A host-side reader of the GGUF v2/v3 files the converters write
@@ -382,32 +444,39 @@ int  tsk_dit_tensor_info(const tsk_dit *dit, int i, const char **name, int64_t n
 int  tsk_dit_set_tensor(tsk_dit *dit, const char *name, const float *host_f32,
                         int64_t n_elements);
 /*
- * One flow evaluation for B (<= max_batch) rows, all pointers HOST:
- *   latent [B, T, latent_dim], t [B], text [B, text_seq, hidden]
- *   -> flow [B, T, latent_dim].
+ * One flow evaluation for B (<= max_batch) rows, all pointers HOST, in the
+ * layouts of ts_dit::forward (src/mmdit.h:26-29, src/mmdit.cpp:138, :289)
+ * with the batch as the outermost dimension:
+ *   latent ggml ne = [T, latent_dim, B]  (C order [B][latent_dim][T]),
+ *   t [B], text ne = [hidden, text_seq, B]  (C order [B][text_seq][hidden])
+ *   -> flow ne = [latent_dim, T, B]  (C order [B][T][latent_dim]).
  */
 int  tsk_dit_forward(tsk_dit *dit, int B, int T, const float *latent, const float *t,
                      const float *text, float *flow, tsk_stream stream);
-/* Same with DEVICE pointers for latent / text / flow (f32) and the B
- * timesteps on the HOST (the t-embedding is built on the host in fp32 as
- * mmdit.cpp:305-314 does); no host synchronisation. */
+/* Same with DEVICE pointers for latent / text / flow (f32, same layouts) and
+ * the B timesteps on the HOST (the t-embedding is built on the host in fp32
+ * as mmdit.cpp:305-314 does); no host synchronisation. */
 int  tsk_dit_forward_device(tsk_dit *dit, int B, int T, const float *latent_d,
                             const float *t_host, const float *text_d, float *flow_d,
                             tsk_stream stream);
 /*
  * Rectified-flow Euler sampler with CFG (ts_dit::sample, mmdit.cpp:344-376),
- * cond/uncond batched as B=2 per step. HOST pointers:
- *   noise [T, latent_dim], text_cond / text_uncond [text_seq, hidden]
- *   -> out [T, latent_dim]; flow0 (nullable) = CFG velocity of step 0.
+ * cond/uncond batched as B=2 per step. HOST pointers, ts_dit::sample's
+ * layouts (src/mmdit.h:31-33):
+ *   noise ne = [T, latent_dim] (C order [latent_dim][T]),
+ *   text_cond / text_uncond ne = [hidden, text_seq]
+ *   -> out ne = [T, latent_dim]; flow0 (nullable, ne = [T, latent_dim]) =
+ *   the CFG velocity of step 0.
  */
 int  tsk_dit_sample(tsk_dit *dit, int T, const float *noise, const float *text_cond,
                     const float *text_uncond, int steps, float cfg_scale,
                     float *out, float *flow0, tsk_stream stream);
 /* dit.* metadata of convert_thinksound.py:38-45 over the values already in cfg */
 int  tsk_dit_config_from_gguf(const tsk_gguf *g, tsk_dit_config *cfg);
-/* every weight by name from a GGUF file: F32 / F16 / BF16 / Q8_0 tensors,
- * converted to f32 and set as tsk_dit_set_tensor does (matrices rounded to
- * the driver's BF16, so a Q8_0 file loads as bf16(fp32(d) * q)) */
+/* every weight by name from a GGUF file: F32 / F16 / BF16 tensors, converted
+ * to f32 and set as tsk_dit_set_tensor does (matrices rounded to the
+ * driver's BF16); a Q8_0 matrix returns TSK_ERR_TYPE (this driver runs BF16
+ * weights) */
 int  tsk_dit_load_gguf(tsk_dit *dit, const tsk_gguf *g);
 
 /*

@@ -72,6 +72,8 @@ def lib():
                    "orc_fp32_to_bf16_row", "orc_bf16_to_fp32_row"):
             getattr(L, nm).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_gelu_tanh.argtypes = [ctypes.c_float]
+        L.orc_gelu_tanh.restype = ctypes.c_float
         L.orc_dit_create.argtypes = [ctypes.POINTER(DitConfig)]
         L.orc_dit_create.restype = ctypes.c_void_p
         L.orc_dit_destroy.argtypes = [ctypes.c_void_p]
@@ -177,6 +179,13 @@ def _ttype(arr, bf16):
 
 
 # ---------------------------------------------------------------- Q8_0
+def gelu_tanh(x):
+    """orc_gelu_tanh element by element (float32 in and out)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = lib().orc_gelu_tanh
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
 def quantize_q8_0(x, mode=Q8_CPU_SIMD):
     """(..., K) float32 -> (rows, K/32, 34) uint8 ggml block_q8_0 bytes."""
     x = np.ascontiguousarray(x, dtype=np.float32)

@@ -13,6 +13,7 @@
 #include "tsk_oracle.h"
 
 #include <math.h>
+#include <immintrin.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -163,7 +164,7 @@ static inline float tget(const tsk_tensor *t, const char *p) {
 typedef struct {
     const tsk_tensor *a, *b, *bias; tsk_tensor *dst;
     int64_t K, M, N;           /* N = all src1 rows (ne1*ne2*ne3) */
-    float  *bx;                /* src1 rows converted to a's vec_dot precision (F32 values) */
+    double *bx;                /* src1 rows converted to a's vec_dot precision (exact in fp64) */
     orc_block_q8_0 *bq;        /* src1 rows quantized (Q8_0 weights) */
     float  *arow_buf;          /* per-thread not needed: rows converted on the fly */
 } mm_ctx;
@@ -179,31 +180,74 @@ static inline char *d_row(tsk_tensor *d, int64_t n) {
     return (char *) d->data + n1 * d->nb[1] + n2 * d->nb[2] + n3 * d->nb[3];
 }
 
-/* dot product with 8 independent fp64 lanes (fixed order, vectorisable) */
-static double dot_f64(const float *x, const float *y, int64_t K) {
-    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int64_t k = 0;
-    for (; k + 8 <= K; k += 8)
-        for (int j = 0; j < 8; ++j) acc[j] += (double) x[k + j] * (double) y[k + j];
+/* Dot products in fp64 with 8 independent lanes: lane j sums the products
+ * of k = j, j + 8, ... in k order (each product of two floats is exact in
+ * fp64), then s = ((0 + lane0) + lane1) + ... + lane7, then the k % 8 tail
+ * in k order. Four weight rows share one pass over an x row (32 independent
+ * accumulator chains); every output keeps exactly this summation order. */
+typedef double orc_v4d __attribute__((vector_size(32)));
+
+static inline orc_v4d ld4d(const double *p) { orc_v4d v; memcpy(&v, p, sizeof(v)); return v; }
+
+static double lanes_sum(orc_v4d lo, orc_v4d hi) {
     double s = 0.0;
-    for (int j = 0; j < 8; ++j) s += acc[j];
-    for (; k < K; ++k) s += (double) x[k] * (double) y[k];
+    for (int j = 0; j < 4; ++j) s += lo[j];
+    for (int j = 0; j < 4; ++j) s += hi[j];
     return s;
 }
 
+/* lane-wise acc + a * b with one rounding: a and b hold float values, so
+ * a * b is exact in fp64 and this is the same double as round(a * b) + acc */
+static inline orc_v4d mad4d(orc_v4d acc, orc_v4d a, orc_v4d b) {
+    __m256d r = _mm256_fmadd_pd((__m256d) a, (__m256d) b, (__m256d) acc);
+    return (orc_v4d) r;
+}
+
+/* w: 4 rows of K doubles (row stride K), y: K doubles */
+static void dot4_f64(const double *w, const double *y, int64_t K, double out[4]) {
+    orc_v4d l0 = {0, 0, 0, 0}, h0 = l0, l1 = l0, h1 = l0, l2 = l0, h2 = l0, l3 = l0, h3 = l0;
+    int64_t k = 0;
+    for (; k + 8 <= K; k += 8) {
+        const orc_v4d ylo = ld4d(y + k), yhi = ld4d(y + k + 4);
+        l0 = mad4d(l0, ld4d(w + k), ylo);          h0 = mad4d(h0, ld4d(w + k + 4), yhi);
+        l1 = mad4d(l1, ld4d(w + K + k), ylo);      h1 = mad4d(h1, ld4d(w + K + k + 4), yhi);
+        l2 = mad4d(l2, ld4d(w + 2 * K + k), ylo);  h2 = mad4d(h2, ld4d(w + 2 * K + k + 4), yhi);
+        l3 = mad4d(l3, ld4d(w + 3 * K + k), ylo);  h3 = mad4d(h3, ld4d(w + 3 * K + k + 4), yhi);
+    }
+    out[0] = lanes_sum(l0, h0); out[1] = lanes_sum(l1, h1);
+    out[2] = lanes_sum(l2, h2); out[3] = lanes_sum(l3, h3);
+    for (; k < K; ++k)
+        for (int r = 0; r < 4; ++r) out[r] += w[r * K + k] * y[k];
+}
+
+/* weight rows in chunks of 16 (converted to fp64 once), each x row read once
+ * per chunk and multiplied with its four groups of four rows */
 static void mm_rows_float(void *p, int64_t lo, int64_t hi) {
     mm_ctx *c = (mm_ctx *) p;
     const tsk_tensor *a = c->a;
-    float *wrow = (float *) malloc(sizeof(float) * c->K);
-    for (int64_t m = lo; m < hi; ++m) {
-        const char *ar = (const char *) a->data + m * a->nb[1];
-        for (int64_t k = 0; k < c->K; ++k) wrow[k] = tget(a, ar + k * a->nb[0]);
-        const float bm = c->bias ? ((const float *) c->bias->data)[m] : 0.0f;
+    const int64_t K = c->K;
+    enum { CH = 16 };
+    double *wrow = (double *) malloc(sizeof(double) * (size_t) (CH * K));
+    for (int64_t m0 = lo; m0 < hi; m0 += CH) {
+        const int nm = hi - m0 < CH ? (int) (hi - m0) : CH;
+        for (int r = 0; r < CH; ++r) {
+            /* rows past hi repeat the last one (computed, never stored) */
+            const int64_t m = m0 + (r < nm ? r : nm - 1);
+            const char *ar = (const char *) a->data + m * a->nb[1];
+            for (int64_t k = 0; k < K; ++k) wrow[r * K + k] = (double) tget(a, ar + k * a->nb[0]);
+        }
         for (int64_t n = 0; n < c->N; ++n) {
-            double s = dot_f64(wrow, c->bx + n * c->K, c->K);
-            float v = (float) s;
-            if (c->bias) v += bm;
-            *(float *) (d_row(c->dst, n) + m * sizeof(float)) = v;
+            float *dr = (float *) d_row(c->dst, n);
+            for (int g = 0; g * 4 < nm; ++g) {
+                double s[4];
+                dot4_f64(wrow + (size_t) g * 4 * K, c->bx + n * K, K, s);
+                for (int r = 0; r < 4 && g * 4 + r < nm; ++r) {
+                    const int64_t m = m0 + g * 4 + r;
+                    float v = (float) s[r];
+                    if (c->bias) v += ((const float *) c->bias->data)[m];
+                    dr[m] = v;
+                }
+            }
         }
     }
     free(wrow);
@@ -251,15 +295,15 @@ int orc_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias
     }
     if (a->type != TSK_TYPE_F32 && a->type != TSK_TYPE_F16 && a->type != TSK_TYPE_BF16) return TSK_ERR_TYPE;
     /* src1 converted to the weight's vec_dot type (BF16: RNE to bf16; F16: to fp16) */
-    c.bx = (float *) malloc(sizeof(float) * (size_t) (c.N * K));
+    c.bx = (double *) malloc(sizeof(double) * (size_t) (c.N * K));
     for (int64_t n = 0; n < c.N; ++n) {
         const float *xr = (const float *) b_row(b, n);
-        float *o = c.bx + n * K;
+        double *o = c.bx + n * K;
         for (int64_t k = 0; k < K; ++k) {
             float x = xr[k];
             if (a->type == TSK_TYPE_BF16) x = orc_bf16_to_fp32(orc_fp32_to_bf16(x));
             else if (a->type == TSK_TYPE_F16) x = orc_fp16_to_fp32(orc_fp32_to_fp16(x));
-            o[k] = x;
+            o[k] = (double) x;
         }
     }
     orc_parallel(M, mm_rows_float, &c);
@@ -279,19 +323,40 @@ typedef struct {
     float m0, m1; uint32_t n_head_log2;
 } fa_ctx;
 
+/* K and V of one (kv head, batch item) as floats, converted once per slice
+ * (the rows of a thread's range mostly share one slice) */
+typedef struct {
+    int64_t ik2, iq3;
+    float *K, *V;
+} fa_slice;
+
+static void fa_load_slice(const fa_ctx *c, fa_slice *sl, int64_t ik2, int64_t iq3) {
+    if (sl->ik2 == ik2 && sl->iq3 == iq3) return;
+    for (int64_t ic = 0; ic < c->Nkv; ++ic) {
+        const char *kp = (const char *) c->k->data + ic * c->k->nb[1] + ik2 * c->k->nb[2] + iq3 * c->k->nb[3];
+        const char *vp = (const char *) c->v->data + ic * c->v->nb[1] + ik2 * c->v->nb[2] + iq3 * c->v->nb[3];
+        for (int64_t d = 0; d < c->D; ++d) sl->K[ic * c->D + d] = tget(c->k, kp + d * c->k->nb[0]);
+        for (int64_t d = 0; d < c->Dv; ++d) sl->V[ic * c->Dv + d] = tget(c->v, vp + d * c->v->nb[0]);
+    }
+    sl->ik2 = ik2;
+    sl->iq3 = iq3;
+}
+
 static void fa_rows(void *p, int64_t lo, int64_t hi) {
     fa_ctx *c = (fa_ctx *) p;
     const int64_t D = c->D, Dv = c->Dv;
     float *Qc = (float *) malloc(sizeof(float) * D);
-    float *Kr = (float *) malloc(sizeof(float) * D);
-    float *Vr = (float *) malloc(sizeof(float) * Dv);
     double *acc = (double *) malloc(sizeof(double) * Dv);
     uint16_t *acc16 = (uint16_t *) malloc(sizeof(uint16_t) * Dv);
+    fa_slice sl = { -1, -1, (float *) malloc(sizeof(float) * (size_t) (c->Nkv * D)),
+                    (float *) malloc(sizeof(float) * (size_t) (c->Nkv * Dv)) };
+    double *sdots = (double *) malloc(sizeof(double) * (size_t) c->Nkv);
     float scale = c->scale;
     if (c->softcap != 0.0f) scale /= c->softcap;
     for (int64_t r = lo; r < hi; ++r) {
         const int64_t iq1 = r % c->Nq, iq2 = (r / c->Nq) % c->H, iq3 = r / (c->Nq * c->H);
         const int64_t ik2 = iq2 / (c->H / c->Hkv);
+        fa_load_slice(c, &sl, ik2, iq3);
         /* ALiBi slope (ggml): 1 when max_bias == 0 */
         float slope = 1.0f;
         if (c->max_bias > 0.0f) {
@@ -307,6 +372,26 @@ static void fa_rows(void *p, int64_t lo, int64_t hi) {
             else if (c->k->type == TSK_TYPE_BF16) x = orc_bf16_to_fp32(orc_fp32_to_bf16(x));
             Qc[d] = x;
         }
+        /* q.k of every key, each one summed over d in order in fp64 (exact
+         * products); four keys side by side as independent chains */
+        int64_t ic = 0;
+        for (; ic + 4 <= c->Nkv; ic += 4) {
+            const float *k0 = sl.K + ic * D;
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                const double qd = (double) Qc[d];
+                s0 += qd * (double) k0[d];
+                s1 += qd * (double) k0[D + d];
+                s2 += qd * (double) k0[2 * D + d];
+                s3 += qd * (double) k0[3 * D + d];
+            }
+            sdots[ic] = s0; sdots[ic + 1] = s1; sdots[ic + 2] = s2; sdots[ic + 3] = s3;
+        }
+        for (; ic < c->Nkv; ++ic) {
+            double sd = 0.0;
+            for (int64_t d = 0; d < D; ++d) sd += (double) Qc[d] * (double) sl.K[ic * D + d];
+            sdots[ic] = sd;
+        }
         const char *mp = NULL;
         if (c->mask) {
             const tsk_tensor *mk = c->mask;
@@ -315,7 +400,7 @@ static void fa_rows(void *p, int64_t lo, int64_t hi) {
         double S = 0.0; float M = -INFINITY;
         for (int64_t d = 0; d < Dv; ++d) { acc[d] = 0.0; acc16[d] = 0; }
         const int f16acc = c->vacc_f16 && c->v->type == TSK_TYPE_F16;
-        for (int64_t ic = 0; ic < c->Nkv; ++ic) {
+        for (ic = 0; ic < c->Nkv; ++ic) {
             float mv = 0.0f;
             if (mp) {
                 float mval = c->mask->type == TSK_TYPE_F16 ? orc_fp16_to_fp32(((const uint16_t *) mp)[ic])
@@ -323,17 +408,12 @@ static void fa_rows(void *p, int64_t lo, int64_t hi) {
                 mv = slope * mval;
                 if (mv == -INFINITY) continue;
             }
-            const char *kp = (const char *) c->k->data + ic * c->k->nb[1] + ik2 * c->k->nb[2] + iq3 * c->k->nb[3];
-            for (int64_t d = 0; d < D; ++d) Kr[d] = tget(c->k, kp + d * c->k->nb[0]);
-            double sd = 0.0;
-            for (int64_t d = 0; d < D; ++d) sd += (double) Qc[d] * (double) Kr[d];
-            float s = (float) sd * scale;
+            float s = (float) sdots[ic] * scale;
             if (c->softcap != 0.0f) s = c->softcap * tanhf(s);
             s += mv;
             const float Mold = M;
             float ms = 1.0f, vs = 1.0f;
-            const char *vp = (const char *) c->v->data + ic * c->v->nb[1] + ik2 * c->v->nb[2] + iq3 * c->v->nb[3];
-            for (int64_t d = 0; d < Dv; ++d) Vr[d] = tget(c->v, vp + d * c->v->nb[0]);
+            const float *Vr = sl.V + ic * Dv;
             if (s > M) { M = s; ms = expf(Mold - M); } else { vs = expf(s - M); }
             if (f16acc) {
                 /* ggml_vec_scale_f16 / ggml_vec_mad_f16: every update rounds to fp16 */
@@ -354,7 +434,7 @@ static void fa_rows(void *p, int64_t lo, int64_t hi) {
             o[d] = (float) (a * S_inv);
         }
     }
-    free(Qc); free(Kr); free(Vr); free(acc); free(acc16);
+    free(Qc); free(acc); free(acc16); free(sl.K); free(sl.V); free(sdots);
 }
 
 int orc_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,

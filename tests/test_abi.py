@@ -222,3 +222,51 @@ def test_conv_validation(tsk):
     pk = kernel_desc(T, T.BF16, 2816, 1024, 3, 2, True)
     assert lib.tsk_conv1d_pack_weight(ctypes.byref(w), ctypes.byref(pk), None) == -7
     assert lib.tsk_conv1d_pack_weight(ctypes.byref(w), ctypes.byref(w), None) == -4
+
+
+def test_workspace_size(tsk):
+    """tsk_workspace_size: the scratch each node takes from its stream's
+    workspace, computed on the host from the descriptors (no GPU, no init)."""
+    T = tsk
+    lib = T.load()
+    P = ctypes.POINTER(T.TskTensor)
+
+    def ws(op, srcs, dst):
+        arr = (P * len(srcs))(*[ctypes.pointer(s) if s is not None else P() for s in srcs])
+        n = ctypes.c_size_t(12345)
+        rc = lib.tsk_workspace_size(op, arr, len(srcs), ctypes.byref(dst), ctypes.byref(n))
+        return rc, n.value
+
+    a = fake(T, T.BF16, (3072, 1024), 2)
+    assert ws(T.OP_MUL_MAT, [a, fake(T, T.F32, (388, 1024), 4)], fake(T, T.F32, (388, 3072), 4)) == (0, 388 * 1024 * 2)
+    assert ws(T.OP_MUL_MAT, [a, fake(T, T.BF16, (388, 1024), 2)], fake(T, T.F32, (388, 3072), 4)) == (0, 0)
+    assert ws(T.OP_MUL_MAT, [a, fake(T, T.F32, (388, 1000), 4)], fake(T, T.F32, (388, 3072), 4))[0] == -3
+    q = T.TskTensor()
+    q.type = T.Q8_0
+    q.ne[:] = [1024, 64, 1, 1]
+    q.nb[:] = [34, 34 * 32, 34 * 32 * 64, 34 * 32 * 64]
+    q.data = 0x100000
+    # repacked weights (aligned to 256) + activation planes (int8 rows, then f32 block scales)
+    wbytes = (1024 * 64 + 2 * 64 * 32 + 255) // 256 * 256
+    act = (5 * 1024 + 4 * 5 * 32 + 255) // 256 * 256
+    assert ws(T.OP_MUL_MAT, [q, fake(T, T.F32, (5, 1024), 4)], fake(T, T.F32, (5, 64), 4)) == (0, wbytes + act)
+    qf = fake(T, T.F32, (1, 16, 420, 64), 4)
+    kv = fake(T, T.F16, (1, 16, 420, 64), 2)
+    o = fake(T, T.F32, (1, 420, 16, 64), 4)
+    assert ws(T.OP_FLASH_ATTN_EXT, [qf, kv, kv], o) == (0, 2 * 16 * 64 * 448)        # V^T, fp16, 64-key padded
+    assert ws(T.OP_FLASH_ATTN_EXT, [qf, kv, kv, fake(T, T.F16, (1, 1, 420, 420), 2)], o) == (0, 0)   # masked: none
+    w = kernel_desc(T, T.BF16, 2816, 1024, 3, 2)                    # ggml layout: packed per call
+    x = fake(T, T.F32, (2, 646, 1024), 4)
+    y = fake(T, T.F32, (2, 646, 2816), 4)
+    assert ws(T.OP_CONV1D, [w, x], y) == (0, 3 * 1024 * 2816 * 2 + 2 * 646 * 1024 * 2)
+    assert ws(T.OP_CONV1D, [kernel_desc(T, T.BF16, 2816, 1024, 3, 2, True), x], y) == (0, 2 * 646 * 1024 * 2)
+    xt = fake(T, T.F32, (2, 200, 2048), 4)
+    qd = T.TskTensor()
+    qd.type = T.Q8_0
+    qd.ne[:] = [2048, 200, 2, 1]
+    qd.nb[:] = [34, 64 * 34, 64 * 34 * 200, 64 * 34 * 400]
+    qd.data = 0x100000
+    # int8 planes [400][2048] and f32 scales [400][64]
+    assert ws(T.OP_RMS_NORM_Q8_0, [xt, fake(T, T.F32, (2048,), 4)], qd) == (0, 400 * 2048 + 400 * 64 * 4)
+    assert ws(T.OP_RMS_NORM_MUL, [xt], xt) == (0, 0)
+    assert ws(99, [xt], xt)[0] == -6

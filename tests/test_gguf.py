@@ -95,11 +95,22 @@ def test_dit_load_gguf_matches_set_tensor(tsk, tmp_path, orc):
     assert c2.depth == 3 and c2.fused_depth == 1
     g.load_into(b)
     rng = np.random.default_rng(5)
-    lat = rng.standard_normal((2, 40, 64), dtype=np.float32)
+    lat = rng.standard_normal((2, 64, 40), dtype=np.float32)     # ne = [T, latent_dim, B]
     txt = rng.standard_normal((2, 77, 1024), dtype=np.float32)
     t = np.array([0.7, 0.7], np.float32)
     np.testing.assert_array_equal(a.forward(lat, t, txt), b.forward(lat, t, txt))
     g.close()
+    # a Q8_0 matrix is refused: this driver runs BF16 weights
+    qname = next(n for n, w in W.items() if w.ndim == 2 and w.shape[1] % 32 == 0)
+    qt = [gw.q8_0_tensor(qname, orc.quantize_q8_0(W[qname]), W[qname].shape[1]) if tt[0] == qname else tt
+          for tt in tensors]
+    path_q = tmp_path / "dit_q8.gguf"
+    gw.write_gguf(path_q, {"dit.depth": (gw.U32, 3), "dit.fused_depth": (gw.U32, 1)}, qt)
+    gq = tsk.Gguf(path_q)
+    with pytest.raises(tsk.TskError) as ei:
+        gq.load_into(b)
+    assert ei.value.status == -2
+    gq.close()
     a.close()
     b.close()
 

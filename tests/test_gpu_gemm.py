@@ -115,11 +115,16 @@ def test_q8_0_dequant_and_quant_bit_exact(env):
     assert np.array_equal(kat.numpy(), g["kat_deq"])
 
 
-@pytest.mark.parametrize("N,K,M", [(512, 5120, 2048), (300, 4096, 1024), (77, 2176, 256)])
-def test_q8_0_cooperative_matches_2x2_wave_kernel(env, N, K, M, monkeypatch):
-    """The cooperative Q8_0 tiles stage block scales in 2048-k segments for long
-    K; each output still sums its blocks in block order, so it equals the
-    2 x 2-wave kernel bit for bit."""
+@pytest.mark.parametrize("cfg", [2, 5])
+@pytest.mark.parametrize("N,K,M", [(512, 5120, 2048), (300, 4096, 1024), (77, 2176, 256), (130, 2176, 208),
+                                   (1446, 1024, 3072)])
+def test_q8_0_cooperative_matches_2x2_wave_kernel(env, N, K, M, cfg, monkeypatch):
+    """Both cooperative Q8_0 tiles (cfg 2: 64 x 64, the T5 qkv / wi shape;
+    cfg 5: 32 x 64, rows x tokens) stage block scales in 1024-k segments for
+    long K (2176 and 5120: three and five segments, the last one partial);
+    each output still sums its blocks in block order, so both equal the
+    2 x 2-wave kernel bit for bit. M = 208 (M % 32 == 16) leaves cfg 5 a
+    partial last row tile; N = 77 and 130 partial token tiles."""
     tsk, orc = env
     rng = np.random.default_rng(K + M)
     blocks = np.zeros((M, K // 32, 34), np.uint8)
@@ -129,7 +134,15 @@ def test_q8_0_cooperative_matches_2x2_wave_kernel(env, N, K, M, monkeypatch):
     blocks[..., 2:] = qs.view(np.uint8)
     x = tsk.to_device(rng.standard_normal((N, K)).astype(np.float32))
     sp = tsk.q8_0_repack(tsk.to_device(blocks))
-    y = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
-    monkeypatch.setenv("TSK_Q8_OLD", "1")
-    y_old = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
+    try:
+        monkeypatch.setenv("TSK_Q8_CFG", str(cfg))
+        tsk.init(0, reread=True)
+        y = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
+        monkeypatch.setenv("TSK_Q8_OLD", "1")
+        tsk.init(0, reread=True)
+        y_old = tsk.mul_mat(sp, x, a_type=tsk.Q8_0_SPLIT).numpy()
+    finally:
+        monkeypatch.delenv("TSK_Q8_OLD", raising=False)
+        monkeypatch.delenv("TSK_Q8_CFG", raising=False)
+        tsk.init(0, reread=True)
     assert np.array_equal(y, y_old)

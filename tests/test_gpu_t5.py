@@ -50,6 +50,54 @@ def test_t5_attention_config4(env):
     assert e <= 1e-5
 
 
+@pytest.mark.parametrize("n,n_max", [(100, 128), (512, 512), (520, 600)])
+def test_t5_attention_relative_bias_table(env, n, n_max):
+    """The encoder's attention mode (tsk_t5_attention): the bias read from a
+    per-head table over k - q plus the key padding, instead of a materialised
+    [H][n][n] mask, against the reference's explicit chain. n = 100 (not a
+    multiple of 64) and 512 run two key ranges per workgroup (at most one
+    workgroup per CU), 520 x 32 heads the one-range launch; padded keys at
+    the end and in the middle; the table longer than needed (n_max > n)."""
+    tsk, orc = env
+    rng = np.random.default_rng(n)
+    H, D = 32, 64
+    q, k, v = (rng.standard_normal((n, H, D)).astype(np.float32) * 0.35 for _ in range(3))
+    rel_bias = rng.standard_normal((32, H)).astype(np.float32)
+    ids = np.arange(1, n + 1, dtype=np.int32)
+    ids[-n // 8:] = 0
+    ids[n // 3: n // 3 + 5] = 0
+    bucket = np.array([orc.t5_bucket(r) for r in range(-(n_max - 1), n_max)], dtype=np.int64)
+    lut = np.ascontiguousarray(rel_bias[bucket].T)                   # (H, 2 n_max - 1)
+    dev = tsk.to_device
+    qb, kb, vb = (dev(np.ascontiguousarray(a.transpose(1, 0, 2))[None]) for a in (q, k, v))
+    valid = dev((ids != 0).astype(np.uint8))
+    o = tsk.t5_attention(qb, kb, vb, dev(lut), valid, scale=1.0).numpy()[0]
+    ref = orc.t5_attention(q, k, v, orc.t5_attention_mask(rel_bias, ids))
+    e = rel_l2(o, ref)
+    print(f"T5 attention, bias table: n={n} n_max={n_max} rel-L2 {e:.2e}", flush=True)
+    assert e <= 1e-5
+
+
+def test_rms_norm_q8_0_fused_bits(env):
+    """The encoder's fused norm + Q8_0 quantize gives the same bits as
+    tsk_rms_norm_mul followed by tsk_q8_0_quantize, at every row width it
+    runs (1024, 2048, 4096), with an all-zero block (d = 0, q = 0), a block
+    whose amax sits on a block boundary lane and a constant block."""
+    tsk, orc = env
+    rng = np.random.default_rng(17)
+    for n in (1024, 2048, 4096):
+        x = rng.standard_normal((37, n)).astype(np.float32)
+        x[3, 64:96] = 0.0                                  # one all-zero block
+        x[5, 31] = 40.0                                    # amax in the block's last lane
+        x[6, 128:160] = 0.75                               # constant block: every q = 127
+        w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        xd, wd = tsk.to_device(x), tsk.to_device(w)
+        fused = tsk.rms_norm_q8_0(xd, wd, 1e-6).numpy()
+        two = tsk.q8_0_quantize(tsk.rms_norm_mul(xd, wd, 1e-6)).numpy()
+        assert np.array_equal(fused, two), f"n={n}"
+        assert not fused[3, 2:3, 2:].any() and fused[3, 2, :2].view(np.float16)[0] == 0
+
+
 def q8_random(rng, K, M, scale):
     """ggml Q8_0 blocks of a [K, M] weight: int8 U[-127, 127], fp16 d = scale"""
     qs = rng.integers(-127, 128, size=(M, K // 32, 32), dtype=np.int8)

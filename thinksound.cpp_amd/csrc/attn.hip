@@ -18,6 +18,7 @@
 // F32 K/V: fp32 MFMA (16x16x4) throughout.
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -356,9 +357,12 @@ hipError_t launch_attn_t(const AttnParams &p, hipStream_t s) {
     const int rows_per_wg_big = 4 * 2 * 16;
     const int64_t wgs_big = (int64_t) ((p.Nq + rows_per_wg_big - 1) / rows_per_wg_big) * p.H * p.B;
     const int64_t wgs_small = (int64_t) ((p.Nq + 63) / 64) * p.H * p.B;
-    if (KVE == Elt::F32 && wgs_small <= 256) {
-        // F32 K/V on at most one workgroup per CU: two key ranges per
-        // workgroup (139 KiB of LDS), so two waves share each SIMD
+    // F32 K/V on at most one workgroup per CU: two key ranges per workgroup
+    // (139 KiB of static LDS), so two waves share each SIMD; only where the
+    // device gives a workgroup that much LDS
+    constexpr size_t ks2_lds = sizeof(float) * 2 * 2 * (KT * LDS32 + D * LDS32);
+    const DeviceInfo &dev = device_info();
+    if (KVE == Elt::F32 && wgs_small <= dev.cus && dev.lds_per_block >= ks2_lds) {
         dim3 grid((p.Nq + 63) / 64, p.H, p.B);
         launch_kernel((attn_kernel<QE, KVE, OE, 4, 1, 2>), grid, dim3(512), 0, s, p);
     } else if (KVE != Elt::F32 && wgs_big >= 256) {

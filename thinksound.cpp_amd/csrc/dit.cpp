@@ -105,7 +105,7 @@ struct tsk_dit {
     float *freq = nullptr;          // t-embedding frequencies [H/2] (host formula)
     float *rope_cs = nullptr;       // RoPE (cos, sin) [max_latent][head_dim] of the latent positions
     // block GEMM tile shape per projection (qkv, out, fc1, fc2): a launch_gemm_ks
-    // cfg, or 0 for the shape rule of gemm_cfg_for() (TSK_GEMM_CFG overrides)
+    // cfg, or 0 for the shape rule of gemm_cfg_for() (Tuning::gemm_cfg overrides)
     int gemm_cfg[4] = {0, 0, 0, 0};
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
@@ -223,8 +223,8 @@ int validate_cfg(const tsk_dit_config *c) {
         return fail(TSK_ERR_SHAPE, "depth %d / fused_depth %d", c->depth, c->fused_depth);
     if (c->mlp_kind != TSK_MLP_GELU_TANH) return fail(TSK_ERR_UNSUPPORTED, "mlp_kind %d", c->mlp_kind);
     if (c->weight_type != TSK_TYPE_BF16) return fail(TSK_ERR_UNSUPPORTED, "DiT weights must be BF16");
-    if (c->mlp_hidden % 64 || c->latent_dim % 8 || c->latent_dim < 8 || c->text_seq < 1)
-        return fail(TSK_ERR_SHAPE, "mlp_hidden %% 64, latent_dim %% 8");
+    if (c->mlp_hidden % 64 || c->latent_dim % 8 || c->latent_dim < 8 || c->latent_dim > c->hidden || c->text_seq < 1)
+        return fail(TSK_ERR_SHAPE, "mlp_hidden %% 64, latent_dim %% 8 and <= hidden");
     if (c->max_batch < 1 || c->max_batch > 32 || c->max_latent < 1) return fail(TSK_ERR_SHAPE, "capacity");
     if (!(c->ln_eps > 0) || !(c->qk_eps > 0) || !(c->rope_theta > 0) || !(c->t_max_period > 0))
         return fail(TSK_ERR_INVALID_ARG, "eps / theta / period");
@@ -267,15 +267,10 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     if ((rc = require_init())) return rc;
     tsk_dit *d = new tsk_dit();
     d->cfg = *cfg;
-    // attention launch shape override for tuning sweeps: 10 * key ranges + query blocks
-    if (const char *ac = getenv("TSK_ATTN_CFG")) d->attn_cfg = atoi(ac);
-    // block GEMM tile shapes for tuning sweeps: one digit per projection (qkv, out, fc1, fc2)
-    // (one hex digit each, 0 = the launcher's choice)
-    if (const char *gc = getenv("TSK_GEMM_CFG"))
-        for (int i = 0; i < 4 && gc[i]; ++i)
-            d->gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0'
-                           : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10
-                           : gc[i] >= 'A' && gc[i] <= 'Z' ? gc[i] - 'A' + 36 : 0;
+    // launch-shape overrides of tuning sweeps (attention shape, block GEMM
+    // tiles per projection), fixed at create
+    d->attn_cfg = tuning().attn_cfg;
+    for (int i = 0; i < 4; ++i) d->gemm_cfg[i] = tuning().gemm_cfg[i];
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -713,8 +708,11 @@ int run_conditioning(tsk_dit *d, int B, const float *t_host, int jmain, hipStrea
     return TSK_OK;
 }
 
-int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t_host, const float *text_d,
-                 float *flow_d, hipStream_t st) {
+// latent_d: [B][T][latent_dim] (token-major, the sampler's own state) or,
+// with latent_cm, [B][latent_dim][T] (ne0 = T, ts_dit::forward's input);
+// flow_d: [B][T][latent_dim] (ne0 = latent_dim, ts_dit::forward's output)
+int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, bool latent_cm, const float *t_host,
+                 const float *text_d, float *flow_d, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, St = c.text_seq, nj = c.depth - c.fused_depth;
     hipError_t e;
@@ -727,8 +725,10 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, const float *t
     // side stream, and these small launches would wait behind them
     {
         Timed tm(d, TSK_ROLE_OTHER, 2.0 * B * T * c.latent_dim * H, 2.0 * H * c.latent_dim + 4.0 * B * T * (c.latent_dim + H), st);
-        e = launch_proj_f32(wptr<uint16_t>(d, "audio_input_proj.weight"), wptr<float>(d, "audio_input_proj.bias"), latent_d,
-                            c.latent_dim, B * T, c.latent_dim, H, d->lat, H, st);
+        const uint16_t *w_in = wptr<uint16_t>(d, "audio_input_proj.weight");
+        const float *b_in = wptr<float>(d, "audio_input_proj.bias");
+        e = latent_cm ? launch_proj_f32_cm(w_in, b_in, latent_d, T, B * T, c.latent_dim, H, d->lat, H, d->xf, st)
+                      : launch_proj_f32(w_in, b_in, latent_d, c.latent_dim, B * T, c.latent_dim, H, d->lat, H, st);
         if (e != hipSuccess) return hip_fail(e, "input projection");
     }
     if ((e = hipMemcpyAsync(d->txt, text_d, sizeof(float) * B * St * H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
@@ -811,7 +811,7 @@ extern "C" int tsk_dit_forward_device(tsk_dit *d, int B, int T, const float *lat
                                       const float *text_d, float *flow_d, tsk_stream stream) {
     int rc = check_forward_args(d, B, T, latent_d, t_host, text_d, flow_d);
     if (rc) return rc;
-    return forward_impl(d, B, T, latent_d, t_host, text_d, flow_d, (hipStream_t) stream);
+    return forward_impl(d, B, T, latent_d, true, t_host, text_d, flow_d, (hipStream_t) stream);
 }
 
 extern "C" int tsk_dit_forward(tsk_dit *d, int B, int T, const float *latent, const float *t, const float *text,
@@ -827,7 +827,7 @@ extern "C" int tsk_dit_forward(tsk_dit *d, int B, int T, const float *latent, co
     txt_d = lat_d + nl;
     rc = hipcheck(hipMemcpyAsync(lat_d, latent, sizeof(float) * nl, hipMemcpyHostToDevice, st), "latent upload");
     if (!rc) rc = hipcheck(hipMemcpyAsync(txt_d, text, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text upload");
-    if (!rc) rc = forward_impl(d, B, T, lat_d, t, txt_d, d->flow, st);
+    if (!rc) rc = forward_impl(d, B, T, lat_d, true, t, txt_d, d->flow, st);
     if (!rc) rc = hipcheck(hipMemcpyAsync(flow, d->flow, sizeof(float) * nl, hipMemcpyDeviceToHost, st), "flow download");
     if (!rc) rc = hipcheck(hipStreamSynchronize(st), "stream sync");
     (void) hipStreamSynchronize(st);
@@ -930,14 +930,19 @@ extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float
         d->s_flow0 = d->s_x + 5 * cap;
         d->s_text2 = d->s_x + 6 * cap;
     }
-    if ((rc = hipcheck(hipMemcpyAsync(d->s_x, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
-    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
-    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2 + n, noise, sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    // noise / out / flow0 are [latent_dim][T] (ne0 = T) as in ts_dit::sample;
+    // the state on the device is token-major [T][latent_dim]
+    const int L = c.latent_dim;
+    std::vector<float> xt(n);
+    for (int t = 0; t < T; ++t)
+        for (int ch = 0; ch < L; ++ch) xt[(size_t) t * L + ch] = noise[(size_t) ch * T + t];
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x, xt.data(), sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2, xt.data(), sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(d->s_x2 + n, xt.data(), sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2, text_cond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2 + nt, text_uncond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
-    // TSK_DIT_SCHED=0 computes the conditioning inside every step instead
-    const char *sched_env = getenv("TSK_DIT_SCHED");
-    const bool use_sched = !(sched_env && sched_env[0] == '0');
+    // Tuning::dit_sched off computes the conditioning inside every step instead
+    const bool use_sched = tuning().dit_sched;
     if (use_sched && (rc = build_schedule(d, steps, st))) return rc;
     struct SchedGuard {
         tsk_dit *d;
@@ -949,15 +954,22 @@ extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float
         const float t_prev = 1.0f - (float) (s + 1) / (float) steps;
         const float tt[2] = {t_curr, t_curr};
         d->cur_sched = use_sched ? d->sched + (size_t) s * d->sched_row : nullptr;
-        if ((rc = forward_impl(d, 2, T, d->s_x2, tt, d->s_text2, d->s_flow2, st))) return rc;
+        if ((rc = forward_impl(d, 2, T, d->s_x2, false, tt, d->s_text2, d->s_flow2, st))) return rc;
         hipError_t e = launch_cfg_euler(d->s_flow2, (int64_t) n, cfg_scale, t_prev - t_curr, d->s_x, d->s_x2,
                                         s == 0 ? d->s_flow0 : nullptr, st);
         if (e != hipSuccess) return hip_fail(e, "cfg_euler");
     }
-    if ((rc = hipcheck(hipMemcpyAsync(out, d->s_x, sizeof(float) * n, hipMemcpyDeviceToHost, st), "out"))) return rc;
-    if (flow0 && (rc = hipcheck(hipMemcpyAsync(flow0, d->s_flow0, sizeof(float) * n, hipMemcpyDeviceToHost, st), "flow0")))
+    std::vector<float> xo(n), f0(flow0 ? n : 0);
+    if ((rc = hipcheck(hipMemcpyAsync(xo.data(), d->s_x, sizeof(float) * n, hipMemcpyDeviceToHost, st), "out"))) return rc;
+    if (flow0 && (rc = hipcheck(hipMemcpyAsync(f0.data(), d->s_flow0, sizeof(float) * n, hipMemcpyDeviceToHost, st), "flow0")))
         return rc;
-    return hipcheck(hipStreamSynchronize(st), "sync");
+    if ((rc = hipcheck(hipStreamSynchronize(st), "sync"))) return rc;
+    for (int t = 0; t < T; ++t)
+        for (int ch = 0; ch < L; ++ch) {
+            out[(size_t) ch * T + t] = xo[(size_t) t * L + ch];
+            if (flow0) flow0[(size_t) ch * T + t] = f0[(size_t) t * L + ch];
+        }
+    return TSK_OK;
 }
 
 // ------------------------------------------------------------------ timing

@@ -17,6 +17,7 @@
 // tiles are double buffered through LDS with one barrier per K step.
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 #include <cstdlib>
 #include <cstring>
@@ -667,26 +668,30 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // of 1024 k (three 64 x 64 workgroups per CU). Measured on MI355X at 1446
     // rows: 64 x 64 tiles with a 2-stage ring (1024 -> 3072: 51.5 -> 34.7 us
     // against the 2 x 2-wave kernel below, which stays for other shapes;
-    // TSK_Q8_OLD forces it for comparisons).
+    // Tuning::q8_old forces it for comparisons).
+    const Tuning &tu = tuning();
     const bool coop = p.K % 128 == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
                       ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
-                      !std::getenv("TSK_Q8_OLD");
+                      !tu.q8_old;
     if (coop) {
         // 64 x 64 tiles with a 2-stage ring; 32 x 64 (weight rows x tokens)
         // when the 64 x 64 grid would hold fewer than two tiles per CU
         // (measured: 1446 x 1024 outputs at K = 1024 / 4096 19.8 -> 18.1 / 54.4
-        // -> 48.3 us; the T5 o / wo projections). TSK_Q8_CFG picks a shape for
-        // sweeps: 1 = 64 x 64 / 3 stages, 2 = 64 x 64 / 2 stages, 3 = 128 x 64,
-        // 4 = 64 x 128, 5 = 32 x 64 (2 stages)
+        // -> 48.3 us; the T5 o / wo projections). Tuning::q8_cfg picks a
+        // shape: 2 = 64 x 64 / 2 stages, 5 = 32 x 64 (2 stages); sweep builds
+        // (TSK_SWEEP_VARIANTS) add 1 = 64 x 64 / 3 stages, 3 = 128 x 64,
+        // 4 = 64 x 128
         const int64_t tiles64 = (int64_t) ((p.M + 63) / 64) * ((p.N + 63) / 64);
-        int cfg = tiles64 < 512 ? 5 : 2;
-        if (const char *e = getenv("TSK_Q8_CFG")) cfg = atoi(e);
+        const int cfg = tu.q8_cfg ? tu.q8_cfg : tiles64 < 512 ? 5 : 2;
         switch (cfg) {
             case 2: return p.y_bf16 ? q8c_epi<4, 4, 2, true>(p, s) : q8c_epi<4, 4, 2, false>(p, s);
+            case 5: return p.y_bf16 ? q8c_epi<2, 4, 2, true>(p, s) : q8c_epi<2, 4, 2, false>(p, s);
+#if TSK_SWEEP_VARIANTS
+            case 1: return p.y_bf16 ? q8c_epi<4, 4, 3, true>(p, s) : q8c_epi<4, 4, 3, false>(p, s);
             case 3: return p.y_bf16 ? q8c_epi<8, 4, 2, true>(p, s) : q8c_epi<8, 4, 2, false>(p, s);
             case 4: return p.y_bf16 ? q8c_epi<4, 8, 2, true>(p, s) : q8c_epi<4, 8, 2, false>(p, s);
-            case 5: return p.y_bf16 ? q8c_epi<2, 4, 2, true>(p, s) : q8c_epi<2, 4, 2, false>(p, s);
-            default: return p.y_bf16 ? q8c_epi<4, 4, 3, true>(p, s) : q8c_epi<4, 4, 3, false>(p, s);
+#endif
+            default: return hipErrorInvalidValue;
         }
     }
     return p.y_bf16 ? gemm_q8_epi<2, 2, 2, 2, true>(p, s) : gemm_q8_epi<2, 2, 2, 2, false>(p, s);

@@ -41,6 +41,7 @@
 
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -850,19 +851,23 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
     // with K % 64 == 0 (and IC % 64 == 0 for convolutions) the 64-wide row
     // stages, 128 x 64 tiles (2 stages) from ~400 such tiles, 64 x 64 tiles
     // (3 stages) below; otherwise the 32-wide stages, 128 x 64 from ~512
-    // tiles. TSK_COOP_CFG forces a shape (12, 22, 28, 29, 30, 32) for sweeps.
+    // tiles. Tuning::coop_cfg forces a shape (12, 22, 28, 29, 30; 32 in sweep
+    // builds).
     bool k64 = true;
     for (int i = 0; i < g.nprob; ++i) k64 = k64 && g.p[i].K % 64 == 0 && (!conv || g.p[i].conv_ic % 64 == 0);
     int cfg = k64 ? (tiles >= 400 ? 29 : 30) : (tiles >= 512 ? 12 : 22);
-    if (const char *e = getenv("TSK_COOP_CFG")) cfg = atoi(e);
+    if (tuning().coop_cfg) cfg = tuning().coop_cfg;
     if (!k64 && cfg >= 28) cfg = tiles >= 512 ? 12 : 22;
     switch (cfg) {
         case 12: return conv ? conv_epi<8, 4, 4, true>(g, epi, s) : conv_epi<8, 4, 4, false>(g, epi, s);
+        case 22: return conv ? conv_epi<4, 4, 4, true>(g, epi, s) : conv_epi<4, 4, 4, false>(g, epi, s);
         case 28: return conv ? conv_epi<8, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 3, false, MODE_COOP64>(g, epi, s);
         case 29: return conv ? conv_epi<8, 4, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 2, false, MODE_COOP64>(g, epi, s);
         case 30: return conv ? conv_epi<4, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<4, 4, 3, false, MODE_COOP64>(g, epi, s);
+#if TSK_SWEEP_VARIANTS
         case 32: return conv ? conv_epi<8, 8, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 8, 2, false, MODE_COOP64>(g, epi, s);
-        default: return conv ? conv_epi<4, 4, 4, true>(g, epi, s) : conv_epi<4, 4, 4, false>(g, epi, s);
+#endif
+        default: return hipErrorInvalidValue;
     }
 }
 
@@ -885,8 +890,12 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         if (epi != EPI_PARTIAL && p.splits != 1) return hipErrorInvalidValue;
         if (epi == EPI_QKV && (p.M % 192 || p.seq < 1 || (p.rope && !p.rope_cs))) return hipErrorInvalidValue;
     }
-    // 128 x 64 tiles by default; 64 x 64 when that leaves most CUs idle
-    if (!cfg) cfg = gemm_ks_tiles(g, 128, 64) >= 160 ? 1 : 2;
+    // The DiT driver picks one of cfg 22 / 28 / 29 / 30 per projection (0:
+    // 64 x 64 tiles of 64-wide row stages). The other tile shapes and main
+    // loops (K-split rings, register prefetch, pipelined cooperative, 128 x
+    // 128) exist for sweeps only and are compiled with TSK_SWEEP_VARIANTS.
+    if (!cfg) cfg = 30;
+#if TSK_SWEEP_VARIANTS
     if (cfg >= 6 && cfg <= 10) {
         // register prefetch: every wave's stage count a multiple of the depth
         const int depth = cfg == 7 || cfg == 8 || cfg == 10 ? 2 : 4;
@@ -896,6 +905,7 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
             if (kts % (4 * depth) || (p.K / 32) % p.splits) return hipErrorInvalidValue;
         }
     }
+#endif
     for (int i = 0; i < g.nprob; ++i)
         if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
                                 cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33 ||
@@ -905,6 +915,11 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
             epi == EPI_QKV)
             return hipErrorInvalidValue;
     switch (cfg) {
+        case 22: return ks_epi<4, 4, 4, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 4 stages
+        case 28: return ks_epi<8, 4, 3, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 3 stages of 64 k rows
+        case 29: return ks_epi<8, 4, 2, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 2 stages of 64 k rows
+        case 30: return ks_epi<4, 4, 3, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 3 stages of 64 k rows
+#if TSK_SWEEP_VARIANTS
         case 1: return ks_epi<8, 4, 3>(g, epi, s);   // 128 x 64, 3 stages
         case 2: return ks_epi<4, 4, 3>(g, epi, s);   // 64 x 64, 3 stages
         case 3: return ks_epi<4, 8, 2>(g, epi, s);   // 64 x 128, 2 stages
@@ -926,20 +941,17 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         case 19: return ks_epi<8, 4, 6, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 6 stages
         case 20: return ks_epi<8, 4, 3, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 3 stages
         case 21: return ks_epi<8, 4, 2, MODE_COOP>(g, epi, s);    // 128 x 64 cooperative, 2 stages
-        case 22: return ks_epi<4, 4, 4, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 4 stages
         case 23: return ks_epi<4, 4, 3, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 3 stages
         case 24: return ks_epi<8, 4, 4, MODE_COOP_PIPE>(g, epi, s);   // 128 x 64 cooperative, pipelined, 4 stages
         case 25: return ks_epi<4, 4, 4, MODE_COOP_PIPE>(g, epi, s);   // 64 x 64 cooperative, pipelined, 4 stages
         case 26: return ks_epi<8, 4, 5, MODE_COOP_PIPE>(g, epi, s);   // 128 x 64 cooperative, pipelined, 5 stages
         case 27: return ks_epi<8, 8, 4, MODE_COOP_PIPE>(g, epi, s);   // 128 x 128 cooperative, pipelined, 4 stages
-        case 28: return ks_epi<8, 4, 3, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 3 stages of 64 k rows
-        case 29: return ks_epi<8, 4, 2, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 2 stages of 64 k rows
-        case 30: return ks_epi<4, 4, 3, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 3 stages of 64 k rows
         case 31: return ks_epi<4, 4, 2, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 2 stages of 64 k rows
         case 32: return ks_epi<8, 8, 2, MODE_COOP64>(g, epi, s);   // 128 x 128 cooperative, 2 stages of 64 k rows
         case 33: return ks_epi<4, 4, 4, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 4 stages of 64 k rows
         case 34: return ks_epi<4, 4, 5, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 5 stages of 64 k rows
         case 35: return ks_epi<4, 4, 6, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 6 stages of 64 k rows
+#endif
         default: return hipErrorInvalidValue;
     }
 }

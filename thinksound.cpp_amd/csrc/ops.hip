@@ -8,6 +8,7 @@
 
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -207,6 +208,20 @@ __global__ void q8_quantize_blocks_kernel(const float *x, int64_t ld_x, int64_t 
     BlockQ8 *o = (BlockQ8 *) (blocks + row * ld_blocks) + kb;
     o->d = f32_to_f16_bits(d);
     for (int j = 0; j < 32; ++j) o->qs[j] = (int8_t) __builtin_rintf(xr[j] * id);
+}
+
+// Q8_0 planes (int8 [rows][K], f32 scales [rows][K/32] holding fp16 values)
+// -> ggml blocks {fp16 d; int8 qs[32]}: one thread per block, bit-preserving
+__global__ void q8_planes_to_blocks_kernel(const int8_t *qx, const float *dx, int64_t rows, int64_t K,
+                                           char *blocks, int64_t ld_blocks) {
+    const int64_t KB = K / 32;
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= rows * KB) return;
+    const int64_t row = blk / KB, kb = blk % KB;
+    BlockQ8 *o = (BlockQ8 *) (blocks + row * ld_blocks) + kb;
+    o->d = f32_to_f16_bits(dx[blk]);
+    const int8_t *q = qx + row * K + kb * 32;
+    for (int j = 0; j < 32; ++j) o->qs[j] = q[j];
 }
 
 __global__ void q8_dequantize_kernel(const char *src, int split, int64_t rows, int64_t K, int64_t ld_src,
@@ -532,16 +547,29 @@ __global__ __launch_bounds__(256) void proj_f32_kt_kernel(const uint16_t *w, con
 // m0 + l's K weights in registers, a workgroup runs TT tokens whose rows are
 // staged in LDS (float4 broadcasts); k is summed as in proj_f32_kernel
 // (a[k % 4] in k order, then ((a0 + a1) + (a2 + a3)) + bias).
+// cm_T > 0: x is channel-major per batch item, [N / cm_T][K][cm_T] (the
+// ne0 = T latent of ts_dit::forward), token n = b * cm_T + t.
 template <int K, int TT>
 __global__ __launch_bounds__(256) void proj_f32_rows_kernel(const uint16_t *w, const float *bias, const float *x,
-                                                            int64_t ld_x, int N, int M, float *y, int64_t ld_y) {
+                                                            int64_t ld_x, int N, int M, float *y, int64_t ld_y,
+                                                            int cm_T) {
     __shared__ __attribute__((aligned(16))) float xs[TT][K];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * 64, n0 = blockIdx.y * TT;
-    for (int i = threadIdx.x; i < TT * (K / 4); i += 256) {
-        const int t = i / (K / 4), c = (i - t * (K / 4)) * 4;
-        const int n = min(n0 + t, N - 1);
-        *(f32x4 *) &xs[t][c] = *(const f32x4 *) (x + (int64_t) n * ld_x + c);
+    if (cm_T > 0) {
+        // consecutive threads read consecutive tokens of one channel
+        for (int i = threadIdx.x; i < TT * K; i += 256) {
+            const int t = i % TT, c = i / TT;
+            const int n = min(n0 + t, N - 1);
+            const int b = n / cm_T, tt = n - b * cm_T;
+            xs[t][c] = x[((int64_t) b * K + c) * cm_T + tt];
+        }
+    } else {
+        for (int i = threadIdx.x; i < TT * (K / 4); i += 256) {
+            const int t = i / (K / 4), c = (i - t * (K / 4)) * 4;
+            const int n = min(n0 + t, N - 1);
+            *(f32x4 *) &xs[t][c] = *(const f32x4 *) (x + (int64_t) n * ld_x + c);
+        }
     }
     const int m = m0 + lane;
     const uint16_t *wr = w + (int64_t) (m < M ? m : M - 1) * K;
@@ -751,6 +779,13 @@ hipError_t launch_q8_quantize_blocks(const float *x, int64_t ld_x, int64_t rows,
     return hipGetLastError();
 }
 
+hipError_t launch_q8_planes_to_blocks(const int8_t *qx, const float *dx, int64_t rows, int64_t K, void *blocks,
+                                     int64_t ld_blocks, hipStream_t s) {
+    launch_kernel(q8_planes_to_blocks_kernel, dim3(blocks_for(rows * (K / 32), 256)), dim3(256), 0, s, qx, dx, rows,
+                  K, (char *) blocks, ld_blocks);
+    return hipGetLastError();
+}
+
 hipError_t launch_q8_dequantize(const void *src, int split, int64_t rows, int64_t K, int64_t ld_src, float *y,
                                 int64_t ld_y, hipStream_t s) {
     launch_kernel(q8_dequantize_kernel, dim3(blocks_for(rows * K, 256)), dim3(256), 0, s, (const char *) src,
@@ -772,8 +807,7 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
-    static const bool block_rows = std::getenv("TSK_LN_BLOCK") != nullptr;   // A/B against the block kernel
-    if (g.H == 1024 && !block_rows) {
+    if (g.H == 1024 && !tuning().ln_block) {
         if (g.y_f32) launch_kernel(ln_wave_kernel<true, 4>, dim3(rows), dim3(64), 0, s, g);
         else launch_kernel(ln_wave_kernel<false, 4>, dim3(rows), dim3(64), 0, s, g);
         return hipGetLastError();
@@ -784,8 +818,8 @@ hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
 }
 
 hipError_t launch_gemv_jobs(const GemvJob *jobs_dev, int njobs, int max_m, int B, int K, hipStream_t s) {
-    // rows per wave at B <= 2 (TSK_GEMV_RW = 1, 2, 4 for sweeps; 2 measured best on the adaLN lists)
-    static const int rw_env = std::getenv("TSK_GEMV_RW") ? std::atoi(std::getenv("TSK_GEMV_RW")) : 2;
+    // rows per wave at B <= 2 (2 measured best on the adaLN lists; 1 and 4 for sweeps)
+    const int rw_env = tuning().gemv_rw;
     if (B <= 2 && rw_env == 4)
         launch_kernel(gemv_jobs_kernel<2, 4>, dim3(blocks_for(max_m, 16), njobs), dim3(256), 0, s, jobs_dev, B, K);
     else if (B <= 2 && rw_env == 2)
@@ -810,12 +844,36 @@ hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x,
     }
     if (K == 64) {     // the latent input: weights in registers, 16 tokens per workgroup
         launch_kernel(proj_f32_rows_kernel<64, 16>, dim3((unsigned) ((M + 63) / 64), (unsigned) ((N + 15) / 16)),
-                      dim3(256), 0, s, w, bias, x, ld_x, N, M, y, ld_y);
+                      dim3(256), 0, s, w, bias, x, ld_x, N, M, y, ld_y, 0);
         return hipGetLastError();
     }
     const int64_t waves = (int64_t) N * ((M + 63) / 64);
     launch_kernel(proj_f32_kernel, dim3(blocks_for(waves, 4)), dim3(256), 0, s, w, bias, x, ld_x, N, K, M, y, ld_y);
     return hipGetLastError();
+}
+
+// [B][C][T] -> [B][T][C] (f32)
+__global__ void transpose_ct_kernel(const float *x, int B, int C, int T, float *y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t) B * C * T) return;
+    const int t = (int) (i % T), c = (int) ((i / T) % C), b = (int) (i / ((int64_t) T * C));
+    y[((int64_t) b * T + t) * C + c] = x[i];
+}
+
+hipError_t launch_proj_f32_cm(const uint16_t *w, const float *bias, const float *x, int T, int N, int K, int M,
+                              float *y, int64_t ld_y, float *tmp, hipStream_t s) {
+    if (N < 1 || M < 1 || K < 8 || K % 8 || T < 1 || N % T) return hipErrorInvalidValue;
+    if (K == 64) {
+        launch_kernel(proj_f32_rows_kernel<64, 16>, dim3((unsigned) ((M + 63) / 64), (unsigned) ((N + 15) / 16)),
+                      dim3(256), 0, s, w, bias, x, (int64_t) K, N, M, y, ld_y, T);
+        return hipGetLastError();
+    }
+    // other widths: token-major copy in tmp ([N][K] f32), then the row kernels
+    const int64_t n = (int64_t) N * K;
+    launch_kernel(transpose_ct_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, s, x, N / T, K, T, tmp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_proj_f32(w, bias, tmp, K, N, K, M, y, ld_y, s);
 }
 
 hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, int IW, int IC, int KW, int OW, int N,

@@ -7,7 +7,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "../../include/tsk/tsk.h"
 #include "tsk_internal.h"
@@ -34,31 +37,66 @@ int hip_fail(hipError_t e, const char *what) {
     return fail(TSK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// ---- per-process device state: one workspace per device, grown on demand
+// ---- per-process state: tuning, device limits and per-stream workspaces
 namespace {
 std::mutex g_mu;
 int g_device = -1;
-struct Workspace { void *ptr = nullptr; size_t size = 0; };
-Workspace g_ws[64][2];
+Tuning g_tuning;
+DeviceInfo g_dev;
+// one workspace per (device, stream): library-owned (grown on demand) or
+// bound by the caller (external, never reallocated)
+struct Workspace {
+    void *ptr = nullptr;
+    size_t size = 0;
+    bool external = false;
+};
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return e && *e ? atoi(e) : dflt;
+}
+
+void read_tuning() {
+    Tuning t;
+    t.q8_cfg = env_int("TSK_Q8_CFG", 0);
+    t.q8_old = env_int("TSK_Q8_OLD", 0) != 0;
+    t.coop_cfg = env_int("TSK_COOP_CFG", 0);
+    t.attn_cfg = env_int("TSK_ATTN_CFG", 0);
+    t.dit_sched = env_int("TSK_DIT_SCHED", 1) != 0;
+    t.ln_block = env_int("TSK_LN_BLOCK", 0) != 0;
+    t.gemv_rw = env_int("TSK_GEMV_RW", 2);
+    // one character per projection (qkv, out, fc1, fc2): 0-9, a-z = 10-35
+    if (const char *gc = getenv("TSK_GEMM_CFG"))
+        for (int i = 0; i < 4 && gc[i]; ++i)
+            t.gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10 : 0;
+    g_tuning = t;
+}
 }  // namespace
+
+const Tuning &tuning() { return g_tuning; }
+const DeviceInfo &device_info() { return g_dev; }
 
 int require_init() {
     if (g_device < 0) return fail(TSK_ERR_NOT_INIT, "tsk_init() has not been called");
     return TSK_OK;
 }
 
-int workspace(size_t bytes, void **out, int slot) {
-    std::lock_guard<std::mutex> lk(g_mu);
+int workspace(hipStream_t s, size_t bytes, void **out) {
+    *out = nullptr;
+    if (!bytes) return TSK_OK;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    if (dev < 0 || dev >= 64) return fail(TSK_ERR_INVALID_ARG, "device id %d out of range", dev);
-    if (slot < 0 || slot > 1) return fail(TSK_ERR_INVALID_ARG, "workspace slot %d", slot);
-    Workspace &w = g_ws[dev][slot];
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace &w = g_ws[std::make_pair(dev, s)];
     if (w.size < bytes) {
-        // the old buffer may still be read by queued kernels of any stream
-        e = hipDeviceSynchronize();
-        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+        if (w.external)
+            return fail(TSK_ERR_NOMEM, "the workspace bound to this stream holds %zu bytes, the call needs %zu", w.size,
+                        bytes);
+        // only work queued on s reads this stream's buffer
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
         if (w.ptr) (void) hipFree(w.ptr);
         w.ptr = nullptr;
         w.size = 0;
@@ -135,7 +173,14 @@ extern "C" int tsk_init(int device) {
     if (device < 0 || device >= n) return fail(TSK_ERR_INVALID_ARG, "device %d of %d", device, n);
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    DeviceInfo di;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0) di.cus = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+        di.lds_per_block = (size_t) v;
     std::lock_guard<std::mutex> lk(g_mu);
+    read_tuning();
+    g_dev = di;
     g_device = device;
     return TSK_OK;
 }
@@ -144,13 +189,52 @@ extern "C" int tsk_shutdown(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_device < 0) return TSK_OK;
     (void) hipDeviceSynchronize();
-    for (auto &dev : g_ws)
-        for (auto &w : dev) {
-            if (w.ptr) (void) hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.size = 0;
-        }
+    for (auto &kv : g_ws)
+        if (kv.second.ptr && !kv.second.external) (void) hipFree(kv.second.ptr);
+    g_ws.clear();
     g_device = -1;
+    return TSK_OK;
+}
+
+extern "C" int tsk_set_workspace(tsk_stream stream, void *ptr, size_t bytes) {
+    int rc = require_init();
+    if (rc) return rc;
+    if (!ptr != !bytes) return fail(TSK_ERR_INVALID_ARG, "ptr and bytes must both be set or both be zero");
+    if (ptr && ((uintptr_t) ptr & 255)) return fail(TSK_ERR_ALIGN, "workspace must be 256-byte aligned");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    hipStream_t s = (hipStream_t) stream;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace &w = g_ws[std::make_pair(dev, s)];
+    if (w.ptr && !w.external) {
+        // the library-owned buffer may still be read by work queued on s
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void) hipFree(w.ptr);
+    }
+    w.ptr = ptr;
+    w.size = bytes;
+    w.external = ptr != nullptr;
+    return TSK_OK;
+}
+
+extern "C" int tsk_release_workspace(tsk_stream stream) {
+    int rc = require_init();
+    if (rc) return rc;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    hipStream_t s = (hipStream_t) stream;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ws.find(std::make_pair(dev, s));
+    if (it == g_ws.end()) return TSK_OK;
+    if (it->second.ptr && !it->second.external) {
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void) hipFree(it->second.ptr);
+    }
+    g_ws.erase(it);
     return TSK_OK;
 }
 
@@ -224,29 +308,75 @@ int validate_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor 
 
 }  // namespace
 
-extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, tsk_tensor *dst,
-                           tsk_stream stream) {
-    int rc = validate_mul_mat(a, b, bias, dst);
-    if (rc) return rc;
-    if ((rc = require_init())) return rc;
-    hipStream_t s = (hipStream_t) stream;
+namespace {
+
+// Scratch of one call: the workspace of its stream (tsk_set_workspace or the
+// library's own), or a fixed region with a hard limit.
+struct Scratch {
+    hipStream_t s;
+    void *fixed;
+    size_t cap;
+    int get(size_t bytes, void **out) const {
+        if (!fixed) return workspace(s, bytes, out);
+        if (bytes > cap)
+            return fail(TSK_ERR_NOMEM, "the call needs %zu bytes of scratch, the limit is %zu", bytes, cap);
+        *out = bytes ? fixed : nullptr;
+        return TSK_OK;
+    }
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t) 255; }
+
+// How tsk_mul_mat runs a validated node, and the scratch it needs.
+struct MulMatPlan {
+    bool uni;            // rows of b and dst uniformly strided: one GEMM of Nslice rows
+    int64_t nslices, Nslice;
+    bool coop;           // BF16 weights on the cooperative tiles
+    size_t cast_bytes;   // coop with f32 b: b rounded to bf16 rows
+    size_t wbytes;       // Q8_0: the weights repacked into planes
+    size_t act_bytes;    // Q8_0 / Q8_0_SPLIT: the quantized activation planes
+    size_t bytes;        // total scratch
+};
+
+MulMatPlan plan_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *dst) {
+    MulMatPlan pl;
+    memset(&pl, 0, sizeof(pl));
+    const int64_t K = a->ne[0], M = a->ne[1];
+    // slices of uniformly strided rows: one launch per (i2, i3) unless rows are uniform
+    pl.uni = rows_uniform(b) && rows_uniform(dst);
+    pl.nslices = pl.uni ? 1 : b->ne[2] * b->ne[3];
+    pl.Nslice = pl.uni ? b->ne[1] * b->ne[2] * b->ne[3] : b->ne[1];
+    pl.coop = a->type == TSK_TYPE_BF16 && pl.uni && M % 16 == 0 && K % 32 == 0 && a->nb[1] % 16 == 0;
+    if (pl.coop && b->type == TSK_TYPE_F32) pl.cast_bytes = align256((size_t) (pl.Nslice * K) * 2);
+    if (a->type == TSK_TYPE_Q8_0 || a->type == TSK_TYPE_Q8_0_SPLIT) {
+        pl.wbytes = a->type == TSK_TYPE_Q8_0 ? align256(tsk_q8_0_split_nbytes(K, M)) : 0;
+        pl.act_bytes = (((size_t) (pl.Nslice * K) + 15) & ~(size_t) 15) + sizeof(float) * (size_t) (pl.Nslice * (K / 32));
+        pl.act_bytes = align256(pl.act_bytes);
+    }
+    pl.bytes = pl.cast_bytes + pl.wbytes + pl.act_bytes;
+    return pl;
+}
+
+int mul_mat_impl(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, tsk_tensor *dst,
+                 const Scratch &scr) {
+    hipStream_t s = scr.s;
     const int64_t K = a->ne[0], M = a->ne[1];
     const int es_b = elt_size(b->type), es_d = elt_size(dst->type);
-
-    // slices of uniformly strided rows: one launch per (i2, i3) unless rows are uniform
-    const bool uni = rows_uniform(b) && rows_uniform(dst);
-    const int64_t nslices = uni ? 1 : b->ne[2] * b->ne[3];
-    const int64_t Nslice = uni ? b->ne[1] * b->ne[2] * b->ne[3] : b->ne[1];
+    const MulMatPlan pl = plan_mul_mat(a, b, dst);
+    int rc;
+    char *ws = nullptr;
+    if ((rc = scr.get(pl.bytes, (void **) &ws))) return rc;
+    const int64_t nslices = pl.nslices, Nslice = pl.Nslice;
 
     // BF16 weights with M % 16 == 0, K % 32 == 0 and uniformly strided rows:
     // the cooperative tiles of gemm_ks.hip on bf16 activation rows (f32 b is
-    // rounded to bf16 into the workspace first: ggml's conversion of src1)
-    if (a->type == TSK_TYPE_BF16 && uni && M % 16 == 0 && K % 32 == 0 && a->nb[1] % 16 == 0) {
+    // rounded to bf16 into the scratch first: ggml's conversion of src1)
+    if (pl.coop) {
         uint16_t *xb = nullptr;
         const int64_t N = Nslice;
         const int64_t ld_b = (int64_t) (b->nb[1] / es_b);
         if (b->type == TSK_TYPE_F32) {
-            if ((rc = workspace((size_t) (N * K) * 2, (void **) &xb))) return rc;
+            xb = (uint16_t *) ws;
             hipError_t e = launch_cast_rows_bf16((const float *) b->data, ld_b, 0, (int) std::min<int64_t>(N, 1 << 30), N,
                                                  (int) K, xb, s);
             if (e != hipSuccess) return hip_fail(e, "mul_mat input cast");
@@ -267,16 +397,10 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
         return e == hipSuccess ? TSK_OK : hip_fail(e, "mul_mat launch");
     }
 
-    // Q8_0 weights: repack raw ggml blocks into planes in the workspace
+    // Q8_0 weights: repack raw ggml blocks into planes in the scratch
     const int8_t *qw = nullptr;
     const uint16_t *dw = nullptr;
-    char *ws = nullptr;
-    size_t wbytes = 0;
     if (a->type == TSK_TYPE_Q8_0 || a->type == TSK_TYPE_Q8_0_SPLIT) {
-        const size_t act = (size_t) (Nslice * K) + sizeof(float) * (size_t) (Nslice * (K / 32));
-        wbytes = a->type == TSK_TYPE_Q8_0 ? tsk_q8_0_split_nbytes(K, M) : 0;
-        const size_t total = ((wbytes + 255) & ~(size_t) 255) + act + 256;
-        if ((rc = workspace(total, (void **) &ws))) return rc;
         if (a->type == TSK_TYPE_Q8_0) {
             hipError_t e = launch_q8_repack(a->data, (int64_t) a->nb[1], M, K, ws, s);
             if (e != hipSuccess) return hip_fail(e, "q8 repack");
@@ -316,7 +440,7 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
             q.M = p.M; q.N = p.N; q.K = p.K; q.splits = 1;
             e = launch_gemm_f32(q, p.y_bf16, s);
         } else {
-            char *act = ws + ((wbytes + 255) & ~(size_t) 255);
+            char *act = ws + pl.wbytes;
             int8_t *qx = (int8_t *) act;
             float *dx = (float *) (act + (((size_t) (Nslice * K) + 15) & ~(size_t) 15));
             e = launch_quantize_rows_q8(p.x, p.x_f32, p.ld_x, p.N, p.K, qx, dx, s);
@@ -330,6 +454,16 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
         if (e != hipSuccess) return hip_fail(e, "mul_mat launch");
     }
     return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, tsk_tensor *dst,
+                           tsk_stream stream) {
+    int rc = validate_mul_mat(a, b, bias, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    return mul_mat_impl(a, b, bias, dst, Scratch{(hipStream_t) stream, nullptr, 0});
 }
 
 // ------------------------------------------------------------------ flash_attn_ext
@@ -391,6 +525,14 @@ bool fa_fast_eligible(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor
     return true;
 }
 
+// scratch of the fast path: V transposed to fp16 [B * H][64][ldv]
+size_t fa_ws_bytes(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v, const tsk_tensor *mask,
+                   float max_bias, float softcap, const tsk_tensor *dst) {
+    if (!fa_fast_eligible(q, k, v, mask, max_bias, softcap, dst)) return 0;
+    const int64_t ldv = (k->ne[1] + 63) / 64 * 64;
+    return align256((size_t) 2 * q->ne[3] * q->ne[2] * 64 * ldv);
+}
+
 }  // namespace
 
 extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
@@ -404,8 +546,8 @@ extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, cons
         const int Nkv = (int) k->ne[1], H = (int) q->ne[2], B = (int) q->ne[3];
         const int ldv = (Nkv + 63) / 64 * 64;
         void *ws = nullptr;
-        if ((rc = workspace((size_t) 2 * B * H * 64 * ldv, &ws))) return rc;
         hipStream_t st = (hipStream_t) stream;
+        if ((rc = workspace(st, fa_ws_bytes(q, k, v, mask, max_bias, logit_softcap, dst), &ws))) return rc;
         hipError_t e = launch_vt_transpose(v->data, v->type == TSK_TYPE_BF16, (int64_t) v->nb[1], (int64_t) v->nb[2],
                                            (int64_t) v->nb[3], Nkv, H, B, (uint16_t *) ws, ldv, st);
         if (e != hipSuccess) return hip_fail(e, "flash_attn_ext V transpose");
@@ -451,6 +593,99 @@ extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, cons
     hipError_t e = launch_attention(p, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "flash_attn_ext launch");
     return TSK_OK;
+}
+
+// ------------------------------------------------------------------ RMS norm -> Q8_0
+namespace {
+
+int check_w(const tsk_tensor *w, int64_t n);
+
+int validate_rms_norm_q8(const tsk_tensor *x, const tsk_tensor *w, const tsk_tensor *dst) {
+    int rc;
+    if ((rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst"))) return rc;
+    if ((rc = check_w(w, x->ne[0]))) return rc;
+    if (x->type != TSK_TYPE_F32 || dst->type != TSK_TYPE_Q8_0) return fail(TSK_ERR_TYPE, "x F32 -> dst Q8_0");
+    if (!same_shape(x, dst)) return fail(TSK_ERR_SHAPE, "x and dst shapes differ");
+    const int64_t n = x->ne[0];
+    if (n != 1024 && n != 2048 && n != 4096)
+        return fail(TSK_ERR_UNSUPPORTED, "rows of %lld (1024, 2048 or 4096 elements)", (long long) n);
+    if ((rc = check_rows(x, "x", 16))) return rc;
+    if (!aligned(w->data, 16)) return fail(TSK_ERR_ALIGN, "w must be 16-byte aligned");
+    if (dst->nb[0] != 34 || dst->nb[1] < (size_t) (n / 32) * 34) return fail(TSK_ERR_STRIDE, "dst Q8_0 rows");
+    if (!rows_uniform(x) || !rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "rows must be uniformly strided");
+    return TSK_OK;
+}
+
+size_t rms_norm_q8_ws_bytes(const tsk_tensor *x) {
+    const size_t rows = (size_t) (x->ne[1] * x->ne[2] * x->ne[3]), n = (size_t) x->ne[0];
+    return align256(rows * n) + align256(rows * (n / 32) * sizeof(float));
+}
+
+}  // namespace
+
+extern "C" int tsk_rms_norm_q8_0(const tsk_tensor *x, const tsk_tensor *w, float eps, tsk_tensor *dst,
+                                 tsk_stream stream) {
+    int rc = validate_rms_norm_q8(x, w, dst);
+    if (rc) return rc;
+    if (!(eps >= 0.0f)) return fail(TSK_ERR_INVALID_ARG, "eps");
+    if ((rc = require_init())) return rc;
+    hipStream_t s = (hipStream_t) stream;
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3], n = x->ne[0];
+    char *ws = nullptr;
+    if ((rc = workspace(s, rms_norm_q8_ws_bytes(x), (void **) &ws))) return rc;
+    int8_t *qx = (int8_t *) ws;
+    float *dx = (float *) (ws + align256((size_t) (rows * n)));
+    hipError_t e = launch_rms_norm_q8((const float *) x->data, (int64_t) (x->nb[1] / 4), (const float *) w->data, eps,
+                                      qx, dx, rows, (int) n, s);
+    if (e == hipSuccess) e = launch_q8_planes_to_blocks(qx, dx, rows, n, dst->data, (int64_t) dst->nb[1], s);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "rms_norm_q8 launch");
+}
+
+// ------------------------------------------------------------------ T5 attention
+extern "C" int tsk_t5_attention(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
+                                const tsk_tensor *rel_lut, const uint8_t *key_valid, float scale, tsk_tensor *dst,
+                                tsk_stream stream) {
+    int rc;
+    if ((rc = check_tensor(q, "q")) || (rc = check_tensor(k, "k")) || (rc = check_tensor(v, "v")) ||
+        (rc = check_tensor(rel_lut, "rel_lut")) || (rc = check_tensor(dst, "dst")))
+        return rc;
+    if (!key_valid) return fail(TSK_ERR_INVALID_ARG, "key_valid is NULL");
+    for (const tsk_tensor *t : {q, k, v, rel_lut, (const tsk_tensor *) dst})
+        if (t->type != TSK_TYPE_F32) return fail(TSK_ERR_TYPE, "q, k, v, rel_lut and dst must be F32");
+    const int64_t n = q->ne[1], H = q->ne[2];
+    if (q->ne[0] != 64 || !same_shape(q, k) || !same_shape(q, v) || q->ne[3] != 1)
+        return fail(TSK_ERR_SHAPE, "q, k, v must be [64, n, H, 1]");
+    if (dst->ne[0] != 64 || dst->ne[1] != H || dst->ne[2] != n || dst->ne[3] != 1)
+        return fail(TSK_ERR_SHAPE, "dst must be [64, H, n, 1]");
+    const int64_t nl = rel_lut->ne[0];
+    if (nl % 2 == 0 || (nl + 1) / 2 < n || rel_lut->ne[1] != H || rel_lut->ne[2] * rel_lut->ne[3] != 1)
+        return fail(TSK_ERR_SHAPE, "rel_lut must be [2 n_max - 1, H] with n_max >= n = %lld", (long long) n);
+    if (rel_lut->nb[0] != 4 || rel_lut->nb[1] % 4 || !aligned(rel_lut->data, 4))
+        return fail(TSK_ERR_STRIDE, "rel_lut rows must be contiguous");
+    if ((rc = check_rows(q, "q", 16)) || (rc = check_rows(k, "k", 16)) || (rc = check_rows(v, "v", 16)) ||
+        (rc = check_rows(dst, "dst", 16)))
+        return rc;
+    if (!(scale > 0.0f)) return fail(TSK_ERR_INVALID_ARG, "scale must be > 0");
+    if ((rc = require_init())) return rc;
+    AttnParams p;
+    memset(&p, 0, sizeof(p));
+    p.q = q->data; p.k = k->data; p.v = v->data; p.o = dst->data;
+    p.q_type = p.kv_type = TSK_TYPE_F32;
+    p.Nq = p.Nkv = (int) n; p.H = p.Hkv = (int) H; p.B = 1;
+    p.q_nb1 = q->nb[1]; p.q_nb2 = q->nb[2]; p.q_nb3 = q->nb[3];
+    p.k_nb1 = k->nb[1]; p.k_nb2 = k->nb[2]; p.k_nb3 = k->nb[3];
+    p.v_nb1 = v->nb[1]; p.v_nb2 = v->nb[2]; p.v_nb3 = v->nb[3];
+    p.m_ne2 = p.m_ne3 = 1;
+    p.o_nb1 = dst->nb[1]; p.o_nb2 = dst->nb[2]; p.o_nb3 = dst->nb[3];
+    p.scale = scale;
+    p.n_head_log2 = 1u << (uint32_t) floorf(log2f((float) H));
+    p.m0 = p.m1 = 1.0f;
+    p.rel_lut = (const float *) rel_lut->data;
+    p.rel_nh = (int64_t) (rel_lut->nb[1] / 4);
+    p.rel_off = (int) ((nl - 1) / 2);
+    p.key_valid = key_valid;
+    hipError_t e = launch_attention(p, (hipStream_t) stream);
+    return e == hipSuccess ? TSK_OK : hip_fail(e, "t5 attention launch");
 }
 
 // ------------------------------------------------------------------ norms / rope
@@ -659,8 +894,6 @@ int validate_conv(const tsk_tensor *w, const tsk_tensor *bias, const tsk_tensor 
     return TSK_OK;
 }
 
-size_t align256(size_t n) { return (n + 255) & ~(size_t) 255; }
-
 // bytes a kw-major copy of w needs in scratch (0 if w is used in place)
 size_t conv_pack_bytes(const tsk_tensor *w) {
     return kw_major(w) ? 0 : align256((size_t) (w->ne[0] * w->ne[1] * w->ne[2]) * (size_t) elt_size(w->type));
@@ -735,6 +968,11 @@ int conv_gemm(int wtype, const void *wrows, const void *w3rows, int64_t ld_w, co
     return e == hipSuccess ? TSK_OK : hip_fail(e, "conv GEMM launch");
 }
 
+// scratch of tsk_conv1d: the kw-major kernel copy and the bf16 input rows
+size_t conv1d_ws_bytes(const tsk_tensor *w, const tsk_tensor *x) {
+    return conv_pack_bytes(w) + conv_cast_bytes(w->type, x->type == TSK_TYPE_F32, w->ne[1], x->ne[1], x->ne[2], w->ne[2]);
+}
+
 int validate_im2col(const tsk_tensor *kernel, const tsk_tensor *x, int s0, int p0, int d0, const tsk_tensor *dst) {
     int rc;
     if (!kernel) return fail(TSK_ERR_INVALID_ARG, "kernel is NULL");
@@ -805,8 +1043,7 @@ extern "C" int tsk_conv1d(const tsk_tensor *w, const tsk_tensor *bias, const tsk
     char *ws = nullptr;
     const int x_f32 = x->type == TSK_TYPE_F32;
     const size_t cast = conv_cast_bytes(w->type, x_f32, w->ne[1], x->ne[1], x->ne[2], w->ne[2]);
-    const size_t need = conv_pack_bytes(w) + cast;
-    if (need && (rc = workspace(need, (void **) &ws, 1))) return rc;
+    if ((rc = workspace(s, conv1d_ws_bytes(w, x), (void **) &ws))) return rc;
     uint16_t *xcast = cast ? (uint16_t *) ws : nullptr;
     char *pk = ws + cast;
     const void *wr = nullptr;
@@ -835,6 +1072,20 @@ extern "C" int tsk_swiglu(const tsk_tensor *a, const tsk_tensor *b, tsk_tensor *
 
 namespace {
 
+// scratch of convmlp / mlp: the hidden state [B * OW1][HID] (bf16 for BF16
+// kernels: the conversion w2's mul_mat applies), f32 h3 for F32 kernels, the
+// bf16 input rows and the kw-major kernel copies
+size_t swiglu_mlp_ws_bytes(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, int KW1, int IC, int HID,
+                           int pad, int x_f32, int IW, int B) {
+    const int OW1 = (int) conv_out_len(IW, KW1, 1, pad, 1);
+    if (OW1 < 1) return 0;
+    const bool bf16 = w1->type == TSK_TYPE_BF16;
+    const size_t nh = (size_t) B * OW1 * HID;
+    const size_t hbytes = align256(nh * (bf16 ? 2 : 4)), h3bytes = bf16 ? 0 : align256(nh * 4);
+    return hbytes + h3bytes + conv_cast_bytes(w1->type, x_f32, IC, IW, B, HID) + conv_pack_bytes(w1) +
+           conv_pack_bytes(w3) + conv_pack_bytes(w2);
+}
+
 // convmlp / mlp on validated operands: geometry of the two convolutions
 // (KW = 1, p = 0 for mlp), x rows [B][IW][IC], dst rows [B * OW2][OC]
 int swiglu_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, int KW1, int IC, int HID, int KW2,
@@ -844,15 +1095,12 @@ int swiglu_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
     const int OW2 = (int) conv_out_len(OW1, KW2, 1, pad, 1);
     if (OW1 < 1 || OW2 < 1) return fail(TSK_ERR_SHAPE, "output length < 1");
     const bool bf16 = w1->type == TSK_TYPE_BF16;
-    // scratch: hidden [B * OW1][HID] (bf16 for BF16 kernels: the conversion
-    // w2's mul_mat applies), f32 h3 for F32 kernels, then packed kernels
     const size_t nh = (size_t) B * OW1 * HID;
     const size_t hbytes = align256(nh * (bf16 ? 2 : 4)), h3bytes = bf16 ? 0 : align256(nh * 4);
     const size_t cast = conv_cast_bytes(w1->type, x_f32, IC, IW, B, HID);
-    const size_t total = hbytes + h3bytes + cast + conv_pack_bytes(w1) + conv_pack_bytes(w3) + conv_pack_bytes(w2);
     char *ws = nullptr;
     int rc;
-    if ((rc = workspace(total, (void **) &ws, 1))) return rc;
+    if ((rc = workspace(s, swiglu_mlp_ws_bytes(w1, w3, w2, KW1, IC, HID, pad, x_f32, IW, B), (void **) &ws))) return rc;
     void *h = ws;
     float *h3 = bf16 ? nullptr : (float *) (ws + hbytes);
     uint16_t *xcast = cast ? (uint16_t *) (ws + hbytes + h3bytes) : nullptr;
@@ -888,8 +1136,10 @@ int check_mlp_types(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor
 
 }  // namespace
 
-extern "C" int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
-                                   const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream) {
+namespace {
+
+int validate_conv_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x,
+                      const tsk_tensor *dst) {
     int rc;
     if ((rc = check_conv_weight(w1, "w1")) || (rc = check_conv_weight(w3, "w3")) || (rc = check_conv_weight(w2, "w2")) ||
         (rc = check_conv_act(x, "x")) || (rc = check_conv_act(dst, "dst")))
@@ -908,6 +1158,16 @@ extern "C" int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, c
     if (!rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "dst rows must be uniformly strided");
     if (KW1 * IC > (1 << 30) || KW2 * HID > (1 << 30) || OW1 * x->ne[2] * HID > ((int64_t) 1 << 40))
         return fail(TSK_ERR_SHAPE, "convmlp too large");
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2,
+                                   const tsk_tensor *x, tsk_tensor *dst, tsk_stream stream) {
+    int rc = validate_conv_mlp(w1, w3, w2, x, dst);
+    if (rc) return rc;
+    const int64_t KW1 = w1->ne[0], IC = w1->ne[1], HID = w1->ne[2], KW2 = w2->ne[0], OC = w2->ne[2];
     if ((rc = require_init())) return rc;
     const int esx = elt_size(x->type), esy = elt_size(dst->type);
     return swiglu_mlp(w1, w3, w2, (int) KW1, (int) IC, (int) HID, (int) KW2, (int) OC, 1, x->data,
@@ -916,8 +1176,21 @@ extern "C" int tsk_conv_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, c
                       (hipStream_t) stream);
 }
 
-extern "C" int tsk_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x,
-                              tsk_tensor *dst, tsk_stream stream) {
+namespace {
+
+// a linear weight [K, M] (rows contiguous) as the kw-major conv kernel [1, K, M]
+tsk_tensor linear_as_kernel(const tsk_tensor *w) {
+    const size_t es = (size_t) elt_size(w->type);
+    tsk_tensor k;
+    k.type = w->type;
+    k.ne[0] = 1; k.ne[1] = w->ne[0]; k.ne[2] = w->ne[1]; k.ne[3] = 1;
+    k.nb[0] = (size_t) w->ne[0] * es; k.nb[1] = es; k.nb[2] = w->nb[1]; k.nb[3] = w->nb[1] * (size_t) w->ne[1];
+    k.data = w->data;
+    return k;
+}
+
+int validate_mlp(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x,
+                 const tsk_tensor *dst) {
     int rc;
     if ((rc = check_tensor(w1, "w1")) || (rc = check_tensor(w3, "w3")) || (rc = check_tensor(w2, "w2")) ||
         (rc = check_tensor(x, "x")) || (rc = check_tensor(dst, "dst")))
@@ -941,20 +1214,21 @@ extern "C" int tsk_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const 
     if (!rows_uniform(x) || !rows_uniform(dst)) return fail(TSK_ERR_STRIDE, "x and dst rows must be uniformly strided");
     const int64_t N = x->ne[1] * x->ne[2] * x->ne[3];
     if (N > (1 << 30)) return fail(TSK_ERR_SHAPE, "too many rows");
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_mlp_swiglu(const tsk_tensor *w1, const tsk_tensor *w3, const tsk_tensor *w2, const tsk_tensor *x,
+                              tsk_tensor *dst, tsk_stream stream) {
+    int rc = validate_mlp(w1, w3, w2, x, dst);
+    if (rc) return rc;
+    const int64_t IC = w1->ne[0], HID = w1->ne[1], OC = w2->ne[1];
+    const int64_t N = x->ne[1] * x->ne[2] * x->ne[3];
     if ((rc = require_init())) return rc;
     // a linear layer is the KW = 1, padding 0 convolution over one sequence of N rows
     const int esx = elt_size(x->type), esy = elt_size(dst->type);
-    auto as_kernel = [](const tsk_tensor *w) {
-        // [K, M] rows -> the kw-major conv kernel [1, K, M]
-        const size_t es = (size_t) elt_size(w->type);
-        tsk_tensor k;
-        k.type = w->type;
-        k.ne[0] = 1; k.ne[1] = w->ne[0]; k.ne[2] = w->ne[1]; k.ne[3] = 1;
-        k.nb[0] = (size_t) w->ne[0] * es; k.nb[1] = es; k.nb[2] = w->nb[1]; k.nb[3] = w->nb[1] * (size_t) w->ne[1];
-        k.data = w->data;
-        return k;
-    };
-    const tsk_tensor k1 = as_kernel(w1), k3 = as_kernel(w3), k2 = as_kernel(w2);
+    const tsk_tensor k1 = linear_as_kernel(w1), k3 = linear_as_kernel(w3), k2 = linear_as_kernel(w2);
     return swiglu_mlp(&k1, &k3, &k2, 1, (int) IC, (int) HID, 1, (int) OC, 0, x->data, x->type == TSK_TYPE_F32,
                       (int64_t) (x->nb[1] / esx), 0, (int) N, 1, dst->data, dst->type == TSK_TYPE_BF16,
                       (int64_t) (dst->nb[1] / esy), (hipStream_t) stream);
@@ -1004,4 +1278,61 @@ extern "C" int tsk_supports_op(int op, const tsk_tensor *const *srcs, int n_srcs
             rc = TSK_ERR_UNSUPPORTED;
     }
     return rc == TSK_OK ? 1 : 0;
+}
+
+// ------------------------------------------------------------------ workspace_size
+extern "C" int tsk_workspace_size(int op, const tsk_tensor *const *srcs, int n_srcs, const tsk_tensor *dst,
+                                  size_t *bytes) {
+    // validation only: data pointers are swapped for a dummy aligned address
+    static char dummy[64] __attribute__((aligned(64)));
+    if (!bytes) return fail(TSK_ERR_INVALID_ARG, "bytes is NULL");
+    *bytes = 0;
+    if (!srcs || !dst || n_srcs < 1 || n_srcs > 5) return fail(TSK_ERR_INVALID_ARG, "srcs / dst");
+    tsk_tensor t[5], d = *dst;
+    for (int i = 0; i < n_srcs; ++i) {
+        if (!srcs[i]) { t[i].type = -1; continue; }
+        t[i] = *srcs[i];
+        t[i].data = dummy;
+    }
+    d.data = dummy;
+    auto opt = [&](int i) -> const tsk_tensor * { return i < n_srcs && srcs[i] ? &t[i] : nullptr; };
+    auto need = [&](int n) { return n_srcs >= n ? TSK_OK : fail(TSK_ERR_INVALID_ARG, "op %d needs %d srcs", op, n); };
+    int rc;
+    switch (op) {
+        case TSK_OP_MUL_MAT:
+            if ((rc = need(2)) || (rc = validate_mul_mat(&t[0], &t[1], opt(2), &d))) return rc;
+            *bytes = plan_mul_mat(&t[0], &t[1], &d).bytes;
+            return TSK_OK;
+        case TSK_OP_FLASH_ATTN_EXT:
+            if ((rc = need(3)) || (rc = validate_fa(&t[0], &t[1], &t[2], opt(3), 0.125f, 0.0f, 0.0f, TSK_PREC_F32, &d)))
+                return rc;
+            *bytes = fa_ws_bytes(&t[0], &t[1], &t[2], opt(3), 0.0f, 0.0f, &d);
+            return TSK_OK;
+        case TSK_OP_CONV1D:
+            if ((rc = need(2)) || (rc = validate_conv(&t[0], opt(2), &t[1], 1, 1, 1, &d))) return rc;
+            *bytes = conv1d_ws_bytes(&t[0], &t[1]);
+            return TSK_OK;
+        case TSK_OP_CONV_MLP_SWIGLU:
+            if ((rc = need(4)) || (rc = validate_conv_mlp(&t[0], &t[1], &t[2], &t[3], &d))) return rc;
+            *bytes = swiglu_mlp_ws_bytes(&t[0], &t[1], &t[2], (int) t[0].ne[0], (int) t[0].ne[1], (int) t[0].ne[2], 1,
+                                         t[3].type == TSK_TYPE_F32, (int) t[3].ne[1], (int) t[3].ne[2]);
+            return TSK_OK;
+        case TSK_OP_MLP_SWIGLU:
+            if ((rc = need(4)) || (rc = validate_mlp(&t[0], &t[1], &t[2], &t[3], &d))) return rc;
+        {
+            // linear layers are k = 1, padding 0 convolutions over the N rows
+            const tsk_tensor k1 = linear_as_kernel(&t[0]), k3 = linear_as_kernel(&t[1]), k2 = linear_as_kernel(&t[2]);
+            *bytes = swiglu_mlp_ws_bytes(&k1, &k3, &k2, 1, (int) t[0].ne[0], (int) t[0].ne[1], 0,
+                                         t[3].type == TSK_TYPE_F32, (int) (t[3].ne[1] * t[3].ne[2] * t[3].ne[3]), 1);
+            return TSK_OK;
+        }
+        case TSK_OP_RMS_NORM_Q8_0:
+            if ((rc = need(2)) || (rc = validate_rms_norm_q8(&t[0], &t[1], &d))) return rc;
+            *bytes = rms_norm_q8_ws_bytes(&t[0]);
+            return TSK_OK;
+        case TSK_OP_RMS_NORM_MUL: case TSK_OP_ROPE_EXT: case TSK_OP_NORM: case TSK_OP_IM2COL:
+            return TSK_OK;   // no scratch
+        default:
+            return fail(TSK_ERR_UNSUPPORTED, "op %d", op);
+    }
 }

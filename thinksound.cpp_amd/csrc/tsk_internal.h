@@ -228,6 +228,10 @@ hipError_t launch_q8_quantize_blocks(const float *x, int64_t ld_x, int64_t rows,
                                      void *blocks, int64_t ld_blocks, hipStream_t s);
 hipError_t launch_q8_dequantize(const void *src, int split, int64_t rows, int64_t K,
                                 int64_t ld_src, float *y, int64_t ld_y, hipStream_t s);
+// Q8_0 planes (qx int8 [rows][K], dx f32 [rows][K/32] of fp16 values) ->
+// ggml blocks with row stride ld_blocks bytes (bit-preserving)
+hipError_t launch_q8_planes_to_blocks(const int8_t *qx, const float *dx, int64_t rows, int64_t K, void *blocks,
+                                     int64_t ld_blocks, hipStream_t s);
 hipError_t launch_q8_repack(const void *src, int64_t ld_src, int64_t rows, int64_t K,
                             void *dst, hipStream_t s);
 hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s);
@@ -299,6 +303,10 @@ hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, 
 // fp32 fma accumulation (the DiT's input and output projections)
 hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,
                            float *y, int64_t ld_y, hipStream_t s);
+// the same with x channel-major per batch item, [N / T][K][T] (ne0 = T): the
+// latent layout of ts_dit::forward; tmp holds N * K floats (used when K != 64)
+hipError_t launch_proj_f32_cm(const uint16_t *w, const float *bias, const float *x, int T, int N, int K, int M,
+                              float *y, int64_t ld_y, float *tmp, hipStream_t s);
 // t-embedding: temb[b, k] = cos(t_b * freq[k]), temb[b, H/2 + k] = sin(t_b * freq[k])
 struct TimeVals { float t[32]; };
 hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb,

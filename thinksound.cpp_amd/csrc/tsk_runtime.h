@@ -1,4 +1,5 @@
-// tsk_runtime.h — error reporting and the per-device workspace of the C ABI.
+// tsk_runtime.h — error reporting, per-stream workspaces and launch tuning of
+// the C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,9 +12,42 @@ int fail(int status, const char *fmt, ...);
 int hip_fail(hipError_t e, const char *what);
 // TSK_OK if tsk_init() was called
 int require_init();
-// device scratch of at least `bytes`, owned by the library (one per device and
-// slot: slot 0 serves single operators, slot 1 the composite entry points that
-// call them); growing it synchronises the device
-int workspace(size_t bytes, void **out, int slot = 0);
+
+// Device scratch of at least `bytes` for one call enqueued on stream s: the
+// buffer the caller bound to s with tsk_set_workspace (TSK_ERR_NOMEM if it is
+// too small; never reallocated), or else one library-owned buffer per
+// (device, stream), grown on demand. Growing waits for s only (the previous
+// buffer can only be read by work queued on s) and reallocates; a caller that
+// cannot allow that binds its own buffer, sized by tsk_workspace_size.
+int workspace(hipStream_t s, size_t bytes, void **out);
+
+// Launch-shape overrides for tuning sweeps and A/B tests, read from the
+// environment by tsk_init (every call re-reads them) and never on a launch:
+//   TSK_Q8_CFG    Q8_0 cooperative tile (2 = 64 x 64, 5 = 32 x 64; 0 = rule)
+//   TSK_Q8_OLD    1: the 2 x 2-wave Q8_0 kernel for every shape
+//   TSK_COOP_CFG  cooperative BF16 tile of the C-ABI GEMMs (0 = rule)
+//   TSK_GEMM_CFG  DiT block GEMM tiles, one character per projection
+//   TSK_ATTN_CFG  DiT attention launch shape (10 * key ranges + query blocks)
+//   TSK_DIT_SCHED 0: the sampler computes its conditioning inside every step
+//   TSK_LN_BLOCK  1: LayerNorm rows as one workgroup each (A/B reference)
+//   TSK_GEMV_RW   rows per wave of the adaLN GEMVs (1, 2, 4)
+struct Tuning {
+    int q8_cfg = 0;
+    bool q8_old = false;
+    int coop_cfg = 0;
+    int gemm_cfg[4] = {0, 0, 0, 0};
+    int attn_cfg = 0;
+    bool dit_sched = true;
+    bool ln_block = false;
+    int gemv_rw = 2;
+};
+const Tuning &tuning();
+
+// Device limits read once per tsk_init for the current device.
+struct DeviceInfo {
+    int cus = 256;               // compute units
+    size_t lds_per_block = 160 * 1024;   // bytes of LDS a workgroup may allocate
+};
+const DeviceInfo &device_info();
 
 }  // namespace tsk

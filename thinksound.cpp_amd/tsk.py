@@ -19,6 +19,7 @@ F32, F16, Q8_0, I32, BF16, Q8_0_SPLIT = 0, 1, 8, 26, 30, 0x1008
 PREC_DEFAULT, PREC_F32 = 0, 10
 ROPE_NORMAL = 0
 OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_RMS_NORM_MUL, OP_ROPE_EXT, OP_NORM, OP_IM2COL, OP_CONV1D = 1, 2, 3, 4, 5, 6, 7
+OP_CONV_MLP_SWIGLU, OP_MLP_SWIGLU, OP_RMS_NORM_Q8_0 = 8, 9, 10
 STATUS = {0: "TSK_OK", -1: "TSK_ERR_INVALID_ARG", -2: "TSK_ERR_TYPE", -3: "TSK_ERR_SHAPE",
           -4: "TSK_ERR_STRIDE", -5: "TSK_ERR_ALIGN", -6: "TSK_ERR_UNSUPPORTED",
           -7: "TSK_ERR_NOT_INIT", -8: "TSK_ERR_HIP", -9: "TSK_ERR_NOMEM"}
@@ -68,6 +69,8 @@ def load():
         "tsk_mul_mat": ([P, P, P, P, vp], i),
         "tsk_flash_attn_ext": ([P, P, P, P, f, f, f, i, P, vp], i),
         "tsk_rms_norm_mul": ([P, P, f, P, vp], i),
+        "tsk_t5_attention": ([P, P, P, P, vp, f, P, vp], i),
+        "tsk_rms_norm_q8_0": ([P, P, f, P, vp], i),
         "tsk_norm": ([P, f, P, vp], i),
         "tsk_rope_ext": ([P, P, i, i, f, f, f, f, P, vp], i),
         "tsk_qk_norm_rope": ([P, P, P, f, i, f, f, P, vp], i),
@@ -75,6 +78,9 @@ def load():
         "tsk_q8_0_repack": ([P, P, vp], i),
         "tsk_q8_0_split_nbytes": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_size_t),
         "tsk_supports_op": ([i, ctypes.POINTER(P), i, P], i),
+        "tsk_workspace_size": ([i, ctypes.POINTER(P), i, P, ctypes.POINTER(ctypes.c_size_t)], i),
+        "tsk_set_workspace": ([vp, vp, ctypes.c_size_t], i),
+        "tsk_release_workspace": ([vp], i),
         "tsk_im2col_1d": ([P, P, i, i, i, P, vp], i),
         "tsk_conv1d": ([P, P, P, i, i, i, P, vp], i),
         "tsk_conv1d_pack_weight": ([P, P, vp], i),
@@ -137,9 +143,11 @@ def check(rc):
 _initialised = False
 
 
-def init(device=0):
+def init(device=0, reread=False):
+    """tsk_init once per process; reread=True calls it again (it re-reads the
+    TSK_* launch-shape overrides from the environment)."""
     global _initialised
-    if not _initialised:
+    if not _initialised or reread:
         check(load().tsk_init(device))
         _initialised = True
 
@@ -162,6 +170,7 @@ def hip():
                          "hipMemcpy": [vp, vp, sz, i], "hipMemcpyAsync": [vp, vp, sz, i, vp],
                          "hipMemset": [vp, i, sz], "hipDeviceSynchronize": [],
                          "hipStreamSynchronize": [vp], "hipEventCreate": [ctypes.POINTER(vp)],
+                         "hipStreamCreate": [ctypes.POINTER(vp)], "hipStreamDestroy": [vp],
                          "hipEventDestroy": [vp], "hipEventRecord": [vp, vp],
                          "hipEventSynchronize": [vp],
                          "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp]}.items():
@@ -278,7 +287,7 @@ class Event:
         self.h = p
 
     def record(self, stream=None):
-        _hipcheck(hip().hipEventRecord(self.h, stream), "hipEventRecord")
+        _hipcheck(hip().hipEventRecord(self.h, _stream(stream)), "hipEventRecord")
 
     def elapsed_ms(self, end):
         _hipcheck(hip().hipEventSynchronize(end.h), "hipEventSynchronize")
@@ -339,8 +348,27 @@ def desc(t, ttype=None):
     return d
 
 
-def _stream():
-    return None     # the null stream
+class Stream:
+    """A HIP stream of the runtime libtsk.so links (default priority)."""
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _hipcheck(hip().hipStreamCreate(ctypes.byref(p)), "hipStreamCreate")
+        self.h = p
+
+    def synchronize(self):
+        _hipcheck(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
+
+    def destroy(self):
+        if getattr(self, "h", None) is not None:
+            release_workspace(self)
+            hip().hipStreamDestroy(self.h)
+            self.h = None
+
+
+def _stream(stream=None):
+    """hipStream_t of a Stream (None: the null stream)."""
+    return None if stream is None else stream.h
 
 
 def _ref(x):
@@ -348,7 +376,7 @@ def _ref(x):
 
 
 # ---------------------------------------------------------------- operators
-def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype="f32"):
+def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype="f32", stream=None):
     """ggml_mul_mat(a, b) (+bias): a (M, K) weights, b (..., N, K) -> (..., N, M)."""
     init()
     at = a_type if a_type is not None else a.ttype
@@ -357,12 +385,13 @@ def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype="f32"):
         out = DeviceArray(tuple(b.shape[:-1]) + (M,), out_dtype)
     da, db, dd = desc(a, at), desc(b), desc(out)
     dbias = desc(bias) if bias is not None else None
-    check(load().tsk_mul_mat(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd), _stream()))
+    check(load().tsk_mul_mat(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd),
+                             _stream(stream)))
     return out
 
 
 def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0, prec=PREC_F32,
-                   out=None, out_dtype="f32"):
+                   out=None, out_dtype="f32", stream=None):
     """q (B, H, Nq, D), k/v (B, Hkv, Nkv, D) -> (B, Nq, H, D) (ggml's permuted result)."""
     init()
     B, H, Nq, D = q.shape
@@ -371,8 +400,53 @@ def flash_attn_ext(q, k, v, mask=None, scale=0.125, max_bias=0.0, softcap=0.0, p
     dq, dk, dv, dd = desc(q), desc(k), desc(v), desc(out)
     dm = desc(mask) if mask is not None else None
     check(load().tsk_flash_attn_ext(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), _ref(dm),
-                                    scale, max_bias, softcap, prec, ctypes.byref(dd), _stream()))
+                                    scale, max_bias, softcap, prec, ctypes.byref(dd), _stream(stream)))
     return out
+
+
+def t5_attention(q, k, v, rel_lut, key_valid, scale=1.0, out=None):
+    """T5 self-attention with a relative-position bias table: q/k/v (1, H, n, 64)
+    views, rel_lut (H, 2 n_max - 1) f32, key_valid u8 (n,) -> (1, n, H, 64)."""
+    init()
+    _, H, n, D = q.shape
+    if out is None:
+        out = DeviceArray((1, n, H, D), "f32")
+    dq, dk, dv, dl, dd = desc(q), desc(k), desc(v), desc(rel_lut), desc(out)
+    check(load().tsk_t5_attention(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), ctypes.byref(dl),
+                                  ctypes.c_void_p(key_valid.data_ptr()), scale, ctypes.byref(dd), _stream()))
+    return out
+
+
+def workspace_size(op, srcs, dst):
+    """tsk_workspace_size: srcs are DeviceArrays, (DeviceArray, ttype) pairs or None."""
+    P = ctypes.POINTER(TskTensor)
+    descs = []
+    for x in srcs:
+        if x is None:
+            descs.append(None)
+        elif isinstance(x, tuple):
+            descs.append(desc(x[0], x[1]))
+        else:
+            descs.append(desc(x))
+    arr = (P * len(descs))(*[ctypes.pointer(d) if d is not None else P() for d in descs])
+    dd = desc(dst)
+    n = ctypes.c_size_t()
+    check(load().tsk_workspace_size(op, arr, len(descs), ctypes.byref(dd), ctypes.byref(n)))
+    return n.value
+
+
+def set_workspace(buf, stream=None):
+    """Bind DeviceArray buf (or None to unbind) as the workspace of `stream`."""
+    init()
+    if buf is None:
+        check(load().tsk_set_workspace(_stream(stream), None, 0))
+    else:
+        check(load().tsk_set_workspace(_stream(stream), ctypes.c_void_p(buf.data_ptr()), buf.nbytes))
+
+
+def release_workspace(stream=None):
+    init()
+    check(load().tsk_release_workspace(_stream(stream)))
 
 
 def rms_norm_mul(x, w, eps, out=None):
@@ -409,6 +483,16 @@ def qk_norm_rope(x, w, pos, eps=1e-6, n_dims=64, freq_base=10000.0, freq_scale=1
     dp = desc(pos) if pos is not None else None
     check(load().tsk_qk_norm_rope(ctypes.byref(dx), ctypes.byref(dw), _ref(dp), eps, n_dims, freq_base,
                                   freq_scale, ctypes.byref(dd), _stream()))
+    return out
+
+
+def rms_norm_q8_0(x, w, eps):
+    """T5's rms_norm * w straight into ggml Q8_0 blocks: x (rows, n) f32 -> u8 (rows, n/32, 34)."""
+    init()
+    rows, n = x.shape
+    out = DeviceArray((rows, n // 32, 34), "u8")
+    dx, dw, dd = desc(x), desc(w), desc(out, Q8_0)
+    check(load().tsk_rms_norm_q8_0(ctypes.byref(dx), ctypes.byref(dw), eps, ctypes.byref(dd), _stream()))
     return out
 
 
@@ -604,22 +688,23 @@ class Dit:
         check(load().tsk_dit_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
 
     def forward(self, latent, t, text):
-        """host numpy arrays: latent (B, T, L), t (B,), text (B, text_seq, hidden) -> flow (B, T, L)."""
+        """ts_dit::forward layouts, host numpy arrays: latent (B, L, T) (ggml ne =
+        [T, L, B]), t (B,), text (B, text_seq, hidden) -> flow (B, T, L)."""
         import numpy as np
         latent = np.ascontiguousarray(latent, dtype=np.float32)
         t = np.ascontiguousarray(t, dtype=np.float32)
         text = np.ascontiguousarray(text, dtype=np.float32)
-        B, T, L = latent.shape
-        flow = np.empty_like(latent)
+        B, L, T = latent.shape
+        flow = np.empty((B, T, L), np.float32)
         check(load().tsk_dit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data, text.ctypes.data,
                                      flow.ctypes.data, _stream()))
         return flow
 
     def forward_device(self, latent, t, text, flow):
-        """DeviceArrays latent (B, T, L), text (B, S, H), flow out (f32); t host numpy (B,)."""
+        """DeviceArrays latent (B, L, T), text (B, S, H), flow out (B, T, L) f32; t host numpy (B,)."""
         import numpy as np
         t = np.ascontiguousarray(t, dtype=np.float32)
-        B, T, _ = latent.shape
+        B, _, T = latent.shape
         check(load().tsk_dit_forward_device(self.h, B, T, ctypes.c_void_p(latent.data_ptr()),
                                             t.ctypes.data, ctypes.c_void_p(text.data_ptr()),
                                             ctypes.c_void_p(flow.data_ptr()), _stream()))
@@ -641,11 +726,13 @@ class Dit:
         return out
 
     def sample(self, noise, text_cond, text_uncond, steps=24, cfg_scale=5.0):
+        """ts_dit::sample layouts: noise (L, T) (ggml ne = [T, L]), text (text_seq, hidden)
+        -> (latent (L, T), flow0 (L, T))."""
         import numpy as np
         noise = np.ascontiguousarray(noise, dtype=np.float32)
         text_cond = np.ascontiguousarray(text_cond, dtype=np.float32)
         text_uncond = np.ascontiguousarray(text_uncond, dtype=np.float32)
-        T, L = noise.shape
+        L, T = noise.shape
         out = np.empty_like(noise)
         flow0 = np.empty_like(noise)
         check(load().tsk_dit_sample(self.h, T, noise.ctypes.data, text_cond.ctypes.data,
