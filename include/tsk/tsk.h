@@ -144,6 +144,22 @@ int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias
                 tsk_tensor *dst, tsk_stream stream);
 
 /*
+ * tsk_mul_mat that allocates nothing: no counterpart in the reference (ggml's
+ * backends own their scratch pools). For callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same operands, semantics and results (bit for bit) as
+ * tsk_mul_mat; its scratch (the bf16 rows of f32 activations, the Q8_0
+ * repack and activation planes) lives in one fixed array of
+ * TSK_MUL_MAT_NOALLOC_SCRATCH bytes per GPU, resident until the process
+ * ends; a node needing more (tsk_workspace_size) returns TSK_ERR_NOMEM
+ * before any launch. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams or threads) race.
+ */
+#define TSK_MUL_MAT_NOALLOC_SCRATCH (32u << 20)
+int tsk_mul_mat_noalloc(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias,
+                        tsk_tensor *dst, tsk_stream stream);
+
+/*
  * ggml_flash_attn_ext semantics (non-causal, online softmax):
  *   q    : ne = [D, Nq, H, B]   F32, F16 or BF16
  *   k    : ne = [D, Nkv, Hkv, B] F32, F16 or BF16   (H % Hkv == 0)

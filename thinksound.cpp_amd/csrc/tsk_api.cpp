@@ -74,6 +74,30 @@ void read_tuning() {
 }
 }  // namespace
 
+// Scratch of tsk_mul_mat_noalloc: one fixed array in every GPU's memory (it
+// stays resident until the process ends). Host code never uses the array's
+// name as an address: its device address comes from hipGetSymbolAddress,
+// once per device with that device current.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) TSK_MUL_MAT_NOALLOC_SCRATCH;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+namespace {
+void *g_scratch_ptr[64];   // per device; nullptr until looked up
+
+// the device address of `scratch` on device dev (current); g_mu held
+int scratch_address_locked(int dev, void **out) {
+    if (dev < 0 || dev >= 64) return fail(TSK_ERR_INVALID_ARG, "device id %d out of range", dev);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(TSK_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TSK_OK;
+}
+}  // namespace
+
 const Tuning &tuning() { return g_tuning; }
 const DeviceInfo &device_info() { return g_dev; }
 
@@ -179,6 +203,9 @@ extern "C" int tsk_init(int device) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
         di.lds_per_block = (size_t) v;
     std::lock_guard<std::mutex> lk(g_mu);
+    void *sp = nullptr;
+    int rc = scratch_address_locked(device, &sp);
+    if (rc) return rc;
     read_tuning();
     g_dev = di;
     g_device = device;
@@ -464,6 +491,26 @@ extern "C" int tsk_mul_mat(const tsk_tensor *a, const tsk_tensor *b, const tsk_t
     if (rc) return rc;
     if ((rc = require_init())) return rc;
     return mul_mat_impl(a, b, bias, dst, Scratch{(hipStream_t) stream, nullptr, 0});
+}
+
+extern "C" int tsk_mul_mat_noalloc(const tsk_tensor *a, const tsk_tensor *b, const tsk_tensor *bias, tsk_tensor *dst,
+                                   tsk_stream stream) {
+    int rc = validate_mul_mat(a, b, bias, dst);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    const size_t need = plan_mul_mat(a, b, dst).bytes;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(TSK_ERR_NOMEM, "tsk_mul_mat_noalloc: the node needs %zu bytes of scratch, the fixed limit is %zu",
+                    need, NOALLOC_SCRATCH_BYTES);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    void *sp = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if ((rc = scratch_address_locked(dev, &sp))) return rc;
+    }
+    return mul_mat_impl(a, b, bias, dst, Scratch{(hipStream_t) stream, sp, NOALLOC_SCRATCH_BYTES});
 }
 
 // ------------------------------------------------------------------ flash_attn_ext

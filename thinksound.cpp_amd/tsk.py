@@ -67,6 +67,7 @@ def load():
         "tsk_status_string": ([i], ctypes.c_char_p), "tsk_last_error": ([], ctypes.c_char_p),
         "tsk_version": ([], ctypes.c_char_p),
         "tsk_mul_mat": ([P, P, P, P, vp], i),
+        "tsk_mul_mat_noalloc": ([P, P, P, P, vp], i),
         "tsk_flash_attn_ext": ([P, P, P, P, f, f, f, i, P, vp], i),
         "tsk_rms_norm_mul": ([P, P, f, P, vp], i),
         "tsk_t5_attention": ([P, P, P, P, vp, f, P, vp], i),
@@ -387,6 +388,20 @@ def mul_mat(a, b, bias=None, out=None, a_type=None, out_dtype="f32", stream=None
     dbias = desc(bias) if bias is not None else None
     check(load().tsk_mul_mat(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd),
                              _stream(stream)))
+    return out
+
+
+def mul_mat_noalloc(a, b, bias=None, out=None, a_type=None, out_dtype="f32", stream=None):
+    """mul_mat through tsk_mul_mat_noalloc (scratch in the library's fixed per-GPU array)."""
+    init()
+    at = a_type if a_type is not None else a.ttype
+    M = a.shape[0] if at != Q8_0_SPLIT else a.logical_shape[1]
+    if out is None:
+        out = DeviceArray(tuple(b.shape[:-1]) + (M,), out_dtype)
+    da, db, dd = desc(a, at), desc(b), desc(out)
+    dbias = desc(bias) if bias is not None else None
+    check(load().tsk_mul_mat_noalloc(ctypes.byref(da), ctypes.byref(db), _ref(dbias), ctypes.byref(dd),
+                                     _stream(stream)))
     return out
 
 
