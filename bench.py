@@ -332,6 +332,33 @@ def main():
     sample30 = {"steps": 24, "cfg_scale": 5.0, "latent_tokens": 646, "seconds": round(wall, 5),
                 "sampler_steps_per_s": round(24 / wall, 2), "ms_per_step": round(wall / 24 * 1e3, 4)}
 
+    # the Q8_0 driver (block projections as Q8_0 weights, Q8_0 x Q8_0 products)
+    # on the 9 s step: the same seeded weights, quantized with ggml's reference
+    # quantizer by tsk_dit_set_tensor
+    dq = tsk.Dit(tsk.dit_config(max_batch=2, max_latent=194, weight_type=8))
+    for k, v in weights.items():
+        dq.set_tensor(k, v)
+    lat, t, txt = make_inputs(2, 194)
+    lat_d, txt_d = tsk.to_device(np.ascontiguousarray(lat.transpose(0, 2, 1))), tsk.to_device(txt)
+    flow_q = tsk.empty((2, 194, 64))
+    for _ in range(args.warmup):
+        dq.forward_device(lat_d, t, txt_d, flow_q)
+    tsk.synchronize()
+    sq, eq = tsk.Event(), tsk.Event()
+    sq.record()
+    for _ in range(args.steps):
+        dq.forward_device(lat_d, t, txt_d, flow_q)
+    eq.record()
+    tsk.synchronize()
+    ms_q8 = sq.elapsed_ms(eq) / args.steps
+    dq.timing(True)
+    for _ in range(args.steps):
+        dq.forward_device(lat_d, t, txt_d, flow_q)
+    tsk.synchronize()
+    dq.timing(False)
+    roles_q8 = dq.timing_read()
+    dq.close()
+
     # the reference graph's convolution glue at 30 s (B = 2, 646 positions):
     # convmlp 1024 -> 2816 -> 1024 (k3, padding 1, SwiGLU) and a conv_cl
     # linear1 1024 -> 1024 (k3), BF16 kernels packed kw-major once, f32 input
@@ -380,6 +407,10 @@ def main():
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
         "conv_30s": conv30,
         "q8_0_projections_30s": q8,
+        "q8_0_flow_step_9s": {"steps_per_s": round(1000.0 / ms_q8, 2), "ms_per_step": round(ms_q8, 4),
+                              "weights": "Q8_0 attn.qkv / linear1 / ffn.fc1 / ffn.fc2 (ggml reference "
+                                         "quantizer), other matrices BF16",
+                              "breakdown": breakdown(roles_q8, args.steps)},
         "t5_encoder_config4": t5,
     }
     if not args.no_cpu_baseline:

@@ -439,7 +439,10 @@ typedef struct tsk_dit_config {
     int   text_seq;      /* 77   */
     int   mlp_hidden;    /* 4096 */
     int   mlp_kind;      /* enum tsk_mlp_kind */
-    int   weight_type;   /* TSK_TYPE_BF16 (only weight type of the DiT driver) */
+    int   weight_type;   /* TSK_TYPE_BF16, or TSK_TYPE_Q8_0: the block
+                            projections (attn.qkv, linear1, ffn.fc1, ffn.fc2)
+                            as Q8_0 with Q8_0-quantized activations (ggml's
+                            Q8_0 x Q8_0 mul_mat); every other matrix BF16 */
     int   max_batch;     /* capacity: batch rows per forward (2 for CFG) */
     int   max_latent;    /* capacity: latent tokens T                    */
     float rope_theta;    /* 10000 */
@@ -456,9 +459,21 @@ void tsk_dit_destroy(tsk_dit *dit);
 /* Number of named weight tensors and the i-th name / ggml shape. */
 int  tsk_dit_n_tensors(const tsk_dit *dit);
 int  tsk_dit_tensor_info(const tsk_dit *dit, int i, const char **name, int64_t ne[4]);
-/* Upload one named weight from HOST f32 data (converted to the weight type). */
+/* Upload one named weight from HOST f32 data, converted to the type the
+ * driver stores it in: BF16 (RNE) matrices, F32 vectors, and for the Q8_0
+ * driver's block projections ggml's reference Q8_0 quantization
+ * (quantize_row_q8_0_ref; the converter's gguf-py quantize is bit-identical,
+ * convert/quantize_gguf.py:41). */
 int  tsk_dit_set_tensor(tsk_dit *dit, const char *name, const float *host_f32,
                         int64_t n_elements);
+/* Upload a Q8_0 block projection of the Q8_0 driver from HOST ggml Q8_0
+ * blocks as stored in a GGUF file (34 bytes per 32 values along ne[0],
+ * nbytes exact): bit-preserving. TSK_ERR_TYPE for a tensor the driver does
+ * not store as Q8_0. */
+int  tsk_dit_set_tensor_q8_0(tsk_dit *dit, const char *name, const void *blocks, size_t nbytes);
+/* The type the driver stores tensor i in: TSK_TYPE_BF16, TSK_TYPE_Q8_0 or
+ * TSK_TYPE_F32 (a negative status for a bad index). */
+int  tsk_dit_tensor_type(const tsk_dit *dit, int i);
 /*
  * One flow evaluation for B (<= max_batch) rows, all pointers HOST, in the
  * layouts of ts_dit::forward (src/mmdit.h:26-29, src/mmdit.cpp:138, :289)
@@ -489,10 +504,11 @@ int  tsk_dit_sample(tsk_dit *dit, int T, const float *noise, const float *text_c
                     float *out, float *flow0, tsk_stream stream);
 /* dit.* metadata of convert_thinksound.py:38-45 over the values already in cfg */
 int  tsk_dit_config_from_gguf(const tsk_gguf *g, tsk_dit_config *cfg);
-/* every weight by name from a GGUF file: F32 / F16 / BF16 tensors, converted
- * to f32 and set as tsk_dit_set_tensor does (matrices rounded to the
- * driver's BF16); a Q8_0 matrix returns TSK_ERR_TYPE (this driver runs BF16
- * weights) */
+/* every weight by name from a GGUF file: Q8_0 tensors the driver stores as
+ * Q8_0 bit for bit (tsk_dit_set_tensor_q8_0); F32 / F16 / BF16 tensors
+ * converted to f32 and set as tsk_dit_set_tensor does; a Q8_0 tensor the
+ * driver stores in another type returns TSK_ERR_TYPE (bf16(d * q) would not
+ * be the Q8_0 x Q8_0 product the file asks for) */
 int  tsk_dit_load_gguf(tsk_dit *dit, const tsk_gguf *g);
 
 /*

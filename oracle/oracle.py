@@ -77,6 +77,7 @@ def lib():
         L.orc_dit_create.argtypes = [ctypes.POINTER(DitConfig)]
         L.orc_dit_create.restype = ctypes.c_void_p
         L.orc_dit_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_dit_set_tensor_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_size_t]
         L.orc_dit_n_tensors.argtypes = [ctypes.c_void_p]
         L.orc_dit_tensor_info.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
@@ -378,6 +379,12 @@ class OracleDiT:
     def set_tensor(self, name, arr):
         arr = np.ascontiguousarray(arr, dtype=np.float32)
         rc = lib().orc_dit_set_tensor(self.h, name.encode(), arr.ctypes.data, arr.size)
+        assert rc == 0, (name, rc)
+
+    def set_tensor_q8_0(self, name, blocks):
+        """ggml Q8_0 blocks (uint8, 34 bytes per 32 values) of a Q8_0 block projection"""
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        rc = lib().orc_dit_set_tensor_q8_0(self.h, name.encode(), blocks.ctypes.data, blocks.nbytes)
         assert rc == 0, (name, rc)
 
     def forward(self, latent, t, text, act_bf16=True, kv_f16=True):

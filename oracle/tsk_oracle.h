@@ -91,6 +91,8 @@ typedef struct orc_dit orc_dit;
 orc_dit *orc_dit_create(const tsk_dit_config *cfg);
 void     orc_dit_destroy(orc_dit *d);
 int      orc_dit_set_tensor(orc_dit *d, const char *name, const float *src, int64_t n);
+/* weight_type Q8_0: the block projections' ggml Q8_0 blocks, as stored */
+int      orc_dit_set_tensor_q8_0(orc_dit *d, const char *name, const void *blocks, size_t nbytes);
 int      orc_dit_n_tensors(const orc_dit *d);
 /* name and ggml ne[0], ne[1] of the i-th weight */
 int      orc_dit_tensor_info(const orc_dit *d, int i, const char **name, int64_t *ne0, int64_t *ne1);

@@ -25,7 +25,14 @@
 #include <stdlib.h>
 #include <string.h>
 
-typedef struct { char name[96]; int64_t ne[2]; float *data; } orc_w;
+/* a weight: f32 values, or (q8) ggml Q8_0 blocks [ne1][ne0 / 32] */
+typedef struct { char name[96]; int64_t ne[2]; float *data; uint8_t *q8; } orc_w;
+
+/* the Q8_0 driver's Q8_0 matrices: the block projections */
+static int is_block_proj(const char *name) {
+    return strstr(name, ".attn.qkv.weight") || strstr(name, ".linear1.weight") || strstr(name, ".ffn.fc1.weight") ||
+           strstr(name, ".ffn.fc2.weight");
+}
 
 struct orc_dit {
     tsk_dit_config cfg;
@@ -42,6 +49,8 @@ static void add_w(orc_dit *d, const char *name, int64_t ne0, int64_t ne1) {
     snprintf(w->name, sizeof(w->name), "%s", name);
     w->ne[0] = ne0; w->ne[1] = ne1;
     w->data = (float *) calloc((size_t) (ne0 * ne1), sizeof(float));
+    w->q8 = d->cfg.weight_type == TSK_TYPE_Q8_0 && is_block_proj(name)
+                ? (uint8_t *) calloc((size_t) (ne0 / 32 * ne1), 34) : NULL;
 }
 
 static void add_block(orc_dit *d, const char *p, int pre_only) {
@@ -93,7 +102,7 @@ orc_dit *orc_dit_create(const tsk_dit_config *cfg) {
 
 void orc_dit_destroy(orc_dit *d) {
     if (!d) return;
-    for (int i = 0; i < d->nw; ++i) free(d->w[i].data);
+    for (int i = 0; i < d->nw; ++i) { free(d->w[i].data); free(d->w[i].q8); }
     free(d->w); free(d);
 }
 
@@ -113,11 +122,26 @@ static orc_w *find_w(orc_dit *d, const char *name) {
     abort();
 }
 
+/* f32 values; a Q8_0 weight is quantized with ggml's reference quantizer
+ * (quantize_row_q8_0_ref: id = 1 / d, round half away) */
 int orc_dit_set_tensor(orc_dit *d, const char *name, const float *src, int64_t n) {
     for (int i = 0; i < d->nw; ++i) {
         if (strcmp(d->w[i].name, name)) continue;
         if (n != d->w[i].ne[0] * d->w[i].ne[1]) return TSK_ERR_SHAPE;
         memcpy(d->w[i].data, src, sizeof(float) * (size_t) n);
+        if (d->w[i].q8) orc_quantize_q8_0(src, d->w[i].q8, n, ORC_Q8_CPU_REF);
+        return TSK_OK;
+    }
+    return TSK_ERR_INVALID_ARG;
+}
+
+/* ggml Q8_0 blocks of a Q8_0 weight, as stored */
+int orc_dit_set_tensor_q8_0(orc_dit *d, const char *name, const void *blocks, size_t nbytes) {
+    for (int i = 0; i < d->nw; ++i) {
+        if (strcmp(d->w[i].name, name)) continue;
+        if (!d->w[i].q8) return TSK_ERR_TYPE;
+        if (nbytes != (size_t) (d->w[i].ne[0] / 32 * d->w[i].ne[1]) * 34) return TSK_ERR_SHAPE;
+        memcpy(d->w[i].q8, blocks, nbytes);
         return TSK_OK;
     }
     return TSK_ERR_INVALID_ARG;
@@ -140,7 +164,12 @@ static void lin(orc_dit *d, const char *wname, const char *bname, const float *x
     tsk_tensor tbias = { TSK_TYPE_F32, {M, 1, 1, 1}, {4, 4 * M, 4 * M, 4 * M}, b ? b->data : NULL };
     float *xr = NULL;
     const int block_proj = strstr(wname, ".attn.qkv.") || strstr(wname, ".linear1.") || strstr(wname, ".ffn.fc");
-    if (act_bf16 && block_proj) {
+    if (w->q8) {
+        /* Q8_0 weight: ggml_mul_mat quantizes x to Q8_0 (the x86 path) */
+        ta.type = TSK_TYPE_Q8_0;
+        ta.nb[0] = 34; ta.nb[1] = (size_t) (K / 32) * 34; ta.nb[2] = ta.nb[3] = ta.nb[1] * (size_t) M;
+        ta.data = w->q8;
+    } else if (act_bf16 && block_proj) {
         xr = (float *) malloc(sizeof(float) * (size_t) (K * N));
         for (int64_t i = 0; i < K * N; ++i) xr[i] = orc_bf16_to_fp32(orc_fp32_to_bf16(x[i]));
         tb.data = xr;

@@ -1,0 +1,171 @@
+"""The Q8_0 MM-DiT driver (tsk_dit_config.weight_type = Q8_0): the block
+projections (attn.qkv, linear1, ffn.fc1, ffn.fc2) are ggml Q8_0 weights and
+every activation they read is quantized to Q8_0 first, so each product is
+ggml's Q8_0 x Q8_0 vec_dot (exact int32 block sums, fp32 scaling); the rest
+of the step is the BF16 driver's. Compared with the oracle's restatement run
+with the same Q8_0 blocks.
+
+Both sides quantize activations with the x86 rule (d = amax / 127 as fp16,
+q = rne(x 127 / amax)); an activation that lands within an ulp of a rounding
+boundary can round differently when its fp32 value differs by summation
+order, so each flow step is checked against max(2e-3, 2 x the oracle's own
+change under a one-ulp (1e-7 relative) change of its input latent)."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+Q8_0 = 8
+
+
+@pytest.fixture(scope="module")
+def env(orc):
+    from __graft_entry__ import ensure_built, load_tsk
+    ensure_built()
+    tsk = load_tsk()
+    tsk.init(0)
+    return tsk, orc
+
+
+def build_q8_pair(tsk, orc, seed=1234, raw=True, **kw):
+    """driver + oracle with the same weights; the Q8_0 projections as ggml
+    blocks from ggml's reference quantizer (raw) or quantized by each side from
+    the same f32 values"""
+    kw = dict(kw, weight_type=Q8_0)
+    dit = tsk.Dit(tsk.dit_config(**kw))
+    od = orc.OracleDiT(orc.dit_config(**kw))
+    names = dit.tensors()
+    assert names == od.tensors()
+    types = dit.tensor_types()
+    W = tsk.synthetic_weights(names, seed=seed)
+    for k, v in W.items():
+        if types[k] == Q8_0 and raw:
+            blocks = orc.quantize_q8_0(v, orc.Q8_CPU_REF)
+            dit.set_tensor_q8_0(k, blocks)
+            od.set_tensor_q8_0(k, blocks)
+        else:
+            dit.set_tensor(k, v)
+            od.set_tensor(k, v)
+    return dit, od, W, types
+
+
+def inputs(B, T, seed=4242, t=0.5):
+    rng = np.random.default_rng(seed)
+    lat = rng.standard_normal((B, T, 64), dtype=np.float32)
+    txt = rng.standard_normal((B, 77, 1024), dtype=np.float32)
+    return lat, np.full(B, t, np.float32), txt
+
+
+def cm(lat):
+    return np.ascontiguousarray(lat.transpose(0, 2, 1))
+
+
+def one_ulp_sensitivity(od, lat, t, txt, seed=99):
+    rng = np.random.default_rng(seed)
+    ref = od.forward(lat, t, txt, act_bf16=True, kv_f16=True)
+    pert = (lat * (1 + 1e-7 * rng.standard_normal(lat.shape))).astype(np.float32)
+    return ref, rel_l2(od.forward(pert, t, txt, act_bf16=True, kv_f16=True), ref)
+
+
+def test_q8_types_and_host_quantizer(env):
+    """exactly the four block projections are Q8_0, and tsk_dit_set_tensor's
+    host quantization of f32 weights is ggml's reference quantizer bit for
+    bit (same forward output as uploading its blocks)"""
+    tsk, orc = env
+    kw = dict(depth=2, fused_depth=1, max_latent=64)
+    a, _, W, types = build_q8_pair(tsk, orc, raw=True, **kw)
+    b, _, _, _ = build_q8_pair(tsk, orc, raw=False, **kw)
+    q8 = sorted(k for k, ty in types.items() if ty == Q8_0)
+    assert q8 and all(any(k.endswith(s) for s in (".attn.qkv.weight", ".linear1.weight", ".ffn.fc1.weight",
+                                                   ".ffn.fc2.weight")) for k in q8)
+    assert len(q8) == 4 + 1 + 4              # joint latent, joint text (pre_only: qkv only), fused
+    lat, t, txt = inputs(2, 40)
+    assert np.array_equal(a.forward(cm(lat), t, txt), b.forward(cm(lat), t, txt))
+    with pytest.raises(tsk.TskError):
+        a.set_tensor_q8_0("t_embed.mlp.0.weight", np.zeros((1024, 32, 34), np.uint8))
+    a.close()
+    b.close()
+
+
+def test_q8_small_forward(env):
+    tsk, orc = env
+    dit, od, _, _ = build_q8_pair(tsk, orc, depth=3, fused_depth=1, max_latent=64)
+    lat, t, txt = inputs(2, 50)
+    f = dit.forward(cm(lat), t, txt)
+    ref, sens = one_ulp_sensitivity(od, lat, t, txt)
+    e = rel_l2(f, ref)
+    print(f"Q8_0 small DiT vs oracle Q8_0 path: rel-L2 {e:.3e} (oracle one-ulp sensitivity {sens:.3e})", flush=True)
+    assert e <= max(2e-3, 2 * sens)
+    dit.close()
+
+
+def test_q8_config2_flow_step(env):
+    """configuration 2's step (9 s, 194 + 77 tokens, CFG batch 2, 21 blocks)
+    with Q8_0 block projections"""
+    tsk, orc = env
+    dit, od, _, _ = build_q8_pair(tsk, orc)
+    lat, t, txt = inputs(2, 194)
+    f = dit.forward(cm(lat), t, txt)
+    ref, sens = one_ulp_sensitivity(od, lat, t, txt)
+    e = rel_l2(f, ref)
+    print(f"Q8_0 config 2 step vs oracle Q8_0 path: rel-L2 {e:.3e} (oracle one-ulp sensitivity {sens:.3e})",
+          flush=True)
+    assert e <= max(2e-3, 2 * sens)
+    assert np.array_equal(dit.forward(cm(lat), t, txt), f)          # deterministic
+    f1 = dit.forward(cm(lat[1:]), t[1:], txt[1:])
+    assert np.array_equal(f1[0], f[1])                              # batch rows independent
+    dit.close()
+
+
+def test_q8_sampler(env):
+    """ts_dit::sample with the Q8_0 driver: 3 steps, CFG 5, against the
+    oracle's sampler with the same Q8_0 blocks. flow0 = u + 5 (c - u)
+    multiplies the independent rounding noise of the two forwards by ~6.4, so
+    flow0 and the latent are held to max(5e-3, 2.5 x the oracle sampler's own
+    change under a one-ulp change of its noise, the larger of two draws)."""
+    tsk, orc = env
+    dit, od, _, _ = build_q8_pair(tsk, orc, depth=2, fused_depth=1, max_latent=64)
+    rng = np.random.default_rng(4242)
+    noise = rng.standard_normal((40, 64), dtype=np.float32)
+    tc = rng.standard_normal((77, 1024), dtype=np.float32)
+    tu = rng.standard_normal((77, 1024), dtype=np.float32)
+    x, flow0 = dit.sample(noise.T, tc, tu, steps=3, cfg_scale=5.0)
+    rx, rflow0 = od.sample(noise, tc, tu, steps=3, cfg_scale=5.0, act_bf16=True, kv_f16=True)
+    s0 = sx = 0.0
+    for _ in range(2):
+        pert = (noise * (1 + 1e-7 * rng.standard_normal(noise.shape))).astype(np.float32)
+        px, pflow0 = od.sample(pert, tc, tu, steps=3, cfg_scale=5.0, act_bf16=True, kv_f16=True)
+        s0, sx = max(s0, rel_l2(pflow0, rflow0)), max(sx, rel_l2(px, rx))
+    e0, ex = rel_l2(flow0.T, rflow0), rel_l2(x.T, rx)
+    print(f"Q8_0 sampler: flow0 {e0:.3e}, latent {ex:.3e} (oracle one-ulp sensitivity {s0:.3e}, {sx:.3e})",
+          flush=True)
+    assert e0 <= max(5e-3, 2.5 * s0) and ex <= max(5e-3, 2.5 * sx)
+    dit.close()
+
+
+def test_q8_load_gguf(env, tmp_path):
+    """a GGUF file with Q8_0 block projections (the q8 converter's output) loads
+    bit for bit: the same forward as uploading the blocks directly"""
+    import gguf_writer as gw
+    tsk, orc = env
+    kw = dict(depth=2, fused_depth=1, max_latent=64)
+    a, _, W, types = build_q8_pair(tsk, orc, **kw)
+    tensors = []
+    for name, w in W.items():
+        if types[name] == Q8_0:
+            tensors.append(gw.q8_0_tensor(name, orc.quantize_q8_0(w, orc.Q8_CPU_REF), w.shape[1]))
+        elif w.ndim == 2:
+            tensors.append(gw.bf16_tensor(name, orc.f32_to_bf16_bits(w)))
+        else:
+            tensors.append(gw.f32_tensor(name, w))
+    path = tmp_path / "dit_q8.gguf"
+    gw.write_gguf(path, {"dit.depth": (gw.U32, 2), "dit.fused_depth": (gw.U32, 1)}, tensors)
+    g = tsk.Gguf(path)
+    b = tsk.Dit(tsk.dit_config(weight_type=Q8_0, **kw))
+    g.load_into(b)
+    lat, t, txt = inputs(2, 40, seed=5)
+    assert np.array_equal(a.forward(cm(lat), t, txt), b.forward(cm(lat), t, txt))
+    g.close()
+    a.close()
+    b.close()

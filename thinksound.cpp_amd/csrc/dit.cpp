@@ -41,6 +41,7 @@ struct WInfo {
     bool matrix;           // stored bf16
     bool qkv_perm;         // rows (or entries) permuted (h d j) -> [q | k | v]
     bool tiled;            // stored in the MFMA-tiled layout of the block GEMMs
+    bool q8;               // stored as Q8_0 planes: int8 [ne1][ne0], fp16 d [ne1][ne0 / 32]
     size_t offset;         // bytes into the weight blob
     float amax;            // max |value| of a vector as last set (0 until then)
 };
@@ -58,8 +59,14 @@ constexpr int KSPLIT_OUT = 2;    // linear1 (K = hidden)
 constexpr int KSPLIT_FC2 = 4;    // ffn.fc2 (K = mlp_hidden)
 constexpr int KSPLIT_MAX = 4;
 
+struct Q8W {                // a Q8_0 matrix as planes
+    const int8_t *q;
+    const uint16_t *d;
+};
+
 struct StreamW {           // one MMDitSingleBlock's weights
     const uint16_t *ada_w, *qkv_w, *l1_w, *fc1_w, *fc2_w;
+    Q8W qkv_q, l1_q, fc1_q, fc2_q;   // the Q8_0 driver's block projections
     const float *ada_b, *qkv_b, *qn, *kn, *l1_b, *fc1_b, *fc2_b;
     bool pre_only;
     float *mod;            // [max_batch][nmod * H] adaLN output
@@ -116,6 +123,14 @@ struct tsk_dit {
     RoleTiming rt[TSK_ROLE_COUNT];
     // sampler buffers
     float *s_x = nullptr, *s_x2 = nullptr, *s_text2 = nullptr, *s_flow2 = nullptr, *s_flow0 = nullptr;
+    // Q8_0 driver (weight_type Q8_0): f32 QKV rows [rows][3 H], f32 attention
+    // output [B][Ntot][H], f32 GELU outputs [rows][F], and the Q8_0 planes of
+    // the activations a block projection reads (int8 qx [rows][<= F], f32
+    // block scales dx [rows][<= F / 32]); latent rows first, text rows from
+    // the capacity offset
+    bool q8 = false;
+    float *qkv32 = nullptr, *o32 = nullptr, *h32 = nullptr, *dx = nullptr;
+    int8_t *qx = nullptr;
 };
 
 namespace {
@@ -160,7 +175,9 @@ void add(tsk_dit *d, const std::string &name, int64_t ne0, int64_t ne1, bool mat
     wi.ne1 = ne1;
     wi.matrix = matrix;
     wi.qkv_perm = perm;
-    wi.tiled = tiled;
+    // the block projections (the tiled matrices) are Q8_0 in the Q8_0 driver
+    wi.q8 = tiled && d->cfg.weight_type == TSK_TYPE_Q8_0;
+    wi.tiled = tiled && !wi.q8;
     wi.offset = 0;
     wi.amax = 0.0f;
     d->idx[name] = (int) d->w.size();
@@ -203,6 +220,21 @@ StreamW stream_weights(tsk_dit *d, const std::string &p, bool pre_only) {
     s.kn = wptr<float>(d, p + ".attn.k_norm.weight");
     s.qn_idx = d->idx.at(p + ".attn.q_norm.weight");
     s.kn_idx = d->idx.at(p + ".attn.k_norm.weight");
+    auto q8w = [&](const std::string &name) {
+        const WInfo &wi = d->w[d->idx.at(name)];
+        Q8W r{nullptr, nullptr};
+        if (wi.q8) {
+            r.q = (const int8_t *) (d->blob + wi.offset);
+            r.d = (const uint16_t *) (d->blob + wi.offset + (size_t) (wi.ne0 * wi.ne1));
+        }
+        return r;
+    };
+    s.qkv_q = q8w(p + ".attn.qkv.weight");
+    if (!pre_only) {
+        s.l1_q = q8w(p + ".linear1.weight");
+        s.fc1_q = q8w(p + ".ffn.fc1.weight");
+        s.fc2_q = q8w(p + ".ffn.fc2.weight");
+    }
     if (!pre_only) {
         s.l1_w = wptr<uint16_t>(d, p + ".linear1.weight");
         s.l1_b = wptr<float>(d, p + ".linear1.bias");
@@ -222,7 +254,10 @@ int validate_cfg(const tsk_dit_config *c) {
     if (c->depth < c->fused_depth || c->depth - c->fused_depth < 1 || c->fused_depth < 0)
         return fail(TSK_ERR_SHAPE, "depth %d / fused_depth %d", c->depth, c->fused_depth);
     if (c->mlp_kind != TSK_MLP_GELU_TANH) return fail(TSK_ERR_UNSUPPORTED, "mlp_kind %d", c->mlp_kind);
-    if (c->weight_type != TSK_TYPE_BF16) return fail(TSK_ERR_UNSUPPORTED, "DiT weights must be BF16");
+    if (c->weight_type != TSK_TYPE_BF16 && c->weight_type != TSK_TYPE_Q8_0)
+        return fail(TSK_ERR_UNSUPPORTED, "DiT weights must be BF16 or Q8_0");
+    if (c->weight_type == TSK_TYPE_Q8_0 && ((c->hidden != 1024 && c->hidden != 2048) || c->mlp_hidden % 128))
+        return fail(TSK_ERR_UNSUPPORTED, "the Q8_0 driver needs hidden 1024 or 2048 and mlp_hidden %% 128 == 0");
     if (c->mlp_hidden % 64 || c->latent_dim % 8 || c->latent_dim < 8 || c->latent_dim > c->hidden || c->text_seq < 1)
         return fail(TSK_ERR_SHAPE, "mlp_hidden %% 64, latent_dim %% 8 and <= hidden");
     if (c->max_batch < 1 || c->max_batch > 32 || c->max_latent < 1) return fail(TSK_ERR_SHAPE, "capacity");
@@ -253,7 +288,8 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     void *bufs[] = {d->sched, d->sched_act, d->sched_jobs,
                     d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
                     d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
-                    d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */};
+                    d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */,
+                    d->qkv32, d->o32, d->h32, d->qx, d->dx};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
     delete d;
@@ -291,7 +327,8 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     size_t off = 0;
     for (auto &wi : d->w) {
         wi.offset = off;
-        off += ((size_t) (wi.ne0 * wi.ne1) * (wi.matrix ? 2 : 4) + 255) & ~(size_t) 255;
+        const size_t bytes = wi.q8 ? tsk_q8_0_split_nbytes(wi.ne0, wi.ne1) : (size_t) (wi.ne0 * wi.ne1) * (wi.matrix ? 2 : 4);
+        off += (bytes + 255) & ~(size_t) 255;
     }
     d->blob_bytes = off;
 
@@ -326,6 +363,16 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->jobs_dev, sizeof(GemvJob) * (nstreams + 3))) ||
         (rc = alloc((void **) &d->freq, sizeof(float) * (H / 2))) ||
         (rc = alloc((void **) &d->rope_cs, sizeof(float) * T * c.head_dim))) {
+        tsk_dit_destroy(d);
+        return rc;
+    }
+    d->q8 = c.weight_type == TSK_TYPE_Q8_0;
+    if (d->q8 &&
+        ((rc = alloc((void **) &d->qkv32, sizeof(float) * rows * 3 * H)) ||
+         (rc = alloc((void **) &d->o32, sizeof(float) * rows * H)) ||
+         (rc = alloc((void **) &d->h32, sizeof(float) * rows * F)) ||
+         (rc = alloc((void **) &d->qx, (size_t) rows * F)) ||
+         (rc = alloc((void **) &d->dx, sizeof(float) * rows * (F / 32))))) {
         tsk_dit_destroy(d);
         return rc;
     }
@@ -412,7 +459,68 @@ extern "C" int tsk_dit_tensor_info(const tsk_dit *d, int i, const char **name, i
     return TSK_OK;
 }
 
-// host f32 -> device (bf16 for matrices), with the (h d j) -> [q|k|v] row permutation
+namespace {
+
+// fp32 -> fp16 bits, round to nearest even (the GGML_FP32_TO_FP16 of a
+// Q8_0 block scale)
+uint16_t host_f16_bits(float f) {
+    const _Float16 h = (_Float16) f;
+    uint16_t b;
+    memcpy(&b, &h, 2);
+    return b;
+}
+
+// Q8_0 blocks [M][K / 32] of 34 bytes -> the driver's planes (int8 [M][K],
+// fp16 d [M][K / 32]) on the device; rows already in the driver's order
+int upload_q8_blocks(tsk_dit *d, const WInfo &wi, const uint8_t *blocks) {
+    const int64_t K = wi.ne0, M = wi.ne1, KB = K / 32;
+    std::vector<uint8_t> planes(tsk_q8_0_split_nbytes(K, M));
+    uint16_t *dp = (uint16_t *) (planes.data() + (size_t) (M * K));
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t kb = 0; kb < KB; ++kb) {
+            const uint8_t *blk = blocks + (m * KB + kb) * 34;
+            memcpy(&dp[m * KB + kb], blk, 2);
+            memcpy(&planes[(size_t) (m * K + kb * 32)], blk + 2, 32);
+        }
+    return hipcheck(hipMemcpy(d->blob + wi.offset, planes.data(), planes.size(), hipMemcpyHostToDevice), "set_tensor copy");
+}
+
+// rows of the (h d j)-interleaved QKV output order -> [q | k | v] blocks:
+// source row 3 i + j -> destination row j H + i (rows of rowbytes bytes)
+std::vector<uint8_t> permute_qkv_rows(const void *src, int H, size_t rowbytes) {
+    std::vector<uint8_t> out((size_t) 3 * H * rowbytes);
+    for (int64_t i = 0; i < H; ++i)
+        for (int j = 0; j < 3; ++j)
+            memcpy(&out[(size_t) (j * H + i) * rowbytes], (const uint8_t *) src + (size_t) (3 * i + j) * rowbytes, rowbytes);
+    return out;
+}
+
+}  // namespace
+
+extern "C" int tsk_dit_tensor_type(const tsk_dit *d, int i) {
+    if (!d || i < 0 || i >= (int) d->w.size()) return fail(TSK_ERR_INVALID_ARG, "tensor index %d", i);
+    const WInfo &wi = d->w[i];
+    return wi.q8 ? TSK_TYPE_Q8_0 : wi.matrix ? TSK_TYPE_BF16 : TSK_TYPE_F32;
+}
+
+extern "C" int tsk_dit_set_tensor_q8_0(tsk_dit *d, const char *name, const void *blocks, size_t nbytes) {
+    if (!d || !name || !blocks) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = d->idx.find(name);
+    if (it == d->idx.end()) return fail(TSK_ERR_INVALID_ARG, "unknown tensor '%s'", name);
+    const WInfo &wi = d->w[it->second];
+    if (!wi.q8) return fail(TSK_ERR_TYPE, "'%s' is not stored as Q8_0 by this driver", name);
+    const size_t rowbytes = (size_t) (wi.ne0 / 32) * 34;
+    if (nbytes != rowbytes * (size_t) wi.ne1)
+        return fail(TSK_ERR_SHAPE, "'%s' has %zu bytes of Q8_0 blocks, got %zu", name, rowbytes * (size_t) wi.ne1, nbytes);
+    if (wi.qkv_perm) {
+        const std::vector<uint8_t> pb = permute_qkv_rows(blocks, d->cfg.hidden, rowbytes);
+        return upload_q8_blocks(d, wi, pb.data());
+    }
+    return upload_q8_blocks(d, wi, (const uint8_t *) blocks);
+}
+
+// host f32 -> device (bf16 for matrices, Q8_0 for the Q8_0 driver's block
+// projections), with the (h d j) -> [q|k|v] row permutation
 extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src, int64_t n) {
     if (!d || !name || !src) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
     auto it = d->idx.find(name);
@@ -432,6 +540,25 @@ extern "C" int tsk_dit_set_tensor(tsk_dit *d, const char *name, const float *src
         s = perm.data();
     }
     char *dst = d->blob + wi.offset;
+    if (wi.q8) {
+        // ggml's reference Q8_0 quantizer (quantize_row_q8_0_ref; the gguf-py
+        // converter's quantize, convert/quantize_gguf.py:41, is bit-identical):
+        // d = amax / 127, q = round-half-away(x / d), d stored as fp16
+        const int64_t K = wi.ne0, M = wi.ne1, KB = K / 32;
+        std::vector<uint8_t> blocks((size_t) (M * KB) * 34);
+        for (int64_t bi = 0; bi < M * KB; ++bi) {
+            const float *x = s + bi * 32;
+            float amax = 0.0f;
+            for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+            const float dd = amax / 127.0f;
+            const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            uint8_t *blk = &blocks[(size_t) bi * 34];
+            const uint16_t h = host_f16_bits(dd);
+            memcpy(blk, &h, 2);
+            for (int j = 0; j < 32; ++j) blk[2 + j] = (uint8_t) (int8_t) roundf(x[j] * id);
+        }
+        return upload_q8_blocks(d, wi, blocks.data());
+    }
     if (!wi.matrix) {
         float a = 0.0f;
         for (int64_t i = 0; i < n; ++i) a = fmaxf(a, fabsf(src[i]));
@@ -474,6 +601,7 @@ struct StreamRun {
     int rope;               // RoPE on q/k (latent stream)
     uint16_t *xn, *h;       // bf16 LN outputs / GELU outputs of this stream
     float *part;            // split-K partials of this stream
+    int64_t row_off;        // first row of this stream in the capacity layout (xn, h, qx, ...)
     // residual update still owed from the previous projection (split-K partials)
     const float *pend_bias = nullptr, *pend_gate = nullptr;
     int64_t pend_ld_gate = 0;   // row stride of the owing block's modulation
@@ -509,13 +637,14 @@ GemmProblem gemm_problem(const void *x, int64_t ld_x, const uint16_t *w, const f
     return q;
 }
 
-// LN + modulate of every stream (paying the residual updates they owe) into xn
+// LN + modulate of every stream (paying the residual updates they owe) into
+// xn (bf16), or into the Q8_0 planes qx / dx for the Q8_0 driver
 int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden;
     LnGroup g;
     memset(&g, 0, sizeof(g));
-    g.nstream = ns; g.H = H; g.eps = c.ln_eps; g.y_f32 = 0;
+    g.nstream = ns; g.H = H; g.eps = c.ln_eps; g.y_mode = d->q8 ? LN_Y_Q8 : LN_Y_BF16;
     double rows = 0.0, pbytes = 0.0;
     for (int i = 0; i < ns; ++i) {
         const StreamW &w = *r[i].w;
@@ -524,6 +653,10 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
         const float *m = mod_of(d, w);
         const float *sh = m + (which ? 3 : 0) * H, *sc = m + (which ? 4 : 1) * H;
         g.s[i] = ln_stream(r[i], B, H, ldm, sh, sc, r[i].xn);
+        if (d->q8) {
+            g.s[i].y = d->qx + r[i].row_off * H;
+            g.s[i].yd = d->dx + r[i].row_off * (H / 32);
+        }
         rows += (double) B * r[i].S;
         pbytes += 4.0 * r[i].pend_split * B * r[i].S * H;
         r[i].pend_split = 0;
@@ -632,6 +765,138 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     return hipcheck(launch_gemm_ks(g2, EPI_PARTIAL, gemm_cfg_for(d, 3, B * r[0].S), st), "fc2 gemm");
 }
 
+// ---- the Q8_0 driver's block projections (weight_type Q8_0): every
+// projection reads Q8_0 planes of f32 activations (ggml_mul_mat's conversion
+// of src1 for a Q8_0 weight) and runs gemm_q8c: exact int32 block sums, fp32
+// rescale and accumulation
+
+GemmParams q8_problem(const tsk_dit *d, const Q8W &w, const StreamRun &r, int B, int K, int M, const float *bias) {
+    GemmParams p;
+    memset(&p, 0, sizeof(p));
+    p.qw = w.q; p.dw = w.d;
+    p.qx = d->qx + r.row_off * K;
+    p.dx = d->dx + r.row_off * (K / 32);
+    p.M = M; p.N = B * r.S; p.K = K;
+    p.bias = bias;
+    p.rows_per_gate = 1;
+    return p;
+}
+
+double q8_bytes(int N, int K, int M, int out_bytes) {
+    return (double) M * K * (1.0 + 2.0 / 32) + (double) N * K * (1.0 + 4.0 / 32) + (double) N * M * out_bytes;
+}
+
+// QKV GEMM into f32 rows, then RMSNorm / RoPE / fp16 scatter into the
+// attention operands
+int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
+    const tsk_dit_config &c = d->cfg;
+    const int H = c.hidden;
+    int rc;
+    for (int i = 0; i < ns; ++i) {
+        GemmParams p = q8_problem(d, r[i].w->qkv_q, r[i], B, H, 3 * H, r[i].w->qkv_b);
+        p.y = d->qkv32 + r[i].row_off * 3 * H;
+        p.ld_y = 3 * H;
+        p.epi = EPI_STORE;
+        Timed tm(d, TSK_ROLE_QKV, 2.0 * p.N * H * 3.0 * H, q8_bytes(p.N, H, 3 * H, 4), st);
+        if ((rc = hipcheck(launch_gemm_q8(p, st), "qkv q8 gemm"))) return rc;
+    }
+    for (int i = 0; i < ns; ++i) {
+        QkvScatter q;
+        memset(&q, 0, sizeof(q));
+        q.qkv = d->qkv32 + r[i].row_off * 3 * H;
+        q.ld = 3 * H;
+        q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
+        q.rope_cs = r[i].rope ? d->rope_cs : nullptr;
+        q.q = d->q; q.k = d->k; q.vt = d->vt; q.ldv = d->ldv;
+        q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope;
+        q.nh = c.n_head; q.rows = B * r[i].S;
+        q.eps = c.qk_eps;
+        q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), as run_qkv
+        const double rows = (double) B * r[i].S;
+        Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * 3 * H, 12.0 * rows * 3 * H, st);
+        if ((rc = hipcheck(launch_qkv_scatter(q, st), "qkv scatter"))) return rc;
+    }
+    return TSK_OK;
+}
+
+// linear1 on the f32 attention output of each stream (quantized per stream),
+// gate_msa * (linear1 + bias) added to the residual in the epilogue
+int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
+    const int H = d->cfg.hidden;
+    int rc;
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        Timed tm(d, TSK_ROLE_OTHER, 3.0 * B * r[i].S * H, 5.125 * B * r[i].S * H, st);
+        if ((rc = hipcheck(launch_quantize_rows_q8(d->o32 + (size_t) r[i].tok_off * H, 1, H, B * r[i].S, H,
+                                                   d->qx + r[i].row_off * H, d->dx + r[i].row_off * (H / 32), st,
+                                                   r[i].S, Ntot),
+                           "linear1 quantize")))
+            return rc;
+    }
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        GemmParams p = q8_problem(d, r[i].w->l1_q, r[i], B, H, H, r[i].w->l1_b);
+        p.epi = EPI_GATE_RES;
+        p.res = r[i].x; p.ld_res = H;
+        p.gate = mod_of(d, *r[i].w) + 2 * H;   // gate_msa
+        p.ld_gate = mod_ld(d, *r[i].w);
+        p.rows_per_gate = r[i].S;
+        Timed tm(d, TSK_ROLE_OUT, 2.0 * p.N * H * H, q8_bytes(p.N, H, H, 8), st);
+        if ((rc = hipcheck(launch_gemm_q8(p, st), "linear1 q8 gemm"))) return rc;
+    }
+    return TSK_OK;
+}
+
+// fc1 (+ GELU, f32 out) of every stream, then per stream the quantize of the
+// GELU output and fc2 with gate_mlp * (fc2 + bias) added to the residual
+int run_mlp_q8(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
+    const int H = d->cfg.hidden, F = d->cfg.mlp_hidden;
+    int rc;
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        GemmParams p = q8_problem(d, r[i].w->fc1_q, r[i], B, H, F, r[i].w->fc1_b);
+        p.y = d->h32 + r[i].row_off * F;
+        p.ld_y = F;
+        p.epi = EPI_GELU;
+        Timed tm(d, TSK_ROLE_FC1, 2.0 * p.N * H * F, q8_bytes(p.N, H, F, 4), st);
+        if ((rc = hipcheck(launch_gemm_q8(p, st), "fc1 q8 gemm"))) return rc;
+    }
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        const int rows = B * r[i].S;
+        {
+            Timed tm(d, TSK_ROLE_OTHER, 3.0 * rows * F, 5.125 * rows * F, st);
+            if ((rc = hipcheck(launch_quantize_rows_q8(d->h32 + r[i].row_off * F, 1, F, rows, F, d->qx + r[i].row_off * F,
+                                                       d->dx + r[i].row_off * (F / 32), st),
+                               "fc2 quantize")))
+                return rc;
+        }
+        GemmParams p = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, r[i].w->fc2_b);
+        p.epi = EPI_GATE_RES;
+        p.res = r[i].x; p.ld_res = H;
+        p.gate = mod_of(d, *r[i].w) + 5 * H;   // gate_mlp
+        p.ld_gate = mod_ld(d, *r[i].w);
+        p.rows_per_gate = r[i].S;
+        Timed tm(d, TSK_ROLE_FC2, 2.0 * p.N * H * F, q8_bytes(p.N, F, H, 8), st);
+        if ((rc = hipcheck(launch_gemm_q8(p, st), "fc2 q8 gemm"))) return rc;
+    }
+    return TSK_OK;
+}
+
+int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream_t st);
+
+// one block of the Q8_0 driver over the streams r[0..ns)
+int block_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
+    int rc;
+    if ((rc = run_ln(d, r, ns, B, 0, st))) return rc;
+    if ((rc = run_qkv_q8(d, r, ns, B, Ntot, st))) return rc;
+    if ((rc = attention(d, r, ns, B, Ntot, st))) return rc;
+    if ((rc = run_out_q8(d, r, ns, B, Ntot, st))) return rc;
+    const int nmlp = ns == 2 && r[1].w->pre_only ? 1 : ns;
+    if ((rc = run_ln(d, r, nmlp, B, 1, st))) return rc;
+    return run_mlp_q8(d, r, nmlp, B, st);
+}
+
 // Attention over the concatenated q/k/vt of the streams in r[0..ns). q was
 // written pre-multiplied by scale * log2(e) (run_qkv). q and k are RMS-normed
 // (|x / rms(x)| = 8 for 64 dims) times w, and RoPE is a rotation, so every
@@ -642,15 +907,18 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     const tsk_dit_config &c = d->cfg;
     AttnFastParams p;
     memset(&p, 0, sizeof(p));
-    p.q = d->q; p.k = d->k; p.vt = d->vt; p.o = d->o;
-    p.q_type = TSK_TYPE_F16; p.k_bf16 = 0; p.out_bf16 = 1;
+    // Q8_0 driver: f32 output, which linear1 quantizes to Q8_0 (the flash
+    // attention node's F32 result, src/mmdit.cpp:91-93)
+    const int es = d->q8 ? 4 : 2;
+    p.q = d->q; p.k = d->k; p.vt = d->vt; p.o = d->q8 ? (void *) d->o32 : (void *) d->o;
+    p.q_type = TSK_TYPE_F16; p.k_bf16 = 0; p.out_bf16 = d->q8 ? 0 : 1;
     p.Nq = p.Nkv = Ntot; p.H = c.n_head; p.B = B;
     p.q_nb1 = p.k_nb1 = 128;
     p.q_nb2 = p.k_nb2 = (int64_t) 128 * Ntot;
     p.q_nb3 = p.k_nb3 = (int64_t) 128 * Ntot * c.n_head;
     p.vt_bh = (int64_t) 64 * d->ldv;
     p.ldv = d->ldv;
-    p.o_nb1 = 128; p.o_nb2 = (int64_t) 2 * c.hidden; p.o_nb3 = (int64_t) 2 * c.hidden * Ntot;
+    p.o_nb1 = 64 * es; p.o_nb2 = (int64_t) es * c.hidden; p.o_nb3 = (int64_t) es * c.hidden * Ntot;
     p.c = 1.4426950408889634f / sqrtf((float) c.head_dim);
     p.q_prescaled = 1;
     float aq = 0.0f, ak = 0.0f;
@@ -748,9 +1016,10 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, bool latent_cm
     const size_t cap = (size_t) c.max_batch * c.max_latent;
     StreamRun L, X;
     L.w = nullptr; L.x = d->lat; L.S = T; L.tok_off = 0; L.rope = 1;
-    L.xn = d->xn; L.h = d->h; L.part = d->part;
+    L.xn = d->xn; L.h = d->h; L.part = d->part; L.row_off = 0;
     X.w = nullptr; X.x = d->txt; X.S = St; X.tok_off = T; X.rope = 0;
     X.xn = d->xn + cap * H; X.h = d->h + cap * c.mlp_hidden; X.part = d->part + (size_t) KSPLIT_MAX * cap * H;
+    X.row_off = (int64_t) cap;
     // joint blocks: LN -> QKV (+RMSNorm/RoPE/F16 epilogue) -> attention over the
     // concatenated tokens -> linear1 (split-K) -> residual + LN -> fc1 (+GELU)
     // -> fc2 (split-K, residual paid by the next LN); both streams per launch
@@ -760,6 +1029,12 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, bool latent_cm
         L.w = &d->joint_lat[i];
         X.w = &d->joint_txt[i];
         StreamRun r2[2] = {L, X};
+        if (d->q8) {
+            if ((rc = block_q8(d, r2, 2, B, Nj, st))) return rc;
+            L = r2[0];
+            X = r2[1];
+            continue;
+        }
         if ((rc = run_ln(d, r2, 2, B, 0, st))) return rc;
         if ((rc = run_qkv(d, r2, 2, B, Nj, st))) return rc;
         if ((rc = attention(d, r2, 2, B, Nj, st))) return rc;
@@ -774,6 +1049,10 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, bool latent_cm
     if ((rc = join())) return rc;
     for (int i = 0; i < c.fused_depth; ++i) {
         L.w = &d->fused[i];
+        if (d->q8) {
+            if ((rc = block_q8(d, &L, 1, B, T, st))) return rc;
+            continue;
+        }
         if ((rc = run_ln(d, &L, 1, B, 0, st))) return rc;
         if ((rc = run_qkv(d, &L, 1, B, T, st))) return rc;
         if ((rc = attention(d, &L, 1, B, T, st))) return rc;
@@ -787,7 +1066,7 @@ int forward_impl(tsk_dit *d, int B, int T, const float *latent_d, bool latent_cm
         const float *fmod = d->cur_sched ? d->cur_sched + d->sched_final : d->final_mod;
         LnGroup g;
         memset(&g, 0, sizeof(g));
-        g.nstream = 1; g.H = H; g.eps = c.ln_eps; g.y_f32 = 1;
+        g.nstream = 1; g.H = H; g.eps = c.ln_eps; g.y_mode = LN_Y_F32;
         g.s[0] = ln_stream(L, B, H, d->cur_sched ? 0 : 2 * H, fmod, fmod + H, d->xf);
         Timed tm(d, TSK_ROLE_OTHER, 10.0 * B * T * H, 16.0 * B * T * H + 4.0 * L.pend_split * B * T * H, st);
         if ((e = launch_ln_group(g, st)) != hipSuccess) return hip_fail(e, "final ln");

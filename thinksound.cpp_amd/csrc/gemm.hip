@@ -543,21 +543,26 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
 // ------------------------------------------------------------------ activation quantization
 // One thread per 32-block: d = amax/127 (stored as the fp32 value of its fp16
 // rounding), q = rne(x * (127/amax)) — ggml-cpu's x86 quantize_row_q8_0.
+// Row n of the output reads source row (n / grp) * gstride + n % grp (grp
+// > 0: rows gathered from a grouped layout, e.g. one stream's tokens of every
+// batch item in [B][Ntot] rows), else row n.
 template <bool XF32>
-__global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int K, int8_t *qx, float *dx) {
+__global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int K, int8_t *qx, float *dx, int grp,
+                                        int64_t gstride) {
     const int KB = K / 32;
     const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (blk >= (int64_t) N * KB) return;
     const int row = (int) (blk / KB), kb = (int) (blk % KB);
+    const int64_t src = grp > 0 ? (int64_t) (row / grp) * gstride + row % grp : row;
     float v[32];
     if constexpr (XF32) {
-        const float *xr = (const float *) x + (int64_t) row * ld_x + kb * 32;
+        const float *xr = (const float *) x + src * ld_x + kb * 32;
         for (int j = 0; j < 32; j += 4) {
             f32x4 t = *(const f32x4 *) (xr + j);
             v[j] = t[0]; v[j + 1] = t[1]; v[j + 2] = t[2]; v[j + 3] = t[3];
         }
     } else {
-        const uint16_t *xr = (const uint16_t *) x + (int64_t) row * ld_x + kb * 32;
+        const uint16_t *xr = (const uint16_t *) x + src * ld_x + kb * 32;
         for (int j = 0; j < 32; ++j) v[j] = bf16_bits_to_f32(xr[j]);
     }
     float amax = 0.0f;
@@ -697,13 +702,13 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     return p.y_bf16 ? gemm_q8_epi<2, 2, 2, 2, true>(p, s) : gemm_q8_epi<2, 2, 2, 2, false>(p, s);
 }
 
-hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K,
-                                   int8_t *qx, float *dx, hipStream_t s) {
+hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K, int8_t *qx, float *dx,
+                                   hipStream_t s, int grp, int64_t gstride) {
     const int64_t nblk = (int64_t) N * (K / 32);
     const int threads = 256;
     dim3 grid((unsigned) ((nblk + threads - 1) / threads));
-    if (x_f32) launch_kernel(quantize_rows_q8_kernel<true>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
-    else launch_kernel(quantize_rows_q8_kernel<false>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx);
+    if (x_f32) launch_kernel(quantize_rows_q8_kernel<true>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx, grp, gstride);
+    else launch_kernel(quantize_rows_q8_kernel<false>, grid, dim3(threads), 0, s, x, ld_x, N, K, qx, dx, grp, gstride);
     return hipGetLastError();
 }
 

@@ -357,10 +357,12 @@ extern "C" int tsk_t5_config_from_gguf(const tsk_gguf *g, tsk_t5_config *c) {
     return TSK_OK;
 }
 
-// every DiT weight by name, converted to f32 on the host (F32 / F16 / BF16
-// exactly) and handed to tsk_dit_set_tensor, which rounds matrices to the
-// driver's BF16. A Q8_0 matrix is refused: rounding bf16(fp32(d) * q) would
-// not run the Q8_0 x Q8_0 products a Q8_0 DiT file asks for.
+// every DiT weight by name: Q8_0 tensors the driver stores as Q8_0 bit for
+// bit; others converted to f32 on the host (F32 / F16 / BF16 exactly) and
+// handed to tsk_dit_set_tensor, which rounds matrices to the driver's BF16 (or
+// quantizes the Q8_0 driver's block projections). A Q8_0 tensor the driver
+// stores otherwise is refused: bf16(fp32(d) * q) would not run the
+// Q8_0 x Q8_0 products the file asks for.
 extern "C" int tsk_dit_load_gguf(tsk_dit *dit, const tsk_gguf *g) {
     if (!dit || !g) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
     std::vector<float> buf;
@@ -375,8 +377,15 @@ extern "C" int tsk_dit_load_gguf(tsk_dit *dit, const tsk_gguf *g) {
             return fail(TSK_ERR_SHAPE, "GGUF tensor '%s' is [%lld, %lld], the driver needs [%lld, %lld]", name,
                         (long long) ti->ne[0], (long long) (ti->ne[1] * ti->ne[2] * ti->ne[3]), (long long) ne[0],
                         (long long) ne[1]);
-        if (ti->type == TSK_TYPE_Q8_0)
-            return fail(TSK_ERR_TYPE, "GGUF tensor '%s' is Q8_0: this DiT driver runs BF16 weights", name);
+        const int dtype = tsk_dit_tensor_type(dit, i);
+        if (ti->type == TSK_TYPE_Q8_0) {
+            if (dtype != TSK_TYPE_Q8_0)
+                return fail(TSK_ERR_TYPE, "GGUF tensor '%s' is Q8_0: this DiT driver stores it as type %d", name, dtype);
+            std::vector<uint8_t> raw((size_t) (ne[0] / 32) * 34 * (size_t) ne[1]);
+            if ((rc = tsk_gguf_read_tensor(g, name, 0, raw.data(), raw.size()))) return rc;
+            if ((rc = tsk_dit_set_tensor_q8_0(dit, name, raw.data(), raw.size()))) return rc;
+            continue;
+        }
         buf.resize((size_t) (ne[0] * ne[1]));
         if ((rc = tsk_gguf_read_tensor(g, name, 1, buf.data(), buf.size() * 4))) return rc;
         if ((rc = tsk_dit_set_tensor(dit, name, buf.data(), (int64_t) buf.size()))) return rc;

@@ -349,7 +349,13 @@ __global__ __launch_bounds__(256) void ln_group_kernel(const LnGroup g) {
 // row (residual, split slices, bias, gate, shift, scale) is issued before the
 // first reduction, and both reductions stay inside the wave (no LDS, no
 // barrier).
-template <bool YF32, int NV>
+// YM: LN_Y_BF16 / LN_Y_F32 rows, or LN_Y_Q8 -- the row quantized to Q8_0
+// planes (int8 st.y [rows][H], f32 scales st.yd [rows][H / 32]) as
+// quantize_rows_q8_kernel quantizes an f32 row: the 32-element block of
+// element (lane + 64 j) * 4 + e is held by lanes 8 (b % 8) .. + 7 at register
+// j, so its amax is three DPP steps (the conversion ggml_mul_mat applies to
+// src1 for a Q8_0 weight).
+template <int YM, int NV>
 __device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps) {
     constexpr int H = 256 * NV;
     const int lane = threadIdx.x, b = r / st.rows_per_b;
@@ -400,7 +406,20 @@ __device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps
         const int i = (lane + 64 * j) * 4;
         float o[4];
         for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mean) * rs * (scv[j][e] + 1.0f) + shv[j][e];
-        if constexpr (YF32) {
+        if constexpr (YM == LN_Y_Q8) {
+            float amax = 0.0f;
+            for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(o[e]));
+#pragma unroll
+            for (int k = 0; k < 3; ++k) amax = fmaxf(amax, dpp_f(amax, k));   // the 8 lanes of the block
+            const float d = amax / 127.0f;
+            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            if ((lane & 7) == 0) st.yd[(int64_t) r * (H / 32) + 8 * j + (lane >> 3)] = f16_bits_to_f32(f32_to_f16_bits(d));
+            int8_t q[4];
+            for (int e = 0; e < 4; ++e) q[e] = (int8_t) __builtin_rintf(o[e] * id);
+            uint32_t w4;
+            __builtin_memcpy(&w4, q, 4);
+            *(uint32_t *) ((int8_t *) st.y + (int64_t) r * st.ld_y + i) = w4;
+        } else if constexpr (YM == LN_Y_F32) {
             *(f32x4 *) ((float *) st.y + (int64_t) r * st.ld_y + i) = f32x4{o[0], o[1], o[2], o[3]};
         } else {
             uint16_t ob[4];
@@ -412,11 +431,11 @@ __device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps
     }
 }
 
-template <bool YF32, int NV>
+template <int YM, int NV>
 __global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
     const int r = blockIdx.x;
-    if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YF32, NV>(g.s[1], r - g.s[0].rows, g.eps);
-    else ln_wave_row<YF32, NV>(g.s[0], r, g.eps);
+    if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YM, NV>(g.s[1], r - g.s[0].rows, g.eps);
+    else ln_wave_row<YM, NV>(g.s[0], r, g.eps);
 }
 
 // GEMV list: one wave per output row; lane k-slices of 8, f32 activations
@@ -807,12 +826,19 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
-    if (g.H == 1024 && !tuning().ln_block) {
-        if (g.y_f32) launch_kernel(ln_wave_kernel<true, 4>, dim3(rows), dim3(64), 0, s, g);
-        else launch_kernel(ln_wave_kernel<false, 4>, dim3(rows), dim3(64), 0, s, g);
+    if (g.y_mode == LN_Y_Q8) {
+        // Q8_0 output: the wave kernel only (H = 1024 or 2048)
+        if (g.H == 1024) launch_kernel(ln_wave_kernel<LN_Y_Q8, 4>, dim3(rows), dim3(64), 0, s, g);
+        else if (g.H == 2048) launch_kernel(ln_wave_kernel<LN_Y_Q8, 8>, dim3(rows), dim3(64), 0, s, g);
+        else return hipErrorInvalidValue;
         return hipGetLastError();
     }
-    if (g.y_f32) launch_kernel(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
+    if (g.H == 1024 && !tuning().ln_block) {
+        if (g.y_mode == LN_Y_F32) launch_kernel(ln_wave_kernel<LN_Y_F32, 4>, dim3(rows), dim3(64), 0, s, g);
+        else launch_kernel(ln_wave_kernel<LN_Y_BF16, 4>, dim3(rows), dim3(64), 0, s, g);
+        return hipGetLastError();
+    }
+    if (g.y_mode == LN_Y_F32) launch_kernel(ln_group_kernel<true>, dim3(rows), dim3(256), 0, s, g);
     else launch_kernel(ln_group_kernel<false>, dim3(rows), dim3(256), 0, s, g);
     return hipGetLastError();
 }
@@ -858,6 +884,45 @@ __global__ void transpose_ct_kernel(const float *x, int B, int C, int T, float *
     if (i >= (int64_t) B * C * T) return;
     const int t = (int) (i % T), c = (int) ((i / T) % C), b = (int) (i / ((int64_t) T * C));
     y[((int64_t) b * T + t) * C + c] = x[i];
+}
+
+// one wave per (row, head): lane d holds dimension d of q, k and v
+__global__ __launch_bounds__(256) void qkv_scatter_kernel(const QkvScatter p) {
+    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= (int64_t) p.rows * p.nh) return;
+    const int lane = threadIdx.x & 63;
+    const int n = (int) (w / p.nh), h = (int) (w % p.nh);
+    const int H = p.nh * 64, b = n / p.seq, s = n % p.seq, tok = p.tok_off + s;
+    const float *row = p.qkv + (int64_t) n * p.ld + h * 64 + lane;
+    float x[3] = {row[0], row[H], row[2 * H]};
+    const float wv[2] = {p.qn_w[lane], p.kn_w[lane]};
+    float cs[2] = {1.0f, 0.0f};
+    if (p.rope) {
+        cs[0] = p.rope_cs[(int64_t) s * 64 + (lane & ~1)];
+        cs[1] = p.rope_cs[(int64_t) s * 64 + (lane | 1)];
+    }
+    const int64_t bh = (int64_t) b * p.nh + h;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const float sc = 1.0f / sqrtf(wave_sum(x[t] * x[t]) / 64.0f + p.eps);
+        float y = x[t] * sc * wv[t];
+        if (p.rope) {
+            // adjacent pair (2 i, 2 i + 1): the partner is lane ^ 1
+            const float o = dpp_f(y, 0);
+            y = (lane & 1) ? o * cs[1] + y * cs[0] : y * cs[0] - o * cs[1];
+        }
+        if (t == 0) y *= p.q_scale;
+        uint16_t *dst = t == 0 ? p.q : p.k;
+        dst[(bh * p.Ntot + tok) * 64 + lane] = f32_to_f16_bits(y);
+    }
+    p.vt[(bh * 64 + lane) * p.ldv + vt_pos(tok)] = f32_to_f16_bits(x[2]);
+}
+
+hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s) {
+    if (p.rows < 1 || p.nh < 1 || p.seq < 1) return hipErrorInvalidValue;
+    const int64_t waves = (int64_t) p.rows * p.nh;
+    launch_kernel(qkv_scatter_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_proj_f32_cm(const uint16_t *w, const float *bias, const float *x, int T, int N, int K, int M,

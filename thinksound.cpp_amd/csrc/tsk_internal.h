@@ -204,9 +204,25 @@ inline int64_t tiled_index(int64_t m, int64_t k, int64_t K) {
 }
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s);
 // Activation quantization to planes for launch_gemm_q8 (ggml-cpu x86 rounding).
-// x rows of K (f32 or bf16, row stride ld_x elements).
+// x rows of K (f32 or bf16, row stride ld_x elements); grp > 0 gathers output
+// row n from source row (n / grp) * gstride + n % grp.
 hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K,
-                                   int8_t *qx, float *dx, hipStream_t s);
+                                   int8_t *qx, float *dx, hipStream_t s, int grp = 0, int64_t gstride = 0);
+// The QKV epilogue of the BF16 block GEMMs as a kernel over f32 rows (the
+// Q8_0 driver's QKV GEMM stores them): row n = b * seq + s of qkv [rows][3 H]
+// ([q | k | v] head-major, bias included) -> RMSNorm(eps) * w on q and k,
+// RoPE on q and k from rope_cs (when rope), q * q_scale, fp16 into q / k
+// [B][nh][Ntot][64] at token tok_off + s and into V^T [B][nh][64][ldv] at
+// vt_pos(tok_off + s).
+struct QkvScatter {
+    const float *qkv;
+    int64_t ld;
+    const float *qn_w, *kn_w, *rope_cs;
+    uint16_t *q, *k, *vt;
+    int ldv, seq, Ntot, tok_off, rope, nh, rows;
+    float eps, q_scale;
+};
+hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s);
 
 // ---------------------------------------------------------------- small ops
 // generic 4-D strided views used by the C-ABI element-wise entry points
@@ -240,7 +256,8 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 // Residual update + LayerNorm + modulate for up to two streams in one launch.
 // Row r of a stream (b = r / rows_per_b):
 //   if part: x[r] += gate[b * ld_gate] * (sum_{s < nsplit} part[s * part_stride + r * H] + bias)
-//   y[r] = LN(x[r], eps) * (1 + scale[b]) + shift[b]   (bf16, or f32 when y_f32)
+//   y[r] = LN(x[r], eps) * (1 + scale[b]) + shift[b]   (bf16, f32, or Q8_0 planes: y_mode)
+enum LnOut : int { LN_Y_BF16 = 0, LN_Y_F32 = 1, LN_Y_Q8 = 2 };
 struct LnStream {
     float *x;                     // f32 rows of H (in/out), row stride ld_x
     int64_t ld_x;
@@ -252,13 +269,14 @@ struct LnStream {
     int64_t ld_gate;
     const float *shift, *scale;   // [B][ld_mod]
     int64_t ld_mod;
-    void *y;                      // output rows, row stride ld_y
+    void *y;                      // output rows, row stride ld_y (LN_Y_Q8: int8 planes)
     int64_t ld_y;
+    float *yd;                    // LN_Y_Q8: f32 block scales [rows][H / 32]
     int rows, rows_per_b;
 };
 struct LnGroup {
     LnStream s[2];
-    int nstream, H, y_f32;
+    int nstream, H, y_mode;       // LnOut
     float eps;
 };
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s);

@@ -12,6 +12,8 @@ path: if libtsk.so is missing, load() raises.
 import ctypes
 import os
 
+import numpy as np
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libtsk.so")
 
@@ -120,6 +122,8 @@ def load():
         "tsk_dit_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p),
                                  ctypes.POINTER(ctypes.c_int64)], i),
         "tsk_dit_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_dit_set_tensor_q8_0": ([vp, ctypes.c_char_p, vp, ctypes.c_size_t], i),
+        "tsk_dit_tensor_type": ([vp, i], i),
         "tsk_dit_forward": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_forward_device": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_sample": ([vp, i, vp, vp, vp, i, f, vp, vp, vp], i),
@@ -700,7 +704,18 @@ class Dit:
 
     def set_tensor(self, name, host_f32):
         """host_f32: contiguous numpy float32 array."""
+        host_f32 = np.ascontiguousarray(host_f32, dtype=np.float32)
         check(load().tsk_dit_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
+
+    def set_tensor_q8_0(self, name, blocks):
+        """ggml Q8_0 blocks (uint8, 34 bytes per 32 values) of a Q8_0 block projection."""
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        check(load().tsk_dit_set_tensor_q8_0(self.h, name.encode(), blocks.ctypes.data, blocks.nbytes))
+
+    def tensor_types(self):
+        """{name: stored type id} (BF16 / Q8_0 / F32)"""
+        L = load()
+        return {nm: L.tsk_dit_tensor_type(self.h, k_) for k_, (nm, _) in enumerate(self.tensors())}
 
     def forward(self, latent, t, text):
         """ts_dit::forward layouts, host numpy arrays: latent (B, L, T) (ggml ne =
