@@ -20,6 +20,9 @@
  *   tsk_conv_mlp_swiglu <- convmlp                             src/mmdit.cpp:39-44
  *   tsk_mlp_swiglu      <- mlp                                 src/mmdit.cpp:47-52
  *   tsk_dit_*           <- ts_dit::load / forward / sample     src/mmdit.h:9-42
+ *                          (the benchmarked two-stream block shape)
+ *   tsk_mmdit_*         <- ts_dit::forward / sample, the reference's own
+ *                          three-stream graph                   src/mmdit.cpp:119-376
  *   tsk_t5_attention    <- mul_mat(k,q) + bias + pad -> soft_max -> mul_mat
  *                                                              src/t5_encoder.cpp:68-73
  *   tsk_t5_*            <- ts_t5::load / encode                src/t5_encoder.cpp:28-104
@@ -533,6 +536,91 @@ enum tsk_dit_role {
 int  tsk_dit_timing(tsk_dit *dit, int enable);
 int  tsk_dit_timing_read(tsk_dit *dit, int role, double *ms, int64_t *launches,
                          double *flop, double *bytes);
+
+/* ---- The reference's MM-DiT graph (ts_dit, src/mmdit.h:9-42) -------------
+ * ts_dit::forward / ts_dit::sample as src/mmdit.cpp:119-376 builds them:
+ * three streams (latent | clip | text) in 7 joint blocks, 14 fused blocks on
+ * the latent, k3 convolutions (linear1, SwiGLU convMLP) on the latent and clip
+ * streams, SwiGLU MLPs on text, per-token adaLN from extended_c (the sync
+ * features interpolated to T plus global_c) on the latent stream and from
+ * global_c on clip / text, a 154-token text stream (text_f padded to t5_dim
+ * and concatenated with the T5 features), a k7 output convolution. Weights
+ * by the converter's names (convert/convert_thinksound.py:32) in the types of
+ * the BF16 GGUF (convert/quantize_gguf.py --type bf16): BF16 2-D / 3-D
+ * weights, F32 for the t_embed MLP, sync_pos_emb, the learned empties and
+ * every vector. Each BF16 product rounds its input to bf16 (ggml_mul_mat's
+ * src1 conversion); K / V are F16 in the attention (mmdit.cpp:89-90). */
+typedef struct tsk_mmdit tsk_mmdit;
+
+typedef struct tsk_mmdit_config {
+    int   hidden;        /* 1024 (dit.hidden_dim)  */
+    int   n_head;        /* 16   (head_dim 64)     */
+    int   head_dim;      /* 64   */
+    int   depth;         /* 21   */
+    int   fused_depth;   /* 14   */
+    int   latent_dim;    /* 64   */
+    int   text_seq;      /* 77   (the text stream holds 2 text_seq tokens) */
+    int   clip_dim;      /* 1024 */
+    int   sync_dim;      /* 768  */
+    int   t5_dim;        /* 2048 (text_f is zero-padded to this width, mmdit.cpp:179) */
+    int   mlp_hidden;    /* 2816 (SwiGLU width of every MLP) */
+    int   max_batch;     /* capacity: batch rows per forward (2 for CFG) */
+    int   max_latent;    /* capacity: latent tokens T         */
+    int   max_clip;      /* capacity: clip frames             */
+    int   max_sync;      /* capacity: sync frames (multiple of 8) */
+    float rope_theta;    /* 10000 */
+    float t_max_period;  /* 1     */
+} tsk_mmdit_config;
+
+/* the reference's sizes (mmdit.h:17-22) and capacities for 30 s clips */
+void tsk_mmdit_default_config(tsk_mmdit_config *cfg);
+int  tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out);
+void tsk_mmdit_destroy(tsk_mmdit *m);
+int  tsk_mmdit_n_tensors(const tsk_mmdit *m);
+/* name and ggml ne of tensor i: linear [in, out], conv [KW, IC, OC] */
+int  tsk_mmdit_tensor_info(const tsk_mmdit *m, int i, const char **name, int64_t ne[4]);
+/* the type the driver holds tensor i in: TSK_TYPE_BF16 or TSK_TYPE_F32 */
+int  tsk_mmdit_tensor_type(const tsk_mmdit *m, int i);
+/* Upload one weight from HOST f32 values in ggml / PyTorch memory order
+ * (linear [out][in], conv [OC][IC][KW]); BF16 tensors are rounded RNE. */
+int  tsk_mmdit_set_tensor(tsk_mmdit *m, const char *name, const float *host_f32, int64_t n);
+/*
+ * One flow evaluation for B (<= max_batch) rows, all pointers HOST, each
+ * per-row block in the layout ts_dit::forward takes (src/mmdit.h:26-29,
+ * src/mmdit.cpp:138-143), the batch outermost:
+ *   latent ne = [T, latent_dim, B], t [B], clip_f ne = [clip_dim, clip_S, B],
+ *   sync_f ne = [sync_dim, sync_S, B] (sync_S a multiple of 8),
+ *   text_f ne = [clip_dim, text_seq, B], t5 ne = [t5_dim, text_seq, B],
+ *   global_text ne = [clip_dim, B]  ->  flow ne = [latent_dim, T, B].
+ */
+int  tsk_mmdit_forward(tsk_mmdit *m, int B, int T, const float *latent, const float *t, int clip_S,
+                       const float *clip_f, int sync_S, const float *sync_f, const float *text_f,
+                       const float *t5, const float *global_text, float *flow, tsk_stream stream);
+/*
+ * Stage outputs (the dbg map of ts_dit::forward, src/mmdit.cpp:125, :333-336).
+ * With tsk_mmdit_debug(m, 1) every forward keeps, in host memory, the
+ * tensors the reference names x_in, t_emb, clip_pp, text_pp, clip_fc,
+ * text_fc, gcmlp, global_c, extended_c, jb0_lat, jb0_clip, jb0_text (after
+ * joint block 0; needs a fused block or a second joint block), after_joint,
+ * after_fused: f32, ggml [H, S, B] (C order [B][S][H]). Each capture
+ * synchronises the stream: a debugging aid, not for timed runs.
+ * tsk_mmdit_debug_size returns the element count (negative status if the
+ * last forward kept no such stage).
+ */
+int     tsk_mmdit_debug(tsk_mmdit *m, int enable);
+int64_t tsk_mmdit_debug_size(const tsk_mmdit *m, const char *name);
+int     tsk_mmdit_debug_get(const tsk_mmdit *m, const char *name, float *out, int64_t n);
+/*
+ * ts_dit::sample (src/mmdit.cpp:344-376): `steps` Euler steps of rectified
+ * flow with CFG; each step runs the conditional and the unconditional
+ * forward (empty_string_feat, empty_t5_feat, zero global text) as one B = 2
+ * forward. HOST pointers in ts_dit::sample's layouts: noise / out ne =
+ * [T, latent_dim]; flow0 (nullable) ne = [T, latent_dim], the CFG velocity of
+ * step 0. Needs max_batch >= 2.
+ */
+int  tsk_mmdit_sample(tsk_mmdit *m, int T, const float *noise, int clip_S, const float *clip_f, int sync_S,
+                      const float *sync_f, const float *text_f, const float *t5, const float *global_text,
+                      int steps, float cfg_scale, float *out, float *flow0, tsk_stream stream);
 
 #ifdef __cplusplus
 }

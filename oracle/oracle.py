@@ -38,6 +38,13 @@ class DitConfig(ctypes.Structure):
         [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
 
 
+class MMDitConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
+        "sync_dim", "t5_dim", "mlp_hidden", "max_batch", "max_latent", "max_clip", "max_sync")] + \
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")]
+
+
 _lib = None
 
 
@@ -108,6 +115,20 @@ def lib():
         L.orc_conv1d.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P]
         L.orc_swiglu.argtypes = [vp, vp, vp, ctypes.c_int64]
         L.orc_conv_mlp_swiglu.argtypes = [P, P, P, P, P]
+        L.orc_mmdit_create.argtypes = [ctypes.POINTER(MMDitConfig)]
+        L.orc_mmdit_create.restype = vp
+        L.orc_mmdit_destroy.argtypes = [vp]
+        L.orc_mmdit_n_tensors.argtypes = [vp]
+        L.orc_mmdit_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+                                            ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int)]
+        L.orc_mmdit_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
+        L.orc_mmdit_forward.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp, ctypes.c_int, vp,
+                                        vp, vp, vp, vp, ctypes.c_int, ctypes.c_int]
+        L.orc_mmdit_stage_size.argtypes = [vp, ctypes.c_char_p]
+        L.orc_mmdit_stage_size.restype = ctypes.c_int64
+        L.orc_mmdit_stage.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
+        L.orc_mmdit_sample.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, vp, ctypes.c_int, vp, vp, vp, vp,
+                                       ctypes.c_int, ctypes.c_float, vp, vp, ctypes.c_int, ctypes.c_int]
         L.orc_mlp_swiglu.argtypes = [P, P, P, P, P]
         _lib = L
     return _lib
@@ -410,6 +431,81 @@ class OracleDiT:
                                   text_uncond.ctypes.data, steps, cfg_scale, out.ctypes.data,
                                   flow0.ctypes.data, int(act_bf16), int(kv_f16))
         assert rc == 0
+        return out, flow0
+
+
+# ---------------------------------------------------------------- the reference's MM-DiT graph
+def mmdit_config(**kw):
+    """the reference's sizes (src/mmdit.h:17-22) with capacities for 30 s"""
+    c = MMDitConfig(hidden=1024, n_head=16, head_dim=64, depth=21, fused_depth=14, latent_dim=64, text_seq=77,
+                    clip_dim=1024, sync_dim=768, t5_dim=2048, mlp_hidden=2816, max_batch=2, max_latent=646,
+                    max_clip=240, max_sync=720, rope_theta=10000.0, t_max_period=1.0)
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+class OracleMMDiT:
+    """ts_dit::forward / ::sample restated (tsk_oracle_mmdit.c). Arrays in
+    numpy C order of the ggml layouts: latent (B, L, T), clip (B, S_c, clip_dim),
+    sync (B, S_s, sync_dim), text (B, 77, clip_dim), t5 (B, 77, t5_dim),
+    g (B, clip_dim) -> flow (B, T, L)."""
+
+    def __init__(self, cfg):
+        self.cfg = cfg
+        self.h = lib().orc_mmdit_create(ctypes.byref(cfg))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_mmdit_destroy(self.h)
+            self.h = None
+
+    def tensors(self):
+        """[(name, ggml ne (3), type)]"""
+        out = []
+        for i in range(lib().orc_mmdit_n_tensors(self.h)):
+            nm, ne, ty = ctypes.c_char_p(), (ctypes.c_int64 * 3)(), ctypes.c_int()
+            assert lib().orc_mmdit_tensor_info(self.h, i, ctypes.byref(nm), ne, ctypes.byref(ty)) == 0
+            out.append((nm.value.decode(), tuple(ne), ty.value))
+        return out
+
+    def set_tensor(self, name, arr):
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        rc = lib().orc_mmdit_set_tensor(self.h, name.encode(), arr.ctypes.data, arr.size)
+        assert rc == 0, (name, rc)
+
+    @staticmethod
+    def _c(a):
+        return np.ascontiguousarray(a, dtype=np.float32)
+
+    def forward(self, latent, t, clip, sync, text, t5, g, act_bf16=True, kv_f16=True):
+        latent, t, clip, sync, text, t5, g = (self._c(a) for a in (latent, t, clip, sync, text, t5, g))
+        B, L, T = latent.shape
+        flow = np.empty((B, T, L), dtype=np.float32)
+        rc = lib().orc_mmdit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data, clip.shape[1],
+                                     clip.ctypes.data, sync.shape[1], sync.ctypes.data, text.ctypes.data,
+                                     t5.ctypes.data, g.ctypes.data, flow.ctypes.data, int(act_bf16), int(kv_f16))
+        assert rc == 0, rc
+        return flow
+
+    def stage(self, name):
+        """a stage output of the last forward (flat, batch rows concatenated)"""
+        n = lib().orc_mmdit_stage_size(self.h, name.encode())
+        assert n >= 0, name
+        out = np.empty(n, np.float32)
+        assert lib().orc_mmdit_stage(self.h, name.encode(), out.ctypes.data, n) == 0
+        return out
+
+    def sample(self, noise, clip, sync, text, t5, g, steps=24, cfg_scale=5.0, act_bf16=True, kv_f16=True):
+        """noise / out / flow0 (L, T)"""
+        noise, clip, sync, text, t5, g = (self._c(a) for a in (noise, clip, sync, text, t5, g))
+        L, T = noise.shape
+        out = np.empty((L, T), dtype=np.float32)
+        flow0 = np.empty((L, T), dtype=np.float32)
+        rc = lib().orc_mmdit_sample(self.h, T, noise.ctypes.data, clip.shape[0], clip.ctypes.data, sync.shape[0],
+                                    sync.ctypes.data, text.ctypes.data, t5.ctypes.data, g.ctypes.data, steps,
+                                    cfg_scale, out.ctypes.data, flow0.ctypes.data, int(act_bf16), int(kv_f16))
+        assert rc == 0, rc
         return out, flow0
 
 

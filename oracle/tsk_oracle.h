@@ -107,6 +107,31 @@ int      orc_dit_sample(orc_dit *d, int T, const float *noise, const float *text
                         const float *text_uncond, int steps, float cfg_scale, float *out,
                         float *flow0, int act_bf16, int kv_f16);
 
+/* ---- The reference's MM-DiT graph (ts_dit::forward / ::sample,
+ * src/mmdit.cpp:119-376), tsk_oracle_mmdit.c --------------------------------
+ * Weights by the converter's names from host f32 in ggml order; matrices are
+ * BF16 when act_bf16 (ggml_mul_mat rounds src1), else F32; the t_embed MLP
+ * and every vector F32. kv_f16 casts K / V to F16 (mmdit.cpp:89-90). Layouts
+ * as tsk_mmdit_forward / tsk_mmdit_sample. */
+typedef struct orc_mmdit orc_mmdit;
+orc_mmdit *orc_mmdit_create(const tsk_mmdit_config *cfg);
+void     orc_mmdit_destroy(orc_mmdit *m);
+int      orc_mmdit_n_tensors(const orc_mmdit *m);
+int      orc_mmdit_tensor_info(const orc_mmdit *m, int i, const char **name, int64_t ne[3], int *type);
+int      orc_mmdit_set_tensor(orc_mmdit *m, const char *name, const float *src, int64_t n);
+int      orc_mmdit_forward(orc_mmdit *m, int B, int T, const float *latent, const float *t, int clip_S,
+                           const float *clip_f, int sync_S, const float *sync_f, const float *text_f,
+                           const float *t5, const float *global_text, float *flow, int act_bf16, int kv_f16);
+/* stage outputs of the last orc_mmdit_forward by the reference's debug names
+ * (x_in, t_emb, clip_pp, text_pp, clip_fc, text_fc, gcmlp, global_c,
+ * extended_c, jb0_lat, jb0_clip, jb0_text, after_joint, after_fused; ggml
+ * [H, S] per batch row, rows concatenated); size -1 if absent */
+int64_t  orc_mmdit_stage_size(const orc_mmdit *m, const char *name);
+int      orc_mmdit_stage(const orc_mmdit *m, const char *name, float *out, int64_t n);
+int      orc_mmdit_sample(orc_mmdit *m, int T, const float *noise, int clip_S, const float *clip_f, int sync_S,
+                          const float *sync_f, const float *text_f, const float *t5, const float *global_text,
+                          int steps, float cfg_scale, float *out, float *flow0, int act_bf16, int kv_f16);
+
 /* ---- T5 encoder stack (ts_t5::encode, src/t5_encoder.cpp:40-104) ---------
  * Relative-position bucket of t5_encoder.cpp:14-26 (bidirectional). */
 int      orc_t5_bucket(int rel, int num_buckets, int max_dist);

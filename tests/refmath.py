@@ -344,3 +344,156 @@ def t5_encode_ref(W, cfg, x, ids, layers=None, final_norm=True):
         h = rms(x, W[p + ".ffn_norm"])
         x = x + mm(p + ".wo", gelu_tanh(mm(p + ".wi_0", h)) * mm(p + ".wi_1", h))
     return rms(x, W["out_norm"]) if final_norm else x
+
+
+def conv1d_ref(W, name, x, pad, bias=True):
+    """y[t] = sum_kw W[:, :, kw] x[t + kw - pad] (+ b), zero outside the
+    sequence: PyTorch Conv1d(stride 1) with W (OC, IC, KW), x (S, IC)."""
+    w = np.asarray(W[name + ".weight"], np.float64)
+    oc, ic, kw = w.shape
+    x = np.asarray(x, np.float64)
+    S = x.shape[0]
+    xp = np.concatenate([np.zeros((pad, ic)), x, np.zeros((pad, ic))])
+    y = np.zeros((S + 2 * pad - kw + 1, oc))
+    for j in range(kw):
+        y += xp[j:j + y.shape[0]] @ w[:, :, j].T
+    if bias:
+        y = y + np.asarray(W[name + ".bias"], np.float64)
+    return y
+
+
+def mmdit_forward_ref(W, cfg, latent, t, clip, sync, text, t5, g, swap_shift_scale=False, clip_rope_unscaled=False,
+                      sync_index_no_half=False, text_pad_left=False, latent_cond_global=False, clip_frozen=False,
+                      gate_mlp_index=5):
+    """The reference's MM-DiT graph (src/mmdit.cpp:119-342) in fp64, B = 1:
+    latent (L, T), t scalar, clip (S_c, clip_dim), sync (S_s, sync_dim),
+    text (text_seq, clip_dim), t5 (text_seq, t5_dim), g (clip_dim,) ->
+    flow (T, L). Written from the graph's structure:
+      x = convmlp(silu(conv_k3(latent^T)));  c_t = mlp_t(temb(t))
+      clip = convmlp(silu(W clip + b));  sync = convmlp(silu(conv_k7(sync + pos)))
+      text = mlp(silu(W [text | 0 ; t5] + b))           (154 tokens)
+      global = c_t + swiglu_mlp(W_c mean(clip) + b_c + W_t g + b_t)
+      ext[t] = sync[floor((t + 0.5) S_s / T)] + global
+    joint blocks: the latent stream's adaLN from ext (one modulation per
+    token), clip / text from global; RoPE on latent (scale 1) and clip
+    (scale T / S_c); attention over latent | clip | text; linear1 and the
+    MLP are k3 convolutions on latent / clip, linear on text; the last
+    block's clip / text pre_only. Fused blocks on the latent with ext; final
+    adaLN(ext), LN / modulate, conv k7.
+    Switches plant the structural mistakes the pin must catch."""
+    H, nh, hd = cfg["hidden"], cfg["n_head"], cfg["head_dim"]
+    nj = cfg["depth"] - cfg["fused_depth"]
+    X = 2 * cfg["text_seq"]
+
+    def swiglu_conv(p, x):
+        return conv1d_ref(W, p + ".w2", silu(conv1d_ref(W, p + ".w1", x, 1, False)) *
+                          conv1d_ref(W, p + ".w3", x, 1, False), 1, False)
+
+    def swiglu_lin(p, x):
+        return _lin(W, p + ".w2", silu(_lin(W, p + ".w1", x, False)) * _lin(W, p + ".w3", x, False), False)
+
+    def layer_norm(x):
+        mu = x.mean(-1, keepdims=True)
+        var = ((x - mu) ** 2).mean(-1, keepdims=True)
+        return (x - mu) / np.sqrt(var + 1e-5)
+
+    lat = np.asarray(latent, np.float64).T
+    T = lat.shape[0]
+    lat = swiglu_conv("audio_input_proj.2", silu(conv1d_ref(W, "audio_input_proj.0", lat, 1)))
+    te = _lin(W, "t_embed.mlp.2", silu(_lin(W, "t_embed.mlp.0", timestep_embedding_ref(t, H, cfg["t_max_period"]))))
+    clip = swiglu_conv("clip_input_proj.2", silu(_lin(W, "clip_input_proj.0", clip)))
+    Sc = clip.shape[0]
+    sync = np.asarray(sync, np.float64)
+    Ss = sync.shape[0]
+    pos = np.asarray(W["sync_pos_emb"], np.float64)                   # (8, sync_dim)
+    sync = sync + pos[np.arange(Ss) % 8]
+    sync = swiglu_conv("sync_input_proj.2", silu(conv1d_ref(W, "sync_input_proj.0", sync, 3)))
+    txt_pad = np.zeros((cfg["text_seq"], cfg["t5_dim"]))
+    if text_pad_left:
+        txt_pad[:, cfg["t5_dim"] - cfg["clip_dim"]:] = text
+    else:
+        txt_pad[:, :cfg["clip_dim"]] = text
+    seq = [txt_pad, np.asarray(t5, np.float64)]
+    txt = swiglu_lin("text_input_proj.2", silu(_lin(W, "text_input_proj.0", np.concatenate(seq))))
+    gvec = _lin(W, "clip_cond_proj", clip.mean(0)) + _lin(W, "text_cond_proj", g)
+    gc = swiglu_lin("global_cond_mlp", gvec) + te
+    idx = (np.floor(np.arange(T) * Ss / T) if sync_index_no_half else np.floor((np.arange(T) + 0.5) * Ss / T)).astype(int)
+    ext = sync[idx] + gc
+    s_ext, s_gc = silu(ext), silu(gc)
+    ang_l = rope_angles_ggml(T, hd, cfg["rope_theta"])
+    ang_c = rope_angles_ggml(Sc, hd, cfg["rope_theta"], 1.0 if clip_rope_unscaled else T / Sc)
+
+    def pre_attn(p, x, cond, ang, pre_only):
+        mod = _lin(W, p + ".adaLN_modulation.1", cond)          # (S or 1, n H)
+        mod = np.broadcast_to(mod.reshape(-1, mod.shape[-1]), (x.shape[0], mod.shape[-1]))
+        ch = [mod[:, i * H:(i + 1) * H] for i in range(2 if pre_only else 6)]
+        shift, scale = (ch[1], ch[0]) if swap_shift_scale else (ch[0], ch[1])
+        xn = layer_norm(x) * (1.0 + scale) + shift
+        qkv = _lin(W, p + ".attn.qkv", xn).reshape(x.shape[0], nh, hd, 3)
+        q, k, v = qkv[..., 0], qkv[..., 1], qkv[..., 2]
+        q = q / np.sqrt((q * q).mean(-1, keepdims=True) + 1e-6) * np.asarray(W[p + ".attn.q_norm.weight"], np.float64)
+        k = k / np.sqrt((k * k).mean(-1, keepdims=True) + 1e-6) * np.asarray(W[p + ".attn.k_norm.weight"], np.float64)
+        if ang is not None:
+            q, k = rope_apply(q, ang), rope_apply(k, ang)
+        return q, k, v, ch
+
+    def attend(qs, ks, vs):
+        q, k, v = (np.concatenate(a, axis=0) for a in (qs, ks, vs))
+        s = np.einsum("qhd,khd->hqk", q, k) / np.sqrt(hd)
+        s = s - s.max(-1, keepdims=True)
+        pr = np.exp(s)
+        pr /= pr.sum(-1, keepdims=True)
+        return np.einsum("hqk,khd->qhd", pr, v).reshape(q.shape[0], H)
+
+    def post_attn(p, x, o, ch, conv):
+        l1 = conv1d_ref(W, p + ".linear1", o, 1) if conv else _lin(W, p + ".linear1", o)
+        x = x + l1 * ch[2]
+        r = layer_norm(x) * (1.0 + ch[4]) + ch[3]
+        f = swiglu_conv(p + ".ffn", r) if conv else swiglu_lin(p + ".ffn", r)
+        return x + f * ch[gate_mlp_index]
+
+    lat_cond = s_gc[None, :] if latent_cond_global else s_ext
+    for i in range(nj):
+        pre_only = i == nj - 1
+        pl, pc, pt = (f"joint_blocks.{i}.{s}_block" for s in ("latent", "clip", "text"))
+        ql, kl, vl, chl = pre_attn(pl, lat, lat_cond, ang_l, False)
+        qc, kc, vc, chc = pre_attn(pc, clip, s_gc[None, :], ang_c, pre_only)
+        qt, kt, vt, cht = pre_attn(pt, txt, s_gc[None, :], None, pre_only)
+        o = attend([ql, qc, qt], [kl, kc, kt], [vl, vc, vt])
+        lat = post_attn(pl, lat, o[:T], chl, True)
+        if not pre_only:
+            if not clip_frozen:
+                clip = post_attn(pc, clip, o[T:T + Sc], chc, True)
+            txt = post_attn(pt, txt, o[T + Sc:T + Sc + X], cht, False)
+    for i in range(cfg["fused_depth"]):
+        p = f"fused_blocks.{i}"
+        q, k, v, ch = pre_attn(p, lat, lat_cond, ang_l, False)
+        lat = post_attn(p, lat, attend([q], [k], [v]), ch, True)
+    fm = _lin(W, "final_layer.adaLN_modulation.1", lat_cond)
+    fm = np.broadcast_to(fm.reshape(-1, 2 * H), (T, 2 * H))
+    fx = layer_norm(lat) * (1.0 + fm[:, H:]) + fm[:, :H]
+    return conv1d_ref(W, "final_layer.conv", fx, 3)
+
+
+def mmdit_sample_ref(W, cfg, noise, clip, sync, text, t5, g, steps, cfg_scale):
+    """ts_dit::sample (src/mmdit.cpp:344-376) over mmdit_forward_ref: the
+    unconditional forward on the learned empties (stored (clip_dim, 77) /
+    (t5_dim, 77) in ggml order, i.e. token rows) and a zero global text
+    feature; noise (L, T) -> (x (L, T), flow0 (L, T))."""
+    x = np.asarray(noise, np.float64).copy()
+    es = np.asarray(W["empty_string_feat"], np.float64)
+    et = np.asarray(W["empty_t5_feat"], np.float64)
+    zg = np.zeros(cfg["clip_dim"])
+    f = np.float32
+    flow0 = None
+    for s in range(steps):
+        t_curr = float(f(1.0) - f(s) / f(steps))
+        t_next = float(f(1.0) - f(s + 1) / f(steps))
+        dt = float(f(f(t_next) - f(t_curr)))
+        fc = mmdit_forward_ref(W, cfg, x, t_curr, clip, sync, text, t5, g).T
+        fu = mmdit_forward_ref(W, cfg, x, t_curr, clip, sync, es, et, zg).T
+        v = fu + (fc - fu) * cfg_scale
+        if s == 0:
+            flow0 = v
+        x = x + dt * v
+    return x, flow0

@@ -1,0 +1,180 @@
+"""The reference's MM-DiT graph on gfx950 (tsk_mmdit_*: three streams latent |
+clip | text, k3 convolutions, SwiGLU MLPs, per-token extended_c adaLN, the
+154-token text stream, the k7 output convolution; src/mmdit.cpp:119-376)
+against the oracle's restatement of the same graph (pinned against an fp64
+formulation in test_oracle_mmdit.py).
+
+Both sides run the BF16 GGUF's arithmetic: every BF16 product rounds its
+input to bf16 (ggml_mul_mat's src1 conversion), K / V are F16. The device's
+attention rounds differently from ggml-cpu's (q pre-scaled to fp16, P in
+fp16 for the PV product, exp2), changes of ~1e-4 relative in the attention
+output. Downstream, every activation is rounded to bf16 again before the next
+product, and a change d << ulp of a value flips its bf16 rounding with
+probability ~d / ulp, by a full ulp: the expected error grows like
+sqrt(d ulp), far above d. The oracle shows the same: switching its K / V
+from F16 to F32 moves the flow by 3.6e-3 with bf16 activations and by 2.9e-4
+with F32 activations (one joint block). So a forward is held to
+max(2e-3, 2 x that K/V change of the oracle on the same inputs); the
+conditioning stages, which have no attention, to 1e-3. The all-F32 oracle
+path is printed for reference: the BF16 model's distance from it is a
+property of the model, not of the device code."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env(orc):
+    from __graft_entry__ import ensure_built, load_tsk
+    ensure_built()
+    tsk = load_tsk()
+    tsk.init(0)
+    return tsk, orc
+
+
+def build_pair(tsk, orc, seed=1234, **kw):
+    m = tsk.MMDit(tsk.mmdit_config(**kw))
+    od = orc.OracleMMDiT(orc.mmdit_config(**kw))
+    names = m.tensors()
+    assert names == od.tensors()
+    W = tsk.mmdit_synthetic_weights(names, seed=seed)
+    for k, v in W.items():
+        m.set_tensor(k, v)
+        od.set_tensor(k, v)
+    return m, od, W
+
+
+def inputs(B, T, Sc, Ss, seed=4242):
+    """latent (B, 64, T), clip (B, Sc, 1024), sync (B, Ss, 768), text (B, 77,
+    1024), t5 (B, 77, 2048), global text (B, 1024), all N(0, 1)"""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32)
+    return f(B, 64, T), f(B, Sc, 1024), f(B, Ss, 768), f(B, 77, 1024), f(B, 77, 2048), f(B, 1024)
+
+
+def kv_floor(od, args, ref):
+    """the oracle's own change when its attention takes K / V in F32 instead
+    of the reference's F16 cast: the size of the change that one rounding of
+    the attention operands makes"""
+    return rel_l2(od.forward(*args, kv_f16=False), ref)
+
+
+def check_forward(m, od, B, T, Sc, Ss, t, label, seed=4242):
+    lat, clip, sync, text, t5, g = inputs(B, T, Sc, Ss, seed)
+    tt = np.full(B, t, np.float32)
+    f = m.forward(lat, tt, clip, sync, text, t5, g)
+    assert f.shape == (B, T, 64) and np.isfinite(f).all()
+    args = (lat, tt, clip, sync, text, t5, g)
+    ref = od.forward(*args)
+    floor = kv_floor(od, args, ref)
+    e = rel_l2(f, ref)
+    e32 = rel_l2(f, od.forward(*args, act_bf16=False, kv_f16=False))
+    print(f"{label}: rel-L2 {e:.3e} vs the oracle's BF16 path (its K/V F16-vs-F32 change {floor:.3e}); "
+          f"{e32:.3e} vs the F32 path", flush=True)
+    assert e <= max(2e-3, 2 * floor)
+    return f, args
+
+
+def test_mmdit_small_forward(env):
+    """2 joint blocks (the second with pre_only clip / text) + 1 fused block,
+    B = 2, short streams"""
+    tsk, orc = env
+    m, od, _ = build_pair(tsk, orc, depth=3, fused_depth=1, max_latent=64, max_clip=16, max_sync=48)
+    f, args = check_forward(m, od, 2, 40, 10, 32, 0.5, "reference graph, 3 blocks, T=40")
+    # batch rows independent, deterministic
+    f1 = m.forward(*(a[1:] for a in args))
+    assert np.array_equal(f1[0], f[1])
+    assert np.array_equal(m.forward(*args), f)
+    m.close()
+
+
+COND_STAGES = ("x_in", "t_emb", "clip_pp", "text_pp", "clip_fc", "text_fc", "gcmlp", "global_c", "extended_c")
+BLOCK_STAGES = ("jb0_lat", "jb0_clip", "jb0_text", "after_joint", "after_fused")
+
+
+def test_mmdit_stages(env):
+    """the reference's debug stages (src/mmdit.cpp:333-336). The conditioning
+    (input projections, t-embedding, clip mean, global / extended
+    conditioning) has no attention: there the two sides differ only where an
+    fp32 sum taken in another order lands next to a bf16 rounding boundary of
+    a later product's input. A difference d (relative) flips a rounding with
+    probability ~d / ulp and adds ~sqrt(d ulp): the F32-weight t_embed MLP
+    agrees to 1e-6, clip_pp (K = 8448 sums, d ~ 1e-5) to 1e-5, its mean's
+    rounding makes clip_fc ~2e-4, and two more roundings on 2 x 1024 values
+    make the global conditioning ~7e-4 (measured). Held to 1e-3 rel-L2, below
+    the ~4e-3 that one missing or extra bf16 rounding of an operand makes.
+    The block stages carry the attention's fp16 roundings: held to the
+    flow's bound."""
+    tsk, orc = env
+    m, od, _ = build_pair(tsk, orc, depth=3, fused_depth=1, max_latent=64, max_clip=16, max_sync=48)
+    m.debug(True)
+    lat, clip, sync, text, t5, g = inputs(2, 40, 10, 32, seed=11)
+    tt = np.array([0.8, 0.3], np.float32)
+    args = (lat, tt, clip, sync, text, t5, g)
+    m.forward(*args)
+    od.forward(*args, kv_f16=False)
+    kv = {s: od.stage(s) for s in BLOCK_STAGES}          # stages of the F32-K/V oracle run
+    od.forward(*args)
+    bad = []
+    for s in COND_STAGES:
+        e = rel_l2(m.stage(s), od.stage(s))
+        print(f"stage {s}: rel-L2 {e:.3e}", flush=True)
+        if e > 1e-3:
+            bad.append(s)
+    for s in BLOCK_STAGES:
+        e = rel_l2(m.stage(s), od.stage(s))
+        floor = rel_l2(kv[s], od.stage(s))
+        print(f"stage {s}: rel-L2 {e:.3e} (oracle K/V F16 vs F32: {floor:.3e})", flush=True)
+        if e > max(2e-3, 2 * floor):
+            bad.append(s)
+    assert not bad, bad
+    m.debug(False)
+    m.close()
+
+
+def test_mmdit_forward_9s_shapes(env):
+    """the 9 s token counts (194 latent, 72 clip at 8 fps, 216 sync at 24 fps,
+    154 text), 2 joint + 2 fused blocks at full width"""
+    tsk, orc = env
+    m, od, _ = build_pair(tsk, orc, depth=4, fused_depth=2, max_latent=194, max_clip=72, max_sync=216)
+    check_forward(m, od, 2, 194, 72, 216, 0.7, "reference graph, 4 blocks, 9 s shapes")
+    # a smaller call after the larger one on the same buffers
+    check_forward(m, od, 1, 60, 20, 64, 0.2, "reference graph, 4 blocks, T=60 after T=194", seed=7)
+    m.close()
+
+
+def test_mmdit_sampler(env):
+    """ts_dit::sample: 3 Euler steps, CFG 5, the unconditional branch on the
+    learned empties; flow0 and the latent held to max(5e-3, 2 x the oracle
+    sampler's own change when its K / V are F32 instead of F16)."""
+    tsk, orc = env
+    m, od, _ = build_pair(tsk, orc, depth=3, fused_depth=1, max_latent=64, max_clip=16, max_sync=48)
+    lat, clip, sync, text, t5, g = inputs(1, 40, 10, 32, seed=5)
+    x, flow0 = m.sample(lat[0], clip[0], sync[0], text[0], t5[0], g[0], steps=3, cfg_scale=5.0)
+    rx, rflow0 = od.sample(lat[0], clip[0], sync[0], text[0], t5[0], g[0], steps=3, cfg_scale=5.0)
+    kx, kf = od.sample(lat[0], clip[0], sync[0], text[0], t5[0], g[0], steps=3, cfg_scale=5.0, kv_f16=False)
+    s0, sx = rel_l2(kf, rflow0), rel_l2(kx, rx)
+    e0, ex = rel_l2(flow0, rflow0), rel_l2(x, rx)
+    print(f"reference-graph sampler: flow0 {e0:.3e}, latent {ex:.3e} (oracle K/V F16-vs-F32 change {s0:.3e}, "
+          f"{sx:.3e})", flush=True)
+    assert e0 <= max(5e-3, 2 * s0) and ex <= max(5e-3, 2 * sx)
+    m.close()
+
+
+def test_mmdit_rejects_bad_shapes(env):
+    tsk, _ = env
+    m = tsk.MMDit(tsk.mmdit_config(depth=2, fused_depth=1, max_latent=32, max_clip=8, max_sync=16))
+    lat, clip, sync, text, t5, g = inputs(1, 20, 5, 16)
+    t = np.full(1, 0.5, np.float32)
+    with pytest.raises(tsk.TskError):          # sync frames not a multiple of 8
+        m.forward(lat, t, clip, sync[:, :12], text, t5, g)
+    with pytest.raises(tsk.TskError):          # clip frames beyond the capacity
+        m.forward(lat, t, np.zeros((1, 9, 1024), np.float32), sync, text, t5, g)
+    with pytest.raises(tsk.TskError):          # latent beyond the capacity
+        m.forward(np.zeros((1, 64, 33), np.float32), t, clip, sync, text, t5, g)
+    with pytest.raises(tsk.TskError):
+        m.set_tensor("no.such.weight", np.zeros(4, np.float32))
+    m.close()

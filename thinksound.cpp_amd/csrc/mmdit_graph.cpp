@@ -1,0 +1,964 @@
+// mmdit_graph.cpp — the reference's MM-DiT graph on gfx950: ts_dit::forward
+// and ts_dit::sample as src/mmdit.cpp:119-376 build them (counterpart of
+// src/mmdit.h:9-42), with the kernels of this library:
+//   audio_input_proj: conv k3 -> silu -> convMLP                 (:150-155)
+//   t_embed MLP                                                   (:157-161)
+//   clip_input_proj: linear -> silu -> convMLP                    (:165-167)
+//   sync + pos_emb -> conv k7 -> silu -> convMLP -> nearest-exact (:168-178)
+//   text: pad text_f, concat t5 -> linear -> silu -> MLP          (:179-183)
+//   global_c = t_emb + global_cond_mlp(clip_cond(mean clip) + text_cond(g))
+//   extended_c = sync + global_c                                  (:184-196)
+//   7 joint blocks over latent | clip | text (the last clip / text pre_only),
+//   14 fused blocks on the latent, all with conv k3 linear1 / convMLP on the
+//   latent and clip streams and linear / MLP on text              (:203-281)
+//   final adaLN(extended_c) -> LN / modulate -> conv k7           (:284-289)
+// Every BF16 weight product rounds its input to bf16 first (ggml_mul_mat's
+// conversion of src1), as the BF16 GGUF runs; the residual streams, norms and
+// softmax are fp32. Glue that the reference emits as separate nodes is fused:
+// LN + modulate + the previous gate * residual update (one kernel), qkv
+// split + RMSNorm + RoPE + the F16 cast of K / V + the concatenation (one
+// kernel per stream), im2col inside the convolution GEMMs.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/tsk/tsk.h"
+#include "tsk_internal.h"
+#include "tsk_runtime.h"
+
+using namespace tsk;
+
+namespace {
+
+enum Kind { K_LIN = 0, K_CONV = 1, K_VEC = 2 };
+
+struct MW {
+    std::string name;
+    int64_t ne[3];          // ggml ne: linear [in, out]; conv [KW, IC, OC]; vector [n] / [a, b]
+    int kind;
+    bool f32;               // a matrix kept F32 (the t_embed MLP of the BF16 GGUF)
+    bool qkv_perm;          // rows (or entries) of a qkv projection: (h d j) -> [q | k | v]
+    size_t offset;
+    float amax;             // max |value| of a vector as last set
+};
+
+struct Lin { const uint16_t *w; const float *b; int K, M; const float *wf; };   // bf16 (or f32 wf) [M][K]
+struct Conv { const uint16_t *w; const float *b; int KW, IC, OC; };   // bf16 kw-major [OC][KW * IC]
+
+struct Block {
+    bool pre_only, conv;     // conv: latent / clip streams (k3 linear1 and convMLP)
+    int nmod;
+    Lin ada, qkv, l1, w1, w3, w2;   // l1 / w1 / w3 / w2 as linear layers (text) ...
+    Conv l1c, w1c, w3c, w2c;        // ... or k3 convolutions (latent / clip)
+    const float *qn, *kn;
+    int qn_idx, kn_idx;
+};
+
+}  // namespace
+
+struct tsk_mmdit {
+    tsk_mmdit_config cfg;
+    std::vector<MW> w;
+    std::unordered_map<std::string, int> idx;
+    char *blob = nullptr;
+    std::vector<Block> jl, jc, jt, fb;   // joint latent / clip / text, fused
+    std::vector<float> h_pos_emb, h_empty_str, h_empty_t5;   // host copies for the forward / sampler
+    // activations (capacity max_batch x max_*)
+    float *lat = nullptr, *clip = nullptr, *txt = nullptr, *sync = nullptr, *ext = nullptr;
+    uint16_t *silu_ext = nullptr, *silu_gc = nullptr;
+    float *vec = nullptr;                 // [8][B][H]: te0, te, text_fc, clip_mean, clip_fc, gsum, gc, spare
+    uint16_t *vec16 = nullptr;            // [4][B][max(H, clip_dim)] bf16 vectors
+    // adaLN outputs, two per stream: block i writes [i & 1] while the previous
+    // block's gate_mlp in [(i - 1) & 1] is still owed to the residual
+    float *mod_l[2] = {}, *mod_c[2] = {}, *mod_t[2] = {};
+    uint16_t *xn = nullptr, *hid = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr;
+    float *part = nullptr, *qkv32 = nullptr, *tmp32 = nullptr, *rope_l = nullptr, *rope_c = nullptr;
+    uint16_t *in16 = nullptr;             // bf16 copies of the staged inputs
+    float *in32 = nullptr;                // f32 staging of the inputs
+    uint16_t *act16 = nullptr;            // bf16(silu(.)) rows of the input projections
+    size_t in_cap = 0;                    // elements of in16 / in32
+    int ldv = 0, Nmax = 0, Rmax = 0;
+    // stage outputs of the last forward by the reference's debug names
+    // (src/mmdit.cpp:333-336), kept while `debug` is set
+    bool debug = false;
+    std::map<std::string, std::vector<float>> stages;
+};
+
+namespace {
+
+int hipcheck(hipError_t e, const char *what) { return e == hipSuccess ? TSK_OK : hip_fail(e, what); }
+
+// debug mode: copy n floats of a device stage tensor to the host under `name`
+int grab(tsk_mmdit *m, const char *name, const float *dev, size_t n, hipStream_t st) {
+    if (!m->debug) return TSK_OK;
+    std::vector<float> v(n);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = hipMemcpy(v.data(), dev, sizeof(float) * n, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "debug stage copy");
+    m->stages[name].swap(v);
+    return TSK_OK;
+}
+
+void addw(tsk_mmdit *m, const std::string &name, int64_t a, int64_t b, int64_t c, int kind, bool perm = false) {
+    MW x;
+    x.name = name;
+    x.ne[0] = a; x.ne[1] = b; x.ne[2] = c;
+    x.kind = kind;
+    x.qkv_perm = perm;
+    x.f32 = false;
+    x.offset = 0;
+    x.amax = 0.0f;
+    m->idx[name] = (int) m->w.size();
+    m->w.push_back(x);
+}
+
+void add_lin(tsk_mmdit *m, const std::string &p, int in, int out, bool bias, bool perm = false) {
+    addw(m, p + ".weight", in, out, 1, K_LIN, perm);
+    if (bias) addw(m, p + ".bias", out, 1, 1, K_VEC, perm);
+}
+
+void add_conv(tsk_mmdit *m, const std::string &p, int kw, int in, int out, bool bias) {
+    addw(m, p + ".weight", kw, in, out, K_CONV);
+    if (bias) addw(m, p + ".bias", out, 1, 1, K_VEC);
+}
+
+// MMDitSingleBlock (docs/ARCHITECTURE.md §6.1): adaLN, qkv, q/k norms, and
+// unless pre_only linear1 + ffn (k3 convolutions, or linear layers for text)
+void add_block(tsk_mmdit *m, const std::string &p, bool pre_only, bool conv) {
+    const int H = m->cfg.hidden, F = m->cfg.mlp_hidden;
+    add_lin(m, p + ".adaLN_modulation.1", H, (pre_only ? 2 : 6) * H, true);
+    add_lin(m, p + ".attn.qkv", H, 3 * H, true, true);
+    addw(m, p + ".attn.q_norm.weight", m->cfg.head_dim, 1, 1, K_VEC);
+    addw(m, p + ".attn.k_norm.weight", m->cfg.head_dim, 1, 1, K_VEC);
+    if (pre_only) return;
+    if (conv) {
+        add_conv(m, p + ".linear1", 3, H, H, true);
+        add_conv(m, p + ".ffn.w1", 3, H, F, false);
+        add_conv(m, p + ".ffn.w3", 3, H, F, false);
+        add_conv(m, p + ".ffn.w2", 3, F, H, false);
+    } else {
+        add_lin(m, p + ".linear1", H, H, true);
+        add_lin(m, p + ".ffn.w1", H, F, false);
+        add_lin(m, p + ".ffn.w3", H, F, false);
+        add_lin(m, p + ".ffn.w2", F, H, false);
+    }
+}
+
+const MW &wi(const tsk_mmdit *m, const std::string &n) { return m->w[m->idx.at(n)]; }
+template <class T> T *wp(const tsk_mmdit *m, const std::string &n) { return (T *) (m->blob + wi(m, n).offset); }
+
+Lin lin_of(const tsk_mmdit *m, const std::string &p, bool bias) {
+    const MW &x = wi(m, p + ".weight");
+    return Lin{x.f32 ? nullptr : wp<uint16_t>(m, p + ".weight"), bias ? wp<float>(m, p + ".bias") : nullptr,
+               (int) x.ne[0], (int) x.ne[1], x.f32 ? wp<float>(m, p + ".weight") : nullptr};
+}
+
+Conv conv_of(const tsk_mmdit *m, const std::string &p, bool bias) {
+    const MW &x = wi(m, p + ".weight");
+    return Conv{wp<uint16_t>(m, p + ".weight"), bias ? wp<float>(m, p + ".bias") : nullptr, (int) x.ne[0],
+                (int) x.ne[1], (int) x.ne[2]};
+}
+
+Block block_of(const tsk_mmdit *m, const std::string &p, bool pre_only, bool conv) {
+    Block b;
+    memset(&b, 0, sizeof(b));
+    b.pre_only = pre_only;
+    b.conv = conv;
+    b.nmod = pre_only ? 2 : 6;
+    b.ada = lin_of(m, p + ".adaLN_modulation.1", true);
+    b.qkv = lin_of(m, p + ".attn.qkv", true);
+    b.qn = wp<float>(m, p + ".attn.q_norm.weight");
+    b.kn = wp<float>(m, p + ".attn.k_norm.weight");
+    b.qn_idx = m->idx.at(p + ".attn.q_norm.weight");
+    b.kn_idx = m->idx.at(p + ".attn.k_norm.weight");
+    if (!pre_only) {
+        if (conv) {
+            b.l1c = conv_of(m, p + ".linear1", true);
+            b.w1c = conv_of(m, p + ".ffn.w1", false);
+            b.w3c = conv_of(m, p + ".ffn.w3", false);
+            b.w2c = conv_of(m, p + ".ffn.w2", false);
+        } else {
+            b.l1 = lin_of(m, p + ".linear1", true);
+            b.w1 = lin_of(m, p + ".ffn.w1", false);
+            b.w3 = lin_of(m, p + ".ffn.w3", false);
+            b.w2 = lin_of(m, p + ".ffn.w2", false);
+        }
+    }
+    return b;
+}
+
+int validate_cfg(const tsk_mmdit_config *c) {
+    if (!c) return fail(TSK_ERR_INVALID_ARG, "cfg is NULL");
+    if (c->head_dim != 64 || c->hidden != c->n_head * 64) return fail(TSK_ERR_UNSUPPORTED, "head_dim must be 64, hidden = 64 n_head");
+    if (c->hidden % 64 || c->mlp_hidden % 64 || c->latent_dim % 32 || c->latent_dim < 32 || c->clip_dim % 64 ||
+        c->sync_dim % 64 || c->t5_dim % 64 || c->t5_dim < c->clip_dim)
+        return fail(TSK_ERR_SHAPE, "hidden, mlp_hidden, clip / sync / t5 dims must be multiples of 64, latent_dim of 32");
+    if (c->depth - c->fused_depth < 1 || c->fused_depth < 0) return fail(TSK_ERR_SHAPE, "depth / fused_depth");
+    if (c->max_batch < 1 || c->max_batch > 32 || c->max_latent < 1 || c->max_clip < 1 || c->max_sync < 8 ||
+        c->text_seq < 1)
+        return fail(TSK_ERR_SHAPE, "capacity");
+    if (!(c->rope_theta > 0) || !(c->t_max_period > 0)) return fail(TSK_ERR_INVALID_ARG, "rope_theta / t_max_period");
+    return TSK_OK;
+}
+
+// ---- GEMMs of the graph (bf16 activation rows, launch_gemm_coop)
+
+// y[n][m] = x[n] . W[m] (+ b): x bf16 rows (ld_x), y f32 or bf16 rows (ld_y)
+// y[n][m] = x[n] . W[m] + b with an F32 weight: f32 activations, fp32 products
+int lin_f32(const Lin &L, const float *x, int N, float *y, hipStream_t s) {
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
+    q.x = x; q.ld_x = L.K;
+    q.wf = L.wf; q.ld_w = L.K;
+    q.bias = L.b;
+    q.y = y; q.ld_y = L.M;
+    q.M = L.M; q.N = N; q.K = L.K; q.splits = 1;
+    return hipcheck(launch_gemm_f32(q, 0, s), "mmdit f32 linear");
+}
+
+int lin(const Lin &L, const uint16_t *x, int64_t ld_x, int N, void *y, int64_t ld_y, bool y_bf16, hipStream_t s,
+        const float *bias_override = nullptr, bool no_bias = false) {
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = x; q.ld_x = ld_x;
+    q.w = L.w; q.ld_w = L.K;
+    q.bias = no_bias ? nullptr : bias_override ? bias_override : L.b;
+    q.y = y; q.ld_y = ld_y;
+    q.M = L.M; q.N = N; q.K = L.K; q.splits = 1;
+    return hipcheck(launch_gemm_coop(g, y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32, s), "mmdit linear");
+}
+
+// conv_cl (stride 1, padding pad): x bf16 rows [B][IW][IC] with row stride
+// ld_x and batch stride xb (elements), y rows [B * IW][OC] (ld_y)
+int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, void *y, int64_t ld_y,
+         bool y_bf16, hipStream_t s, bool no_bias = false) {
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = x; q.ld_x = ld_x; q.x_group_stride = xb;
+    q.w = C.w; q.ld_w = (int64_t) C.KW * C.IC;
+    q.bias = no_bias ? nullptr : C.b;
+    q.y = y; q.ld_y = ld_y;
+    const int OW = IW + 2 * pad - (C.KW - 1);
+    q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = 1;
+    q.conv_ic = C.IC; q.conv_iw = IW; q.conv_ow = OW; q.conv_s = 1; q.conv_p = pad; q.conv_d = 1;
+    return hipcheck(launch_gemm_coop(g, y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32, s), "mmdit conv");
+}
+
+// convmlp / mlp (src/mmdit.cpp:39-52): y = w2(silu(w1 x) * w3 x), the hidden
+// state bf16 in m->hid (the conversion w2's mul_mat applies to it)
+int conv_mlp(tsk_mmdit *m, const Conv &w1, const Conv &w3, const Conv &w2, const uint16_t *x, int64_t ld_x, int64_t xb,
+             int IW, int B, float *y, int64_t ld_y, hipStream_t s) {
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = x; q.ld_x = ld_x; q.x_group_stride = xb;
+    q.w = w1.w; q.w3 = w3.w; q.ld_w = (int64_t) w1.KW * w1.IC;
+    q.y = m->hid; q.ld_y = w1.OC;
+    q.M = w1.OC; q.N = B * IW; q.K = w1.KW * w1.IC; q.splits = 1;
+    q.conv_ic = w1.IC; q.conv_iw = IW; q.conv_ow = IW; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
+    int rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_BF16, s), "mmdit convmlp w1/w3");
+    if (rc) return rc;
+    return conv(w2, m->hid, w1.OC, (int64_t) IW * w1.OC, IW, B, 1, y, ld_y, false, s, true);
+}
+
+int lin_mlp(tsk_mmdit *m, const Lin &w1, const Lin &w3, const Lin &w2, const uint16_t *x, int64_t ld_x, int N, float *y,
+            int64_t ld_y, hipStream_t s) {
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = x; q.ld_x = ld_x;
+    q.w = w1.w; q.w3 = w3.w; q.ld_w = w1.K;
+    q.y = m->hid; q.ld_y = w1.M;
+    q.M = w1.M; q.N = N; q.K = w1.K; q.splits = 1;
+    int rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_BF16, s), "mmdit mlp w1/w3");
+    if (rc) return rc;
+    return lin(w2, m->hid, w1.M, N, y, ld_y, false, s, nullptr, true);
+}
+
+// ---- one stream of a block as the fused kernels see it
+struct Stream {
+    const Block *w;
+    float *x;              // f32 residual rows [B][S][H]
+    int S, tok_off;
+    const float *rope_cs;  // nullptr: no RoPE (text)
+    float *mod;            // [B * rows_mod][nmod * H] adaLN output
+    int per_token;         // modulation per token (latent: extended_c) or per batch item
+    uint16_t *xn;          // bf16 LN output rows
+    float *part;           // f32 output of the previous projection (residual update owed)
+    const float *pend_bias, *pend_gate;
+    int64_t pend_ld;       // row stride of pend_gate (the owing block's adaLN width)
+    bool pending;
+};
+
+LnStream ln_of(const tsk_mmdit *m, Stream &r, int B, int which) {
+    const int H = m->cfg.hidden;
+    LnStream l;
+    memset(&l, 0, sizeof(l));
+    l.x = r.x; l.ld_x = H;
+    const int64_t ldm = (int64_t) r.w->nmod * H;
+    if (r.pending) {
+        l.part = r.part; l.nsplit = 1; l.part_stride = 0;
+        l.bias = r.pend_bias; l.gate = r.pend_gate; l.ld_gate = r.pend_ld;
+        r.pending = false;
+    }
+    l.shift = r.mod + (which ? 3 : 0) * H;
+    l.scale = r.mod + (which ? 4 : 1) * H;
+    l.ld_mod = ldm;
+    l.y = r.xn; l.ld_y = H;
+    l.rows = B * r.S;
+    l.rows_per_b = r.per_token ? 1 : r.S;
+    return l;
+}
+
+// LN(which) of up to three streams (two per launch)
+int run_ln(tsk_mmdit *m, Stream *r, int ns, int B, int which, hipStream_t s) {
+    for (int i0 = 0; i0 < ns; i0 += 2) {
+        LnGroup g;
+        memset(&g, 0, sizeof(g));
+        g.H = m->cfg.hidden;
+        g.eps = 1e-5f;                                   // layernorm() eps, src/mmdit.cpp:59
+        g.y_mode = LN_Y_BF16;
+        g.nstream = ns - i0 >= 2 ? 2 : 1;
+        for (int j = 0; j < g.nstream; ++j) g.s[j] = ln_of(m, r[i0 + j], B, which);
+        int rc = hipcheck(launch_ln_group(g, s), "mmdit layernorm");
+        if (rc) return rc;
+    }
+    return TSK_OK;
+}
+
+// adaLN of every stream: lin(adaLN, silu(cond)) (src/mmdit.cpp:209)
+int run_mods(tsk_mmdit *m, Stream *r, int ns, int B, int T, hipStream_t s) {
+    const int H = m->cfg.hidden;
+    for (int i = 0; i < ns; ++i) {
+        const Block &b = *r[i].w;
+        int rc = r[i].per_token ? lin(b.ada, m->silu_ext, H, B * T, r[i].mod, (int64_t) b.nmod * H, false, s)
+                                : lin(b.ada, m->silu_gc, H, B, r[i].mod, (int64_t) b.nmod * H, false, s);
+        if (rc) return rc;
+    }
+    return TSK_OK;
+}
+
+// qkv -> split / RMSNorm / RoPE / F16 into the joint attention operands
+int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
+    const tsk_mmdit_config &c = m->cfg;
+    const int H = c.hidden;
+    for (int i = 0; i < ns; ++i) {
+        int rc = lin(r[i].w->qkv, r[i].xn, H, B * r[i].S, m->qkv32, 3 * H, false, s);
+        if (rc) return rc;
+        QkvScatter q;
+        memset(&q, 0, sizeof(q));
+        q.qkv = m->qkv32; q.ld = 3 * H;
+        q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
+        q.rope_cs = r[i].rope_cs;
+        q.q = m->q; q.k = m->k; q.vt = m->vt; q.ldv = m->ldv;
+        q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope_cs != nullptr;
+        q.nh = c.n_head; q.rows = B * r[i].S;
+        q.eps = 1e-6f;                                   // rmsnorm_w EPS, src/mmdit.cpp:10
+        q.q_scale = 1.4426950408889634f / 8.0f;          // 1/sqrt(64) * log2(e): the attention's softmax scale
+        if ((rc = hipcheck(launch_qkv_scatter(q, s), "mmdit qkv scatter"))) return rc;
+    }
+    return TSK_OK;
+}
+
+int run_attention(tsk_mmdit *m, const Stream *r, int ns, int B, int Ntot, hipStream_t s) {
+    const tsk_mmdit_config &c = m->cfg;
+    AttnFastParams p;
+    memset(&p, 0, sizeof(p));
+    p.q = m->q; p.k = m->k; p.vt = m->vt; p.o = m->o;
+    p.q_type = TSK_TYPE_F16; p.k_bf16 = 0; p.out_bf16 = 1;
+    p.Nq = p.Nkv = Ntot; p.H = c.n_head; p.B = B;
+    p.q_nb1 = p.k_nb1 = 128;                          // q / k [B][n_head][Ntot][64] fp16
+    p.q_nb2 = p.k_nb2 = (int64_t) 128 * Ntot;
+    p.q_nb3 = p.k_nb3 = (int64_t) 128 * Ntot * c.n_head;
+    p.vt_bh = (int64_t) 64 * m->ldv;
+    p.ldv = m->ldv;
+    p.o_nb1 = 128; p.o_nb2 = (int64_t) 2 * c.hidden; p.o_nb3 = (int64_t) 2 * c.hidden * m->Nmax;
+    p.c = 1.4426950408889634f / 8.0f;
+    p.q_prescaled = 1;
+    float aq = 0.0f, ak = 0.0f;
+    for (int i = 0; i < ns; ++i) {
+        aq = fmaxf(aq, m->w[r[i].w->qn_idx].amax);
+        ak = fmaxf(ak, m->w[r[i].w->kn_idx].amax);
+    }
+    // |q.k| <= 64 max|w_q| max|w_k| after RMSNorm (RoPE is a rotation): no
+    // running max below ATTN_LOGIT_BOUND (1 % margin for the fp16 rounding)
+    p.bounded = 1.01f * 64.0f * p.c * aq * ak <= ATTN_LOGIT_BOUND;
+    p.force_cfg = tuning().attn_cfg;
+    return hipcheck(launch_attn_fast(p, s), "mmdit attention");
+}
+
+// post_attn (src/mmdit.cpp:226-235): linear1 on this stream's attention rows
+// (its residual update is owed to the next LN), LN, ffn (owed to the next LN)
+int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
+    const int H = m->cfg.hidden;
+    int rc;
+    for (int i = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        const Block &b = *r[i].w;
+        const uint16_t *orows = m->o + (size_t) r[i].tok_off * H;
+        const int64_t ob = (int64_t) m->Nmax * H;      // batch stride of the attention output rows
+        if (b.conv) rc = conv(b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, true);
+        else {
+            // text: linear1 rows grouped by batch item
+            GemmGroup g;
+            memset(&g, 0, sizeof(g));
+            g.nprob = 1;
+            GemmProblem &q = g.p[0];
+            q.x = orows; q.ld_x = H; q.x_group_rows = r[i].S; q.x_group_stride = ob;
+            q.w = b.l1.w; q.ld_w = b.l1.K;
+            q.y = r[i].part; q.ld_y = H;
+            q.M = H; q.N = B * r[i].S; q.K = H; q.splits = 1;
+            rc = hipcheck(launch_gemm_coop(g, EPI_STORE_F32, s), "mmdit text linear1");
+        }
+        if (rc) return rc;
+        r[i].pending = true;
+        r[i].pend_bias = b.conv ? b.l1c.b : b.l1.b;
+        r[i].pend_gate = r[i].mod + 2 * H;             // gate_msa
+        r[i].pend_ld = 6 * H;
+    }
+    Stream live[3];
+    int nl = 0;
+    for (int i = 0; i < ns; ++i)
+        if (!r[i].w->pre_only) live[nl++] = r[i];
+    if (!nl) return TSK_OK;
+    if ((rc = run_ln(m, live, nl, B, 1, s))) return rc;
+    for (int i = 0, j = 0; i < ns; ++i) {
+        if (r[i].w->pre_only) continue;
+        r[i].pending = live[j++].pending;
+        const Block &b = *r[i].w;
+        rc = b.conv ? conv_mlp(m, b.w1c, b.w3c, b.w2c, r[i].xn, H, (int64_t) r[i].S * H, r[i].S, B, r[i].part, H, s)
+                    : lin_mlp(m, b.w1, b.w3, b.w2, r[i].xn, H, B * r[i].S, r[i].part, H, s);
+        if (rc) return rc;
+        r[i].pending = true;
+        r[i].pend_bias = nullptr;
+        r[i].pend_gate = r[i].mod + 5 * H;             // gate_mlp
+        r[i].pend_ld = 6 * H;
+    }
+    return TSK_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ lifecycle
+extern "C" void tsk_mmdit_default_config(tsk_mmdit_config *c) {
+    if (!c) return;
+    c->hidden = 1024; c->n_head = 16; c->head_dim = 64; c->depth = 21; c->fused_depth = 14;
+    c->latent_dim = 64; c->text_seq = 77; c->clip_dim = 1024; c->sync_dim = 768; c->t5_dim = 2048;
+    c->mlp_hidden = 2816; c->max_batch = 2; c->max_latent = 646; c->max_clip = 240; c->max_sync = 720;
+    c->rope_theta = 10000.0f; c->t_max_period = 1.0f;
+}
+
+extern "C" void tsk_mmdit_destroy(tsk_mmdit *m) {
+    if (!m) return;
+    (void) hipDeviceSynchronize();
+    void *bufs[] = {m->blob, m->lat, m->clip, m->txt, m->sync, m->ext, m->silu_ext, m->silu_gc, m->vec, m->vec16,
+                    m->mod_l[0], m->mod_l[1], m->mod_c[0], m->mod_c[1], m->mod_t[0], m->mod_t[1], m->xn, m->hid,
+                    m->o, m->q, m->k, m->vt, m->part, m->qkv32, m->tmp32, m->rope_l, m->rope_c, m->in16, m->in32,
+                    m->act16};
+    for (void *b : bufs)
+        if (b) (void) hipFree(b);
+    delete m;
+}
+
+extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
+    if (!out) return fail(TSK_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    int rc = validate_cfg(cfg);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    tsk_mmdit *m = new tsk_mmdit();
+    m->cfg = *cfg;
+    const tsk_mmdit_config &c = m->cfg;
+    const int H = c.hidden, F = c.mlp_hidden, nj = c.depth - c.fused_depth, X = 2 * c.text_seq;
+    // the converter's tensor names (convert/convert_thinksound.py:32) and shapes (docs/ARCHITECTURE.md §6.1)
+    add_conv(m, "audio_input_proj.0", 3, c.latent_dim, H, true);
+    add_conv(m, "audio_input_proj.2.w1", 3, H, F, false);
+    add_conv(m, "audio_input_proj.2.w3", 3, H, F, false);
+    add_conv(m, "audio_input_proj.2.w2", 3, F, H, false);
+    add_lin(m, "clip_input_proj.0", c.clip_dim, H, true);
+    add_conv(m, "clip_input_proj.2.w1", 3, H, F, false);
+    add_conv(m, "clip_input_proj.2.w3", 3, H, F, false);
+    add_conv(m, "clip_input_proj.2.w2", 3, F, H, false);
+    add_conv(m, "sync_input_proj.0", 7, c.sync_dim, H, true);
+    add_conv(m, "sync_input_proj.2.w1", 3, H, F, false);
+    add_conv(m, "sync_input_proj.2.w3", 3, H, F, false);
+    add_conv(m, "sync_input_proj.2.w2", 3, F, H, false);
+    add_lin(m, "text_input_proj.0", c.t5_dim, H, true);
+    add_lin(m, "text_input_proj.2.w1", H, F, false);
+    add_lin(m, "text_input_proj.2.w3", H, F, false);
+    add_lin(m, "text_input_proj.2.w2", F, H, false);
+    add_lin(m, "text_cond_proj", c.clip_dim, H, true);
+    add_lin(m, "clip_cond_proj", H, H, true);
+    add_lin(m, "global_cond_mlp.w1", H, F, false);
+    add_lin(m, "global_cond_mlp.w3", H, F, false);
+    add_lin(m, "global_cond_mlp.w2", F, H, false);
+    addw(m, "sync_pos_emb", c.sync_dim, 8, 1, K_VEC);
+    add_lin(m, "t_embed.mlp.0", H, H, true);
+    add_lin(m, "t_embed.mlp.2", H, H, true);
+    // kept F32 by the BF16 conversion (convert/quantize_gguf.py:11-14: "_emb" names)
+    m->w[m->idx["t_embed.mlp.0.weight"]].f32 = true;
+    m->w[m->idx["t_embed.mlp.2.weight"]].f32 = true;
+    for (int i = 0; i < nj; ++i) {
+        const std::string p = "joint_blocks." + std::to_string(i);
+        add_block(m, p + ".latent_block", false, true);
+        add_block(m, p + ".clip_block", i == nj - 1, true);
+        add_block(m, p + ".text_block", i == nj - 1, false);
+    }
+    for (int i = 0; i < c.fused_depth; ++i) add_block(m, "fused_blocks." + std::to_string(i), false, true);
+    add_lin(m, "final_layer.adaLN_modulation.1", H, 2 * H, true);
+    add_conv(m, "final_layer.conv", 7, H, c.latent_dim, true);
+    addw(m, "empty_string_feat", c.clip_dim, c.text_seq, 1, K_VEC);
+    addw(m, "empty_t5_feat", c.t5_dim, c.text_seq, 1, K_VEC);
+    size_t off = 0;
+    for (auto &x : m->w) {
+        x.offset = off;
+        const size_t n = (size_t) (x.ne[0] * x.ne[1] * x.ne[2]);
+        off += (n * (x.kind == K_VEC || x.f32 ? 4 : 2) + 255) & ~(size_t) 255;
+    }
+    const int B = c.max_batch, T = c.max_latent, C = c.max_clip, S = c.max_sync;
+    m->Nmax = T + C + X;
+    m->ldv = (m->Nmax + 63) / 64 * 64;
+    const int64_t R = (int64_t) B * std::max(std::max(T, C), std::max(S, X));   // rows of the longest stream
+    m->Rmax = (int) R;
+    const int64_t rows3 = (int64_t) B * (T + C + X);
+    const int Wmax = std::max(std::max(H, c.t5_dim), std::max(c.sync_dim, c.clip_dim));
+    // staged inputs per batch row: latent, clip, sync, text | t5, global text, t-embedding
+    m->in_cap = (size_t) B * ((size_t) T * c.latent_dim + (size_t) C * c.clip_dim + (size_t) S * c.sync_dim +
+                              (size_t) X * c.t5_dim + c.clip_dim + H);
+    auto alloc = [&](void **p, size_t bytes) -> int {
+        hipError_t e = hipMalloc(p, bytes);
+        if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return TSK_OK;
+    };
+    if ((rc = alloc((void **) &m->blob, off)) ||
+        (rc = alloc((void **) &m->lat, sizeof(float) * B * T * H)) ||
+        (rc = alloc((void **) &m->clip, sizeof(float) * B * C * H)) ||
+        (rc = alloc((void **) &m->txt, sizeof(float) * B * X * H)) ||
+        (rc = alloc((void **) &m->sync, sizeof(float) * B * S * H)) ||
+        (rc = alloc((void **) &m->ext, sizeof(float) * B * T * H)) ||
+        (rc = alloc((void **) &m->silu_ext, 2 * (size_t) B * T * H)) ||
+        (rc = alloc((void **) &m->silu_gc, 2 * (size_t) B * H)) ||
+        (rc = alloc((void **) &m->vec, sizeof(float) * 8 * B * H)) ||
+        (rc = alloc((void **) &m->vec16, 2 * (size_t) 4 * B * Wmax)) ||
+        (rc = alloc((void **) &m->mod_l[0], sizeof(float) * B * T * 6 * H)) ||
+        (rc = alloc((void **) &m->mod_l[1], sizeof(float) * B * T * 6 * H)) ||
+        (rc = alloc((void **) &m->mod_c[0], sizeof(float) * B * 6 * H)) ||
+        (rc = alloc((void **) &m->mod_c[1], sizeof(float) * B * 6 * H)) ||
+        (rc = alloc((void **) &m->mod_t[0], sizeof(float) * B * 6 * H)) ||
+        (rc = alloc((void **) &m->mod_t[1], sizeof(float) * B * 6 * H)) ||
+        (rc = alloc((void **) &m->xn, 2 * (size_t) rows3 * H)) ||
+        (rc = alloc((void **) &m->hid, 2 * (size_t) R * F)) ||
+        (rc = alloc((void **) &m->o, 2 * (size_t) B * m->Nmax * H)) ||
+        (rc = alloc((void **) &m->q, 2 * (size_t) B * m->Nmax * H)) ||
+        (rc = alloc((void **) &m->k, 2 * (size_t) B * m->Nmax * H)) ||
+        (rc = alloc((void **) &m->vt, 2 * (size_t) B * H * m->ldv)) ||
+        (rc = alloc((void **) &m->part, sizeof(float) * rows3 * H)) ||
+        (rc = alloc((void **) &m->qkv32, sizeof(float) * R * 3 * H)) ||
+        (rc = alloc((void **) &m->tmp32, sizeof(float) * R * std::max(H, c.latent_dim))) ||
+        (rc = alloc((void **) &m->rope_l, sizeof(float) * T * 64)) ||
+        (rc = alloc((void **) &m->rope_c, sizeof(float) * C * 64)) ||
+        (rc = alloc((void **) &m->in16, 2 * m->in_cap)) ||
+        (rc = alloc((void **) &m->in32, sizeof(float) * m->in_cap)) ||
+        (rc = alloc((void **) &m->act16, 2 * (size_t) R * H))) {
+        tsk_mmdit_destroy(m);
+        return rc;
+    }
+    hipError_t e = hipMemset(m->blob, 0, off);
+    // V^T key positions past a call's token count are read (times P = 0)
+    if (e == hipSuccess) e = hipMemset(m->vt, 0, 2 * (size_t) B * H * m->ldv);
+    // latent positions 0 .. T-1, freq_scale 1 (src/mmdit.cpp:96-99, :316-318)
+    if (e == hipSuccess) e = launch_rope_table(m->rope_l, T, 64, powf(c.rope_theta, -2.0f / 64.0f), 1.0f, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) { tsk_mmdit_destroy(m); return hip_fail(e, "mmdit init"); }
+    for (int i = 0; i < nj; ++i) {
+        const std::string p = "joint_blocks." + std::to_string(i);
+        m->jl.push_back(block_of(m, p + ".latent_block", false, true));
+        m->jc.push_back(block_of(m, p + ".clip_block", i == nj - 1, true));
+        m->jt.push_back(block_of(m, p + ".text_block", i == nj - 1, false));
+    }
+    for (int i = 0; i < c.fused_depth; ++i) m->fb.push_back(block_of(m, "fused_blocks." + std::to_string(i), false, true));
+    m->h_pos_emb.assign((size_t) c.sync_dim * 8, 0.0f);
+    m->h_empty_str.assign((size_t) c.clip_dim * c.text_seq, 0.0f);
+    m->h_empty_t5.assign((size_t) c.t5_dim * c.text_seq, 0.0f);
+    *out = m;
+    return TSK_OK;
+}
+
+extern "C" int tsk_mmdit_n_tensors(const tsk_mmdit *m) { return m ? (int) m->w.size() : 0; }
+
+extern "C" int tsk_mmdit_tensor_type(const tsk_mmdit *m, int i) {
+    if (!m || i < 0 || i >= (int) m->w.size()) return fail(TSK_ERR_INVALID_ARG, "tensor index %d", i);
+    return m->w[i].kind == K_VEC || m->w[i].f32 ? TSK_TYPE_F32 : TSK_TYPE_BF16;
+}
+
+extern "C" int tsk_mmdit_tensor_info(const tsk_mmdit *m, int i, const char **name, int64_t ne[4]) {
+    if (!m || i < 0 || i >= (int) m->w.size()) return fail(TSK_ERR_INVALID_ARG, "tensor index %d", i);
+    if (name) *name = m->w[i].name.c_str();
+    if (ne) { ne[0] = m->w[i].ne[0]; ne[1] = m->w[i].ne[1]; ne[2] = m->w[i].ne[2]; ne[3] = 1; }
+    return TSK_OK;
+}
+
+// host f32 in ggml / PyTorch memory order: linear [out][in], conv [OC][IC][KW]
+// (ggml ne [KW, IC, OC]), vectors; matrices -> bf16 (RNE), conv kernels
+// kw-major [OC][KW][IC], qkv rows (and bias entries) (h d j) -> [q | k | v]
+extern "C" int tsk_mmdit_set_tensor(tsk_mmdit *m, const char *name, const float *src, int64_t n) {
+    if (!m || !name || !src) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = m->idx.find(name);
+    if (it == m->idx.end()) return fail(TSK_ERR_INVALID_ARG, "unknown tensor '%s'", name);
+    MW &x = m->w[it->second];
+    const int64_t N = x.ne[0] * x.ne[1] * x.ne[2];
+    if (n != N) return fail(TSK_ERR_SHAPE, "'%s' has %lld elements, got %lld", name, (long long) N, (long long) n);
+    const int H = m->cfg.hidden;
+    std::vector<float> v(src, src + n);
+    if (x.qkv_perm) {
+        const int64_t rowlen = x.kind == K_LIN ? x.ne[0] : 1;
+        for (int64_t i = 0; i < H; ++i)
+            for (int j = 0; j < 3; ++j)
+                memcpy(&v[(size_t) ((j * H + i) * rowlen)], src + (3 * i + j) * rowlen, sizeof(float) * rowlen);
+    }
+    if (x.kind == K_CONV) {
+        const int64_t KW = x.ne[0], IC = x.ne[1], OC = x.ne[2];
+        std::vector<float> t((size_t) n);
+        for (int64_t oc = 0; oc < OC; ++oc)
+            for (int64_t ic = 0; ic < IC; ++ic)
+                for (int64_t kw = 0; kw < KW; ++kw) t[(size_t) ((oc * KW + kw) * IC + ic)] = v[(size_t) ((oc * IC + ic) * KW + kw)];
+        v.swap(t);
+    }
+    hipError_t e;
+    if (x.kind == K_VEC || x.f32) {
+        float a = 0.0f;
+        for (int64_t i = 0; i < n; ++i) a = fmaxf(a, fabsf(src[i]));
+        x.amax = a;
+        if (x.name == "sync_pos_emb") m->h_pos_emb.assign(src, src + n);
+        if (x.name == "empty_string_feat") m->h_empty_str.assign(src, src + n);
+        if (x.name == "empty_t5_feat") m->h_empty_t5.assign(src, src + n);
+        e = hipMemcpy(m->blob + x.offset, v.data(), 4 * (size_t) n, hipMemcpyHostToDevice);
+    } else {
+        std::vector<uint16_t> bf((size_t) n);
+        for (int64_t i = 0; i < n; ++i) {
+            uint32_t u;
+            memcpy(&u, &v[i], 4);
+            bf[i] = (u & 0x7fffffffu) > 0x7f800000u ? (uint16_t) ((u >> 16) | 64u)
+                                                      : (uint16_t) ((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+        }
+        e = hipMemcpy(m->blob + x.offset, bf.data(), 2 * (size_t) n, hipMemcpyHostToDevice);
+    }
+    return hipcheck(e, "mmdit set_tensor copy");
+}
+
+// ------------------------------------------------------------------ forward
+namespace {
+
+int check_fwd(const tsk_mmdit *m, int B, int T, int clip_S, int sync_S) {
+    const tsk_mmdit_config &c = m->cfg;
+    if (B < 1 || B > c.max_batch) return fail(TSK_ERR_SHAPE, "B=%d outside [1, %d]", B, c.max_batch);
+    if (T < 1 || T > c.max_latent) return fail(TSK_ERR_SHAPE, "T=%d outside [1, %d]", T, c.max_latent);
+    if (clip_S < 1 || clip_S > c.max_clip) return fail(TSK_ERR_SHAPE, "clip_S=%d outside [1, %d]", clip_S, c.max_clip);
+    if (sync_S < 8 || sync_S > c.max_sync || sync_S % 8)
+        return fail(TSK_ERR_SHAPE, "sync_S=%d must be a multiple of 8 in [8, %d]", sync_S, c.max_sync);
+    return require_init();
+}
+
+// inputs per batch row (HOST): latent [L][T], clip [clip_S][clip_dim], sync
+// [sync_S][sync_dim], text [text_seq][clip_dim], t5 [text_seq][t5_dim], g
+// [clip_dim]; flow [T][L] (HOST)
+struct Inputs {
+    const float *const *latent, *const *clip, *const *sync, *const *text, *const *t5, *const *g;
+    const float *t;
+};
+
+int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Inputs &in, float *const *flow,
+                 hipStream_t st) {
+    const tsk_mmdit_config &c = m->cfg;
+    const int H = c.hidden, L = c.latent_dim, X = 2 * c.text_seq, nj = c.depth - c.fused_depth;
+    const int Ntot = T + clip_S + X;
+    int rc;
+    // ---- host staging: the latent transposed to rows (the ggml_transpose of
+    // :151), sync + per-segment pos_emb (:169-172), text_f padded to t5_dim
+    // and concatenated with t5 along the sequence (:179-180), the timestep
+    // embedding (:305-314, host fp32 as the reference)
+    const size_t n_lat = (size_t) B * T * L, n_clip = (size_t) B * clip_S * c.clip_dim,
+                 n_sync = (size_t) B * sync_S * c.sync_dim, n_txt = (size_t) B * X * c.t5_dim, n_g = (size_t) B * c.clip_dim,
+                 n_t = (size_t) B * H;
+    std::vector<float> hs(n_lat + n_clip + n_sync + n_txt + n_g + n_t, 0.0f);
+    float *h_lat = hs.data(), *h_clip = h_lat + n_lat, *h_sync = h_clip + n_clip, *h_txt = h_sync + n_sync,
+          *h_g = h_txt + n_txt, *h_t = h_g + n_g;
+    const float fscale_t = 10000.0f / c.t_max_period;
+    for (int b = 0; b < B; ++b) {
+        for (int ch = 0; ch < L; ++ch)
+            for (int t = 0; t < T; ++t) h_lat[((size_t) b * T + t) * L + ch] = in.latent[b][(size_t) ch * T + t];
+        memcpy(h_clip + (size_t) b * clip_S * c.clip_dim, in.clip[b], sizeof(float) * clip_S * c.clip_dim);
+        for (int s = 0; s < sync_S; ++s)
+            for (int ch = 0; ch < c.sync_dim; ++ch)
+                h_sync[((size_t) b * sync_S + s) * c.sync_dim + ch] =
+                    in.sync[b][(size_t) s * c.sync_dim + ch] + m->h_pos_emb[(size_t) (s % 8) * c.sync_dim + ch];
+        for (int s = 0; s < c.text_seq; ++s) {
+            memcpy(h_txt + ((size_t) b * X + s) * c.t5_dim, in.text[b] + (size_t) s * c.clip_dim, sizeof(float) * c.clip_dim);
+            memcpy(h_txt + ((size_t) b * X + c.text_seq + s) * c.t5_dim, in.t5[b] + (size_t) s * c.t5_dim,
+                   sizeof(float) * c.t5_dim);
+        }
+        memcpy(h_g + (size_t) b * c.clip_dim, in.g[b], sizeof(float) * c.clip_dim);
+        for (int kk = 0; kk < H / 2; ++kk) {
+            const float fr = fscale_t * powf(10000.0f, -2.0f * (float) kk / (float) H);
+            h_t[(size_t) b * H + kk] = cosf(in.t[b] * fr);
+            h_t[(size_t) b * H + H / 2 + kk] = sinf(in.t[b] * fr);
+        }
+    }
+    if (hs.size() > m->in_cap) return fail(TSK_ERR_SHAPE, "staged inputs exceed the capacity");
+    float *d32 = m->in32;
+    if ((rc = hipcheck(hipMemcpyAsync(d32, hs.data(), sizeof(float) * hs.size(), hipMemcpyHostToDevice, st), "inputs")))
+        return rc;
+    // bf16 copies of every staged input (the BF16 mul_mats round their src1)
+    uint16_t *d16 = m->in16;
+    if ((rc = hipcheck(launch_f32_to_bf16(d32, d16, (int64_t) hs.size(), st), "inputs bf16"))) return rc;
+    const uint16_t *x_lat = d16, *x_clip = x_lat + n_lat, *x_sync = x_clip + n_clip, *x_txt = x_sync + n_sync,
+                   *x_g = x_txt + n_txt;
+    const float *t_freq = d32 + (n_lat + n_clip + n_sync + n_txt + n_g);
+    float *v = m->vec;   // [8][B][H]
+    float *te0 = v, *te = v + B * H, *tfc = v + 2 * B * H, *cmean = v + 3 * B * H, *cfc = v + 4 * B * H,
+          *gsum = v + 5 * B * H, *gc = v + 6 * B * H;
+    uint16_t *v16 = m->vec16, *a16 = m->act16;
+
+    // ---- audio_input_proj: conv k3 -> silu -> convMLP (:150-155)
+    if ((rc = conv(conv_of(m, "audio_input_proj.0", true), x_lat, L, (int64_t) T * L, T, B, 1, m->tmp32, H, false, st)))
+        return rc;
+    if ((rc = hipcheck(launch_silu_bf16(m->tmp32, a16, (int64_t) B * T * H, st), "silu"))) return rc;
+    if ((rc = conv_mlp(m, conv_of(m, "audio_input_proj.2.w1", false), conv_of(m, "audio_input_proj.2.w3", false),
+                       conv_of(m, "audio_input_proj.2.w2", false), a16, H, (int64_t) T * H, T, B, m->lat, H, st)))
+        return rc;
+    m->stages.clear();
+    if ((rc = grab(m, "x_in", m->lat, (size_t) B * T * H, st))) return rc;
+    // ---- t_embed MLP on the frequency embedding (:157-161), F32 weights
+    if ((rc = lin_f32(lin_of(m, "t_embed.mlp.0", true), t_freq, B, te0, st))) return rc;
+    if ((rc = hipcheck(launch_silu_inplace(te0, (int64_t) B * H, st), "silu"))) return rc;
+    if ((rc = lin_f32(lin_of(m, "t_embed.mlp.2", true), te0, B, te, st))) return rc;
+    if ((rc = grab(m, "t_emb", te, (size_t) B * H, st))) return rc;
+    // ---- clip: linear -> silu -> convMLP (:163-167)
+    if ((rc = lin(lin_of(m, "clip_input_proj.0", true), x_clip, c.clip_dim, B * clip_S, m->tmp32, H, false, st))) return rc;
+    if ((rc = hipcheck(launch_silu_bf16(m->tmp32, a16, (int64_t) B * clip_S * H, st), "silu"))) return rc;
+    if ((rc = conv_mlp(m, conv_of(m, "clip_input_proj.2.w1", false), conv_of(m, "clip_input_proj.2.w3", false),
+                       conv_of(m, "clip_input_proj.2.w2", false), a16, H, (int64_t) clip_S * H, clip_S, B, m->clip, H,
+                       st)))
+        return rc;
+    if ((rc = grab(m, "clip_pp", m->clip, (size_t) B * clip_S * H, st))) return rc;
+    // ---- sync: conv k7 (padding 3) -> silu -> convMLP (:168-177)
+    if ((rc = conv(conv_of(m, "sync_input_proj.0", true), x_sync, c.sync_dim, (int64_t) sync_S * c.sync_dim, sync_S, B, 3,
+                   m->tmp32, H, false, st)))
+        return rc;
+    if ((rc = hipcheck(launch_silu_bf16(m->tmp32, a16, (int64_t) B * sync_S * H, st), "silu"))) return rc;
+    if ((rc = conv_mlp(m, conv_of(m, "sync_input_proj.2.w1", false), conv_of(m, "sync_input_proj.2.w3", false),
+                       conv_of(m, "sync_input_proj.2.w2", false), a16, H, (int64_t) sync_S * H, sync_S, B, m->sync, H,
+                       st)))
+        return rc;
+    // ---- text: linear (t5_dim -> H) -> silu -> MLP (:179-183)
+    if ((rc = lin(lin_of(m, "text_input_proj.0", true), x_txt, c.t5_dim, B * X, m->tmp32, H, false, st))) return rc;
+    if ((rc = hipcheck(launch_silu_bf16(m->tmp32, a16, (int64_t) B * X * H, st), "silu"))) return rc;
+    if ((rc = lin_mlp(m, lin_of(m, "text_input_proj.2.w1", false), lin_of(m, "text_input_proj.2.w3", false),
+                      lin_of(m, "text_input_proj.2.w2", false), a16, H, B * X, m->txt, H, st)))
+        return rc;
+    if ((rc = grab(m, "text_pp", m->txt, (size_t) B * X * H, st))) return rc;
+    // ---- conditioning vectors (:184-196)
+    if ((rc = lin(lin_of(m, "text_cond_proj", true), x_g, c.clip_dim, B, tfc, H, false, st))) return rc;
+    if ((rc = hipcheck(launch_row_mean(m->clip, B, clip_S, H, cmean, st), "clip mean"))) return rc;
+    if ((rc = hipcheck(launch_f32_to_bf16(cmean, v16, (int64_t) B * H, st), "bf16"))) return rc;
+    if ((rc = lin(lin_of(m, "clip_cond_proj", true), v16, H, B, cfc, H, false, st))) return rc;
+    if ((rc = hipcheck(launch_add_f32(cfc, tfc, gsum, (int64_t) B * H, st), "add"))) return rc;
+    if ((rc = hipcheck(launch_f32_to_bf16(gsum, v16, (int64_t) B * H, st), "bf16"))) return rc;
+    if ((rc = lin_mlp(m, lin_of(m, "global_cond_mlp.w1", false), lin_of(m, "global_cond_mlp.w3", false),
+                      lin_of(m, "global_cond_mlp.w2", false), v16, H, B, gc, H, st)))
+        return rc;
+    if ((rc = grab(m, "clip_fc", cfc, (size_t) B * H, st)) || (rc = grab(m, "text_fc", tfc, (size_t) B * H, st)) ||
+        (rc = grab(m, "gcmlp", gc, (size_t) B * H, st)))
+        return rc;
+    if ((rc = hipcheck(launch_add_f32(gc, te, gc, (int64_t) B * H, st), "add"))) return rc;
+    if ((rc = hipcheck(launch_sync_extend(m->sync, B, sync_S, T, H, gc, m->ext, st), "extended_c"))) return rc;
+    if ((rc = grab(m, "global_c", gc, (size_t) B * H, st)) || (rc = grab(m, "extended_c", m->ext, (size_t) B * T * H, st)))
+        return rc;
+    // silu(extended_c) and silu(global_c), the adaLN inputs (:209)
+    if ((rc = hipcheck(launch_silu_bf16(m->ext, m->silu_ext, (int64_t) B * T * H, st), "silu"))) return rc;
+    if ((rc = hipcheck(launch_silu_bf16(gc, m->silu_gc, (int64_t) B * H, st), "silu"))) return rc;
+    // clip RoPE: positions 0 .. clip_S - 1, freq_scale T / clip_S (:237, :318)
+    if ((rc = hipcheck(launch_rope_table(m->rope_c, clip_S, 64, powf(c.rope_theta, -2.0f / 64.0f),
+                                         (float) T / (float) clip_S, st),
+                       "clip rope table")))
+        return rc;
+
+    // ---- joint blocks over latent | clip | text (:238-271)
+    const size_t rL = 0, rC = (size_t) B * T, rX = rC + (size_t) B * clip_S;   // stream rows in xn / part
+    Stream Ls, Cs, Xs;
+    memset(&Ls, 0, sizeof(Ls));
+    memset(&Cs, 0, sizeof(Cs));
+    memset(&Xs, 0, sizeof(Xs));
+    Ls.x = m->lat; Ls.S = T; Ls.tok_off = 0; Ls.rope_cs = m->rope_l; Ls.per_token = 1;
+    Ls.xn = m->xn + rL * H; Ls.part = m->part + rL * H;
+    Cs.x = m->clip; Cs.S = clip_S; Cs.tok_off = T; Cs.rope_cs = m->rope_c; Cs.per_token = 0;
+    Cs.xn = m->xn + rC * H; Cs.part = m->part + rC * H;
+    Xs.x = m->txt; Xs.S = X; Xs.tok_off = T + clip_S; Xs.rope_cs = nullptr; Xs.per_token = 0;
+    Xs.xn = m->xn + rX * H; Xs.part = m->part + rX * H;
+    // a block's residual updates are applied by the next LayerNorm launch:
+    // the stage tensors after block 0 and after the joint blocks are taken
+    // right after that launch
+    bool cap_jb0 = false, cap_joint = false;
+    auto capture = [&]() -> int {
+        int r = TSK_OK;
+        if (cap_jb0) {
+            cap_jb0 = false;
+            if ((r = grab(m, "jb0_lat", m->lat, (size_t) B * T * H, st)) ||
+                (r = grab(m, "jb0_clip", m->clip, (size_t) B * clip_S * H, st)) ||
+                (r = grab(m, "jb0_text", m->txt, (size_t) B * X * H, st)))
+                return r;
+        }
+        if (cap_joint) {
+            cap_joint = false;
+            r = grab(m, "after_joint", m->lat, (size_t) B * T * H, st);
+        }
+        return r;
+    };
+    int blk = 0;
+    for (int i = 0; i < nj; ++i, ++blk) {
+        Ls.w = &m->jl[i];
+        Cs.w = &m->jc[i];
+        Xs.w = &m->jt[i];
+        Ls.mod = m->mod_l[blk & 1];
+        Cs.mod = m->mod_c[blk & 1];
+        Xs.mod = m->mod_t[blk & 1];
+        Stream r3[3] = {Ls, Cs, Xs};
+        if ((rc = run_mods(m, r3, 3, B, T, st))) return rc;
+        if ((rc = run_ln(m, r3, 3, B, 0, st)) || (rc = capture())) return rc;
+        if ((rc = run_qkv(m, r3, 3, B, Ntot, st))) return rc;
+        if ((rc = run_attention(m, r3, 3, B, Ntot, st))) return rc;
+        if ((rc = run_post(m, r3, 3, B, st))) return rc;
+        Ls = r3[0];
+        Cs = r3[1];
+        Xs = r3[2];
+        cap_jb0 = i == 0;
+    }
+    cap_joint = true;
+    // ---- fused blocks on the latent with extended_c (:274-281)
+    for (int i = 0; i < c.fused_depth; ++i, ++blk) {
+        Ls.w = &m->fb[i];
+        Ls.mod = m->mod_l[blk & 1];
+        if ((rc = run_mods(m, &Ls, 1, B, T, st))) return rc;
+        if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
+        if ((rc = run_qkv(m, &Ls, 1, B, T, st))) return rc;
+        if ((rc = run_attention(m, &Ls, 1, B, T, st))) return rc;
+        if ((rc = run_post(m, &Ls, 1, B, st))) return rc;
+    }
+    // ---- final layer: adaLN(extended_c) -> LN / modulate -> conv k7 (:284-289)
+    Block fin;
+    memset(&fin, 0, sizeof(fin));
+    fin.nmod = 2;
+    fin.ada = lin_of(m, "final_layer.adaLN_modulation.1", true);
+    Ls.w = &fin;
+    Ls.mod = m->mod_l[blk & 1];
+    if ((rc = run_mods(m, &Ls, 1, B, T, st))) return rc;
+    if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
+    if ((rc = grab(m, "after_fused", m->lat, (size_t) B * T * H, st))) return rc;
+    const Conv fc = conv_of(m, "final_layer.conv", true);
+    if ((rc = conv(fc, Ls.xn, H, (int64_t) T * H, T, B, 3, m->tmp32, L, false, st))) return rc;
+    std::vector<float> hf((size_t) B * T * L);
+    if ((rc = hipcheck(hipMemcpyAsync(hf.data(), m->tmp32, sizeof(float) * hf.size(), hipMemcpyDeviceToHost, st), "flow")))
+        return rc;
+    if ((rc = hipcheck(hipStreamSynchronize(st), "sync"))) return rc;
+    for (int b = 0; b < B; ++b) memcpy(flow[b], hf.data() + (size_t) b * T * L, sizeof(float) * T * L);
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" int tsk_mmdit_forward(tsk_mmdit *m, int B, int T, const float *latent, const float *t, int clip_S,
+                                 const float *clip_f, int sync_S, const float *sync_f, const float *text_f,
+                                 const float *t5, const float *global_text, float *flow, tsk_stream stream) {
+    if (!m || !latent || !t || !clip_f || !sync_f || !text_f || !t5 || !global_text || !flow)
+        return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    int rc = check_fwd(m, B, T, clip_S, sync_S);
+    if (rc) return rc;
+    const tsk_mmdit_config &c = m->cfg;
+    std::vector<const float *> pl(B), pc(B), ps(B), px(B), p5(B), pg(B);
+    std::vector<float *> pf(B);
+    for (int b = 0; b < B; ++b) {
+        pl[b] = latent + (size_t) b * c.latent_dim * T;
+        pc[b] = clip_f + (size_t) b * clip_S * c.clip_dim;
+        ps[b] = sync_f + (size_t) b * sync_S * c.sync_dim;
+        px[b] = text_f + (size_t) b * c.text_seq * c.clip_dim;
+        p5[b] = t5 + (size_t) b * c.text_seq * c.t5_dim;
+        pg[b] = global_text + (size_t) b * c.clip_dim;
+        pf[b] = flow + (size_t) b * T * c.latent_dim;
+    }
+    Inputs in{pl.data(), pc.data(), ps.data(), px.data(), p5.data(), pg.data(), t};
+    return forward_impl(m, B, T, clip_S, sync_S, in, pf.data(), (hipStream_t) stream);
+}
+
+extern "C" int tsk_mmdit_debug(tsk_mmdit *m, int enable) {
+    if (!m) return fail(TSK_ERR_INVALID_ARG, "m is NULL");
+    m->debug = enable != 0;
+    if (!m->debug) m->stages.clear();
+    return TSK_OK;
+}
+
+extern "C" int64_t tsk_mmdit_debug_size(const tsk_mmdit *m, const char *name) {
+    if (!m || !name) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = m->stages.find(name);
+    return it == m->stages.end() ? (int64_t) fail(TSK_ERR_INVALID_ARG, "no stage '%s'", name) : (int64_t) it->second.size();
+}
+
+extern "C" int tsk_mmdit_debug_get(const tsk_mmdit *m, const char *name, float *out, int64_t n) {
+    if (!m || !name || !out) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = m->stages.find(name);
+    if (it == m->stages.end()) return fail(TSK_ERR_INVALID_ARG, "no stage '%s'", name);
+    if ((size_t) n != it->second.size()) return fail(TSK_ERR_SHAPE, "stage '%s' has %zu values", name, it->second.size());
+    memcpy(out, it->second.data(), sizeof(float) * (size_t) n);
+    return TSK_OK;
+}
+
+// ts_dit::sample (src/mmdit.cpp:344-376): per step one forward of B = 2 rows,
+// row 0 conditional, row 1 unconditional (the learned empty_string_feat /
+// empty_t5_feat and a zero global text feature, :350-357); v = u + cfg (c - u)
+// and x += dt v on the host in the reference's order
+extern "C" int tsk_mmdit_sample(tsk_mmdit *m, int T, const float *noise, int clip_S, const float *clip_f, int sync_S,
+                                const float *sync_f, const float *text_f, const float *t5, const float *global_text,
+                                int steps, float cfg_scale, float *out, float *flow0, tsk_stream stream) {
+    if (!m || !noise || !clip_f || !sync_f || !text_f || !t5 || !global_text || !out)
+        return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    if (m->cfg.max_batch < 2) return fail(TSK_ERR_SHAPE, "CFG needs max_batch >= 2");
+    if (steps < 1) return fail(TSK_ERR_INVALID_ARG, "steps=%d", steps);
+    int rc = check_fwd(m, 2, T, clip_S, sync_S);
+    if (rc) return rc;
+    const tsk_mmdit_config &c = m->cfg;
+    const int L = c.latent_dim;
+    std::vector<float> x(noise, noise + (size_t) T * L), zeros((size_t) c.clip_dim, 0.0f);
+    std::vector<float> fc((size_t) T * L), fu((size_t) T * L);
+    for (int s = 0; s < steps; ++s) {
+        const float t_curr = 1.0f - (float) s / (float) steps;
+        const float t_prev = 1.0f - (float) (s + 1) / (float) steps;
+        const float dt = t_prev - t_curr;
+        const float tt[2] = {t_curr, t_curr};
+        const float *pl[2] = {x.data(), x.data()}, *pc[2] = {clip_f, clip_f}, *ps[2] = {sync_f, sync_f};
+        const float *px[2] = {text_f, m->h_empty_str.data()}, *p5[2] = {t5, m->h_empty_t5.data()},
+                    *pg[2] = {global_text, zeros.data()};
+        float *pf[2] = {fc.data(), fu.data()};
+        Inputs in{pl, pc, ps, px, p5, pg, tt};
+        if ((rc = forward_impl(m, 2, T, clip_S, sync_S, in, pf, (hipStream_t) stream))) return rc;
+        // fc, fu are [T][L] (ne0 = L); x is [L][T] (ne0 = T)
+        for (int ch = 0; ch < L; ++ch)
+            for (int t = 0; t < T; ++t) {
+                const float fcv = fc[(size_t) t * L + ch], fuv = fu[(size_t) t * L + ch];
+                const float vv = fuv + (fcv - fuv) * cfg_scale;
+                if (s == 0 && flow0) flow0[(size_t) ch * T + t] = vv;
+                x[(size_t) ch * T + t] += dt * vv;
+            }
+    }
+    memcpy(out, x.data(), sizeof(float) * x.size());
+    return TSK_OK;
+}

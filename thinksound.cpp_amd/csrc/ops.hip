@@ -925,6 +925,65 @@ hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- glue of the reference graph (src/mmdit.cpp:150-200, :285-289)
+
+// y = bf16(silu(x)) (silu before the bf16 conversion of a BF16 mul_mat's src1)
+__global__ void silu_bf16_kernel(const float *x, uint16_t *y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    y[i] = f32_to_bf16_bits(v / (1.0f + expf(-v)));
+}
+
+// y[i] = a[i] + b[i] (f32)
+__global__ void add_f32_kernel(const float *a, const float *b, float *y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i] + b[i];
+}
+
+// mean over the S rows of each batch item: x [B][S][H] -> y [B][H]; the sum
+// in double rounded to fp32, then divided by S (ggml_mean, src/mmdit.cpp:186)
+__global__ void row_mean_kernel(const float *x, int S, int H, float *y) {
+    const int b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= H) return;
+    const float *xb = x + (int64_t) b * S * H + c;
+    double s = 0.0;
+    for (int i = 0; i < S; ++i) s += (double) xb[(int64_t) i * H];
+    y[(int64_t) b * H + c] = (float) s / (float) S;
+}
+
+// extended_c[b][t] = sync[b][idx(t)] + g[b], idx(t) = floor((t + 0.5) S / T)
+// (ggml_get_rows with the nearest-exact index of src/mmdit.cpp:319, then the
+// broadcast add of global_c, :196)
+__global__ void sync_extend_kernel(const float *sync, int S, int T, int H, const float *g, float *y) {
+    const int t = blockIdx.x, b = blockIdx.y;
+    const int idx = min((int) floorf(((float) t + 0.5f) * (float) S / (float) T), S - 1);
+    const float *src = sync + ((int64_t) b * S + idx) * H;
+    const float *gb = g + (int64_t) b * H;
+    float *dst = y + ((int64_t) b * T + t) * H;
+    for (int c = threadIdx.x; c < H; c += blockDim.x) dst[c] = src[c] + gb[c];
+}
+
+hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s) {
+    launch_kernel(silu_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_f32(const float *a, const float *b, float *y, int64_t n, hipStream_t s) {
+    launch_kernel(add_f32_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, a, b, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_mean(const float *x, int B, int S, int H, float *y, hipStream_t s) {
+    launch_kernel(row_mean_kernel, dim3(blocks_for(H, 256), B), dim3(256), 0, s, x, S, H, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_sync_extend(const float *sync, int B, int S, int T, int H, const float *g, float *y, hipStream_t s) {
+    launch_kernel(sync_extend_kernel, dim3(T, B), dim3(256), 0, s, sync, S, T, H, g, y);
+    return hipGetLastError();
+}
+
 hipError_t launch_proj_f32_cm(const uint16_t *w, const float *bias, const float *x, int T, int N, int K, int M,
                               float *y, int64_t ld_y, float *tmp, hipStream_t s) {
     if (N < 1 || M < 1 || K < 8 || K % 8 || T < 1 || N % T) return hipErrorInvalidValue;

@@ -329,6 +329,13 @@ hipError_t launch_proj_f32_cm(const uint16_t *w, const float *bias, const float 
 struct TimeVals { float t[32]; };
 hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, int H, float *temb,
                                  hipStream_t s);
+// glue of the reference graph: y = bf16(silu(x)); y = a + b; the mean over
+// the S rows of [B][S][H]; extended_c = sync rows at floor((t + 0.5) S / T)
+// plus g[b] (nearest-exact interpolation of src/mmdit.cpp:319, :196)
+hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s);
+hipError_t launch_add_f32(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
+hipError_t launch_row_mean(const float *x, int B, int S, int H, float *y, hipStream_t s);
+hipError_t launch_sync_extend(const float *sync, int B, int S, int T, int H, const float *g, float *y, hipStream_t s);
 // CFG combine + Euler step: x[i] += dt * (fu + (fc - fu) * cfg); flow0 optional
 hipError_t launch_cfg_euler(const float *flow2, int64_t n, float cfg, float dt, float *x,
                             float *x2, float *flow0, hipStream_t s);

@@ -51,6 +51,13 @@ class DitConfig(ctypes.Structure):
         [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
 
 
+class MMDitConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
+        "sync_dim", "t5_dim", "mlp_hidden", "max_batch", "max_latent", "max_clip", "max_sync")] + \
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")]
+
+
 _lib = None
 
 
@@ -127,6 +134,18 @@ def load():
         "tsk_dit_forward": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_forward_device": ([vp, i, i, vp, vp, vp, vp, vp], i),
         "tsk_dit_sample": ([vp, i, vp, vp, vp, i, f, vp, vp, vp], i),
+        "tsk_mmdit_default_config": ([ctypes.POINTER(MMDitConfig)], None),
+        "tsk_mmdit_create": ([ctypes.POINTER(MMDitConfig), ctypes.POINTER(vp)], i),
+        "tsk_mmdit_destroy": ([vp], None),
+        "tsk_mmdit_n_tensors": ([vp], i),
+        "tsk_mmdit_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)], i),
+        "tsk_mmdit_tensor_type": ([vp, i], i),
+        "tsk_mmdit_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_mmdit_forward": ([vp, i, i, vp, vp, i, vp, i, vp, vp, vp, vp, vp, vp], i),
+        "tsk_mmdit_sample": ([vp, i, vp, i, vp, i, vp, vp, vp, vp, i, f, vp, vp, vp], i),
+        "tsk_mmdit_debug": ([vp, i], i),
+        "tsk_mmdit_debug_size": ([vp, ctypes.c_char_p], ctypes.c_int64),
+        "tsk_mmdit_debug_get": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
         "tsk_dit_timing": ([vp, i], i),
         "tsk_dit_timing_read": ([vp, i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
                                  ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], i),
@@ -768,6 +787,121 @@ class Dit:
         check(load().tsk_dit_sample(self.h, T, noise.ctypes.data, text_cond.ctypes.data,
                                     text_uncond.ctypes.data, steps, cfg_scale, out.ctypes.data,
                                     flow0.ctypes.data, _stream()))
+        return out, flow0
+
+
+# ---------------------------------------------------------------- the reference's MM-DiT graph
+def mmdit_config(**kw):
+    c = MMDitConfig()
+    load().tsk_mmdit_default_config(ctypes.byref(c))
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+def mmdit_synthetic_weights(tensors, seed=1234, std=0.02):
+    """Seeded random-init weights {name: float32 array in ggml / PyTorch order}
+    for [(name, ne, type)]: BF16 tensors N(0, std) rounded to bf16 (RNE), F32
+    matrices and biases N(0, std), q/k norm weights 1 + N(0, std), the learned
+    empty features N(0, 1). Each tensor has its own stream (seed, crc32(name))."""
+    import zlib
+    out = {}
+    for name, ne, ty in tensors:
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        shape = tuple(int(x) for x in reversed(ne))
+        while len(shape) > 1 and shape[0] == 1:
+            shape = shape[1:]
+        n = int(np.prod(shape))
+        sd = 1.0 if name.startswith("empty_") else std
+        w = rng.standard_normal(n, dtype=np.float32) * np.float32(sd)
+        if name.endswith("norm.weight"):
+            w += np.float32(1.0)
+        if ty == BF16:
+            u = w.view(np.uint32)
+            u = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+            w = u.view(np.float32)
+        out[name] = w.reshape(shape)
+    return out
+
+
+class MMDit:
+    """ts_dit counterpart running the reference's graph (src/mmdit.cpp:119-376):
+    named BF16 / F32 weights on the GPU, forward() and sample()."""
+
+    def __init__(self, cfg=None):
+        init()
+        self.cfg = cfg if cfg is not None else mmdit_config()
+        h = ctypes.c_void_p()
+        check(load().tsk_mmdit_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().tsk_mmdit_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """[(name, ggml ne (3), type id)] of every weight"""
+        L = load()
+        out = []
+        for k_ in range(L.tsk_mmdit_n_tensors(self.h)):
+            nm = ctypes.c_char_p()
+            ne = (ctypes.c_int64 * 4)()
+            check(L.tsk_mmdit_tensor_info(self.h, k_, ctypes.byref(nm), ne))
+            out.append((nm.value.decode(), tuple(ne)[:3], L.tsk_mmdit_tensor_type(self.h, k_)))
+        return out
+
+    def set_tensor(self, name, host_f32):
+        host_f32 = np.ascontiguousarray(host_f32, dtype=np.float32)
+        check(load().tsk_mmdit_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
+
+    @staticmethod
+    def _c(a):
+        return np.ascontiguousarray(a, dtype=np.float32)
+
+    def forward(self, latent, t, clip, sync, text, t5, g):
+        """ts_dit::forward layouts with the batch outermost: latent (B, L, T),
+        t (B,), clip (B, S_c, clip_dim), sync (B, S_s, sync_dim), text
+        (B, text_seq, clip_dim), t5 (B, text_seq, t5_dim), g (B, clip_dim)
+        -> flow (B, T, L)"""
+        latent, t, clip, sync, text, t5, g = (self._c(a) for a in (latent, t, clip, sync, text, t5, g))
+        B, L, T = latent.shape
+        flow = np.empty((B, T, L), np.float32)
+        check(load().tsk_mmdit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data, clip.shape[1],
+                                       clip.ctypes.data, sync.shape[1], sync.ctypes.data, text.ctypes.data,
+                                       t5.ctypes.data, g.ctypes.data, flow.ctypes.data, _stream()))
+        return flow
+
+    def debug(self, enable=True):
+        """keep the stage outputs of every forward (src/mmdit.cpp:333-336)"""
+        check(load().tsk_mmdit_debug(self.h, int(bool(enable))))
+
+    def stage(self, name):
+        """a stage output of the last forward, flat in [B][S][H] order"""
+        L = load()
+        n = L.tsk_mmdit_debug_size(self.h, name.encode())
+        check(int(n) if n < 0 else 0)
+        out = np.empty(int(n), np.float32)
+        check(L.tsk_mmdit_debug_get(self.h, name.encode(), out.ctypes.data, n))
+        return out
+
+    def sample(self, noise, clip, sync, text, t5, g, steps=24, cfg_scale=5.0):
+        """ts_dit::sample layouts: noise (L, T), clip (S_c, clip_dim), sync
+        (S_s, sync_dim), text (text_seq, clip_dim), t5 (text_seq, t5_dim), g
+        (clip_dim,) -> (latent (L, T), flow0 (L, T))"""
+        noise, clip, sync, text, t5, g = (self._c(a) for a in (noise, clip, sync, text, t5, g))
+        L, T = noise.shape
+        out = np.empty_like(noise)
+        flow0 = np.empty_like(noise)
+        check(load().tsk_mmdit_sample(self.h, T, noise.ctypes.data, clip.shape[0], clip.ctypes.data, sync.shape[0],
+                                      sync.ctypes.data, text.ctypes.data, t5.ctypes.data, g.ctypes.data, steps,
+                                      cfg_scale, out.ctypes.data, flow0.ctypes.data, _stream()))
         return out, flow0
 
 
