@@ -596,6 +596,11 @@ int  tsk_mmdit_set_tensor(tsk_mmdit *m, const char *name, const float *host_f32,
 int  tsk_mmdit_forward(tsk_mmdit *m, int B, int T, const float *latent, const float *t, int clip_S,
                        const float *clip_f, int sync_S, const float *sync_f, const float *text_f,
                        const float *t5, const float *global_text, float *flow, tsk_stream stream);
+/* Same with DEVICE arrays (f32, the same layouts) for the inputs and flow,
+ * t [B] on the HOST; no host synchronisation. */
+int  tsk_mmdit_forward_device(tsk_mmdit *m, int B, int T, const float *latent_d, const float *t, int clip_S,
+                              const float *clip_d, int sync_S, const float *sync_d, const float *text_d,
+                              const float *t5_d, const float *global_text_d, float *flow_d, tsk_stream stream);
 /*
  * Stage outputs (the dbg map of ts_dit::forward, src/mmdit.cpp:125, :333-336).
  * With tsk_mmdit_debug(m, 1) every forward keeps, in host memory, the

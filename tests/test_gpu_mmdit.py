@@ -91,6 +91,24 @@ def test_mmdit_small_forward(env):
     m.close()
 
 
+def test_mmdit_forward_device_matches_host(env):
+    """tsk_mmdit_forward_device (device-resident inputs, no host sync) gives
+    the host entry point's bits"""
+    tsk, orc = env
+    m = tsk.MMDit(tsk.mmdit_config(depth=2, fused_depth=1, max_latent=64, max_clip=16, max_sync=48))
+    for k, v in tsk.mmdit_synthetic_weights(m.tensors(), seed=3).items():
+        m.set_tensor(k, v)
+    lat, clip, sync, text, t5, g = inputs(2, 37, 9, 24, seed=21)
+    t = np.array([0.6, 0.25], np.float32)
+    ref = m.forward(lat, t, clip, sync, text, t5, g)
+    dev = [tsk.to_device(a) for a in (lat, clip, sync, text, t5, g)]
+    flow = tsk.empty((2, 37, 64))
+    m.forward_device(dev[0], t, *dev[1:], flow)
+    tsk.synchronize()
+    assert np.array_equal(flow.numpy(), ref)
+    m.close()
+
+
 COND_STAGES = ("x_in", "t_emb", "clip_pp", "text_pp", "clip_fc", "text_fc", "gcmlp", "global_c", "extended_c")
 BLOCK_STAGES = ("jb0_lat", "jb0_clip", "jb0_text", "after_joint", "after_fused")
 

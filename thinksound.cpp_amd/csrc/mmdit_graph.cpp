@@ -81,6 +81,7 @@ struct tsk_mmdit {
     uint16_t *in16 = nullptr;             // bf16 copies of the staged inputs
     float *in32 = nullptr;                // f32 staging of the inputs
     uint16_t *act16 = nullptr;            // bf16(silu(.)) rows of the input projections
+    float *freq = nullptr, *temb = nullptr;   // t-embedding frequencies [H / 2] and embeddings [B][H]
     size_t in_cap = 0;                    // elements of in16 / in32
     int ldv = 0, Nmax = 0, Rmax = 0;
     // stage outputs of the last forward by the reference's debug names
@@ -465,7 +466,7 @@ extern "C" void tsk_mmdit_destroy(tsk_mmdit *m) {
     void *bufs[] = {m->blob, m->lat, m->clip, m->txt, m->sync, m->ext, m->silu_ext, m->silu_gc, m->vec, m->vec16,
                     m->mod_l[0], m->mod_l[1], m->mod_c[0], m->mod_c[1], m->mod_t[0], m->mod_t[1], m->xn, m->hid,
                     m->o, m->q, m->k, m->vt, m->part, m->qkv32, m->tmp32, m->rope_l, m->rope_c, m->in16, m->in32,
-                    m->act16};
+                    m->act16, m->freq, m->temb};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
     delete m;
@@ -533,9 +534,9 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
     m->Rmax = (int) R;
     const int64_t rows3 = (int64_t) B * (T + C + X);
     const int Wmax = std::max(std::max(H, c.t5_dim), std::max(c.sync_dim, c.clip_dim));
-    // staged inputs per batch row: latent, clip, sync, text | t5, global text, t-embedding
+    // staged inputs per batch row: latent, clip, sync, text | t5, global text
     m->in_cap = (size_t) B * ((size_t) T * c.latent_dim + (size_t) C * c.clip_dim + (size_t) S * c.sync_dim +
-                              (size_t) X * c.t5_dim + c.clip_dim + H);
+                              (size_t) X * c.t5_dim + c.clip_dim);
     auto alloc = [&](void **p, size_t bytes) -> int {
         hipError_t e = hipMalloc(p, bytes);
         if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -570,11 +571,19 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         (rc = alloc((void **) &m->rope_c, sizeof(float) * C * 64)) ||
         (rc = alloc((void **) &m->in16, 2 * m->in_cap)) ||
         (rc = alloc((void **) &m->in32, sizeof(float) * m->in_cap)) ||
-        (rc = alloc((void **) &m->act16, 2 * (size_t) R * H))) {
+        (rc = alloc((void **) &m->act16, 2 * (size_t) R * H)) ||
+        (rc = alloc((void **) &m->freq, sizeof(float) * (H / 2))) ||
+        (rc = alloc((void **) &m->temb, sizeof(float) * B * H))) {
         tsk_mmdit_destroy(m);
         return rc;
     }
-    hipError_t e = hipMemset(m->blob, 0, off);
+    // t-embedding frequencies f_k = (1e4 / max_period) 1e4^(-2k / H) in host
+    // fp32 as src/mmdit.cpp:309-311 evaluates them
+    std::vector<float> fr(H / 2);
+    for (int kk = 0; kk < H / 2; ++kk)
+        fr[kk] = (10000.0f / c.t_max_period) * powf(10000.0f, -2.0f * (float) kk / (float) H);
+    hipError_t e = hipMemcpy(m->freq, fr.data(), sizeof(float) * fr.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(m->blob, 0, off);
     // V^T key positions past a call's token count are read (times P = 0)
     if (e == hipSuccess) e = hipMemset(m->vt, 0, 2 * (size_t) B * H * m->ldv);
     // latent positions 0 .. T-1, freq_scale 1 (src/mmdit.cpp:96-99, :316-318)
@@ -673,58 +682,87 @@ int check_fwd(const tsk_mmdit *m, int B, int T, int clip_S, int sync_S) {
 // inputs per batch row (HOST): latent [L][T], clip [clip_S][clip_dim], sync
 // [sync_S][sync_dim], text [text_seq][clip_dim], t5 [text_seq][t5_dim], g
 // [clip_dim]; flow [T][L] (HOST)
+// the inputs of one forward: HOST rows (one pointer per batch row, each in
+// ts_dit::forward's layout) or DEVICE arrays with the batch outermost; t on
+// the host either way
 struct Inputs {
+    bool device;
     const float *const *latent, *const *clip, *const *sync, *const *text, *const *t5, *const *g;
+    const float *d_latent, *d_clip, *d_sync, *d_text, *d_t5, *d_g;
     const float *t;
 };
 
+// flow: per-row HOST outputs (host inputs; the call synchronises) or one
+// DEVICE array [B][T][latent_dim] (device inputs; no host synchronisation)
 int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Inputs &in, float *const *flow,
-                 hipStream_t st) {
+                 float *d_flow, hipStream_t st) {
     const tsk_mmdit_config &c = m->cfg;
     const int H = c.hidden, L = c.latent_dim, X = 2 * c.text_seq, nj = c.depth - c.fused_depth;
     const int Ntot = T + clip_S + X;
     int rc;
-    // ---- host staging: the latent transposed to rows (the ggml_transpose of
-    // :151), sync + per-segment pos_emb (:169-172), text_f padded to t5_dim
-    // and concatenated with t5 along the sequence (:179-180), the timestep
-    // embedding (:305-314, host fp32 as the reference)
+    // ---- staging into one f32 area: the latent transposed to rows (the
+    // ggml_transpose of :151), clip, sync + per-segment pos_emb (:169-172),
+    // text_f zero-padded to t5_dim and concatenated with t5 along the
+    // sequence (:179-180), the global text feature
     const size_t n_lat = (size_t) B * T * L, n_clip = (size_t) B * clip_S * c.clip_dim,
-                 n_sync = (size_t) B * sync_S * c.sync_dim, n_txt = (size_t) B * X * c.t5_dim, n_g = (size_t) B * c.clip_dim,
-                 n_t = (size_t) B * H;
-    std::vector<float> hs(n_lat + n_clip + n_sync + n_txt + n_g + n_t, 0.0f);
-    float *h_lat = hs.data(), *h_clip = h_lat + n_lat, *h_sync = h_clip + n_clip, *h_txt = h_sync + n_sync,
-          *h_g = h_txt + n_txt, *h_t = h_g + n_g;
-    const float fscale_t = 10000.0f / c.t_max_period;
-    for (int b = 0; b < B; ++b) {
-        for (int ch = 0; ch < L; ++ch)
-            for (int t = 0; t < T; ++t) h_lat[((size_t) b * T + t) * L + ch] = in.latent[b][(size_t) ch * T + t];
-        memcpy(h_clip + (size_t) b * clip_S * c.clip_dim, in.clip[b], sizeof(float) * clip_S * c.clip_dim);
-        for (int s = 0; s < sync_S; ++s)
-            for (int ch = 0; ch < c.sync_dim; ++ch)
-                h_sync[((size_t) b * sync_S + s) * c.sync_dim + ch] =
-                    in.sync[b][(size_t) s * c.sync_dim + ch] + m->h_pos_emb[(size_t) (s % 8) * c.sync_dim + ch];
-        for (int s = 0; s < c.text_seq; ++s) {
-            memcpy(h_txt + ((size_t) b * X + s) * c.t5_dim, in.text[b] + (size_t) s * c.clip_dim, sizeof(float) * c.clip_dim);
-            memcpy(h_txt + ((size_t) b * X + c.text_seq + s) * c.t5_dim, in.t5[b] + (size_t) s * c.t5_dim,
-                   sizeof(float) * c.t5_dim);
-        }
-        memcpy(h_g + (size_t) b * c.clip_dim, in.g[b], sizeof(float) * c.clip_dim);
-        for (int kk = 0; kk < H / 2; ++kk) {
-            const float fr = fscale_t * powf(10000.0f, -2.0f * (float) kk / (float) H);
-            h_t[(size_t) b * H + kk] = cosf(in.t[b] * fr);
-            h_t[(size_t) b * H + H / 2 + kk] = sinf(in.t[b] * fr);
-        }
-    }
-    if (hs.size() > m->in_cap) return fail(TSK_ERR_SHAPE, "staged inputs exceed the capacity");
+                 n_sync = (size_t) B * sync_S * c.sync_dim, n_txt = (size_t) B * X * c.t5_dim, n_g = (size_t) B * c.clip_dim;
+    const size_t n_all = n_lat + n_clip + n_sync + n_txt + n_g;
+    if (n_all > m->in_cap) return fail(TSK_ERR_SHAPE, "staged inputs exceed the capacity");
     float *d32 = m->in32;
-    if ((rc = hipcheck(hipMemcpyAsync(d32, hs.data(), sizeof(float) * hs.size(), hipMemcpyHostToDevice, st), "inputs")))
-        return rc;
+    float *s_lat = d32, *s_clip = s_lat + n_lat, *s_sync = s_clip + n_clip, *s_txt = s_sync + n_sync, *s_g = s_txt + n_txt;
+    if (!in.device) {
+        std::vector<float> hs(n_all, 0.0f);
+        float *h_lat = hs.data(), *h_clip = h_lat + n_lat, *h_sync = h_clip + n_clip, *h_txt = h_sync + n_sync,
+              *h_g = h_txt + n_txt;
+        for (int b = 0; b < B; ++b) {
+            for (int ch = 0; ch < L; ++ch)
+                for (int t = 0; t < T; ++t) h_lat[((size_t) b * T + t) * L + ch] = in.latent[b][(size_t) ch * T + t];
+            memcpy(h_clip + (size_t) b * clip_S * c.clip_dim, in.clip[b], sizeof(float) * clip_S * c.clip_dim);
+            for (int s = 0; s < sync_S; ++s)
+                for (int ch = 0; ch < c.sync_dim; ++ch)
+                    h_sync[((size_t) b * sync_S + s) * c.sync_dim + ch] =
+                        in.sync[b][(size_t) s * c.sync_dim + ch] + m->h_pos_emb[(size_t) (s % 8) * c.sync_dim + ch];
+            for (int s = 0; s < c.text_seq; ++s) {
+                memcpy(h_txt + ((size_t) b * X + s) * c.t5_dim, in.text[b] + (size_t) s * c.clip_dim,
+                       sizeof(float) * c.clip_dim);
+                memcpy(h_txt + ((size_t) b * X + c.text_seq + s) * c.t5_dim, in.t5[b] + (size_t) s * c.t5_dim,
+                       sizeof(float) * c.t5_dim);
+            }
+            memcpy(h_g + (size_t) b * c.clip_dim, in.g[b], sizeof(float) * c.clip_dim);
+        }
+        // the copy returns once the pageable source has been consumed
+        if ((rc = hipcheck(hipMemcpyAsync(d32, hs.data(), sizeof(float) * n_all, hipMemcpyHostToDevice, st), "inputs")))
+            return rc;
+    } else {
+        const float *pe = wp<float>(m, "sync_pos_emb");
+        hipError_t e = launch_transpose_ct(in.d_latent, B, L, T, s_lat, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(s_clip, in.d_clip, sizeof(float) * n_clip, hipMemcpyDeviceToDevice, st);
+        if (e == hipSuccess) e = launch_add_period_rows(in.d_sync, (int64_t) B * sync_S, c.sync_dim, pe, 8, s_sync, st);
+        if (e == hipSuccess) e = hipMemsetAsync(s_txt, 0, sizeof(float) * n_txt, st);
+        for (int b = 0; b < B && e == hipSuccess; ++b) {
+            e = hipMemcpy2DAsync(s_txt + (size_t) b * X * c.t5_dim, sizeof(float) * c.t5_dim,
+                                 in.d_text + (size_t) b * c.text_seq * c.clip_dim, sizeof(float) * c.clip_dim,
+                                 sizeof(float) * c.clip_dim, c.text_seq, hipMemcpyDeviceToDevice, st);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(s_txt + ((size_t) b * X + c.text_seq) * c.t5_dim,
+                                   in.d_t5 + (size_t) b * c.text_seq * c.t5_dim,
+                                   sizeof(float) * c.text_seq * c.t5_dim, hipMemcpyDeviceToDevice, st);
+        }
+        if (e == hipSuccess) e = hipMemcpyAsync(s_g, in.d_g, sizeof(float) * n_g, hipMemcpyDeviceToDevice, st);
+        if ((rc = hipcheck(e, "device inputs"))) return rc;
+    }
     // bf16 copies of every staged input (the BF16 mul_mats round their src1)
     uint16_t *d16 = m->in16;
-    if ((rc = hipcheck(launch_f32_to_bf16(d32, d16, (int64_t) hs.size(), st), "inputs bf16"))) return rc;
+    if ((rc = hipcheck(launch_f32_to_bf16(d32, d16, (int64_t) n_all, st), "inputs bf16"))) return rc;
     const uint16_t *x_lat = d16, *x_clip = x_lat + n_lat, *x_sync = x_clip + n_clip, *x_txt = x_sync + n_sync,
                    *x_g = x_txt + n_txt;
-    const float *t_freq = d32 + (n_lat + n_clip + n_sync + n_txt + n_g);
+    // timestep embedding [cos(t f_k), sin(t f_k)] (:305-314; f_k from the host formula)
+    TimeVals tv;
+    memset(&tv, 0, sizeof(tv));
+    for (int b = 0; b < B; ++b) tv.t[b] = in.t[b];
+    if ((rc = hipcheck(launch_timestep_embed(m->freq, tv, B, H, m->temb, st), "timestep embedding"))) return rc;
+    const float *t_freq = m->temb;
     float *v = m->vec;   // [8][B][H]
     float *te0 = v, *te = v + B * H, *tfc = v + 2 * B * H, *cmean = v + 3 * B * H, *cfc = v + 4 * B * H,
           *gsum = v + 5 * B * H, *gc = v + 6 * B * H;
@@ -866,7 +904,8 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
     if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
     if ((rc = grab(m, "after_fused", m->lat, (size_t) B * T * H, st))) return rc;
     const Conv fc = conv_of(m, "final_layer.conv", true);
-    if ((rc = conv(fc, Ls.xn, H, (int64_t) T * H, T, B, 3, m->tmp32, L, false, st))) return rc;
+    if ((rc = conv(fc, Ls.xn, H, (int64_t) T * H, T, B, 3, in.device ? d_flow : m->tmp32, L, false, st))) return rc;
+    if (in.device) return TSK_OK;
     std::vector<float> hf((size_t) B * T * L);
     if ((rc = hipcheck(hipMemcpyAsync(hf.data(), m->tmp32, sizeof(float) * hf.size(), hipMemcpyDeviceToHost, st), "flow")))
         return rc;
@@ -896,8 +935,22 @@ extern "C" int tsk_mmdit_forward(tsk_mmdit *m, int B, int T, const float *latent
         pg[b] = global_text + (size_t) b * c.clip_dim;
         pf[b] = flow + (size_t) b * T * c.latent_dim;
     }
-    Inputs in{pl.data(), pc.data(), ps.data(), px.data(), p5.data(), pg.data(), t};
-    return forward_impl(m, B, T, clip_S, sync_S, in, pf.data(), (hipStream_t) stream);
+    Inputs in{false, pl.data(), pc.data(), ps.data(), px.data(), p5.data(), pg.data(),
+              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, t};
+    return forward_impl(m, B, T, clip_S, sync_S, in, pf.data(), nullptr, (hipStream_t) stream);
+}
+
+extern "C" int tsk_mmdit_forward_device(tsk_mmdit *m, int B, int T, const float *latent_d, const float *t,
+                                        int clip_S, const float *clip_d, int sync_S, const float *sync_d,
+                                        const float *text_d, const float *t5_d, const float *global_text_d,
+                                        float *flow_d, tsk_stream stream) {
+    if (!m || !latent_d || !t || !clip_d || !sync_d || !text_d || !t5_d || !global_text_d || !flow_d)
+        return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    int rc = check_fwd(m, B, T, clip_S, sync_S);
+    if (rc) return rc;
+    Inputs in{true, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+              latent_d, clip_d, sync_d, text_d, t5_d, global_text_d, t};
+    return forward_impl(m, B, T, clip_S, sync_S, in, nullptr, flow_d, (hipStream_t) stream);
 }
 
 extern "C" int tsk_mmdit_debug(tsk_mmdit *m, int enable) {
@@ -948,8 +1001,8 @@ extern "C" int tsk_mmdit_sample(tsk_mmdit *m, int T, const float *noise, int cli
         const float *px[2] = {text_f, m->h_empty_str.data()}, *p5[2] = {t5, m->h_empty_t5.data()},
                     *pg[2] = {global_text, zeros.data()};
         float *pf[2] = {fc.data(), fu.data()};
-        Inputs in{pl, pc, ps, px, p5, pg, tt};
-        if ((rc = forward_impl(m, 2, T, clip_S, sync_S, in, pf, (hipStream_t) stream))) return rc;
+        Inputs in{false, pl, pc, ps, px, p5, pg, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, tt};
+        if ((rc = forward_impl(m, 2, T, clip_S, sync_S, in, pf, nullptr, (hipStream_t) stream))) return rc;
         // fc, fu are [T][L] (ne0 = L); x is [L][T] (ne0 = T)
         for (int ch = 0; ch < L; ++ch)
             for (int t = 0; t < T; ++t) {

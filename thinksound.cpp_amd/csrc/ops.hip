@@ -964,6 +964,28 @@ __global__ void sync_extend_kernel(const float *sync, int S, int T, int H, const
     for (int c = threadIdx.x; c < H; c += blockDim.x) dst[c] = src[c] + gb[c];
 }
 
+// y[r][c] = x[r][c] + pe[(r % period)][c]
+__global__ void add_period_rows_kernel(const float *x, int64_t rows, int cols, const float *pe, int period, float *y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols;
+    const int c = (int) (i % cols);
+    y[i] = x[i] + pe[(r % period) * cols + c];
+}
+
+hipError_t launch_transpose_ct(const float *x, int B, int C, int T, float *y, hipStream_t s) {
+    const int64_t n = (int64_t) B * C * T;
+    launch_kernel(transpose_ct_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, B, C, T, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_period_rows(const float *x, int64_t rows, int cols, const float *pe, int period, float *y,
+                                  hipStream_t s) {
+    launch_kernel(add_period_rows_kernel, dim3(blocks_for(rows * cols, 256)), dim3(256), 0, s, x, rows, cols, pe,
+                  period, y);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s) {
     launch_kernel(silu_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
     return hipGetLastError();

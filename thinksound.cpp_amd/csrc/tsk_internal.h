@@ -333,6 +333,10 @@ hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, i
 // the S rows of [B][S][H]; extended_c = sync rows at floor((t + 0.5) S / T)
 // plus g[b] (nearest-exact interpolation of src/mmdit.cpp:319, :196)
 hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s);
+// [B][C][T] -> [B][T][C] (f32); y[r][c] = x[r][c] + pe[r % period][c]
+hipError_t launch_transpose_ct(const float *x, int B, int C, int T, float *y, hipStream_t s);
+hipError_t launch_add_period_rows(const float *x, int64_t rows, int cols, const float *pe, int period, float *y,
+                                  hipStream_t s);
 hipError_t launch_add_f32(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
 hipError_t launch_row_mean(const float *x, int B, int S, int H, float *y, hipStream_t s);
 hipError_t launch_sync_extend(const float *sync, int B, int S, int T, int H, const float *g, float *y, hipStream_t s);

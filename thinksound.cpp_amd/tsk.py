@@ -143,6 +143,7 @@ def load():
         "tsk_mmdit_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
         "tsk_mmdit_forward": ([vp, i, i, vp, vp, i, vp, i, vp, vp, vp, vp, vp, vp], i),
         "tsk_mmdit_sample": ([vp, i, vp, i, vp, i, vp, vp, vp, vp, i, f, vp, vp, vp], i),
+        "tsk_mmdit_forward_device": ([vp, i, i, vp, vp, i, vp, i, vp, vp, vp, vp, vp, vp], i),
         "tsk_mmdit_debug": ([vp, i], i),
         "tsk_mmdit_debug_size": ([vp, ctypes.c_char_p], ctypes.c_int64),
         "tsk_mmdit_debug_get": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
@@ -876,6 +877,15 @@ class MMDit:
         check(load().tsk_mmdit_forward(self.h, B, T, latent.ctypes.data, t.ctypes.data, clip.shape[1],
                                        clip.ctypes.data, sync.shape[1], sync.ctypes.data, text.ctypes.data,
                                        t5.ctypes.data, g.ctypes.data, flow.ctypes.data, _stream()))
+        return flow
+
+    def forward_device(self, latent, t, clip, sync, text, t5, g, flow):
+        """DeviceArrays in forward()'s layouts, flow out (B, T, L); t host (B,)"""
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        B, _, T = latent.shape
+        d = lambda a: ctypes.c_void_p(a.data_ptr())
+        check(load().tsk_mmdit_forward_device(self.h, B, T, d(latent), t.ctypes.data, clip.shape[1], d(clip),
+                                              sync.shape[1], d(sync), d(text), d(t5), d(g), d(flow), _stream()))
         return flow
 
     def debug(self, enable=True):
