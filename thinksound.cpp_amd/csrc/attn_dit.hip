@@ -203,6 +203,9 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 
             // S^T - m = K . Q^T + cm: s[mb][4 r + jj] for key 32 mb + 8 r + 4 hi + jj, query l32
             f32x16 s[2];
+#if TSK_ATTN_PRIO
+            __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
                 if constexpr (BOUNDED) {
@@ -221,6 +224,9 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
                                                                         __builtin_bit_cast(f16x8, qraw[ks]), s[mb], 0, 0, 0);
                 }
             }
+#if TSK_ATTN_PRIO
+            __builtin_amdgcn_s_setprio(0);
+#endif
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -275,11 +281,17 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
                         l_run = __builtin_amdgcn_fdot2(pr, one, l_run, false);
                     }
                 // O^T += V^T . P^T
+#if TSK_ATTN_PRIO
+                __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int h2 = 0; h2 < 2; ++h2)
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[db][2 * mb + h2], pf[h2], o[db], 0, 0, 0);
+#if TSK_ATTN_PRIO
+                __builtin_amdgcn_s_setprio(0);
+#endif
             }
         }
         // the next tile has landed (this wave's loads; the barrier covers the others')

@@ -55,9 +55,7 @@ struct RoleTiming {
 
 // split-K slices of the two K-reducing block projections; fixed, so every
 // output element is summed in the same order whatever the batch or length
-constexpr int KSPLIT_OUT = 2;    // linear1 (K = hidden)
-constexpr int KSPLIT_FC2 = 4;    // ffn.fc2 (K = mlp_hidden)
-constexpr int KSPLIT_MAX = 4;
+constexpr int KSPLIT_MAX = 4;    // split-K slices of linear1 (default 2) / ffn.fc2 (default 4), Tuning
 
 struct Q8W {                // a Q8_0 matrix as planes
     const int8_t *q;
@@ -114,6 +112,7 @@ struct tsk_dit {
     // block GEMM tile shape per projection (qkv, out, fc1, fc2): a launch_gemm_ks
     // cfg, or 0 for the shape rule of gemm_cfg_for() (Tuning::gemm_cfg overrides)
     int gemm_cfg[4] = {0, 0, 0, 0};
+    int ksplit_out = 2, ksplit_fc2 = 4;
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
     // second stream for the adaLN GEMVs of the later blocks (HBM-bound) while
@@ -307,6 +306,8 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     // tiles per projection), fixed at create
     d->attn_cfg = tuning().attn_cfg;
     for (int i = 0; i < 4; ++i) d->gemm_cfg[i] = tuning().gemm_cfg[i];
+    d->ksplit_out = tuning().ksplit_out;
+    d->ksplit_fc2 = tuning().ksplit_fc2;
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
     add(d, "audio_input_proj.weight", c.latent_dim, H, true);
@@ -720,13 +721,13 @@ int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         q = gemm_problem(d->o + (size_t) r[i].tok_off * H, H, r[i].w->l1_w, nullptr, r[i].part, H, rows, H, H);
         q.x_group_rows = r[i].S;
         q.x_group_stride = (int64_t) Ntot * H;
-        q.splits = KSPLIT_OUT;
-        r[i].pend_split = KSPLIT_OUT;
+        q.splits = d->ksplit_out;
+        r[i].pend_split = d->ksplit_out;
         r[i].pend_bias = r[i].w->l1_b;
         r[i].pend_gate = mod_of(d, *r[i].w) + 2 * H;   // gate_msa
         r[i].pend_ld_gate = mod_ld(d, *r[i].w);
         fl += 2.0 * rows * H * H;
-        by += 2.0 * H * H + 2.0 * rows * H + 4.0 * KSPLIT_OUT * rows * H;
+        by += 2.0 * H * H + 2.0 * rows * H + 4.0 * d->ksplit_out * rows * H;
     }
     if (!g.nprob) return TSK_OK;
     Timed tm(d, TSK_ROLE_OUT, fl, by, st);
@@ -745,14 +746,14 @@ int run_mlp(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
         g1.p[g1.nprob++] = gemm_problem(r[i].xn, H, r[i].w->fc1_w, r[i].w->fc1_b, r[i].h, F, rows, H, F);
         GemmProblem &q = g2.p[g2.nprob++];
         q = gemm_problem(r[i].h, F, r[i].w->fc2_w, nullptr, r[i].part, H, rows, F, H);
-        q.splits = KSPLIT_FC2;
-        r[i].pend_split = KSPLIT_FC2;
+        q.splits = d->ksplit_fc2;
+        r[i].pend_split = d->ksplit_fc2;
         r[i].pend_bias = r[i].w->fc2_b;
         r[i].pend_gate = mod_of(d, *r[i].w) + 5 * H;   // gate_mlp
         r[i].pend_ld_gate = mod_ld(d, *r[i].w);
         fl += 2.0 * rows * H * F;
         by1 += 2.0 * F * H + 2.0 * rows * H + 2.0 * rows * F;
-        by2 += 2.0 * H * F + 2.0 * rows * F + 4.0 * KSPLIT_FC2 * rows * H;
+        by2 += 2.0 * H * F + 2.0 * rows * F + 4.0 * d->ksplit_fc2 * rows * H;
     }
     if (!g1.nprob) return TSK_OK;
     int rc;

@@ -137,13 +137,15 @@ enum : int {
     MODE_DIRECT = 1,   // K-split waves, operands straight into registers
     MODE_COOP = 2,     // 2 x 2 waves over the tile, one shared LDS ring
     MODE_COOP_PIPE = 3,// MODE_COOP with the next stage's fragments read from LDS during this stage's MFMAs
-    MODE_COOP64 = 4    // MODE_COOP with 64-wide k stages of whole 128-byte rows (swizzled in LDS)
+    MODE_COOP64 = 4,   // MODE_COOP with 64-wide k stages of whole 128-byte rows (swizzled in LDS)
+    MODE_PF = 5        // MODE_COOP64's LDS layout, double-buffered, fed from R stages of register prefetch
 };
 
 template <int TM, int TN, int R, int MODE, int KH = 1>
 constexpr size_t lds_bytes() {
-    constexpr bool coop = MODE == MODE_COOP || MODE == MODE_COOP_PIPE || MODE == MODE_COOP64;
+    constexpr bool coop = MODE == MODE_COOP || MODE == MODE_COOP_PIPE || MODE == MODE_COOP64 || MODE == MODE_PF;
     constexpr size_t ring = MODE == MODE_DIRECT ? 0
+                          : MODE == MODE_PF     ? (size_t) 2 * 2 * (TM + TN) * 1024
                           : MODE == MODE_COOP64 ? (size_t) R * 2 * (TM + TN) * 1024
                           : coop                ? (size_t) R * KH * (TM + TN) * 1024
                                                 : (size_t) 4 * R * (TM + TN) * 1024;
@@ -163,9 +165,9 @@ constexpr bool epi_swiglu(int epi) { return epi == EPI_SWIGLU_F32 || epi == EPI_
 template <int TM, int TN, int R, int MODE, int EPI, int KH, bool CONV>
 __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord tc, uint8_t *lds) {
     constexpr int BM = 16 * TM, BN = 16 * TN, L = TM + TN, STAGE = KH * L * 1024;
-    constexpr bool PIPE = MODE == MODE_COOP_PIPE, C64 = MODE == MODE_COOP64;
+    constexpr bool PIPE = MODE == MODE_COOP_PIPE, PF = MODE == MODE_PF, C64 = MODE == MODE_COOP64 || PF;
     constexpr bool COOP = MODE == MODE_COOP || PIPE || C64, DIRECT = MODE == MODE_DIRECT;
-    static_assert(!COOP || (TM % 2 == 0 && TN % 2 == 0 && L % 4 == 0), "cooperative tile shape");
+    static_assert(!COOP || (TM % 2 == 0 && TN % 2 == 0 && (C64 ? L % 2 : L % 4) == 0), "cooperative tile shape");
     static_assert((COOP && !PIPE && !C64) || KH == 1, "KH: 32-wide k tiles per cooperative stage");
     static_assert(!PIPE || R >= 3, "pipelined fragments need three ring slots");
     static_assert(COOP || (!CONV && !epi_swiglu(EPI)), "convolutions and SwiGLU run cooperative tiles");
@@ -327,6 +329,86 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
         int aro[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) aro[kh] = p.w_tiled ? kh * 1024 + lane * 16 : roff[kh];
+        // every fragment of the stage is read before the first MFMA (the
+        // scheduling barrier keeps the compiler from interleaving reads and
+        // MFMAs, which serialises on the LDS latency): the second half's reads
+        // are in flight during the first half's MFMAs
+        auto compute = [&](const uint8_t *src) {
+            bf16x8 a[2][TMW], b[2][TNW];
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+                for (int i = 0; i < TMW; ++i) a[kh][i] = *(const bf16x8 *) (src + (wm * TMW + i) * USZ + aro[kh]);
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) b[kh][j] = *(const bf16x8 *) (src + (TM + wn * TNW + j) * USZ + roff[kh]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TNW; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kh][i], b[kh][j], acc[i][j], 0, 0, 0);
+        };
+        if constexpr (PF) {
+            // R stages of this wave's loads in flight in registers; LDS holds
+            // two stages (the one being read, the one being written). Every
+            // iteration issues one stage's loads unconditionally (past the
+            // last stage it re-reads the last one), so the count of loads in
+            // flight is the same on every trip and the compiler's own counter
+            // waits (before each LDS write of a register set) wait for exactly
+            // one stage.
+            u32x4 rg[R][LW];
+            auto gload = [&](int t, int set) {
+                t = min(t, ns - 1);
+#pragma unroll
+                for (int q = 0; q < LW; ++q) {
+                    const uint16_t *src = qsrc[q] + (int64_t) t * qstep[q];
+                    if constexpr (CONV) {
+                        const bool isb = q < 4 ? qisb[q] : (wave + 4 * q) / 2 >= TM;
+                        if (isb) {
+                            const int k = (kt0 + 2 * t) * 32, kw = k / p.conv_ic, ic0 = k - kw * p.conv_ic;
+                            const int iw = qconv[q] + kw * p.conv_d;
+                            src = iw >= 0 && iw < p.conv_iw ? qsrc[q] + (int64_t) iw * p.ld_x + ic0 : g_zero_row + qchk[q];
+                        }
+                    }
+                    rg[set][q] = *(const u32x4 *) src;
+                }
+            };
+            auto swrite = [&](int set, int slot) {
+                uint8_t *dst = lds + slot * STG + lane * 16;
+#pragma unroll
+                for (int q = 0; q < LW; ++q) *(u32x4 *) (dst + qlds[q]) = rg[set][q];
+            };
+            if (ns > 0) {
+#pragma unroll
+                for (int s = 0; s < R; ++s) gload(s, s);
+                swrite(0, 0);
+                gload(R, 0);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                // trip t reads stage t from slot t % 2, writes stage t + 1 from
+                // register set (t + 1) % R into the other slot, refills that
+                // set with stage t + 1 + R; the barrier ends every wave's reads
+                // of slot t % 2 before trip t + 1 overwrites it. Trips run R at
+                // a time so that every register set index is a constant (a
+                // register array indexed at run time would live in scratch).
+                // The LDS writes and refills are unconditional (past the last
+                // stage they move copies of it that nobody reads): the same
+                // loads are in flight on every path, so the compiler's counter
+                // wait before each write lets R - 1 stages stay in flight.
+                for (int t0 = 0; t0 < ns; t0 += R) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const int t = t0 + r;
+                        if (t < ns) compute(lds + (t & 1) * STG);
+                        swrite((r + 1) % R, (t + 1) & 1);
+                        gload(t + 1 + R, (r + 1) % R);
+                        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    }
+                }
+            }
+        } else {
 #pragma unroll
         for (int s = 0; s < R - 1; ++s)
             if (s < ns) cissue(s, s);
@@ -335,21 +417,9 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
             wait_stages<LW, R - 1>(min(ns - 1 - t, R - 2));
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (t + R - 1 < ns) cissue(t + R - 1, slot == 0 ? R - 1 : slot - 1);
-            const uint8_t *src = lds + slot * STG;
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                bf16x8 a[TMW], b[TNW];
-#pragma unroll
-                for (int i = 0; i < TMW; ++i) a[i] = *(const bf16x8 *) (src + (wm * TMW + i) * USZ + aro[kh]);
-#pragma unroll
-                for (int j = 0; j < TNW; ++j) b[j] = *(const bf16x8 *) (src + (TM + wn * TNW + j) * USZ + roff[kh]);
-#pragma unroll
-                for (int i = 0; i < TMW; ++i)
-#pragma unroll
-                    for (int j = 0; j < TNW; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-            }
+            compute(lds + slot * STG);
             slot = slot + 1 == R ? 0 : slot + 1;
+        }
         }
     } else if constexpr (PIPE) {
         // shared ring as below (KH = 1); the fragments of stage t + 1 are read
@@ -784,7 +854,8 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
         p.tiles_n = (p.N + BN - 1) / BN;
         p.kt_split = (p.K / 32 + p.splits - 1) / p.splits;
         if (KH > 1 && ((p.K / 32) % p.splits || p.kt_split % KH)) return hipErrorInvalidValue;
-        if (MODE == MODE_COOP64 && ((p.K / 32) % p.splits || p.kt_split % 2 || (CONV && p.conv_ic % 64)))
+        if ((MODE == MODE_COOP64 || MODE == MODE_PF) &&
+            ((p.K / 32) % p.splits || p.kt_split % 2 || (CONV && p.conv_ic % 64)))
             return hipErrorInvalidValue;
         p.block_begin = (nblocks + 7) & ~7;
         nblocks = p.block_begin + p.tiles_m * p.tiles_n * p.splits;
@@ -909,7 +980,7 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     for (int i = 0; i < g.nprob; ++i)
         if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
                                 cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33 ||
-                                cfg == 34 || cfg == 35
+                                cfg == 34 || cfg == 35 || cfg == 39 || cfg == 40
                             ? 64
                             : 128) &&
             epi == EPI_QKV)
@@ -951,6 +1022,19 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
         case 33: return ks_epi<4, 4, 4, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 4 stages of 64 k rows
         case 34: return ks_epi<4, 4, 5, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 5 stages of 64 k rows
         case 35: return ks_epi<4, 4, 6, MODE_COOP64>(g, epi, s);   // 64 x 64 cooperative, 6 stages of 64 k rows
+        case 36: return ks_epi<8, 4, 2, MODE_PF>(g, epi, s);   // 128 x 64, 2 register stages, LDS double buffer
+        case 37: return ks_epi<8, 4, 3, MODE_PF>(g, epi, s);   // 128 x 64, 3 register stages
+        case 38: return ks_epi<8, 8, 2, MODE_PF>(g, epi, s);   // 128 x 128, 2 register stages
+        case 39: return ks_epi<4, 4, 3, MODE_PF>(g, epi, s);   // 64 x 64, 3 register stages
+        case 40: return ks_epi<4, 4, 4, MODE_PF>(g, epi, s);   // 64 x 64, 4 register stages
+        case 41: return ks_epi<8, 4, 4, MODE_PF>(g, epi, s);   // 128 x 64, 4 register stages
+        case 42: return ks_epi<8, 10, 3, MODE_COOP64>(g, epi, s);   // 128 x 160, 3 stages of 64 k rows
+        case 43: return ks_epi<8, 10, 4, MODE_COOP64>(g, epi, s);   // 128 x 160, 4 stages
+        case 44: return ks_epi<8, 12, 3, MODE_COOP64>(g, epi, s);   // 128 x 192, 3 stages
+        case 45: return ks_epi<8, 10, 2, MODE_PF>(g, epi, s);       // 128 x 160, 2 register stages
+        case 46: return ks_epi<8, 12, 2, MODE_PF>(g, epi, s);       // 128 x 192, 2 register stages
+        case 47: return ks_epi<8, 10, 2, MODE_COOP64>(g, epi, s);   // 128 x 160, 2 stages
+        case 48: return ks_epi<8, 12, 2, MODE_COOP64>(g, epi, s);   // 128 x 192, 2 stages
 #endif
         default: return hipErrorInvalidValue;
     }

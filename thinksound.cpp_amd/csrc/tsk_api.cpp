@@ -66,10 +66,19 @@ void read_tuning() {
     t.dit_sched = env_int("TSK_DIT_SCHED", 1) != 0;
     t.ln_block = env_int("TSK_LN_BLOCK", 0) != 0;
     t.gemv_rw = env_int("TSK_GEMV_RW", 2);
-    // one character per projection (qkv, out, fc1, fc2): 0-9, a-z = 10-35
+    // two digits: split-K of linear1 and of ffn.fc2 in the DiT driver
+    if (const char *ks = getenv("TSK_KSPLIT"))
+        if ((ks[0] == '1' || ks[0] == '2' || ks[0] == '4') && (ks[1] == '1' || ks[1] == '2' || ks[1] == '4')) {
+            t.ksplit_out = ks[0] - '0';
+            t.ksplit_fc2 = ks[1] - '0';
+        }
+    // one character per projection (qkv, out, fc1, fc2): 0-9, a-z = 10-35, A-Z = 36-61
     if (const char *gc = getenv("TSK_GEMM_CFG"))
         for (int i = 0; i < 4 && gc[i]; ++i)
-            t.gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9' ? gc[i] - '0' : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10 : 0;
+            t.gemm_cfg[i] = gc[i] >= '0' && gc[i] <= '9'   ? gc[i] - '0'
+                            : gc[i] >= 'a' && gc[i] <= 'z' ? gc[i] - 'a' + 10
+                            : gc[i] >= 'A' && gc[i] <= 'Z' ? gc[i] - 'A' + 36
+                                                           : 0;
     g_tuning = t;
 }
 }  // namespace

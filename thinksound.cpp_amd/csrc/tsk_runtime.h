@@ -40,6 +40,7 @@ struct Tuning {
     bool dit_sched = true;
     bool ln_block = false;
     int gemv_rw = 2;
+    int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
 };
 const Tuning &tuning();
 
