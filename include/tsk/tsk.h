@@ -26,6 +26,7 @@
  *   tsk_t5_attention    <- mul_mat(k,q) + bias + pad -> soft_max -> mul_mat
  *                                                              src/t5_encoder.cpp:68-73
  *   tsk_t5_*            <- ts_t5::load / encode                src/t5_encoder.cpp:28-104
+ *   tsk_vae_*           <- ts_vae::load / decode               src/vae_decoder.cpp:7-124
  *
  * Conventions (all follow ggml):
  *   - tensors are non-owning views: ne[] = extents with ne[0] fastest,
@@ -626,6 +627,54 @@ int     tsk_mmdit_debug_get(const tsk_mmdit *m, const char *name, float *out, in
 int  tsk_mmdit_sample(tsk_mmdit *m, int T, const float *noise, int clip_S, const float *clip_f, int sync_S,
                       const float *sync_f, const float *text_f, const float *t5, const float *global_text,
                       int steps, float cfg_scale, float *out, float *flow0, tsk_stream stream);
+
+/* ---- Oobleck VAE decoder (ts_vae, src/vae_decoder.h:6-17) ---------------
+ * ts_vae::decode (src/vae_decoder.cpp:62-124): conv k7 (latent_dim ->
+ * 16 channels), 5 decoder blocks (SnakeBeta -> transposed conv of stride s,
+ * kernel 2 s -> residual units of dilation 1, 3, 9: x + conv_k1(snake(
+ * conv_k7_dil(snake(x))))), SnakeBeta -> conv k7 (no bias) -> out_channels.
+ * SnakeBeta is y = x + sin^2(exp(alpha) x) exp(-beta) per channel
+ * (:14-24). All weights and arithmetic F32 (the converter keeps the VAE F32,
+ * convert/convert_vae.py:5): every convolution is an F32 x F32 ggml_mul_mat
+ * (fp32 products and sums). The transposed convolutions take the converter's
+ * conv1d kernels (flipped, channels swapped, convert/convert_vae.py:19-26) and
+ * run as one 3-tap convolution whose output channels are the s phases of the
+ * upsampled sequence -- the same sums as the reference's zero-stuffed conv1d
+ * (:36-58) without its multiplications by the inserted zeros. */
+typedef struct tsk_vae tsk_vae;
+
+typedef struct tsk_vae_config {
+    int latent_dim;      /* 64  (vae.latent_dim)   */
+    int channels;        /* 128 (vae.channels)     */
+    int out_channels;    /* 2   (vae.out_channels) */
+    int c_mults[5];      /* 1, 2, 4, 8, 16 (vae.c_mults)  */
+    int strides[5];      /* 2, 4, 4, 8, 8  (vae.strides)  */
+    int max_latent;      /* capacity: latent frames per decode */
+} tsk_vae_config;
+
+/* the reference's configuration (convert/convert_vae.py:60-66), max_latent 646 */
+void tsk_vae_default_config(tsk_vae_config *cfg);
+int  tsk_vae_create(const tsk_vae_config *cfg, tsk_vae **out);
+void tsk_vae_destroy(tsk_vae *v);
+/* Named weights of the converter (decoder.layers.*; conv kernels ggml ne
+ * [K, IC, OC], the transposed convolutions already as conv1d kernels;
+ * vectors alpha / beta / bias), all F32. */
+int  tsk_vae_n_tensors(const tsk_vae *v);
+int  tsk_vae_tensor_info(const tsk_vae *v, int i, const char **name, int64_t ne[4]);
+/* HOST f32 values in ggml / PyTorch memory order */
+int  tsk_vae_set_tensor(tsk_vae *v, const char *name, const float *host_f32, int64_t n);
+/* Upsampling factor: the product of the strides (2048). */
+int  tsk_vae_hop(const tsk_vae *v);
+/*
+ * Decode T <= max_latent latent frames, HOST pointers in ts_vae's layouts
+ * (src/vae_decoder.h:7-8): latent ne = [T, latent_dim] (C order
+ * [latent_dim][T]) -> audio ne = [T_audio, out_channels] planar (C order
+ * [out_channels][T_audio]), T_audio = T * hop. Returns TSK_OK or a negative
+ * status; *t_audio receives T_audio.
+ */
+int  tsk_vae_decode(tsk_vae *v, int T, const float *latent, float *audio, int64_t *t_audio, tsk_stream stream);
+/* Same with DEVICE latent / audio arrays; no host synchronisation. */
+int  tsk_vae_decode_device(tsk_vae *v, int T, const float *latent_d, float *audio_d, tsk_stream stream);
 
 #ifdef __cplusplus
 }

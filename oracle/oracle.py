@@ -38,6 +38,11 @@ class DitConfig(ctypes.Structure):
         [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
 
 
+class VaeConfig(ctypes.Structure):
+    _fields_ = [("latent_dim", ctypes.c_int), ("channels", ctypes.c_int), ("out_channels", ctypes.c_int),
+                ("c_mults", ctypes.c_int * 5), ("strides", ctypes.c_int * 5), ("max_latent", ctypes.c_int)]
+
+
 class MMDitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
@@ -124,6 +129,13 @@ def lib():
         L.orc_mmdit_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
         L.orc_mmdit_forward.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp, ctypes.c_int, vp,
                                         vp, vp, vp, vp, ctypes.c_int, ctypes.c_int]
+        L.orc_vae_create.argtypes = [ctypes.POINTER(VaeConfig)]
+        L.orc_vae_create.restype = vp
+        L.orc_vae_destroy.argtypes = [vp]
+        L.orc_vae_n_tensors.argtypes = [vp]
+        L.orc_vae_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)]
+        L.orc_vae_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
+        L.orc_vae_decode.argtypes = [vp, ctypes.c_int, vp, vp]
         L.orc_mmdit_stage_size.argtypes = [vp, ctypes.c_char_p]
         L.orc_mmdit_stage_size.restype = ctypes.c_int64
         L.orc_mmdit_stage.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
@@ -507,6 +519,50 @@ class OracleMMDiT:
                                     cfg_scale, out.ctypes.data, flow0.ctypes.data, int(act_bf16), int(kv_f16))
         assert rc == 0, rc
         return out, flow0
+
+
+# ---------------------------------------------------------------- Oobleck VAE decoder
+def vae_config(**kw):
+    """the reference's decoder (convert/convert_vae.py:60-66)"""
+    c = VaeConfig(latent_dim=64, channels=128, out_channels=2, max_latent=646)
+    c.c_mults[:] = kw.pop("c_mults", [1, 2, 4, 8, 16])
+    c.strides[:] = kw.pop("strides", [2, 4, 4, 8, 8])
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+class OracleVae:
+    """ts_vae::decode restated (tsk_oracle_vae.c): latent (L, T) -> audio (C_out, T * hop)"""
+
+    def __init__(self, cfg):
+        self.cfg = cfg
+        self.hop = int(np.prod(list(cfg.strides)))
+        self.h = lib().orc_vae_create(ctypes.byref(cfg))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_vae_destroy(self.h)
+            self.h = None
+
+    def tensors(self):
+        out = []
+        for i in range(lib().orc_vae_n_tensors(self.h)):
+            nm, ne = ctypes.c_char_p(), (ctypes.c_int64 * 3)()
+            assert lib().orc_vae_tensor_info(self.h, i, ctypes.byref(nm), ne) == 0
+            out.append((nm.value.decode(), tuple(ne)))
+        return out
+
+    def set_tensor(self, name, arr):
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        assert lib().orc_vae_set_tensor(self.h, name.encode(), arr.ctypes.data, arr.size) == 0, name
+
+    def decode(self, latent):
+        latent = np.ascontiguousarray(latent, dtype=np.float32)
+        L, T = latent.shape
+        audio = np.empty((self.cfg.out_channels, T * self.hop), np.float32)
+        assert lib().orc_vae_decode(self.h, T, latent.ctypes.data, audio.ctypes.data) == 0
+        return audio
 
 
 # ---------------------------------------------------------------- T5 encoder (config 4)

@@ -132,6 +132,17 @@ int      orc_mmdit_sample(orc_mmdit *m, int T, const float *noise, int clip_S, c
                           const float *sync_f, const float *text_f, const float *t5, const float *global_text,
                           int steps, float cfg_scale, float *out, float *flow0, int act_bf16, int kv_f16);
 
+/* ---- Oobleck VAE decoder (ts_vae::decode, src/vae_decoder.cpp:62-124),
+ * tsk_oracle_vae.c: weights by the converter's names from host f32 in ggml
+ * order; latent [latent_dim][T] -> audio [out_channels][T * hop]. */
+typedef struct orc_vae orc_vae;
+orc_vae *orc_vae_create(const tsk_vae_config *cfg);
+void     orc_vae_destroy(orc_vae *v);
+int      orc_vae_n_tensors(const orc_vae *v);
+int      orc_vae_tensor_info(const orc_vae *v, int i, const char **name, int64_t ne[3]);
+int      orc_vae_set_tensor(orc_vae *v, const char *name, const float *src, int64_t n);
+int      orc_vae_decode(orc_vae *v, int T, const float *latent, float *audio);
+
 /* ---- T5 encoder stack (ts_t5::encode, src/t5_encoder.cpp:40-104) ---------
  * Relative-position bucket of t5_encoder.cpp:14-26 (bidirectional). */
 int      orc_t5_bucket(int rel, int num_buckets, int max_dist);

@@ -146,8 +146,18 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
                 for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
             } else {
                 float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
-                if (full) *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
-                else for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+                if (p.accumulate) {
+                    if (full) {
+                        const f32x4 v = *(const f32x4 *) yr;
+                        *(f32x4 *) yr = f32x4{v[0] + o[0], v[1] + o[1], v[2] + o[2], v[3] + o[3]};
+                    } else {
+                        for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] += o[r];
+                    }
+                } else if (full) {
+                    *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                } else {
+                    for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+                }
             }
         }
     }
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
 
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s) {
     constexpr int TM = 4, TN = 2, BM = 2 * TM * 16, BN = 2 * TN * 16;
-    if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf) return hipErrorInvalidValue;
+    if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf || (p.accumulate && y_bf16)) return hipErrorInvalidValue;
     if (p.conv_ic && (p.conv_ic % 4 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;

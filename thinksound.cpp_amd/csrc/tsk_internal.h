@@ -156,6 +156,7 @@ struct GemmProblem {
     int splits;                    // K slices (EPI_PARTIAL), else 1
     const uint16_t *w3;            // EPI_SWIGLU_*: the second weight (same layout as w)
     const float *wf;               // launch_gemm_f32: f32 weights [M][K] row-major (ld_w)
+    int accumulate;                // launch_gemm_f32: y += acc + bias (f32 y)
     // implicit im2col (conv_ic > 0): row n of X is output position ow = n % conv_ow
     // of batch item b = n / conv_ow, and column k = kw * conv_ic + ic reads
     // x[b * x_group_stride + (ow * conv_s + kw * conv_d - conv_p) * ld_x + ic],
@@ -315,6 +316,10 @@ hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64
 // F32-weight GEMM (gemm_f32.hip): p.wf [M][K] (ld_w), f32 activations p.x
 // (plain rows or implicit im2col), y f32 or bf16 (+bias)
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s);
+// SnakeBeta on token-major rows: y[t][c] = x[t][c] + sin^2(x[t][c] ea[c]) eb[c]
+// (ea = exp(alpha), eb = exp(-beta)), rows x cols f32 (x may equal y)
+hipError_t launch_snake(const float *x, const float *ea, const float *eb, int64_t rows, int cols, float *y,
+                        hipStream_t s);
 // y = silu(a) * b, f32, n elements
 hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
 // y[n, m] = sum_k W[m, k] x[n, k] + bias[m]: bf16 row-major W, f32 x and y,

@@ -1,0 +1,358 @@
+// vae.cpp — the Oobleck VAE decoder of ts_vae::decode (src/vae_decoder.cpp:
+// 62-124) on gfx950, F32 throughout (the converter keeps the VAE F32).
+//
+// Activations are token-major rows [T][C] (channels fastest), so every
+// convolution is one F32 GEMM over implicit im2col rows (launch_gemm_f32,
+// fp32 MFMA): y[t][oc] = sum_{kw, ic} W[oc][kw][ic] x[t + kw d - p][ic].
+// The reference keeps [T, C] with time fastest and runs im2col + mul_mat; the
+// sums are the same products in another order.
+//
+// Transposed convolution (stride s, kernel K = 2 s, padding s / 2): the
+// reference zero-stuffs the input (s - 1 zeros after every frame) and runs a
+// stride-1 conv1d with the converter's flipped kernel W' and padding
+// K - 1 - s / 2 (:36-58). Output t = s q + r then takes exactly two taps,
+// k = k0(r) and k0(r) + s with k0(r) = (K - 1 - s / 2 - r) mod s, reading
+// input frames q + c(r) and q + c(r) + 1, c(r) = (r + k0(r) - (K - 1 - s / 2)) / s
+// in {-1, 0}. All s phases read frames q - 1, q, q + 1: one 3-tap convolution
+// (padding 1) with s * OC output channels -- channel r * OC + oc holds phase r
+// -- whose output rows [T][s * OC] are the upsampled rows [s T][OC]. Each
+// phase's unused tap is a zero weight, so every output is the reference's
+// sum of the same two products (plus zero terms, which change no fp32 sum).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/tsk/tsk.h"
+#include "tsk_internal.h"
+#include "tsk_runtime.h"
+
+using namespace tsk;
+
+namespace {
+
+struct VW {
+    std::string name;
+    int64_t ne[3];
+    bool conv, ct;          // convolution kernel; transposed-convolution kernel
+    int stride;             // ct: the stride s
+    size_t offset;          // device float offset of the prepared layout
+    size_t count;           // floats stored
+};
+
+}  // namespace
+
+struct tsk_vae {
+    tsk_vae_config cfg;
+    std::vector<VW> w;
+    std::unordered_map<std::string, int> idx;
+    float *blob = nullptr;
+    float *act[3] = {nullptr, nullptr, nullptr};   // activation rows, max_latent * hop * channels each
+    float *lat = nullptr;                          // latent rows [T][latent_dim]
+    size_t act_cap = 0;
+    int hop = 1;
+};
+
+namespace {
+
+int hipcheck(hipError_t e, const char *what) { return e == hipSuccess ? TSK_OK : hip_fail(e, what); }
+
+void addv(tsk_vae *v, const std::string &name, int64_t a, int64_t b, int64_t c, bool conv, bool ct = false,
+          int stride = 0) {
+    VW x;
+    x.name = name;
+    x.ne[0] = a; x.ne[1] = b; x.ne[2] = c;
+    x.conv = conv;
+    x.ct = ct;
+    x.stride = stride;
+    x.offset = 0;
+    // prepared layouts: conv kw-major [OC][K * IC]; transposed conv the merged
+    // 3-tap kernel [s * OC][3 * IC] and its bias replicated [s * OC]
+    x.count = ct ? (size_t) stride * c * 3 * b : (size_t) (a * b * c);
+    v->idx[name] = (int) v->w.size();
+    v->w.push_back(x);
+}
+
+// channels of decoder block n (n = 0 .. 4 -> decoder.layers.1 .. 5): in, out, stride
+void block_dims(const tsk_vae_config &c, int n, int *in, int *out, int *s) {
+    const int mult[6] = {1, c.c_mults[0], c.c_mults[1], c.c_mults[2], c.c_mults[3], c.c_mults[4]};
+    *in = mult[5 - n] * c.channels;
+    *out = mult[4 - n] * c.channels;
+    *s = c.strides[4 - n];
+}
+
+const VW &wi(const tsk_vae *v, const std::string &n) { return v->w[v->idx.at(n)]; }
+const float *wp(const tsk_vae *v, const std::string &n) { return v->blob + wi(v, n).offset; }
+
+// y rows [T_out][OC] = conv(x rows [T_in][IC]) + bias, stride 1 (F32 GEMM)
+int conv(const tsk_vae *v, const std::string &p, bool bias, const float *x, int IC, int T_in, int pad, int dil,
+         float *y, bool accumulate, hipStream_t s) {
+    const VW &w = wi(v, p + ".weight");
+    const int KW = (int) w.ne[0], OC = (int) w.ne[2];
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
+    q.x = x; q.ld_x = IC;
+    q.wf = wp(v, p + ".weight"); q.ld_w = (int64_t) KW * IC;
+    q.bias = bias ? wp(v, p + ".bias") : nullptr;
+    q.y = y; q.ld_y = OC;
+    const int T_out = T_in + 2 * pad - dil * (KW - 1);
+    q.M = OC; q.N = T_out; q.K = KW * IC; q.splits = 1;
+    if (KW > 1 || pad) {
+        q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_out; q.conv_s = 1; q.conv_p = pad; q.conv_d = dil;
+    }
+    q.accumulate = accumulate ? 1 : 0;
+    return hipcheck(launch_gemm_f32(q, 0, s), "vae conv");
+}
+
+// transposed convolution as the merged 3-tap convolution: y rows [s T_in][OC]
+int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T_in, float *y, hipStream_t s) {
+    const VW &w = wi(v, p + ".weight");
+    const int OC = (int) w.ne[2], st = w.stride;
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
+    q.x = x; q.ld_x = IC;
+    q.wf = wp(v, p + ".weight"); q.ld_w = (int64_t) 3 * IC;
+    q.bias = wp(v, p + ".bias");
+    q.y = y; q.ld_y = (int64_t) st * OC;
+    q.M = st * OC; q.N = T_in; q.K = 3 * IC; q.splits = 1;
+    q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_in; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
+    return hipcheck(launch_gemm_f32(q, 0, s), "vae transposed conv");
+}
+
+int snake(const tsk_vae *v, const std::string &p, const float *x, int64_t rows, int C, float *y, hipStream_t s) {
+    return hipcheck(launch_snake(x, wp(v, p + ".alpha"), wp(v, p + ".beta"), rows, C, y, s), "vae snake");
+}
+
+int validate(const tsk_vae_config *c) {
+    if (!c) return fail(TSK_ERR_INVALID_ARG, "cfg is NULL");
+    if (c->latent_dim < 4 || c->latent_dim % 4 || c->channels < 4 || c->channels % 4 || c->out_channels < 1 ||
+        c->max_latent < 1)
+        return fail(TSK_ERR_SHAPE, "latent_dim and channels must be multiples of 4");
+    int64_t hop = 1;
+    for (int i = 0; i < 5; ++i) {
+        if (c->c_mults[i] < 1 || c->strides[i] < 2 || c->strides[i] % 2)
+            return fail(TSK_ERR_SHAPE, "c_mults >= 1, strides even");
+        hop *= c->strides[i];
+    }
+    if ((int64_t) c->max_latent * hop > (1 << 28)) return fail(TSK_ERR_SHAPE, "max_latent * hop too large");
+    return TSK_OK;
+}
+
+}  // namespace
+
+extern "C" void tsk_vae_default_config(tsk_vae_config *c) {
+    if (!c) return;
+    c->latent_dim = 64; c->channels = 128; c->out_channels = 2;
+    const int m[5] = {1, 2, 4, 8, 16}, st[5] = {2, 4, 4, 8, 8};
+    for (int i = 0; i < 5; ++i) { c->c_mults[i] = m[i]; c->strides[i] = st[i]; }
+    c->max_latent = 646;
+}
+
+extern "C" void tsk_vae_destroy(tsk_vae *v) {
+    if (!v) return;
+    (void) hipDeviceSynchronize();
+    if (v->blob) (void) hipFree(v->blob);
+    for (float *a : v->act)
+        if (a) (void) hipFree(a);
+    if (v->lat) (void) hipFree(v->lat);
+    delete v;
+}
+
+extern "C" int tsk_vae_create(const tsk_vae_config *cfg, tsk_vae **out) {
+    if (!out) return fail(TSK_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    int rc = validate(cfg);
+    if (rc) return rc;
+    if ((rc = require_init())) return rc;
+    tsk_vae *v = new tsk_vae();
+    v->cfg = *cfg;
+    const tsk_vae_config &c = v->cfg;
+    int in0, out0, s0;
+    block_dims(c, 0, &in0, &out0, &s0);
+    // the converter's names (convert/convert_vae.py:34-56, src/vae_decoder.cpp:73-107)
+    addv(v, "decoder.layers.0.weight", 7, c.latent_dim, in0, true);
+    addv(v, "decoder.layers.0.bias", in0, 1, 1, false);
+    int64_t max_ch_t = (int64_t) in0;                 // largest channels x frames per latent frame
+    int64_t up = 1;
+    for (int n = 0; n < 5; ++n) {
+        int ci, co, st;
+        block_dims(c, n, &ci, &co, &st);
+        const std::string bp = "decoder.layers." + std::to_string(n + 1);
+        addv(v, bp + ".layers.0.alpha", ci, 1, 1, false);
+        addv(v, bp + ".layers.0.beta", ci, 1, 1, false);
+        addv(v, bp + ".layers.1.weight", 2 * st, ci, co, true, true, st);
+        addv(v, bp + ".layers.1.bias", co, 1, 1, false, false, st);   // replicated over the s phases
+        v->w.back().count = (size_t) st * co;
+        for (int r = 0; r < 3; ++r) {
+            const std::string rp = bp + ".layers." + std::to_string(r + 2);
+            addv(v, rp + ".layers.0.alpha", co, 1, 1, false);
+            addv(v, rp + ".layers.0.beta", co, 1, 1, false);
+            addv(v, rp + ".layers.1.weight", 7, co, co, true);
+            addv(v, rp + ".layers.1.bias", co, 1, 1, false);
+            addv(v, rp + ".layers.2.alpha", co, 1, 1, false);
+            addv(v, rp + ".layers.2.beta", co, 1, 1, false);
+            addv(v, rp + ".layers.3.weight", 1, co, co, true);
+            addv(v, rp + ".layers.3.bias", co, 1, 1, false);
+        }
+        up *= st;
+        max_ch_t = std::max(max_ch_t, up * co);
+    }
+    int lin, lout, ls;
+    block_dims(c, 4, &lin, &lout, &ls);
+    addv(v, "decoder.layers.6.alpha", lout, 1, 1, false);
+    addv(v, "decoder.layers.6.beta", lout, 1, 1, false);
+    addv(v, "decoder.layers.7.weight", 7, lout, c.out_channels, true);
+    v->hop = (int) up;
+    max_ch_t = std::max(max_ch_t, up * c.out_channels);
+    size_t off = 0;
+    for (auto &x : v->w) {
+        x.offset = off;
+        off += (x.count + 63) & ~(size_t) 63;
+    }
+    v->act_cap = (size_t) c.max_latent * (size_t) max_ch_t;
+    auto alloc = [&](void **p, size_t bytes) -> int {
+        hipError_t e = hipMalloc(p, bytes);
+        if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return TSK_OK;
+    };
+    if ((rc = alloc((void **) &v->blob, sizeof(float) * off)) ||
+        (rc = alloc((void **) &v->act[0], sizeof(float) * v->act_cap)) ||
+        (rc = alloc((void **) &v->act[1], sizeof(float) * v->act_cap)) ||
+        (rc = alloc((void **) &v->act[2], sizeof(float) * v->act_cap)) ||
+        (rc = alloc((void **) &v->lat, sizeof(float) * (size_t) c.max_latent * c.latent_dim))) {
+        tsk_vae_destroy(v);
+        return rc;
+    }
+    hipError_t e = hipMemset(v->blob, 0, sizeof(float) * off);
+    if (e != hipSuccess) { tsk_vae_destroy(v); return hip_fail(e, "vae init"); }
+    *out = v;
+    return TSK_OK;
+}
+
+extern "C" int tsk_vae_n_tensors(const tsk_vae *v) { return v ? (int) v->w.size() : 0; }
+
+extern "C" int tsk_vae_tensor_info(const tsk_vae *v, int i, const char **name, int64_t ne[4]) {
+    if (!v || i < 0 || i >= (int) v->w.size()) return fail(TSK_ERR_INVALID_ARG, "tensor index %d", i);
+    if (name) *name = v->w[i].name.c_str();
+    if (ne) { ne[0] = v->w[i].ne[0]; ne[1] = v->w[i].ne[1]; ne[2] = v->w[i].ne[2]; ne[3] = 1; }
+    return TSK_OK;
+}
+
+extern "C" int tsk_vae_hop(const tsk_vae *v) { return v ? v->hop : 0; }
+
+// host f32 in ggml / PyTorch order: conv kernels [OC][IC][K]; alpha / beta
+// stored as exp(alpha) / exp(-beta) (the snake's two exponentials, :18-19)
+extern "C" int tsk_vae_set_tensor(tsk_vae *v, const char *name, const float *src, int64_t n) {
+    if (!v || !name || !src) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    auto it = v->idx.find(name);
+    if (it == v->idx.end()) return fail(TSK_ERR_INVALID_ARG, "unknown tensor '%s'", name);
+    const VW &x = v->w[it->second];
+    const int64_t N = x.ne[0] * x.ne[1] * x.ne[2];
+    if (n != N) return fail(TSK_ERR_SHAPE, "'%s' has %lld elements, got %lld", name, (long long) N, (long long) n);
+    std::vector<float> t(x.count, 0.0f);
+    const std::string nm = name;
+    const bool is_alpha = nm.size() > 6 && nm.compare(nm.size() - 6, 6, ".alpha") == 0;
+    const bool is_beta = nm.size() > 5 && nm.compare(nm.size() - 5, 5, ".beta") == 0;
+    if (x.ct) {
+        // merged 3-tap kernel: row r * OC + oc, tap j (input frame q - 1 + j),
+        // channel ic = W'[oc][ic][k] for the phase's two taps k
+        const int64_t K = x.ne[0], IC = x.ne[1], OC = x.ne[2], st = x.stride, P = K - 1 - st / 2;
+        for (int64_t r = 0; r < st; ++r) {
+            const int64_t k0 = ((P - r) % st + st) % st;
+            const int64_t c0 = (r + k0 - P) / st;          // -1 or 0 (r + k0 - P is a multiple of st)
+            for (int m = 0; m < 2; ++m) {
+                const int64_t k = k0 + m * st, j = c0 + m + 1;
+                for (int64_t oc = 0; oc < OC; ++oc)
+                    for (int64_t ic = 0; ic < IC; ++ic)
+                        t[(size_t) (((r * OC + oc) * 3 + j) * IC + ic)] = src[(oc * IC + ic) * K + k];
+            }
+        }
+    } else if (x.conv) {
+        const int64_t K = x.ne[0], IC = x.ne[1], OC = x.ne[2];
+        for (int64_t oc = 0; oc < OC; ++oc)
+            for (int64_t ic = 0; ic < IC; ++ic)
+                for (int64_t k = 0; k < K; ++k) t[(size_t) ((oc * K + k) * IC + ic)] = src[(oc * IC + ic) * K + k];
+    } else if (x.stride) {
+        for (int64_t r = 0; r < x.stride; ++r)
+            for (int64_t i = 0; i < n; ++i) t[(size_t) (r * n + i)] = src[i];
+    } else {
+        for (int64_t i = 0; i < n; ++i) t[i] = is_alpha ? expf(src[i]) : is_beta ? expf(-src[i]) : src[i];
+    }
+    return hipcheck(hipMemcpy(v->blob + x.offset, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice),
+                    "vae set_tensor copy");
+}
+
+namespace {
+
+int decode_impl(tsk_vae *v, int T, const float *latent_d, float *audio_d, hipStream_t st) {
+    const tsk_vae_config &c = v->cfg;
+    int rc;
+    // latent ne = [T, latent_dim] (time fastest) -> rows [T][latent_dim]
+    if ((rc = hipcheck(launch_transpose_ct(latent_d, 1, c.latent_dim, T, v->lat, st), "vae latent"))) return rc;
+    float *x = v->act[0], *h = v->act[1], *g = v->act[2];
+    int in0, out0, s0;
+    block_dims(c, 0, &in0, &out0, &s0);
+    if ((rc = conv(v, "decoder.layers.0", true, v->lat, c.latent_dim, T, 3, 1, x, false, st))) return rc;
+    int64_t frames = T;
+    int C = in0;
+    const int dil[3] = {1, 3, 9};
+    for (int n = 0; n < 5; ++n) {
+        int ci, co, s;
+        block_dims(c, n, &ci, &co, &s);
+        const std::string bp = "decoder.layers." + std::to_string(n + 1);
+        if ((rc = snake(v, bp + ".layers.0", x, frames, ci, h, st))) return rc;
+        if ((rc = conv_t(v, bp + ".layers.1", h, ci, (int) frames, x, st))) return rc;
+        frames *= s;
+        C = co;
+        for (int r = 0; r < 3; ++r) {
+            // x += conv_k1(snake(conv_k7_dil(snake(x))))  (the residual unit, :99-105)
+            const std::string rp = bp + ".layers." + std::to_string(r + 2);
+            if ((rc = snake(v, rp + ".layers.0", x, frames, C, h, st))) return rc;
+            if ((rc = conv(v, rp + ".layers.1", true, h, C, (int) frames, 3 * dil[r], dil[r], g, false, st))) return rc;
+            if ((rc = snake(v, rp + ".layers.2", g, frames, C, g, st))) return rc;
+            if ((rc = conv(v, rp + ".layers.3", true, g, C, (int) frames, 0, 1, x, true, st))) return rc;
+        }
+    }
+    // final snake -> conv k7 (no bias) -> rows [T_audio][out_channels] -> planar
+    if ((rc = snake(v, "decoder.layers.6", x, frames, C, h, st))) return rc;
+    if ((rc = conv(v, "decoder.layers.7", false, h, C, (int) frames, 3, 1, g, false, st))) return rc;
+    return hipcheck(launch_transpose_ct(g, 1, (int) frames, c.out_channels, audio_d, st), "vae audio");
+}
+
+}  // namespace
+
+extern "C" int tsk_vae_decode_device(tsk_vae *v, int T, const float *latent_d, float *audio_d, tsk_stream stream) {
+    if (!v || !latent_d || !audio_d) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    if (T < 1 || T > v->cfg.max_latent) return fail(TSK_ERR_SHAPE, "T=%d outside [1, %d]", T, v->cfg.max_latent);
+    int rc = require_init();
+    if (rc) return rc;
+    return decode_impl(v, T, latent_d, audio_d, (hipStream_t) stream);
+}
+
+extern "C" int tsk_vae_decode(tsk_vae *v, int T, const float *latent, float *audio, int64_t *t_audio,
+                              tsk_stream stream) {
+    if (!v || !latent || !audio) return fail(TSK_ERR_INVALID_ARG, "NULL argument");
+    if (T < 1 || T > v->cfg.max_latent) return fail(TSK_ERR_SHAPE, "T=%d outside [1, %d]", T, v->cfg.max_latent);
+    int rc = require_init();
+    if (rc) return rc;
+    const tsk_vae_config &c = v->cfg;
+    const size_t n_in = (size_t) T * c.latent_dim, n_out = (size_t) T * v->hop * c.out_channels;
+    hipStream_t st = (hipStream_t) stream;
+    // device staging: the latent after the activation rows of buffer 2 (free
+    // until the last convolution), the audio in buffer 1 (the last snake's
+    // output is consumed before the transpose writes it)
+    float *d_lat = v->act[2] + (v->act_cap - n_in);
+    float *d_audio = v->act[0];
+    if (n_out > v->act_cap) return fail(TSK_ERR_SHAPE, "audio exceeds the capacity");
+    if ((rc = hipcheck(hipMemcpyAsync(d_lat, latent, sizeof(float) * n_in, hipMemcpyHostToDevice, st), "latent")))
+        return rc;
+    if ((rc = decode_impl(v, T, d_lat, d_audio, st))) return rc;
+    if ((rc = hipcheck(hipMemcpyAsync(audio, d_audio, sizeof(float) * n_out, hipMemcpyDeviceToHost, st), "audio")))
+        return rc;
+    if ((rc = hipcheck(hipStreamSynchronize(st), "sync"))) return rc;
+    if (t_audio) *t_audio = (int64_t) T * v->hop;
+    return TSK_OK;
+}

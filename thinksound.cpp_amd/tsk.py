@@ -51,6 +51,11 @@ class DitConfig(ctypes.Structure):
         [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period", "ln_eps", "qk_eps")]
 
 
+class VaeConfig(ctypes.Structure):
+    _fields_ = [("latent_dim", ctypes.c_int), ("channels", ctypes.c_int), ("out_channels", ctypes.c_int),
+                ("c_mults", ctypes.c_int * 5), ("strides", ctypes.c_int * 5), ("max_latent", ctypes.c_int)]
+
+
 class MMDitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
@@ -147,6 +152,15 @@ def load():
         "tsk_mmdit_debug": ([vp, i], i),
         "tsk_mmdit_debug_size": ([vp, ctypes.c_char_p], ctypes.c_int64),
         "tsk_mmdit_debug_get": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_vae_default_config": ([ctypes.POINTER(VaeConfig)], None),
+        "tsk_vae_create": ([ctypes.POINTER(VaeConfig), ctypes.POINTER(vp)], i),
+        "tsk_vae_destroy": ([vp], None),
+        "tsk_vae_n_tensors": ([vp], i),
+        "tsk_vae_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)], i),
+        "tsk_vae_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_vae_hop": ([vp], i),
+        "tsk_vae_decode": ([vp, i, vp, vp, ctypes.POINTER(ctypes.c_int64), vp], i),
+        "tsk_vae_decode_device": ([vp, i, vp, vp, vp], i),
         "tsk_dit_timing": ([vp, i], i),
         "tsk_dit_timing_read": ([vp, i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
                                  ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], i),
@@ -913,6 +927,95 @@ class MMDit:
                                       sync.ctypes.data, text.ctypes.data, t5.ctypes.data, g.ctypes.data, steps,
                                       cfg_scale, out.ctypes.data, flow0.ctypes.data, _stream()))
         return out, flow0
+
+
+# ---------------------------------------------------------------- Oobleck VAE decoder (ts_vae)
+def vae_config(**kw):
+    c = VaeConfig()
+    load().tsk_vae_default_config(ctypes.byref(c))
+    if "c_mults" in kw:
+        c.c_mults[:] = kw.pop("c_mults")
+    if "strides" in kw:
+        c.strides[:] = kw.pop("strides")
+    for k_, v_ in kw.items():
+        setattr(c, k_, v_)
+    return c
+
+
+def vae_synthetic_weights(tensors, seed=77, snake_std=0.5):
+    """seeded weights {name: float32 array in ggml / PyTorch order}: conv
+    kernels N(0, 1 / (K IC)) (variance-preserving), biases N(0, 0.02), snake
+    alpha / beta N(0, snake_std) (log-scale parameters)"""
+    import zlib
+    out = {}
+    for name, ne in tensors:
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        shape = tuple(int(x) for x in reversed(ne))
+        while len(shape) > 1 and shape[0] == 1:
+            shape = shape[1:]
+        n = int(np.prod(shape))
+        if name.endswith(".weight"):
+            w = rng.standard_normal(n) / np.sqrt(ne[0] * ne[1])
+        elif name.endswith(".bias"):
+            w = rng.standard_normal(n) * 0.02
+        else:
+            w = rng.standard_normal(n) * snake_std
+        out[name] = w.astype(np.float32).reshape(shape)
+    return out
+
+
+class Vae:
+    """ts_vae counterpart (src/vae_decoder.h:6-17): named F32 weights on the
+    GPU and decode()"""
+
+    def __init__(self, cfg=None):
+        init()
+        self.cfg = cfg if cfg is not None else vae_config()
+        h = ctypes.c_void_p()
+        check(load().tsk_vae_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self.h = h
+        self.hop = load().tsk_vae_hop(self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().tsk_vae_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        L = load()
+        out = []
+        for k_ in range(L.tsk_vae_n_tensors(self.h)):
+            nm = ctypes.c_char_p()
+            ne = (ctypes.c_int64 * 4)()
+            check(L.tsk_vae_tensor_info(self.h, k_, ctypes.byref(nm), ne))
+            out.append((nm.value.decode(), tuple(ne)[:3]))
+        return out
+
+    def set_tensor(self, name, host_f32):
+        host_f32 = np.ascontiguousarray(host_f32, dtype=np.float32)
+        check(load().tsk_vae_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
+
+    def decode(self, latent):
+        """latent (latent_dim, T) (ggml ne = [T, latent_dim]) -> audio (out_channels, T * hop)"""
+        latent = np.ascontiguousarray(latent, dtype=np.float32)
+        L, T = latent.shape
+        audio = np.empty((self.cfg.out_channels, T * self.hop), np.float32)
+        ta = ctypes.c_int64()
+        check(load().tsk_vae_decode(self.h, T, latent.ctypes.data, audio.ctypes.data, ctypes.byref(ta), _stream()))
+        assert ta.value == T * self.hop
+        return audio
+
+    def decode_device(self, latent, audio):
+        """DeviceArrays latent (latent_dim, T), audio out (out_channels, T * hop)"""
+        check(load().tsk_vae_decode_device(self.h, latent.shape[1], ctypes.c_void_p(latent.data_ptr()),
+                                           ctypes.c_void_p(audio.data_ptr()), _stream()))
+        return audio
 
 
 # ---------------------------------------------------------------- T5 encoder (ts_t5)
