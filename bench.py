@@ -326,6 +326,34 @@ def graph_bench(tsk, steps, warmup=3):
     return out
 
 
+def vae_bench(tsk, reps=3):
+    """the Oobleck VAE decode of a 9 s (194 latent frames -> 397312 samples)
+    and a 30 s (646 -> 1323008) latent, F32 weights (random, variance
+    preserving), latent resident in HBM; HIP events around `reps` decodes"""
+    import numpy as np
+    v = tsk.Vae(tsk.vae_config(max_latent=646))
+    for k, w in tsk.vae_synthetic_weights(v.tensors(), seed=77, snake_std=0.1).items():
+        v.set_tensor(k, w)
+    out = {}
+    rng = np.random.default_rng(4242)
+    for label, T in (("9s", 194), ("30s", 646)):
+        lat = tsk.to_device(rng.standard_normal((64, T), dtype=np.float32))
+        audio = tsk.empty((2, T * v.hop))
+        v.decode_device(lat, audio)
+        tsk.synchronize()
+        s, e = tsk.Event(), tsk.Event()
+        s.record()
+        for _ in range(reps):
+            v.decode_device(lat, audio)
+        e.record()
+        tsk.synchronize()
+        ms = s.elapsed_ms(e) / reps
+        out[label] = {"ms": round(ms, 3), "latent_frames": T, "samples": T * v.hop,
+                      "realtime_factor": round(T * v.hop / 44100.0 / (ms / 1e3), 1)}
+    v.close()
+    return out
+
+
 def copy_calibration(nbytes=256 << 20, reps=5):
     """A plain device-to-device copy of known size: each launch reads and writes nbytes."""
     import torch
@@ -448,6 +476,8 @@ def main():
     conv30 = conv_bench(tsk, reps=max(5, args.steps))
     # the reference's own three-stream graph at 9 s and 30 s
     graph = graph_bench(tsk, max(5, args.steps // 2))
+    # the VAE decode after the sampler
+    vae = vae_bench(tsk)
     # configuration 3's Q8_0 projection GEMMs at 30 s and configuration 4's T5 stack
     q8 = q8_bench(tsk)
     t5 = t5_bench(tsk)
@@ -498,6 +528,7 @@ def main():
                               "breakdown": breakdown(roles_q8, args.steps)},
         "t5_encoder_config4": t5,
         "reference_graph": graph,
+        "vae_decode": vae,
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9
