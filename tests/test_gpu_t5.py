@@ -12,7 +12,11 @@ oracle's own one-layer output then moves by ~3e-3 (measured below on every
 case). The device and the oracle differ by fp32 summation order, so each
 layer is checked from the device's own input (teacher forcing) against
 max(1e-3, 2 x that one-ulp sensitivity), and the whole stack end to end
-against 2 x the oracle's end-to-end sensitivity to a one-ulp input change."""
+against 2 x the oracle's end-to-end sensitivity to a one-ulp input change.
+Configuration 4's full stack runs twice: with q / k damped to trained-T5
+logit scales (end to end checked too), and with the configuration's own
+weight distribution, whose N(0, 64) logits make the random 24-layer stack
+chaotic (per layer checked, end to end finite and deterministic)."""
 import numpy as np
 import pytest
 
@@ -105,18 +109,19 @@ def q8_random(rng, K, M, scale):
     return np.ascontiguousarray(np.concatenate([d.reshape(M, K // 32, 2), qs.view(np.uint8)], axis=2))
 
 
-def t5_weights(names, rng, d):
+def t5_weights(names, rng, d, qk_damp=True):
     """(name, data) one at a time (the 24-layer set is 1.2 GB of Q8_0 blocks).
-    Q8_0 scales keep activations at unit variance; q and k are scaled down by
-    8^(1/2) so that logits (64-term dot products, no softmax scale in T5) are
-    about N(0, 1) as in a trained T5 -- with unit-variance q and k the logits
-    are N(0, 64) and the random network is chaotic: a 1e-4 difference at one
+    Q8_0 scales keep activations at unit variance. qk_damp scales q and k down
+    by 8^(1/2) so that logits (64-term dot products, no softmax scale in T5)
+    are about N(0, 1) as in a trained T5; without it (configuration 4 as
+    specified: every Q8_0 weight U[-127, 127] at one scale) the logits are
+    N(0, 64) and the random network is chaotic: a 1e-4 difference at one
     layer grows to decorrelation within 24 layers."""
     for name, ne, ty in names:
         if ty == 8:      # Q8_0 [K, M]
             K = ne[0]
             s = 1.0 / np.sqrt(K * 127.0 * 127.0 / 3.0)
-            if name.endswith(".q") or name.endswith(".k"):
+            if qk_damp and (name.endswith(".q") or name.endswith(".k")):
                 s /= np.sqrt(8.0)
             yield name, q8_random(rng, K, ne[1], s)
         elif name == "rel_bias":
@@ -130,7 +135,12 @@ def ulp_perturbed(x, seed=1):
     return (x * (1.0 + 1e-7 * np.random.default_rng(seed).standard_normal(x.shape))).astype(np.float32)
 
 
-def check_stack(t5, ot, x, ids, layers):
+def check_stack(t5, ot, x, ids, layers, end_to_end=True):
+    """every layer from the device's own input (teacher forcing) against
+    max(1e-3, 2 x the oracle's one-ulp sensitivity at that layer); the whole
+    stack against 2 x its end-to-end sensitivity when end_to_end (a chaotic
+    stack decorrelates any two implementations, so there only the per-layer
+    bound is a parity bound)"""
     y = t5.encode(x, ids)
     ref = ot.encode(x, ids)
     e = rel_l2(y, ref)
@@ -148,7 +158,8 @@ def check_stack(t5, ot, x, ids, layers):
     assert np.all(np.isfinite(y))
     for a, f in rows:
         assert a <= max(1e-3, 2.0 * f)
-    assert e <= max(1e-3, 2.0 * e_floor)
+    if end_to_end:
+        assert e <= max(1e-3, 2.0 * e_floor)
     return y
 
 
@@ -176,17 +187,23 @@ def test_t5_encoder_stack(env, layers, n, pad):
     t5.close()
 
 
-def test_t5_config4_full_stack(env):
-    """configuration 4 as specified: 24 layers, 512 tokens, last 64 padded."""
+@pytest.mark.parametrize("qk_damp", [True, False])
+def test_t5_config4_full_stack(env, qk_damp):
+    """configuration 4: 24 layers, 512 tokens, last 64 padded. With the
+    damped q / k the stack is checked end to end as well; with the
+    configuration's own logit distribution (every weight U[-127, 127] at one
+    scale, logits N(0, 64)) every layer is checked from the device's own
+    input, and the end-to-end output must be finite and deterministic."""
     tsk, orc = env
     t5 = tsk.T5(tsk.t5_config())
     ot = orc.OracleT5(orc.t5_config())
     rng = np.random.default_rng(44)
-    for k_, v_ in t5_weights(t5.tensors(), rng, 2048):
+    for k_, v_ in t5_weights(t5.tensors(), rng, 2048, qk_damp=qk_damp):
         t5.set_tensor(k_, v_)
         ot.set_tensor(k_, v_)
     x = rng.standard_normal((512, 2048)).astype(np.float32)
     ids = np.arange(1, 513, dtype=np.int32)
     ids[-64:] = 0
-    check_stack(t5, ot, x, ids, 24)
+    y = check_stack(t5, ot, x, ids, 24, end_to_end=qk_damp)
+    np.testing.assert_array_equal(t5.encode(x, ids), y)
     t5.close()
