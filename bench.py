@@ -421,6 +421,14 @@ def main():
     # config 2 (9 s): timed steps; per-kernel HIP events around every launch inside them
     ms_plain, _, inputs9 = run(194, args.steps, args.warmup, False)
     ms_timed, roles9, _ = run(194, args.steps, 1, True)
+    # the host entry point tsk_dit_forward at 9 s: host latent / text in, flow
+    # out, the PCIe copies and the final synchronisation inside the timing
+    lat_h = np.ascontiguousarray(inputs9[0].transpose(0, 2, 1))
+    dit.forward(lat_h, inputs9[1], inputs9[2])
+    t_host = time.perf_counter()
+    for _ in range(args.steps):
+        dit.forward(lat_h, inputs9[1], inputs9[2])
+    ms_host = (time.perf_counter() - t_host) * 1e3 / args.steps
     # 30 s (646 latent + 77 text tokens): steps/s (plain), attention at N = 723 (timed)
     ms30, _, _ = run(646, max(5, args.steps // 2), 2, False)
     _, roles30, _ = run(646, max(5, args.steps // 2), 1, True)
@@ -518,6 +526,9 @@ def main():
         "steps_per_s_30s": round(1000.0 / ms30, 2),
         "sample_24_steps_30s": sample30,
         "ms_per_step_with_kernel_events": round(ms_timed, 4),
+        "host_entry_9s": {"steps_per_s": round(1000.0 / ms_host, 2), "ms_per_step": round(ms_host, 4),
+                          "note": "tsk_dit_forward from host buffers: PCIe copies in and out and a "
+                                  "synchronisation per step included"},
         "breakdown_9s": breakdown(roles9, args.steps),
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
         "conv_30s": conv30,
