@@ -114,6 +114,32 @@ def test_full_forward_longer_latents(env, T):
     dit.close()
 
 
+def test_l2_prefetch_changes_no_bits(env, monkeypatch):
+    """The LN kernels' early fetch of the next projections' weights into L2
+    (on by default from 512 activation rows) reads memory and changes no
+    arithmetic: forced on at T = 194 (388 rows) and off at T = 646 (1292
+    rows), the flow equals the default run bit for bit; joint blocks (two
+    weight sets per LN, a pre_only text stream) and fused blocks."""
+    tsk, orc = env
+    dit = tsk.Dit(tsk.dit_config(depth=3, fused_depth=1, max_latent=646))
+    for k, v in tsk.synthetic_weights(dit.tensors(), seed=77).items():
+        dit.set_tensor(k, v)
+    try:
+        for T, forced in ((194, "1"), (646, "0")):
+            lat, t, txt = inputs(2, T, seed=T + 1)
+            ref = dit.forward(cm(lat), t, txt)
+            monkeypatch.setenv("TSK_L2PF", forced)
+            tsk.init(0, reread=True)
+            f = dit.forward(cm(lat), t, txt)
+            monkeypatch.delenv("TSK_L2PF")
+            tsk.init(0, reread=True)
+            assert np.isfinite(ref).all() and np.array_equal(f, ref), T
+    finally:
+        monkeypatch.delenv("TSK_L2PF", raising=False)
+        tsk.init(0, reread=True)
+        dit.close()
+
+
 def test_ragged_t_and_device_entry(env):
     tsk, orc = env
     dit, od = build_pair(tsk, orc, depth=2, fused_depth=1, max_latent=64, max_batch=3)

@@ -638,6 +638,8 @@ GemmProblem gemm_problem(const void *x, int64_t ld_x, const uint16_t *w, const f
     return q;
 }
 
+int gemm_cfg_for(const tsk_dit *d, int role, int rows);
+
 // LN + modulate of every stream (paying the residual updates they owe) into
 // xn (bf16), or into the Q8_0 planes qx / dx for the Q8_0 driver
 int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
@@ -661,6 +663,35 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
         rows += (double) B * r[i].S;
         pbytes += 4.0 * r[i].pend_split * B * r[i].S * H;
         r[i].pend_split = 0;
+    }
+    // BF16 driver: the LN workgroups fetch the weights of the projections that
+    // follow into the L2 of the XCDs that will read them (qkv and linear1
+    // after the attention LN, fc1 and fc2 after the MLP LN). The LN then ends
+    // only when those loads have landed; measured on MI355X this pays from
+    // ~800 latent rows (T = 400: 1.95 -> 1.86 ms, 30 s: 2.46 -> 2.33 ms per
+    // step) and breaks even at 388 (9 s), where the LN kernels are too short
+    // to cover the extra 16-32 MB of weight reads: on from 512 rows.
+    const int rows0 = B * r[0].S;
+    const int pf_mode = tuning().l2_prefetch;
+    if (!d->q8 && (pf_mode > 0 || (pf_mode < 0 && rows0 >= 512))) {
+        auto add = [&](const uint16_t *w, int K, int M, int role, int splits) {
+            const int bm = gemm_ks_bm(gemm_cfg_for(d, role, rows0));
+            L2Prefetch &f = g.pf[g.npf];
+            f.w = w; f.kt_n = K / 32; f.rb_tile = bm / 16; f.rb_n = M / 16;
+            f.tiles_m = (M + bm - 1) / bm; f.splits = splits;
+            if ((f.tiles_m * f.splits) % 8 == 0 && f.kt_n % splits == 0) ++g.npf;
+        };
+        for (int i = 0; i < ns; ++i) {
+            const StreamW &w = *r[i].w;
+            if (which == 0) add(w.qkv_w, H, 3 * H, 0, 1);
+            else if (!w.pre_only) add(w.fc1_w, H, c.mlp_hidden, 2, 1);
+        }
+        for (int i = 0; i < ns; ++i) {
+            const StreamW &w = *r[i].w;
+            if (w.pre_only) continue;
+            if (which == 0) add(w.l1_w, H, H, 1, d->ksplit_out);
+            else add(w.fc2_w, c.mlp_hidden, H, 3, d->ksplit_fc2);
+        }
     }
     Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * H, 14.0 * rows * H + pbytes, st);
     return hipcheck(launch_ln_group(g, st), "ln_group");

@@ -942,6 +942,15 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
     }
 }
 
+int gemm_ks_bm(int cfg) {
+    if (!cfg) cfg = 30;
+    return cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 || cfg == 22 ||
+                   cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33 || cfg == 34 || cfg == 35 ||
+                   cfg == 39 || cfg == 40
+               ? 64
+               : 128;
+}
+
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn) {
     int n = 0;
     for (int i = 0; i < g.nprob; ++i) {
@@ -978,13 +987,7 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     }
 #endif
     for (int i = 0; i < g.nprob; ++i)
-        if (g.p[i].M % (cfg == 2 || cfg == 3 || cfg == 5 || cfg == 6 || cfg == 8 || cfg == 13 || cfg == 18 ||
-                                cfg == 22 || cfg == 23 || cfg == 25 || cfg == 30 || cfg == 31 || cfg == 33 ||
-                                cfg == 34 || cfg == 35 || cfg == 39 || cfg == 40
-                            ? 64
-                            : 128) &&
-            epi == EPI_QKV)
-            return hipErrorInvalidValue;
+        if (g.p[i].M % gemm_ks_bm(cfg) && epi == EPI_QKV) return hipErrorInvalidValue;
     switch (cfg) {
         case 22: return ks_epi<4, 4, 4, MODE_COOP>(g, epi, s);    // 64 x 64 cooperative, 4 stages
         case 28: return ks_epi<8, 4, 3, MODE_COOP64>(g, epi, s);   // 128 x 64 cooperative, 3 stages of 64 k rows

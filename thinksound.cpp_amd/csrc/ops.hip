@@ -431,11 +431,41 @@ __device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps
     }
 }
 
+// The workgroups on XCD x (blockIdx.x % 8 == x) touch one dword of every
+// 128-byte line of the weight tiles the following GEMM runs on XCD x, so its
+// first stages find them in that XCD's L2 instead of waiting on memory. The
+// touches are loads into a 256-byte LDS slot that is never read; the caller
+// waits for them (vmcnt) before the workgroup ends.
+__device__ __forceinline__ void l2_prefetch(const L2Prefetch *pf, int npf, void *sink) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int xcd = (int) (blockIdx.x & 7), wg = (int) (blockIdx.x >> 3);
+    const int nwg = (int) ((gridDim.x + 7 - xcd) >> 3);      // workgroups on this XCD
+    const int lane = threadIdx.x & 63;
+    for (int i = 0; i < npf; ++i) {
+        const L2Prefetch &f = pf[i];
+        const int kts = f.kt_n / f.splits;                     // k tiles (1 KiB each) per slice
+        const int per_rb = kts * 8, per_pair = f.rb_tile * per_rb;
+        const int total = (f.tiles_m * f.splits >> 3) * per_pair;
+        for (int l = wg * 64 + lane; l < total; l += nwg * 64) {
+            const int pi = l / per_pair, rem = l - pi * per_pair;
+            const int c = xcd + 8 * pi, tm = c / f.splits, sp = c - tm * f.splits;
+            const int rbl = rem / per_rb, ln = rem - rbl * per_rb;
+            const int rb = tm * f.rb_tile + rbl;
+            if (rb < f.rb_n)
+                __builtin_amdgcn_global_load_lds(f.w + ((int64_t) rb * f.kt_n + sp * kts) * 512 + ln * 64,
+                                                 (lds_void *) sink, 4, 0, 0);
+        }
+    }
+}
+
 template <int YM, int NV>
 __global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
+    __shared__ __attribute__((aligned(16))) uint32_t sink[64];
     const int r = blockIdx.x;
+    if (g.npf) l2_prefetch(g.pf, g.npf, sink);
     if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YM, NV>(g.s[1], r - g.s[0].rows, g.eps);
     else ln_wave_row<YM, NV>(g.s[0], r, g.eps);
+    if (g.npf) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // GEMV list: one wave per output row; lane k-slices of 8, f32 activations
@@ -825,6 +855,13 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
 
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
+    if (g.npf < 0 || g.npf > L2PF_MAX) return hipErrorInvalidValue;
+    for (int i = 0; i < g.npf; ++i) {
+        const L2Prefetch &f = g.pf[i];
+        if (!f.w || f.kt_n < 1 || f.splits < 1 || f.kt_n % f.splits || f.rb_tile < 1 || f.rb_n < 1 ||
+            (f.tiles_m * f.splits) % 8 || (int64_t) f.tiles_m * f.rb_tile < f.rb_n)
+            return hipErrorInvalidValue;
+    }
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
     if (g.y_mode == LN_Y_Q8) {
         // Q8_0 output: the wave kernel only (H = 1024 or 2048)

@@ -186,6 +186,8 @@ hipError_t launch_gemm_group(GemmGroup &g, int flags, int epi, hipStream_t s);
 // 1..5 force one (128x64 / 64x64 / 64x128 / 128x64 2-stage / 64x64 4-stage).
 hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s);
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn);
+// output rows per tile (BM) of a launch_gemm_ks configuration
+int gemm_ks_bm(int cfg);
 // Cooperative-tile GEMM of gemm_ks.hip over row-major (or tiled) bf16 weights
 // and bf16 activation rows, optionally an implicit im2col (conv_ic % 32 == 0)
 // and the SwiGLU epilogue: EPI_STORE_F32 / _BF16, EPI_SWIGLU_F32 / _BF16.
@@ -275,10 +277,24 @@ struct LnStream {
     float *yd;                    // LN_Y_Q8: f32 block scales [rows][H / 32]
     int rows, rows_per_b;
 };
+// Weights of a block GEMM that follows, fetched early into the L2 of the XCD
+// that the GEMM will run each weight tile on: with (tiles_m * splits) % 8 ==
+// 0, launch_gemm_ks deals the (m tile, split) pairs c = tm * splits + split to
+// XCD c % 8 (workgroup L runs on XCD L % 8). One dword per 128-byte line.
+struct L2Prefetch {
+    const uint16_t *w;            // MFMA-tiled bf16 weights: row block rb, k tile kt at (rb * kt_n + kt) * 512
+    int kt_n;                     // K / 32
+    int rb_tile;                  // 16-row blocks per m tile of the GEMM
+    int rb_n;                     // M / 16
+    int tiles_m, splits;
+};
+constexpr int L2PF_MAX = 4;
 struct LnGroup {
     LnStream s[2];
     int nstream, H, y_mode;       // LnOut
     float eps;
+    L2Prefetch pf[L2PF_MAX];      // touched by the LN workgroups while they run (npf 0: none)
+    int npf;
 };
 hipError_t launch_ln_group(const LnGroup &g, hipStream_t s);
 // y = x / sqrt(mean(x^2) + eps) * w on F32 rows of n in {1024, 2048, 4096}
