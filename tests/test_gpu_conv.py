@@ -182,6 +182,32 @@ def test_conv_mlp_swiglu_bf16(env, B, IW, IC, HID, OC):
     assert np.array_equal(tsk.conv_mlp_swiglu(p1, p3, p2, xd).numpy(), got)
 
 
+def test_conv_mlp_swiglu_128x128_tiles(env, monkeypatch):
+    """The reference graph's 30 s convMLP (B = 2, 646 positions, 1024 -> 2816
+    -> 1024, k3) runs its w1 / w3 GEMM on 128 x 128 tiles (484 of them): the
+    oracle bound, and the same bits as 128 x 64 tiles (TSK_COOP_CFG=29: the
+    tile shape changes no summation order)."""
+    tsk, orc = env
+    rng = np.random.default_rng(646)
+    B, IW, IC, HID, OC = 2, 646, 1024, 2816, 1024
+    w1, w3 = kernel(orc, rng, HID, IC, 3), kernel(orc, rng, HID, IC, 3)
+    w2 = kernel(orc, rng, OC, HID, 3)
+    x = rng.standard_normal((B, IW, IC)).astype(np.float32)
+    ds = [tsk.conv1d_pack_weight(tsk.bf16_to_device(w)) for w in (w1, w3, w2)]
+    xd = tsk.to_device(x)
+    got = tsk.conv_mlp_swiglu(*ds, xd).numpy()
+    try:
+        monkeypatch.setenv("TSK_COOP_CFG", "29")
+        tsk.init(0, reread=True)
+        narrow = tsk.conv_mlp_swiglu(*ds, xd).numpy()
+    finally:
+        monkeypatch.delenv("TSK_COOP_CFG", raising=False)
+        tsk.init(0, reread=True)
+    assert np.array_equal(got, narrow)
+    ref = orc.conv_mlp_swiglu(w1, w3, w2, x, w_type=orc.BF16)
+    assert rel_l2(got, ref) <= 3e-4
+
+
 def test_conv_mlp_swiglu_f32(env):
     tsk, orc = env
     rng = np.random.default_rng(17)

@@ -20,7 +20,7 @@ def env(orc):
 
 SHAPES_BF16 = [(388, 1024, 3072), (388, 1024, 1024), (542, 1024, 4096), (388, 4096, 1024),
                (154, 2048, 1024), (194, 3072, 2816), (194, 8448, 1024), (2, 1024, 6144),
-               (1, 64, 1024), (7, 40, 12), (1446, 1024, 3072)]
+               (1, 64, 1024), (7, 40, 12), (1446, 1024, 3072), (1292, 1024, 6144)]
 
 
 @pytest.mark.parametrize("N,K,M", SHAPES_BF16)

@@ -903,7 +903,7 @@ hipError_t conv_epi(GemmGroup &g, int epi, hipStream_t s) {
 hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
     if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
     const bool conv = g.p[0].conv_ic != 0;
-    int64_t tiles = 0;   // 128 x 64 tiles (64 x 64 output features for SwiGLU)
+    int64_t tiles = 0, tiles128 = 0;   // 128 x 64 and 128 x 128 tiles (64 output features for SwiGLU)
     for (int i = 0; i < g.nprob; ++i) {
         const GemmProblem &p = g.p[i];
         if (p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits != 1 || (p.conv_ic != 0) != conv)
@@ -917,16 +917,20 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
                      p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow || p.x_group_stride % 8))
             return hipErrorInvalidValue;
         tiles += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 63) / 64);
+        tiles128 += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 127) / 128);
     }
     // Tile shape, measured on MI355X over the convolution / MLP / DiT shapes:
     // with K % 64 == 0 (and IC % 64 == 0 for convolutions) the 64-wide row
-    // stages, 128 x 64 tiles (2 stages) from ~400 such tiles, 64 x 64 tiles
-    // (3 stages) below; otherwise the 32-wide stages, 128 x 64 from ~512
-    // tiles. Tuning::coop_cfg forces a shape (12, 22, 28, 29, 30; 32 in sweep
-    // builds).
+    // stages: 128 x 128 tiles (2 stages, two workgroups per CU) from ~400 such
+    // tiles (the reference graph's 30 s convMLP w1 / w3, 1292 x 3072 x 2 x
+    // 2816: 78 -> 52 us, half the operand loads per MFMA of 128 x 64 tiles
+    // and one round of workgroups instead of two), 128 x 64 tiles (2 stages)
+    // from ~400 of those, 64 x 64 tiles (3 stages) below; otherwise the
+    // 32-wide stages, 128 x 64 from ~512 tiles. Tuning::coop_cfg forces a
+    // shape (12, 22, 28, 29, 30, 32).
     bool k64 = true;
     for (int i = 0; i < g.nprob; ++i) k64 = k64 && g.p[i].K % 64 == 0 && (!conv || g.p[i].conv_ic % 64 == 0);
-    int cfg = k64 ? (tiles >= 400 ? 29 : 30) : (tiles >= 512 ? 12 : 22);
+    int cfg = k64 ? (tiles128 >= 400 ? 32 : tiles >= 400 ? 29 : 30) : (tiles >= 512 ? 12 : 22);
     if (tuning().coop_cfg) cfg = tuning().coop_cfg;
     if (!k64 && cfg >= 28) cfg = tiles >= 512 ? 12 : 22;
     switch (cfg) {
@@ -935,9 +939,7 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
         case 28: return conv ? conv_epi<8, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 3, false, MODE_COOP64>(g, epi, s);
         case 29: return conv ? conv_epi<8, 4, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 4, 2, false, MODE_COOP64>(g, epi, s);
         case 30: return conv ? conv_epi<4, 4, 3, true, MODE_COOP64>(g, epi, s) : conv_epi<4, 4, 3, false, MODE_COOP64>(g, epi, s);
-#if TSK_SWEEP_VARIANTS
         case 32: return conv ? conv_epi<8, 8, 2, true, MODE_COOP64>(g, epi, s) : conv_epi<8, 8, 2, false, MODE_COOP64>(g, epi, s);
-#endif
         default: return hipErrorInvalidValue;
     }
 }

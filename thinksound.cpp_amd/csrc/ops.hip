@@ -980,13 +980,21 @@ __global__ void add_f32_kernel(const float *a, const float *b, float *y, int64_t
 
 // mean over the S rows of each batch item: x [B][S][H] -> y [B][H]; the sum
 // in double rounded to fp32, then divided by S (ggml_mean, src/mmdit.cpp:186)
-__global__ void row_mean_kernel(const float *x, int S, int H, float *y) {
-    const int b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= H) return;
-    const float *xb = x + (int64_t) b * S * H + c;
+// 64 columns per workgroup: wave w sums rows [w S / 4, (w + 1) S / 4) in
+// double, then the four partial sums are added in order (a sum of at most a
+// few thousand floats of similar size is exact in double in either order)
+__global__ __launch_bounds__(256) void row_mean_kernel(const float *x, int S, int H, float *y) {
+    __shared__ double part[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int b = blockIdx.y, c = blockIdx.x * 64 + lane;
+    const int r0 = (int) ((int64_t) S * w / 4), r1 = (int) ((int64_t) S * (w + 1) / 4);
     double s = 0.0;
-    for (int i = 0; i < S; ++i) s += (double) xb[(int64_t) i * H];
-    y[(int64_t) b * H + c] = (float) s / (float) S;
+    if (c < H)
+        for (int i = r0; i < r1; ++i) s += (double) x[((int64_t) b * S + i) * H + c];
+    part[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && c < H)
+        y[(int64_t) b * H + c] = (float) (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]) / (float) S;
 }
 
 // extended_c[b][t] = sync[b][idx(t)] + g[b], idx(t) = floor((t + 0.5) S / T)
@@ -1052,7 +1060,7 @@ hipError_t launch_add_f32(const float *a, const float *b, float *y, int64_t n, h
 }
 
 hipError_t launch_row_mean(const float *x, int B, int S, int H, float *y, hipStream_t s) {
-    launch_kernel(row_mean_kernel, dim3(blocks_for(H, 256), B), dim3(256), 0, s, x, S, H, y);
+    launch_kernel(row_mean_kernel, dim3((H + 63) / 64, B), dim3(256), 0, s, x, S, H, y);
     return hipGetLastError();
 }
 
