@@ -894,6 +894,7 @@ hipError_t conv_epi(GemmGroup &g, int epi, hipStream_t s) {
         case EPI_STORE_BF16: return ks_launch<TM, TN, R, MODE, EPI_STORE_BF16, 1, CONV>(g, s);
         case EPI_SWIGLU_F32: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_F32, 1, CONV>(g, s);
         case EPI_SWIGLU_BF16: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_BF16, 1, CONV>(g, s);
+        case EPI_PARTIAL: return ks_launch<TM, TN, R, MODE, EPI_PARTIAL, 1, CONV>(g, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -906,8 +907,10 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
     int64_t tiles = 0, tiles128 = 0;   // 128 x 64 and 128 x 128 tiles (64 output features for SwiGLU)
     for (int i = 0; i < g.nprob; ++i) {
         const GemmProblem &p = g.p[i];
-        if (p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits != 1 || (p.conv_ic != 0) != conv)
+        if (p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits < 1 || (p.conv_ic != 0) != conv)
             return hipErrorInvalidValue;
+        // split-K (slices [split][N][ld_y] of f32 partial sums) only as EPI_PARTIAL
+        if (p.splits != 1 && (epi != EPI_PARTIAL || (p.K / 32) % p.splits)) return hipErrorInvalidValue;
         if (!p.w_tiled && (p.ld_w % 8 || ((uintptr_t) p.w & 15) || (p.w3 && ((uintptr_t) p.w3 & 15))))
             return hipErrorInvalidValue;
         if (p.w_tiled && epi_swiglu(epi)) return hipErrorInvalidValue;
@@ -916,8 +919,10 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
         if (conv && (p.conv_ic % 32 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                      p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow || p.x_group_stride % 8))
             return hipErrorInvalidValue;
-        tiles += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 63) / 64);
-        tiles128 += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 127) / 128);
+        tiles += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) * ((p.N + 63) / 64) *
+                 p.splits;
+        tiles128 += (int64_t) ((p.M + (epi_swiglu(epi) ? 63 : 127)) / (epi_swiglu(epi) ? 64 : 128)) *
+                    ((p.N + 127) / 128) * p.splits;
     }
     // Tile shape, measured on MI355X over the convolution / MLP / DiT shapes:
     // with K % 64 == 0 (and IC % 64 == 0 for convolutions) the 64-wide row

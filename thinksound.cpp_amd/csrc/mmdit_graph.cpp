@@ -239,7 +239,7 @@ int lin(const Lin &L, const uint16_t *x, int64_t ld_x, int N, void *y, int64_t l
 // conv_cl (stride 1, padding pad): x bf16 rows [B][IW][IC] with row stride
 // ld_x and batch stride xb (elements), y rows [B * IW][OC] (ld_y)
 int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, void *y, int64_t ld_y,
-         bool y_bf16, hipStream_t s, bool no_bias = false) {
+         bool y_bf16, hipStream_t s, bool no_bias = false, int splits = 1) {
     GemmGroup g;
     memset(&g, 0, sizeof(g));
     g.nprob = 1;
@@ -249,15 +249,30 @@ int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int
     q.bias = no_bias ? nullptr : C.b;
     q.y = y; q.ld_y = ld_y;
     const int OW = IW + 2 * pad - (C.KW - 1);
-    q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = 1;
+    q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = splits;
     q.conv_ic = C.IC; q.conv_iw = IW; q.conv_ow = OW; q.conv_s = 1; q.conv_p = pad; q.conv_d = 1;
-    return hipcheck(launch_gemm_coop(g, y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32, s), "mmdit conv");
+    const int epi = splits > 1 ? EPI_PARTIAL : y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32;
+    return hipcheck(launch_gemm_coop(g, epi, s), "mmdit conv");
+}
+
+// K slices of a residual-branch convolution (linear1, convMLP w2) whose
+// partial sums the next LayerNorm adds up: with few output tiles (1024
+// outputs x 388 rows at 9 s is 112 tiles of 64 x 64) each workgroup would
+// stream all of K = 3072 / 8448 alone; the slices fill the 256 CUs (up to
+// three workgroups each).
+constexpr int GRAPH_KSPLIT_MAX = 4;
+int conv_splits(const Conv &C, int N) {
+    const int64_t tiles = (int64_t) ((C.OC + 63) / 64) * ((N + 63) / 64);
+    const int kt = C.KW * C.IC / 32;
+    int sp = 1;
+    while (sp < GRAPH_KSPLIT_MAX && tiles * sp * 2 <= 768 && kt % (2 * sp) == 0 && (kt / (2 * sp)) % 2 == 0) sp *= 2;
+    return sp;
 }
 
 // convmlp / mlp (src/mmdit.cpp:39-52): y = w2(silu(w1 x) * w3 x), the hidden
 // state bf16 in m->hid (the conversion w2's mul_mat applies to it)
 int conv_mlp(tsk_mmdit *m, const Conv &w1, const Conv &w3, const Conv &w2, const uint16_t *x, int64_t ld_x, int64_t xb,
-             int IW, int B, float *y, int64_t ld_y, hipStream_t s) {
+             int IW, int B, float *y, int64_t ld_y, hipStream_t s, int splits = 1) {
     GemmGroup g;
     memset(&g, 0, sizeof(g));
     g.nprob = 1;
@@ -269,7 +284,7 @@ int conv_mlp(tsk_mmdit *m, const Conv &w1, const Conv &w3, const Conv &w2, const
     q.conv_ic = w1.IC; q.conv_iw = IW; q.conv_ow = IW; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
     int rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_BF16, s), "mmdit convmlp w1/w3");
     if (rc) return rc;
-    return conv(w2, m->hid, w1.OC, (int64_t) IW * w1.OC, IW, B, 1, y, ld_y, false, s, true);
+    return conv(w2, m->hid, w1.OC, (int64_t) IW * w1.OC, IW, B, 1, y, ld_y, false, s, true, splits);
 }
 
 int lin_mlp(tsk_mmdit *m, const Lin &w1, const Lin &w3, const Lin &w2, const uint16_t *x, int64_t ld_x, int N, float *y,
@@ -299,6 +314,7 @@ struct Stream {
     float *part;           // f32 output of the previous projection (residual update owed)
     const float *pend_bias, *pend_gate;
     int64_t pend_ld;       // row stride of pend_gate (the owing block's adaLN width)
+    int pend_split;        // K slices of part ([split][B S][H]) the owed update is summed from
     bool pending;
 };
 
@@ -309,7 +325,7 @@ LnStream ln_of(const tsk_mmdit *m, Stream &r, int B, int which) {
     l.x = r.x; l.ld_x = H;
     const int64_t ldm = (int64_t) r.w->nmod * H;
     if (r.pending) {
-        l.part = r.part; l.nsplit = 1; l.part_stride = 0;
+        l.part = r.part; l.nsplit = r.pend_split > 1 ? r.pend_split : 1; l.part_stride = (int64_t) B * r.S * H;
         l.bias = r.pend_bias; l.gate = r.pend_gate; l.ld_gate = r.pend_ld;
         r.pending = false;
     }
@@ -409,7 +425,8 @@ int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         const Block &b = *r[i].w;
         const uint16_t *orows = m->o + (size_t) r[i].tok_off * H;
         const int64_t ob = (int64_t) m->Nmax * H;      // batch stride of the attention output rows
-        if (b.conv) rc = conv(b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, true);
+        r[i].pend_split = b.conv ? conv_splits(b.l1c, B * r[i].S) : 1;
+        if (b.conv) rc = conv(b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, true, r[i].pend_split);
         else {
             // text: linear1 rows grouped by batch item
             GemmGroup g;
@@ -438,7 +455,9 @@ int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         if (r[i].w->pre_only) continue;
         r[i].pending = live[j++].pending;
         const Block &b = *r[i].w;
-        rc = b.conv ? conv_mlp(m, b.w1c, b.w3c, b.w2c, r[i].xn, H, (int64_t) r[i].S * H, r[i].S, B, r[i].part, H, s)
+        r[i].pend_split = b.conv ? conv_splits(b.w2c, B * r[i].S) : 1;
+        rc = b.conv ? conv_mlp(m, b.w1c, b.w3c, b.w2c, r[i].xn, H, (int64_t) r[i].S * H, r[i].S, B, r[i].part, H, s,
+                               r[i].pend_split)
                     : lin_mlp(m, b.w1, b.w3, b.w2, r[i].xn, H, B * r[i].S, r[i].part, H, s);
         if (rc) return rc;
         r[i].pending = true;
@@ -564,7 +583,7 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         (rc = alloc((void **) &m->q, 2 * (size_t) B * m->Nmax * H)) ||
         (rc = alloc((void **) &m->k, 2 * (size_t) B * m->Nmax * H)) ||
         (rc = alloc((void **) &m->vt, 2 * (size_t) B * H * m->ldv)) ||
-        (rc = alloc((void **) &m->part, sizeof(float) * rows3 * H)) ||
+        (rc = alloc((void **) &m->part, sizeof(float) * GRAPH_KSPLIT_MAX * rows3 * H)) ||
         (rc = alloc((void **) &m->qkv32, sizeof(float) * R * 3 * H)) ||
         (rc = alloc((void **) &m->tmp32, sizeof(float) * R * std::max(H, c.latent_dim))) ||
         (rc = alloc((void **) &m->rope_l, sizeof(float) * T * 64)) ||
@@ -839,11 +858,11 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
     memset(&Cs, 0, sizeof(Cs));
     memset(&Xs, 0, sizeof(Xs));
     Ls.x = m->lat; Ls.S = T; Ls.tok_off = 0; Ls.rope_cs = m->rope_l; Ls.per_token = 1;
-    Ls.xn = m->xn + rL * H; Ls.part = m->part + rL * H;
+    Ls.xn = m->xn + rL * H; Ls.part = m->part + GRAPH_KSPLIT_MAX * rL * H;
     Cs.x = m->clip; Cs.S = clip_S; Cs.tok_off = T; Cs.rope_cs = m->rope_c; Cs.per_token = 0;
-    Cs.xn = m->xn + rC * H; Cs.part = m->part + rC * H;
+    Cs.xn = m->xn + rC * H; Cs.part = m->part + GRAPH_KSPLIT_MAX * rC * H;
     Xs.x = m->txt; Xs.S = X; Xs.tok_off = T + clip_S; Xs.rope_cs = nullptr; Xs.per_token = 0;
-    Xs.xn = m->xn + rX * H; Xs.part = m->part + rX * H;
+    Xs.xn = m->xn + rX * H; Xs.part = m->part + GRAPH_KSPLIT_MAX * rX * H;
     // a block's residual updates are applied by the next LayerNorm launch:
     // the stage tensors after block 0 and after the joint blocks are taken
     // right after that launch
