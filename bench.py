@@ -168,6 +168,38 @@ def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
     return out
 
 
+def attention_node_bench(tsk, reps=20, B=2, H=16, N=723, seed=33):
+    """The flash_attn_ext node with bf16 Q / K / V as a ggml graph hands it
+    over (the 30 s joint attention, 646 latent + 77 text tokens, 16 x 64
+    heads, B = 2; scale 1/8, F32 precision): tsk_flash_attn_ext, i.e. the V
+    transpose into the stream's workspace plus the attention kernel, on
+    device-resident N(0, 1) operands (what QK-RMSNorm leaves: rows of unit
+    RMS). us per call and TFLOP/s by 4 B H N^2 64."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+
+    def bf16(shape):
+        u = rng.standard_normal(shape, dtype=np.float32).view(np.uint32)
+        return tsk.bf16_to_device(((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16))
+
+    q, k, v = bf16((B, H, N, 64)), bf16((B, H, N, 64)), bf16((B, H, N, 64))
+    out = tsk.empty((B, N, H, 64))
+    for _ in range(3):
+        tsk.flash_attn_ext(q, k, v, scale=0.125, out=out)
+    tsk.synchronize()
+    s, e = tsk.Event(), tsk.Event()
+    s.record()
+    for _ in range(reps):
+        tsk.flash_attn_ext(q, k, v, scale=0.125, out=out)
+    e.record()
+    tsk.synchronize()
+    us = s.elapsed_ms(e) / reps * 1e3
+    tf = 4.0 * B * H * N * N * 64 / (us * 1e-6) / 1e12
+    return {"us": round(us, 2), "tflops": round(tf, 1), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "shape": f"B={B} H={H} N={N} D=64, bf16 Q/K/V, f32 output",
+            "note": "includes the V transpose launch of the ggml node path"}
+
+
 def q8_blocks(rng, M, K, scale):
     """ggml Q8_0 blocks (M, K/32, 34) uint8: fp16 scale then int8 values uniform in [-127, 127]."""
     import numpy as np
@@ -482,6 +514,8 @@ def main():
     # convmlp 1024 -> 2816 -> 1024 (k3, padding 1, SwiGLU) and a conv_cl
     # linear1 1024 -> 1024 (k3), BF16 kernels packed kw-major once, f32 input
     conv30 = conv_bench(tsk, reps=max(5, args.steps))
+    # configuration 3's attention as the ggml node (bf16 Q / K / V, 723 tokens)
+    attn_node = attention_node_bench(tsk, reps=max(5, args.steps))
     # the reference's own three-stream graph at 9 s and 30 s
     graph = graph_bench(tsk, max(5, args.steps // 2))
     # the VAE decode after the sampler
@@ -532,6 +566,7 @@ def main():
         "breakdown_9s": breakdown(roles9, args.steps),
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
         "conv_30s": conv30,
+        "attention_node_bf16_30s": attn_node,
         "q8_0_projections_30s": q8,
         "q8_0_flow_step_9s": {"steps_per_s": round(1000.0 / ms_q8, 2), "ms_per_step": round(ms_q8, 4),
                               "weights": "Q8_0 attn.qkv / linear1 / ffn.fc1 / ffn.fc2 (ggml reference "

@@ -668,18 +668,21 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
     // follow into the L2 of the XCDs that will read them (qkv and linear1
     // after the attention LN, fc1 and fc2 after the MLP LN). The LN then ends
     // only when those loads have landed; measured on MI355X this pays from
-    // ~800 latent rows (T = 400: 1.95 -> 1.86 ms, 30 s: 2.46 -> 2.33 ms per
-    // step) and breaks even at 388 (9 s), where the LN kernels are too short
-    // to cover the extra 16-32 MB of weight reads: on from 512 rows.
+    // ~800 latent rows (T = 400: 1.94 -> 1.92 ms, 30 s: 2.44-2.46 -> 2.33-2.39
+    // ms per step on different boxes) and breaks even at 388 (9 s), where the
+    // LN kernels are too short to cover the extra 16-32 MB of weight reads:
+    // on from 512 rows.
     const int rows0 = B * r[0].S;
     const int pf_mode = tuning().l2_prefetch;
+    L2PrefetchList pf;
+    memset(&pf, 0, sizeof(pf));
     if (!d->q8 && (pf_mode > 0 || (pf_mode < 0 && rows0 >= 512))) {
         auto add = [&](const uint16_t *w, int K, int M, int role, int splits) {
             const int bm = gemm_ks_bm(gemm_cfg_for(d, role, rows0));
-            L2Prefetch &f = g.pf[g.npf];
+            L2Prefetch &f = pf.pf[pf.npf];
             f.w = w; f.kt_n = K / 32; f.rb_tile = bm / 16; f.rb_n = M / 16;
             f.tiles_m = (M + bm - 1) / bm; f.splits = splits;
-            if ((f.tiles_m * f.splits) % 8 == 0 && f.kt_n % splits == 0) ++g.npf;
+            if ((f.tiles_m * f.splits) % 8 == 0 && f.kt_n % splits == 0) ++pf.npf;
         };
         for (int i = 0; i < ns; ++i) {
             const StreamW &w = *r[i].w;
@@ -694,7 +697,7 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
         }
     }
     Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * H, 14.0 * rows * H + pbytes, st);
-    return hipcheck(launch_ln_group(g, st), "ln_group");
+    return hipcheck(launch_ln_group(g, st, pf.npf ? &pf : nullptr), "ln_group");
 }
 
 // Block GEMM tile shape by projection and activation rows of the larger

@@ -460,12 +460,20 @@ __device__ __forceinline__ void l2_prefetch(const L2Prefetch *pf, int npf, void 
 
 template <int YM, int NV>
 __global__ __launch_bounds__(64) void ln_wave_kernel(const LnGroup g) {
-    __shared__ __attribute__((aligned(16))) uint32_t sink[64];
     const int r = blockIdx.x;
-    if (g.npf) l2_prefetch(g.pf, g.npf, sink);
     if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YM, NV>(g.s[1], r - g.s[0].rows, g.eps);
     else ln_wave_row<YM, NV>(g.s[0], r, g.eps);
-    if (g.npf) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// the same rows, the workgroups also touching the next GEMMs' weights into L2
+template <int YM, int NV>
+__global__ __launch_bounds__(64) void ln_wave_pf_kernel(const LnGroup g, const L2PrefetchList pf) {
+    __shared__ __attribute__((aligned(16))) uint32_t sink[64];
+    const int r = blockIdx.x;
+    l2_prefetch(pf.pf, pf.npf, sink);
+    if (g.nstream > 1 && r >= g.s[0].rows) ln_wave_row<YM, NV>(g.s[1], r - g.s[0].rows, g.eps);
+    else ln_wave_row<YM, NV>(g.s[0], r, g.eps);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // GEMV list: one wave per output row; lane k-slices of 8, f32 activations
@@ -853,14 +861,21 @@ hipError_t launch_f32_to_bf16(const float *x, uint16_t *y, int64_t n, hipStream_
     return hipGetLastError();
 }
 
-hipError_t launch_ln_group(const LnGroup &g, hipStream_t s) {
+hipError_t launch_ln_group(const LnGroup &g, hipStream_t s, const L2PrefetchList *pf) {
     if (g.nstream < 1 || g.nstream > 2 || g.H < 4 || g.H % 4 || g.H > 4096) return hipErrorInvalidValue;
-    if (g.npf < 0 || g.npf > L2PF_MAX) return hipErrorInvalidValue;
-    for (int i = 0; i < g.npf; ++i) {
-        const L2Prefetch &f = g.pf[i];
+    if (pf && (pf->npf < 0 || pf->npf > L2PF_MAX)) return hipErrorInvalidValue;
+    for (int i = 0; pf && i < pf->npf; ++i) {
+        const L2Prefetch &f = pf->pf[i];
         if (!f.w || f.kt_n < 1 || f.splits < 1 || f.kt_n % f.splits || f.rb_tile < 1 || f.rb_n < 1 ||
             (f.tiles_m * f.splits) % 8 || (int64_t) f.tiles_m * f.rb_tile < f.rb_n)
             return hipErrorInvalidValue;
+    }
+    if (pf && pf->npf > 0) {
+        // the BF16 DiT's LN (H = 1024, bf16 rows) only
+        const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
+        if (g.H != 1024 || g.y_mode != LN_Y_BF16) return hipErrorInvalidValue;
+        launch_kernel(ln_wave_pf_kernel<LN_Y_BF16, 4>, dim3(rows), dim3(64), 0, s, g, *pf);
+        return hipGetLastError();
     }
     const int rows = g.s[0].rows + (g.nstream > 1 ? g.s[1].rows : 0);
     if (g.y_mode == LN_Y_Q8) {

@@ -289,14 +289,17 @@ struct L2Prefetch {
     int tiles_m, splits;
 };
 constexpr int L2PF_MAX = 4;
+struct L2PrefetchList {
+    L2Prefetch pf[L2PF_MAX];
+    int npf;
+};
 struct LnGroup {
     LnStream s[2];
     int nstream, H, y_mode;       // LnOut
     float eps;
-    L2Prefetch pf[L2PF_MAX];      // touched by the LN workgroups while they run (npf 0: none)
-    int npf;
 };
-hipError_t launch_ln_group(const LnGroup &g, hipStream_t s);
+// pf (nullable, npf > 0): weights the LN workgroups touch into L2 while they run
+hipError_t launch_ln_group(const LnGroup &g, hipStream_t s, const L2PrefetchList *pf = nullptr);
 // y = x / sqrt(mean(x^2) + eps) * w on F32 rows of n in {1024, 2048, 4096}
 // (16-byte aligned), quantized to Q8_0 planes qx [rows][n] / dx [rows][n/32]
 // as launch_quantize_rows_q8 does: the two launches' bits in one
