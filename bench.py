@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
+PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 
 
 def make_inputs(B, T, seed=4242):
@@ -380,10 +381,32 @@ def vae_bench(tsk, reps=3):
         e.record()
         tsk.synchronize()
         ms = s.elapsed_ms(e) / reps
+        fl = vae_flops(tsk.vae_config(), T)
+        tf = fl / (ms / 1e3) / 1e12
         out[label] = {"ms": round(ms, 3), "latent_frames": T, "samples": T * v.hop,
-                      "realtime_factor": round(T * v.hop / 44100.0 / (ms / 1e3), 1)}
+                      "realtime_factor": round(T * v.hop / 44100.0 / (ms / 1e3), 1),
+                      "tflops": round(tf, 1), "frac_of_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)}
     v.close()
     return out
+
+
+def vae_flops(c, T):
+    """Multiply-adds x 2 of the Oobleck decoder's convolutions for T latent
+    frames (src/vae_decoder.cpp:62-124): conv k7 latent -> 16 C; per block
+    (multipliers run backwards) a transposed convolution of stride s whose
+    output samples each take 2 taps (kernel 2 s) and three residual units of a
+    k7 and a k1 convolution; the final k7 conv C -> out. (The device runs the
+    transposed convolutions as 3-tap phase convolutions, a third more MFMA
+    work than counted here; the reference's zero-stuffed form does s x more.)"""
+    C = c.channels
+    mult = [1] + list(c.c_mults)
+    t = T
+    fl = 2.0 * t * mult[5] * C * c.latent_dim * 7
+    for n in range(5):
+        ic, oc, st = mult[5 - n] * C, mult[4 - n] * C, c.strides[4 - n]
+        t *= st
+        fl += 2.0 * t * oc * ic * 2 + 3 * 2.0 * t * oc * oc * (7 + 1)
+    return fl + 2.0 * t * c.out_channels * C * 7
 
 
 def copy_calibration(nbytes=256 << 20, reps=5):

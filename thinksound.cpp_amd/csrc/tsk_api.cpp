@@ -619,6 +619,7 @@ extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, cons
         f.ldv = ldv;
         f.o_nb1 = dst->nb[1]; f.o_nb2 = dst->nb[2]; f.o_nb3 = dst->nb[3];
         f.c = scale * 1.4426950408889634f;
+        f.force_cfg = tuning().attn_cfg;
         e = launch_attn_fast(f, st);
         if (e != hipSuccess) return hip_fail(e, "flash_attn_ext launch");
         return TSK_OK;
