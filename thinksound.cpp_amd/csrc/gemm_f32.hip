@@ -26,8 +26,8 @@ constexpr int NT = 256;
 constexpr int BK = 32;
 constexpr int LDK = BK + 4;   // floats per LDS row: 16-B aligned, the 16 rows of a read hit distinct banks
 
-template <int TM, int TN, bool YBF16>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
+template <int TM, int TN, bool YBF16, bool SNAKE>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const F32Snake sk) {
     constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
     constexpr int WCH = BM * (BK / 4), XCH = BN * (BK / 4);   // 16-B chunks per tile
     constexpr int WPER = WCH / NT, XPER = XCH / NT;
@@ -136,6 +136,14 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
         if (p.bias)
             for (int r = 0; r < 4 && m0 + r < p.M; ++r) bv[r] = p.bias[m0 + r];
+        float ea[4] = {0.f, 0.f, 0.f, 0.f}, eb[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (SNAKE) {
+            const int c0 = m0 % sk.period;   // period is a multiple of 4: c0 + 3 < period
+            for (int r = 0; r < 4 && m0 + r < p.M; ++r) {
+                ea[r] = sk.ea[c0 + r];
+                eb[r] = sk.eb[c0 + r];
+            }
+        }
         for (int j = 0; j < TN; ++j) {
             const int n = bn0 + (wn * TN + j) * 16 + lr;
             if (n >= p.N) continue;
@@ -146,17 +154,42 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
                 for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
             } else {
                 float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
+                float v[4];
                 if (p.accumulate) {
                     if (full) {
-                        const f32x4 v = *(const f32x4 *) yr;
-                        *(f32x4 *) yr = f32x4{v[0] + o[0], v[1] + o[1], v[2] + o[2], v[3] + o[3]};
+                        const f32x4 a = *(const f32x4 *) yr;
+                        for (int r = 0; r < 4; ++r) v[r] = a[r] + o[r];
                     } else {
-                        for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] += o[r];
+                        for (int r = 0; r < 4; ++r) v[r] = m0 + r < p.M ? yr[r] + o[r] : 0.0f;
                     }
-                } else if (full) {
-                    *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
                 } else {
-                    for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = o[r];
+                    for (int r = 0; r < 4; ++r) v[r] = o[r];
+                }
+                float sv[4];
+                if constexpr (SNAKE)
+                    for (int r = 0; r < 4; ++r) {
+                        const float sn = sinf(v[r] * ea[r]);
+                        sv[r] = v[r] + (sn * sn) * eb[r];
+                    }
+                // y: the snake in place (SNAKE without y2) or the plain value;
+                // y2: the snake next to it
+                const bool in_place = SNAKE && !sk.y2;
+                float w[4];
+                for (int r = 0; r < 4; ++r) w[r] = in_place ? sv[r] : v[r];
+                if (full) {
+                    *(f32x4 *) yr = f32x4{w[0], w[1], w[2], w[3]};
+                } else {
+                    for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = w[r];
+                }
+                if constexpr (SNAKE) {
+                    if (sk.y2) {
+                        float *y2r = sk.y2 + (int64_t) n * p.ld_y + m0;
+                        if (full) {
+                            *(f32x4 *) y2r = f32x4{sv[0], sv[1], sv[2], sv[3]};
+                        } else {
+                            for (int r = 0; r < 4 && m0 + r < p.M; ++r) y2r[r] = sv[r];
+                        }
+                    }
                 }
             }
         }
@@ -165,15 +198,19 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p) {
 
 }  // namespace
 
-hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s) {
+hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake) {
     constexpr int TM = 4, TN = 2, BM = 2 * TM * 16, BN = 2 * TN * 16;
     if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf || (p.accumulate && y_bf16)) return hipErrorInvalidValue;
+    if (snake && (y_bf16 || !snake->ea || !snake->eb || snake->period < 4 || snake->period % 4 || p.M % snake->period))
+        return hipErrorInvalidValue;
     if (p.conv_ic && (p.conv_ic % 4 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;
     dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
-    if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true>), grid, dim3(NT), 0, s, p);
-    else launch_kernel((gemm_f32_kernel<TM, TN, false>), grid, dim3(NT), 0, s, p);
+    const F32Snake none = {nullptr, nullptr, nullptr, 1};
+    if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true, false>), grid, dim3(NT), 0, s, p, none);
+    else if (snake) launch_kernel((gemm_f32_kernel<TM, TN, false, true>), grid, dim3(NT), 0, s, p, *snake);
+    else launch_kernel((gemm_f32_kernel<TM, TN, false, false>), grid, dim3(NT), 0, s, p, none);
     return hipGetLastError();
 }
 

@@ -1046,24 +1046,6 @@ hipError_t launch_add_period_rows(const float *x, int64_t rows, int cols, const 
     return hipGetLastError();
 }
 
-// SnakeBeta (src/vae_decoder.cpp:14-24): x + sin(x ea)^2 eb, in the
-// reference's node order (mul, sin, sqr, mul, add)
-__global__ void snake_kernel(const float *x, const float *ea, const float *eb, int64_t n, int cols, float *y) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const int c = (int) (i % cols);
-    const float v = x[i];
-    const float sn = sinf(v * ea[c]);
-    y[i] = v + (sn * sn) * eb[c];
-}
-
-hipError_t launch_snake(const float *x, const float *ea, const float *eb, int64_t rows, int cols, float *y,
-                        hipStream_t s) {
-    const int64_t n = rows * cols;
-    launch_kernel(snake_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, ea, eb, n, cols, y);
-    return hipGetLastError();
-}
-
 hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s) {
     launch_kernel(silu_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
     return hipGetLastError();

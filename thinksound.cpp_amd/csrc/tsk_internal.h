@@ -332,13 +332,20 @@ hipError_t launch_cast_rows_bf16(const float *x, int64_t ld_x, int64_t ld_b, int
 // kw-major rows dst[oc][kw * IC + ic]
 hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
                             hipStream_t s);
+// SnakeBeta v + sin^2(v ea[c]) eb[c] (src/vae_decoder.cpp:14-24, in the
+// reference's node order mul, sin, sqr, mul, add) applied to an f32 GEMM's
+// output: c = m % period (period a multiple of 4 dividing M), ea = exp(alpha),
+// eb = exp(-beta); written in place of the output (y2 null), or next to it
+// into y2 (same row stride; the output itself then stays plain)
+struct F32Snake {
+    const float *ea, *eb;
+    float *y2;
+    int period;
+};
 // F32-weight GEMM (gemm_f32.hip): p.wf [M][K] (ld_w), f32 activations p.x
-// (plain rows or implicit im2col), y f32 or bf16 (+bias)
-hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s);
-// SnakeBeta on token-major rows: y[t][c] = x[t][c] + sin^2(x[t][c] ea[c]) eb[c]
-// (ea = exp(alpha), eb = exp(-beta)), rows x cols f32 (x may equal y)
-hipError_t launch_snake(const float *x, const float *ea, const float *eb, int64_t rows, int cols, float *y,
-                        hipStream_t s);
+// (plain rows or implicit im2col), y f32 or bf16 (+bias), optionally followed
+// by a SnakeBeta (f32 y only)
+hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake = nullptr);
 // y = silu(a) * b, f32, n elements
 hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
 // y[n, m] = sum_k W[m, k] x[n, k] + bias[m]: bf16 row-major W, f32 x and y,

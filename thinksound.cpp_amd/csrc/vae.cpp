@@ -24,6 +24,7 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "../../include/tsk/tsk.h"
@@ -87,9 +88,16 @@ void block_dims(const tsk_vae_config &c, int n, int *in, int *out, int *s) {
 const VW &wi(const tsk_vae *v, const std::string &n) { return v->w[v->idx.at(n)]; }
 const float *wp(const tsk_vae *v, const std::string &n) { return v->blob + wi(v, n).offset; }
 
-// y rows [T_out][OC] = conv(x rows [T_in][IC]) + bias, stride 1 (F32 GEMM)
+// the SnakeBeta of the named parameters over C channels, for a GEMM epilogue:
+// in place of the output (y2 null) or next to it into y2
+F32Snake snake_epi(const tsk_vae *v, const std::string &p, int C, float *y2) {
+    return F32Snake{wp(v, p + ".alpha"), wp(v, p + ".beta"), y2, C};
+}
+
+// y rows [T_out][OC] = conv(x rows [T_in][IC]) + bias, stride 1 (F32 GEMM),
+// optionally followed by a SnakeBeta
 int conv(const tsk_vae *v, const std::string &p, bool bias, const float *x, int IC, int T_in, int pad, int dil,
-         float *y, bool accumulate, hipStream_t s) {
+         float *y, bool accumulate, hipStream_t s, const F32Snake *sk = nullptr) {
     const VW &w = wi(v, p + ".weight");
     const int KW = (int) w.ne[0], OC = (int) w.ne[2];
     GemmProblem q;
@@ -104,11 +112,12 @@ int conv(const tsk_vae *v, const std::string &p, bool bias, const float *x, int 
         q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_out; q.conv_s = 1; q.conv_p = pad; q.conv_d = dil;
     }
     q.accumulate = accumulate ? 1 : 0;
-    return hipcheck(launch_gemm_f32(q, 0, s), "vae conv");
+    return hipcheck(launch_gemm_f32(q, 0, s, sk), "vae conv");
 }
 
 // transposed convolution as the merged 3-tap convolution: y rows [s T_in][OC]
-int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T_in, float *y, hipStream_t s) {
+int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T_in, float *y, hipStream_t s,
+           const F32Snake *sk = nullptr) {
     const VW &w = wi(v, p + ".weight");
     const int OC = (int) w.ne[2], st = w.stride;
     GemmProblem q;
@@ -119,11 +128,7 @@ int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T
     q.y = y; q.ld_y = (int64_t) st * OC;
     q.M = st * OC; q.N = T_in; q.K = 3 * IC; q.splits = 1;
     q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_in; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
-    return hipcheck(launch_gemm_f32(q, 0, s), "vae transposed conv");
-}
-
-int snake(const tsk_vae *v, const std::string &p, const float *x, int64_t rows, int C, float *y, hipStream_t s) {
-    return hipcheck(launch_snake(x, wp(v, p + ".alpha"), wp(v, p + ".beta"), rows, C, y, s), "vae snake");
+    return hipcheck(launch_gemm_f32(q, 0, s, sk), "vae transposed conv");
 }
 
 int validate(const tsk_vae_config *c) {
@@ -292,10 +297,16 @@ int decode_impl(tsk_vae *v, int T, const float *latent_d, float *audio_d, hipStr
     int rc;
     // latent ne = [T, latent_dim] (time fastest) -> rows [T][latent_dim]
     if ((rc = hipcheck(launch_transpose_ct(latent_d, 1, c.latent_dim, T, v->lat, st), "vae latent"))) return rc;
-    float *x = v->act[0], *h = v->act[1], *g = v->act[2];
+    // Every SnakeBeta runs in the epilogue of the convolution that produces
+    // its input: x (buffer 0) holds the residual stream, sx (buffer 1 or 2)
+    // the snake of x that the next convolution reads, t the other one. A
+    // convolution never writes the buffer it reads.
+    float *x = v->act[0], *sx = v->act[1], *t = v->act[2];
     int in0, out0, s0;
     block_dims(c, 0, &in0, &out0, &s0);
-    if ((rc = conv(v, "decoder.layers.0", true, v->lat, c.latent_dim, T, 3, 1, x, false, st))) return rc;
+    // conv k7 -> snake of block 1 (the conv's own output is not used again)
+    F32Snake sk = snake_epi(v, "decoder.layers.1.layers.0", in0, nullptr);
+    if ((rc = conv(v, "decoder.layers.0", true, v->lat, c.latent_dim, T, 3, 1, sx, false, st, &sk))) return rc;
     int64_t frames = T;
     int C = in0;
     const int dil[3] = {1, 3, 9};
@@ -303,23 +314,29 @@ int decode_impl(tsk_vae *v, int T, const float *latent_d, float *audio_d, hipStr
         int ci, co, s;
         block_dims(c, n, &ci, &co, &s);
         const std::string bp = "decoder.layers." + std::to_string(n + 1);
-        if ((rc = snake(v, bp + ".layers.0", x, frames, ci, h, st))) return rc;
-        if ((rc = conv_t(v, bp + ".layers.1", h, ci, (int) frames, x, st))) return rc;
+        // x = conv_t(snake(x)); t = snake of the first residual unit's input
+        sk = snake_epi(v, bp + ".layers.2.layers.0", co, t);
+        if ((rc = conv_t(v, bp + ".layers.1", sx, ci, (int) frames, x, st, &sk))) return rc;
+        std::swap(sx, t);
         frames *= s;
         C = co;
         for (int r = 0; r < 3; ++r) {
             // x += conv_k1(snake(conv_k7_dil(snake(x))))  (the residual unit, :99-105)
             const std::string rp = bp + ".layers." + std::to_string(r + 2);
-            if ((rc = snake(v, rp + ".layers.0", x, frames, C, h, st))) return rc;
-            if ((rc = conv(v, rp + ".layers.1", true, h, C, (int) frames, 3 * dil[r], dil[r], g, false, st))) return rc;
-            if ((rc = snake(v, rp + ".layers.2", g, frames, C, g, st))) return rc;
-            if ((rc = conv(v, rp + ".layers.3", true, g, C, (int) frames, 0, 1, x, true, st))) return rc;
+            sk = snake_epi(v, rp + ".layers.2", C, nullptr);
+            if ((rc = conv(v, rp + ".layers.1", true, sx, C, (int) frames, 3 * dil[r], dil[r], t, false, st, &sk)))
+                return rc;
+            // the next snake of x: the next unit's, the next block's, or the final one
+            const std::string np = r < 2 ? bp + ".layers." + std::to_string(r + 3) + ".layers.0"
+                                 : n < 4 ? "decoder.layers." + std::to_string(n + 2) + ".layers.0"
+                                         : std::string("decoder.layers.6");
+            sk = snake_epi(v, np, C, sx);
+            if ((rc = conv(v, rp + ".layers.3", true, t, C, (int) frames, 0, 1, x, true, st, &sk))) return rc;
         }
     }
-    // final snake -> conv k7 (no bias) -> rows [T_audio][out_channels] -> planar
-    if ((rc = snake(v, "decoder.layers.6", x, frames, C, h, st))) return rc;
-    if ((rc = conv(v, "decoder.layers.7", false, h, C, (int) frames, 3, 1, g, false, st))) return rc;
-    return hipcheck(launch_transpose_ct(g, 1, (int) frames, c.out_channels, audio_d, st), "vae audio");
+    // conv k7 (no bias) of the final snake -> rows [T_audio][out_channels] -> planar
+    if ((rc = conv(v, "decoder.layers.7", false, sx, C, (int) frames, 3, 1, t, false, st))) return rc;
+    return hipcheck(launch_transpose_ct(t, 1, (int) frames, c.out_channels, audio_d, st), "vae audio");
 }
 
 }  // namespace
@@ -341,9 +358,9 @@ extern "C" int tsk_vae_decode(tsk_vae *v, int T, const float *latent, float *aud
     const tsk_vae_config &c = v->cfg;
     const size_t n_in = (size_t) T * c.latent_dim, n_out = (size_t) T * v->hop * c.out_channels;
     hipStream_t st = (hipStream_t) stream;
-    // device staging: the latent after the activation rows of buffer 2 (free
-    // until the last convolution), the audio in buffer 1 (the last snake's
-    // output is consumed before the transpose writes it)
+    // device staging: the latent at the end of buffer 2 (read by the first
+    // transpose, before any convolution writes there), the audio in buffer 0
+    // (the residual stream, last read by the last residual unit)
     float *d_lat = v->act[2] + (v->act_cap - n_in);
     float *d_audio = v->act[0];
     if (n_out > v->act_cap) return fail(TSK_ERR_SHAPE, "audio exceeds the capacity");
