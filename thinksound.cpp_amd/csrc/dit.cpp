@@ -854,8 +854,25 @@ int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
     return TSK_OK;
 }
 
+// split-K partials of a Q8_0 projection into the stream's partial slices;
+// the next LN adds gate * (sum of the slices + bias) to the residual, as for
+// the BF16 projections
+void q8_partials(const tsk_dit *d, GemmParams &p, StreamRun &r, int B, int splits, const float *bias, int gate_chunk) {
+    const int H = d->cfg.hidden;
+    p.bias = nullptr;
+    p.epi = EPI_STORE;
+    p.y = r.part; p.ld_y = H;
+    p.splits = splits;
+    p.part_stride = (int64_t) B * r.S * H;
+    r.pend_split = splits;
+    r.pend_bias = bias;
+    r.pend_gate = mod_of(d, *r.w) + gate_chunk * H;
+    r.pend_ld_gate = mod_ld(d, *r.w);
+}
+
 // linear1 on the f32 attention output of each stream (quantized per stream),
-// gate_msa * (linear1 + bias) added to the residual in the epilogue
+// split-K partials; gate_msa * (linear1 + bias) is added to the residual by
+// the next LN
 int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const int H = d->cfg.hidden;
     int rc;
@@ -870,20 +887,17 @@ int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
     }
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
-        GemmParams p = q8_problem(d, r[i].w->l1_q, r[i], B, H, H, r[i].w->l1_b);
-        p.epi = EPI_GATE_RES;
-        p.res = r[i].x; p.ld_res = H;
-        p.gate = mod_of(d, *r[i].w) + 2 * H;   // gate_msa
-        p.ld_gate = mod_ld(d, *r[i].w);
-        p.rows_per_gate = r[i].S;
-        Timed tm(d, TSK_ROLE_OUT, 2.0 * p.N * H * H, q8_bytes(p.N, H, H, 8), st);
+        GemmParams p = q8_problem(d, r[i].w->l1_q, r[i], B, H, H, nullptr);
+        q8_partials(d, p, r[i], B, d->ksplit_out, r[i].w->l1_b, 2);   // gate_msa
+        Timed tm(d, TSK_ROLE_OUT, 2.0 * p.N * H * H, q8_bytes(p.N, H, H, 4 * p.splits), st);
         if ((rc = hipcheck(launch_gemm_q8(p, st), "linear1 q8 gemm"))) return rc;
     }
     return TSK_OK;
 }
 
 // fc1 (+ GELU, f32 out) of every stream, then per stream the quantize of the
-// GELU output and fc2 with gate_mlp * (fc2 + bias) added to the residual
+// GELU output and fc2 as split-K partials (gate_mlp * (fc2 + bias) is added
+// to the residual by the next LN)
 int run_mlp_q8(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     const int H = d->cfg.hidden, F = d->cfg.mlp_hidden;
     int rc;
@@ -906,13 +920,9 @@ int run_mlp_q8(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
                                "fc2 quantize")))
                 return rc;
         }
-        GemmParams p = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, r[i].w->fc2_b);
-        p.epi = EPI_GATE_RES;
-        p.res = r[i].x; p.ld_res = H;
-        p.gate = mod_of(d, *r[i].w) + 5 * H;   // gate_mlp
-        p.ld_gate = mod_ld(d, *r[i].w);
-        p.rows_per_gate = r[i].S;
-        Timed tm(d, TSK_ROLE_FC2, 2.0 * p.N * H * F, q8_bytes(p.N, F, H, 8), st);
+        GemmParams p = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, nullptr);
+        q8_partials(d, p, r[i], B, d->ksplit_fc2, r[i].w->fc2_b, 5);   // gate_mlp
+        Timed tm(d, TSK_ROLE_FC2, 2.0 * p.N * H * F, q8_bytes(p.N, F, H, 4 * p.splits), st);
         if ((rc = hipcheck(launch_gemm_q8(p, st), "fc2 q8 gemm"))) return rc;
     }
     return TSK_OK;

@@ -349,7 +349,9 @@ void gemm_q8_kernel(const GemmParams p) {
 // into LDS as f32 [block][row] (weights) and [block][token] (activations).
 // Per block: one int8 MFMA 16x16x32 gives the exact integer block dot, then
 // acc += float(isum) * (d_w * d_x) -- the same expression, in the same block
-// order, as gemm_q8_kernel, so both produce the same bits.
+// order, as gemm_q8_kernel, so both produce the same bits. With p.splits > 1
+// the grid also runs over K slices, each summing its blocks in order into
+// its own f32 partial (the consumer adds the slices).
 namespace {
 typedef __attribute__((address_space(3))) void lds_void_t;
 __device__ __forceinline__ void q8_g2l16(const void *src, void *lds_base) {
@@ -367,19 +369,24 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     constexpr int BM = 16 * TM, BN = 16 * TN, TMW = TM / 2, TNW = TN / 2;
     constexpr int U = TM + TN, USZ = 2048, STG = U * USZ, LW = 2 * U / 4;
     static_assert(TM % 2 == 0 && TN % 2 == 0 && (2 * U) % 4 == 0 && R >= 2 && R <= 4, "tile shape");
-    const int KB = p.K / 32, ns = p.K / 128;
-    const int li = blockIdx.x;
-    int tm, tn;
-    if ((tiles_m & 7) == 0) {
-        // XCD x (= workgroup id mod 8) owns m tiles x, x + 8, ... and every token tile of each
+    // (m tile, K slice) units c = tm * S + sp; K slice sp covers blocks
+    // [kbase, kbase + KB) of rows KBR blocks long
+    const int S = p.splits > 1 ? p.splits : 1;
+    const int KBR = p.K / 32, KB = KBR / S, ns = KB / 4;
+    const int li = blockIdx.x, cm = tiles_m * S;
+    int c, tn;
+    if ((cm & 7) == 0) {
+        // XCD x (= workgroup id mod 8) owns units x, x + 8, ... and every token tile of each
         const int sidx = li >> 3;
-        tm = (li & 7) + 8 * (sidx / tiles_n);
+        c = (li & 7) + 8 * (sidx / tiles_n);
         tn = sidx % tiles_n;
     } else {
-        tm = li % tiles_m;
-        tn = li / tiles_m;
+        c = li % cm;
+        tn = li / cm;
     }
-    if (tm >= tiles_m || tn >= tiles_n) return;
+    if (c >= cm || tn >= tiles_n) return;
+    const int tm = c / S, sp = c - tm * S;
+    const int kb0s = KB * sp;                       // first block of this slice
     const int bm0 = tm * BM, bn0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -402,12 +409,12 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             const int e = tid + 256 * i, row = e % BM, q4 = e / BM;
-            if (q4 < nq) pw[i] = *(const u32x2 *) (p.dw + (int64_t) min(bm0 + row, p.M - 1) * KB + kb0 + 4 * q4);
+            if (q4 < nq) pw[i] = *(const u32x2 *) (p.dw + (int64_t) min(bm0 + row, p.M - 1) * KBR + kb0s + kb0 + 4 * q4);
         }
 #pragma unroll
         for (int i = 0; i < PX; ++i) {
             const int e = tid + 256 * i, tok = e % BN, q4 = e / BN;
-            if (q4 < nq) px[i] = *(const f32x4 *) (p.dx + (int64_t) min(bn0 + tok, p.N - 1) * KB + kb0 + 4 * q4);
+            if (q4 < nq) px[i] = *(const f32x4 *) (p.dx + (int64_t) min(bn0 + tok, p.N - 1) * KBR + kb0s + kb0 + 4 * q4);
         }
     };
     auto store_scales = [&](int seg) {
@@ -443,10 +450,10 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
         qlds[q] = u * USZ + h * 1024;
         if (u < TM) {
             const int rb = min((bm0 >> 4) + u, (p.M >> 4) - 1);
-            qsrc[q] = p.qw + (int64_t) (rb * 16 + 8 * h + r8) * p.K + chunk;
+            qsrc[q] = p.qw + (int64_t) (rb * 16 + 8 * h + r8) * p.K + 32 * kb0s + chunk;
         } else {
             const int n = min(bn0 + 16 * (u - TM) + 8 * h + r8, p.N - 1);
-            qsrc[q] = p.qx + (int64_t) n * p.K + chunk;
+            qsrc[q] = p.qx + (int64_t) n * p.K + 32 * kb0s + chunk;
         }
     }
     auto issue = [&](int t, int slot) {
@@ -537,7 +544,15 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     for (int i = 0; i < TMW; ++i) m0[i] = bm0 + 16 * (wm * TMW + i) + 4 * lg;
 #pragma unroll
     for (int j = 0; j < TNW; ++j) nn[j] = bn0 + 16 * (wn * TNW + j) + lr;
-    epilogue_frags<EPI, YBF16, TMW, TNW>(p, m0, nn, acc);
+    if (S > 1) {
+        // this slice's partial sums, no bias (the host allows EPI_STORE into f32 only)
+        GemmParams q = p;
+        q.y = (float *) p.y + sp * p.part_stride;
+        q.bias = nullptr;
+        epilogue_frags<EPI, YBF16, TMW, TNW>(q, m0, nn, acc);
+    } else {
+        epilogue_frags<EPI, YBF16, TMW, TNW>(p, m0, nn, acc);
+    }
 }
 
 // ------------------------------------------------------------------ activation quantization
@@ -649,7 +664,8 @@ hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
             (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
         attr = lds;
     }
-    launch_kernel(kern, dim3(tiles_m * tiles_n), dim3(256), lds, s, p, tiles_m, tiles_n);
+    launch_kernel(kern, dim3(tiles_m * tiles_n * (p.splits > 1 ? p.splits : 1)), dim3(256), lds, s, p, tiles_m,
+                  tiles_n);
     return hipGetLastError();
 }
 
@@ -675,9 +691,13 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // against the 2 x 2-wave kernel below, which stays for other shapes;
     // Tuning::q8_old forces it for comparisons).
     const Tuning &tu = tuning();
-    const bool coop = p.K % 128 == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
+    const int S = p.splits > 1 ? p.splits : 1;
+    const bool coop = p.K % (128 * S) == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 &&
                       ((uintptr_t) p.qx & 15) == 0 && ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 &&
                       !tu.q8_old;
+    // split-K partials: cooperative tiles only, f32 stores of the slices
+    if (S > 1 && (!coop || p.epi != EPI_STORE || p.y_bf16 || p.part_stride < (int64_t) p.N * p.ld_y))
+        return hipErrorInvalidValue;
     if (coop) {
         // 64 x 64 tiles with a 2-stage ring; 32 x 64 (weight rows x tokens)
         // when the 64 x 64 grid would hold fewer than two tiles per CU
@@ -687,7 +707,7 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
         // (TSK_SWEEP_VARIANTS) add 1 = 64 x 64 / 3 stages, 3 = 128 x 64,
         // 4 = 64 x 128
         const int64_t tiles64 = (int64_t) ((p.M + 63) / 64) * ((p.N + 63) / 64);
-        const int cfg = tu.q8_cfg ? tu.q8_cfg : tiles64 < 512 ? 5 : 2;
+        const int cfg = tu.q8_cfg ? tu.q8_cfg : tiles64 * S < 512 ? 5 : 2;
         switch (cfg) {
             case 2: return p.y_bf16 ? q8c_epi<4, 4, 2, true>(p, s) : q8c_epi<4, 4, 2, false>(p, s);
             case 5: return p.y_bf16 ? q8c_epi<2, 4, 2, true>(p, s) : q8c_epi<2, 4, 2, false>(p, s);

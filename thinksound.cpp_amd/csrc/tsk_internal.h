@@ -124,6 +124,11 @@ struct GemmParams {
     const float *dx;
     const int8_t *qw;        // [M][K]
     const uint16_t *dw;      // [M][K/32] fp16 bits
+    // Q8_0 cooperative tiles, split-K (splits > 1, EPI_STORE into f32 y, no
+    // bias): slice s sums k in [s K / splits, (s + 1) K / splits) into
+    // y + s * part_stride
+    int splits;
+    int64_t part_stride;
 };
 hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s);
 
