@@ -128,8 +128,8 @@ struct tsk_dit {
     // block scales dx [rows][<= F / 32]); latent rows first, text rows from
     // the capacity offset
     bool q8 = false;
-    float *qkv32 = nullptr, *o32 = nullptr, *h32 = nullptr, *dx = nullptr;
-    int8_t *qx = nullptr;
+    float *qkv32 = nullptr, *o32 = nullptr, *dx = nullptr, *dh = nullptr;
+    int8_t *qx = nullptr, *qh = nullptr;   // qh / dh: the GELU output of fc1 as Q8_0 planes (fc2's input)
 };
 
 namespace {
@@ -288,7 +288,7 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
                     d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
                     d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */,
-                    d->qkv32, d->o32, d->h32, d->qx, d->dx};
+                    d->qkv32, d->o32, d->qh, d->dh, d->qx, d->dx};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
     delete d;
@@ -371,7 +371,8 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     if (d->q8 &&
         ((rc = alloc((void **) &d->qkv32, sizeof(float) * rows * 3 * H)) ||
          (rc = alloc((void **) &d->o32, sizeof(float) * rows * H)) ||
-         (rc = alloc((void **) &d->h32, sizeof(float) * rows * F)) ||
+         (rc = alloc((void **) &d->qh, (size_t) rows * F)) ||
+         (rc = alloc((void **) &d->dh, sizeof(float) * rows * (F / 32))) ||
          (rc = alloc((void **) &d->qx, (size_t) rows * F)) ||
          (rc = alloc((void **) &d->dx, sizeof(float) * rows * (F / 32))))) {
         tsk_dit_destroy(d);
@@ -817,7 +818,7 @@ GemmParams q8_problem(const tsk_dit *d, const Q8W &w, const StreamRun &r, int B,
     return p;
 }
 
-double q8_bytes(int N, int K, int M, int out_bytes) {
+double q8_bytes(int N, int K, int M, double out_bytes) {
     return (double) M * K * (1.0 + 2.0 / 32) + (double) N * K * (1.0 + 4.0 / 32) + (double) N * M * out_bytes;
 }
 
@@ -895,32 +896,27 @@ int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
     return TSK_OK;
 }
 
-// fc1 (+ GELU, f32 out) of every stream, then per stream the quantize of the
-// GELU output and fc2 as split-K partials (gate_mlp * (fc2 + bias) is added
-// to the residual by the next LN)
+// fc1 of every stream with GELU and the Q8_0 conversion of its output in the
+// epilogue (into qh / dh: fc1 still reads qx), then fc2 as split-K partials
+// (gate_mlp * (fc2 + bias) is added to the residual by the next LN)
 int run_mlp_q8(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     const int H = d->cfg.hidden, F = d->cfg.mlp_hidden;
     int rc;
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
         GemmParams p = q8_problem(d, r[i].w->fc1_q, r[i], B, H, F, r[i].w->fc1_b);
-        p.y = d->h32 + r[i].row_off * F;
+        p.y = d->qh + r[i].row_off * F;
         p.ld_y = F;
-        p.epi = EPI_GELU;
-        Timed tm(d, TSK_ROLE_FC1, 2.0 * p.N * H * F, q8_bytes(p.N, H, F, 4), st);
+        p.yd = d->dh + r[i].row_off * (F / 32);
+        p.epi = EPI_GELU_Q8;
+        Timed tm(d, TSK_ROLE_FC1, 2.0 * p.N * H * F, q8_bytes(p.N, H, F, 1.125), st);
         if ((rc = hipcheck(launch_gemm_q8(p, st), "fc1 q8 gemm"))) return rc;
     }
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
-        const int rows = B * r[i].S;
-        {
-            Timed tm(d, TSK_ROLE_OTHER, 3.0 * rows * F, 5.125 * rows * F, st);
-            if ((rc = hipcheck(launch_quantize_rows_q8(d->h32 + r[i].row_off * F, 1, F, rows, F, d->qx + r[i].row_off * F,
-                                                       d->dx + r[i].row_off * (F / 32), st),
-                               "fc2 quantize")))
-                return rc;
-        }
         GemmParams p = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, nullptr);
+        p.qx = d->qh + r[i].row_off * F;
+        p.dx = d->dh + r[i].row_off * (F / 32);
         q8_partials(d, p, r[i], B, d->ksplit_fc2, r[i].w->fc2_b, 5);   // gate_mlp
         Timed tm(d, TSK_ROLE_FC2, 2.0 * p.N * H * F, q8_bytes(p.N, F, H, 4 * p.splits), st);
         if ((rc = hipcheck(launch_gemm_q8(p, st), "fc2 q8 gemm"))) return rc;

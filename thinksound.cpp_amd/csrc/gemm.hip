@@ -544,7 +544,65 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     for (int i = 0; i < TMW; ++i) m0[i] = bm0 + 16 * (wm * TMW + i) + 4 * lg;
 #pragma unroll
     for (int j = 0; j < TNW; ++j) nn[j] = bn0 + 16 * (wn * TNW + j) + lr;
-    if (S > 1) {
+    if constexpr (EPI == EPI_GELU_Q8) {
+        // GELU, then ggml's Q8_0 conversion of every token's 32-feature block
+        // (the arithmetic of quantize_rows_q8_kernel: the same bits as storing
+        // the f32 GELU rows and quantizing them). A block is this wave's 32
+        // rows (TMW = 2), or 16 rows in each of the waves wm = 0, 1 (TMW = 1:
+        // partial maxima exchanged through LDS). Lanes lg = 0..3 hold rows
+        // 4 lg .. 4 lg + 3 of a 16-row fragment for token lr.
+        float v[TMW][TNW][4], am[TNW];
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) am[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TMW; ++i) {
+            float bv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias && m0[i] < p.M)
+                for (int r = 0; r < 4; ++r) bv[r] = p.bias[m0[i] + r];
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    v[i][j][r] = gelu_tanh_f(acc[i][j][r] + bv[r]);
+                    am[j] = fmaxf(am[j], fabsf(v[i][j][r]));
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+            am[j] = fmaxf(am[j], __shfl_xor(am[j], 16));
+            am[j] = fmaxf(am[j], __shfl_xor(am[j], 32));
+        }
+        if constexpr (TMW == 1) {
+            float *xa = (float *) lds;
+            __syncthreads();                     // every wave is done with the ring
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+                if (lg == 0) xa[((wn * TNW + j) * 16 + lr) * 2 + wm] = am[j];
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                const int e = ((wn * TNW + j) * 16 + lr) * 2;
+                am[j] = fmaxf(xa[e], xa[e + 1]);
+            }
+        }
+        const int kb = (bm0 >> 5) + (TMW == 2 ? wm : 0);
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) {
+            const int n = nn[j];
+            if (n >= p.N || bm0 >= p.M) continue;
+            const float d = am[j] / 127.0f;
+            const float id = am[j] != 0.0f ? 127.0f / am[j] : 0.0f;
+            if (lg == 0 && (TMW == 2 || wm == 0)) p.yd[(int64_t) n * (p.M / 32) + kb] = f16_bits_to_f32(f32_to_f16_bits(d));
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) {
+                int8_t q[4];
+                for (int r = 0; r < 4; ++r) q[r] = (int8_t) __builtin_rintf(v[i][j][r] * id);
+                uint32_t w4;
+                __builtin_memcpy(&w4, q, 4);
+                *(uint32_t *) ((int8_t *) p.y + (int64_t) n * p.ld_y + m0[i]) = w4;
+            }
+        }
+    } else if (S > 1) {
         // this slice's partial sums, no bias (the host allows EPI_STORE into f32 only)
         GemmParams q = p;
         q.y = (float *) p.y + sp * p.part_stride;
@@ -677,6 +735,7 @@ hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
         case EPI_GEGLU:
             if (p.M % 4 || p.y_bf16) return hipErrorInvalidValue;
             return q8c_launch<TM, TN, R, EPI_GEGLU, false>(p, s);
+        case EPI_GELU_Q8: return q8c_launch<TM, TN, R, EPI_GELU_Q8, false>(p, s);
         default: return q8c_launch<TM, TN, R, EPI_STORE, YBF16>(p, s);
     }
 }
@@ -697,6 +756,10 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
                       !tu.q8_old;
     // split-K partials: cooperative tiles only, f32 stores of the slices
     if (S > 1 && (!coop || p.epi != EPI_STORE || p.y_bf16 || p.part_stride < (int64_t) p.N * p.ld_y))
+        return hipErrorInvalidValue;
+    // GELU into Q8_0 planes: cooperative tiles only, whole 32-feature blocks
+    // in every tile
+    if (p.epi == EPI_GELU_Q8 && (!coop || S > 1 || p.y_bf16 || p.M % 64 || !p.yd || p.ld_y < p.M || p.ld_y % 4))
         return hipErrorInvalidValue;
     if (coop) {
         // 64 x 64 tiles with a 2-stage ring; 32 x 64 (weight rows x tokens)

@@ -99,7 +99,11 @@ enum GemmEpi : int {
     EPI_STORE = 0,      // Y = acc (+bias)
     EPI_GELU = 1,       // Y = gelu_tanh(acc + bias)
     EPI_GATE_RES = 2,   // R[n, m] += gate[n / rows_per_gate, m] * (acc + bias); Y unused
-    EPI_GEGLU = 3       // rows interleaved (a_j, b_j): Y[n, j] = gelu_tanh(a_j) * b_j, M even (Q8_0 only)
+    EPI_GEGLU = 3,      // rows interleaved (a_j, b_j): Y[n, j] = gelu_tanh(a_j) * b_j, M even (Q8_0 only)
+    // gelu_tanh(acc + bias) converted to Q8_0 planes for the next Q8_0 GEMM:
+    // Y int8 [N][ld_y], yd f32 block scales [N][M / 32] (Q8_0 cooperative
+    // tiles only, M % 64 == 0)
+    EPI_GELU_Q8 = 4
 };
 
 struct GemmParams {
@@ -129,6 +133,7 @@ struct GemmParams {
     // y + s * part_stride
     int splits;
     int64_t part_stride;
+    float *yd;               // EPI_GELU_Q8: block scales of the output planes
 };
 hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s);
 
