@@ -971,9 +971,10 @@ hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s) {
     if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
     for (int i = 0; i < g.nprob; ++i) {
         const GemmProblem &p = g.p[i];
-        if (!p.w_tiled || p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits < 1 ||
-            p.splits > p.K / 32)
+        if (p.M < 16 || p.M % 16 || p.N < 1 || p.K < 32 || p.K % 32 || p.splits < 1 || p.splits > p.K / 32)
             return hipErrorInvalidValue;
+        // row-major weights (the reference graph's qkv) as in launch_gemm_coop
+        if (!p.w_tiled && (p.ld_w % 8 || ((uintptr_t) p.w & 15) || p.w3)) return hipErrorInvalidValue;
         if (epi != EPI_PARTIAL && p.splits != 1) return hipErrorInvalidValue;
         if (epi == EPI_QKV && (p.M % 192 || p.seq < 1 || (p.rope && !p.rope_cs))) return hipErrorInvalidValue;
     }

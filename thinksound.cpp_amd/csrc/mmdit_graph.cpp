@@ -20,6 +20,7 @@
 // kernel per stream), im2col inside the convolution GEMMs.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -77,7 +78,7 @@ struct tsk_mmdit {
     // block's gate_mlp in [(i - 1) & 1] is still owed to the residual
     float *mod_l[2] = {}, *mod_c[2] = {}, *mod_t[2] = {};
     uint16_t *xn = nullptr, *hid = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr;
-    float *part = nullptr, *qkv32 = nullptr, *tmp32 = nullptr, *rope_l = nullptr, *rope_c = nullptr;
+    float *part = nullptr, *tmp32 = nullptr, *rope_l = nullptr, *rope_c = nullptr;
     uint16_t *in16 = nullptr;             // bf16 copies of the staged inputs
     float *in32 = nullptr;                // f32 staging of the inputs
     uint16_t *act16 = nullptr;            // bf16(silu(.)) rows of the input projections
@@ -366,24 +367,36 @@ int run_mods(tsk_mmdit *m, Stream *r, int ns, int B, int T, hipStream_t s) {
     return TSK_OK;
 }
 
-// qkv -> split / RMSNorm / RoPE / F16 into the joint attention operands
+// qkv with the split / RMSNorm / RoPE / F16 scatter into the joint attention
+// operands in the GEMM epilogue (EPI_QKV); up to two streams per launch
 int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
     const tsk_mmdit_config &c = m->cfg;
     const int H = c.hidden;
-    for (int i = 0; i < ns; ++i) {
-        int rc = lin(r[i].w->qkv, r[i].xn, H, B * r[i].S, m->qkv32, 3 * H, false, s);
+    for (int i0 = 0; i0 < ns; i0 += 2) {
+        GemmGroup g;
+        memset(&g, 0, sizeof(g));
+        g.nprob = std::min(2, ns - i0);
+        int rows0 = 0;
+        for (int k = 0; k < g.nprob; ++k) {
+            const Stream &st = r[i0 + k];
+            const Lin &L = st.w->qkv;
+            GemmProblem &q = g.p[k];
+            q.x = st.xn; q.ld_x = H;
+            q.w = L.w; q.ld_w = L.K;
+            q.bias = L.b;
+            q.M = L.M; q.N = B * st.S; q.K = L.K; q.splits = 1;
+            q.qn_w = st.w->qn; q.kn_w = st.w->kn;
+            q.q = m->q; q.k = m->k; q.vt = m->vt; q.ldv = m->ldv;
+            q.seq = st.S; q.Ntot = Ntot; q.tok_off = st.tok_off;
+            q.rope = st.rope_cs != nullptr;
+            q.rope_cs = st.rope_cs;
+            q.eps = 1e-6f;                                   // rmsnorm_w EPS, src/mmdit.cpp:10
+            q.q_scale = 1.4426950408889634f / 8.0f;          // 1/sqrt(64) * log2(e): the attention's softmax scale
+            rows0 = std::max(rows0, q.N);
+        }
+        // 128 x 64 tiles from 1100 activation rows, 64 x 64 below (the DiT's qkv rule)
+        const int rc = hipcheck(launch_gemm_ks(g, EPI_QKV, rows0 >= 1100 ? 29 : 30, s), "mmdit qkv gemm");
         if (rc) return rc;
-        QkvScatter q;
-        memset(&q, 0, sizeof(q));
-        q.qkv = m->qkv32; q.ld = 3 * H;
-        q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
-        q.rope_cs = r[i].rope_cs;
-        q.q = m->q; q.k = m->k; q.vt = m->vt; q.ldv = m->ldv;
-        q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope_cs != nullptr;
-        q.nh = c.n_head; q.rows = B * r[i].S;
-        q.eps = 1e-6f;                                   // rmsnorm_w EPS, src/mmdit.cpp:10
-        q.q_scale = 1.4426950408889634f / 8.0f;          // 1/sqrt(64) * log2(e): the attention's softmax scale
-        if ((rc = hipcheck(launch_qkv_scatter(q, s), "mmdit qkv scatter"))) return rc;
     }
     return TSK_OK;
 }
@@ -484,7 +497,7 @@ extern "C" void tsk_mmdit_destroy(tsk_mmdit *m) {
     (void) hipDeviceSynchronize();
     void *bufs[] = {m->blob, m->lat, m->clip, m->txt, m->sync, m->ext, m->silu_ext, m->silu_gc, m->vec, m->vec16,
                     m->mod_l[0], m->mod_l[1], m->mod_c[0], m->mod_c[1], m->mod_t[0], m->mod_t[1], m->xn, m->hid,
-                    m->o, m->q, m->k, m->vt, m->part, m->qkv32, m->tmp32, m->rope_l, m->rope_c, m->in16, m->in32,
+                    m->o, m->q, m->k, m->vt, m->part, m->tmp32, m->rope_l, m->rope_c, m->in16, m->in32,
                     m->act16, m->freq, m->temb};
     for (void *b : bufs)
         if (b) (void) hipFree(b);
@@ -584,7 +597,6 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         (rc = alloc((void **) &m->k, 2 * (size_t) B * m->Nmax * H)) ||
         (rc = alloc((void **) &m->vt, 2 * (size_t) B * H * m->ldv)) ||
         (rc = alloc((void **) &m->part, sizeof(float) * GRAPH_KSPLIT_MAX * rows3 * H)) ||
-        (rc = alloc((void **) &m->qkv32, sizeof(float) * R * 3 * H)) ||
         (rc = alloc((void **) &m->tmp32, sizeof(float) * R * std::max(H, c.latent_dim))) ||
         (rc = alloc((void **) &m->rope_l, sizeof(float) * T * 64)) ||
         (rc = alloc((void **) &m->rope_c, sizeof(float) * C * 64)) ||

@@ -192,8 +192,9 @@ struct GemmGroup {
 };
 hipError_t launch_gemm_group(GemmGroup &g, int flags, int epi, hipStream_t s);
 // The DiT block projections (gemm_ks.hip): bf16 activations, MFMA-tiled
-// weights (w_tiled, M % 16 == 0, K % 32 == 0). cfg 0 picks the tile shape;
-// 1..5 force one (128x64 / 64x64 / 64x128 / 128x64 2-stage / 64x64 4-stage).
+// weights (w_tiled) or row-major ones (ld_w % 8 == 0, 16-byte aligned),
+// M % 16 == 0, K % 32 == 0. cfg picks the tile shape: 0 / 30 64 x 64, 22
+// 64 x 64 of 32-wide stages, 28 / 29 128 x 64 (3 / 2 stages).
 hipError_t launch_gemm_ks(GemmGroup &g, int epi, int cfg, hipStream_t s);
 int gemm_ks_tiles(const GemmGroup &g, int bm, int bn);
 // output rows per tile (BM) of a launch_gemm_ks configuration
