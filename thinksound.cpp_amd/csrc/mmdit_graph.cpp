@@ -239,12 +239,10 @@ int lin(const Lin &L, const uint16_t *x, int64_t ld_x, int N, void *y, int64_t l
 
 // conv_cl (stride 1, padding pad): x bf16 rows [B][IW][IC] with row stride
 // ld_x and batch stride xb (elements), y rows [B * IW][OC] (ld_y)
-int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, void *y, int64_t ld_y,
-         bool y_bf16, hipStream_t s, bool no_bias = false, int splits = 1) {
-    GemmGroup g;
-    memset(&g, 0, sizeof(g));
-    g.nprob = 1;
-    GemmProblem &q = g.p[0];
+GemmProblem conv_problem(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, void *y,
+                         int64_t ld_y, bool no_bias, int splits) {
+    GemmProblem q;
+    memset(&q, 0, sizeof(q));
     q.x = x; q.ld_x = ld_x; q.x_group_stride = xb;
     q.w = C.w; q.ld_w = (int64_t) C.KW * C.IC;
     q.bias = no_bias ? nullptr : C.b;
@@ -252,6 +250,15 @@ int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int
     const int OW = IW + 2 * pad - (C.KW - 1);
     q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = splits;
     q.conv_ic = C.IC; q.conv_iw = IW; q.conv_ow = OW; q.conv_s = 1; q.conv_p = pad; q.conv_d = 1;
+    return q;
+}
+
+int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, void *y, int64_t ld_y,
+         bool y_bf16, hipStream_t s, bool no_bias = false, int splits = 1) {
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    g.p[0] = conv_problem(C, x, ld_x, xb, IW, B, pad, y, ld_y, no_bias, splits);
     const int epi = splits > 1 ? EPI_PARTIAL : y_bf16 ? EPI_STORE_BF16 : EPI_STORE_F32;
     return hipcheck(launch_gemm_coop(g, epi, s), "mmdit conv");
 }
@@ -429,18 +436,24 @@ int run_attention(tsk_mmdit *m, const Stream *r, int ns, int B, int Ntot, hipStr
 }
 
 // post_attn (src/mmdit.cpp:226-235): linear1 on this stream's attention rows
-// (its residual update is owed to the next LN), LN, ffn (owed to the next LN)
+// (its residual update is owed to the next LN), LN, ffn (owed to the next LN).
+// The k3 convolutions of the latent and clip streams share their launches
+// (two problems per GEMM); their partial sums and convMLP hidden states sit
+// in separate slices.
 int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
-    const int H = m->cfg.hidden;
+    const int H = m->cfg.hidden, F = m->cfg.mlp_hidden;
+    const int64_t ob = (int64_t) m->Nmax * H;      // batch stride of the attention output rows
     int rc;
+    GemmGroup gl;
+    memset(&gl, 0, sizeof(gl));
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
         const Block &b = *r[i].w;
         const uint16_t *orows = m->o + (size_t) r[i].tok_off * H;
-        const int64_t ob = (int64_t) m->Nmax * H;      // batch stride of the attention output rows
-        r[i].pend_split = b.conv ? conv_splits(b.l1c, B * r[i].S) : 1;
-        if (b.conv) rc = conv(b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, true, r[i].pend_split);
-        else {
+        if (b.conv) {
+            r[i].pend_split = conv_splits(b.l1c, B * r[i].S);
+            gl.p[gl.nprob++] = conv_problem(b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, true, r[i].pend_split);
+        } else {
             // text: linear1 rows grouped by batch item
             GemmGroup g;
             memset(&g, 0, sizeof(g));
@@ -450,33 +463,52 @@ int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
             q.w = b.l1.w; q.ld_w = b.l1.K;
             q.y = r[i].part; q.ld_y = H;
             q.M = H; q.N = B * r[i].S; q.K = H; q.splits = 1;
-            rc = hipcheck(launch_gemm_coop(g, EPI_STORE_F32, s), "mmdit text linear1");
+            r[i].pend_split = 1;
+            if ((rc = hipcheck(launch_gemm_coop(g, EPI_STORE_F32, s), "mmdit text linear1"))) return rc;
         }
-        if (rc) return rc;
         r[i].pending = true;
         r[i].pend_bias = b.conv ? b.l1c.b : b.l1.b;
         r[i].pend_gate = r[i].mod + 2 * H;             // gate_msa
         r[i].pend_ld = 6 * H;
     }
+    // K slices (one when splits = 1) of both conv streams, no bias
+    if (gl.nprob && (rc = hipcheck(launch_gemm_coop(gl, EPI_PARTIAL, s), "mmdit linear1 conv"))) return rc;
     Stream live[3];
     int nl = 0;
     for (int i = 0; i < ns; ++i)
         if (!r[i].w->pre_only) live[nl++] = r[i];
     if (!nl) return TSK_OK;
     if ((rc = run_ln(m, live, nl, B, 1, s))) return rc;
+    GemmGroup g13, g2;
+    memset(&g13, 0, sizeof(g13));
+    memset(&g2, 0, sizeof(g2));
+    int64_t hoff = 0;                                  // hidden-state slice of the next conv stream
     for (int i = 0, j = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
         r[i].pending = live[j++].pending;
         const Block &b = *r[i].w;
-        r[i].pend_split = b.conv ? conv_splits(b.w2c, B * r[i].S) : 1;
-        rc = b.conv ? conv_mlp(m, b.w1c, b.w3c, b.w2c, r[i].xn, H, (int64_t) r[i].S * H, r[i].S, B, r[i].part, H, s,
-                               r[i].pend_split)
-                    : lin_mlp(m, b.w1, b.w3, b.w2, r[i].xn, H, B * r[i].S, r[i].part, H, s);
-        if (rc) return rc;
+        if (b.conv) {
+            uint16_t *hid = m->hid + hoff;
+            hoff += (int64_t) B * r[i].S * F;
+            GemmProblem &q = g13.p[g13.nprob++];
+            q = conv_problem(b.w1c, r[i].xn, H, (int64_t) r[i].S * H, r[i].S, B, 1, hid, F, true, 1);
+            q.w3 = b.w3c.w;
+            r[i].pend_split = conv_splits(b.w2c, B * r[i].S);
+            g2.p[g2.nprob++] = conv_problem(b.w2c, hid, F, (int64_t) r[i].S * F, r[i].S, B, 1, r[i].part, H, true,
+                                            r[i].pend_split);
+        } else {
+            r[i].pend_split = 1;
+            if ((rc = lin_mlp(m, b.w1, b.w3, b.w2, r[i].xn, H, B * r[i].S, r[i].part, H, s))) return rc;
+        }
         r[i].pending = true;
         r[i].pend_bias = nullptr;
         r[i].pend_gate = r[i].mod + 5 * H;             // gate_mlp
         r[i].pend_ld = 6 * H;
+    }
+    if (g13.nprob) {
+        // convmlp (src/mmdit.cpp:39-52): w2(silu(w1 x) * w3 x), the hidden state bf16
+        if ((rc = hipcheck(launch_gemm_coop(g13, EPI_SWIGLU_BF16, s), "mmdit convmlp w1/w3"))) return rc;
+        if ((rc = hipcheck(launch_gemm_coop(g2, EPI_PARTIAL, s), "mmdit convmlp w2"))) return rc;
     }
     return TSK_OK;
 }
@@ -591,7 +623,7 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         (rc = alloc((void **) &m->mod_t[0], sizeof(float) * B * 6 * H)) ||
         (rc = alloc((void **) &m->mod_t[1], sizeof(float) * B * 6 * H)) ||
         (rc = alloc((void **) &m->xn, 2 * (size_t) rows3 * H)) ||
-        (rc = alloc((void **) &m->hid, 2 * (size_t) R * F)) ||
+        (rc = alloc((void **) &m->hid, 2 * (size_t) std::max(R, (int64_t) B * (T + C)) * F)) ||
         (rc = alloc((void **) &m->o, 2 * (size_t) B * m->Nmax * H)) ||
         (rc = alloc((void **) &m->q, 2 * (size_t) B * m->Nmax * H)) ||
         (rc = alloc((void **) &m->k, 2 * (size_t) B * m->Nmax * H)) ||
