@@ -58,6 +58,7 @@ struct Block {
     Conv l1c, w1c, w3c, w2c;        // ... or k3 convolutions (latent / clip)
     const float *qn, *kn;
     int qn_idx, kn_idx;
+    int64_t mod_col;         // first column of this block's adaLN outputs in its set
 };
 
 }  // namespace
@@ -74,9 +75,13 @@ struct tsk_mmdit {
     uint16_t *silu_ext = nullptr, *silu_gc = nullptr;
     float *vec = nullptr;                 // [8][B][H]: te0, te, text_fc, clip_mean, clip_fc, gsum, gc, spare
     uint16_t *vec16 = nullptr;            // [4][B][max(H, clip_dim)] bf16 vectors
-    // adaLN outputs, two per stream: block i writes [i & 1] while the previous
-    // block's gate_mlp in [(i - 1) & 1] is still owed to the residual
-    float *mod_l[2] = {}, *mod_c[2] = {}, *mod_t[2] = {};
+    // adaLN outputs of every block in one pass per forward: the per-token set
+    // (latent blocks, then the final layer) [B][T][Ml] and the per-item set
+    // (clip blocks, then text blocks) [B][Mg]; Block::mod_col is a block's
+    // first column
+    float *mods_lat = nullptr, *mods_gc = nullptr;
+    Lin ada_lat{}, ada_gc{};              // the blocks' adaLN weights / biases back to back in the blob
+    int64_t fin_mod_col = 0;
     uint16_t *xn = nullptr, *hid = nullptr, *o = nullptr, *q = nullptr, *k = nullptr, *vt = nullptr;
     float *part = nullptr, *tmp32 = nullptr, *rope_l = nullptr, *rope_c = nullptr;
     uint16_t *in16 = nullptr;             // bf16 copies of the staged inputs
@@ -316,7 +321,8 @@ struct Stream {
     float *x;              // f32 residual rows [B][S][H]
     int S, tok_off;
     const float *rope_cs;  // nullptr: no RoPE (text)
-    float *mod;            // [B * rows_mod][nmod * H] adaLN output
+    float *mod;            // this block's adaLN outputs: [B * rows_mod] rows of stride ld_mod
+    int64_t ld_mod;
     int per_token;         // modulation per token (latent: extended_c) or per batch item
     uint16_t *xn;          // bf16 LN output rows
     float *part;           // f32 output of the previous projection (residual update owed)
@@ -331,7 +337,7 @@ LnStream ln_of(const tsk_mmdit *m, Stream &r, int B, int which) {
     LnStream l;
     memset(&l, 0, sizeof(l));
     l.x = r.x; l.ld_x = H;
-    const int64_t ldm = (int64_t) r.w->nmod * H;
+    const int64_t ldm = r.ld_mod;
     if (r.pending) {
         l.part = r.part; l.nsplit = r.pend_split > 1 ? r.pend_split : 1; l.part_stride = (int64_t) B * r.S * H;
         l.bias = r.pend_bias; l.gate = r.pend_gate; l.ld_gate = r.pend_ld;
@@ -362,17 +368,6 @@ int run_ln(tsk_mmdit *m, Stream *r, int ns, int B, int which, hipStream_t s) {
     return TSK_OK;
 }
 
-// adaLN of every stream: lin(adaLN, silu(cond)) (src/mmdit.cpp:209)
-int run_mods(tsk_mmdit *m, Stream *r, int ns, int B, int T, hipStream_t s) {
-    const int H = m->cfg.hidden;
-    for (int i = 0; i < ns; ++i) {
-        const Block &b = *r[i].w;
-        int rc = r[i].per_token ? lin(b.ada, m->silu_ext, H, B * T, r[i].mod, (int64_t) b.nmod * H, false, s)
-                                : lin(b.ada, m->silu_gc, H, B, r[i].mod, (int64_t) b.nmod * H, false, s);
-        if (rc) return rc;
-    }
-    return TSK_OK;
-}
 
 // qkv with the split / RMSNorm / RoPE / F16 scatter into the joint attention
 // operands in the GEMM epilogue (EPI_QKV); up to two streams per launch
@@ -469,7 +464,7 @@ int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         r[i].pending = true;
         r[i].pend_bias = b.conv ? b.l1c.b : b.l1.b;
         r[i].pend_gate = r[i].mod + 2 * H;             // gate_msa
-        r[i].pend_ld = 6 * H;
+        r[i].pend_ld = r[i].ld_mod;
     }
     // K slices (one when splits = 1) of both conv streams, no bias
     if (gl.nprob && (rc = hipcheck(launch_gemm_coop(gl, EPI_PARTIAL, s), "mmdit linear1 conv"))) return rc;
@@ -503,7 +498,7 @@ int run_post(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         r[i].pending = true;
         r[i].pend_bias = nullptr;
         r[i].pend_gate = r[i].mod + 5 * H;             // gate_mlp
-        r[i].pend_ld = 6 * H;
+        r[i].pend_ld = r[i].ld_mod;
     }
     if (g13.nprob) {
         // convmlp (src/mmdit.cpp:39-52): w2(silu(w1 x) * w3 x), the hidden state bf16
@@ -528,7 +523,7 @@ extern "C" void tsk_mmdit_destroy(tsk_mmdit *m) {
     if (!m) return;
     (void) hipDeviceSynchronize();
     void *bufs[] = {m->blob, m->lat, m->clip, m->txt, m->sync, m->ext, m->silu_ext, m->silu_gc, m->vec, m->vec16,
-                    m->mod_l[0], m->mod_l[1], m->mod_c[0], m->mod_c[1], m->mod_t[0], m->mod_t[1], m->xn, m->hid,
+                    m->mods_lat, m->mods_gc, m->xn, m->hid,
                     m->o, m->q, m->k, m->vt, m->part, m->tmp32, m->rope_l, m->rope_c, m->in16, m->in32,
                     m->act16, m->freq, m->temb};
     for (void *b : bufs)
@@ -585,13 +580,35 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
     add_conv(m, "final_layer.conv", 7, H, c.latent_dim, true);
     addw(m, "empty_string_feat", c.clip_dim, c.text_seq, 1, K_VEC);
     addw(m, "empty_t5_feat", c.t5_dim, c.text_seq, 1, K_VEC);
+    // blob placement: the adaLN weights, then biases, of the latent blocks and
+    // the final layer back to back (rows of one [Ml][H] matrix, 256-byte
+    // multiples: no gaps), the same for the clip and text blocks, then every
+    // other tensor in inventory order; each set's adaLN is one GEMM per forward
+    std::vector<std::string> ada_l, ada_g;
+    for (int i = 0; i < nj; ++i) ada_l.push_back("joint_blocks." + std::to_string(i) + ".latent_block");
+    for (int i = 0; i < c.fused_depth; ++i) ada_l.push_back("fused_blocks." + std::to_string(i));
+    ada_l.push_back("final_layer");
+    for (int i = 0; i < nj; ++i) ada_g.push_back("joint_blocks." + std::to_string(i) + ".clip_block");
+    for (int i = 0; i < nj; ++i) ada_g.push_back("joint_blocks." + std::to_string(i) + ".text_block");
     size_t off = 0;
-    for (auto &x : m->w) {
+    std::vector<bool> placed(m->w.size(), false);
+    auto place = [&](const std::string &name) {
+        const int i = m->idx.at(name);
+        MW &x = m->w[i];
         x.offset = off;
         const size_t n = (size_t) (x.ne[0] * x.ne[1] * x.ne[2]);
         off += (n * (x.kind == K_VEC || x.f32 ? 4 : 2) + 255) & ~(size_t) 255;
+        placed[i] = true;
+    };
+    for (const auto *set : {&ada_l, &ada_g}) {
+        for (const auto &p : *set) place(p + ".adaLN_modulation.1.weight");
+        for (const auto &p : *set) place(p + ".adaLN_modulation.1.bias");
     }
+    for (size_t i = 0; i < m->w.size(); ++i)
+        if (!placed[i]) place(m->w[i].name);
     const int B = c.max_batch, T = c.max_latent, C = c.max_clip, S = c.max_sync;
+    const int64_t Ml = (int64_t) (nj + c.fused_depth) * 6 * H + 2 * H;          // latent blocks + final layer
+    const int64_t Mg = (int64_t) 2 * (nj - 1) * 6 * H + 2 * 2 * H;             // clip + text (last pre_only)
     m->Nmax = T + C + X;
     m->ldv = (m->Nmax + 63) / 64 * 64;
     const int64_t R = (int64_t) B * std::max(std::max(T, C), std::max(S, X));   // rows of the longest stream
@@ -616,12 +633,8 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         (rc = alloc((void **) &m->silu_gc, 2 * (size_t) B * H)) ||
         (rc = alloc((void **) &m->vec, sizeof(float) * 8 * B * H)) ||
         (rc = alloc((void **) &m->vec16, 2 * (size_t) 4 * B * Wmax)) ||
-        (rc = alloc((void **) &m->mod_l[0], sizeof(float) * B * T * 6 * H)) ||
-        (rc = alloc((void **) &m->mod_l[1], sizeof(float) * B * T * 6 * H)) ||
-        (rc = alloc((void **) &m->mod_c[0], sizeof(float) * B * 6 * H)) ||
-        (rc = alloc((void **) &m->mod_c[1], sizeof(float) * B * 6 * H)) ||
-        (rc = alloc((void **) &m->mod_t[0], sizeof(float) * B * 6 * H)) ||
-        (rc = alloc((void **) &m->mod_t[1], sizeof(float) * B * 6 * H)) ||
+        (rc = alloc((void **) &m->mods_lat, sizeof(float) * B * T * Ml)) ||
+        (rc = alloc((void **) &m->mods_gc, sizeof(float) * B * Mg)) ||
         (rc = alloc((void **) &m->xn, 2 * (size_t) rows3 * H)) ||
         (rc = alloc((void **) &m->hid, 2 * (size_t) std::max(R, (int64_t) B * (T + C)) * F)) ||
         (rc = alloc((void **) &m->o, 2 * (size_t) B * m->Nmax * H)) ||
@@ -660,6 +673,27 @@ extern "C" int tsk_mmdit_create(const tsk_mmdit_config *cfg, tsk_mmdit **out) {
         m->jt.push_back(block_of(m, p + ".text_block", i == nj - 1, false));
     }
     for (int i = 0; i < c.fused_depth; ++i) m->fb.push_back(block_of(m, "fused_blocks." + std::to_string(i), false, true));
+    // the two adaLN sets: columns in blob order (latent blocks, fused blocks,
+    // final layer; clip blocks, text blocks)
+    int64_t col = 0;
+    for (auto &b : m->jl) { b.mod_col = col; col += (int64_t) b.nmod * H; }
+    for (auto &b : m->fb) { b.mod_col = col; col += (int64_t) b.nmod * H; }
+    m->fin_mod_col = col;
+    col = 0;
+    for (auto &b : m->jc) { b.mod_col = col; col += (int64_t) b.nmod * H; }
+    for (auto &b : m->jt) { b.mod_col = col; col += (int64_t) b.nmod * H; }
+    m->ada_lat = Lin{m->jl[0].ada.w, m->jl[0].ada.b, H, (int) Ml, nullptr};
+    m->ada_gc = Lin{m->jc[0].ada.w, m->jc[0].ada.b, H, (int) Mg, nullptr};
+    const Lin fin = lin_of(m, "final_layer.adaLN_modulation.1", true);
+    bool packed = fin.w == m->ada_lat.w + m->fin_mod_col * H && fin.b == m->ada_lat.b + m->fin_mod_col;
+    for (const auto *v : {&m->jl, &m->fb})
+        for (const Block &b : *v) packed = packed && b.ada.w == m->ada_lat.w + b.mod_col * H && b.ada.b == m->ada_lat.b + b.mod_col;
+    for (const auto *v : {&m->jc, &m->jt})
+        for (const Block &b : *v) packed = packed && b.ada.w == m->ada_gc.w + b.mod_col * H && b.ada.b == m->ada_gc.b + b.mod_col;
+    if (!packed) {
+        tsk_mmdit_destroy(m);
+        return fail(TSK_ERR_UNSUPPORTED, "adaLN weights are not packed");
+    }
     m->h_pos_emb.assign((size_t) c.sync_dim * 8, 0.0f);
     m->h_empty_str.assign((size_t) c.clip_dim * c.text_seq, 0.0f);
     m->h_empty_t5.assign((size_t) c.t5_dim * c.text_seq, 0.0f);
@@ -889,6 +923,13 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
     // silu(extended_c) and silu(global_c), the adaLN inputs (:209)
     if ((rc = hipcheck(launch_silu_bf16(m->ext, m->silu_ext, (int64_t) B * T * H, st), "silu"))) return rc;
     if ((rc = hipcheck(launch_silu_bf16(gc, m->silu_gc, (int64_t) B * H, st), "silu"))) return rc;
+    // every block's adaLN (lin(adaLN, silu(c)), :209) in two GEMMs: per token
+    // from extended_c (latent blocks, final layer), per item from global_c
+    // (clip and text blocks); each output is the same dot product a per-block
+    // launch computes
+    const int64_t Ml = m->ada_lat.M, Mg = m->ada_gc.M;
+    if ((rc = lin(m->ada_lat, m->silu_ext, H, B * T, m->mods_lat, Ml, false, st))) return rc;
+    if ((rc = lin(m->ada_gc, m->silu_gc, H, B, m->mods_gc, Mg, false, st))) return rc;
     // clip RoPE: positions 0 .. clip_S - 1, freq_scale T / clip_S (:237, :318)
     if ((rc = hipcheck(launch_rope_table(m->rope_c, clip_S, 64, powf(c.rope_theta, -2.0f / 64.0f),
                                          (float) T / (float) clip_S, st),
@@ -926,16 +967,14 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
         }
         return r;
     };
-    int blk = 0;
-    for (int i = 0; i < nj; ++i, ++blk) {
+    for (int i = 0; i < nj; ++i) {
         Ls.w = &m->jl[i];
         Cs.w = &m->jc[i];
         Xs.w = &m->jt[i];
-        Ls.mod = m->mod_l[blk & 1];
-        Cs.mod = m->mod_c[blk & 1];
-        Xs.mod = m->mod_t[blk & 1];
+        Ls.mod = m->mods_lat + Ls.w->mod_col; Ls.ld_mod = Ml;
+        Cs.mod = m->mods_gc + Cs.w->mod_col; Cs.ld_mod = Mg;
+        Xs.mod = m->mods_gc + Xs.w->mod_col; Xs.ld_mod = Mg;
         Stream r3[3] = {Ls, Cs, Xs};
-        if ((rc = run_mods(m, r3, 3, B, T, st))) return rc;
         if ((rc = run_ln(m, r3, 3, B, 0, st)) || (rc = capture())) return rc;
         if ((rc = run_qkv(m, r3, 3, B, Ntot, st))) return rc;
         if ((rc = run_attention(m, r3, 3, B, Ntot, st))) return rc;
@@ -947,10 +986,9 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
     }
     cap_joint = true;
     // ---- fused blocks on the latent with extended_c (:274-281)
-    for (int i = 0; i < c.fused_depth; ++i, ++blk) {
+    for (int i = 0; i < c.fused_depth; ++i) {
         Ls.w = &m->fb[i];
-        Ls.mod = m->mod_l[blk & 1];
-        if ((rc = run_mods(m, &Ls, 1, B, T, st))) return rc;
+        Ls.mod = m->mods_lat + Ls.w->mod_col; Ls.ld_mod = Ml;
         if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
         if ((rc = run_qkv(m, &Ls, 1, B, T, st))) return rc;
         if ((rc = run_attention(m, &Ls, 1, B, T, st))) return rc;
@@ -962,8 +1000,7 @@ int forward_impl(tsk_mmdit *m, int B, int T, int clip_S, int sync_S, const Input
     fin.nmod = 2;
     fin.ada = lin_of(m, "final_layer.adaLN_modulation.1", true);
     Ls.w = &fin;
-    Ls.mod = m->mod_l[blk & 1];
-    if ((rc = run_mods(m, &Ls, 1, B, T, st))) return rc;
+    Ls.mod = m->mods_lat + m->fin_mod_col; Ls.ld_mod = Ml;
     if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
     if ((rc = grab(m, "after_fused", m->lat, (size_t) B * T * H, st))) return rc;
     const Conv fc = conv_of(m, "final_layer.conv", true);
