@@ -89,7 +89,8 @@ template <bool KBF16, bool BOUNDED, int KS, int QB>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     constexpr int NB = nbuf(KS, QB);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar tile loop and load bases
     const int g = wave / QB, qb = wave % QB;
     const int l32 = lane & 31, hi = lane >> 5;
 
@@ -130,26 +131,41 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     constexpr int NJ = (16 - 1) / QB + 1;       // wave-loads of wave qb: j = qb + QB * i < 16
     const int r8 = lane >> 3;
     const int ch0 = (lane & 7) ^ (lane >> 4), ch1 = (lane & 7) ^ (4 | (lane >> 4));
-    const char *krow0 = kp + (int64_t) r8 * p.k_nb1;
-    const uint16_t *vrow0 = vp + (int64_t) r8 * p.ldv;
+    // per-lane byte offsets of this wave's wave-loads, the same for every
+    // tile: a tile adds one wave-uniform base (key0 rows of K, key0 columns
+    // of V^T), so issuing it costs scalar arithmetic only
+    uint32_t ioff[NJ];
+#pragma unroll
+    for (int i = 0; i < NJ; ++i) {
+        const int j = qb + QB * i < 16 ? qb + QB * i : 0;
+        const int ch = (j & 1) ? ch1 : ch0;
+        const int row = (j & 7) * 8 + r8;
+        ioff[i] = j < 8 ? (uint32_t) (row * p.k_nb1 + ch * 16) : (uint32_t) (2 * (row * p.ldv + ch * 8));
+    }
     auto issue = [&](int tile, int buf) {
         uint16_t *dst = gb + buf * TILE_H;
         const int key0 = tile * KT;
-        const bool last = tile == ntiles - 1;
+        if (tile == ntiles - 1) {
 #pragma unroll
-        for (int i = 0; i < NJ; ++i) {
-            const int j = qb + QB * i;
-            if (j >= 16) break;
-            const int ch = (j & 1) ? ch1 : ch0;
-            const void *src;
-            if (j < 8) {
-                const int rowu = key0 + (j & 7) * 8;                 // wave-uniform part of the key row
-                src = last ? (const void *) (kp + (int64_t) min(rowu + r8, p.Nkv - 1) * p.k_nb1 + ch * 16)
-                           : (const void *) (krow0 + (int64_t) rowu * p.k_nb1 + ch * 16);
-            } else {
-                src = vrow0 + (int64_t) ((j & 7) * 8) * p.ldv + key0 + ch * 8;
+            for (int i = 0; i < NJ; ++i) {
+                const int j = qb + QB * i;
+                if (j >= 16) break;
+                const int ch = (j & 1) ? ch1 : ch0;
+                const void *src;
+                if (j < 8) src = (const void *) (kp + (int64_t) min(key0 + (j & 7) * 8 + r8, p.Nkv - 1) * p.k_nb1 + ch * 16);
+                else src = (const void *) ((const char *) vp + 2 * key0 + ioff[i]);
+                __builtin_amdgcn_global_load_lds(src, (lds_void *) (dst + j * 512), 16, 0, 0);
             }
-            __builtin_amdgcn_global_load_lds(src, (lds_void *) (dst + j * 512), 16, 0, 0);
+        } else {
+            const char *kb = kp + (int64_t) key0 * p.k_nb1;
+            const char *vb = (const char *) vp + 2 * key0;
+#pragma unroll
+            for (int i = 0; i < NJ; ++i) {
+                const int j = qb + QB * i;
+                if (j >= 16) break;
+                __builtin_amdgcn_global_load_lds((const void *) ((j < 8 ? kb : vb) + ioff[i]), (lds_void *) (dst + j * 512),
+                                                 16, 0, 0);
+            }
         }
     };
 
@@ -329,14 +345,17 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         // each range weighted by exp2(m_range - m_max)
         constexpr int JW = 32 / KS;
         static_assert(JW % 4 == 0, "whole 4-dim groups per wave");
-        float *mo = (float *) lds;                        // [KS][QB][32][64] partial O^T
+        float *mo = (float *) lds;                        // [KS][QB][8][64][4] partial O^T
         float *ml = mo + KS * QB * 32 * 64;               // [KS][QB][2][64]  m, l
         {
-            float *dst = mo + (g * QB + qb) * 32 * 64;
+            // value v = 16 db + e of this lane at [v / 4][lane][v % 4]: 16-byte LDS accesses
+            float *dst = mo + (g * QB + qb) * 32 * 64 + lane * 4;
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) dst[(16 * db + e) * 64 + lane] = o[db][e];
+                for (int r = 0; r < 4; ++r)
+                    *(f32x4 *) (dst + (4 * db + r) * 256) =
+                        f32x4{o[db][4 * r], o[db][4 * r + 1], o[db][4 * r + 2], o[db][4 * r + 3]};
             float *dl = ml + (g * QB + qb) * 128;
             dl[lane] = m_run;
             dl[64 + lane] = l_run;
@@ -359,9 +378,13 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         for (int jj = 0; jj < JW; ++jj) oj[jj] = 0.0f;
 #pragma unroll
         for (int g2 = 0; g2 < KS; ++g2) {
-            const float *src = mo + (g2 * QB + qb) * 32 * 64 + g * JW * 64 + lane;
+            const float *src = mo + (g2 * QB + qb) * 32 * 64 + (g * JW / 4) * 256 + lane * 4;
 #pragma unroll
-            for (int jj = 0; jj < JW; ++jj) oj[jj] += src[jj * 64] * wt[g2];
+            for (int k4 = 0; k4 < JW / 4; ++k4) {
+                const f32x4 v4 = *(const f32x4 *) (src + k4 * 256);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) oj[4 * k4 + jj] += v4[jj] * wt[g2];
+            }
         }
         const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
         const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
