@@ -40,8 +40,10 @@ void attn_kernel(const AttnParams p) {
     constexpr int NT = NW * 64;      // threads of one key range
     constexpr int QROWS = NW * QB * 16;
 
-    const int tid = threadIdx.x % NT, ks = threadIdx.x / NT;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x % NT;
+    // wave-uniform: the key range and the wave's query rows stay in scalar registers
+    const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x / NT);
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
     const int h = blockIdx.y, b = blockIdx.z;
     const int hk = h / (p.H / p.Hkv);
