@@ -131,41 +131,31 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     constexpr int NJ = (16 - 1) / QB + 1;       // wave-loads of wave qb: j = qb + QB * i < 16
     const int r8 = lane >> 3;
     const int ch0 = (lane & 7) ^ (lane >> 4), ch1 = (lane & 7) ^ (4 | (lane >> 4));
-    // per-lane byte offsets of this wave's wave-loads, the same for every
-    // tile: a tile adds one wave-uniform base (key0 rows of K, key0 columns
-    // of V^T), so issuing it costs scalar arithmetic only
-    uint32_t ioff[NJ];
-#pragma unroll
-    for (int i = 0; i < NJ; ++i) {
-        const int j = qb + QB * i < 16 ? qb + QB * i : 0;
-        const int ch = (j & 1) ? ch1 : ch0;
-        const int row = (j & 7) * 8 + r8;
-        ioff[i] = j < 8 ? (uint32_t) (row * p.k_nb1 + ch * 16) : (uint32_t) (2 * (row * p.ldv + ch * 8));
-    }
+    // Tile loads are buffer loads into LDS: a buffer descriptor per operand of
+    // this (batch, head), a per-lane byte offset that is the same for every
+    // tile (one per chunk parity) and a wave-uniform offset per wave-load, so
+    // issuing a tile is scalar arithmetic only. The K descriptor ends after
+    // row Nkv - 1: rows past it (the last tile's padding, masked to -inf
+    // below) read as zeros.
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void *) kp, (short) 0, (int) ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *) vp, (short) 0, (int) (64 * p.ldv * 2), 0x00020000);
+    const uint32_t koff0 = (uint32_t) (r8 * p.k_nb1 + ch0 * 16), koff1 = (uint32_t) (r8 * p.k_nb1 + ch1 * 16);
+    const uint32_t voff0 = (uint32_t) (2 * (r8 * p.ldv + ch0 * 8)), voff1 = (uint32_t) (2 * (r8 * p.ldv + ch1 * 8));
     auto issue = [&](int tile, int buf) {
         uint16_t *dst = gb + buf * TILE_H;
         const int key0 = tile * KT;
-        if (tile == ntiles - 1) {
 #pragma unroll
-            for (int i = 0; i < NJ; ++i) {
-                const int j = qb + QB * i;
-                if (j >= 16) break;
-                const int ch = (j & 1) ? ch1 : ch0;
-                const void *src;
-                if (j < 8) src = (const void *) (kp + (int64_t) min(key0 + (j & 7) * 8 + r8, p.Nkv - 1) * p.k_nb1 + ch * 16);
-                else src = (const void *) ((const char *) vp + 2 * key0 + ioff[i]);
-                __builtin_amdgcn_global_load_lds(src, (lds_void *) (dst + j * 512), 16, 0, 0);
-            }
-        } else {
-            const char *kb = kp + (int64_t) key0 * p.k_nb1;
-            const char *vb = (const char *) vp + 2 * key0;
-#pragma unroll
-            for (int i = 0; i < NJ; ++i) {
-                const int j = qb + QB * i;
-                if (j >= 16) break;
-                __builtin_amdgcn_global_load_lds((const void *) ((j < 8 ? kb : vb) + ioff[i]), (lds_void *) (dst + j * 512),
-                                                 16, 0, 0);
-            }
+        for (int i = 0; i < NJ; ++i) {
+            const int j = qb + QB * i;
+            if (j >= 16) break;
+            if (j < 8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *) (dst + j * 512), 16, (j & 1) ? koff1 : koff0,
+                                                         (int) ((key0 + (j & 7) * 8) * p.k_nb1), 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *) (dst + j * 512), 16, (j & 1) ? voff1 : voff0,
+                                                         2 * ((j & 7) * 8 * p.ldv + key0), 0, 0);
         }
     };
 
@@ -478,6 +468,10 @@ int attn_fast_default_cfg(int Nq, int H, int B, int bounded) {
 
 hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
     if (p.Nq < 1 || p.Nkv < 1 || p.H < 1 || p.B < 1 || p.ldv < (p.Nkv + KT - 1) / KT * KT) return hipErrorInvalidValue;
+    // buffer descriptors: 31-bit byte ranges per (batch, head)
+    if ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128 >= ((int64_t) 1 << 31) || p.k_nb1 < 128 ||
+        (int64_t) 128 * p.ldv >= ((int64_t) 1 << 31))
+        return hipErrorInvalidValue;
     const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.bounded && !p.k_bf16);
     if (p.bounded && !p.k_bf16) return launch_cfg<false, true>(p, cfg, s);
     return p.k_bf16 ? launch_cfg<true, false>(p, cfg, s) : launch_cfg<false, false>(p, cfg, s);
