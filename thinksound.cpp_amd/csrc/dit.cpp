@@ -113,6 +113,7 @@ struct tsk_dit {
     // cfg, or 0 for the shape rule of gemm_cfg_for() (Tuning::gemm_cfg overrides)
     int gemm_cfg[4] = {0, 0, 0, 0};
     int ksplit_out = 2, ksplit_fc2 = 4;
+    bool ksplit_auto = true;        // linear1's split-K by latent tokens (ksplit_out_for)
     bool timing = false;
     int attn_cfg = 0;               // attention launch shape override (0: automatic)
     // second stream for the adaLN GEMVs of the later blocks (HBM-bound) while
@@ -307,6 +308,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
     d->attn_cfg = tuning().attn_cfg;
     for (int i = 0; i < 4; ++i) d->gemm_cfg[i] = tuning().gemm_cfg[i];
     d->ksplit_out = tuning().ksplit_out;
+    d->ksplit_auto = !tuning().ksplit_set;
     d->ksplit_fc2 = tuning().ksplit_fc2;
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden, nj = c.depth - c.fused_depth;
@@ -641,6 +643,17 @@ GemmProblem gemm_problem(const void *x, int64_t ld_x, const uint16_t *w, const f
 
 int gemm_cfg_for(const tsk_dit *d, int role, int rows);
 
+// split-K slices of the BF16 driver's linear1 (K = 1024) by latent tokens per
+// batch item (never by batch, so that batch rows stay independent bit for
+// bit): two below 550, where 16 x 64-row tiles per few hundred rows leave
+// most CUs idle, one from there (MI355X, 30 s: the GEMM 9.4 -> 9.1 us and its
+// LN reading one slice instead of two, 422 -> 426 steps/s; at 9 s one slice
+// loses 670 -> 654)
+int ksplit_out_for(const tsk_dit *d, int seq) {
+    if (!d->ksplit_auto) return d->ksplit_out;
+    return seq >= 550 ? 1 : 2;
+}
+
 // LN + modulate of every stream (paying the residual updates they owe) into
 // xn (bf16), or into the Q8_0 planes qx / dx for the Q8_0 driver
 int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
@@ -693,7 +706,7 @@ int run_ln(tsk_dit *d, StreamRun *r, int ns, int B, int which, hipStream_t st) {
         for (int i = 0; i < ns; ++i) {
             const StreamW &w = *r[i].w;
             if (w.pre_only) continue;
-            if (which == 0) add(w.l1_w, H, H, 1, d->ksplit_out);
+            if (which == 0) add(w.l1_w, H, H, 1, ksplit_out_for(d, r[0].S));
             else add(w.fc2_w, c.mlp_hidden, H, 3, d->ksplit_fc2);
         }
     }
@@ -756,13 +769,13 @@ int run_out(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         q = gemm_problem(d->o + (size_t) r[i].tok_off * H, H, r[i].w->l1_w, nullptr, r[i].part, H, rows, H, H);
         q.x_group_rows = r[i].S;
         q.x_group_stride = (int64_t) Ntot * H;
-        q.splits = d->ksplit_out;
-        r[i].pend_split = d->ksplit_out;
+        q.splits = ksplit_out_for(d, r[0].S);
+        r[i].pend_split = q.splits;
         r[i].pend_bias = r[i].w->l1_b;
         r[i].pend_gate = mod_of(d, *r[i].w) + 2 * H;   // gate_msa
         r[i].pend_ld_gate = mod_ld(d, *r[i].w);
         fl += 2.0 * rows * H * H;
-        by += 2.0 * H * H + 2.0 * rows * H + 4.0 * d->ksplit_out * rows * H;
+        by += 2.0 * H * H + 2.0 * rows * H + 4.0 * q.splits * rows * H;
     }
     if (!g.nprob) return TSK_OK;
     Timed tm(d, TSK_ROLE_OUT, fl, by, st);

@@ -72,6 +72,7 @@ void read_tuning() {
         if ((ks[0] == '1' || ks[0] == '2' || ks[0] == '4') && (ks[1] == '1' || ks[1] == '2' || ks[1] == '4')) {
             t.ksplit_out = ks[0] - '0';
             t.ksplit_fc2 = ks[1] - '0';
+            t.ksplit_set = true;
         }
     // one character per projection (qkv, out, fc1, fc2): 0-9, a-z = 10-35, A-Z = 36-61
     if (const char *gc = getenv("TSK_GEMM_CFG"))

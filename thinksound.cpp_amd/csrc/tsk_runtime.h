@@ -41,6 +41,7 @@ struct Tuning {
     bool ln_block = false;
     int gemv_rw = 2;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
+    bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:
                                           // -1 by activation rows, 0 never, 1 always
 };
