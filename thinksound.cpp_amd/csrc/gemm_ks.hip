@@ -733,7 +733,7 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
             if (sec < 2) {
                 // the 16 lanes of this (token, head) pair form one DPP row
                 const float ss = row16_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
-                const float sc = 1.0f / sqrtf(ss / 64.0f + p.eps);
+                const float sc = __builtin_amdgcn_rsqf(ss / 64.0f + p.eps);   // v_rsq_f32, within 1 ulp
                 for (int e = 0; e < 4; ++e) x[e] = x[e] * sc * wv[e];
                 if (p.rope) {
                     // (cos, sin) of pairs 2 sl, 2 sl + 1 at position spos
@@ -775,7 +775,9 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
             const float h1[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             const float h3[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
             float o[8];
-            for (int e = 0; e < 8; ++e) o[e] = h1[e] / (1.0f + expf(-h1[e])) * h3[e];
+            // silu(h1) = h1 / (1 + exp(-h1)), the quotient through the hardware
+            // reciprocal (within 1 ulp): exp(-h1) = inf gives 0, = 0 gives h1
+            for (int e = 0; e < 8; ++e) o[e] = h1[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-h1[e])) * h3[e];
             if constexpr (EPI == EPI_SWIGLU_BF16) {
                 uint16_t t8[8];
                 for (int e = 0; e < 8; ++e) t8[e] = f32_to_bf16_bits(o[e]);
