@@ -454,6 +454,45 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(const void *v, int v_
     }
 }
 
+// The same transpose with 16-byte accesses (rows and strides 16-byte
+// aligned): a thread loads 8 dims of one key row and stores 8 consecutive
+// V^T slots of one dim row, whose keys vt_pos() gives (an involution: slot p
+// holds key vt_pos(p)).
+__global__ __launch_bounds__(256) void vt_transpose16_kernel(const void *v, int v_bf16, int64_t nb1, int64_t nb2,
+                                                             int64_t nb3, int Nkv, int H, uint16_t *vt, int ldv) {
+    __shared__ __attribute__((aligned(16))) uint16_t t[64][72];
+    const int bh = blockIdx.y, b = bh / H, h = bh % H, k0 = blockIdx.x * 64;
+    const char *vb = (const char *) v + (int64_t) h * nb2 + (int64_t) b * nb3;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int i = threadIdx.x + 256 * r, kk = i >> 3, c = i & 7;
+        u32x4 x = u32x4{0, 0, 0, 0};
+        if (k0 + kk < Nkv) {
+            x = *(const u32x4 *) (vb + (int64_t) (k0 + kk) * nb1 + 16 * c);
+            if (v_bf16) {
+                uint16_t e[8];
+                __builtin_memcpy(e, &x, 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) e[j] = f32_to_f16_bits(bf16_bits_to_f32(e[j]));
+                __builtin_memcpy(&x, e, 16);
+            }
+        }
+        *(u32x4 *) &t[kk][8 * c] = x;
+    }
+    __syncthreads();
+    uint16_t *dst = vt + (int64_t) bh * 64 * ldv + k0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int i = threadIdx.x + 256 * r, d = i >> 3, c = i & 7;
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = t[vt_pos(8 * c + j)][d];
+        u32x4 x;
+        __builtin_memcpy(&x, e, 16);
+        *(u32x4 *) (dst + (int64_t) d * ldv + 8 * c) = x;
+    }
+}
+
 }  // namespace
 
 // (key ranges, query blocks) per workgroup, from MI355X sweeps over the
@@ -461,7 +500,7 @@ __global__ __launch_bounds__(256) void vt_transpose_kernel(const void *v, int v_
 // (batch, head) pairs spread over the 256 CUs with 2-3 waves per SIMD
 int attn_fast_default_cfg(int Nq, int H, int B, int bounded) {
     const int qblocks = (Nq + 31) / 32 * H * B;
-    if (qblocks >= 640) return bounded ? 43 : 24;
+    if (qblocks >= 640) return 43;   // bf16 node, N = 723, B = 2: 4 x 3 19.3 us, 2 x 4 20.0-20.5 us
     if (qblocks >= 256) return 42;
     return 41;
 }
@@ -479,8 +518,14 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
 
 hipError_t launch_vt_transpose(const void *v, int v_bf16, int64_t nb1, int64_t nb2, int64_t nb3, int Nkv, int H, int B,
                                uint16_t *vt, int ldv, hipStream_t s) {
-    launch_kernel(vt_transpose_kernel, dim3(ldv / 64, H * B), dim3(256), 0, s, v, v_bf16, nb1, nb2, nb3, Nkv, H,
-                       vt, ldv);
+    const bool a16 = ((uintptr_t) v | (uintptr_t) vt | (uint64_t) nb1 | (uint64_t) nb2 | (uint64_t) nb3) % 16 == 0 &&
+                     ldv % 64 == 0;
+    if (a16)
+        launch_kernel(vt_transpose16_kernel, dim3(ldv / 64, H * B), dim3(256), 0, s, v, v_bf16, nb1, nb2, nb3, Nkv, H,
+                      vt, ldv);
+    else
+        launch_kernel(vt_transpose_kernel, dim3(ldv / 64, H * B), dim3(256), 0, s, v, v_bf16, nb1, nb2, nb3, Nkv, H,
+                      vt, ldv);
     return hipGetLastError();
 }
 
