@@ -498,9 +498,11 @@ __global__ __launch_bounds__(256) void vt_transpose16_kernel(const void *v, int 
 // (key ranges, query blocks) per workgroup, from MI355X sweeps over the
 // MM-DiT shapes (B=2, 16 heads, N = 194 .. 1040): 32-row query blocks of all
 // (batch, head) pairs spread over the 256 CUs with 2-3 waves per SIMD
-int attn_fast_default_cfg(int Nq, int H, int B, int bounded) {
+int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16) {
     const int qblocks = (Nq + 31) / 32 * H * B;
-    if (qblocks >= 640) return 43;   // bf16 node, N = 723, B = 2: 4 x 3 19.3 us, 2 x 4 20.0-20.5 us
+    // bf16 K: the 4 x 3 instance spills a register to scratch (19.3 us at N =
+    // 723, B = 2 against 20.0-20.5 us for 2 x 4), so it keeps 2 x 4
+    if (qblocks >= 640) return k_bf16 ? 24 : 43;
     if (qblocks >= 256) return 42;
     return 41;
 }
@@ -511,7 +513,7 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
     if ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128 >= ((int64_t) 1 << 31) || p.k_nb1 < 128 ||
         (int64_t) 128 * p.ldv >= ((int64_t) 1 << 31))
         return hipErrorInvalidValue;
-    const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.bounded && !p.k_bf16);
+    const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.k_bf16);
     if (p.bounded && !p.k_bf16) return launch_cfg<false, true>(p, cfg, s);
     return p.k_bf16 ? launch_cfg<true, false>(p, cfg, s) : launch_cfg<false, false>(p, cfg, s);
 }

@@ -86,7 +86,7 @@ struct AttnFastParams {
 // exp2 of it (~6e3) and sums of it over 2^14 keys stay far inside fp16 / fp32.
 constexpr float ATTN_LOGIT_BOUND = 14.0f;
 hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s);
-int attn_fast_default_cfg(int Nq, int H, int B, int bounded);
+int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16);
 // V (F16/BF16 rows of 64, ggml strides) -> the transposed fp16 layout above
 hipError_t launch_vt_transpose(const void *v, int v_bf16, int64_t nb1, int64_t nb2, int64_t nb3, int Nkv, int H,
                                int B, uint16_t *vt, int ldv, hipStream_t s);
