@@ -114,3 +114,50 @@ def test_strided_views_and_determinism(env):
     assert np.array_equal(o1, o2)
     ref = orc.flash_attn_ext(qkv[:, 0], qkv[:, 1], qkv[:, 2])
     assert rel_l2(o1, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("kv,N", [("f16", 723), ("f16", 130), ("bf16", 723), ("bf16", 61)])
+@pytest.mark.parametrize("v_offset", [0, 8])
+def test_fast_path_permuted_views(env, kv, N, v_offset):
+    """16-bit K/V as the permuted views ggml hands over (storage [B][N][H][64]:
+    the key-row stride is H * 128 bytes, not one row), N not a multiple of 64
+    (the last tile's K rows past N read as zeros through the buffer range and are
+    masked), sizes on the 4 x 3 / 2 x 4 and 4 x 1 launch shapes, V at the start of
+    its buffer or 16 bytes into it; a V 2 bytes off 16-byte alignment is refused
+    on the host (TSK_ERR_ALIGN) before any launch."""
+    tsk, orc = env
+    rng = np.random.default_rng(7 * N + v_offset)
+    B, H = 2, 16
+    q = rng.standard_normal((B, N, H, 64)).astype(np.float32)
+    kf = rng.standard_normal((B, N, H, 64)).astype(np.float32)
+    vf = rng.standard_normal((B, N, H, 64)).astype(np.float32)
+    perm = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))   # (B, H, N, 64)
+    st = (N * H * 64, 64, H * 64, 1)                                 # element strides of the permuted view
+    if kv == "f16":
+        kb, vb = kf.astype(np.float16), vf.astype(np.float16)
+        kd = tsk.to_device(kb)
+        vbuf = tsk.DeviceArray((B * N * H * 64 + 16,), "f16")
+        vhost = np.zeros(B * N * H * 64 + 16, np.float16)
+        vhost[v_offset:v_offset + vb.size] = vb.ravel()
+        qd = tsk.to_device(q)
+        ref = orc.flash_attn_ext(perm(q), perm(kb), perm(vb), scale=0.125)
+    else:
+        qbits, kbits, vbits = (orc.f32_to_bf16_bits(a) for a in (q, kf, vf))
+        kd = tsk.bf16_to_device(kbits)
+        vbuf = tsk.DeviceArray((B * N * H * 64 + 16,), "bf16")
+        vhost = np.zeros(B * N * H * 64 + 16, np.uint16)
+        vhost[v_offset:v_offset + vbits.size] = vbits.ravel()
+        qd = tsk.bf16_to_device(qbits)
+        ref = orc.flash_attn_ext(perm(qbits), perm(kbits), perm(vbits), scale=0.125, kv_bf16=True, q_bf16=True)
+    import ctypes
+    tsk._hipcheck(tsk.hip().hipMemcpy(ctypes.c_void_p(vbuf.ptr), ctypes.c_void_p(vhost.ctypes.data), vhost.nbytes, 1),
+                  "hipMemcpy H2D")
+    qv = qd.view(0, (B, H, N, 64), st)
+    kvw = kd.view(0, (B, H, N, 64), st)
+    vv = vbuf.view(v_offset, (B, H, N, 64), st)
+    o1 = tsk.flash_attn_ext(qv, kvw, vv, scale=0.125).numpy()
+    o2 = tsk.flash_attn_ext(qv, kvw, vv, scale=0.125).numpy()
+    assert np.array_equal(o1, o2)
+    assert rel_l2(o1, ref) <= 1e-3
+    with pytest.raises(tsk.TskError, match="ALIGN"):
+        tsk.flash_attn_ext(qv, kvw, vbuf.view(v_offset + 1, (B, H, N, 64), st), scale=0.125)
