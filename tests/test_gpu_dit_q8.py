@@ -169,3 +169,27 @@ def test_q8_load_gguf(env, tmp_path):
     g.close()
     a.close()
     b.close()
+
+
+def test_stream_pairs_change_no_bits(env, monkeypatch):
+    """A joint block's two Q8_0 projections run as one launch (both streams'
+    tiles in one grid); each output is summed in the same order as when the
+    streams run as two launches (TSK_Q8_PAIR=0): the flow is bit-equal, at 9 s
+    and at a length where the tile shape changes (T = 400), over joint blocks
+    with a pre_only text stream and fused blocks."""
+    tsk, orc = env
+    dit, _, _, _ = build_q8_pair(tsk, orc, depth=3, fused_depth=1, max_latent=400)
+    try:
+        for T in (194, 400):
+            lat, t, txt = inputs(2, T, seed=T + 3)
+            ref = dit.forward(cm(lat), t, txt)
+            monkeypatch.setenv("TSK_Q8_PAIR", "0")
+            tsk.init(0, reread=True)
+            f = dit.forward(cm(lat), t, txt)
+            monkeypatch.delenv("TSK_Q8_PAIR")
+            tsk.init(0, reread=True)
+            assert np.isfinite(ref).all() and np.array_equal(f, ref), T
+    finally:
+        monkeypatch.delenv("TSK_Q8_PAIR", raising=False)
+        tsk.init(0, reread=True)
+        dit.close()

@@ -835,19 +835,34 @@ double q8_bytes(int N, int K, int M, double out_bytes) {
     return (double) M * K * (1.0 + 2.0 / 32) + (double) N * K * (1.0 + 4.0 / 32) + (double) N * M * out_bytes;
 }
 
+// the Q8_0 projections of the active streams: a joint block's two in one
+// launch (launch_gemm_q8_pair), one stream alone otherwise
+int q8_launch(tsk_dit *d, const GemmParams *ps, int n, int role, double fl, double by, const char *what,
+              hipStream_t st) {
+    if (n < 1) return TSK_OK;
+    Timed tm(d, role, fl, by, st);
+    return hipcheck(n == 2 ? launch_gemm_q8_pair(ps[0], ps[1], st) : launch_gemm_q8(ps[0], st), what);
+}
+
 // QKV GEMM into f32 rows, then RMSNorm / RoPE / fp16 scatter into the
 // attention operands
 int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden;
     int rc;
-    for (int i = 0; i < ns; ++i) {
-        GemmParams p = q8_problem(d, r[i].w->qkv_q, r[i], B, H, 3 * H, r[i].w->qkv_b);
-        p.y = d->qkv32 + r[i].row_off * 3 * H;
-        p.ld_y = 3 * H;
-        p.epi = EPI_STORE;
-        Timed tm(d, TSK_ROLE_QKV, 2.0 * p.N * H * 3.0 * H, q8_bytes(p.N, H, 3 * H, 4), st);
-        if ((rc = hipcheck(launch_gemm_q8(p, st), "qkv q8 gemm"))) return rc;
+    {
+        GemmParams ps[2];
+        double fl = 0.0, by = 0.0;
+        for (int i = 0; i < ns; ++i) {
+            GemmParams &p = ps[i];
+            p = q8_problem(d, r[i].w->qkv_q, r[i], B, H, 3 * H, r[i].w->qkv_b);
+            p.y = d->qkv32 + r[i].row_off * 3 * H;
+            p.ld_y = 3 * H;
+            p.epi = EPI_STORE;
+            fl += 2.0 * p.N * H * 3.0 * H;
+            by += q8_bytes(p.N, H, 3 * H, 4);
+        }
+        if ((rc = q8_launch(d, ps, ns, TSK_ROLE_QKV, fl, by, "qkv q8 gemm", st))) return rc;
     }
     for (int i = 0; i < ns; ++i) {
         QkvScatter q;
@@ -899,14 +914,18 @@ int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
                            "linear1 quantize")))
             return rc;
     }
+    GemmParams ps[2];
+    int n = 0;
+    double fl = 0.0, by = 0.0;
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
-        GemmParams p = q8_problem(d, r[i].w->l1_q, r[i], B, H, H, nullptr);
+        GemmParams &p = ps[n++];
+        p = q8_problem(d, r[i].w->l1_q, r[i], B, H, H, nullptr);
         q8_partials(d, p, r[i], B, d->ksplit_out, r[i].w->l1_b, 2);   // gate_msa
-        Timed tm(d, TSK_ROLE_OUT, 2.0 * p.N * H * H, q8_bytes(p.N, H, H, 4 * p.splits), st);
-        if ((rc = hipcheck(launch_gemm_q8(p, st), "linear1 q8 gemm"))) return rc;
+        fl += 2.0 * p.N * H * H;
+        by += q8_bytes(p.N, H, H, 4 * p.splits);
     }
-    return TSK_OK;
+    return q8_launch(d, ps, n, TSK_ROLE_OUT, fl, by, "linear1 q8 gemm", st);
 }
 
 // fc1 of every stream with GELU and the Q8_0 conversion of its output in the
@@ -915,26 +934,28 @@ int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
 int run_mlp_q8(tsk_dit *d, StreamRun *r, int ns, int B, hipStream_t st) {
     const int H = d->cfg.hidden, F = d->cfg.mlp_hidden;
     int rc;
+    GemmParams p1[2], p2[2];
+    int n = 0;
+    double fl = 0.0, by1 = 0.0, by2 = 0.0;
     for (int i = 0; i < ns; ++i) {
         if (r[i].w->pre_only) continue;
-        GemmParams p = q8_problem(d, r[i].w->fc1_q, r[i], B, H, F, r[i].w->fc1_b);
+        GemmParams &p = p1[n];
+        p = q8_problem(d, r[i].w->fc1_q, r[i], B, H, F, r[i].w->fc1_b);
         p.y = d->qh + r[i].row_off * F;
         p.ld_y = F;
         p.yd = d->dh + r[i].row_off * (F / 32);
         p.epi = EPI_GELU_Q8;
-        Timed tm(d, TSK_ROLE_FC1, 2.0 * p.N * H * F, q8_bytes(p.N, H, F, 1.125), st);
-        if ((rc = hipcheck(launch_gemm_q8(p, st), "fc1 q8 gemm"))) return rc;
+        GemmParams &q = p2[n++];
+        q = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, nullptr);
+        q.qx = d->qh + r[i].row_off * F;
+        q.dx = d->dh + r[i].row_off * (F / 32);
+        q8_partials(d, q, r[i], B, d->ksplit_fc2, r[i].w->fc2_b, 5);   // gate_mlp
+        fl += 2.0 * p.N * H * F;
+        by1 += q8_bytes(p.N, H, F, 1.125);
+        by2 += q8_bytes(q.N, F, H, 4 * q.splits);
     }
-    for (int i = 0; i < ns; ++i) {
-        if (r[i].w->pre_only) continue;
-        GemmParams p = q8_problem(d, r[i].w->fc2_q, r[i], B, F, H, nullptr);
-        p.qx = d->qh + r[i].row_off * F;
-        p.dx = d->dh + r[i].row_off * (F / 32);
-        q8_partials(d, p, r[i], B, d->ksplit_fc2, r[i].w->fc2_b, 5);   // gate_mlp
-        Timed tm(d, TSK_ROLE_FC2, 2.0 * p.N * H * F, q8_bytes(p.N, F, H, 4 * p.splits), st);
-        if ((rc = hipcheck(launch_gemm_q8(p, st), "fc2 q8 gemm"))) return rc;
-    }
-    return TSK_OK;
+    if ((rc = q8_launch(d, p1, n, TSK_ROLE_FC1, fl, by1, "fc1 q8 gemm", st))) return rc;
+    return q8_launch(d, p2, n, TSK_ROLE_FC2, fl, by2, "fc2 q8 gemm", st);
 }
 
 int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream_t st);

@@ -363,8 +363,10 @@ __device__ __forceinline__ void q8_wait_vm() {
 }
 }  // namespace
 
+// One output tile of problem p; li = the workgroup's index within p's tiles
+// (p is a kernel argument read by name, never through a runtime index)
 template <int TM, int TN, int R, int EPI, bool YBF16>
-__global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int tiles_m, int tiles_n) {
+__device__ __forceinline__ void q8c_tile(const GemmParams &p, const int li, const int tiles_m, const int tiles_n) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int BM = 16 * TM, BN = 16 * TN, TMW = TM / 2, TNW = TN / 2;
     constexpr int U = TM + TN, USZ = 2048, STG = U * USZ, LW = 2 * U / 4;
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     // [kbase, kbase + KB) of rows KBR blocks long
     const int S = p.splits > 1 ? p.splits : 1;
     const int KBR = p.K / 32, KB = KBR / S, ns = KB / 4;
-    const int li = blockIdx.x, cm = tiles_m * S;
+    const int cm = tiles_m * S;
     int c, tn;
     if ((cm & 7) == 0) {
         // XCD x (= workgroup id mod 8) owns units x, x + 8, ... and every token tile of each
@@ -613,6 +615,21 @@ __global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int t
     }
 }
 
+template <int TM, int TN, int R, int EPI, bool YBF16>
+__global__ __launch_bounds__(256) void gemm_q8c_kernel(const GemmParams p, int tiles_m, int tiles_n) {
+    q8c_tile<TM, TN, R, EPI, YBF16>(p, (int) blockIdx.x, tiles_m, tiles_n);
+}
+
+// two problems in one launch (the latent and text streams of a joint block):
+// workgroups from begin1 (a multiple of 8, so that the XCD a unit lands on is
+// the same in both numberings) run p1
+template <int TM, int TN, int R, int EPI, bool YBF16>
+__global__ __launch_bounds__(256) void gemm_q8c_pair_kernel(const GemmParams p0, const GemmParams p1, int tm0, int tn0,
+                                                            int tm1, int tn1, int begin1) {
+    if ((int) blockIdx.x >= begin1) q8c_tile<TM, TN, R, EPI, YBF16>(p1, (int) blockIdx.x - begin1, tm1, tn1);
+    else q8c_tile<TM, TN, R, EPI, YBF16>(p0, (int) blockIdx.x, tm0, tn0);
+}
+
 // ------------------------------------------------------------------ activation quantization
 // One thread per 32-block: d = amax/127 (stored as the fp32 value of its fp16
 // rounding), q = rne(x * (127/amax)) — ggml-cpu's x86 quantize_row_q8_0.
@@ -727,6 +744,38 @@ hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int TM, int TN, int R, int EPI, bool YBF16>
+hipError_t q8c_launch_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t s) {
+    constexpr int BM = 16 * TM, BN = 16 * TN;
+    const int tm0 = (p0.M + BM - 1) / BM, tn0 = (p0.N + BN - 1) / BN;
+    const int tm1 = (p1.M + BM - 1) / BM, tn1 = (p1.N + BN - 1) / BN;
+    const int S0 = p0.splits > 1 ? p0.splits : 1, S1 = p1.splits > 1 ? p1.splits : 1;
+    const size_t lds = (size_t) R * (TM + TN) * 2048 +
+                       (size_t) std::min(std::max(p0.K, p1.K) / 32, Q8_SEG) * (BM + BN) * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    auto kern = gemm_q8c_pair_kernel<TM, TN, R, EPI, YBF16>;
+    static size_t attr = 0;
+    if (lds > attr) {
+        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
+            (void) hipGetLastError();
+        attr = lds;
+    }
+    const int begin1 = (tm0 * tn0 * S0 + 7) & ~7;
+    launch_kernel(kern, dim3(begin1 + tm1 * tn1 * S1), dim3(256), lds, s, p0, p1, tm0, tn0, tm1, tn1, begin1);
+    return hipGetLastError();
+}
+
+template <int TM, int TN, int R, bool YBF16>
+hipError_t q8c_epi_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t s) {
+    switch (p0.epi) {
+        case EPI_GELU: return q8c_launch_pair<TM, TN, R, EPI_GELU, YBF16>(p0, p1, s);
+        case EPI_GATE_RES: return q8c_launch_pair<TM, TN, R, EPI_GATE_RES, false>(p0, p1, s);
+        case EPI_GELU_Q8: return q8c_launch_pair<TM, TN, R, EPI_GELU_Q8, false>(p0, p1, s);
+        case EPI_STORE: return q8c_launch_pair<TM, TN, R, EPI_STORE, YBF16>(p0, p1, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int TM, int TN, int R, bool YBF16>
 hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
     switch (p.epi) {
@@ -783,6 +832,38 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
         }
     }
     return p.y_bf16 ? gemm_q8_epi<2, 2, 2, 2, true>(p, s) : gemm_q8_epi<2, 2, 2, 2, false>(p, s);
+}
+
+hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t s) {
+    // one launch when both problems take the cooperative tiles with the same
+    // epilogue, output type and split count (each output is still summed in
+    // the same order, whatever the tile shape or the launch it runs in);
+    // otherwise two launches
+    const Tuning &tu = tuning();
+    auto coop = [&](const GemmParams &p) {
+        const int S = p.splits > 1 ? p.splits : 1;
+        return p.K % (128 * S) == 0 && p.M % 16 == 0 && ((uintptr_t) p.qw & 15) == 0 && ((uintptr_t) p.qx & 15) == 0 &&
+               ((uintptr_t) p.dw & 7) == 0 && ((uintptr_t) p.dx & 15) == 0 && !tu.q8_old;
+    };
+    const bool pair = tu.q8_pair && coop(p0) && coop(p1) && p0.epi == p1.epi && p0.y_bf16 == p1.y_bf16 &&
+                      p0.splits == p1.splits && p0.epi != EPI_GEGLU;
+    if (pair) {
+        const int S = p0.splits > 1 ? p0.splits : 1;
+        // the single-problem checks of launch_gemm_q8, on each problem
+        for (const GemmParams *p : {&p0, &p1}) {
+            if (S > 1 && (p->epi != EPI_STORE || p->y_bf16 || p->part_stride < (int64_t) p->N * p->ld_y))
+                return hipErrorInvalidValue;
+            if (p->epi == EPI_GELU_Q8 && (S > 1 || p->y_bf16 || p->M % 64 || !p->yd || p->ld_y < p->M || p->ld_y % 4))
+                return hipErrorInvalidValue;
+        }
+        const int64_t tiles64 = (int64_t) ((p0.M + 63) / 64) * ((p0.N + 63) / 64) +
+                                (int64_t) ((p1.M + 63) / 64) * ((p1.N + 63) / 64);
+        const int cfg = tu.q8_cfg ? tu.q8_cfg : tiles64 * S < 512 ? 5 : 2;
+        if (cfg == 2) return p0.y_bf16 ? q8c_epi_pair<4, 4, 2, true>(p0, p1, s) : q8c_epi_pair<4, 4, 2, false>(p0, p1, s);
+        if (cfg == 5) return p0.y_bf16 ? q8c_epi_pair<2, 4, 2, true>(p0, p1, s) : q8c_epi_pair<2, 4, 2, false>(p0, p1, s);
+    }
+    hipError_t e = launch_gemm_q8(p0, s);
+    return e != hipSuccess ? e : launch_gemm_q8(p1, s);
 }
 
 hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K, int8_t *qx, float *dx,

@@ -61,6 +61,7 @@ void read_tuning() {
     Tuning t;
     t.q8_cfg = env_int("TSK_Q8_CFG", 0);
     t.q8_old = env_int("TSK_Q8_OLD", 0) != 0;
+    t.q8_pair = env_int("TSK_Q8_PAIR", 1) != 0;
     t.coop_cfg = env_int("TSK_COOP_CFG", 0);
     t.attn_cfg = env_int("TSK_ATTN_CFG", 0);
     t.dit_sched = env_int("TSK_DIT_SCHED", 1) != 0;

@@ -217,6 +217,9 @@ inline int64_t tiled_index(int64_t m, int64_t k, int64_t K) {
     return ((m / 16) * (K / 32) + k / 32) * 512 + ((m % 16) + 16 * ((k % 32) / 8)) * 8 + (k % 8);
 }
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s);
+// the same for two problems (a joint block's streams), in one launch when they
+// share the cooperative tile configuration (same epilogue, output type, splits)
+hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t s);
 // Activation quantization to planes for launch_gemm_q8 (ggml-cpu x86 rounding).
 // x rows of K (f32 or bf16, row stride ld_x elements); grp > 0 gathers output
 // row n from source row (n / grp) * gstride + n % grp.

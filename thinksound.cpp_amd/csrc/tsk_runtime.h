@@ -25,6 +25,7 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 // environment by tsk_init (every call re-reads them) and never on a launch:
 //   TSK_Q8_CFG    Q8_0 cooperative tile (2 = 64 x 64, 5 = 32 x 64; 0 = rule)
 //   TSK_Q8_OLD    1: the 2 x 2-wave Q8_0 kernel for every shape
+//   TSK_Q8_PAIR   0: the Q8_0 DiT's two streams as separate launches (A/B reference)
 //   TSK_COOP_CFG  cooperative BF16 tile of the C-ABI GEMMs (0 = rule)
 //   TSK_GEMM_CFG  DiT block GEMM tiles, one character per projection
 //   TSK_ATTN_CFG  DiT attention launch shape (10 * key ranges + query blocks)
@@ -34,6 +35,7 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
+    bool q8_pair = true;                  // a joint block's two Q8_0 projections in one launch
     int coop_cfg = 0;
     int gemm_cfg[4] = {0, 0, 0, 0};
     int attn_cfg = 0;
