@@ -864,8 +864,10 @@ int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
         }
         if ((rc = q8_launch(d, ps, ns, TSK_ROLE_QKV, fl, by, "qkv q8 gemm", st))) return rc;
     }
+    QkvScatter qs[2];
+    double rows = 0.0;
     for (int i = 0; i < ns; ++i) {
-        QkvScatter q;
+        QkvScatter &q = qs[i];
         memset(&q, 0, sizeof(q));
         q.qkv = d->qkv32 + r[i].row_off * 3 * H;
         q.ld = 3 * H;
@@ -876,11 +878,11 @@ int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
         q.nh = c.n_head; q.rows = B * r[i].S;
         q.eps = c.qk_eps;
         q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), as run_qkv
-        const double rows = (double) B * r[i].S;
-        Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * 3 * H, 12.0 * rows * 3 * H, st);
-        if ((rc = hipcheck(launch_qkv_scatter(q, st), "qkv scatter"))) return rc;
+        rows += (double) B * r[i].S;
     }
-    return TSK_OK;
+    // both streams of a joint block in one launch
+    Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * 3 * H, 12.0 * rows * 3 * H, st);
+    return hipcheck(ns == 2 ? launch_qkv_scatter2(qs[0], qs[1], st) : launch_qkv_scatter(qs[0], st), "qkv scatter");
 }
 
 // split-K partials of a Q8_0 projection into the stream's partial slices;
@@ -905,14 +907,29 @@ void q8_partials(const tsk_dit *d, GemmParams &p, StreamRun &r, int B, int split
 int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const int H = d->cfg.hidden;
     int rc;
-    for (int i = 0; i < ns; ++i) {
-        if (r[i].w->pre_only) continue;
-        Timed tm(d, TSK_ROLE_OTHER, 3.0 * B * r[i].S * H, 5.125 * B * r[i].S * H, st);
-        if ((rc = hipcheck(launch_quantize_rows_q8(d->o32 + (size_t) r[i].tok_off * H, 1, H, B * r[i].S, H,
-                                                   d->qx + r[i].row_off * H, d->dx + r[i].row_off * (H / 32), st,
-                                                   r[i].S, Ntot),
-                           "linear1 quantize")))
-            return rc;
+    {
+        // the attention output of every stream that has a linear1, as Q8_0 planes
+        // (one launch for a joint block's two streams)
+        QuantRows qr[2];
+        int nq = 0;
+        double rows = 0.0;
+        for (int i = 0; i < ns; ++i) {
+            if (r[i].w->pre_only) continue;
+            QuantRows &q = qr[nq++];
+            q.x = d->o32 + (size_t) r[i].tok_off * H; q.ld_x = H;
+            q.N = B * r[i].S; q.K = H;
+            q.qx = d->qx + r[i].row_off * H; q.dx = d->dx + r[i].row_off * (H / 32);
+            q.grp = r[i].S; q.gstride = Ntot;
+            rows += (double) q.N;
+        }
+        if (nq) {
+            Timed tm(d, TSK_ROLE_OTHER, 3.0 * rows * H, 5.125 * rows * H, st);
+            rc = hipcheck(nq == 2 ? launch_quantize_rows_q8_pair(qr[0], qr[1], st)
+                                  : launch_quantize_rows_q8(qr[0].x, 1, qr[0].ld_x, qr[0].N, qr[0].K, qr[0].qx, qr[0].dx,
+                                                            st, qr[0].grp, qr[0].gstride),
+                          "linear1 quantize");
+            if (rc) return rc;
+        }
     }
     GemmParams ps[2];
     int n = 0;

@@ -636,12 +636,11 @@ __global__ __launch_bounds__(256) void gemm_q8c_pair_kernel(const GemmParams p0,
 // Row n of the output reads source row (n / grp) * gstride + n % grp (grp
 // > 0: rows gathered from a grouped layout, e.g. one stream's tokens of every
 // batch item in [B][Ntot] rows), else row n.
+// one 32-element block blk of rows from x (see quantize_rows_q8_kernel)
 template <bool XF32>
-__global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int K, int8_t *qx, float *dx, int grp,
-                                        int64_t gstride) {
+__device__ __forceinline__ void quantize_block_q8(const void *x, int64_t ld_x, int K, int8_t *qx, float *dx, int grp,
+                                                  int64_t gstride, const int64_t blk) {
     const int KB = K / 32;
-    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (blk >= (int64_t) N * KB) return;
     const int row = (int) (blk / KB), kb = (int) (blk % KB);
     const int64_t src = grp > 0 ? (int64_t) (row / grp) * gstride + row % grp : row;
     float v[32];
@@ -665,6 +664,22 @@ __global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int 
     int8_t *o = qx + (int64_t) row * K + kb * 32;
     *(u32x4 *) o = *(const u32x4 *) q;
     *(u32x4 *) (o + 16) = *(const u32x4 *) (q + 16);
+}
+
+template <bool XF32>
+__global__ void quantize_rows_q8_kernel(const void *x, int64_t ld_x, int N, int K, int8_t *qx, float *dx, int grp,
+                                        int64_t gstride) {
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk < (int64_t) N * (K / 32)) quantize_block_q8<XF32>(x, ld_x, K, qx, dx, grp, gstride, blk);
+}
+
+// two row sets (two streams) in one launch: blocks from N0 * K / 32 on quantize set 1
+__global__ void quantize_rows_q8_pair_kernel(const QuantRows r0, const QuantRows r1) {
+    const int64_t blk = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n0 = (int64_t) r0.N * (r0.K / 32);
+    if (blk < n0) quantize_block_q8<true>(r0.x, r0.ld_x, r0.K, r0.qx, r0.dx, r0.grp, r0.gstride, blk);
+    else if (blk - n0 < (int64_t) r1.N * (r1.K / 32))
+        quantize_block_q8<true>(r1.x, r1.ld_x, r1.K, r1.qx, r1.dx, r1.grp, r1.gstride, blk - n0);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -864,6 +879,14 @@ hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipSt
     }
     hipError_t e = launch_gemm_q8(p0, s);
     return e != hipSuccess ? e : launch_gemm_q8(p1, s);
+}
+
+hipError_t launch_quantize_rows_q8_pair(const QuantRows &r0, const QuantRows &r1, hipStream_t s) {
+    for (const QuantRows *r : {&r0, &r1})
+        if (r->N < 1 || r->K < 32 || r->K % 32) return hipErrorInvalidValue;
+    const int64_t nblk = (int64_t) r0.N * (r0.K / 32) + (int64_t) r1.N * (r1.K / 32);
+    launch_kernel(quantize_rows_q8_pair_kernel, dim3((unsigned) ((nblk + 255) / 256)), dim3(256), 0, s, r0, r1);
+    return hipGetLastError();
 }
 
 hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K, int8_t *qx, float *dx,

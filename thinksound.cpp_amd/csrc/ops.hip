@@ -939,9 +939,8 @@ __global__ void transpose_ct_kernel(const float *x, int B, int C, int T, float *
 }
 
 // one wave per (row, head): lane d holds dimension d of q, k and v
-__global__ __launch_bounds__(256) void qkv_scatter_kernel(const QkvScatter p) {
-    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w >= (int64_t) p.rows * p.nh) return;
+// wave w of stream p: token w / nh, head w % nh
+__device__ __forceinline__ void qkv_scatter_wave(const QkvScatter &p, const int64_t w) {
     const int lane = threadIdx.x & 63;
     const int n = (int) (w / p.nh), h = (int) (w % p.nh);
     const int H = p.nh * 64, b = n / p.seq, s = n % p.seq, tok = p.tok_off + s;
@@ -970,10 +969,30 @@ __global__ __launch_bounds__(256) void qkv_scatter_kernel(const QkvScatter p) {
     p.vt[(bh * 64 + lane) * p.ldv + vt_pos(tok)] = f32_to_f16_bits(x[2]);
 }
 
+__global__ __launch_bounds__(256) void qkv_scatter_kernel(const QkvScatter p) {
+    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w < (int64_t) p.rows * p.nh) qkv_scatter_wave(p, w);
+}
+
+// two streams in one launch: waves from p0.rows * p0.nh on run p1
+__global__ __launch_bounds__(256) void qkv_scatter2_kernel(const QkvScatter p0, const QkvScatter p1) {
+    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6), w0 = (int64_t) p0.rows * p0.nh;
+    if (w < w0) qkv_scatter_wave(p0, w);
+    else if (w - w0 < (int64_t) p1.rows * p1.nh) qkv_scatter_wave(p1, w - w0);
+}
+
 hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s) {
     if (p.rows < 1 || p.nh < 1 || p.seq < 1) return hipErrorInvalidValue;
     const int64_t waves = (int64_t) p.rows * p.nh;
     launch_kernel(qkv_scatter_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_scatter2(const QkvScatter &p0, const QkvScatter &p1, hipStream_t s) {
+    for (const QkvScatter *p : {&p0, &p1})
+        if (p->rows < 1 || p->nh < 1 || p->seq < 1) return hipErrorInvalidValue;
+    const int64_t waves = (int64_t) p0.rows * p0.nh + (int64_t) p1.rows * p1.nh;
+    launch_kernel(qkv_scatter2_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, p0, p1);
     return hipGetLastError();
 }
 

@@ -225,6 +225,17 @@ hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipSt
 // row n from source row (n / grp) * gstride + n % grp.
 hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K,
                                    int8_t *qx, float *dx, hipStream_t s, int grp = 0, int64_t gstride = 0);
+// f32 rows of two streams quantized in one launch (each as launch_quantize_rows_q8)
+struct QuantRows {
+    const float *x;
+    int64_t ld_x;
+    int N, K;
+    int8_t *qx;
+    float *dx;
+    int grp;
+    int64_t gstride;
+};
+hipError_t launch_quantize_rows_q8_pair(const QuantRows &r0, const QuantRows &r1, hipStream_t s);
 // The QKV epilogue of the BF16 block GEMMs as a kernel over f32 rows (the
 // Q8_0 driver's QKV GEMM stores them): row n = b * seq + s of qkv [rows][3 H]
 // ([q | k | v] head-major, bias included) -> RMSNorm(eps) * w on q and k,
@@ -240,6 +251,8 @@ struct QkvScatter {
     float eps, q_scale;
 };
 hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s);
+// two streams' scatters in one launch
+hipError_t launch_qkv_scatter2(const QkvScatter &p0, const QkvScatter &p1, hipStream_t s);
 
 // ---------------------------------------------------------------- small ops
 // generic 4-D strided views used by the C-ABI element-wise entry points
