@@ -195,6 +195,78 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const uint16_t *kb = gb + buf * TILE_H;
         const uint16_t *vb = kb + KT * 64;
         const int nbuf_next = buf + (NB - 1) >= NB ? buf - 1 : buf + (NB - 1);   // (buf + NB - 1) % NB
+        if constexpr (BOUNDED && !KBF16) {
+          if (tile < tend) {
+            // Bounded logits (no running max): the first 32 keys' K . Q^T, then
+            // the second 32 keys' products issued in the same scheduling region
+            // as the first half's exponentials and P . V, so that a wave's
+            // MFMAs and VALU work overlap; V^T fragments are read per half.
+            // The same operations in the same order per output as below.
+            u32x4 ka[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) ka[ks] = *(const u32x4 *) (kb + swz(l32, 2 * ks + hi));
+            if (tile + NB - 1 < tend) issue(tile + NB - 1, nbuf_next);
+            f32x16 s0, s1;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s0[e] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ka[ks]),
+                                                           __builtin_bit_cast(f16x8, qraw[ks]), s0, 0, 0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) ka[ks] = *(const u32x4 *) (kb + swz(32 + l32, 2 * ks + hi));
+            const int lim = tile == ntiles - 1 ? p.Nkv - tile * KT : KT;
+            auto mask = [&](f32x16 &sv, int mb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (32 * mb + 8 * (e >> 2) + 4 * hi + (e & 3) >= lim) sv[e] = -INFINITY;
+            };
+            auto softmax_pv = [&](const f32x16 &sv, const f16x8 (&va)[2][2]) {
+                f16x8 pf[2];
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) pf[h2][t] = (_Float16) __builtin_amdgcn_exp2f(sv[8 * h2 + t]);
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) {
+                        const f16x2 pr = {pf[h2][t], pf[h2][t + 1]};
+                        l_run = __builtin_amdgcn_fdot2(pr, one, l_run, false);
+                    }
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2)
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][h2], pf[h2], o[db], 0, 0, 0);
+            };
+            if (lim < KT) mask(s0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s1[e] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, ka[ks]),
+                                                           __builtin_bit_cast(f16x8, qraw[ks]), s1, 0, 0, 0);
+            {
+                f16x8 va[2][2];
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2) va[db][h2] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * h2 + hi));
+                softmax_pv(s0, va);
+            }
+            if (lim < KT) mask(s1, 1);
+            {
+                f16x8 va[2][2];
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2)
+                        va[db][h2] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * (2 + h2) + hi));
+                softmax_pv(s1, va);
+            }
+          }
+        } else
         if (tile < tend) {
             // K fragments of this tile first, then the loads NB - 1 tiles ahead
             // (into another buffer); the V^T fragments are read after the
