@@ -276,42 +276,6 @@ def t5_bench(tsk, seed=44, reps=3):
             "tops": round(per_layer * c.n_layers / wall / 1e12, 1)}
 
 
-def graph_weights(tensors, seed=1234, std=0.02):
-    """(name, array) of random-init weights for the reference graph's 1.28 G parameters: every
-    matrix a window (at a seeded offset, wrapping) of one pool of 2^24 N(0, std)
-    values rounded to bf16, vectors N(0, std) (q/k norm weights 1 + N(0, std)),
-    the learned empties N(0, 1) -- drawing 1.28 G fresh normals would take
-    minutes on the host and changes nothing a timing can see"""
-    import numpy as np
-
-    def window(pool, off, n):
-        w = np.empty(n, np.float32)
-        i = 0
-        while i < n:
-            k = min(n - i, pool.size - off)
-            w[i:i + k] = pool[off:off + k]
-            i, off = i + k, 0
-        return w
-    rng = np.random.default_rng(seed)
-    pool = (rng.standard_normal(1 << 24, dtype=np.float32) * np.float32(std)).view(np.uint32)
-    pool = ((pool + np.uint32(0x7FFF) + ((pool >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000))
-    pool = pool.view(np.float32)
-    for name, ne, ty in tensors:
-        shape = tuple(int(x) for x in reversed(ne))
-        while len(shape) > 1 and shape[0] == 1:
-            shape = shape[1:]
-        n = int(np.prod(shape))
-        if name.startswith("empty_"):
-            w = rng.standard_normal(n, dtype=np.float32)
-        elif len(shape) == 1:
-            w = rng.standard_normal(n, dtype=np.float32) * np.float32(std)
-            if name.endswith("norm.weight"):
-                w += np.float32(1.0)
-        else:
-            w = window(pool, int(rng.integers(0, pool.size)), n)
-        yield name, w.reshape(shape)
-
-
 def graph_bench(tsk, steps, warmup=3):
     """the reference's own MM-DiT graph (tsk_mmdit: latent | clip | text
     streams, k3 conv linear1 / convMLP, SwiGLU MLPs of 2816, per-token
@@ -321,7 +285,7 @@ def graph_bench(tsk, steps, warmup=3):
     `steps` forwards; plus the 24-step CFG-5 sampler at 30 s (wall clock)"""
     import numpy as np
     m = tsk.MMDit(tsk.mmdit_config())
-    for k, v in graph_weights(m.tensors()):
+    for k, v in tsk.mmdit_pool_weights(m.tensors()):
         m.set_tensor(k, v)
     rng = np.random.default_rng(4242)
     out = {}

@@ -546,11 +546,21 @@ int  tsk_dit_timing_read(tsk_dit *dit, int role, double *ms, int64_t *launches,
  * features interpolated to T plus global_c) on the latent stream and from
  * global_c on clip / text, a 154-token text stream (text_f padded to t5_dim
  * and concatenated with the T5 features), a k7 output convolution. Weights
- * by the converter's names (convert/convert_thinksound.py:32) in the types of
- * the BF16 GGUF (convert/quantize_gguf.py --type bf16): BF16 2-D / 3-D
- * weights, F32 for the t_embed MLP, sync_pos_emb, the learned empties and
- * every vector. Each BF16 product rounds its input to bf16 (ggml_mul_mat's
- * src1 conversion); K / V are F16 in the attention (mmdit.cpp:89-90). */
+ * by the converter's names (convert/convert_thinksound.py:32), each held in
+ * one type and multiplied with ggml_mul_mat's semantics for it (src1
+ * converted to the weight's vec_dot type): BF16 (input rounded to bf16),
+ * F32, or Q8_0 (input quantized per 32 values, exact int32 block sums).
+ * tsk_mmdit_create takes the types from cfg->weight_type, as the converters
+ * write the files: TSK_TYPE_BF16 (convert/quantize_gguf.py --type bf16: BF16
+ * linears and convolutions, the t_embed MLP F32), TSK_TYPE_Q8_0
+ * (quantize_gguf.py, :9-15: 2-D linears with ne0 % 32 == 0 Q8_0, the 3-D
+ * convolution kernels and "_emb" / "norm" / "empty" names F32) or
+ * TSK_TYPE_F32 (the F32 GGUF); tsk_mmdit_create_from_gguf takes each
+ * tensor's type from the file. sync_pos_emb, the learned empties and every
+ * vector are F32. K / V are F16 in the attention (mmdit.cpp:89-90).
+ * A model handles one call at a time, in its stream's order: it owns its
+ * activations, staging and sampler state, so calls on one model from two
+ * streams race; callers that need concurrency create a model per stream. */
 typedef struct tsk_mmdit tsk_mmdit;
 
 typedef struct tsk_mmdit_config {
@@ -571,6 +581,8 @@ typedef struct tsk_mmdit_config {
     int   max_sync;      /* capacity: sync frames (multiple of 8) */
     float rope_theta;    /* 10000 */
     float t_max_period;  /* 1     */
+    int   weight_type;   /* TSK_TYPE_BF16 (default), TSK_TYPE_Q8_0 or TSK_TYPE_F32: the
+                            converters' storage rule tsk_mmdit_create applies */
 } tsk_mmdit_config;
 
 /* the reference's sizes (mmdit.h:17-22) and capacities for 30 s clips */
@@ -580,11 +592,27 @@ void tsk_mmdit_destroy(tsk_mmdit *m);
 int  tsk_mmdit_n_tensors(const tsk_mmdit *m);
 /* name and ggml ne of tensor i: linear [in, out], conv [KW, IC, OC] */
 int  tsk_mmdit_tensor_info(const tsk_mmdit *m, int i, const char **name, int64_t ne[4]);
-/* the type the driver holds tensor i in: TSK_TYPE_BF16 or TSK_TYPE_F32 */
+/* the type the model holds tensor i in: TSK_TYPE_BF16, TSK_TYPE_F32 or TSK_TYPE_Q8_0 */
 int  tsk_mmdit_tensor_type(const tsk_mmdit *m, int i);
 /* Upload one weight from HOST f32 values in ggml / PyTorch memory order
- * (linear [out][in], conv [OC][IC][KW]); BF16 tensors are rounded RNE. */
+ * (linear [out][in], conv [OC][IC][KW]); BF16 tensors are rounded RNE, Q8_0
+ * tensors quantized with ggml's reference quantizer (quantize_row_q8_0_ref). */
 int  tsk_mmdit_set_tensor(tsk_mmdit *m, const char *name, const float *host_f32, int64_t n);
+/* Upload a Q8_0 tensor's blocks {fp16 d; int8 qs[32]} bit for bit (HOST,
+ * rows in the file's order: ne[1] rows of ne[0] / 32 blocks). */
+int  tsk_mmdit_set_tensor_q8_0(tsk_mmdit *m, const char *name, const void *blocks, size_t nbytes);
+/* ts_dit::load (src/mmdit.cpp:104-116; ts_model::load_backend,
+ * src/common/ts_model.cpp:13-41). tsk_mmdit_config_from_gguf reads the model
+ * sizes from the dit.* keys of convert/convert_thinksound.py:38-45 (absent
+ * keys keep *cfg's values), the SwiGLU width from audio_input_proj.2.w1, and
+ * sets weight_type to the file's (Q8_0 if any tensor is Q8_0); capacities
+ * stay the caller's. tsk_mmdit_create_from_gguf creates a model holding
+ * every tensor in its file type (F32, BF16 or Q8_0; F16 matrices are
+ * refused) and loads it. tsk_mmdit_load_gguf loads a file into a model whose
+ * types it matches: Q8_0 blocks bit for bit, other types by value. */
+int  tsk_mmdit_config_from_gguf(const tsk_gguf *g, tsk_mmdit_config *cfg);
+int  tsk_mmdit_create_from_gguf(const tsk_gguf *g, const tsk_mmdit_config *cfg, tsk_mmdit **out);
+int  tsk_mmdit_load_gguf(tsk_mmdit *m, const tsk_gguf *g);
 /*
  * One flow evaluation for B (<= max_batch) rows, all pointers HOST, each
  * per-row block in the layout ts_dit::forward takes (src/mmdit.h:26-29,
@@ -622,7 +650,10 @@ int     tsk_mmdit_debug_get(const tsk_mmdit *m, const char *name, float *out, in
  * forward (empty_string_feat, empty_t5_feat, zero global text) as one B = 2
  * forward. HOST pointers in ts_dit::sample's layouts: noise / out ne =
  * [T, latent_dim]; flow0 (nullable) ne = [T, latent_dim], the CFG velocity of
- * step 0. Needs max_batch >= 2.
+ * step 0. Needs max_batch >= 2. The conditioning that does not depend on t
+ * is computed once per call; the latent stays on the device between steps
+ * and the CFG / Euler update runs there in the reference's rounding (the
+ * same bits as a host loop over tsk_mmdit_forward).
  */
 int  tsk_mmdit_sample(tsk_mmdit *m, int T, const float *noise, int clip_S, const float *clip_f, int sync_S,
                       const float *sync_f, const float *text_f, const float *t5, const float *global_text,

@@ -47,7 +47,7 @@ class MMDitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
         "sync_dim", "t5_dim", "mlp_hidden", "max_batch", "max_latent", "max_clip", "max_sync")] + \
-        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")]
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")] + [("weight_type", ctypes.c_int)]
 
 
 _lib = None
@@ -127,6 +127,8 @@ def lib():
         L.orc_mmdit_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
                                             ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int)]
         L.orc_mmdit_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_int64]
+        L.orc_mmdit_set_tensor_q8_0.argtypes = [vp, ctypes.c_char_p, vp, ctypes.c_size_t]
+        L.orc_mmdit_set_type.argtypes = [vp, ctypes.c_char_p, ctypes.c_int]
         L.orc_mmdit_forward.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp, ctypes.c_int, vp,
                                         vp, vp, vp, vp, ctypes.c_int, ctypes.c_int]
         L.orc_vae_create.argtypes = [ctypes.POINTER(VaeConfig)]
@@ -451,7 +453,7 @@ def mmdit_config(**kw):
     """the reference's sizes (src/mmdit.h:17-22) with capacities for 30 s"""
     c = MMDitConfig(hidden=1024, n_head=16, head_dim=64, depth=21, fused_depth=14, latent_dim=64, text_seq=77,
                     clip_dim=1024, sync_dim=768, t5_dim=2048, mlp_hidden=2816, max_batch=2, max_latent=646,
-                    max_clip=240, max_sync=720, rope_theta=10000.0, t_max_period=1.0)
+                    max_clip=240, max_sync=720, rope_theta=10000.0, t_max_period=1.0, weight_type=BF16)
     for k_, v_ in kw.items():
         setattr(c, k_, v_)
     return c
@@ -484,6 +486,16 @@ class OracleMMDiT:
     def set_tensor(self, name, arr):
         arr = np.ascontiguousarray(arr, dtype=np.float32)
         rc = lib().orc_mmdit_set_tensor(self.h, name.encode(), arr.ctypes.data, arr.size)
+        assert rc == 0, (name, rc)
+
+    def set_tensor_q8_0(self, name, blocks):
+        """Q8_0 blocks (bytes / uint8 array) as a GGUF file holds them"""
+        b = np.ascontiguousarray(np.frombuffer(bytes(blocks), np.uint8))
+        rc = lib().orc_mmdit_set_tensor_q8_0(self.h, name.encode(), b.ctypes.data, b.size)
+        assert rc == 0, (name, rc)
+
+    def set_type(self, name, type_id):
+        rc = lib().orc_mmdit_set_type(self.h, name.encode(), int(type_id))
         assert rc == 0, (name, rc)
 
     @staticmethod

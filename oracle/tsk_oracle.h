@@ -109,16 +109,20 @@ int      orc_dit_sample(orc_dit *d, int T, const float *noise, const float *text
 
 /* ---- The reference's MM-DiT graph (ts_dit::forward / ::sample,
  * src/mmdit.cpp:119-376), tsk_oracle_mmdit.c --------------------------------
- * Weights by the converter's names from host f32 in ggml order; matrices are
- * BF16 when act_bf16 (ggml_mul_mat rounds src1), else F32; the t_embed MLP
- * and every vector F32. kv_f16 casts K / V to F16 (mmdit.cpp:89-90). Layouts
- * as tsk_mmdit_forward / tsk_mmdit_sample. */
+ * Weights by the converter's names from host f32 in ggml order (or Q8_0
+ * blocks), each stored in the type cfg->weight_type's converter rule gives it
+ * (orc_mmdit_set_type overrides one); with act_bf16 the products run in the
+ * stored types (BF16: src1 rounded; Q8_0: src1 quantized), else all in F32 on
+ * the same values. kv_f16 casts K / V to F16 (mmdit.cpp:89-90). Layouts as
+ * tsk_mmdit_forward / tsk_mmdit_sample. */
 typedef struct orc_mmdit orc_mmdit;
 orc_mmdit *orc_mmdit_create(const tsk_mmdit_config *cfg);
 void     orc_mmdit_destroy(orc_mmdit *m);
 int      orc_mmdit_n_tensors(const orc_mmdit *m);
 int      orc_mmdit_tensor_info(const orc_mmdit *m, int i, const char **name, int64_t ne[3], int *type);
 int      orc_mmdit_set_tensor(orc_mmdit *m, const char *name, const float *src, int64_t n);
+int      orc_mmdit_set_tensor_q8_0(orc_mmdit *m, const char *name, const void *blocks, size_t nbytes);
+int      orc_mmdit_set_type(orc_mmdit *m, const char *name, int type);
 int      orc_mmdit_forward(orc_mmdit *m, int B, int T, const float *latent, const float *t, int clip_S,
                            const float *clip_f, int sync_S, const float *sync_f, const float *text_f,
                            const float *t5, const float *global_text, float *flow, int act_bf16, int kv_f16);

@@ -16,9 +16,16 @@
  *   blocks, final layer                                              :203-289
  *   sampler: v = u + cfg (c - u), x += dt v                          :344-376
  *
- * Matrix weights are BF16 (ggml_mul_mat rounds its src1 to bf16) when
- * act_bf16, else F32 (the "GGML F32 path"); the t_embed MLP is F32 either
- * way (the BF16 GGUF keeps "_emb" names F32, convert/quantize_gguf.py:11-14).
+ * Each weight has a stored type, as the converters write the files
+ * (convert/quantize_gguf.py:9-15): under weight_type BF16 every matrix is
+ * BF16 but the t_embed MLP ("_emb" names) F32; under Q8_0 the 2-D linears
+ * with ne0 % 32 == 0 and no "_emb" / "norm" / "empty" in their names are
+ * Q8_0 and the convolutions F32; under F32 all are F32 (orc_mmdit_set_type
+ * overrides one tensor's type, as a GGUF file may). With act_bf16 the
+ * products run in the stored types (ggml_mul_mat converts its src1 to the
+ * weight's vec_dot type: bf16 rounding, Q8_0 quantization); without, every
+ * product is F32 on the same weight values (the "GGML F32 path"; a Q8_0
+ * weight as its dequantized values).
  */
 #include <math.h>
 #include <stdio.h>
@@ -32,9 +39,10 @@ enum { MK_LIN = 0, MK_CONV = 1, MK_VEC = 2 };
 typedef struct {
     char name[200];
     int64_t ne[3];
-    int kind, f32only;
-    float *data;       /* f32 values in ggml order */
+    int kind, type;    /* type: TSK_TYPE_F32 / BF16 / Q8_0 as stored */
+    float *data;       /* f32 values in ggml order (a Q8_0 tensor's dequantized values) */
     uint16_t *bf;      /* bf16 copy of a BF16 matrix */
+    uint8_t *q8;       /* Q8_0 blocks of a Q8_0 matrix, ne[1] rows of ne[0] / 32 */
 } mw;
 
 /* stage outputs of the last forward, concatenated over its batch rows (the
@@ -86,6 +94,28 @@ int orc_mmdit_stage(const orc_mmdit *m, const char *name, float *out, int64_t n)
     return TSK_ERR_INVALID_ARG;
 }
 
+/* the stored type of a weight under a model-wide weight type (the
+ * converters' rule, convert/quantize_gguf.py:9-15) */
+static int rule_type(int wt, const mw *x) {
+    if (x->kind == MK_VEC || wt == TSK_TYPE_F32) return TSK_TYPE_F32;
+    const int emb = strstr(x->name, "_emb") != NULL;
+    if (wt == TSK_TYPE_BF16) return emb ? TSK_TYPE_F32 : TSK_TYPE_BF16;
+    if (x->kind == MK_CONV || emb || strstr(x->name, "norm") || strstr(x->name, "empty") || x->ne[0] % 32)
+        return TSK_TYPE_F32;
+    return TSK_TYPE_Q8_0;
+}
+
+static int64_t nel(const mw *x) { return x->ne[0] * x->ne[1] * x->ne[2]; }
+
+/* (re)allocate the typed copy of a weight */
+static void set_type(mw *x, int type) {
+    free(x->bf); free(x->q8);
+    x->bf = NULL; x->q8 = NULL;
+    x->type = type;
+    if (type == TSK_TYPE_BF16) x->bf = (uint16_t *) calloc((size_t) nel(x), sizeof(uint16_t));
+    if (type == TSK_TYPE_Q8_0) x->q8 = (uint8_t *) calloc((size_t) (nel(x) / 32), 34);
+}
+
 static void addw(orc_mmdit *m, const char *name, int64_t a, int64_t b, int64_t c, int kind) {
     if (m->nw == m->capw) {
         m->capw = m->capw ? 2 * m->capw : 128;
@@ -96,9 +126,8 @@ static void addw(orc_mmdit *m, const char *name, int64_t a, int64_t b, int64_t c
     snprintf(x->name, sizeof(x->name), "%s", name);
     x->ne[0] = a; x->ne[1] = b; x->ne[2] = c;
     x->kind = kind;
-    x->f32only = kind == MK_VEC || strstr(name, "_emb") != NULL;
     x->data = (float *) calloc((size_t) (a * b * c), sizeof(float));
-    if (!x->f32only) x->bf = (uint16_t *) calloc((size_t) (a * b * c), sizeof(uint16_t));
+    set_type(x, rule_type(m->cfg.weight_type, x));
 }
 
 static void add_lin(orc_mmdit *m, const char *p, int in, int out, int bias) {
@@ -182,7 +211,7 @@ orc_mmdit *orc_mmdit_create(const tsk_mmdit_config *cfg) {
 
 void orc_mmdit_destroy(orc_mmdit *m) {
     if (!m) return;
-    for (int i = 0; i < m->nw; ++i) { free(m->w[i].data); free(m->w[i].bf); }
+    for (int i = 0; i < m->nw; ++i) { free(m->w[i].data); free(m->w[i].bf); free(m->w[i].q8); }
     stage_reset(m);
     free(m->w);
     free(m);
@@ -194,7 +223,7 @@ int orc_mmdit_tensor_info(const orc_mmdit *m, int i, const char **name, int64_t 
     if (i < 0 || i >= m->nw) return TSK_ERR_INVALID_ARG;
     *name = m->w[i].name;
     for (int j = 0; j < 3; ++j) ne[j] = m->w[i].ne[j];
-    *type = m->w[i].f32only ? TSK_TYPE_F32 : TSK_TYPE_BF16;
+    *type = m->w[i].type;
     return TSK_OK;
 }
 
@@ -204,16 +233,48 @@ static mw *find_w(orc_mmdit *m, const char *name) {
     abort();
 }
 
+static mw *lookup(orc_mmdit *m, const char *name) {
+    for (int i = 0; i < m->nw; ++i) if (!strcmp(m->w[i].name, name)) return &m->w[i];
+    return NULL;
+}
+
+/* f32 values; a Q8_0 tensor is quantized with ggml's reference quantizer
+ * (quantize_row_q8_0_ref) and keeps its dequantized values as data */
 int orc_mmdit_set_tensor(orc_mmdit *m, const char *name, const float *src, int64_t n) {
-    for (int i = 0; i < m->nw; ++i) {
-        mw *x = &m->w[i];
-        if (strcmp(x->name, name)) continue;
-        if (n != x->ne[0] * x->ne[1] * x->ne[2]) return TSK_ERR_SHAPE;
-        memcpy(x->data, src, sizeof(float) * (size_t) n);
-        if (x->bf) orc_fp32_to_bf16_row(src, x->bf, n);
+    mw *x = lookup(m, name);
+    if (!x) return TSK_ERR_INVALID_ARG;
+    if (n != nel(x)) return TSK_ERR_SHAPE;
+    if (x->type == TSK_TYPE_Q8_0) {
+        orc_quantize_q8_0(src, x->q8, n, ORC_Q8_CPU_REF);
+        orc_dequantize_q8_0(x->q8, x->data, n);
         return TSK_OK;
     }
-    return TSK_ERR_INVALID_ARG;
+    memcpy(x->data, src, sizeof(float) * (size_t) n);
+    if (x->bf) orc_fp32_to_bf16_row(src, x->bf, n);
+    return TSK_OK;
+}
+
+/* Q8_0 blocks as a GGUF file holds them */
+int orc_mmdit_set_tensor_q8_0(orc_mmdit *m, const char *name, const void *blocks, size_t nbytes) {
+    mw *x = lookup(m, name);
+    if (!x) return TSK_ERR_INVALID_ARG;
+    if (x->type != TSK_TYPE_Q8_0) return TSK_ERR_TYPE;
+    if (nbytes != (size_t) (nel(x) / 32) * 34) return TSK_ERR_SHAPE;
+    memcpy(x->q8, blocks, nbytes);
+    orc_dequantize_q8_0(x->q8, x->data, nel(x));
+    return TSK_OK;
+}
+
+/* the stored type of one weight (F32 for vectors; Q8_0 for 2-D weights with
+ * ne0 % 32 == 0 only) */
+int orc_mmdit_set_type(orc_mmdit *m, const char *name, int type) {
+    mw *x = lookup(m, name);
+    if (!x) return TSK_ERR_INVALID_ARG;
+    const int ok = type == TSK_TYPE_F32 || (x->kind != MK_VEC && type == TSK_TYPE_BF16) ||
+                   (x->kind == MK_LIN && type == TSK_TYPE_Q8_0 && x->ne[0] % 32 == 0);
+    if (!ok) return TSK_ERR_TYPE;
+    set_type(x, type);
+    return TSK_OK;
 }
 
 /* ---- node helpers: activations are ggml [C, S] (C fastest), contiguous */
@@ -223,10 +284,16 @@ static tsk_tensor act(float *p, int64_t C, int64_t S) {
     return t;
 }
 
-/* a weight as ggml holds it: BF16 when act_bf16 (and not kept F32), else F32 */
+/* a weight as ggml holds it: its stored type when act_bf16, else F32 */
 static tsk_tensor wten(orc_mmdit *m, const char *name, int act_bf16) {
     mw *x = find_w(m, name);
-    const int bf = act_bf16 && x->bf;
+    if (act_bf16 && x->type == TSK_TYPE_Q8_0) {
+        const size_t row = (size_t) (x->ne[0] / 32) * 34;
+        tsk_tensor t = { TSK_TYPE_Q8_0, {x->ne[0], x->ne[1], x->ne[2], 1},
+                         {34, row, row * (size_t) x->ne[1], row * (size_t) (x->ne[1] * x->ne[2])}, x->q8 };
+        return t;
+    }
+    const int bf = act_bf16 && x->type == TSK_TYPE_BF16;
     const size_t es = bf ? 2 : 4;
     tsk_tensor t = { bf ? TSK_TYPE_BF16 : TSK_TYPE_F32, {x->ne[0], x->ne[1], x->ne[2], 1},
                      {es, es * (size_t) x->ne[0], es * (size_t) (x->ne[0] * x->ne[1]),

@@ -93,6 +93,45 @@ def test_config2_flow_step(env):
     dit.close()
 
 
+def test_config2_unbounded_attention(env):
+    """config 2 (21 blocks, T = 194, CFG batch 2) with every q / k RMSNorm
+    weight scaled by 2.5 (2.5 + N(0, 0.05), as trained norm weights may be):
+    then 64 max|w_q| max|w_k| / 8 ~ 53 bounds the logits, beyond the
+    14 / log2(e) ~ 9.7 under which the attention runs without a running max,
+    so every attention launch of the step takes the running-max kernel with
+    far sharper softmax rows. Held to max(2e-3, 2 x the oracle's own change
+    when its K / V are F32 instead of F16) against the oracle with the
+    device's precision policy; the distance from the F32 path is printed."""
+    tsk, orc = env
+    cfg = tsk.dit_config()
+    dit = tsk.Dit(cfg)
+    od = orc.OracleDiT(orc.dit_config())
+    names = dit.tensors()
+    W = tsk.synthetic_weights(names, seed=1234)
+    scaled = 0
+    for k, v in W.items():
+        if k.endswith("norm.weight"):
+            v = v * np.float32(2.5)
+            scaled += 1
+        dit.set_tensor(k, v)
+        od.set_tensor(k, v)
+    assert scaled == 2 * (2 * (cfg.depth - cfg.fused_depth) + cfg.fused_depth)
+    # the launcher's test: 1.01 * 64 * log2(e) / 8 * max|w_q| * max|w_k| <= 14
+    amax = max(float(np.abs(v).max()) * 2.5 for k, v in W.items() if k.endswith("norm.weight"))
+    assert 1.01 * 64 * 1.4426950408889634 / 8 * amax * amax > 14.0
+    lat, t, txt = inputs(2, 194, seed=17)
+    f = dit.forward(cm(lat), t, txt)
+    ref = od.forward(lat, t, txt, act_bf16=True, kv_f16=True)
+    floor = rel_l2(od.forward(lat, t, txt, act_bf16=True, kv_f16=False), ref)
+    e32 = rel_l2(f, od.forward(lat, t, txt, act_bf16=False, kv_f16=True))
+    e = rel_l2(f, ref)
+    print(f"config 2, unbounded attention: rel-L2 {e:.3e} vs the policy-matched oracle (its K/V F16-vs-F32 "
+          f"change {floor:.3e}), {e32:.3e} vs the F32 path", flush=True)
+    assert np.isfinite(f).all()
+    assert e <= max(2e-3, 2 * floor)
+    dit.close()
+
+
 @pytest.mark.parametrize("T", [400, 646])
 def test_full_forward_longer_latents(env, T):
     """Every block GEMM tile shape and attention launch shape of the longer

@@ -122,3 +122,65 @@ def test_mmdit_sample_matches_fp64_restatement(small):
     Wu = dict(W, empty_string_feat=text[0], empty_t5_feat=t5[0])
     wx, _ = refmath.mmdit_sample_ref(Wu, SMALL, lat[0], clip[0], sync[0], text[0], t5[0], g[0], 3, 5.0)
     assert rel_l2(x, wx) > 100 * TOL
+
+
+def test_q8_0_types_and_dequantized_f32_path(orc):
+    """weight_type Q8_0 (convert/quantize_gguf.py:9-15): the 2-D linears with
+    ne0 % 32 == 0 are held as Q8_0 (ggml's reference quantizer), the
+    convolutions, the t_embed MLP and every vector F32. The oracle's F32 path
+    then runs on the dequantized values: it matches the fp64 restatement fed
+    those values (pins the quantizer round trip and the inventory), and the
+    Q8_0 path -- the same weights with every Q8_0 product's input quantized
+    per 32 values (orc_mul_mat, pinned by brute force) -- differs from it by
+    the activation quantization only."""
+    od = orc.OracleMMDiT(orc.mmdit_config(**dict(SMALL, weight_type=orc.Q8_0)))
+    ty = {n: t for n, _, t in od.tensors()}
+    assert ty["joint_blocks.0.latent_block.attn.qkv.weight"] == orc.Q8_0
+    assert ty["text_input_proj.2.w2.weight"] == orc.Q8_0
+    assert ty["joint_blocks.0.latent_block.ffn.w1.weight"] == orc.F32
+    assert ty["t_embed.mlp.0.weight"] == orc.F32 and ty["empty_string_feat"] == orc.F32
+    W = weights(od.tensors(), 12)
+    Wq = {}
+    for k, v in W.items():
+        od.set_tensor(k, v)
+        if ty[k] == orc.Q8_0:
+            Wq[k] = orc.dequantize_q8_0(orc.quantize_q8_0(v, orc.Q8_CPU_REF)).reshape(v.shape)
+        else:
+            Wq[k] = v
+    lat, clip, sync, text, t5, g = inputs(1, 12, 5, 16, seed=7)
+    t = np.array([0.6], np.float32)
+    got = od.forward(lat, t, clip, sync, text, t5, g, act_bf16=False, kv_f16=False)[0]
+    ref = refmath.mmdit_forward_ref(Wq, SMALL, lat[0], 0.6, clip[0], sync[0], text[0], t5[0], g[0])
+    e = rel_l2(got, ref)
+    assert e <= TOL, e
+    # the undequantized weights are another model
+    assert rel_l2(got, refmath.mmdit_forward_ref(W, SMALL, lat[0], 0.6, clip[0], sync[0], text[0], t5[0],
+                                                 g[0])) > 100 * TOL
+    q = od.forward(lat, t, clip, sync, text, t5, g, act_bf16=True, kv_f16=False)[0]
+    eq = rel_l2(q, got)
+    print(f"Q8_0 oracle: F32 path on dequantized weights vs fp64 {e:.2e}; Q8_0 products vs F32 path {eq:.2e}")
+    assert 1e-4 < eq < 5e-2
+
+
+def test_q8_0_blocks_equal_quantized_values(orc):
+    """orc_mmdit_set_tensor_q8_0 with the blocks of ggml's reference
+    quantizer gives the bits of set_tensor on the f32 values; set_type makes
+    a single tensor Q8_0 (the converter's --quant q8_0 t_embed)"""
+    cfg = orc.mmdit_config(**dict(SMALL, weight_type=orc.Q8_0))
+    a, b = orc.OracleMMDiT(cfg), orc.OracleMMDiT(cfg)
+    for o in (a, b):
+        o.set_type("t_embed.mlp.0.weight", orc.Q8_0)
+    ty = {n: t for n, _, t in a.tensors()}
+    assert ty["t_embed.mlp.0.weight"] == orc.Q8_0
+    W = weights(a.tensors(), 13)
+    for k, v in W.items():
+        a.set_tensor(k, v)
+        if ty[k] == orc.Q8_0:
+            b.set_tensor_q8_0(k, orc.quantize_q8_0(v, orc.Q8_CPU_REF).tobytes())
+        else:
+            b.set_tensor(k, v)
+    lat, clip, sync, text, t5, g = inputs(1, 10, 5, 16, seed=8)
+    t = np.array([0.4], np.float32)
+    fa = a.forward(lat, t, clip, sync, text, t5, g)
+    assert np.array_equal(fa, b.forward(lat, t, clip, sync, text, t5, g))
+    assert np.isfinite(fa).all()

@@ -722,8 +722,11 @@ __global__ void timestep_embed_kernel(const float *freq, const TimeVals tv, int 
     temb[(int64_t) b * H + half + k] = sinf(a);
 }
 
+// v = u + (c - u) cfg, x += dt v with every product and sum rounded as the
+// reference's host loop writes them (src/mmdit.cpp:366-372): no FMA contraction
 __global__ void cfg_euler_kernel(const float *flow2, int64_t n, float cfg, float dt, float *x, float *x2,
                                  float *flow0) {
+#pragma clang fp contract(off)
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float fc = flow2[i], fu = flow2[n + i];

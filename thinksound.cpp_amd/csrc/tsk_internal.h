@@ -222,7 +222,8 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s);
 hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t s);
 // Activation quantization to planes for launch_gemm_q8 (ggml-cpu x86 rounding).
 // x rows of K (f32 or bf16, row stride ld_x elements); grp > 0 gathers output
-// row n from source row (n / grp) * gstride + n % grp.
+// row n from source row (n / grp) * gstride + n % grp (gstride in ROWS of
+// ld_x, unlike the element strides of GemmProblem::x_group_stride).
 hipError_t launch_quantize_rows_q8(const void *x, int x_f32, int64_t ld_x, int N, int K,
                                    int8_t *qx, float *dx, hipStream_t s, int grp = 0, int64_t gstride = 0);
 // f32 rows of two streams quantized in one launch (each as launch_quantize_rows_q8)

@@ -60,7 +60,7 @@ class MMDitConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "hidden", "n_head", "head_dim", "depth", "fused_depth", "latent_dim", "text_seq", "clip_dim",
         "sync_dim", "t5_dim", "mlp_hidden", "max_batch", "max_latent", "max_clip", "max_sync")] + \
-        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")]
+        [(n, ctypes.c_float) for n in ("rope_theta", "t_max_period")] + [("weight_type", ctypes.c_int)]
 
 
 _lib = None
@@ -146,6 +146,10 @@ def load():
         "tsk_mmdit_tensor_info": ([vp, i, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)], i),
         "tsk_mmdit_tensor_type": ([vp, i], i),
         "tsk_mmdit_set_tensor": ([vp, ctypes.c_char_p, vp, ctypes.c_int64], i),
+        "tsk_mmdit_set_tensor_q8_0": ([vp, ctypes.c_char_p, vp, ctypes.c_size_t], i),
+        "tsk_mmdit_config_from_gguf": ([vp, ctypes.POINTER(MMDitConfig)], i),
+        "tsk_mmdit_create_from_gguf": ([vp, ctypes.POINTER(MMDitConfig), ctypes.POINTER(vp)], i),
+        "tsk_mmdit_load_gguf": ([vp, vp], i),
         "tsk_mmdit_forward": ([vp, i, i, vp, vp, i, vp, i, vp, vp, vp, vp, vp, vp], i),
         "tsk_mmdit_sample": ([vp, i, vp, i, vp, i, vp, vp, vp, vp, i, f, vp, vp, vp], i),
         "tsk_mmdit_forward_device": ([vp, i, i, vp, vp, i, vp, i, vp, vp, vp, vp, vp, vp], i),
@@ -839,15 +843,56 @@ def mmdit_synthetic_weights(tensors, seed=1234, std=0.02):
     return out
 
 
+def mmdit_pool_weights(tensors, seed=1234, std=0.02, pool_size=1 << 24):
+    """(name, array) pairs of random-init weights for the reference graph's
+    1.28 G parameters, generated lazily: every matrix a window (at a seeded
+    offset, wrapping) of one pool of N(0, std) values rounded to bf16; vectors
+    N(0, std) (q/k norm weights 1 + N(0, std)); the learned empties N(0, 1).
+    Drawing 1.28 G fresh normals takes minutes on a host; the windows give
+    every matrix its own values at the cost of shared statistics."""
+    def window(pool, off, n):
+        w = np.empty(n, np.float32)
+        i = 0
+        while i < n:
+            k = min(n - i, pool.size - off)
+            w[i:i + k] = pool[off:off + k]
+            i, off = i + k, 0
+        return w
+    rng = np.random.default_rng(seed)
+    pool = (rng.standard_normal(pool_size, dtype=np.float32) * np.float32(std)).view(np.uint32)
+    pool = ((pool + np.uint32(0x7FFF) + ((pool >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000))
+    pool = pool.view(np.float32)
+    for name, ne, _ty in tensors:
+        shape = tuple(int(x) for x in reversed(ne))
+        while len(shape) > 1 and shape[0] == 1:
+            shape = shape[1:]
+        n = int(np.prod(shape))
+        if name.startswith("empty_"):
+            w = rng.standard_normal(n, dtype=np.float32)
+        elif len(shape) == 1:
+            w = rng.standard_normal(n, dtype=np.float32) * np.float32(std)
+            if name.endswith("norm.weight"):
+                w += np.float32(1.0)
+        else:
+            w = window(pool, int(rng.integers(0, pool.size)), n)
+        yield name, w.reshape(shape)
+
+
 class MMDit:
     """ts_dit counterpart running the reference's graph (src/mmdit.cpp:119-376):
-    named BF16 / F32 weights on the GPU, forward() and sample()."""
+    named BF16 / F32 / Q8_0 weights on the GPU, forward() and sample()."""
 
-    def __init__(self, cfg=None):
+    def __init__(self, cfg=None, gguf=None):
+        """cfg: sizes, capacities and weight_type; gguf: a Gguf file whose
+        tensors' types the model takes and whose weights it loads
+        (ts_dit::load)"""
         init()
         self.cfg = cfg if cfg is not None else mmdit_config()
         h = ctypes.c_void_p()
-        check(load().tsk_mmdit_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        if gguf is None:
+            check(load().tsk_mmdit_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        else:
+            check(load().tsk_mmdit_create_from_gguf(gguf.h, ctypes.byref(self.cfg), ctypes.byref(h)))
         self.h = h
 
     def close(self):
@@ -875,6 +920,14 @@ class MMDit:
     def set_tensor(self, name, host_f32):
         host_f32 = np.ascontiguousarray(host_f32, dtype=np.float32)
         check(load().tsk_mmdit_set_tensor(self.h, name.encode(), host_f32.ctypes.data, host_f32.size))
+
+    def set_tensor_q8_0(self, name, blocks):
+        """Q8_0 blocks (bytes / uint8 array) of a tensor held as Q8_0"""
+        b = np.ascontiguousarray(np.frombuffer(bytes(blocks), np.uint8))
+        check(load().tsk_mmdit_set_tensor_q8_0(self.h, name.encode(), b.ctypes.data, b.size))
+
+    def load_gguf(self, gguf):
+        check(load().tsk_mmdit_load_gguf(self.h, gguf.h))
 
     @staticmethod
     def _c(a):
@@ -1162,6 +1215,14 @@ class Gguf:
     def t5_config(self, **kw):
         c = t5_config(**kw)
         check(load().tsk_t5_config_from_gguf(self.h, ctypes.byref(c)))
+        return c
+
+    def mmdit_config(self, **kw):
+        """the reference graph's sizes from the file; kw (capacities) applied after"""
+        c = mmdit_config()
+        check(load().tsk_mmdit_config_from_gguf(self.h, ctypes.byref(c)))
+        for k_, v_ in kw.items():
+            setattr(c, k_, v_)
         return c
 
     def load_into(self, model):
