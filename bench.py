@@ -89,14 +89,17 @@ def cpu_info():
     return {"model": model, "flags": flags, "logical_cpus": os.cpu_count(), "allowed_cpus": allowed}
 
 
-def cpu_baseline(weights, lat, t, txt, runs=5):
+def cpu_baseline(weights, lat, t, txt, inputs30, runs=5, runs30=3):
     """The oracle's flow step (the same weights and inputs as the GPU step) on
     this host: one warm-up, then the median of `runs` timed steps, at 4
     threads (ggml-cpu's default thread count: the reference never sets
     n_threads, src/common/ts_backend.h:10-16) and at every allowed core (at
     most 16, the host share of one GPU); CFG as one B = 2 forward, and as the
     reference's two B = 1 forwards per step (src/mmdit.cpp:363-364) on all
-    allowed cores."""
+    allowed cores. At 30 s (646 + 77 tokens, the sampler's step) the median
+    of `runs30` steps at both thread counts (one warm-up on all cores), and
+    the 24-step sample as 24 of those steps (each step runs the same
+    forward; the CFG / Euler update is negligible next to it)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     info = cpu_info()
@@ -124,6 +127,26 @@ def cpu_baseline(weights, lat, t, txt, runs=5):
     med_all, walls_all = timed(nthreads, b2)
     med_b1, walls_b1 = timed(nthreads, two_b1)
     med_4, walls_4 = timed(4, b2)
+    lat30, t30, txt30 = inputs30
+    b2_30 = lambda: od.forward(lat30, t30, txt30, act_bf16=True, kv_f16=True)
+    oracle.set_threads(nthreads)
+    b2_30()
+    walls30 = {}
+    for th in (nthreads, 4):
+        oracle.set_threads(th)
+        w = []
+        for _ in range(runs30):
+            t0 = time.perf_counter()
+            b2_30()
+            w.append(time.perf_counter() - t0)
+        walls30[th] = (sorted(w)[len(w) // 2], [round(x, 3) for x in w])
+    med30 = walls30[nthreads][0]
+    step30 = {"threads": nthreads, "steps_per_s": round(1.0 / med30, 4), "median_s": round(med30, 4),
+              "runs_s": walls30[nthreads][1],
+              "threads_4": {"steps_per_s": round(1.0 / walls30[4][0], 4), "median_s": round(walls30[4][0], 4),
+                            "runs_s": walls30[4][1]},
+              "sample_24_steps_s": round(24 * med30, 2),
+              "sample_24_steps_s_threads_4": round(24 * walls30[4][0], 2)}
     return {"value": round(1.0 / med_all, 4), "unit": "steps/s", "cores": nthreads, "kind": "port",
             "sample": f"one full 21-block CFG-batched flow step at 9 s (B=2, 194+77 tokens), the oracle's C "
                       f"restatement of ggml-cpu semantics on {nthreads} threads; 1 warm-up, median of {runs}",
@@ -131,7 +154,8 @@ def cpu_baseline(weights, lat, t, txt, runs=5):
             "median_s": round(med_all, 4), "runs_s": walls_all,
             "threads_4": {"steps_per_s": round(1.0 / med_4, 4), "median_s": round(med_4, 4), "runs_s": walls_4},
             "cfg_two_b1_forwards": {"threads": nthreads, "steps_per_s": round(1.0 / med_b1, 4),
-                                    "median_s": round(med_b1, 4), "runs_s": walls_b1}}
+                                    "median_s": round(med_b1, 4), "runs_s": walls_b1},
+            "step_30s": step30}
 
 
 def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
@@ -282,44 +306,65 @@ def graph_bench(tsk, steps, warmup=3):
     extended_c adaLN, 154 text tokens, k7 output conv; src/mmdit.cpp:119-342)
     at 9 s (194 latent, 72 clip, 216 sync frames) and 30 s (646, 240, 720):
     one B = 2 (CFG) forward per step, inputs resident in HBM, HIP events around
-    `steps` forwards; plus the 24-step CFG-5 sampler at 30 s (wall clock)"""
+    `steps` forwards; the 24-step CFG-5 sampler at 30 s (wall clock, host
+    inputs and result); and the same graph with the Q8_0 GGUF's weight types
+    (convert/quantize_gguf.py: 2-D linears Q8_0, the 3-D convolution kernels
+    F32 on fp32 MFMA)"""
     import numpy as np
-    m = tsk.MMDit(tsk.mmdit_config())
-    for k, v in tsk.mmdit_pool_weights(m.tensors()):
-        m.set_tensor(k, v)
-    rng = np.random.default_rng(4242)
     out = {}
-    for label, T, Sc, Ss in (("9s", 194, 72, 216), ("30s", 646, 240, 720)):
+    rng = np.random.default_rng(4242)
+    shapes = (("9s", 194, 72, 216), ("30s", 646, 240, 720))
+    inputs = {}
+    for label, T, Sc, Ss in shapes:
         f = lambda *sh: rng.standard_normal(sh, dtype=np.float32)
-        host = (f(2, 64, T), f(2, Sc, 1024), f(2, Ss, 768), f(2, 77, 1024), f(2, 77, 2048), f(2, 1024))
+        inputs[label] = (f(2, 64, T), f(2, Sc, 1024), f(2, Ss, 768), f(2, 77, 1024), f(2, 77, 2048), f(2, 1024))
+
+    def timed_forwards(m, label, T, Sc, Ss, n, nwarm):
+        host = inputs[label]
         dev = [tsk.to_device(a) for a in host]
         t = np.full(2, 0.5, np.float32)
         flow = tsk.empty((2, T, 64))
-        for _ in range(warmup):
+        for _ in range(nwarm):
             m.forward_device(dev[0], t, *dev[1:], flow)
         tsk.synchronize()
         s, e = tsk.Event(), tsk.Event()
         s.record()
-        for _ in range(steps):
+        for _ in range(n):
             m.forward_device(dev[0], t, *dev[1:], flow)
         e.record()
         tsk.synchronize()
-        ms = s.elapsed_ms(e) / steps
-        out[label] = {"steps_per_s": round(1000.0 / ms, 2), "ms_per_step": round(ms, 4), "latent_tokens": T,
-                      "clip_frames": Sc, "sync_frames": Ss, "joint_tokens": T + Sc + 154}
-        if label == "30s":
-            noise = host[0][0]
-            m.sample(noise, host[1][0], host[2][0], host[3][0], host[4][0], host[5][0], steps=24, cfg_scale=5.0)
-            walls = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                m.sample(noise, host[1][0], host[2][0], host[3][0], host[4][0], host[5][0], steps=24, cfg_scale=5.0)
-                walls.append(time.perf_counter() - t0)
-            wall = sorted(walls)[1]
-            out["sample_24_steps_30s"] = {"seconds": round(wall, 4), "sampler_steps_per_s": round(24 / wall, 2),
-                                          "note": "host-side CFG / Euler, inputs re-staged from the host per step"}
+        ms = s.elapsed_ms(e) / n
+        return {"steps_per_s": round(1000.0 / ms, 2), "ms_per_step": round(ms, 4), "latent_tokens": T,
+                "clip_frames": Sc, "sync_frames": Ss, "joint_tokens": T + Sc + 154}
+
+    m = tsk.MMDit(tsk.mmdit_config())
+    for k, v in tsk.mmdit_pool_weights(m.tensors()):
+        m.set_tensor(k, v)
+    for label, T, Sc, Ss in shapes:
+        out[label] = timed_forwards(m, label, T, Sc, Ss, steps, warmup)
+    host = inputs["30s"]
+    a = (host[0][0], host[1][0], host[2][0], host[3][0], host[4][0], host[5][0])
+    m.sample(*a, steps=24, cfg_scale=5.0)
+    walls = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        m.sample(*a, steps=24, cfg_scale=5.0)
+        walls.append(time.perf_counter() - t0)
+    wall = sorted(walls)[1]
+    out["sample_24_steps_30s"] = {
+        "seconds": round(wall, 4), "sampler_steps_per_s": round(24 / wall, 2),
+        "vs_24_forwards": round(wall / (24 * out["30s"]["ms_per_step"] / 1e3), 4),
+        "note": "t-independent conditioning once per sample, latent and CFG / Euler on the device; "
+                "wall clock incl. the host inputs' upload and the result's download"}
     m.close()
     out["weights"] = "BF16 (t_embed MLP F32), 1.28 G parameters, random-init from a seeded N(0, 0.02) pool"
+    mq = tsk.MMDit(tsk.mmdit_config(weight_type=8))
+    for k, v in tsk.mmdit_pool_weights(mq.tensors()):
+        mq.set_tensor(k, v)
+    out["q8_0"] = {label: timed_forwards(mq, label, T, Sc, Ss, max(3, steps // 2), 1) for label, T, Sc, Ss in shapes}
+    out["q8_0"]["weights"] = ("the Q8_0 GGUF's types: 2-D linears Q8_0 (ggml's reference quantizer), 3-D "
+                              "convolution kernels, t_embed MLP and vectors F32")
+    mq.close()
     return out
 
 
@@ -449,8 +494,17 @@ def main():
         dit.forward(lat_h, inputs9[1], inputs9[2])
     ms_host = (time.perf_counter() - t_host) * 1e3 / args.steps
     # 30 s (646 latent + 77 text tokens): steps/s (plain), attention at N = 723 (timed)
-    ms30, _, _ = run(646, max(5, args.steps // 2), 2, False)
+    ms30, _, inputs30 = run(646, max(5, args.steps // 2), 2, False)
     _, roles30, _ = run(646, max(5, args.steps // 2), 1, True)
+    # the same 30 s step with every q / k RMSNorm weight scaled by 2.5: logits
+    # beyond the bound of the max-free softmax, so every attention launch runs
+    # the running-max kernel (trained norm weights may be that large)
+    norms = {k: v for k, v in weights.items() if k.endswith("norm.weight")}
+    for k, v in norms.items():
+        dit.set_tensor(k, v * np.float32(2.5))
+    ms30u, roles30u, _ = run(646, max(5, args.steps // 2), 2, True)
+    for k, v in norms.items():
+        dit.set_tensor(k, v)
 
     # config 5: the full 24-step rectified-flow Euler sampler with CFG 5 at 30 s
     # (646 latent + 77 text tokens, cond/uncond batched as B = 2 per step),
@@ -543,7 +597,11 @@ def main():
                                "d=1024, 16x64 heads, GELU MLP 4x, 7 joint + 14 fused blocks, BF16 weights",
                    "global_batch": 2, "seq_len": 271, "parallelism": "single GPU"},
         "roofline": rf,
-        "attention": {"9s": attn(roles9, args.steps), "30s": attn(roles30, max(5, args.steps // 2))},
+        "attention": {"9s": attn(roles9, args.steps), "30s": attn(roles30, max(5, args.steps // 2)),
+                      "30s_unbounded": dict(attn(roles30u, max(5, args.steps // 2)),
+                                            step_ms=round(ms30u, 4),
+                                            note="q / k norm weights x 2.5: the running-max kernel; step_ms "
+                                                 "includes per-launch HIP events")},
         "steps_per_s_30s": round(1000.0 / ms30, 2),
         "sample_24_steps_30s": sample30,
         "ms_per_step_with_kernel_events": round(ms_timed, 4),
@@ -565,7 +623,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         lat, t, txt = inputs9
-        out["cpu_baseline"] = cpu_baseline(weights, lat, t, txt)
+        out["cpu_baseline"] = cpu_baseline(weights, lat, t, txt, inputs30)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

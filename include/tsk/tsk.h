@@ -107,7 +107,11 @@ typedef void *tsk_stream;   /* hipStream_t */
 
 /* Select the HIP device, read its limits (CU count, LDS per workgroup) and
  * the launch-shape overrides of tuning sweeps (TSK_* environment variables,
- * read here and never on a launch). Idempotent; a later call re-reads them. */
+ * read here and never on a launch). Idempotent; a later call re-reads them,
+ * so it must not run while other threads have operators in flight.
+ * Operators are reentrant across streams; a model object (tsk_dit, tsk_mmdit,
+ * tsk_t5, tsk_vae) owns its activations and runs one call at a time in its
+ * stream's order -- concurrent callers use one model per stream. */
 int         tsk_init(int device);
 /* Release library-owned device memory (workspaces). */
 int         tsk_shutdown(void);

@@ -39,6 +39,7 @@
 // the row sum adds the same fp16 P values in fp32 (v_dot2).
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -477,13 +478,7 @@ hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
     if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128) * 4);
     auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB>;
-    static size_t attr = 0;
-    if (lds > attr) {
-        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
-            hipSuccess)
-            (void) hipGetLastError();
-        attr = lds;
-    }
+    lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(grid), dim3(64 * KS * QB), lds, s, p);
     return hipGetLastError();
 }

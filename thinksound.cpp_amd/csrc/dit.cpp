@@ -84,6 +84,7 @@ struct tsk_dit {
     std::vector<StreamW> joint_lat, joint_txt, fused;
     // activations
     float *lat = nullptr, *txt = nullptr, *flow = nullptr, *xf = nullptr;
+    float *in_stage = nullptr;      // tsk_dit_forward's device copies of the host latent and text
     float *temb = nullptr, *tmp_c = nullptr, *cvec = nullptr;
     float *mods = nullptr;
     float *final_mod = nullptr;     // [max_batch][2H] final-layer adaLN output
@@ -286,7 +287,8 @@ extern "C" void tsk_dit_destroy(tsk_dit *d) {
     if (d->ev_join) (void) hipEventDestroy(d->ev_join);
     if (d->side) (void) hipStreamDestroy(d->side);
     void *bufs[] = {d->sched, d->sched_act, d->sched_jobs,
-                    d->blob, d->lat, d->txt, d->flow, d->xf, d->temb, d->tmp_c, d->cvec, d->mods, d->xn, d->part,
+                    d->blob, d->lat, d->txt, d->flow, d->in_stage, d->xf, d->temb, d->tmp_c, d->cvec, d->mods,
+                    d->xn, d->part,
                     d->q, d->k, d->vt, d->o, d->h, d->jobs_dev, d->freq, d->rope_cs,
                     d->s_x /* one allocation: s_x2, s_flow2, s_flow0, s_text2 point into it */,
                     d->qkv32, d->o32, d->qh, d->dh, d->qx, d->dx};
@@ -351,6 +353,7 @@ extern "C" int tsk_dit_create(const tsk_dit_config *cfg, tsk_dit **out) {
         (rc = alloc((void **) &d->lat, sizeof(float) * B * T * H)) ||
         (rc = alloc((void **) &d->txt, sizeof(float) * B * St * H)) ||
         (rc = alloc((void **) &d->flow, sizeof(float) * B * T * c.latent_dim)) ||
+        (rc = alloc((void **) &d->in_stage, sizeof(float) * B * ((size_t) T * c.latent_dim + (size_t) c.text_seq * H))) ||
         (rc = alloc((void **) &d->xf, sizeof(float) * B * T * H)) ||
         (rc = alloc((void **) &d->temb, sizeof(float) * B * H)) ||
         (rc = alloc((void **) &d->tmp_c, sizeof(float) * B * H)) ||
@@ -1191,18 +1194,16 @@ extern "C" int tsk_dit_forward(tsk_dit *d, int B, int T, const float *latent, co
     if (rc) return rc;
     const tsk_dit_config &c = d->cfg;
     hipStream_t st = (hipStream_t) stream;
-    float *lat_d = nullptr, *txt_d = nullptr;
+    // the host inputs go to the staging buffer allocated at create (B <= max_batch, T <= max_latent)
     const size_t nl = (size_t) B * T * c.latent_dim, nt = (size_t) B * c.text_seq * c.hidden;
-    hipError_t e = hipMalloc((void **) &lat_d, sizeof(float) * (nl + nt));
-    if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc: %s", hipGetErrorString(e));
-    txt_d = lat_d + nl;
+    float *lat_d = d->in_stage, *txt_d = d->in_stage + nl;
     rc = hipcheck(hipMemcpyAsync(lat_d, latent, sizeof(float) * nl, hipMemcpyHostToDevice, st), "latent upload");
     if (!rc) rc = hipcheck(hipMemcpyAsync(txt_d, text, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text upload");
     if (!rc) rc = forward_impl(d, B, T, lat_d, true, t, txt_d, d->flow, st);
     if (!rc) rc = hipcheck(hipMemcpyAsync(flow, d->flow, sizeof(float) * nl, hipMemcpyDeviceToHost, st), "flow download");
-    if (!rc) rc = hipcheck(hipStreamSynchronize(st), "stream sync");
+    // the pageable sources and destination are done with once the stream is
     (void) hipStreamSynchronize(st);
-    (void) hipFree(lat_d);
+    if (!rc) rc = hipcheck(hipGetLastError(), "stream sync");
     return rc;
 }
 
@@ -1312,6 +1313,8 @@ extern "C" int tsk_dit_sample(tsk_dit *d, int T, const float *noise, const float
     if ((rc = hipcheck(hipMemcpyAsync(d->s_x2 + n, xt.data(), sizeof(float) * n, hipMemcpyHostToDevice, st), "noise"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2, text_cond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
     if ((rc = hipcheck(hipMemcpyAsync(d->s_text2 + nt, text_uncond, sizeof(float) * nt, hipMemcpyHostToDevice, st), "text"))) return rc;
+    // xt is pageable host memory that ends with this call: let the stream consume it first
+    if ((rc = hipcheck(hipStreamSynchronize(st), "input upload"))) return rc;
     // Tuning::dit_sched off computes the conditioning inside every step instead
     const bool use_sched = tuning().dit_sched;
     if (use_sched && (rc = build_schedule(d, steps, st))) return rc;

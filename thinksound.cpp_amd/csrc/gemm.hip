@@ -748,12 +748,7 @@ hipError_t q8c_launch(const GemmParams &p, hipStream_t s) {
     const size_t lds = (size_t) R * (TM + TN) * 2048 + (size_t) std::min(p.K / 32, Q8_SEG) * (BM + BN) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto kern = gemm_q8c_kernel<TM, TN, R, EPI, YBF16>;
-    static size_t attr = 0;   // dynamic LDS opted in so far for this kernel
-    if (lds > attr) {
-        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
-            (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
-        attr = lds;
-    }
+    lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(tiles_m * tiles_n * (p.splits > 1 ? p.splits : 1)), dim3(256), lds, s, p, tiles_m,
                   tiles_n);
     return hipGetLastError();
@@ -769,12 +764,7 @@ hipError_t q8c_launch_pair(const GemmParams &p0, const GemmParams &p1, hipStream
                        (size_t) std::min(std::max(p0.K, p1.K) / 32, Q8_SEG) * (BM + BN) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto kern = gemm_q8c_pair_kernel<TM, TN, R, EPI, YBF16>;
-    static size_t attr = 0;
-    if (lds > attr) {
-        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
-            (void) hipGetLastError();
-        attr = lds;
-    }
+    lds_opt_in((const void *) kern, lds);
     const int begin1 = (tm0 * tn0 * S0 + 7) & ~7;
     launch_kernel(kern, dim3(begin1 + tm1 * tn1 * S1), dim3(256), lds, s, p0, p1, tm0, tn0, tm1, tn1, begin1);
     return hipGetLastError();

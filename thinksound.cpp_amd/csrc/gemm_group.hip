@@ -34,6 +34,7 @@
 // accumulation differs from the ggml graph.
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -405,13 +406,7 @@ __global__ __launch_bounds__(NT) void gemm_group_kernel(const GemmGroup g, int K
 template <int TM, int TN, int PF, bool XF32, int EPI>
 hipError_t launch_cfg(const GemmGroup &g, int KC, int nblocks, size_t lds, hipStream_t s) {
     auto kern = gemm_group_kernel<TM, TN, PF, XF32, EPI>;
-    static size_t attr = 0;     // dynamic LDS opted in so far for this kernel
-    if (lds > attr) {
-        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
-            hipSuccess)
-            (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
-        attr = lds;
-    }
+    lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(nblocks), dim3(NT), lds, s, g, KC);
     return hipGetLastError();
 }
@@ -425,15 +420,8 @@ hipError_t group_launch(GemmGroup &g, int flags, int epi, hipStream_t s) {
     if (xf32 && epi != EPI_STORE_F32 && epi != EPI_STORE_BF16 && !swiglu) return hipErrorInvalidValue;
     const int bmo = swiglu ? BM / 2 : BM;
     // K held in LDS per chunk: up to KCMAX, within the device's LDS per workgroup
-    static int kc_dev = 0;
-    if (!kc_dev) {
-        int dev = 0, lmax = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&lmax, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-            return hipErrorInvalidDevice;
-        kc_dev = min(KCMAX, (lmax / (2 * BN) - 8) / KS * KS);
-        if (kc_dev < KS) return hipErrorInvalidConfiguration;
-    }
+    const int kc_dev = min(KCMAX, ((int) device_lds_per_block() / (2 * BN) - 8) / KS * KS);
+    if (kc_dev < KS) return hipErrorInvalidConfiguration;
     int nblocks = 0, kc = KS;
     for (int i = 0; i < g.nprob; ++i) {
         GemmProblem &p = g.p[i];

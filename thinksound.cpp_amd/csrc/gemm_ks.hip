@@ -866,13 +866,7 @@ hipError_t ks_launch(GemmGroup &g, hipStream_t s) {
     static_assert(lds <= 160 * 1024, "LDS");
     auto kern = g.nprob == 2 ? gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV, 2>
                              : gemm_ks_kernel<TM, TN, R, MODE, EPI, KH, CONV, 1>;
-    static bool attr[2] = {false, false};   // dynamic LDS above 64 KiB is opted in once per kernel
-    if (!attr[g.nprob - 1]) {
-        if (hipFuncSetAttribute((const void *) kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) !=
-            hipSuccess)
-            (void) hipGetLastError();   // runtimes that need no opt-in may reject the call
-        attr[g.nprob - 1] = true;
-    }
+    lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(nblocks), dim3(NT), lds, s, g);
     return hipGetLastError();
 }

@@ -400,6 +400,8 @@ extern "C" int tsk_t5_encode_range(tsk_t5 *t, int n, const float *x, const int32
     int rc = hipcheck(hipMemcpyAsync(xin, x, bytes, hipMemcpyHostToDevice, s), "x upload");
     if (!rc) rc = tsk_t5_encode_layers(t, n, xin, ids, layer_begin, layer_end, final_norm, xo, stream);
     if (!rc) rc = hipcheck(hipMemcpyAsync(out, xo, bytes, hipMemcpyDeviceToHost, s), "out download");
-    if (!rc) rc = hipcheck(hipStreamSynchronize(s), "sync");
+    // on every path: the caller's host buffers are done with once the stream is
+    const hipError_t e = hipStreamSynchronize(s);
+    if (!rc) rc = hipcheck(e, "sync");
     return rc;
 }

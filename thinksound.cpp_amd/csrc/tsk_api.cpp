@@ -113,6 +113,36 @@ int scratch_address_locked(int dev, void **out) {
 const Tuning &tuning() { return g_tuning; }
 const DeviceInfo &device_info() { return g_dev; }
 
+namespace {
+std::mutex g_lds_mu;
+std::map<std::pair<const void *, int>, size_t> g_lds_attr;   // (kernel, device) -> LDS bytes opted in
+std::map<int, size_t> g_lds_dev;                             // device -> LDS bytes per workgroup
+}  // namespace
+
+void lds_opt_in(const void *kern, size_t bytes) {
+    if (bytes <= 64 * 1024) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    std::lock_guard<std::mutex> lk(g_lds_mu);
+    size_t &have = g_lds_attr[{kern, dev}];
+    if (bytes <= have) return;
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes) == hipSuccess) have = bytes;
+    else (void) hipGetLastError();
+}
+
+size_t device_lds_per_block() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 64 * 1024;
+    std::lock_guard<std::mutex> lk(g_lds_mu);
+    auto it = g_lds_dev.find(dev);
+    if (it != g_lds_dev.end()) return it->second;
+    int v = 0;
+    const size_t lim = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0
+                           ? (size_t) v : 64 * 1024;
+    g_lds_dev[dev] = lim;
+    return lim;
+}
+
 int require_init() {
     if (g_device < 0) return fail(TSK_ERR_NOT_INIT, "tsk_init() has not been called");
     return TSK_OK;

@@ -49,6 +49,15 @@ struct Tuning {
 };
 const Tuning &tuning();
 
+// Dynamic LDS above the default per-workgroup limit, opted in for kernel
+// `kern` on the current device before its launch (hipFuncSetAttribute acts
+// per device). Thread-safe; a size is recorded only when the runtime accepted
+// it, so a refused opt-in is retried on the next launch (runtimes that need
+// no opt-in may refuse the call: the launch itself then decides).
+void lds_opt_in(const void *kern, size_t bytes);
+// LDS bytes a workgroup may allocate on the current device (cached per device)
+size_t device_lds_per_block();
+
 // Device limits read once per tsk_init for the current device.
 struct DeviceInfo {
     int cus = 256;               // compute units
