@@ -74,3 +74,46 @@ def test_noalloc_refuses_oversized_node(tsk):
     yr = tsk.mul_mat(w, xb)
     tsk.synchronize()
     assert np.array_equal(yb.numpy(), yr.numpy())
+
+
+def test_noalloc_under_graph_capture(tsk):
+    """tsk_mul_mat_noalloc is for callers under HIP graph capture: a BF16 and
+    a Q8_0 node (both staging their activations in the fixed array) captured
+    on one stream in Global mode (a hipMalloc or other call not allowed under
+    capture would fail it), replayed three times with eager work and
+    synchronisations between the replays; every replay gives the bits of
+    tsk_mul_mat"""
+    rng = np.random.default_rng(7)
+    K, M, N = 1024, 3072, 388
+    wb, _ = weights(tsk, rng, "bf16", K, M)
+    wq, atq = weights(tsk, rng, "q8_0", K, M)
+    bias = tsk.to_device((rng.standard_normal(M) * 0.1).astype(np.float32))
+    x1 = tsk.to_device(rng.standard_normal((N, K)).astype(np.float32))
+    x2 = tsk.to_device(rng.standard_normal((N, K)).astype(np.float32))
+    r1 = tsk.mul_mat(wb, x1, bias=bias).numpy()
+    r2 = tsk.mul_mat(wq, x2, a_type=atq).numpy()
+    s = tsk.Stream()
+    y1, y2 = tsk.empty((N, M)), tsk.empty((N, M))
+    # first launches of these kernels outside the capture
+    tsk.mul_mat_noalloc(wb, x1, bias=bias, out=y1, stream=s)
+    tsk.mul_mat_noalloc(wq, x2, a_type=atq, out=y2, stream=s)
+    s.synchronize()
+
+    def work():
+        tsk.mul_mat_noalloc(wb, x1, bias=bias, out=y1, stream=s)
+        tsk.mul_mat_noalloc(wq, x2, a_type=atq, out=y2, stream=s)
+    g = tsk.Graph(s, work)
+    try:
+        for rep in range(3):
+            nan = np.full((N, M), np.nan, np.float32)
+            for y in (y1, y2):                       # eager work between replays
+                tsk._hipcheck(tsk.hip().hipMemcpy(y.data_ptr(), nan.ctypes.data, nan.nbytes, 1), "reset")
+            tsk.mul_mat(wq, x1, a_type=atq)          # other scratch traffic on the null stream
+            tsk.synchronize()
+            g.launch()
+            s.synchronize()
+            assert np.array_equal(y1.numpy(), r1), f"replay {rep}: bf16 node"
+            assert np.array_equal(y2.numpy(), r2), f"replay {rep}: Q8_0 node"
+    finally:
+        g.destroy()
+        s.destroy()

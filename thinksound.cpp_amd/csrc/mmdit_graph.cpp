@@ -604,6 +604,10 @@ int run_ln(tsk_mmdit *m, Stream *r, int ns, int B, int which, hipStream_t s) {
 constexpr float QK_EPS = 1e-6f;                                      // rmsnorm_w EPS, src/mmdit.cpp:10
 constexpr float Q_SCALE = 1.4426950408889634f / 8.0f;                 // 1/sqrt(64) * log2(e): the softmax scale
 
+// tiles of the QKV GEMM: 128 x 64 from 1100 activation rows, 64 x 64 below
+// (the DiT's qkv rule)
+int qkv_cfg(int rows) { return rows >= 1100 ? 29 : 30; }
+
 // qkv with the split / RMSNorm / RoPE / F16 scatter into the joint attention
 // operands in the GEMM epilogue (EPI_QKV); up to two streams per launch
 int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
@@ -631,8 +635,7 @@ int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
             q.q_scale = Q_SCALE;
             rows0 = std::max(rows0, q.N);
         }
-        // 128 x 64 tiles from 1100 activation rows, 64 x 64 below (the DiT's qkv rule)
-        const int rc = hipcheck(launch_gemm_ks(g, EPI_QKV, rows0 >= 1100 ? 29 : 30, s), "mmdit qkv gemm");
+        const int rc = hipcheck(launch_gemm_ks(g, EPI_QKV, qkv_cfg(rows0), s), "mmdit qkv gemm");
         if (rc) return rc;
     }
     return TSK_OK;

@@ -216,7 +216,11 @@ def hip():
                          "hipStreamCreate": [ctypes.POINTER(vp)], "hipStreamDestroy": [vp],
                          "hipEventDestroy": [vp], "hipEventRecord": [vp, vp],
                          "hipEventSynchronize": [vp],
-                         "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp]}.items():
+                         "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
+                         "hipStreamBeginCapture": [vp, i], "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+                         "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, sz],
+                         "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp],
+                         "hipGraphDestroy": [vp]}.items():
             getattr(H, nm).argtypes = args
             getattr(H, nm).restype = i
         _hip = H
@@ -407,6 +411,36 @@ class Stream:
             release_workspace(self)
             hip().hipStreamDestroy(self.h)
             self.h = None
+
+
+class Graph:
+    """The work a function enqueues on `stream`, captured into a HIP graph
+    (hipStreamCaptureModeGlobal: a call that is not allowed under capture,
+    hipMalloc among them, fails the capture) and replayed with launch()."""
+
+    def __init__(self, stream, fn):
+        H = hip()
+        _hipcheck(H.hipStreamBeginCapture(stream.h, 0), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            rc = H.hipStreamEndCapture(stream.h, ctypes.byref(g))
+        _hipcheck(rc, "hipStreamEndCapture")
+        self.graph = g
+        e = ctypes.c_void_p()
+        _hipcheck(H.hipGraphInstantiate(ctypes.byref(e), g, None, None, 0), "hipGraphInstantiate")
+        self.exec = e
+        self.stream = stream
+
+    def launch(self):
+        _hipcheck(hip().hipGraphLaunch(self.exec, self.stream.h), "hipGraphLaunch")
+
+    def destroy(self):
+        if getattr(self, "exec", None) is not None:
+            hip().hipGraphExecDestroy(self.exec)
+            hip().hipGraphDestroy(self.graph)
+            self.exec = None
 
 
 def _stream(stream=None):
