@@ -14,12 +14,18 @@ types, and the GGUF loader (ts_dit::load, src/mmdit.cpp:104-116):
 - the on-device sampler (conditioning once, CFG / Euler on the device)
   against a host loop over tsk_mmdit_forward, bit for bit.
 
-Bounds: a forward is held to max(2e-3, 2 x the oracle's own change when its
-attention takes K / V in F32 instead of the reference's F16 cast) against the
-oracle with the same weight types. With Q8_0 activations a one-ulp change of
-a product's input flips some quantization roundings, as with bf16, so the
-oracle's own sensitivity sets the floor; the F32 model has no such rounding
-and is held to 2e-3 against the F32 path outright."""
+Bounds: a forward is held to max(2e-3, 2 x the oracle's own sensitivity)
+against the oracle with the same weight types. The sensitivity is the larger
+of two changes of the oracle's output: when its attention takes K / V in F32
+instead of the reference's F16 cast, and when its inputs move by 2^-20
+relative (random signs), the size of the differences fp32 summation order
+makes in the F32 products (the F32 stages here and in the oracle differ by
+1-2e-6). With Q8_0 activations such a change flips some quantization
+roundings; a flip in the conditioning vectors (two rows, every token's
+modulation) spreads to every token, so the oracle's own response to that
+perturbation is 7-9e-3 on these models, whatever did the perturbing. The F32
+model has no such rounding and is held to 2e-3 against the F32 path
+outright."""
 import numpy as np
 import pytest
 
@@ -59,16 +65,24 @@ def inputs(B, T, Sc, Ss, seed=4242):
     return f(B, 64, T), f(B, Sc, 1024), f(B, Ss, 768), f(B, 77, 1024), f(B, 77, 2048), f(B, 1024)
 
 
+def jittered(args, seed=7, rel=2.0 ** -20):
+    """every float input times (1 +- rel), random signs (t kept)"""
+    rng = np.random.default_rng(seed)
+    j = lambda a: (a * (1 + np.float32(rel) * rng.choice(np.array([-1, 1], np.float32), a.shape))).astype(np.float32)
+    return (j(args[0]), args[1]) + tuple(j(a) for a in args[2:])
+
+
 def check(m, od, args, label):
     f = m.forward(*args)
     assert np.isfinite(f).all()
     ref = od.forward(*args)
-    floor = rel_l2(od.forward(*args, kv_f16=False), ref)
+    floor_kv = rel_l2(od.forward(*args, kv_f16=False), ref)
+    floor_j = rel_l2(od.forward(*jittered(args)), ref)
     e = rel_l2(f, ref)
     e32 = rel_l2(f, od.forward(*args, act_bf16=False, kv_f16=False))
-    print(f"{label}: rel-L2 {e:.3e} vs the oracle with the same types (its K/V F16-vs-F32 change {floor:.3e}); "
-          f"{e32:.3e} vs the F32 path", flush=True)
-    assert e <= max(2e-3, 2 * floor)
+    print(f"{label}: rel-L2 {e:.3e} vs the oracle with the same types (its own change: K/V F16-vs-F32 "
+          f"{floor_kv:.3e}, inputs x (1 +- 2^-20) {floor_j:.3e}); {e32:.3e} vs the F32 path", flush=True)
+    assert e <= max(2e-3, 2 * max(floor_kv, floor_j))
     return f
 
 

@@ -65,7 +65,10 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
     }
 
     f32x4 wreg[WPER], xreg[XPER];
-    const int nk = (p.K + BK - 1) / BK;
+    // split-K: slice z sums the k tiles [z nk / S, (z + 1) nk / S) into its own
+    // output slice (the caller sums the slices in order)
+    const int nk_all = (p.K + BK - 1) / BK, S = p.splits > 1 ? p.splits : 1, z = (int) blockIdx.z;
+    const int kt0 = z * nk_all / S, nk = (z + 1) * nk_all / S;
     auto gload = [&](int kt) {
         const int k0 = kt * BK;
         for (int i = 0; i < WPER; ++i) {
@@ -106,11 +109,11 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
     for (int i = 0; i < TM; ++i)
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-    gload(0);
+    gload(kt0);
     lstore(0);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
+    for (int kt = kt0; kt < nk; ++kt) {
+        const int buf = (kt - kt0) & 1;
         if (kt + 1 < nk) gload(kt + 1);
 #pragma unroll
         for (int kb = 0; kb < BK / 16; ++kb) {
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
                 uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
                 for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
             } else {
-                float *yr = (float *) p.y + (int64_t) n * p.ld_y + m0;
+                float *yr = (float *) p.y + (int64_t) z * p.N * p.ld_y + (int64_t) n * p.ld_y + m0;
                 float v[4];
                 if (p.accumulate) {
                     if (full) {
@@ -201,12 +204,15 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake) {
     constexpr int TM = 4, TN = 2, BM = 2 * TM * 16, BN = 2 * TN * 16;
     if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf || (p.accumulate && y_bf16)) return hipErrorInvalidValue;
+    // split-K slices [splits][N][ld_y] of f32 partial sums: no bias, epilogue or accumulation
+    const int S = p.splits > 1 ? p.splits : 1;
+    if (S > 1 && (S > (p.K + 31) / 32 || p.bias || snake || y_bf16 || p.accumulate)) return hipErrorInvalidValue;
     if (snake && (y_bf16 || !snake->ea || !snake->eb || snake->period < 4 || snake->period % 4 || p.M % snake->period))
         return hipErrorInvalidValue;
     if (p.conv_ic && (p.conv_ic % 4 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;
-    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN);
+    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, S);
     const F32Snake none = {nullptr, nullptr, nullptr, 1};
     if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true, false>), grid, dim3(NT), 0, s, p, none);
     else if (snake) launch_kernel((gemm_f32_kernel<TM, TN, false, true>), grid, dim3(NT), 0, s, p, *snake);

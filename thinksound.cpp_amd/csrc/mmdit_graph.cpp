@@ -365,6 +365,23 @@ int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int
 // times the model's batch capacity, never from the call's batch: a batch row
 // is then summed in the same order whatever the batch it runs in.
 constexpr int GRAPH_KSPLIT_MAX = 4;
+// K slices of the f32 path's F32 products (gemm_f32's 128 x 64 tiles): the
+// Q8_0 GGUF keeps the convolution kernels F32, and linear1 / convMLP w2 with
+// 1024 outputs over a few hundred rows are 56-168 tiles with K = 3072 / 8448;
+// slices of at least 256 k until about 1000 workgroups, by the rows per batch
+// item times the batch capacity (never by the call's batch)
+constexpr int F32_KSPLIT_MAX = 8;
+constexpr int PART_SLICES = 8;      // partial-sum slices per stream row in m->part (either path)
+int f32_splits(const tsk_mmdit *m, int M, int K, int S) {
+    const int N = S * m->cfg.max_batch;
+    const int64_t tiles = (int64_t) ((M + 127) / 128) * ((N + 63) / 64);
+    const int nk = (K + 31) / 32;
+    int sp = 1;
+    const int most = std::min(F32_KSPLIT_MAX, std::max(1, tuning().f32_ksplit));
+    while (sp * 2 <= most && tiles * sp * 2 <= 1024 && nk / (2 * sp) >= 8) sp *= 2;
+    return sp;
+}
+
 int conv_splits(const tsk_mmdit *m, const Conv &C, int S) {
     const int N = S * m->cfg.max_batch;
     const int64_t tiles = (int64_t) ((C.OC + 63) / 64) * ((N + 63) / 64);
@@ -468,9 +485,11 @@ int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t 
 }
 
 // conv_cl (stride 1, padding pad) of f32 rows [B][IW][IC] (row stride ld_x,
-// batch stride xb) -> f32 rows [B * OW][OC] (ld_y)
+// batch stride xb) -> f32 rows [B * OW][OC] (ld_y), or with splits > 1 (no
+// bias) K-split partial sums in slices [splits][B * OW][ld_y]
 int g_conv(tsk_mmdit *m, const Conv &C, const float *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, float *y,
-           int64_t ld_y, bool bias, hipStream_t s) {
+           int64_t ld_y, bool bias, hipStream_t s, int splits = 1) {
+    if (splits > 1 && bias) return fail(TSK_ERR_INVALID_ARG, "K-split slices carry no bias");
     if (C.type == TSK_TYPE_F32) {
         GemmProblem q;
         memset(&q, 0, sizeof(q));
@@ -479,22 +498,24 @@ int g_conv(tsk_mmdit *m, const Conv &C, const float *x, int64_t ld_x, int64_t xb
         q.bias = bias ? C.b : nullptr;
         q.y = y; q.ld_y = ld_y;
         const int OW = IW + 2 * pad - (C.KW - 1);
-        q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = 1;
+        q.M = C.OC; q.N = B * OW; q.K = C.KW * C.IC; q.splits = splits;
         q.conv_ic = C.IC; q.conv_iw = IW; q.conv_ow = OW; q.conv_s = 1; q.conv_p = pad; q.conv_d = 1;
         return hipcheck(launch_gemm_f32(q, 0, s), "mmdit f32 conv");
     }
     const Rows src{x, ld_x, IW, xb};
     int rc = rows_bf16(m, src, B * IW, C.IC, s);
     if (rc) return rc;
-    return conv(C, m->cvt16, C.IC, (int64_t) IW * C.IC, IW, B, pad, y, ld_y, false, s, !bias);
+    return conv(C, m->cvt16, C.IC, (int64_t) IW * C.IC, IW, B, pad, y, ld_y, false, s, !bias, splits);
 }
 
 // convmlp / mlp (src/mmdit.cpp:39-52) on f32 rows: y = w2(silu(w1 x) * w3 x)
 // (no biases), the hidden state f32 in m->hid32. Convolutions (conv: rows
-// [B][S][IC], batch stride xb) or linear layers (x rows of B * S).
+// [B][S][IC], batch stride xb) or linear layers (x rows of B * S). F32
+// convolution halves w1 / w3 run as K-split slices (summed by the SiLU * gate
+// kernel); w2 writes y2_splits slices of partial sums (conv, 1: plain y).
 int g_swiglu(tsk_mmdit *m, bool is_conv, const Conv &c1, const Conv &c3, const Conv &c2, const Lin &l1, const Lin &l3,
              const Lin &l2, const float *x, int64_t ld_x, int64_t xb, int S, int B, float *y, int64_t ld_y,
-             hipStream_t s) {
+             hipStream_t s, int y2_splits = 1) {
     const int N = B * S;
     const int F = is_conv ? c1.OC : l1.M;
     const int t1 = is_conv ? c1.type : l1.type, t3 = is_conv ? c3.type : l3.type;
@@ -518,18 +539,22 @@ int g_swiglu(tsk_mmdit *m, bool is_conv, const Conv &c1, const Conv &c3, const C
         }
         if ((rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_F32, s), "mmdit swiglu w1/w3"))) return rc;
     } else {
+        int sp = 1;
         if (is_conv) {
-            if ((rc = g_conv(m, c1, x, ld_x, xb, S, B, 1, m->h1, F, false, s)) ||
-                (rc = g_conv(m, c3, x, ld_x, xb, S, B, 1, m->h3, F, false, s)))
+            if (t1 == TSK_TYPE_F32 && t3 == TSK_TYPE_F32) sp = f32_splits(m, F, c1.KW * c1.IC, S);
+            if ((rc = g_conv(m, c1, x, ld_x, xb, S, B, 1, m->h1, F, false, s, sp)) ||
+                (rc = g_conv(m, c3, x, ld_x, xb, S, B, 1, m->h3, F, false, s, sp)))
                 return rc;
         } else {
             const Rows src{x, ld_x, 0, 0};
             if ((rc = g_lin(m, l1, src, N, m->h1, F, false, s)) || (rc = g_lin(m, l3, src, N, m->h3, F, false, s)))
                 return rc;
         }
-        if ((rc = hipcheck(launch_silu_mul(m->h1, m->h3, m->hid32, (int64_t) N * F, s), "mmdit silu * gate"))) return rc;
+        if ((rc = hipcheck(launch_silu_mul_slices(m->h1, m->h3, sp, (int64_t) N * F, m->hid32, (int64_t) N * F, s),
+                           "mmdit silu * gate")))
+            return rc;
     }
-    if (is_conv) return g_conv(m, c2, m->hid32, F, (int64_t) S * F, S, B, 1, y, ld_y, false, s);
+    if (is_conv) return g_conv(m, c2, m->hid32, F, (int64_t) S * F, S, B, 1, y, ld_y, false, s, y2_splits);
     return g_lin(m, l2, Rows{m->hid32, F, 0, 0}, N, y, ld_y, false, s);
 }
 
@@ -784,11 +809,16 @@ int run_post_f32(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         if (r[i].w->pre_only) continue;
         const Block &b = *r[i].w;
         const float *orows = m->o32 + (size_t) r[i].tok_off * H;
-        if (b.conv) rc = g_conv(m, b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s);
-        else rc = g_lin(m, b.l1, Rows{orows, H, r[i].S, ob}, B * r[i].S, r[i].part, H, false, s);
+        int sp = 1;
+        if (b.conv) {
+            if (b.l1c.type == TSK_TYPE_F32) sp = f32_splits(m, b.l1c.OC, b.l1c.KW * b.l1c.IC, r[i].S);
+            rc = g_conv(m, b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, sp);
+        } else {
+            rc = g_lin(m, b.l1, Rows{orows, H, r[i].S, ob}, B * r[i].S, r[i].part, H, false, s);
+        }
         if (rc) return rc;
         r[i].pending = true;
-        r[i].pend_split = 1;
+        r[i].pend_split = sp;
         r[i].pend_bias = b.conv ? b.l1c.b : b.l1.b;
         r[i].pend_gate = r[i].mod + 2 * H;             // gate_msa
         r[i].pend_ld = r[i].ld_mod;
@@ -804,11 +834,12 @@ int run_post_f32(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         r[i].pending = live[j++].pending;
         const Block &b = *r[i].w;
         const float *xr = (const float *) r[i].xn;
+        const int sp = b.conv && b.w2c.type == TSK_TYPE_F32 ? f32_splits(m, b.w2c.OC, b.w2c.KW * b.w2c.IC, r[i].S) : 1;
         rc = g_swiglu(m, b.conv, b.w1c, b.w3c, b.w2c, b.w1, b.w3, b.w2, xr, H, (int64_t) r[i].S * H, r[i].S, B,
-                      r[i].part, H, s);
+                      r[i].part, H, s, sp);
         if (rc) return rc;
         r[i].pending = true;
-        r[i].pend_split = 1;
+        r[i].pend_split = sp;
         r[i].pend_bias = nullptr;
         r[i].pend_gate = r[i].mod + 5 * H;             // gate_mlp
         r[i].pend_ld = r[i].ld_mod;
@@ -974,7 +1005,7 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
     a(&m->q, 2 * (size_t) B * m->Nmax * H);
     a(&m->k, 2 * (size_t) B * m->Nmax * H);
     a(&m->vt, 2 * (size_t) B * H * m->ldv);
-    a(&m->part, sizeof(float) * GRAPH_KSPLIT_MAX * rows3 * H);
+    a(&m->part, sizeof(float) * PART_SLICES * rows3 * H);
     a(&m->tmp32, sizeof(float) * R * std::max((size_t) H, L));
     a(&m->rope_l, sizeof(float) * T * 64);
     a(&m->rope_c, sizeof(float) * C * 64);
@@ -998,8 +1029,8 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
         a(&m->o32, sizeof(float) * B * m->Nmax * H);
         a(&m->qkv32, sizeof(float) * R * 3 * H);
         a(&m->hid32, sizeof(float) * R * F);
-        a(&m->h1, sizeof(float) * R * F);
-        a(&m->h3, sizeof(float) * R * F);
+        a(&m->h1, sizeof(float) * F32_KSPLIT_MAX * R * F);   // K-split slices of the F32 convMLP halves
+        a(&m->h3, sizeof(float) * F32_KSPLIT_MAX * R * F);
         // conversions: at most R rows (B * T for the per-token adaLN) of the widest input
         const size_t conv_rows = (size_t) std::max(R, (int64_t) B * T);
         if (any_bf16) {
@@ -1452,11 +1483,11 @@ int step(tsk_mmdit *m, const Call &k, const float *t, float *flow, hipStream_t s
     memset(&Cs, 0, sizeof(Cs));
     memset(&Xs, 0, sizeof(Xs));
     Ls.x = m->lat; Ls.S = T; Ls.tok_off = 0; Ls.rope_cs = m->rope_l; Ls.per_token = 1;
-    Ls.xn = xnb + es * rL * H; Ls.part = m->part + GRAPH_KSPLIT_MAX * rL * H;
+    Ls.xn = xnb + es * rL * H; Ls.part = m->part + PART_SLICES * rL * H;
     Cs.x = m->clip; Cs.S = clip_S; Cs.tok_off = T; Cs.rope_cs = m->rope_c; Cs.per_token = 0;
-    Cs.xn = xnb + es * rC * H; Cs.part = m->part + GRAPH_KSPLIT_MAX * rC * H;
+    Cs.xn = xnb + es * rC * H; Cs.part = m->part + PART_SLICES * rC * H;
     Xs.x = m->txt; Xs.S = X; Xs.tok_off = T + clip_S; Xs.rope_cs = nullptr; Xs.per_token = 0;
-    Xs.xn = xnb + es * rX * H; Xs.part = m->part + GRAPH_KSPLIT_MAX * rX * H;
+    Xs.xn = xnb + es * rX * H; Xs.part = m->part + PART_SLICES * rX * H;
     // a block's residual updates are applied by the next LayerNorm launch:
     // the stage tensors after block 0 and after the joint blocks are taken
     // right after that launch

@@ -707,6 +707,18 @@ __global__ void silu_mul_kernel(const float *a, const float *b, float *y, int64_
     if (i < n) { const float v = a[i]; y[i] = v / (1.0f + expf(-v)) * b[i]; }
 }
 
+// the same over K-split slices: a = sum of S slices of stride `stride`, b likewise, summed in slice order
+__global__ void silu_mul_slices_kernel(const float *a, const float *b, int S, int64_t stride, float *y, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = a[i], g = b[i];
+    for (int z = 1; z < S; ++z) {
+        v += a[z * stride + i];
+        g += b[z * stride + i];
+    }
+    y[i] = v / (1.0f + expf(-v)) * g;
+}
+
 __global__ void silu_kernel(float *x, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
@@ -1160,6 +1172,13 @@ hipError_t launch_rms_norm_q8(const float *x, int64_t ldx, const float *w, float
         case 4096: launch_kernel(rms_norm_q8_kernel<16>, grid, blk, 0, s, x, ldx, w, eps, qx, dx, rows); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_slices(const float *a, const float *b, int S, int64_t stride, float *y, int64_t n,
+                                  hipStream_t s) {
+    if (S < 1 || (S > 1 && stride < n)) return hipErrorInvalidValue;
+    launch_kernel(silu_mul_slices_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, a, b, S, stride, y, n);
     return hipGetLastError();
 }
 

@@ -376,6 +376,9 @@ struct F32Snake {
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake = nullptr);
 // y = silu(a) * b, f32, n elements
 hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
+// the same with a and b each the sum of S K-split slices (stride elements apart, summed in order)
+hipError_t launch_silu_mul_slices(const float *a, const float *b, int S, int64_t stride, float *y, int64_t n,
+                                  hipStream_t s);
 // y[n, m] = sum_k W[m, k] x[n, k] + bias[m]: bf16 row-major W, f32 x and y,
 // fp32 fma accumulation (the DiT's input and output projections)
 hipError_t launch_proj_f32(const uint16_t *w, const float *bias, const float *x, int64_t ld_x, int N, int K, int M,

@@ -32,6 +32,7 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_DIT_SCHED 0: the sampler computes its conditioning inside every step
 //   TSK_LN_BLOCK  1: LayerNorm rows as one workgroup each (A/B reference)
 //   TSK_GEMV_RW   rows per wave of the adaLN GEMVs (1, 2, 4)
+//   TSK_F32_KSPLIT  most K slices of the reference graph's F32 convolutions (1 = unsplit, 2, 4, 8)
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
@@ -42,6 +43,7 @@ struct Tuning {
     bool dit_sched = true;
     bool ln_block = false;
     int gemv_rw = 2;
+    int f32_ksplit = 8;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
     bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:
