@@ -193,13 +193,16 @@ def conv_bench(tsk, reps=20, B=2, S=646, H=1024, F=2816, seed=77):
     return out
 
 
-def attention_node_bench(tsk, reps=20, B=2, H=16, N=723, seed=33):
-    """The flash_attn_ext node with bf16 Q / K / V as a ggml graph hands it
-    over (the 30 s joint attention, 646 latent + 77 text tokens, 16 x 64
-    heads, B = 2; scale 1/8, F32 precision): tsk_flash_attn_ext, i.e. the V
-    transpose into the stream's workspace plus the attention kernel, on
+def attention_node_bench(tsk, reps=20, B=2, H=16, N=723, seed=33, types="ref"):
+    """The flash_attn_ext node at the 30 s joint attention (646 latent + 77
+    text tokens, 16 x 64 heads, B = 2; scale 1/8, F32 precision, f32 output) on
     device-resident N(0, 1) operands (what QK-RMSNorm leaves: rows of unit
-    RMS). us per call and TFLOP/s by 4 B H N^2 64."""
+    RMS). types "ref": the node mmdit.cpp:88-92 emits, Q F32 with K / V cast
+    to F16 (V read as rows by the kernel, one launch); "bf16": bf16 Q / K / V
+    (V transposed to fp16 first, two launches). The C entry point is called
+    with prebuilt descriptors, so the Python wrapper's own cost stays out of
+    the loop. us per call and TFLOP/s by 4 B H N^2 64."""
+    import ctypes
     import numpy as np
     rng = np.random.default_rng(seed)
 
@@ -207,22 +210,35 @@ def attention_node_bench(tsk, reps=20, B=2, H=16, N=723, seed=33):
         u = rng.standard_normal(shape, dtype=np.float32).view(np.uint32)
         return tsk.bf16_to_device(((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16))
 
-    q, k, v = bf16((B, H, N, 64)), bf16((B, H, N, 64)), bf16((B, H, N, 64))
+    if types == "ref":
+        f = lambda: rng.standard_normal((B, H, N, 64), dtype=np.float32)
+        q, k, v = tsk.to_device(f()), tsk.to_device(f().astype(np.float16)), tsk.to_device(f().astype(np.float16))
+    else:
+        q, k, v = bf16((B, H, N, 64)), bf16((B, H, N, 64)), bf16((B, H, N, 64))
     out = tsk.empty((B, N, H, 64))
+    tsk.init()
+    L = tsk.load()
+    dq, dk, dv, dd = tsk.desc(q), tsk.desc(k), tsk.desc(v), tsk.desc(out)
+    st = tsk._stream()
+    args = (ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), None, 0.125, 0.0, 0.0, tsk.PREC_F32,
+            ctypes.byref(dd), st)
     for _ in range(3):
-        tsk.flash_attn_ext(q, k, v, scale=0.125, out=out)
+        tsk.check(L.tsk_flash_attn_ext(*args))
     tsk.synchronize()
     s, e = tsk.Event(), tsk.Event()
     s.record()
+    bad = 0
     for _ in range(reps):
-        tsk.flash_attn_ext(q, k, v, scale=0.125, out=out)
+        bad |= L.tsk_flash_attn_ext(*args)
     e.record()
     tsk.synchronize()
+    tsk.check(bad)
     us = s.elapsed_ms(e) / reps * 1e3
     tf = 4.0 * B * H * N * N * 64 / (us * 1e-6) / 1e12
+    shape = ("Q F32, K / V F16 (mmdit.cpp:88-90)" if types == "ref" else "bf16 Q / K / V")
     return {"us": round(us, 2), "tflops": round(tf, 1), "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-            "shape": f"B={B} H={H} N={N} D=64, bf16 Q/K/V, f32 output",
-            "note": "includes the V transpose launch of the ggml node path"}
+            "shape": f"B={B} H={H} N={N} D=64, {shape}, f32 output",
+            "launches": 1 if types == "ref" else 2}
 
 
 def q8_blocks(rng, M, K, scale):
@@ -556,7 +572,8 @@ def main():
     # linear1 1024 -> 1024 (k3), BF16 kernels packed kw-major once, f32 input
     conv30 = conv_bench(tsk, reps=max(5, args.steps))
     # configuration 3's attention as the ggml node (bf16 Q / K / V, 723 tokens)
-    attn_node = attention_node_bench(tsk, reps=max(5, args.steps))
+    attn_node = attention_node_bench(tsk, reps=max(20, args.steps))
+    attn_node_bf16 = attention_node_bench(tsk, reps=max(20, args.steps), types="bf16")
     # the reference's own three-stream graph at 9 s and 30 s
     graph = graph_bench(tsk, max(5, args.steps // 2))
     # the VAE decode after the sampler
@@ -611,7 +628,8 @@ def main():
         "breakdown_9s": breakdown(roles9, args.steps),
         "breakdown_30s": breakdown(roles30, max(5, args.steps // 2)),
         "conv_30s": conv30,
-        "attention_node_bf16_30s": attn_node,
+        "attention_node_30s": attn_node,
+        "attention_node_bf16_30s": attn_node_bf16,
         "q8_0_projections_30s": q8,
         "q8_0_flow_step_9s": {"steps_per_s": round(1000.0 / ms_q8, 2), "ms_per_step": round(ms_q8, 4),
                               "weights": "Q8_0 attn.qkv / linear1 / ffn.fc1 / ffn.fc2 (ggml reference "

@@ -264,7 +264,9 @@ def test_workspace_size(tsk):
     qf = fake(T, T.F32, (1, 16, 420, 64), 4)
     kv = fake(T, T.F16, (1, 16, 420, 64), 2)
     o = fake(T, T.F32, (1, 420, 16, 64), 4)
-    assert ws(T.OP_FLASH_ATTN_EXT, [qf, kv, kv], o) == (0, 2 * 16 * 64 * 448)        # V^T, fp16, 64-key padded
+    assert ws(T.OP_FLASH_ATTN_EXT, [qf, kv, kv], o) == (0, 0)          # F16 V read as rows: no scratch
+    kvb = fake(T, T.BF16, (1, 16, 420, 64), 2)
+    assert ws(T.OP_FLASH_ATTN_EXT, [qf, kvb, kvb], o) == (0, 2 * 16 * 64 * 448)     # bf16 V: V^T, fp16, 64-key padded
     assert ws(T.OP_FLASH_ATTN_EXT, [qf, kv, kv, fake(T, T.F16, (1, 1, 420, 420), 2)], o) == (0, 0)   # masked: none
     w = kernel_desc(T, T.BF16, 2816, 1024, 3, 2)                    # ggml layout: packed per call
     x = fake(T, T.F32, (2, 646, 1024), 4)

@@ -27,15 +27,16 @@ def bf16_bits(a):
 
 def operands(tsk, seed):
     """a BF16 GEMM with f32 activations (scratch: the bf16 rows) and a fast-path
-    flash attention (scratch: V transposed), two different sizes per seed"""
+    flash attention with bf16 K / V (scratch: V transposed to fp16; F16 V is
+    read as rows and takes none), two different sizes per seed"""
     rng = np.random.default_rng(seed)
     N = 300 + 50 * seed
     w = tsk.bf16_to_device(bf16_bits(rng.standard_normal((1024, 1024)) * 0.02))
     x = tsk.to_device(rng.standard_normal((N, 1024)).astype(np.float32))
     nq = 200 + 70 * seed
     q = tsk.to_device(rng.standard_normal((2, 16, nq, 64)).astype(np.float32))
-    k = tsk.to_device(rng.standard_normal((2, 16, nq, 64)).astype(np.float16))
-    v = tsk.to_device(rng.standard_normal((2, 16, nq, 64)).astype(np.float16))
+    k = tsk.bf16_to_device(bf16_bits(rng.standard_normal((2, 16, nq, 64))))
+    v = tsk.bf16_to_device(bf16_bits(rng.standard_normal((2, 16, nq, 64))))
     return w, x, q, k, v
 
 

@@ -27,6 +27,9 @@
 // V^T positions are permuted inside every group of 16 keys (bits 2 and 3 of
 // the key index swapped, an involution) so that each lane's A operand of
 // V^T . P^T is one 16-byte LDS read that matches the keys its P^T slots hold.
+// VROWS (the flash_attn_ext node with F16 V): V tiles come in as rows, like
+// K, and each A operand is two ds_read_b64_tr_b16 transposing reads (4 keys x
+// 16 dims per 16 lanes), so the node needs no V^T pass of its own.
 // Softmax state is rescaled lazily: the running max only moves when a tile's
 // max exceeds it by more than 8 (a factor 256 in fp16 P), which is exact in
 // real arithmetic and keeps P <= 256.
@@ -47,6 +50,17 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i's element j is
+// element i % 4 of the 8 bytes lane 4 j + i / 4 addresses. With lane s of the
+// group addressing row r0 + s / 4, columns c0 + 4 (s % 4) .. + 3 of a
+// row-major 16-bit matrix, lane i receives rows r0 .. r0 + 3 of column c0 + i.
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *) (p));
+}
 
 constexpr int KT = 64;                  // keys per tile
 constexpr int TILE_H = 2 * KT * 64;     // halves per tile buffer: K [64][64] then V^T [64][64]
@@ -86,8 +100,9 @@ __device__ __forceinline__ u32x4 load_q8(const char *row, int d0, int q_type, fl
     return r;
 }
 
-template <bool KBF16, bool BOUNDED, int KS, int QB>
+template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
+    static_assert(!VROWS || (!KBF16 && !BOUNDED), "V rows: fp16 K, running max");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     constexpr int NB = nbuf(KS, QB);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -110,7 +125,8 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 
     const char *qp = (const char *) p.q + (int64_t) h * p.q_nb2 + (int64_t) b * p.q_nb3;
     const char *kp = (const char *) p.k + (int64_t) h * p.k_nb2 + (int64_t) b * p.k_nb3;
-    const uint16_t *vp = p.vt + (int64_t) bh * p.vt_bh;
+    const char *vp = VROWS ? (const char *) p.v + (int64_t) h * p.v_nb2 + (int64_t) b * p.v_nb3
+                           : (const char *) (p.vt + (int64_t) bh * p.vt_bh);
 
     // Q^T fragments (B operand): lane holds Q[q0 + l32][16 ks + 8 hi + 0..7]
     const int q0 = qt * (QB * 32) + qb * 32;
@@ -140,10 +156,26 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     // below) read as zeros.
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc((void *) kp, (short) 0, (int) ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128), 0x00020000);
-    const __amdgpu_buffer_rsrc_t vrs =
-        __builtin_amdgcn_make_buffer_rsrc((void *) vp, (short) 0, (int) (64 * p.ldv * 2), 0x00020000);
+    // V rows (VROWS) end like K's; their chunks are swizzled by 2 (R % 4) instead
+    // of (R / 2) % 8, fixed per lane (R % 4 = (lane / 8) % 4), so that the four
+    // rows of a transposing read hit four distinct pairs of 16-byte slots
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) vp, (short) 0, VROWS ? (int) ((int64_t) (p.Nkv - 1) * p.v_nb1 + 128) : (int) (64 * p.ldv * 2),
+        0x00020000);
     const uint32_t koff0 = (uint32_t) (r8 * p.k_nb1 + ch0 * 16), koff1 = (uint32_t) (r8 * p.k_nb1 + ch1 * 16);
-    const uint32_t voff0 = (uint32_t) (2 * (r8 * p.ldv + ch0 * 8)), voff1 = (uint32_t) (2 * (r8 * p.ldv + ch1 * 8));
+    const uint32_t voff0 = VROWS ? (uint32_t) (r8 * p.v_nb1 + (((lane & 7) ^ (2 * (r8 & 3))) * 16))
+                                 : (uint32_t) (2 * (r8 * p.ldv + ch0 * 8));
+    const uint32_t voff1 = VROWS ? voff0 : (uint32_t) (2 * (r8 * p.ldv + ch1 * 8));
+    // VROWS: this lane's offset (halves) of its first transposing read of a
+    // 16-key group, per 32-dim block db: row 4 hi + (l16 / 4), column
+    // 32 db + 16 (l / 16 % 2) + 4 (l16 % 4) (l16 = lane % 16), swizzled
+    int vr_off[2] = {0, 0};
+    if constexpr (VROWS) {
+        const int l16 = lane & 15, grp = (lane >> 4) & 1;
+        const int lo = (2 * grp + ((l16 & 3) >> 1)) ^ (2 * ((l16 >> 2) & 3));
+#pragma unroll
+        for (int db = 0; db < 2; ++db) vr_off[db] = (4 * hi + (l16 >> 2)) * 64 + ((lo ^ (4 * db)) << 3) + 4 * (l16 & 1);
+    }
     auto issue = [&](int tile, int buf) {
         uint16_t *dst = gb + buf * TILE_H;
         const int key0 = tile * KT;
@@ -154,6 +186,9 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
             if (j < 8)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void *) (dst + j * 512), 16, (j & 1) ? koff1 : koff0,
                                                          (int) ((key0 + (j & 7) * 8) * p.k_nb1), 0, 0);
+            else if constexpr (VROWS)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *) (dst + j * 512), 16, voff0,
+                                                         (int) ((key0 + (j & 7) * 8) * p.v_nb1), 0, 0);
             else
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void *) (dst + j * 512), 16, (j & 1) ? voff1 : voff0,
                                                          2 * ((j & 7) * 8 * p.ldv + key0), 0, 0);
@@ -309,7 +344,17 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) vf[db][cc] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
+                for (int cc = 0; cc < 4; ++cc) {
+                    if constexpr (VROWS) {
+                        // keys 16 cc + 4 hi + 0..3 and 16 cc + 8 + 4 hi + 0..3: the P^T slots of this lane
+                        const s16x4 a = lds_read_tr16(vb + vr_off[db] + 16 * cc * 64);
+                        const s16x4 c2 = lds_read_tr16(vb + vr_off[db] + (16 * cc + 8) * 64);
+                        const s16x8 v8 = {a[0], a[1], a[2], a[3], c2[0], c2[1], c2[2], c2[3]};
+                        vf[db][cc] = __builtin_bit_cast(f16x8, v8);
+                    } else {
+                        vf[db][cc] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
+                    }
+                }
             const int lim = tile == ntiles - 1 ? p.Nkv - tile * KT : KT;
             // softmax and P.V per 32-key half: the second half's MFMAs overlap
             // the first half's exponentials, the first half's P.V the second's
@@ -469,7 +514,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     }
 }
 
-template <bool KBF16, bool BOUNDED, int KS, int QB>
+template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS = false>
 hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     AttnFastParams p = p0;
     p.qtiles = (p.Nq + QB * 32 - 1) / (QB * 32);
@@ -477,22 +522,22 @@ hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     const int grid = (W + 7) / 8 * 8;
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
     if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128) * 4);
-    auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB>;
+    auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB, VROWS>;
     lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(grid), dim3(64 * KS * QB), lds, s, p);
     return hipGetLastError();
 }
 
-template <bool KBF16, bool BOUNDED>
+template <bool KBF16, bool BOUNDED, bool VROWS = false>
 hipError_t launch_cfg(const AttnFastParams &p, int cfg, hipStream_t s) {
     switch (cfg) {
-        case 41: return launch_ks_qb<KBF16, BOUNDED, 4, 1>(p, s);
-        case 42: return launch_ks_qb<KBF16, BOUNDED, 4, 2>(p, s);
-        case 43: return launch_ks_qb<KBF16, BOUNDED, 4, 3>(p, s);
-        case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1>(p, s);
-        case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2>(p, s);
-        case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4>(p, s);
-        case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4>(p, s);
+        case 41: return launch_ks_qb<KBF16, BOUNDED, 4, 1, VROWS>(p, s);
+        case 42: return launch_ks_qb<KBF16, BOUNDED, 4, 2, VROWS>(p, s);
+        case 43: return launch_ks_qb<KBF16, BOUNDED, 4, 3, VROWS>(p, s);
+        case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1, VROWS>(p, s);
+        case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2, VROWS>(p, s);
+        case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4, VROWS>(p, s);
+        case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4, VROWS>(p, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -575,12 +620,22 @@ int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16) {
 }
 
 hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
-    if (p.Nq < 1 || p.Nkv < 1 || p.H < 1 || p.B < 1 || p.ldv < (p.Nkv + KT - 1) / KT * KT) return hipErrorInvalidValue;
+    if (p.Nq < 1 || p.Nkv < 1 || p.H < 1 || p.B < 1 || (!p.v_rows && p.ldv < (p.Nkv + KT - 1) / KT * KT))
+        return hipErrorInvalidValue;
     // buffer descriptors: 31-bit byte ranges per (batch, head)
     if ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128 >= ((int64_t) 1 << 31) || p.k_nb1 < 128 ||
-        (int64_t) 128 * p.ldv >= ((int64_t) 1 << 31))
+        (!p.v_rows && (int64_t) 128 * p.ldv >= ((int64_t) 1 << 31)))
         return hipErrorInvalidValue;
     const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.k_bf16);
+    if (p.v_rows) {
+        // F16 V rows through the transposing LDS reads: fp16 K, running max;
+        // 16-byte aligned rows, 31-bit byte range per (batch, head) like K
+        if (p.k_bf16 || p.bounded || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
+                                              (uint64_t) p.v_nb3) % 16 || p.v_nb1 < 128 ||
+            (int64_t) (p.Nkv - 1) * p.v_nb1 + 128 >= ((int64_t) 1 << 31))
+            return hipErrorInvalidValue;
+        return launch_cfg<false, false, true>(p, cfg, s);
+    }
     if (p.bounded && !p.k_bf16) return launch_cfg<false, true>(p, cfg, s);
     return p.k_bf16 ? launch_cfg<true, false>(p, cfg, s) : launch_cfg<false, false>(p, cfg, s);
 }

@@ -615,10 +615,19 @@ bool fa_fast_eligible(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor
     return true;
 }
 
-// scratch of the fast path: V transposed to fp16 [B * H][64][ldv]
+// F16 V (the cast mmdit.cpp:90 makes) goes to the kernel as rows: 16-byte
+// aligned rows (validate_fa) and a 31-bit byte range per (batch, head)
+bool fa_v_rows(const tsk_tensor *k, const tsk_tensor *v) {
+    if (v->type != TSK_TYPE_F16 || k->type != TSK_TYPE_F16 || !aligned(v->data, 16)) return false;
+    for (int i = 1; i < 4; ++i)
+        if (v->nb[i] % 16) return false;
+    return v->nb[1] >= 128 && (int64_t) (v->ne[1] - 1) * (int64_t) v->nb[1] + 128 < ((int64_t) 1 << 31);
+}
+
+// scratch of the fast path: V transposed to fp16 [B * H][64][ldv] (none for V rows)
 size_t fa_ws_bytes(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v, const tsk_tensor *mask,
                    float max_bias, float softcap, const tsk_tensor *dst) {
-    if (!fa_fast_eligible(q, k, v, mask, max_bias, softcap, dst)) return 0;
+    if (!fa_fast_eligible(q, k, v, mask, max_bias, softcap, dst) || fa_v_rows(k, v)) return 0;
     const int64_t ldv = (k->ne[1] + 63) / 64 * 64;
     return align256((size_t) 2 * q->ne[3] * q->ne[2] * 64 * ldv);
 }
@@ -632,18 +641,26 @@ extern "C" int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, cons
     if (rc) return rc;
     if ((rc = require_init())) return rc;
     if (fa_fast_eligible(q, k, v, mask, max_bias, logit_softcap, dst)) {
-        // transposed fp16 V in the workspace, then the MFMA 32x32 kernel
+        // the MFMA 32x32 kernel: F16 V as rows, else V transposed to fp16 in
+        // the workspace first
         const int Nkv = (int) k->ne[1], H = (int) q->ne[2], B = (int) q->ne[3];
         const int ldv = (Nkv + 63) / 64 * 64;
-        void *ws = nullptr;
         hipStream_t st = (hipStream_t) stream;
-        if ((rc = workspace(st, fa_ws_bytes(q, k, v, mask, max_bias, logit_softcap, dst), &ws))) return rc;
-        hipError_t e = launch_vt_transpose(v->data, v->type == TSK_TYPE_BF16, (int64_t) v->nb[1], (int64_t) v->nb[2],
-                                           (int64_t) v->nb[3], Nkv, H, B, (uint16_t *) ws, ldv, st);
-        if (e != hipSuccess) return hip_fail(e, "flash_attn_ext V transpose");
         AttnFastParams f;
         memset(&f, 0, sizeof(f));
-        f.q = q->data; f.k = k->data; f.vt = (const uint16_t *) ws; f.o = dst->data;
+        hipError_t e;
+        if (fa_v_rows(k, v)) {
+            f.v = v->data; f.v_nb1 = v->nb[1]; f.v_nb2 = v->nb[2]; f.v_nb3 = v->nb[3];
+            f.v_rows = 1;
+        } else {
+            void *ws = nullptr;
+            if ((rc = workspace(st, fa_ws_bytes(q, k, v, mask, max_bias, logit_softcap, dst), &ws))) return rc;
+            e = launch_vt_transpose(v->data, v->type == TSK_TYPE_BF16, (int64_t) v->nb[1], (int64_t) v->nb[2],
+                                    (int64_t) v->nb[3], Nkv, H, B, (uint16_t *) ws, ldv, st);
+            if (e != hipSuccess) return hip_fail(e, "flash_attn_ext V transpose");
+            f.vt = (const uint16_t *) ws;
+        }
+        f.q = q->data; f.k = k->data; f.o = dst->data;
         f.q_type = q->type; f.k_bf16 = k->type == TSK_TYPE_BF16; f.out_bf16 = dst->type == TSK_TYPE_BF16;
         f.Nq = (int) q->ne[1]; f.Nkv = Nkv; f.H = H; f.B = B;
         f.q_nb1 = q->nb[1]; f.q_nb2 = q->nb[2]; f.q_nb3 = q->nb[3];

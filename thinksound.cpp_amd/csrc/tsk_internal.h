@@ -67,7 +67,10 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 // ggml's permuted [D, H, Nq, B] byte strides. c = scale * log2(e).
 struct AttnFastParams {
     const void *q, *k;
-    const uint16_t *vt;
+    const uint16_t *vt;  // V^T (below), or with v_rows the F16 V rows themselves:
+    const void *v;       // v_rows: F16 rows of 64 (ggml strides v_nb1..3, 16-byte aligned)
+    int64_t v_nb1, v_nb2, v_nb3;
+    int v_rows;          // fp16 K only, unbounded: V read as rows, transposed by the LDS reads
     void *o;
     int q_type, k_bf16, out_bf16;
     int Nq, Nkv, H, B;
