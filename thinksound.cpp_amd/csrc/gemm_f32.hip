@@ -11,12 +11,14 @@
 // (4 * (l / 16) + t, t = 0..3), consumed by four MFMAs, so one K block of 16
 // costs TM + TN LDS reads for 4 * TM * TN MFMAs.
 //
-// Workgroup = 2 x 2 waves, each TM x TN 16x16 tiles; operand tiles are
-// double buffered through LDS (global -> registers -> LDS, one barrier per
-// 32-wide K step). The activation rows may be an implicit im2col of a
-// channels-fastest input (GemmProblem::conv_ic, as in gemm_group.hip).
+// Workgroup = 2 x 2 waves, each TM x TN 16x16 tiles (4 x 4 or 4 x 2, by the
+// launcher's rule below); operand tiles are double buffered through LDS
+// (global -> registers -> LDS, one barrier per 32-wide K step). The
+// activation rows may be an implicit im2col of a channels-fastest input
+// (GemmProblem::conv_ic, as in gemm_group.hip).
 #include "tsk_common.h"
 #include "tsk_internal.h"
+#include "tsk_runtime.h"
 
 namespace tsk {
 
@@ -199,10 +201,19 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
     }
 }
 
+template <int TM, int TN>
+void launch_tiles(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake) {
+    constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
+    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, p.splits > 1 ? p.splits : 1);
+    const F32Snake none = {nullptr, nullptr, nullptr, 1};
+    if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true, false>), grid, dim3(NT), 0, s, p, none);
+    else if (snake) launch_kernel((gemm_f32_kernel<TM, TN, false, true>), grid, dim3(NT), 0, s, p, *snake);
+    else launch_kernel((gemm_f32_kernel<TM, TN, false, false>), grid, dim3(NT), 0, s, p, none);
+}
+
 }  // namespace
 
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake) {
-    constexpr int TM = 4, TN = 2, BM = 2 * TM * 16, BN = 2 * TN * 16;
     if (p.M < 1 || p.N < 1 || p.K < 4 || (p.K & 3) || !p.wf || (p.accumulate && y_bf16)) return hipErrorInvalidValue;
     // split-K slices [splits][N][ld_y] of f32 partial sums: no bias, epilogue or accumulation
     const int S = p.splits > 1 ? p.splits : 1;
@@ -212,11 +223,26 @@ hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, cons
     if (p.conv_ic && (p.conv_ic % 4 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;
-    dim3 grid((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, S);
-    const F32Snake none = {nullptr, nullptr, nullptr, 1};
-    if (y_bf16) launch_kernel((gemm_f32_kernel<TM, TN, true, false>), grid, dim3(NT), 0, s, p, none);
-    else if (snake) launch_kernel((gemm_f32_kernel<TM, TN, false, true>), grid, dim3(NT), 0, s, p, *snake);
-    else launch_kernel((gemm_f32_kernel<TM, TN, false, false>), grid, dim3(NT), 0, s, p, none);
+    // 128 x 128 workgroup tiles (4 x 4 per wave, 72 KiB of LDS: two workgroups
+    // per CU) for plain epilogues with at least 256 such tiles whose
+    // workgroups stream a long K: 7-14 % faster than 128 x 64 on the VAE's
+    // residual k1 convolutions and the graph's convMLP w1 / w3 (K = 3072 in
+    // two slices). 128 x 64 otherwise: short K-split slices (the graph's w2,
+    // K = 8448 in 8 slices: 10 % slower on the larger tile), few tiles (the
+    // final k7 convolution's 4-11), and the SnakeBeta epilogue, whose sinf
+    // takes scratch memory next to 64 accumulators a lane (50 % slower).
+    // Every tile shape sums each output in the same order: the same bits.
+    int tile = tuning().f32_tile;
+    if (tile == 0) {
+        const int64_t tiles44 = (int64_t) ((p.M + 127) / 128) * ((p.N + 127) / 128) * S;
+        tile = (!snake && tiles44 >= 256 && (S == 1 || p.K / S >= 1200)) ? 44 : 42;
+    }
+    switch (tile) {
+        case 44: launch_tiles<4, 4>(p, y_bf16, s, snake); break;
+        case 24: launch_tiles<2, 4>(p, y_bf16, s, snake); break;
+        case 22: launch_tiles<2, 2>(p, y_bf16, s, snake); break;
+        default: launch_tiles<4, 2>(p, y_bf16, s, snake); break;
+    }
     return hipGetLastError();
 }
 
