@@ -719,6 +719,86 @@ __global__ void silu_mul_slices_kernel(const float *a, const float *b, int S, in
     y[i] = v / (1.0f + expf(-v)) * g;
 }
 
+// Convolution with few output channels (the VAE's final k7, 128 -> 2
+// channels): stride 1, dilation 1, channels-fastest rows x [T][64 NI] in,
+// planar y[oc][t] (row stride ld_y) out. One wave streams PW consecutive
+// output positions: lane l holds channels l + 64 j of the KW input rows of
+// the window in registers (zero outside [0, T)), one new row per position,
+// prefetched CONV_SO_D rows ahead; each output is a wave sum of per-lane
+// fp32 sums (kw, then j); lane (t - t0) % 64 keeps position t and stores 64
+// positions per channel at once. A 128-row GEMM tile would carry 126 zero
+// rows for these 2 outputs.
+constexpr int CONV_SO_D = 8;
+template <int NI, int KW, int OC>
+__global__ __launch_bounds__(256) void conv_small_oc_kernel(const float *x, int T, const float *w, const float *bias,
+                                                            int pad, float *y, int64_t ld_y, int PW) {
+    constexpr int IC = 64 * NI, D = CONV_SO_D;
+    const int lane = threadIdx.x & 63;
+    const int t0 = (int) (blockIdx.x * 4 + (threadIdx.x >> 6)) * PW;
+    if (t0 >= T) return;
+    const int tend = min(T, t0 + PW);
+    float wr[OC][KW][NI];
+#pragma unroll
+    for (int oc = 0; oc < OC; ++oc)
+#pragma unroll
+        for (int kw = 0; kw < KW; ++kw)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) wr[oc][kw][j] = w[(int64_t) (oc * KW + kw) * IC + 64 * j + lane];
+    auto row = [&](int r, float (&dst)[NI]) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j) dst[j] = (r >= 0 && r < T) ? x[(int64_t) r * IC + 64 * j + lane] : 0.0f;
+    };
+    // window slot kw holds input row t - pad + kw at position t; before t0,
+    // slots 1 .. KW - 1 hold rows t0 - pad .. t0 - pad + KW - 2
+    float win[KW][NI];
+#pragma unroll
+    for (int kw = 1; kw < KW; ++kw) row(t0 - pad + kw - 1, win[kw]);
+    float pf[D][NI], nx[D][NI];
+#pragma unroll
+    for (int i = 0; i < D; ++i) row(t0 - pad + KW - 1 + i, pf[i]);
+    float keep[OC];
+#pragma unroll
+    for (int oc = 0; oc < OC; ++oc) keep[oc] = 0.0f;
+    for (int tc = t0; tc < tend; tc += D) {
+        if (tc + D < tend) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) row(tc + D - pad + KW - 1 + i, nx[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int t = tc + i;
+            if (t >= tend) break;
+#pragma unroll
+            for (int kw = 0; kw + 1 < KW; ++kw)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) win[kw][j] = win[kw + 1][j];
+#pragma unroll
+            for (int j = 0; j < NI; ++j) win[KW - 1][j] = pf[i][j];
+            const int slot = (t - t0) & 63;
+#pragma unroll
+            for (int oc = 0; oc < OC; ++oc) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int kw = 0; kw < KW; ++kw)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j) acc = fmaf(wr[oc][kw][j], win[kw][j], acc);
+                acc = wave_sum(acc);
+                if (lane == slot) keep[oc] = acc;
+            }
+            if (slot == 63 || t == tend - 1) {
+                const int tb = t - slot;
+                if (lane <= slot)
+#pragma unroll
+                    for (int oc = 0; oc < OC; ++oc) y[oc * ld_y + tb + lane] = keep[oc] + (bias ? bias[oc] : 0.0f);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < D; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) pf[i][j] = nx[i][j];
+    }
+}
+
 __global__ void silu_kernel(float *x, int64_t n) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) { const float v = x[i]; x[i] = v / (1.0f + __expf(-v)); }
@@ -1172,6 +1252,18 @@ hipError_t launch_rms_norm_q8(const float *x, int64_t ldx, const float *w, float
         case 4096: launch_kernel(rms_norm_q8_kernel<16>, grid, blk, 0, s, x, ldx, w, eps, qx, dx, rows); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_small_oc(const float *x, int T, int IC, int KW, int OC, const float *w, const float *bias,
+                                 int pad, float *y, int64_t ld_y, hipStream_t s) {
+    constexpr int PW = 256;
+    if (T < 1 || pad < 0 || ld_y < T || !x || !w || !y) return hipErrorInvalidValue;
+    const dim3 grid((unsigned) (((T + PW - 1) / PW + 3) / 4));
+    if (IC == 128 && KW == 7 && OC == 2)
+        launch_kernel((conv_small_oc_kernel<2, 7, 2>), grid, dim3(256), 0, s, x, T, w, bias, pad, y, ld_y, PW);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -400,6 +400,12 @@ hipError_t launch_timestep_embed(const float *freq, const TimeVals &tv, int B, i
 hipError_t launch_silu_bf16(const float *x, uint16_t *y, int64_t n, hipStream_t s);
 // [B][C][T] -> [B][T][C] (f32); y[r][c] = x[r][c] + pe[r % period][c]
 hipError_t launch_transpose_ct(const float *x, int B, int C, int T, float *y, hipStream_t s);
+// stride-1, dilation-1 convolution of channels-fastest rows x [T][IC] into
+// planar y[oc][t] (row stride ld_y) with OC <= 2 output channels: weights
+// [OC][KW][IC], zero padding `pad`, optional bias. IC = 128, KW = 7, OC = 2
+// (the VAE's final convolution); other shapes: hipErrorInvalidValue
+hipError_t launch_conv_small_oc(const float *x, int T, int IC, int KW, int OC, const float *w, const float *bias,
+                                 int pad, float *y, int64_t ld_y, hipStream_t s);
 hipError_t launch_add_period_rows(const float *x, int64_t rows, int cols, const float *pe, int period, float *y,
                                   hipStream_t s);
 hipError_t launch_add_f32(const float *a, const float *b, float *y, int64_t n, hipStream_t s);

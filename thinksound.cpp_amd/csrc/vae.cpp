@@ -334,7 +334,14 @@ int decode_impl(tsk_vae *v, int T, const float *latent_d, float *audio_d, hipStr
             if ((rc = conv(v, rp + ".layers.3", true, t, C, (int) frames, 0, 1, x, true, st, &sk))) return rc;
         }
     }
-    // conv k7 (no bias) of the final snake -> rows [T_audio][out_channels] -> planar
+    // conv k7 (no bias) of the final snake -> planar audio [out_channels][T_audio]:
+    // the stream-per-wave kernel for 128 -> 2 channels, else the GEMM's rows
+    // [T_audio][out_channels] and a transpose
+    const VW &wf = wi(v, "decoder.layers.7.weight");
+    if (C == 128 && wf.ne[0] == 7 && c.out_channels == 2)
+        return hipcheck(launch_conv_small_oc(sx, (int) frames, C, 7, 2, wp(v, "decoder.layers.7.weight"), nullptr, 3,
+                                             audio_d, frames, st),
+                        "vae final convolution");
     if ((rc = conv(v, "decoder.layers.7", false, sx, C, (int) frames, 3, 1, t, false, st))) return rc;
     return hipcheck(launch_transpose_ct(t, 1, (int) frames, c.out_channels, audio_d, st), "vae audio");
 }
