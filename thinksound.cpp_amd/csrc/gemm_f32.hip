@@ -34,8 +34,11 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
     constexpr int WCH = BM * (BK / 4), XCH = BN * (BK / 4);   // 16-B chunks per tile
     constexpr int WPER = WCH / NT, XPER = XCH / NT;
     static_assert(WCH % NT == 0 && XCH % NT == 0, "tile chunks");
-    __shared__ __attribute__((aligned(16))) float Ws[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) float Xs[2][BN * LDK];
+    // operand buffers Ws[2][BM * LDK] and Xs[2][BN * LDK]; after the K loop
+    // the same LDS holds the workgroup's output tile for the epilogue
+    __shared__ __attribute__((aligned(16))) float smem[2 * (BM + BN) * LDK];
+    float (*Ws)[BM * LDK] = reinterpret_cast<float (*)[BM * LDK]>(smem);
+    float (*Xs)[BN * LDK] = reinterpret_cast<float (*)[BN * LDK]>(smem + 2 * BM * LDK);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -134,66 +137,83 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmProblem p, const
         __syncthreads();
     }
 
-    for (int i = 0; i < TM; ++i) {
-        const int m0 = bm0 + (wm * TM + i) * 16 + 4 * lg;
-        if (m0 >= p.M) continue;
-        const bool full = m0 + 3 < p.M;
-        float bv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p.bias)
-            for (int r = 0; r < 4 && m0 + r < p.M; ++r) bv[r] = p.bias[m0 + r];
-        float ea[4] = {0.f, 0.f, 0.f, 0.f}, eb[4] = {0.f, 0.f, 0.f, 0.f};
+    // ---- epilogue through LDS: the accumulators as the workgroup's [BN][BM]
+    // tile (row stride LDT), then four consecutive outputs of one token per
+    // thread, BM / 4 threads a token row: whole-row stores of y / y2, and
+    // the SnakeBeta's sinf with one group of values live at a time
+    constexpr int LDT = BM + 4;
+    static_assert(BN * LDT <= 2 * (BM + BN) * LDK, "output tile fits the operand buffers");
+    float *tile = smem;
+    for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < TN; ++j)
+            *(f32x4 *) &tile[((wn * TN + j) * 16 + lr) * LDT + (wm * TM + i) * 16 + 4 * lg] = acc[i][j];
+    __syncthreads();
+    // NT is a multiple of BM / 4: a thread keeps one group of four output
+    // channels (its bias and SnakeBeta factors loaded once) over NT / (BM / 4)
+    // token rows apart
+    constexpr int G = BM / 4;
+    static_assert(NT % G == 0, "fixed channel group per thread");
+    const int ml = (tid % G) * 4, m0 = bm0 + ml;
+    if (m0 >= p.M) return;
+    const bool full = m0 + 3 < p.M;
+    float bv[4], ea[4], eb[4];
+    for (int r = 0; r < 4; ++r) {
+        const bool in = m0 + r < p.M;
+        bv[r] = (p.bias && in) ? p.bias[m0 + r] : 0.0f;
+        ea[r] = eb[r] = 0.0f;
         if constexpr (SNAKE) {
             const int c0 = m0 % sk.period;   // period is a multiple of 4: c0 + 3 < period
-            for (int r = 0; r < 4 && m0 + r < p.M; ++r) {
+            if (in) {
                 ea[r] = sk.ea[c0 + r];
                 eb[r] = sk.eb[c0 + r];
             }
         }
-        for (int j = 0; j < TN; ++j) {
-            const int n = bn0 + (wn * TN + j) * 16 + lr;
-            if (n >= p.N) continue;
-            float o[4];
-            for (int r = 0; r < 4; ++r) o[r] = acc[i][j][r] + bv[r];
-            if constexpr (YBF16) {
-                uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
-                for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
-            } else {
-                float *yr = (float *) p.y + (int64_t) z * p.N * p.ld_y + (int64_t) n * p.ld_y + m0;
-                float v[4];
-                if (p.accumulate) {
-                    if (full) {
-                        const f32x4 a = *(const f32x4 *) yr;
-                        for (int r = 0; r < 4; ++r) v[r] = a[r] + o[r];
-                    } else {
-                        for (int r = 0; r < 4; ++r) v[r] = m0 + r < p.M ? yr[r] + o[r] : 0.0f;
-                    }
-                } else {
-                    for (int r = 0; r < 4; ++r) v[r] = o[r];
-                }
-                float sv[4];
-                if constexpr (SNAKE)
-                    for (int r = 0; r < 4; ++r) {
-                        const float sn = sinf(v[r] * ea[r]);
-                        sv[r] = v[r] + (sn * sn) * eb[r];
-                    }
-                // y: the snake in place (SNAKE without y2) or the plain value;
-                // y2: the snake next to it
-                const bool in_place = SNAKE && !sk.y2;
-                float w[4];
-                for (int r = 0; r < 4; ++r) w[r] = in_place ? sv[r] : v[r];
+    }
+    for (int nl = tid / G; nl < BN; nl += NT / G) {
+        const int n = bn0 + nl;
+        if (n >= p.N) break;
+        const f32x4 a4 = *(const f32x4 *) &tile[nl * LDT + ml];
+        float o[4];
+        for (int r = 0; r < 4; ++r) o[r] = a4[r] + bv[r];
+        if constexpr (YBF16) {
+            uint16_t *yr = (uint16_t *) p.y + (int64_t) n * p.ld_y + m0;
+            for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = f32_to_bf16_bits(o[r]);
+        } else {
+            float *yr = (float *) p.y + (int64_t) z * p.N * p.ld_y + (int64_t) n * p.ld_y + m0;
+            float v[4];
+            if (p.accumulate) {
                 if (full) {
-                    *(f32x4 *) yr = f32x4{w[0], w[1], w[2], w[3]};
+                    const f32x4 a = *(const f32x4 *) yr;
+                    for (int r = 0; r < 4; ++r) v[r] = a[r] + o[r];
                 } else {
-                    for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = w[r];
+                    for (int r = 0; r < 4; ++r) v[r] = m0 + r < p.M ? yr[r] + o[r] : 0.0f;
                 }
-                if constexpr (SNAKE) {
-                    if (sk.y2) {
-                        float *y2r = sk.y2 + (int64_t) n * p.ld_y + m0;
-                        if (full) {
-                            *(f32x4 *) y2r = f32x4{sv[0], sv[1], sv[2], sv[3]};
-                        } else {
-                            for (int r = 0; r < 4 && m0 + r < p.M; ++r) y2r[r] = sv[r];
-                        }
+            } else {
+                for (int r = 0; r < 4; ++r) v[r] = o[r];
+            }
+            float sv[4];
+            if constexpr (SNAKE)
+                for (int r = 0; r < 4; ++r) {
+                    const float sn = sinf(v[r] * ea[r]);
+                    sv[r] = v[r] + (sn * sn) * eb[r];
+                }
+            // y: the snake in place (SNAKE without y2) or the plain value;
+            // y2: the snake next to it
+            const bool in_place = SNAKE && !sk.y2;
+            float w[4];
+            for (int r = 0; r < 4; ++r) w[r] = in_place ? sv[r] : v[r];
+            if (full) {
+                *(f32x4 *) yr = f32x4{w[0], w[1], w[2], w[3]};
+            } else {
+                for (int r = 0; r < 4 && m0 + r < p.M; ++r) yr[r] = w[r];
+            }
+            if constexpr (SNAKE) {
+                if (sk.y2) {
+                    float *y2r = sk.y2 + (int64_t) n * p.ld_y + m0;
+                    if (full) {
+                        *(f32x4 *) y2r = f32x4{sv[0], sv[1], sv[2], sv[3]};
+                    } else {
+                        for (int r = 0; r < 4 && m0 + r < p.M; ++r) y2r[r] = sv[r];
                     }
                 }
             }
@@ -224,18 +244,17 @@ hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, cons
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;
     // 128 x 128 workgroup tiles (4 x 4 per wave, 72 KiB of LDS: two workgroups
-    // per CU) for plain epilogues with at least 256 such tiles whose
-    // workgroups stream a long K: 7-14 % faster than 128 x 64 on the VAE's
-    // residual k1 convolutions and the graph's convMLP w1 / w3 (K = 3072 in
-    // two slices). 128 x 64 otherwise: short K-split slices (the graph's w2,
-    // K = 8448 in 8 slices: 10 % slower on the larger tile), few tiles (the
-    // final k7 convolution's 4-11), and the SnakeBeta epilogue, whose sinf
-    // takes scratch memory next to 64 accumulators a lane (50 % slower).
-    // Every tile shape sums each output in the same order: the same bits.
+    // per CU) where there are enough such tiles and each workgroup streams a
+    // long K: 7-14 % faster than 128 x 64 on the VAE's convolutions (k7 at
+    // 128-1024 channels 62.5-67.7 -> 69.7-74.2 % of the fp32 peak) and the
+    // graph's convMLP w1 / w3 (K = 3072 in two slices). 128 x 64 otherwise:
+    // short K-split slices (the graph's w2, K = 8448 in 8 slices: 10 % slower
+    // on the larger tile) and few tiles. Every tile shape sums each output in
+    // the same order: the same bits.
     int tile = tuning().f32_tile;
     if (tile == 0) {
         const int64_t tiles44 = (int64_t) ((p.M + 127) / 128) * ((p.N + 127) / 128) * S;
-        tile = (!snake && tiles44 >= 256 && (S == 1 || p.K / S >= 1200)) ? 44 : 42;
+        tile = (tiles44 >= tuning().f32_t44 && (S == 1 || p.K / S >= 1200)) ? 44 : 42;
     }
     switch (tile) {
         case 44: launch_tiles<4, 4>(p, y_bf16, s, snake); break;

@@ -33,7 +33,8 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_LN_BLOCK  1: LayerNorm rows as one workgroup each (A/B reference)
 //   TSK_GEMV_RW   rows per wave of the adaLN GEMVs (1, 2, 4)
 //   TSK_F32_KSPLIT  most K slices of the reference graph's F32 convolutions (1 = unsplit, 2, 4, 8)
-//   TSK_F32_TILE  F32 GEMM wave tiles, 10 * (16-row tiles) + 16-column tiles per wave (0 = 42, 44, 24, 22)
+//   TSK_F32_TILE  F32 GEMM wave tiles, 10 * (16-row tiles) + 16-column tiles per wave (0 = by rule, 42, 44, 24, 22)
+//   TSK_F32_T44   fewest 128 x 128 tiles for which the rule takes them (256)
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
@@ -46,6 +47,7 @@ struct Tuning {
     int gemv_rw = 2;
     int f32_ksplit = 8;
     int f32_tile = 0;
+    int f32_t44 = 256;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
     bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:
