@@ -244,17 +244,17 @@ hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, cons
                       p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow))
         return hipErrorInvalidValue;
     // 128 x 128 workgroup tiles (4 x 4 per wave, 72 KiB of LDS: two workgroups
-    // per CU) where there are enough such tiles and each workgroup streams a
-    // long K: 7-14 % faster than 128 x 64 on the VAE's convolutions (k7 at
-    // 128-1024 channels 62.5-67.7 -> 69.7-74.2 % of the fp32 peak) and the
-    // graph's convMLP w1 / w3 (K = 3072 in two slices). 128 x 64 otherwise:
-    // short K-split slices (the graph's w2, K = 8448 in 8 slices: 10 % slower
-    // on the larger tile) and few tiles. Every tile shape sums each output in
-    // the same order: the same bits.
+    // per CU) where there are enough such tiles: unsplit products (the VAE's
+    // convolutions, k7 at 128-1024 channels 62.5-67.7 -> 69.7-74.2 % of the
+    // fp32 peak) and wide ones in slices of >= 768 k (the graph's 30 s convMLP
+    // w1 / w3, 2816 outputs, K = 3072 in 4 slices: 257 -> 235 us). 128 x 64
+    // otherwise: K-split products with 1024 outputs (the graph's w2 in 8
+    // slices: 255 us against 304) and few tiles. Every tile shape sums each
+    // output in the same order: the same bits.
     int tile = tuning().f32_tile;
     if (tile == 0) {
         const int64_t tiles44 = (int64_t) ((p.M + 127) / 128) * ((p.N + 127) / 128) * S;
-        tile = (tiles44 >= tuning().f32_t44 && (S == 1 || p.K / S >= 1200)) ? 44 : 42;
+        tile = (tiles44 >= tuning().f32_t44 && (S == 1 || (p.K / S >= 768 && p.M >= 2048))) ? 44 : 42;
     }
     switch (tile) {
         case 44: launch_tiles<4, 4>(p, y_bf16, s, snake); break;

@@ -368,8 +368,10 @@ constexpr int GRAPH_KSPLIT_MAX = 4;
 // K slices of the f32 path's F32 products (gemm_f32's 128 x 64 tiles): the
 // Q8_0 GGUF keeps the convolution kernels F32, and linear1 / convMLP w2 with
 // 1024 outputs over a few hundred rows are 56-168 tiles with K = 3072 / 8448;
-// slices of at least 256 k until about 1000 workgroups, by the rows per batch
-// item times the batch capacity (never by the call's batch)
+// slices of at least 256 k until about 2000 workgroups (swept: 8 slices were
+// the fastest for every graph shape but the 30 s latent w1 / w3, best at 4),
+// by the rows per batch item times the batch capacity (never by the call's
+// batch)
 constexpr int F32_KSPLIT_MAX = 8;
 constexpr int PART_SLICES = 8;      // partial-sum slices per stream row in m->part (either path)
 int f32_splits(const tsk_mmdit *m, int M, int K, int S) {
@@ -378,7 +380,7 @@ int f32_splits(const tsk_mmdit *m, int M, int K, int S) {
     const int nk = (K + 31) / 32;
     int sp = 1;
     const int most = std::min(F32_KSPLIT_MAX, std::max(1, tuning().f32_ksplit));
-    while (sp * 2 <= most && tiles * sp * 2 <= 1024 && nk / (2 * sp) >= 8) sp *= 2;
+    while (sp * 2 <= most && tiles * sp * 2 <= 2048 && nk / (2 * sp) >= 8) sp *= 2;
     return sp;
 }
 
