@@ -363,8 +363,9 @@ int conv(const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int
 // stream all of K = 3072 / 8448 alone; the slices fill the 256 CUs (up to
 // three workgroups each). The count follows from the rows per batch item
 // times the model's batch capacity, never from the call's batch: a batch row
-// is then summed in the same order whatever the batch it runs in.
-constexpr int GRAPH_KSPLIT_MAX = 4;
+// is then summed in the same order whatever the batch it runs in. At most
+// TSK_GRAPH_KSPLIT slices (4) below TSK_GRAPH_KSWG workgroups (1536: the
+// 30 s step 6.04 -> 5.90 ms against 768; 8 slices or 3072 no better).
 // K slices of the f32 path's F32 products (gemm_f32's 128 x 64 tiles): the
 // Q8_0 GGUF keeps the convolution kernels F32, and linear1 / convMLP w2 with
 // 1024 outputs over a few hundred rows are 56-168 tiles with K = 3072 / 8448;
@@ -389,7 +390,9 @@ int conv_splits(const tsk_mmdit *m, const Conv &C, int S) {
     const int64_t tiles = (int64_t) ((C.OC + 63) / 64) * ((N + 63) / 64);
     const int kt = C.KW * C.IC / 32;
     int sp = 1;
-    while (sp < GRAPH_KSPLIT_MAX && tiles * sp * 2 <= 768 && kt % (2 * sp) == 0 && (kt / (2 * sp)) % 2 == 0) sp *= 2;
+    const int most = std::min(PART_SLICES, std::max(1, tuning().graph_ksplit));
+    while (sp * 2 <= most && tiles * sp * 2 <= tuning().graph_ks_wg && kt % (2 * sp) == 0 && (kt / (2 * sp)) % 2 == 0)
+        sp *= 2;
     return sp;
 }
 

@@ -35,6 +35,8 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_F32_KSPLIT  most K slices of the reference graph's F32 convolutions (1 = unsplit, 2, 4, 8)
 //   TSK_F32_TILE  F32 GEMM wave tiles, 10 * (16-row tiles) + 16-column tiles per wave (0 = by rule, 42, 44, 24, 22)
 //   TSK_F32_T44   fewest 128 x 128 tiles for which the rule takes them (256)
+//   TSK_GRAPH_KSPLIT / TSK_GRAPH_KSWG  most K slices of the reference graph's bf16 k3 convolutions (4) and
+//                 the workgroup count (64 x 64 tiles x slices) they stop below (1536)
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
@@ -48,6 +50,8 @@ struct Tuning {
     int f32_ksplit = 8;
     int f32_tile = 0;
     int f32_t44 = 256;
+    int graph_ksplit = 4;
+    int graph_ks_wg = 1536;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
     bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:
