@@ -180,6 +180,9 @@ int tsk_mul_mat_noalloc(const tsk_tensor *a, const tsk_tensor *b, const tsk_tens
  * type is used as fp16 in the P.V product (the same cast mmdit.cpp:89-90
  * applies before the node). With F32 K/V everything is fp32.
  * prec: TSK_PREC_DEFAULT or TSK_PREC_F32 (both run fp32 softmax).
+ * Scratch: BF16 V of the unmasked 16-bit path is transposed to fp16 in the
+ * stream's workspace first; F16 V (the node mmdit.cpp:88-92 emits) and the
+ * other paths take none.
  */
 int tsk_flash_attn_ext(const tsk_tensor *q, const tsk_tensor *k, const tsk_tensor *v,
                        const tsk_tensor *mask, float scale, float max_bias,
