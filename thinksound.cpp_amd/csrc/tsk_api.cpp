@@ -72,6 +72,8 @@ void read_tuning() {
     t.f32_t44 = env_int("TSK_F32_T44", 256);
     t.graph_ksplit = env_int("TSK_GRAPH_KSPLIT", 4);
     t.graph_ks_wg = env_int("TSK_GRAPH_KSWG", 1536);
+    t.f32_dl = env_int("TSK_F32_DL", 1);
+    t.f32_dl_ns = env_int("TSK_F32_DL_NS", 2);
     t.l2_prefetch = env_int("TSK_L2PF", -1);
     // two digits: split-K of linear1 and of ffn.fc2 in the DiT driver
     if (const char *ks = getenv("TSK_KSPLIT"))
