@@ -420,9 +420,9 @@ def vae_flops(c, T):
     frames (src/vae_decoder.cpp:62-124): conv k7 latent -> 16 C; per block
     (multipliers run backwards) a transposed convolution of stride s whose
     output samples each take 2 taps (kernel 2 s) and three residual units of a
-    k7 and a k1 convolution; the final k7 conv C -> out. (The device runs the
-    transposed convolutions as 3-tap phase convolutions, a third more MFMA
-    work than counted here; the reference's zero-stuffed form does s x more.)"""
+    k7 and a k1 convolution; the final k7 conv C -> out. (The device runs
+    each transposed convolution as two 2-tap phase products, the work counted
+    here; the reference's zero-stuffed form does s x more.)"""
     C = c.channels
     mult = [1] + list(c.c_mults)
     t = T

@@ -18,6 +18,9 @@
 // -- whose output rows [T][s * OC] are the upsampled rows [s T][OC]. Each
 // phase's unused tap is a zero weight, so every output is the reference's
 // sum of the same two products (plus zero terms, which change no fp32 sum).
+// The phases with c(r) = -1 come first (r < s / 2 for K = 2 s), so the merged
+// kernel runs as two 2-tap products over those two channel ranges (taps 0, 1
+// with padding 1; taps 1, 2 without), skipping the zero taps.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -115,20 +118,59 @@ int conv(const tsk_vae *v, const std::string &p, bool bias, const float *x, int 
     return hipcheck(launch_gemm_f32(q, 0, s, sk), "vae conv");
 }
 
-// transposed convolution as the merged 3-tap convolution: y rows [s T_in][OC]
+// the first phase that reads input frames q and q + 1 (c(r) = 0) when the
+// phases r < it all read q - 1 and q (c(r) = -1), else -1
+int ct_split_phase(int64_t K, int64_t st) {
+    const int64_t P = K - 1 - st / 2;
+    int first0 = -1;
+    for (int64_t r = 0; r < st; ++r) {
+        const int64_t k0 = ((P - r) % st + st) % st, c0 = (r + k0 - P) / st;
+        if (c0 == 0 && first0 < 0) first0 = (int) r;
+        if (c0 == -1 && first0 >= 0) return -1;
+    }
+    return first0 < 0 ? (int) st : first0;
+}
+
+// transposed convolution as the merged 3-tap convolution: y rows [s T_in][OC].
+// Each phase uses two of the three taps, so it runs as two 2-tap products:
+// the phases reading frames q - 1, q (taps 0, 1, padding 1) and those
+// reading q, q + 1 (taps 1, 2, no padding), a third fewer products than the
+// 3-tap kernel whose zero taps added nothing to any sum.
 int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T_in, float *y, hipStream_t s,
            const F32Snake *sk = nullptr) {
     const VW &w = wi(v, p + ".weight");
     const int OC = (int) w.ne[2], st = w.stride;
+    const float *wf = wp(v, p + ".weight"), *bias = wp(v, p + ".bias");
+    const int ra = ct_split_phase(w.ne[0], st);
     GemmProblem q;
     memset(&q, 0, sizeof(q));
     q.x = x; q.ld_x = IC;
-    q.wf = wp(v, p + ".weight"); q.ld_w = (int64_t) 3 * IC;
-    q.bias = wp(v, p + ".bias");
-    q.y = y; q.ld_y = (int64_t) st * OC;
-    q.M = st * OC; q.N = T_in; q.K = 3 * IC; q.splits = 1;
-    q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_in; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
-    return hipcheck(launch_gemm_f32(q, 0, s, sk), "vae transposed conv");
+    q.ld_w = (int64_t) 3 * IC;
+    q.ld_y = (int64_t) st * OC;
+    q.N = T_in; q.splits = 1;
+    q.conv_ic = IC; q.conv_iw = T_in; q.conv_ow = T_in; q.conv_s = 1; q.conv_d = 1;
+    if (ra < 0) {
+        q.wf = wf; q.bias = bias; q.y = y;
+        q.M = st * OC; q.K = 3 * IC; q.conv_p = 1;
+        return hipcheck(launch_gemm_f32(q, 0, s, sk), "vae transposed conv");
+    }
+    for (int g = 0; g < 2; ++g) {
+        const int r0 = g ? ra : 0, r1 = g ? st : ra;
+        if (r1 <= r0) continue;
+        const int64_t row0 = (int64_t) r0 * OC;
+        q.wf = wf + row0 * 3 * IC + (g ? IC : 0);      // taps 1, 2 for the second group
+        q.bias = bias + row0;
+        q.y = y + row0;
+        q.M = (r1 - r0) * OC; q.K = 2 * IC; q.conv_p = g ? 0 : 1;
+        F32Snake sg;
+        if (sk) {
+            sg = *sk;                                   // row0 is a multiple of the period OC
+            if (sg.y2) sg.y2 += row0;
+        }
+        const int rc = hipcheck(launch_gemm_f32(q, 0, s, sk ? &sg : nullptr), "vae transposed conv");
+        if (rc) return rc;
+    }
+    return TSK_OK;
 }
 
 int validate(const tsk_vae_config *c) {
