@@ -193,3 +193,39 @@ def test_stream_pairs_change_no_bits(env, monkeypatch):
         monkeypatch.delenv("TSK_Q8_PAIR", raising=False)
         tsk.init(0, reread=True)
         dit.close()
+
+
+@pytest.mark.parametrize("T,cfg", [(194, None), (40, "43"), (40, "24"), (40, "14")])
+def test_attention_q8_output_bits(env, T, cfg):
+    """the attention writing linear1's Q8_0 planes itself (the default) gives
+    the bits of its f32 output quantized by the separate kernel
+    (TSK_ATTN_Q8=0): joint blocks with a pre_only text stream and the
+    automatic 4 x 1 / 4 x 2 launch shapes (T = 194), and forced 4 x 3, 2 x 4
+    and 1 x 4 shapes (key ranges x query blocks: the Q8_0 block's amax across
+    two waves, one wave's lane pair, a lane pair per 32 dims)"""
+    import os
+    tsk, _ = env
+    lat, t, txt = inputs(2, T)
+    out = {}
+    keys = ("TSK_ATTN_Q8", "TSK_ATTN_CFG")
+    old = {k: os.environ.get(k) for k in keys}
+    try:
+        if cfg:
+            os.environ["TSK_ATTN_CFG"] = cfg
+        for flag in ("0", "1"):
+            os.environ["TSK_ATTN_Q8"] = flag
+            tsk.init(0, reread=True)
+            dit = tsk.Dit(tsk.dit_config(weight_type=Q8_0, max_batch=2, max_latent=T))
+            for k, v in tsk.synthetic_weights(dit.tensors(), seed=99).items():
+                dit.set_tensor(k, v)
+            out[flag] = dit.forward(cm(lat), t, txt)
+            dit.close()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        tsk.init(0, reread=True)
+    assert np.isfinite(out["1"]).all()
+    assert np.array_equal(out["0"], out["1"])

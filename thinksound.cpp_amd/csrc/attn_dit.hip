@@ -100,6 +100,34 @@ __device__ __forceinline__ u32x4 load_q8(const char *row, int d0, int q_type, fl
     return r;
 }
 
+// The Q8_0 output of one lane: values w[4 i .. 4 i + 3] are dims
+// 32 (k / 4) + 8 (k % 4) + 4 hi + 0..3 of query q, k = k0 + i (all in one
+// 32-dim block k0 / 4), amax the block's; quantize_rows_q8's arithmetic
+// (d = amax / 127 kept as fp16, q = rint(x * 127 / amax)). The lane with
+// write_d and hi = 0 stores the block's d.
+__device__ __forceinline__ void q8_store(const AttnFastParams &p, int b, int h, int q, int hi, int k0, int nk,
+                                         const float *w, float amax, bool write_d) {
+    int row = -1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < p.q8_ns && q >= p.q8_tok[i] && q < p.q8_tok[i] + p.q8_S[i])
+            row = p.q8_row[i] + b * p.q8_S[i] + (q - p.q8_tok[i]);
+    if (row < 0) return;
+    const int ld = p.H * 64;
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int8_t *qr = p.q8x + (int64_t) row * ld + h * 64;
+    for (int i = 0; i < nk; ++i) {
+        const int k = k0 + i, d0 = 32 * (k >> 2) + 8 * (k & 3) + 4 * hi;
+        int8_t q4[4];
+        for (int e = 0; e < 4; ++e) q4[e] = (int8_t) __builtin_rintf(w[4 * i + e] * id);
+        uint32_t w4;
+        __builtin_memcpy(&w4, q4, 4);
+        *(uint32_t *) (qr + d0) = w4;
+    }
+    if (write_d && hi == 0) p.q8d[(int64_t) row * (ld / 32) + 2 * h + (k0 >> 2)] = f16_bits_to_f32(f32_to_f16_bits(d));
+}
+
 template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
     static_assert(!VROWS || (!KBF16 && !BOUNDED), "V rows: fp16 K, running max");
@@ -497,6 +525,29 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
         const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (p.q8x) {
+            // Q8_0 planes: the 32-dim block of this lane's values is the
+            // query's lane pair (hi = 0, 1) of this wave and, with 4 ranges,
+            // of wave g ^ 1 (whose amax comes through LDS)
+            static_assert(KS == 2 || KS == 4, "block of 32 dims in one or two waves");
+            float w[JW], amax = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < JW; ++jj) {
+                w[jj] = oj[jj] * inv;
+                amax = fmaxf(amax, fabsf(w[jj]));
+            }
+            const auto asw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+            amax = fmaxf(__uint_as_float(asw[0]), __uint_as_float(asw[1]));
+            if constexpr (KS == 4) {
+                float *xa = ml + KS * QB * 128;                 // [KS][QB][64] block amax
+                xa[(g * QB + qb) * 64 + lane] = amax;
+                __syncthreads();
+                amax = fmaxf(amax, xa[((g ^ 1) * QB + qb) * 64 + lane]);
+            }
+            if (q >= p.Nq) return;
+            q8_store(p, b, h, q, hi, g * (JW / 4), JW / 4, w, amax, KS == 2 || (g & 1) == 0);
+            return;
+        }
         if (q >= p.Nq) return;
 #pragma unroll
         for (int k = 0; k < JW / 4; ++k) store4(g * (JW / 4) + k, oj + 4 * k, inv);
@@ -504,6 +555,22 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
         const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (p.q8x) {
+            // Q8_0 planes: each 32-dim block is this wave's lane pair
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                float w[16], amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    w[e] = o[db][e] * inv;
+                    amax = fmaxf(amax, fabsf(w[e]));
+                }
+                const auto asw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+                amax = fmaxf(__uint_as_float(asw[0]), __uint_as_float(asw[1]));
+                if (q < p.Nq) q8_store(p, b, h, q, hi, 4 * db, 4, w, amax, true);
+            }
+            return;
+        }
         if (q >= p.Nq) return;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -521,7 +588,7 @@ hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     const int W = p.qtiles * p.H * p.B;
     const int grid = (W + 7) / 8 * 8;
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
-    if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128) * 4);
+    if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128 + 64) * 4);   // partial O^T, m / l, Q8_0 amax
     auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB, VROWS>;
     lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(grid), dim3(64 * KS * QB), lds, s, p);

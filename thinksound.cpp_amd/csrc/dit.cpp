@@ -904,9 +904,10 @@ void q8_partials(const tsk_dit *d, GemmParams &p, StreamRun &r, int B, int split
     r.pend_ld_gate = mod_ld(d, *r.w);
 }
 
-// linear1 on the f32 attention output of each stream (quantized per stream),
-// split-K partials; gate_msa * (linear1 + bias) is added to the residual by
-// the next LN
+// linear1 on the attention output of each stream as Q8_0 planes (the
+// attention kernel's own Q8_0 output, or its f32 output quantized per
+// stream), split-K partials; gate_msa * (linear1 + bias) is added to the
+// residual by the next LN
 int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const int H = d->cfg.hidden;
     int rc;
@@ -925,7 +926,7 @@ int run_out_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
             q.grp = r[i].S; q.gstride = Ntot;
             rows += (double) q.N;
         }
-        if (nq) {
+        if (nq && !tuning().attn_q8) {
             Timed tm(d, TSK_ROLE_OTHER, 3.0 * rows * H, 5.125 * rows * H, st);
             rc = hipcheck(nq == 2 ? launch_quantize_rows_q8_pair(qr[0], qr[1], st)
                                   : launch_quantize_rows_q8(qr[0].x, 1, qr[0].ld_x, qr[0].N, qr[0].K, qr[0].qx, qr[0].dx,
@@ -1024,6 +1025,21 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     // 1 % margin for the fp16 rounding of q and k
     p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = d->attn_cfg;
+    if (d->q8 && tuning().attn_q8) {
+        // linear1's Q8_0 activations straight from the attention (the streams
+        // that have a linear1), as quantize_rows_q8 would make them from o32
+        for (int i = 0; i < ns; ++i) {
+            if (r[i].w->pre_only) continue;
+            p.q8_tok[p.q8_ns] = r[i].tok_off;
+            p.q8_S[p.q8_ns] = r[i].S;
+            p.q8_row[p.q8_ns] = (int) r[i].row_off;
+            ++p.q8_ns;
+        }
+        if (p.q8_ns) {
+            p.q8x = d->qx;
+            p.q8d = d->dx;
+        }
+    }
     const double nn = (double) Ntot * Ntot;
     Timed tm(d, TSK_ROLE_ATTN, 4.0 * B * c.n_head * nn * c.head_dim, 4.0 * 2.0 * B * Ntot * c.hidden, st);
     return hipcheck(launch_attn_fast(p, st), "attention");

@@ -84,6 +84,15 @@ struct AttnFastParams {
     int bounded;         // fp16 K only: every |q.k| * c <= ATTN_LOGIT_BOUND (no running max)
     int qtiles;          // set by the launcher
     int force_cfg;       // 0: launcher picks; else 10 * key ranges + query blocks
+    // Q8_0 output (q8x non-null; o is not written): each query row of up to
+    // two streams (tokens [q8_tok[i], q8_tok[i] + q8_S[i]) of every batch
+    // item) quantized per 32 as quantize_rows_q8 does, into the planes
+    // q8x [row][H * 64] int8 and q8d [row][H * 2] f32 (fp16-valued d) at
+    // row q8_row[i] + b * q8_S[i] + (token - q8_tok[i]); other tokens are dropped
+    int8_t *q8x;
+    float *q8d;
+    int q8_ns;
+    int q8_tok[2], q8_S[2], q8_row[2];
 };
 // Logit bound (log2 units) under which softmax runs without a running max:
 // exp2 of it (~6e3) and sums of it over 2^14 keys stay far inside fp16 / fp32.

@@ -37,6 +37,7 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_F32_T44   fewest 128 x 128 tiles for which the rule takes them (256)
 //   TSK_GRAPH_KSPLIT / TSK_GRAPH_KSWG  most K slices of the reference graph's bf16 k3 convolutions (4) and
 //                 the workgroup count (64 x 64 tiles x slices) they stop below (1536)
+//   TSK_ATTN_Q8   Q8_0 driver: the attention writes linear1's Q8_0 activations itself (1), or f32 + quantize (0)
 //   TSK_F32_DL / TSK_F32_DL_NS  F32 GEMM with direct global -> LDS loads (1, default; 0 = register staged)
 //                 and its ring depth (2, default; 3)
 struct Tuning {
@@ -54,6 +55,7 @@ struct Tuning {
     int f32_t44 = 256;
     int graph_ksplit = 4;
     int graph_ks_wg = 1536;
+    int attn_q8 = 1;
     int f32_dl = 1;
     int f32_dl_ns = 2;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
