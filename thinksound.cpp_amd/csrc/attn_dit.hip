@@ -128,9 +128,10 @@ __device__ __forceinline__ void q8_store(const AttnFastParams &p, int b, int h, 
     if (write_d && hi == 0) p.q8d[(int64_t) row * (ld / 32) + 2 * h + (k0 >> 2)] = f16_bits_to_f32(f32_to_f16_bits(d));
 }
 
-template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS>
+template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS, bool Q8>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
     static_assert(!VROWS || (!KBF16 && !BOUNDED), "V rows: fp16 K, running max");
+    static_assert(!Q8 || (!KBF16 && !VROWS), "Q8_0 output: fp16 K, V^T");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     constexpr int NB = nbuf(KS, QB);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lh), __float_as_uint(lh), false, false);
         const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        if (p.q8x) {
+        if constexpr (Q8) {
             // Q8_0 planes: the 32-dim block of this lane's values is the
             // query's lane pair (hi = 0, 1) of this wave and, with 4 ranges,
             // of wave g ^ 1 (whose amax comes through LDS)
@@ -555,7 +556,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
         const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
         const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        if (p.q8x) {
+        if constexpr (Q8) {
             // Q8_0 planes: each 32-dim block is this wave's lane pair
 #pragma unroll
             for (int db = 0; db < 2; ++db) {
@@ -581,7 +582,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     }
 }
 
-template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS = false>
+template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS, bool Q8>
 hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     AttnFastParams p = p0;
     p.qtiles = (p.Nq + QB * 32 - 1) / (QB * 32);
@@ -589,22 +590,22 @@ hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     const int grid = (W + 7) / 8 * 8;
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;
     if (KS > 1) lds = max(lds, (size_t) KS * QB * (32 * 64 + 128 + 64) * 4);   // partial O^T, m / l, Q8_0 amax
-    auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB, VROWS>;
+    auto kern = attn_fast_kernel<KBF16, BOUNDED, KS, QB, VROWS, Q8>;
     lds_opt_in((const void *) kern, lds);
     launch_kernel(kern, dim3(grid), dim3(64 * KS * QB), lds, s, p);
     return hipGetLastError();
 }
 
-template <bool KBF16, bool BOUNDED, bool VROWS = false>
+template <bool KBF16, bool BOUNDED, bool VROWS = false, bool Q8 = false>
 hipError_t launch_cfg(const AttnFastParams &p, int cfg, hipStream_t s) {
     switch (cfg) {
-        case 41: return launch_ks_qb<KBF16, BOUNDED, 4, 1, VROWS>(p, s);
-        case 42: return launch_ks_qb<KBF16, BOUNDED, 4, 2, VROWS>(p, s);
-        case 43: return launch_ks_qb<KBF16, BOUNDED, 4, 3, VROWS>(p, s);
-        case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1, VROWS>(p, s);
-        case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2, VROWS>(p, s);
-        case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4, VROWS>(p, s);
-        case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4, VROWS>(p, s);
+        case 41: return launch_ks_qb<KBF16, BOUNDED, 4, 1, VROWS, Q8>(p, s);
+        case 42: return launch_ks_qb<KBF16, BOUNDED, 4, 2, VROWS, Q8>(p, s);
+        case 43: return launch_ks_qb<KBF16, BOUNDED, 4, 3, VROWS, Q8>(p, s);
+        case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1, VROWS, Q8>(p, s);
+        case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2, VROWS, Q8>(p, s);
+        case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4, VROWS, Q8>(p, s);
+        case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4, VROWS, Q8>(p, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -697,11 +698,16 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
     if (p.v_rows) {
         // F16 V rows through the transposing LDS reads: fp16 K, running max;
         // 16-byte aligned rows, 31-bit byte range per (batch, head) like K
-        if (p.k_bf16 || p.bounded || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
+        if (p.k_bf16 || p.bounded || p.q8x || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
                                               (uint64_t) p.v_nb3) % 16 || p.v_nb1 < 128 ||
             (int64_t) (p.Nkv - 1) * p.v_nb1 + 128 >= ((int64_t) 1 << 31))
             return hipErrorInvalidValue;
         return launch_cfg<false, false, true>(p, cfg, s);
+    }
+    if (p.q8x) {
+        // Q8_0 planes in place of o: fp16 K, V^T
+        if (p.k_bf16) return hipErrorInvalidValue;
+        return p.bounded ? launch_cfg<false, true, false, true>(p, cfg, s) : launch_cfg<false, false, false, true>(p, cfg, s);
     }
     if (p.bounded && !p.k_bf16) return launch_cfg<false, true>(p, cfg, s);
     return p.k_bf16 ? launch_cfg<true, false>(p, cfg, s) : launch_cfg<false, false>(p, cfg, s);
