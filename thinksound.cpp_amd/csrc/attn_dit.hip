@@ -140,13 +140,28 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
     const int l32 = lane & 31, hi = lane >> 5;
 
     // workgroup L runs on XCD L % 8; the units of one (batch, head) are
-    // consecutive within an XCD so its K / V^T stay in that XCD's L2
-    const int W = p.qtiles * p.H * p.B;
-    const int per = (int) (gridDim.x >> 3);
-    const int u = (int) (blockIdx.x & 7) * per + (int) (blockIdx.x >> 3);
-    if (u >= W) return;
-    const int bh = u / p.qtiles, qt = u % p.qtiles;
-    const int b = bh / p.H, h = bh % p.H;
+    // consecutive within an XCD so its K / V^T stay in that XCD's L2. With
+    // xcd_hdiv, XCD x takes the heads whose q / k / V^T its own L2 wrote:
+    // head groups x, x + 8, ... of xcd_hdiv heads, for every batch item
+    int b, h, qt;
+    if (p.xcd_hdiv > 0) {
+        const int x = (int) (blockIdx.x & 7), j = (int) (blockIdx.x >> 3), h8 = p.H >> 3;
+        qt = j % p.qtiles;
+        const int r = j / p.qtiles;
+        if (r >= p.B * h8) return;
+        b = r / h8;
+        const int i = r - b * h8;
+        h = (x + 8 * (i / p.xcd_hdiv)) * p.xcd_hdiv + i % p.xcd_hdiv;
+    } else {
+        const int W = p.qtiles * p.H * p.B;
+        const int per = (int) (gridDim.x >> 3);
+        const int u = (int) (blockIdx.x & 7) * per + (int) (blockIdx.x >> 3);
+        if (u >= W) return;
+        qt = u % p.qtiles;
+        b = u / p.qtiles / p.H;
+        h = u / p.qtiles % p.H;
+    }
+    const int bh = b * p.H + h;
 
     const int ntiles = (p.Nkv + KT - 1) / KT;
     const int tpg = (ntiles + KS - 1) / KS;
@@ -586,6 +601,7 @@ template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS, bool Q8>
 hipError_t launch_ks_qb(const AttnFastParams &p0, hipStream_t s) {
     AttnFastParams p = p0;
     p.qtiles = (p.Nq + QB * 32 - 1) / (QB * 32);
+    if (p.xcd_hdiv < 1 || p.H % (8 * p.xcd_hdiv)) p.xcd_hdiv = 0;
     const int W = p.qtiles * p.H * p.B;
     const int grid = (W + 7) / 8 * 8;
     size_t lds = (size_t) KS * nbuf(KS, QB) * TILE_H * 2;

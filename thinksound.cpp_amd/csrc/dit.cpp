@@ -1025,6 +1025,12 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     // 1 % margin for the fp16 rounding of q and k
     p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = d->attn_cfg;
+    if (!d->q8 && tuning().attn_xcd) {
+        // the BF16 QKV GEMM's XCD split (weight tiles of bm rows, tile m on
+        // XCD m % 8) puts head h's q / k / V^T in the L2 of XCD (h / (bm / 64)) % 8
+        const int bm = gemm_ks_bm(gemm_cfg_for(d, 0, B * r[0].S));
+        if (bm % 64 == 0 && (3 * c.hidden / bm) % 8 == 0) p.xcd_hdiv = bm / 64;
+    }
     if (d->q8 && tuning().attn_q8) {
         // linear1's Q8_0 activations straight from the attention (the streams
         // that have a linear1), as quantize_rows_q8 would make them from o32

@@ -84,6 +84,12 @@ struct AttnFastParams {
     int bounded;         // fp16 K only: every |q.k| * c <= ATTN_LOGIT_BOUND (no running max)
     int qtiles;          // set by the launcher
     int force_cfg;       // 0: launcher picks; else 10 * key ranges + query blocks
+    // > 0: workgroups of head h run on XCD (h / xcd_hdiv) % 8, where a QKV
+    // GEMM with xcd_hdiv heads per weight tile wrote that head's q / k / V^T
+    // (the launcher drops it unless H is a multiple of 8 * xcd_hdiv); 0: the
+    // units of one (batch, head) are consecutive within an XCD in (batch,
+    // head) order
+    int xcd_hdiv;
     // Q8_0 output (q8x non-null; o is not written): each query row of up to
     // two streams (tokens [q8_tok[i], q8_tok[i] + q8_S[i]) of every batch
     // item) quantized per 32 as quantize_rows_q8 does, into the planes
