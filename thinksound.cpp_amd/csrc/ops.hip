@@ -273,6 +273,36 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
     return t;
 }
 
+// acc[j] += slices p[0], p[stride], ..., p[(C - 1) stride] at the lane's
+// offsets (lane + 64 j) * 4, in slice order; every load is issued before the
+// first add, so a run of C slices costs one memory round trip
+template <int NV, int C>
+__device__ __forceinline__ void add_slice_run(f32x4 (&acc)[NV], const float *p, int64_t stride, int lane) {
+    f32x4 t[C][NV];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) t[c][j] = *(const f32x4 *) (p + c * stride + (lane + 64 * j) * 4);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[j][e] += t[c][j][e];
+}
+
+// acc[j] += slices 1 .. nsplit - 1 of p (slice stride `stride`), in order, in
+// runs of up to three slices
+template <int NV>
+__device__ __forceinline__ void add_slices(f32x4 (&acc)[NV], const float *p, int64_t stride, int nsplit, int lane) {
+    for (int sp = 1; sp < nsplit; sp += 3) {
+        const int n = nsplit - sp;
+        if (n >= 3) add_slice_run<NV, 3>(acc, p + sp * stride, stride, lane);
+        else if (n == 2) add_slice_run<NV, 2>(acc, p + sp * stride, stride, lane);
+        else add_slice_run<NV, 1>(acc, p + sp * stride, stride, lane);
+    }
+}
+
 // Residual update + LayerNorm + adaLN modulate, one 256-thread block per row
 // of up to two streams (mmdit.cpp:196-231: x = x + gate * y, then
 // modulate(LN(x), shift, scale) for the next projection):
@@ -296,14 +326,11 @@ __device__ __forceinline__ void ln_group_row(const LnStream &st, int r, int H, f
         v[j] = *(const f32x4 *) (xr + i);
         if (st.part) {
             const float *pp = st.part + (int64_t) r * H + i;
-            f32x4 acc = *(const f32x4 *) pp;
-            for (int sp = 1; sp < st.nsplit; ++sp) {
-                const f32x4 t = *(const f32x4 *) (pp + sp * st.part_stride);
-                for (int e = 0; e < 4; ++e) acc[e] += t[e];
-            }
+            f32x4 acc[1] = {*(const f32x4 *) pp};
+            add_slices<1>(acc, pp, st.part_stride, st.nsplit, 0);
             const f32x4 bv = st.bias ? *(const f32x4 *) (st.bias + i) : f32x4{0, 0, 0, 0};
             const f32x4 gv = *(const f32x4 *) (st.gate + (int64_t) b * st.ld_gate + i);
-            for (int e = 0; e < 4; ++e) v[j][e] += gv[e] * (acc[e] + bv[e]);
+            for (int e = 0; e < 4; ++e) v[j][e] += gv[e] * (acc[0][e] + bv[e]);
             *(f32x4 *) (xr + i) = v[j];
         }
         s += v[j][0] + v[j][1] + v[j][2] + v[j][3];
@@ -379,13 +406,7 @@ __device__ __forceinline__ void ln_wave_row(const LnStream &st, int r, float eps
             gv[j] = *(const f32x4 *) (gr + i);
             bv[j] = st.bias ? *(const f32x4 *) (st.bias + i) : f32x4{0, 0, 0, 0};
         }
-        for (int sp = 1; sp < st.nsplit; ++sp) {
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const f32x4 t = *(const f32x4 *) (st.part + sp * st.part_stride + (int64_t) r * H + (lane + 64 * j) * 4);
-                for (int e = 0; e < 4; ++e) acc[j][e] += t[e];
-            }
-        }
+        add_slices<NV>(acc, st.part + (int64_t) r * H, st.part_stride, st.nsplit, lane);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             for (int e = 0; e < 4; ++e) v[j][e] += gv[j][e] * (acc[j][e] + bv[j][e]);
