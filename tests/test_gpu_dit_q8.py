@@ -229,3 +229,34 @@ def test_attention_q8_output_bits(env, T, cfg):
         tsk.init(0, reread=True)
     assert np.isfinite(out["1"]).all()
     assert np.array_equal(out["0"], out["1"])
+
+
+@pytest.mark.parametrize("T,B", [(194, 2), (40, 2), (23, 1)])
+def test_qkv_epilogue_bits(env, T, B):
+    """the Q8_0 QKV GEMM writing the attention operands in its epilogue (the
+    default) gives the bits of its f32 rows scattered by the separate kernel
+    (TSK_Q8_QKV_FUSED=0): joint blocks (two streams in one launch, a pre_only
+    text stream) and fused blocks, token counts that leave partial 64-token
+    tiles, one and two batch items"""
+    import os
+    tsk, _ = env
+    lat, t, txt = inputs(B, T)
+    out = {}
+    old = os.environ.get("TSK_Q8_QKV_FUSED")
+    try:
+        for flag in ("0", "1"):
+            os.environ["TSK_Q8_QKV_FUSED"] = flag
+            tsk.init(0, reread=True)
+            dit = tsk.Dit(tsk.dit_config(weight_type=Q8_0, max_batch=B, max_latent=T))
+            for k, v in tsk.synthetic_weights(dit.tensors(), seed=99).items():
+                dit.set_tensor(k, v)
+            out[flag] = dit.forward(cm(lat), t, txt)
+            dit.close()
+    finally:
+        if old is None:
+            os.environ.pop("TSK_Q8_QKV_FUSED", None)
+        else:
+            os.environ["TSK_Q8_QKV_FUSED"] = old
+        tsk.init(0, reread=True)
+    assert np.isfinite(out["1"]).all()
+    assert np.array_equal(out["0"], out["1"])

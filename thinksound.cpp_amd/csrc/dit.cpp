@@ -847,26 +847,14 @@ int q8_launch(tsk_dit *d, const GemmParams *ps, int n, int role, double fl, doub
     return hipcheck(n == 2 ? launch_gemm_q8_pair(ps[0], ps[1], st) : launch_gemm_q8(ps[0], st), what);
 }
 
-// QKV GEMM into f32 rows, then RMSNorm / RoPE / fp16 scatter into the
-// attention operands
+// QKV GEMM with the RMSNorm / RoPE / fp16 scatter into the attention
+// operands as its epilogue (or, with Tuning::q8_qkv_fused off, into f32 rows
+// and then the scatter kernel: the same bits)
 int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
     const tsk_dit_config &c = d->cfg;
     const int H = c.hidden;
+    const bool fused = tuning().q8_qkv_fused != 0;
     int rc;
-    {
-        GemmParams ps[2];
-        double fl = 0.0, by = 0.0;
-        for (int i = 0; i < ns; ++i) {
-            GemmParams &p = ps[i];
-            p = q8_problem(d, r[i].w->qkv_q, r[i], B, H, 3 * H, r[i].w->qkv_b);
-            p.y = d->qkv32 + r[i].row_off * 3 * H;
-            p.ld_y = 3 * H;
-            p.epi = EPI_STORE;
-            fl += 2.0 * p.N * H * 3.0 * H;
-            by += q8_bytes(p.N, H, 3 * H, 4);
-        }
-        if ((rc = q8_launch(d, ps, ns, TSK_ROLE_QKV, fl, by, "qkv q8 gemm", st))) return rc;
-    }
     QkvScatter qs[2];
     double rows = 0.0;
     for (int i = 0; i < ns; ++i) {
@@ -883,6 +871,26 @@ int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
         q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), as run_qkv
         rows += (double) B * r[i].S;
     }
+    {
+        GemmParams ps[2];
+        double fl = 0.0, by = 0.0;
+        for (int i = 0; i < ns; ++i) {
+            GemmParams &p = ps[i];
+            p = q8_problem(d, r[i].w->qkv_q, r[i], B, H, 3 * H, r[i].w->qkv_b);
+            if (fused) {
+                p.epi = EPI_QKV_ATTN;
+                p.qs = qs[i];
+            } else {
+                p.y = d->qkv32 + r[i].row_off * 3 * H;
+                p.ld_y = 3 * H;
+                p.epi = EPI_STORE;
+            }
+            fl += 2.0 * p.N * H * 3.0 * H;
+            by += q8_bytes(p.N, H, 3 * H, fused ? 2 : 4);
+        }
+        if ((rc = q8_launch(d, ps, ns, TSK_ROLE_QKV, fl, by, "qkv q8 gemm", st))) return rc;
+    }
+    if (fused) return TSK_OK;
     // both streams of a joint block in one launch
     Timed tm(d, TSK_ROLE_OTHER, 10.0 * rows * 3 * H, 12.0 * rows * 3 * H, st);
     return hipcheck(ns == 2 ? launch_qkv_scatter2(qs[0], qs[1], st) : launch_qkv_scatter(qs[0], st), "qkv scatter");

@@ -15,6 +15,7 @@
 // A = W rows (output features) and B = X rows (tokens), so each lane ends up
 // with 4 consecutive output features of one token (16-B stores). Operand
 // tiles are double buffered through LDS with one barrier per K step.
+#include "qkv_row.h"
 #include "tsk_common.h"
 #include "tsk_internal.h"
 #include "tsk_runtime.h"
@@ -604,6 +605,37 @@ __device__ __forceinline__ void q8c_tile(const GemmParams &p, const int li, cons
                 *(uint32_t *) ((int8_t *) p.y + (int64_t) n * p.ld_y + m0[i]) = w4;
             }
         }
+    } else if constexpr (EPI == EPI_QKV_ATTN) {
+        // acc + bias staged token-major in LDS, then one wave per token: lane d
+        // runs launch_qkv_scatter's arithmetic on feature d of the tile's head
+        // (the same operations in the same order as storing the f32 rows and
+        // scattering them, so the same bits)
+        static_assert(BM == 64, "a tile is one head's q, k or v");
+        constexpr int LDT = BM + 1;
+        float *tt = (float *) lds;
+        float bv[TMW][4];
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bv[i][r] = p.bias ? p.bias[m0[i] + r] : 0.0f;
+        __syncthreads();                         // every wave is done with the ring
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tt[(nn[j] - bn0) * LDT + (m0[i] - bm0) + r] = acc[i][j][r] + bv[i][r];
+        __syncthreads();
+        // row (lane / 16) of wave w: tokens 4 (w + 4 i) + lane / 16, features
+        // 4 sl .. 4 sl + 3 (tokens past N repeat token N - 1, same stores)
+        const int H = p.qs.nh * 64, sec = bm0 / H, head = (bm0 - sec * H) >> 6, sl = lane & 15;
+        for (int t0 = 4 * wave; t0 < BN; t0 += 16) {
+            if (bn0 + t0 >= p.N) break;
+            const int t = min(t0 + (lane >> 4), p.N - 1 - bn0);
+            const float *src = tt + t * LDT + 4 * sl;
+            const float x[4] = {src[0], src[1], src[2], src[3]};
+            qkv_row_store(p.qs, sec, head, bn0 + t, x, sl);
+        }
     } else if (S > 1) {
         // this slice's partial sums, no bias (the host allows EPI_STORE into f32 only)
         GemmParams q = p;
@@ -776,6 +808,9 @@ hipError_t q8c_epi_pair(const GemmParams &p0, const GemmParams &p1, hipStream_t 
         case EPI_GELU: return q8c_launch_pair<TM, TN, R, EPI_GELU, YBF16>(p0, p1, s);
         case EPI_GATE_RES: return q8c_launch_pair<TM, TN, R, EPI_GATE_RES, false>(p0, p1, s);
         case EPI_GELU_Q8: return q8c_launch_pair<TM, TN, R, EPI_GELU_Q8, false>(p0, p1, s);
+        case EPI_QKV_ATTN:
+            if constexpr (TM == 4) return q8c_launch_pair<TM, TN, R, EPI_QKV_ATTN, false>(p0, p1, s);
+            else return hipErrorInvalidValue;
         case EPI_STORE: return q8c_launch_pair<TM, TN, R, EPI_STORE, YBF16>(p0, p1, s);
         default: return hipErrorInvalidValue;
     }
@@ -790,11 +825,23 @@ hipError_t q8c_epi(const GemmParams &p, hipStream_t s) {
             if (p.M % 4 || p.y_bf16) return hipErrorInvalidValue;
             return q8c_launch<TM, TN, R, EPI_GEGLU, false>(p, s);
         case EPI_GELU_Q8: return q8c_launch<TM, TN, R, EPI_GELU_Q8, false>(p, s);
+        case EPI_QKV_ATTN:
+            if constexpr (TM == 4) return q8c_launch<TM, TN, R, EPI_QKV_ATTN, false>(p, s);
+            else return hipErrorInvalidValue;
         default: return q8c_launch<TM, TN, R, EPI_STORE, YBF16>(p, s);
     }
 }
 
 }  // namespace
+
+// EPI_QKV_ATTN: the attention operands of one stream (3 nh heads of 64
+// rows, every pointer the scatter writes or reads)
+static bool qkv_attn_ok(const GemmParams &p) {
+    const QkvScatter &q = p.qs;
+    return p.splits <= 1 && !p.y_bf16 && q.nh > 0 && p.M == 3 * 64 * q.nh && q.seq > 0 && p.N % q.seq == 0 && q.q &&
+           q.k && q.vt && q.qn_w && q.kn_w && (!q.rope || q.rope_cs) && q.ldv % 16 == 0 && q.ldv >= q.Ntot &&
+           q.Ntot >= q.tok_off + q.seq && q.tok_off >= 0;
+}
 
 hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // cooperative tiles when the planes allow them: K % 128 (four-block
@@ -815,6 +862,9 @@ hipError_t launch_gemm_q8(const GemmParams &p, hipStream_t s) {
     // in every tile
     if (p.epi == EPI_GELU_Q8 && (!coop || S > 1 || p.y_bf16 || p.M % 64 || !p.yd || p.ld_y < p.M || p.ld_y % 4))
         return hipErrorInvalidValue;
+    // the attention operands: 64 x 64 tiles only (a tile is one head)
+    if (p.epi == EPI_QKV_ATTN)
+        return coop && qkv_attn_ok(p) ? q8c_epi<4, 4, 2, false>(p, s) : hipErrorInvalidValue;
     if (coop) {
         // 64 x 64 tiles with a 2-stage ring; 32 x 64 (weight rows x tokens)
         // when the 64 x 64 grid would hold fewer than two tiles per CU
@@ -860,7 +910,9 @@ hipError_t launch_gemm_q8_pair(const GemmParams &p0, const GemmParams &p1, hipSt
                 return hipErrorInvalidValue;
             if (p->epi == EPI_GELU_Q8 && (S > 1 || p->y_bf16 || p->M % 64 || !p->yd || p->ld_y < p->M || p->ld_y % 4))
                 return hipErrorInvalidValue;
+            if (p->epi == EPI_QKV_ATTN && !qkv_attn_ok(*p)) return hipErrorInvalidValue;
         }
+        if (p0.epi == EPI_QKV_ATTN) return q8c_epi_pair<4, 4, 2, false>(p0, p1, s);
         const int64_t tiles64 = (int64_t) ((p0.M + 63) / 64) * ((p0.N + 63) / 64) +
                                 (int64_t) ((p1.M + 63) / 64) * ((p1.N + 63) / 64);
         const int cfg = tu.q8_cfg ? tu.q8_cfg : tiles64 * S < 512 ? 5 : 2;

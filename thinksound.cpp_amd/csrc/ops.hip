@@ -6,6 +6,7 @@
 // One wave (64 lanes) or one 256-thread block per row; rows are streamed once.
 #include <cstdlib>
 
+#include "qkv_row.h"
 #include "tsk_common.h"
 #include "tsk_internal.h"
 #include "tsk_runtime.h"
@@ -1054,52 +1055,41 @@ __global__ void transpose_ct_kernel(const float *x, int B, int C, int T, float *
     y[((int64_t) b * T + t) * C + c] = x[i];
 }
 
-// one wave per (row, head): lane d holds dimension d of q, k and v
-// wave w of stream p: token w / nh, head w % nh
+// one 16-lane row per (token, head): lane sl of the row holds dimensions
+// 4 sl .. 4 sl + 3 of q, k and v; row g of stream p: token g / nh, head g % nh
+// (p.rows * p.nh is a multiple of 4, or the last wave's extra rows repeat
+// the last pair, whose stores are the same)
 __device__ __forceinline__ void qkv_scatter_wave(const QkvScatter &p, const int64_t w) {
-    const int lane = threadIdx.x & 63;
-    const int n = (int) (w / p.nh), h = (int) (w % p.nh);
-    const int H = p.nh * 64, b = n / p.seq, s = n % p.seq, tok = p.tok_off + s;
-    const float *row = p.qkv + (int64_t) n * p.ld + h * 64 + lane;
-    float x[3] = {row[0], row[H], row[2 * H]};
-    const float wv[2] = {p.qn_w[lane], p.kn_w[lane]};
-    float cs[2] = {1.0f, 0.0f};
-    if (p.rope) {
-        cs[0] = p.rope_cs[(int64_t) s * 64 + (lane & ~1)];
-        cs[1] = p.rope_cs[(int64_t) s * 64 + (lane | 1)];
-    }
-    const int64_t bh = (int64_t) b * p.nh + h;
+    const int lane = threadIdx.x & 63, sl = lane & 15;
+    const int64_t g = min(4 * w + (lane >> 4), (int64_t) p.rows * p.nh - 1);
+    const int n = (int) (g / p.nh), h = (int) (g % p.nh);
+    const int H = p.nh * 64;
+    const float *row = p.qkv + (int64_t) n * p.ld + h * 64 + 4 * sl;
+    f32x4 v[3];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const float sc = 1.0f / sqrtf(wave_sum(x[t] * x[t]) / 64.0f + p.eps);
-        float y = x[t] * sc * wv[t];
-        if (p.rope) {
-            // adjacent pair (2 i, 2 i + 1): the partner is lane ^ 1
-            const float o = dpp_f(y, 0);
-            y = (lane & 1) ? o * cs[1] + y * cs[0] : y * cs[0] - o * cs[1];
-        }
-        if (t == 0) y *= p.q_scale;
-        uint16_t *dst = t == 0 ? p.q : p.k;
-        dst[(bh * p.Ntot + tok) * 64 + lane] = f32_to_f16_bits(y);
+    for (int sec = 0; sec < 3; ++sec) v[sec] = *(const f32x4 *) (row + sec * H);
+#pragma unroll
+    for (int sec = 0; sec < 3; ++sec) {
+        const float x[4] = {v[sec][0], v[sec][1], v[sec][2], v[sec][3]};
+        qkv_row_store(p, sec, h, n, x, sl);
     }
-    p.vt[(bh * 64 + lane) * p.ldv + vt_pos(tok)] = f32_to_f16_bits(x[2]);
 }
 
 __global__ __launch_bounds__(256) void qkv_scatter_kernel(const QkvScatter p) {
     const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w < (int64_t) p.rows * p.nh) qkv_scatter_wave(p, w);
+    if (w < ((int64_t) p.rows * p.nh + 3) / 4) qkv_scatter_wave(p, w);
 }
 
-// two streams in one launch: waves from p0.rows * p0.nh on run p1
+// two streams in one launch: waves from p0's (rows * nh + 3) / 4 on run p1
 __global__ __launch_bounds__(256) void qkv_scatter2_kernel(const QkvScatter p0, const QkvScatter p1) {
-    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6), w0 = (int64_t) p0.rows * p0.nh;
+    const int64_t w = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6), w0 = ((int64_t) p0.rows * p0.nh + 3) / 4;
     if (w < w0) qkv_scatter_wave(p0, w);
-    else if (w - w0 < (int64_t) p1.rows * p1.nh) qkv_scatter_wave(p1, w - w0);
+    else if (w - w0 < ((int64_t) p1.rows * p1.nh + 3) / 4) qkv_scatter_wave(p1, w - w0);
 }
 
 hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s) {
     if (p.rows < 1 || p.nh < 1 || p.seq < 1) return hipErrorInvalidValue;
-    const int64_t waves = (int64_t) p.rows * p.nh;
+    const int64_t waves = ((int64_t) p.rows * p.nh + 3) / 4;
     launch_kernel(qkv_scatter_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, p);
     return hipGetLastError();
 }
@@ -1107,7 +1097,7 @@ hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s) {
 hipError_t launch_qkv_scatter2(const QkvScatter &p0, const QkvScatter &p1, hipStream_t s) {
     for (const QkvScatter *p : {&p0, &p1})
         if (p->rows < 1 || p->nh < 1 || p->seq < 1) return hipErrorInvalidValue;
-    const int64_t waves = (int64_t) p0.rows * p0.nh + (int64_t) p1.rows * p1.nh;
+    const int64_t waves = ((int64_t) p0.rows * p0.nh + 3) / 4 + ((int64_t) p1.rows * p1.nh + 3) / 4;
     launch_kernel(qkv_scatter2_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, p0, p1);
     return hipGetLastError();
 }

@@ -121,7 +121,27 @@ enum GemmEpi : int {
     // gelu_tanh(acc + bias) converted to Q8_0 planes for the next Q8_0 GEMM:
     // Y int8 [N][ld_y], yd f32 block scales [N][M / 32] (Q8_0 cooperative
     // tiles only, M % 64 == 0)
-    EPI_GELU_Q8 = 4
+    EPI_GELU_Q8 = 4,
+    // acc + bias -> the attention operands, the arithmetic of
+    // launch_qkv_scatter on each token's 64 features of one head (qs: the
+    // scatter's parameters; qkv, ld and rows unused). Q8_0 cooperative 64 x 64
+    // tiles only: a tile is one head's q, k or v for 64 tokens
+    EPI_QKV_ATTN = 5
+};
+
+// The QKV epilogue of the BF16 block GEMMs as a kernel over f32 rows (the
+// Q8_0 driver's QKV GEMM stores them): row n = b * seq + s of qkv [rows][3 H]
+// ([q | k | v] head-major, bias included) -> RMSNorm(eps) * w on q and k,
+// RoPE on q and k from rope_cs (when rope), q * q_scale, fp16 into q / k
+// [B][nh][Ntot][64] at token tok_off + s and into V^T [B][nh][64][ldv] at
+// vt_pos(tok_off + s).
+struct QkvScatter {
+    const float *qkv;
+    int64_t ld;
+    const float *qn_w, *kn_w, *rope_cs;
+    uint16_t *q, *k, *vt;
+    int ldv, seq, Ntot, tok_off, rope, nh, rows;
+    float eps, q_scale;
 };
 
 struct GemmParams {
@@ -152,6 +172,7 @@ struct GemmParams {
     int splits;
     int64_t part_stride;
     float *yd;               // EPI_GELU_Q8: block scales of the output planes
+    QkvScatter qs;           // EPI_QKV_ATTN
 };
 hipError_t launch_gemm_bf16(const GemmParams &p, hipStream_t s);
 
@@ -255,20 +276,7 @@ struct QuantRows {
     int64_t gstride;
 };
 hipError_t launch_quantize_rows_q8_pair(const QuantRows &r0, const QuantRows &r1, hipStream_t s);
-// The QKV epilogue of the BF16 block GEMMs as a kernel over f32 rows (the
-// Q8_0 driver's QKV GEMM stores them): row n = b * seq + s of qkv [rows][3 H]
-// ([q | k | v] head-major, bias included) -> RMSNorm(eps) * w on q and k,
-// RoPE on q and k from rope_cs (when rope), q * q_scale, fp16 into q / k
-// [B][nh][Ntot][64] at token tok_off + s and into V^T [B][nh][64][ldv] at
-// vt_pos(tok_off + s).
-struct QkvScatter {
-    const float *qkv;
-    int64_t ld;
-    const float *qn_w, *kn_w, *rope_cs;
-    uint16_t *q, *k, *vt;
-    int ldv, seq, Ntot, tok_off, rope, nh, rows;
-    float eps, q_scale;
-};
+// the QKV epilogue over f32 rows (QkvScatter, above)
 hipError_t launch_qkv_scatter(const QkvScatter &p, hipStream_t s);
 // two streams' scatters in one launch
 hipError_t launch_qkv_scatter2(const QkvScatter &p0, const QkvScatter &p1, hipStream_t s);
