@@ -450,7 +450,10 @@ int rows_bf16(tsk_mmdit *m, const Rows &src, int N, int K, hipStream_t s) {
 }
 
 // y[n][m] = x[n] . W[m] (+ b), any storage type
-int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t ld_y, bool bias, hipStream_t s) {
+// qs (Q8_0 weights only): the rows go to the attention operands through the
+// GEMM's QKV epilogue instead of y (the caller's scatter is then skipped)
+int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t ld_y, bool bias, hipStream_t s,
+          const QkvScatter *qs = nullptr) {
     const float *b = bias ? L.b : nullptr;
     if (L.type == TSK_TYPE_F32) {
         GemmProblem q;
@@ -484,6 +487,10 @@ int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t 
     p.bias = b;
     p.y = y; p.ld_y = ld_y;
     p.epi = EPI_STORE;
+    if (qs) {
+        p.epi = EPI_QKV_ATTN;
+        p.qs = *qs;
+    }
     p.rows_per_gate = 1;
     p.splits = 1;
     return hipcheck(launch_gemm_q8(p, s), "mmdit q8_0 linear");
@@ -672,14 +679,13 @@ int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
 }
 
 // the f32 path: qkv rows (bias included) then the split / RMSNorm / RoPE /
-// F16 scatter kernel, per stream
+// F16 scatter kernel, per stream; with Q8_0 weights the scatter runs as the
+// GEMM's epilogue
 int run_qkv_f32(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
     const tsk_mmdit_config &c = m->cfg;
     const int H = c.hidden;
     for (int i = 0; i < ns; ++i) {
         const Stream &st = r[i];
-        int rc = g_lin(m, st.w->qkv, Rows{(const float *) st.xn, H, 0, 0}, B * st.S, m->qkv32, 3 * H, true, s);
-        if (rc) return rc;
         QkvScatter q;
         memset(&q, 0, sizeof(q));
         q.qkv = m->qkv32; q.ld = 3 * H;
@@ -690,7 +696,12 @@ int run_qkv_f32(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s)
         q.nh = c.n_head; q.rows = B * st.S;
         q.eps = QK_EPS;
         q.q_scale = Q_SCALE;
-        if ((rc = hipcheck(launch_qkv_scatter(q, s), "mmdit qkv scatter"))) return rc;
+        // Q8_0 weights: the scatter is the GEMM's epilogue (the same bits)
+        const bool fused = st.w->qkv.type == TSK_TYPE_Q8_0 && tuning().q8_qkv_fused;
+        int rc = g_lin(m, st.w->qkv, Rows{(const float *) st.xn, H, 0, 0}, B * st.S, m->qkv32, 3 * H, true, s,
+                       fused ? &q : nullptr);
+        if (rc) return rc;
+        if (!fused && (rc = hipcheck(launch_qkv_scatter(q, s), "mmdit qkv scatter"))) return rc;
     }
     return TSK_OK;
 }
