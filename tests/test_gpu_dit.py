@@ -179,6 +179,32 @@ def test_l2_prefetch_changes_no_bits(env, monkeypatch):
         dit.close()
 
 
+def test_attention_xcd_mapping_changes_no_bits(env, monkeypatch):
+    """Running head h's attention workgroups on the XCD whose L2 the QKV GEMM
+    wrote h's q / k / V^T through (on by default) only moves workgroups: with
+    it off the flow is the same bit for bit, at T = 194 (64-row QKV tiles:
+    head h on XCD h % 8) and T = 646 (128-row tiles: head h on XCD h / 2);
+    joint and fused blocks."""
+    tsk, orc = env
+    dit = tsk.Dit(tsk.dit_config(depth=3, fused_depth=1, max_latent=646))
+    for k, v in tsk.synthetic_weights(dit.tensors(), seed=78).items():
+        dit.set_tensor(k, v)
+    try:
+        for T in (194, 646):
+            lat, t, txt = inputs(2, T, seed=T + 2)
+            ref = dit.forward(cm(lat), t, txt)
+            monkeypatch.setenv("TSK_ATTN_XCD", "0")
+            tsk.init(0, reread=True)
+            f = dit.forward(cm(lat), t, txt)
+            monkeypatch.delenv("TSK_ATTN_XCD")
+            tsk.init(0, reread=True)
+            assert np.isfinite(ref).all() and np.array_equal(f, ref), T
+    finally:
+        monkeypatch.delenv("TSK_ATTN_XCD", raising=False)
+        tsk.init(0, reread=True)
+        dit.close()
+
+
 def test_ragged_t_and_device_entry(env):
     tsk, orc = env
     dit, od = build_pair(tsk, orc, depth=2, fused_depth=1, max_latent=64, max_batch=3)
