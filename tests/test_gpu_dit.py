@@ -205,6 +205,37 @@ def test_attention_xcd_mapping_changes_no_bits(env, monkeypatch):
         dit.close()
 
 
+def test_v_rows_layout_changes_no_bits(env, monkeypatch):
+    """The QKV epilogue writing V as rows [B][H][Ntot][64] that the attention
+    transposes in its LDS reads (the default) feeds the P.V products the same
+    fp16 values as V^T rows do (TSK_ATTN_VROWS=0): the flow is the same bit
+    for bit at T = 194 and T = 646 (bounded attention), joint and fused blocks,
+    and with q / k norm weights scaled so that the running-max kernel runs."""
+    tsk, orc = env
+    dit = tsk.Dit(tsk.dit_config(depth=3, fused_depth=1, max_latent=646))
+    W = tsk.synthetic_weights(dit.tensors(), seed=79)
+    for k, v in W.items():
+        dit.set_tensor(k, v)
+    try:
+        for T, scale in ((194, 1.0), (646, 1.0), (194, 2.5)):
+            if scale != 1.0:
+                for k, v in W.items():
+                    if k.endswith("norm.weight"):
+                        dit.set_tensor(k, v * np.float32(scale))
+            lat, t, txt = inputs(2, T, seed=T + 3)
+            ref = dit.forward(cm(lat), t, txt)
+            monkeypatch.setenv("TSK_ATTN_VROWS", "0")
+            tsk.init(0, reread=True)
+            f = dit.forward(cm(lat), t, txt)
+            monkeypatch.delenv("TSK_ATTN_VROWS")
+            tsk.init(0, reread=True)
+            assert np.isfinite(ref).all() and np.array_equal(f, ref), (T, scale)
+    finally:
+        monkeypatch.delenv("TSK_ATTN_VROWS", raising=False)
+        tsk.init(0, reread=True)
+        dit.close()
+
+
 def test_ragged_t_and_device_entry(env):
     tsk, orc = env
     dit, od = build_pair(tsk, orc, depth=2, fused_depth=1, max_latent=64, max_batch=3)

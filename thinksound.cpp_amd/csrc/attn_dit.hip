@@ -27,9 +27,10 @@
 // V^T positions are permuted inside every group of 16 keys (bits 2 and 3 of
 // the key index swapped, an involution) so that each lane's A operand of
 // V^T . P^T is one 16-byte LDS read that matches the keys its P^T slots hold.
-// VROWS (the flash_attn_ext node with F16 V): V tiles come in as rows, like
-// K, and each A operand is two ds_read_b64_tr_b16 transposing reads (4 keys x
-// 16 dims per 16 lanes), so the node needs no V^T pass of its own.
+// VROWS (the flash_attn_ext node with F16 V, and the BF16 DiT, whose QKV
+// epilogue writes V as rows like K): V tiles come in as rows, like K, and
+// each A operand is two ds_read_b64_tr_b16 transposing reads (4 keys x 16
+// dims per 16 lanes), so no V^T layout is needed.
 // Softmax state is rescaled lazily: the running max only moves when a tile's
 // max exceeds it by more than 8 (a factor 256 in fp16 P), which is exact in
 // real arithmetic and keeps P <= 256.
@@ -130,7 +131,7 @@ __device__ __forceinline__ void q8_store(const AttnFastParams &p, int b, int h, 
 
 template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS, bool Q8>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
-    static_assert(!VROWS || (!KBF16 && !BOUNDED), "V rows: fp16 K, running max");
+    static_assert(!VROWS || !KBF16, "V rows: fp16 K");
     static_assert(!Q8 || (!KBF16 && !VROWS), "Q8_0 output: fp16 K, V^T");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     constexpr int NB = nbuf(KS, QB);
@@ -296,6 +297,18 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) ka[ks] = *(const u32x4 *) (kb + swz(32 + l32, 2 * ks + hi));
             const int lim = tile == ntiles - 1 ? p.Nkv - tile * KT : KT;
+            // V^T . P^T A operand: dims 32 db + (lane % 32), keys 16 cc + 8 h + 4 hi + 0..3
+            // (V^T rows, one 16-byte read), or two transposing reads of V rows
+            auto vfrag = [&](int db, int cc) -> f16x8 {
+                if constexpr (VROWS) {
+                    const s16x4 a = lds_read_tr16(vb + vr_off[db] + 16 * cc * 64);
+                    const s16x4 c2 = lds_read_tr16(vb + vr_off[db] + (16 * cc + 8) * 64);
+                    const s16x8 v8 = {a[0], a[1], a[2], a[3], c2[0], c2[1], c2[2], c2[3]};
+                    return __builtin_bit_cast(f16x8, v8);
+                } else {
+                    return *(const f16x8 *) (vb + swz(32 * db + l32, 2 * cc + hi));
+                }
+            };
             auto mask = [&](f32x16 &sv, int mb) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
@@ -332,7 +345,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
-                    for (int h2 = 0; h2 < 2; ++h2) va[db][h2] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * h2 + hi));
+                    for (int h2 = 0; h2 < 2; ++h2) va[db][h2] = vfrag(db, h2);
                 softmax_pv(s0, va);
             }
             if (lim < KT) mask(s1, 1);
@@ -341,8 +354,7 @@ __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastP
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
-                    for (int h2 = 0; h2 < 2; ++h2)
-                        va[db][h2] = *(const f16x8 *) (vb + swz(32 * db + l32, 2 * (2 + h2) + hi));
+                    for (int h2 = 0; h2 < 2; ++h2) va[db][h2] = vfrag(db, 2 + h2);
                 softmax_pv(s1, va);
             }
           }
@@ -712,13 +724,13 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
         return hipErrorInvalidValue;
     const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.k_bf16);
     if (p.v_rows) {
-        // F16 V rows through the transposing LDS reads: fp16 K, running max;
-        // 16-byte aligned rows, 31-bit byte range per (batch, head) like K
-        if (p.k_bf16 || p.bounded || p.q8x || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
-                                              (uint64_t) p.v_nb3) % 16 || p.v_nb1 < 128 ||
+        // F16 V rows through the transposing LDS reads: fp16 K; 16-byte
+        // aligned rows, 31-bit byte range per (batch, head) like K
+        if (p.k_bf16 || p.q8x || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
+                                          (uint64_t) p.v_nb3) % 16 || p.v_nb1 < 128 ||
             (int64_t) (p.Nkv - 1) * p.v_nb1 + 128 >= ((int64_t) 1 << 31))
             return hipErrorInvalidValue;
-        return launch_cfg<false, false, true>(p, cfg, s);
+        return p.bounded ? launch_cfg<false, true, true>(p, cfg, s) : launch_cfg<false, false, true>(p, cfg, s);
     }
     if (p.q8x) {
         // Q8_0 planes in place of o: fp16 K, V^T

@@ -745,6 +745,7 @@ int run_qkv(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st) {
         q = gemm_problem(r[i].xn, H, r[i].w->qkv_w, r[i].w->qkv_b, nullptr, 0, rows, H, 3 * H);
         q.qn_w = r[i].w->qn; q.kn_w = r[i].w->kn;
         q.q = d->q; q.k = d->k; q.vt = d->vt; q.ldv = d->ldv;
+        q.v_rows = tuning().attn_vrows != 0;   // V as rows like k (read by the attention's transposing LDS reads)
         q.seq = r[i].S; q.Ntot = Ntot; q.tok_off = r[i].tok_off; q.rope = r[i].rope;
         q.theta_scale = powf(c.rope_theta, -2.0f / (float) c.head_dim);
         q.freq_scale = 1.0f;
@@ -1033,6 +1034,12 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     // 1 % margin for the fp16 rounding of q and k
     p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = d->attn_cfg;
+    if (!d->q8 && tuning().attn_vrows) {
+        // the BF16 QKV epilogue wrote V as fp16 rows [B][n_head][Ntot][64] into vt
+        p.v_rows = 1;
+        p.v = d->vt;
+        p.v_nb1 = 128; p.v_nb2 = (int64_t) 128 * Ntot; p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;
+    }
     if (!d->q8 && tuning().attn_xcd) {
         // the BF16 QKV GEMM's XCD split (weight tiles of bm rows, tile m on
         // XCD m % 8) puts head h's q / k / V^T in the L2 of XCD (h / (bm / 64)) % 8

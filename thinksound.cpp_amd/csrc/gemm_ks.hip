@@ -647,7 +647,7 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
         const int grp = tid >> 4, sl = tid & 15;
         constexpr int HPT = BM / 64;                 // heads per tile
         constexpr int U = BNC * HPT / (NT / 16);     // (token, head) pairs per lane group
-        if (bm0 >= 2 * H && p.seq >= BNC) {
+        if (bm0 >= 2 * H && p.seq >= BNC && !p.v_rows) {
             // V tile -> V^T rows: lane (row ml, 4-position chunk) writes 4 consecutive
             // key slots of one V^T row (vt_pos keeps aligned 4-runs together), so a
             // row's 128 bytes leave as whole runs instead of 2-byte scatters. The
@@ -751,11 +751,12 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
                     for (int e = 0; e < 4; ++e) x[e] *= p.q_scale;     // the attention's softmax scale
                 uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]),
                                   f32_to_f16_bits(x[3])};
-                if (sec < 2) {
+                if (sec < 2 || p.v_rows) {
+                    // q, k (and V with v_rows) rows of [B][nh][Ntot][64]
                     u32x2 w2;
                     __builtin_memcpy(&w2, o4, 8);
-                    *(u32x2 *) ((sec ? p.k : p.q) + (((int64_t) b * nh + head) * p.Ntot + p.tok_off + spos) * 64 +
-                                4 * sl) = w2;
+                    uint16_t *dst = sec == 0 ? p.q : sec == 1 ? p.k : p.vt;
+                    *(u32x2 *) (dst + (((int64_t) b * nh + head) * p.Ntot + p.tok_off + spos) * 64 + 4 * sl) = w2;
                 } else {
                     uint16_t *vcol = p.vt + (((int64_t) b * nh + head) * 64 + 4 * sl) * p.ldv + vt_pos(p.tok_off + spos);
                     for (int e = 0; e < 4; ++e) vcol[(int64_t) e * p.ldv] = o4[e];

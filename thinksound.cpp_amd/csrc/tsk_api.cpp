@@ -75,6 +75,7 @@ void read_tuning() {
     t.attn_q8 = env_int("TSK_ATTN_Q8", 1);
     t.attn_xcd = env_int("TSK_ATTN_XCD", 1);
     t.q8_qkv_fused = env_int("TSK_Q8_QKV_FUSED", 1);
+    t.attn_vrows = env_int("TSK_ATTN_VROWS", 1);
     t.f32_dl = env_int("TSK_F32_DL", 1);
     t.f32_dl_ns = env_int("TSK_F32_DL_NS", 2);
     t.l2_prefetch = env_int("TSK_L2PF", -1);

@@ -70,7 +70,7 @@ struct AttnFastParams {
     const uint16_t *vt;  // V^T (below), or with v_rows the F16 V rows themselves:
     const void *v;       // v_rows: F16 rows of 64 (ggml strides v_nb1..3, 16-byte aligned)
     int64_t v_nb1, v_nb2, v_nb3;
-    int v_rows;          // fp16 K only, unbounded: V read as rows, transposed by the LDS reads
+    int v_rows;          // fp16 K only: V read as rows, transposed by the LDS reads
     void *o;
     int q_type, k_bf16, out_bf16;
     int Nq, Nkv, H, B;
@@ -216,6 +216,7 @@ struct GemmProblem {
     uint16_t *q, *k;               // fp16 [B][n_head][Ntot][64]
     uint16_t *vt;                  // fp16 [B][n_head][64][ldv], key positions vt_pos()
     int ldv;
+    int v_rows;                    // V into vt as rows like k instead: fp16 [B][n_head][Ntot][64]
     int seq;                       // rows per batch item (row n -> b = n / seq, s = n % seq)
     int Ntot, tok_off, rope;
     float theta_scale, freq_scale, eps;

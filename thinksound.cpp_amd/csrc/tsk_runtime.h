@@ -57,6 +57,7 @@ struct Tuning {
     int graph_ks_wg = 1536;
     int attn_q8 = 1;
     int attn_xcd = 1;
+    int attn_vrows = 1;
     int q8_qkv_fused = 1;
     int f32_dl = 1;
     int f32_dl_ns = 2;
