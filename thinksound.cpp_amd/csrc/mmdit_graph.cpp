@@ -665,6 +665,7 @@ int run_qkv(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s) {
             q.M = L.M; q.N = B * st.S; q.K = L.K; q.splits = 1;
             q.qn_w = st.w->qn; q.kn_w = st.w->kn;
             q.q = m->q; q.k = m->k; q.vt = m->vt; q.ldv = m->ldv;
+            q.v_rows = tuning().attn_vrows != 0;   // V as rows like k
             q.seq = st.S; q.Ntot = Ntot; q.tok_off = st.tok_off;
             q.rope = st.rope_cs != nullptr;
             q.rope_cs = st.rope_cs;
@@ -733,6 +734,12 @@ int run_attention(tsk_mmdit *m, const Stream *r, int ns, int B, int Ntot, hipStr
     // running max below ATTN_LOGIT_BOUND (1 % margin for the fp16 rounding)
     p.bounded = 1.01f * 64.0f * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = tuning().attn_cfg;
+    if (m->fast && tuning().attn_vrows) {
+        // the fused path's QKV epilogue wrote V as fp16 rows [B][n_head][Ntot][64] into vt
+        p.v_rows = 1;
+        p.v = m->vt;
+        p.v_nb1 = 128; p.v_nb2 = (int64_t) 128 * Ntot; p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;
+    }
     return hipcheck(launch_attn_fast(p, s), "mmdit attention");
 }
 
