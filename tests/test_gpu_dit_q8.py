@@ -260,3 +260,36 @@ def test_qkv_epilogue_bits(env, T, B):
         tsk.init(0, reread=True)
     assert np.isfinite(out["1"]).all()
     assert np.array_equal(out["0"], out["1"])
+
+
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_v_rows_layout_bits(env, fused):
+    """V written as rows [B][H][Ntot][64] (the default) or as V^T rows
+    (TSK_ATTN_VROWS=0) by the Q8_0 QKV epilogue (fused) or the scatter kernel:
+    the attention reads the same fp16 values either way, and the Q8_0 step's
+    output is the same bit for bit"""
+    import os
+    tsk, _ = env
+    lat, t, txt = inputs(2, 194)
+    out = {}
+    keys = ("TSK_ATTN_VROWS", "TSK_Q8_QKV_FUSED")
+    old = {k: os.environ.get(k) for k in keys}
+    try:
+        os.environ["TSK_Q8_QKV_FUSED"] = fused
+        for flag in ("0", "1"):
+            os.environ["TSK_ATTN_VROWS"] = flag
+            tsk.init(0, reread=True)
+            dit = tsk.Dit(tsk.dit_config(weight_type=Q8_0, max_batch=2, max_latent=194))
+            for k, v in tsk.synthetic_weights(dit.tensors(), seed=99).items():
+                dit.set_tensor(k, v)
+            out[flag] = dit.forward(cm(lat), t, txt)
+            dit.close()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        tsk.init(0, reread=True)
+    assert np.isfinite(out["1"]).all()
+    assert np.array_equal(out["0"], out["1"])

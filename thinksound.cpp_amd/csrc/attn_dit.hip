@@ -132,7 +132,7 @@ __device__ __forceinline__ void q8_store(const AttnFastParams &p, int b, int h, 
 template <bool KBF16, bool BOUNDED, int KS, int QB, bool VROWS, bool Q8>
 __global__ __launch_bounds__(64 * KS * QB) void attn_fast_kernel(const AttnFastParams p) {
     static_assert(!VROWS || !KBF16, "V rows: fp16 K");
-    static_assert(!Q8 || (!KBF16 && !VROWS), "Q8_0 output: fp16 K, V^T");
+    static_assert(!Q8 || !KBF16, "Q8_0 output: fp16 K");
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     constexpr int NB = nbuf(KS, QB);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -726,10 +726,11 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
     if (p.v_rows) {
         // F16 V rows through the transposing LDS reads: fp16 K; 16-byte
         // aligned rows, 31-bit byte range per (batch, head) like K
-        if (p.k_bf16 || p.q8x || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 |
-                                          (uint64_t) p.v_nb3) % 16 || p.v_nb1 < 128 ||
-            (int64_t) (p.Nkv - 1) * p.v_nb1 + 128 >= ((int64_t) 1 << 31))
+        if (p.k_bf16 || !p.v || ((uintptr_t) p.v | (uint64_t) p.v_nb1 | (uint64_t) p.v_nb2 | (uint64_t) p.v_nb3) % 16 ||
+            p.v_nb1 < 128 || (int64_t) (p.Nkv - 1) * p.v_nb1 + 128 >= ((int64_t) 1 << 31))
             return hipErrorInvalidValue;
+        if (p.q8x)
+            return p.bounded ? launch_cfg<false, true, true, true>(p, cfg, s) : launch_cfg<false, false, true, true>(p, cfg, s);
         return p.bounded ? launch_cfg<false, true, true>(p, cfg, s) : launch_cfg<false, false, true>(p, cfg, s);
     }
     if (p.q8x) {

@@ -870,6 +870,7 @@ int run_qkv_q8(tsk_dit *d, StreamRun *r, int ns, int B, int Ntot, hipStream_t st
         q.nh = c.n_head; q.rows = B * r[i].S;
         q.eps = c.qk_eps;
         q.q_scale = 1.4426950408889634f / sqrtf((float) c.head_dim);   // scale * log2(e), as run_qkv
+        q.v_rows = tuning().attn_vrows != 0;
         rows += (double) B * r[i].S;
     }
     {
@@ -1034,8 +1035,8 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     // 1 % margin for the fp16 rounding of q and k
     p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = d->attn_cfg;
-    if (!d->q8 && tuning().attn_vrows) {
-        // the BF16 QKV epilogue wrote V as fp16 rows [B][n_head][Ntot][64] into vt
+    if (tuning().attn_vrows) {
+        // the QKV epilogue (BF16 or Q8_0) wrote V as fp16 rows [B][n_head][Ntot][64] into vt
         p.v_rows = 1;
         p.v = d->vt;
         p.v_nb1 = 128; p.v_nb2 = (int64_t) 128 * Ntot; p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;

@@ -697,6 +697,7 @@ int run_qkv_f32(tsk_mmdit *m, Stream *r, int ns, int B, int Ntot, hipStream_t s)
         q.nh = c.n_head; q.rows = B * st.S;
         q.eps = QK_EPS;
         q.q_scale = Q_SCALE;
+        q.v_rows = tuning().attn_vrows != 0;
         // Q8_0 weights: the scatter is the GEMM's epilogue (the same bits)
         const bool fused = st.w->qkv.type == TSK_TYPE_Q8_0 && tuning().q8_qkv_fused;
         int rc = g_lin(m, st.w->qkv, Rows{(const float *) st.xn, H, 0, 0}, B * st.S, m->qkv32, 3 * H, true, s,
@@ -734,8 +735,8 @@ int run_attention(tsk_mmdit *m, const Stream *r, int ns, int B, int Ntot, hipStr
     // running max below ATTN_LOGIT_BOUND (1 % margin for the fp16 rounding)
     p.bounded = 1.01f * 64.0f * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = tuning().attn_cfg;
-    if (m->fast && tuning().attn_vrows) {
-        // the fused path's QKV epilogue wrote V as fp16 rows [B][n_head][Ntot][64] into vt
+    if (tuning().attn_vrows) {
+        // the QKV epilogue or scatter wrote V as fp16 rows [B][n_head][Ntot][64] into vt
         p.v_rows = 1;
         p.v = m->vt;
         p.v_nb1 = 128; p.v_nb2 = (int64_t) 128 * Ntot; p.v_nb3 = (int64_t) 128 * Ntot * c.n_head;

@@ -14,17 +14,25 @@ namespace tsk {
 // features 4 sl .. 4 sl + 3 in x (every lane of the wave takes part, one
 // (token, head) per row). q and k get RMSNorm(eps) * w, RoPE from rope_cs
 // (when rope) and, for q, the factor q_scale, then go to fp16 in
-// [B][nh][Ntot][64] at token tok_off + s; v goes to V^T [B][nh][64][ldv] at
-// vt_pos(tok_off + s). No product is contracted into an FMA or into the fp16
+// [B][nh][Ntot][64] at token tok_off + s; v goes to fp16 in vt, as such rows
+// (v_rows) or as V^T [B][nh][64][ldv] at vt_pos(tok_off + s). No product is contracted into an FMA or into the fp16
 // conversion, so every caller rounds the same way.
 __device__ __forceinline__ void qkv_row_store(const QkvScatter &p, int sec, int h, int n, const float (&x)[4], int sl) {
 #pragma clang fp contract(off)
     const int b = n / p.seq, s = n - b * p.seq, tok = p.tok_off + s;
     const int64_t bh = (int64_t) b * p.nh + h;
     if (sec == 2) {
-        uint16_t *col = p.vt + (bh * 64 + 4 * sl) * p.ldv + vt_pos(tok);
+        if (p.v_rows) {
+            const uint16_t o4[4] = {f32_to_f16_bits(x[0]), f32_to_f16_bits(x[1]), f32_to_f16_bits(x[2]),
+                                    f32_to_f16_bits(x[3])};
+            u32x2 w2;
+            __builtin_memcpy(&w2, o4, 8);
+            *(u32x2 *) (p.vt + (bh * p.Ntot + tok) * 64 + 4 * sl) = w2;
+        } else {
+            uint16_t *col = p.vt + (bh * 64 + 4 * sl) * p.ldv + vt_pos(tok);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) col[(int64_t) e * p.ldv] = f32_to_f16_bits(x[e]);
+            for (int e = 0; e < 4; ++e) col[(int64_t) e * p.ldv] = f32_to_f16_bits(x[e]);
+        }
         return;
     }
     const float *wp = (sec ? p.kn_w : p.qn_w) + 4 * sl;

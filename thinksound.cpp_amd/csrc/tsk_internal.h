@@ -134,7 +134,7 @@ enum GemmEpi : int {
 // ([q | k | v] head-major, bias included) -> RMSNorm(eps) * w on q and k,
 // RoPE on q and k from rope_cs (when rope), q * q_scale, fp16 into q / k
 // [B][nh][Ntot][64] at token tok_off + s and into V^T [B][nh][64][ldv] at
-// vt_pos(tok_off + s).
+// vt_pos(tok_off + s), or with v_rows into vt as rows like k.
 struct QkvScatter {
     const float *qkv;
     int64_t ld;
@@ -142,6 +142,7 @@ struct QkvScatter {
     uint16_t *q, *k, *vt;
     int ldv, seq, Ntot, tok_off, rope, nh, rows;
     float eps, q_scale;
+    int v_rows;          // V into vt as rows like k: fp16 [B][nh][Ntot][64]
 };
 
 struct GemmParams {
