@@ -325,7 +325,7 @@ def graph_bench(tsk, steps, warmup=3):
     `steps` forwards; the 24-step CFG-5 sampler at 30 s (wall clock, host
     inputs and result); and the same graph with the Q8_0 GGUF's weight types
     (convert/quantize_gguf.py: 2-D linears Q8_0, the 3-D convolution kernels
-    F32 on fp32 MFMA)"""
+    F32, their products as three bf16 ones each: the library's default)"""
     import numpy as np
     out = {}
     rng = np.random.default_rng(4242)
@@ -380,6 +380,9 @@ def graph_bench(tsk, steps, warmup=3):
     out["q8_0"] = {label: timed_forwards(mq, label, T, Sc, Ss, max(3, steps // 2), 1) for label, T, Sc, Ss in shapes}
     out["q8_0"]["weights"] = ("the Q8_0 GGUF's types: 2-D linears Q8_0 (ggml's reference quantizer), 3-D "
                               "convolution kernels, t_embed MLP and vectors F32")
+    out["q8_0"]["f32_products"] = ("F32 convolution kernels as three bf16 products (weight planes [hi | lo | hi] "
+                                   "against activation planes [hi | hi | lo], ~2^-17 of |x w| per term); "
+                                   "TSK_F32_SPLIT=0 runs them on fp32 MFMA")
     mq.close()
     return out
 

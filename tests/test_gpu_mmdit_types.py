@@ -5,7 +5,8 @@ types, and the GGUF loader (ts_dit::load, src/mmdit.cpp:104-116):
 - Q8_0 (convert/quantize_gguf.py:9-15): 2-D linears with ne0 % 32 == 0 as
   Q8_0 x Q8_0 products (qkv, every adaLN, the text stream's linear1 / MLP,
   the input and conditioning linears), the 3-D convolution kernels and the
-  t_embed MLP F32 (fp32 products);
+  t_embed MLP F32 (the convolutions as three bf16 products each by default,
+  the t_embed MLP as fp32 products);
 - F32 (the F32 GGUF, the "GGML F32 path" of the accuracy targets);
 - files read by tsk_mmdit_create_from_gguf: a Q8_0 GGUF and a BF16 GGUF give
   the bits of a model holding the same values through set_tensor; a Q8_0
@@ -137,6 +138,61 @@ def test_f32_graph_forward(env):
     print(f"F32 graph vs the oracle's F32 path: rel-L2 {e:.3e}", flush=True)
     assert e <= 2e-3
     m.close()
+
+
+def test_f32_split_products(env, monkeypatch):
+    """F32 matrices as three bf16 products (the default, TSK_F32_SPLIT=1: the
+    weight's planes [hi | lo | hi] against the rows' [hi | hi | lo]) against
+    fp32 MFMA products (TSK_F32_SPLIT=0, read on every call) in the same
+    model, at the 9 s token counts. The latent input projection (x_in: a k3
+    convolution and a convMLP, every kernel F32 in both GGUFs, no attention)
+    moves by the dropped x_lo w_lo terms and the lo roundings only: held to
+    1e-4 of the oracle's F32 stage, where fp32 products agree to 1e-5 and a
+    split that lost its lo planes would be ~2e-3 off. The flows carry the
+    attention's F16 K / V roundings, which such small moves flip here and
+    there (the two modes' flows differ by ~2e-4): the F32 model's flow is
+    held to 2e-3 of the F32 path in both modes, the Q8_0 model's (whose Q8_0
+    activations flip as well) to the oracle's bound in both modes."""
+    tsk, orc = env
+    kw = dict(depth=4, fused_depth=2, max_latent=194, max_clip=72, max_sync=216)
+    args = inputs(2, 194, 72, 216, seed=21)
+    args = (args[0], np.array([0.7, 0.2], np.float32)) + args[1:]
+    for wt in (F32, Q8_0):
+        m, od, _ = build_typed(tsk, orc, wt, **kw)
+        m.debug(True)
+        try:
+            f_split = m.forward(*args)
+            x_split = m.stage("x_in")
+            monkeypatch.setenv("TSK_F32_SPLIT", "0")
+            tsk.init(0, reread=True)
+            f_exact = m.forward(*args)
+            x_exact = m.stage("x_in")
+        finally:
+            monkeypatch.delenv("TSK_F32_SPLIT", raising=False)
+            tsk.init(0, reread=True)
+        m.debug(False)
+        assert np.isfinite(f_split).all() and np.isfinite(f_exact).all()
+        ref = od.forward(*args, act_bf16=False, kv_f16=True)
+        x_ref = od.stage("x_in")
+        xs, xx = rel_l2(x_split, x_ref), rel_l2(x_exact, x_ref)
+        d = rel_l2(f_split, f_exact)
+        print(f"type {wt}, 9 s shapes: x_in vs the oracle's F32 stage: split {xs:.3e}, fp32 products {xx:.3e}; "
+              f"flows split vs fp32 products {d:.3e}", flush=True)
+        assert xs <= 1e-4 and xx <= 1e-5
+        if wt == F32:
+            e_s, e_x = rel_l2(f_split, ref), rel_l2(f_exact, ref)
+            print(f"F32 model: flow vs the F32 path: split {e_s:.3e}, fp32 products {e_x:.3e}", flush=True)
+            assert e_s <= 2e-3 and e_x <= 2e-3
+        else:
+            check(m, od, args, "Q8_0 graph, 9 s shapes, split F32 products")
+            monkeypatch.setenv("TSK_F32_SPLIT", "0")
+            tsk.init(0, reread=True)
+            try:
+                check(m, od, args, "Q8_0 graph, 9 s shapes, fp32 products")
+            finally:
+                monkeypatch.delenv("TSK_F32_SPLIT", raising=False)
+                tsk.init(0, reread=True)
+        m.close()
 
 
 GGUF_KW = dict(depth=3, fused_depth=1, mlp_hidden=512, max_latent=64, max_clip=16, max_sync=48)

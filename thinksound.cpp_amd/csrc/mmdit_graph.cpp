@@ -62,6 +62,8 @@ struct MW {
     bool qkv_perm;          // rows (or entries) of a qkv projection: (h d j) -> [q | k | v]
     size_t offset;          // F32 / BF16 values, or the Q8_0 int8 plane [M][K]
     size_t offset_d;        // Q8_0: the fp16 block-scale plane [M][K / 32]
+    size_t offset_s;        // split F32 matrix: bf16 planes, rows [hi | lo | hi] per K (per kw for a conv)
+    bool split;             // F32 matrix also held as split planes (products as three bf16 ones)
     float amax;             // max |value| of a vector as last set
 };
 
@@ -72,6 +74,7 @@ struct Lin {
     const float *wf;        // F32
     const int8_t *qw;       // Q8_0 planes
     const uint16_t *dw;
+    const uint16_t *ws;     // F32 held split: bf16 rows [M][3 K], [hi | lo | hi]
     const float *b;
     int K, M;
 };
@@ -80,6 +83,7 @@ struct Conv {
     int type;
     const uint16_t *w;
     const float *wf;
+    const uint16_t *ws;     // F32 held split: bf16 rows [OC][KW * 3 IC], [hi | lo | hi] per kw
     const float *b;
     int KW, IC, OC;
 };
@@ -171,7 +175,8 @@ void addw(tsk_mmdit *m, const std::string &name, int64_t a, int64_t b, int64_t c
     x.kind = kind;
     x.type = TSK_TYPE_F32;
     x.qkv_perm = perm;
-    x.offset = x.offset_d = 0;
+    x.offset = x.offset_d = x.offset_s = 0;
+    x.split = false;
     x.amax = 0.0f;
     m->idx[name] = (int) m->w.size();
     m->w.push_back(x);
@@ -240,6 +245,7 @@ Lin lin_of(const tsk_mmdit *m, const std::string &p, bool bias) {
     if (x.type == TSK_TYPE_F32) L.wf = (const float *) base;
     else if (x.type == TSK_TYPE_BF16) L.w = (const uint16_t *) base;
     else { L.qw = (const int8_t *) base; L.dw = (const uint16_t *) (m->blob + x.offset_d); }
+    if (x.split) L.ws = (const uint16_t *) (m->blob + x.offset_s);
     L.b = bias ? wp<float>(m, p + ".bias") : nullptr;
     return L;
 }
@@ -251,6 +257,7 @@ Conv conv_of(const tsk_mmdit *m, const std::string &p, bool bias) {
     C.type = x.type;
     if (x.type == TSK_TYPE_F32) C.wf = wp<float>(m, p + ".weight");
     else C.w = wp<uint16_t>(m, p + ".weight");
+    if (x.split) C.ws = (const uint16_t *) (m->blob + x.offset_s);
     C.b = bias ? wp<float>(m, p + ".bias") : nullptr;
     C.KW = (int) x.ne[0];
     C.IC = (int) x.ne[1];
@@ -449,12 +456,64 @@ int rows_bf16(tsk_mmdit *m, const Rows &src, int N, int K, hipStream_t s) {
                     "mmdit bf16 rows");
 }
 
+// F32 products as three bf16 ones (TSK_F32_SPLIT, for a model created with
+// it): the weight's planes [hi | lo | hi] against the rows' [hi | hi | lo]
+// sum x_hi w_hi + x_hi w_lo + x_lo w_hi over 3 K, which leaves out x_lo w_lo
+// and the roundings of the lo parts, about 2^-17 of |x w| per term (fp32
+// MFMA products: 157 TFLOP/s at most; three bf16 ones: 2.5 PFLOP/s / 3)
+bool split_on(const uint16_t *ws) { return ws && tuning().f32_split; }
+Lin split_lin(const Lin &L) {
+    Lin S = L;
+    S.type = TSK_TYPE_BF16; S.w = L.ws; S.K = 3 * L.K;
+    return S;
+}
+Conv split_conv(const Conv &C) {
+    Conv S = C;
+    S.type = TSK_TYPE_BF16; S.w = C.ws; S.IC = 3 * C.IC;
+    return S;
+}
+// the rows as the split operand [N][3 K] in m->cvt16
+int rows_split3(tsk_mmdit *m, const Rows &src, int N, int K, hipStream_t s) {
+    if ((size_t) N * 3 * K > m->cvt_cap) return fail(TSK_ERR_SHAPE, "split rows of %d x %d exceed the scratch", N, K);
+    const int rpb = src.grp ? src.grp : N;
+    return hipcheck(launch_cast_rows_split3(src.x, src.ld, src.grp ? src.gstride : 0, rpb, N, K, m->cvt16, s),
+                    "mmdit split rows");
+}
+// K slices of a split product (K three times the F32 one, 9216-25344 for
+// the graph's convolutions): the most, up to `most`, that keep the 128 x 128
+// tiles times slices within TSK_SPLIT_WG (512; swept 256-1536 on the Q8_0
+// graph: 384-512 best, 9 s 7.26 against 7.57-7.80 ms per forward, 30 s
+// 12.24 against 13.05-13.12); every slice an even number of 32-k tiles. Counted from the rows per batch
+// item times the batch capacity, so that a batch row is summed in the same
+// order whatever the call's batch.
+int split_slices(const tsk_mmdit *m, int M, int K, int S, int most = PART_SLICES) {
+    const int64_t t = (int64_t) ((M + 127) / 128) * ((S * m->cfg.max_batch + 127) / 128);
+    const int kt = K / 32;
+    int sp = 1;
+    for (int c = 2; c <= most; ++c)
+        if (kt % c == 0 && (kt / c) % 2 == 0 && t * c <= tuning().split_wg) sp = c;
+    return sp;
+}
+constexpr int SPLIT_SUM_MAX = 16;   // slices of a split convolution summed into a plain output
+// K slices of a residual-branch convolution on the f32 path (summed by the
+// next LayerNorm): F32 kernels as fp32 products by f32_splits, as split
+// products by split_slices; BF16 kernels unsplit
+int res_splits(const tsk_mmdit *m, const Conv &C, int S) {
+    if (C.type != TSK_TYPE_F32) return 1;
+    return split_on(C.ws) ? split_slices(m, C.OC, 3 * C.KW * C.IC, S) : f32_splits(m, C.OC, C.KW * C.IC, S);
+}
+
 // y[n][m] = x[n] . W[m] (+ b), any storage type
 // qs (Q8_0 weights only): the rows go to the attention operands through the
 // GEMM's QKV epilogue instead of y (the caller's scatter is then skipped)
 int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t ld_y, bool bias, hipStream_t s,
           const QkvScatter *qs = nullptr) {
     const float *b = bias ? L.b : nullptr;
+    if (L.type == TSK_TYPE_F32 && split_on(L.ws)) {
+        int rc = rows_split3(m, src, N, L.K, s);
+        if (rc) return rc;
+        return lin(split_lin(L), m->cvt16, 3 * L.K, N, y, ld_y, false, s, nullptr, !bias);
+    }
     if (L.type == TSK_TYPE_F32) {
         GemmProblem q;
         memset(&q, 0, sizeof(q));
@@ -502,6 +561,26 @@ int g_lin(tsk_mmdit *m, const Lin &L, const Rows &src, int N, float *y, int64_t 
 int g_conv(tsk_mmdit *m, const Conv &C, const float *x, int64_t ld_x, int64_t xb, int IW, int B, int pad, float *y,
            int64_t ld_y, bool bias, hipStream_t s, int splits = 1) {
     if (splits > 1 && bias) return fail(TSK_ERR_INVALID_ARG, "K-split slices carry no bias");
+    if (C.type == TSK_TYPE_F32 && split_on(C.ws)) {
+        int rc = rows_split3(m, Rows{x, ld_x, IW, xb}, B * IW, C.IC, s);
+        if (rc) return rc;
+        const Conv S = split_conv(C);
+        // a plain output over few tiles (the input projections' and the final
+        // layer's convolutions, up to K = 25344): K-split slices into m->h3
+        // (free outside the SwiGLU halves), summed with the bias
+        const int OW = IW + 2 * pad - (C.KW - 1), N = B * OW;
+        const size_t cap = (size_t) F32_KSPLIT_MAX * m->Rmax * m->cfg.mlp_hidden;   // floats of m->h3
+        const int most = (int) std::min<size_t>(SPLIT_SUM_MAX, cap / ((size_t) m->cfg.max_batch * OW * C.OC));
+        const int sp = splits == 1 && C.OC % 4 == 0 && ld_y % 4 == 0 && ((uintptr_t) y & 15) == 0
+                           ? split_slices(m, C.OC, S.KW * S.IC, OW, most) : 1;
+        if (sp > 1) {
+            if ((rc = conv(S, m->cvt16, S.IC, (int64_t) IW * S.IC, IW, B, pad, m->h3, C.OC, false, s, true, sp)))
+                return rc;
+            return hipcheck(launch_sum_slices(m->h3, sp, (int64_t) N * C.OC, bias ? C.b : nullptr, N, C.OC, y, ld_y, s),
+                            "mmdit split slices");
+        }
+        return conv(S, m->cvt16, S.IC, (int64_t) IW * S.IC, IW, B, pad, y, ld_y, false, s, !bias, splits);
+    }
     if (C.type == TSK_TYPE_F32) {
         GemmProblem q;
         memset(&q, 0, sizeof(q));
@@ -531,23 +610,42 @@ int g_swiglu(tsk_mmdit *m, bool is_conv, const Conv &c1, const Conv &c3, const C
     const int N = B * S;
     const int F = is_conv ? c1.OC : l1.M;
     const int t1 = is_conv ? c1.type : l1.type, t3 = is_conv ? c3.type : l3.type;
+    const bool split = t1 == TSK_TYPE_F32 && t3 == TSK_TYPE_F32 && split_on(is_conv ? c1.ws : l1.ws) &&
+                       split_on(is_conv ? c3.ws : l3.ws);
+    // split convolution halves over few rows (the 9 s shapes: 176 tiles of
+    // 128 x 128 where the fused GEMM would take 64 x 64 ones streaming all of
+    // K = 9216): each half as K-split slices of 128-row tiles, summed by the
+    // SiLU * gate kernel
+    const bool split_sliced = split && is_conv && (int64_t) ((F + 63) / 64) * ((N + 127) / 128) < 400;
     int rc;
-    if (t1 == TSK_TYPE_BF16 && t3 == TSK_TYPE_BF16) {
-        // both halves in one cooperative GEMM with the SwiGLU epilogue, f32 out
-        const int IC = is_conv ? c1.IC : l1.K;
-        if ((rc = rows_bf16(m, is_conv ? Rows{x, ld_x, S, xb} : Rows{x, ld_x, 0, 0}, N, IC, s))) return rc;
+    if (split_sliced) {
+        const int IC = 3 * c1.IC;
+        const int sp = split_slices(m, F, c1.KW * IC, S);
+        if ((rc = rows_split3(m, Rows{x, ld_x, S, xb}, N, c1.IC, s))) return rc;
+        if ((rc = conv(split_conv(c1), m->cvt16, IC, (int64_t) S * IC, S, B, 1, m->h1, F, false, s, true, sp)) ||
+            (rc = conv(split_conv(c3), m->cvt16, IC, (int64_t) S * IC, S, B, 1, m->h3, F, false, s, true, sp)) ||
+            (rc = hipcheck(launch_silu_mul_slices(m->h1, m->h3, sp, (int64_t) N * F, m->hid32, (int64_t) N * F, s),
+                           "mmdit silu * gate")))
+            return rc;
+    } else if ((t1 == TSK_TYPE_BF16 && t3 == TSK_TYPE_BF16) || split) {
+        // both halves in one cooperative GEMM with the SwiGLU epilogue, f32
+        // out; split F32 halves over their planes and the rows' split operand
+        const int f = split ? 3 : 1, IC = f * (is_conv ? c1.IC : l1.K);
+        const Rows src = is_conv ? Rows{x, ld_x, S, xb} : Rows{x, ld_x, 0, 0};
+        if ((rc = split ? rows_split3(m, src, N, IC / 3, s) : rows_bf16(m, src, N, IC, s))) return rc;
         GemmGroup g;
         memset(&g, 0, sizeof(g));
         g.nprob = 1;
         GemmProblem &q = g.p[0];
         q.x = m->cvt16; q.ld_x = IC;
-        q.w = is_conv ? c1.w : l1.w; q.w3 = is_conv ? c3.w : l3.w;
-        q.ld_w = is_conv ? (int64_t) c1.KW * c1.IC : l1.K;
+        q.w = split ? (is_conv ? c1.ws : l1.ws) : is_conv ? c1.w : l1.w;
+        q.w3 = split ? (is_conv ? c3.ws : l3.ws) : is_conv ? c3.w : l3.w;
+        q.ld_w = is_conv ? (int64_t) c1.KW * IC : IC;
         q.y = m->hid32; q.ld_y = F;
-        q.M = F; q.N = N; q.K = is_conv ? c1.KW * c1.IC : l1.K; q.splits = 1;
+        q.M = F; q.N = N; q.K = (int) q.ld_w; q.splits = 1;
         if (is_conv) {
             q.x_group_stride = (int64_t) S * IC;
-            q.conv_ic = c1.IC; q.conv_iw = S; q.conv_ow = S; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
+            q.conv_ic = IC; q.conv_iw = S; q.conv_ow = S; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
         }
         if ((rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_F32, s), "mmdit swiglu w1/w3"))) return rc;
     } else {
@@ -835,7 +933,7 @@ int run_post_f32(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         const float *orows = m->o32 + (size_t) r[i].tok_off * H;
         int sp = 1;
         if (b.conv) {
-            if (b.l1c.type == TSK_TYPE_F32) sp = f32_splits(m, b.l1c.OC, b.l1c.KW * b.l1c.IC, r[i].S);
+            sp = res_splits(m, b.l1c, r[i].S);
             rc = g_conv(m, b.l1c, orows, H, ob, r[i].S, B, 1, r[i].part, H, false, s, sp);
         } else {
             rc = g_lin(m, b.l1, Rows{orows, H, r[i].S, ob}, B * r[i].S, r[i].part, H, false, s);
@@ -858,7 +956,7 @@ int run_post_f32(tsk_mmdit *m, Stream *r, int ns, int B, hipStream_t s) {
         r[i].pending = live[j++].pending;
         const Block &b = *r[i].w;
         const float *xr = (const float *) r[i].xn;
-        const int sp = b.conv && b.w2c.type == TSK_TYPE_F32 ? f32_splits(m, b.w2c.OC, b.w2c.KW * b.w2c.IC, r[i].S) : 1;
+        const int sp = b.conv ? res_splits(m, b.w2c, r[i].S) : 1;
         rc = g_swiglu(m, b.conv, b.w1c, b.w3c, b.w2c, b.w1, b.w3, b.w2, xr, H, (int64_t) r[i].S * H, r[i].S, B,
                       r[i].part, H, s, sp);
         if (rc) return rc;
@@ -962,6 +1060,16 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
         any_q8 = any_q8 || t == TSK_TYPE_Q8_0;
         m->fast = m->fast && t == rule_type(TSK_TYPE_BF16, x);
     }
+    // F32 matrices also held as split bf16 planes (TSK_F32_SPLIT): every
+    // linear and convolution of the f32 path but the adaLN sets (one GEMM
+    // over a whole set) and the t_embed MLP (B rows, fp32 products)
+    bool any_split = false;
+    if (!m->fast && tuning().f32_split)
+        for (MW &x : m->w) {
+            x.split = x.type == TSK_TYPE_F32 && x.kind != K_VEC && x.name.find("adaLN_modulation") == std::string::npos &&
+                      x.name.find("t_embed") == std::string::npos;
+            any_split = any_split || x.split;
+        }
     // blob placement: the adaLN weights (each plane of them), then biases, of
     // the latent blocks and the final layer back to back (rows of one [Ml][H]
     // matrix, 256-byte multiples: no gaps), the same for the clip and text
@@ -978,9 +1086,10 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
     auto place = [&](const std::string &name, int plane) {
         const int i = m->idx.at(name);
         MW &x = m->w[i];
-        const size_t bytes = type_bytes(x.type, x.ne[0] * x.ne[1] * x.ne[2], plane);
+        const int64_t n = x.ne[0] * x.ne[1] * x.ne[2];
+        const size_t bytes = plane == 2 ? (x.split ? 6 * (size_t) n : 0) : type_bytes(x.type, n, plane);
         if (!bytes) return;
-        (plane ? x.offset_d : x.offset) = off;
+        (plane == 2 ? x.offset_s : plane ? x.offset_d : x.offset) = off;
         off += (bytes + 255) & ~(size_t) 255;
         placed[i] |= 1 << plane;
     };
@@ -990,7 +1099,7 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
         for (const auto &p : *set) place(p + ".adaLN_modulation.1.bias", 0);
     }
     for (size_t i = 0; i < m->w.size(); ++i)
-        for (int plane = 0; plane < 2; ++plane)
+        for (int plane = 0; plane < 3; ++plane)
             if (!(placed[i] & (1 << plane))) place(m->w[i].name, plane);
     const int B = c.max_batch, T = c.max_latent, C = c.max_clip, S = c.max_sync;
     const int64_t Ml = (int64_t) (nj + c.fused_depth) * 6 * H + 2 * H;          // latent blocks + final layer
@@ -1055,10 +1164,11 @@ int create_impl(const tsk_mmdit_config *cfg, const TypeFn &type_of, tsk_mmdit **
         a(&m->hid32, sizeof(float) * R * F);
         a(&m->h1, sizeof(float) * F32_KSPLIT_MAX * R * F);   // K-split slices of the F32 convMLP halves
         a(&m->h3, sizeof(float) * F32_KSPLIT_MAX * R * F);
-        // conversions: at most R rows (B * T for the per-token adaLN) of the widest input
+        // conversions: at most R rows (B * T for the per-token adaLN) of the
+        // widest input, three times as wide as split operands
         const size_t conv_rows = (size_t) std::max(R, (int64_t) B * T);
-        if (any_bf16) {
-            m->cvt_cap = conv_rows * Wcv;
+        if (any_bf16 || any_split) {
+            m->cvt_cap = conv_rows * Wcv * (any_split ? 3 : 1);
             a(&m->cvt16, 2 * m->cvt_cap);
         }
         if (any_q8) {
@@ -1204,6 +1314,26 @@ extern "C" int tsk_mmdit_set_tensor(tsk_mmdit *m, const char *name, const float 
     }
     if (x.type == TSK_TYPE_F32) {
         e = hipMemcpy(m->blob + x.offset, v.data(), 4 * (size_t) n, hipMemcpyHostToDevice);
+        if (e == hipSuccess && x.split) {
+            // rows of K (a conv: KW groups of IC per output row) -> [hi | lo | hi]
+            // per group, hi = bf16(w), lo = bf16(w - hi)
+            const int64_t G = x.kind == K_CONV ? x.ne[1] : x.ne[0];
+            std::vector<uint16_t> sp((size_t) (3 * n));
+            for (int64_t g0 = 0; g0 < n; g0 += G)
+                for (int64_t i = 0; i < G; ++i) {
+                    const float w = v[(size_t) (g0 + i)];
+                    const uint16_t hi = host_bf16_bits(w);
+                    uint32_t hb = (uint32_t) hi << 16;
+                    float hf;
+                    memcpy(&hf, &hb, 4);
+                    const uint16_t lo = std::isfinite(hf) ? host_bf16_bits(w - hf) : (uint16_t) 0;
+                    uint16_t *d = &sp[(size_t) (3 * g0 + i)];
+                    d[0] = hi;
+                    d[G] = lo;
+                    d[2 * G] = hi;
+                }
+            e = hipMemcpy(m->blob + x.offset_s, sp.data(), 2 * sp.size(), hipMemcpyHostToDevice);
+        }
     } else if (x.type == TSK_TYPE_BF16) {
         std::vector<uint16_t> bf((size_t) n);
         for (int64_t i = 0; i < n; ++i) bf[i] = host_bf16_bits(v[i]);

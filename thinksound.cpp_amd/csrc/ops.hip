@@ -711,6 +711,37 @@ __global__ void cast_rows_bf16_kernel(const float *x, int64_t ld_x, int64_t ld_b
     *(u32x2 *) (y + r * cols + c) = w;
 }
 
+// f32 rows -> the bf16 operand of a split product: row r of y (3 cols wide)
+// is [hi | hi | lo] with hi = bf16(x), lo = bf16(x - hi), both RNE (x - hi is
+// exact in f32). Against a weight held as [hi | lo | hi] one bf16 GEMM over
+// 3 K sums x_hi w_hi + x_hi w_lo + x_lo w_hi, which is x w up to x_lo w_lo
+// and the rounding of the two lo parts: about 2^-17 of |x w| per term. An
+// infinite or NaN x keeps hi and gets lo = 0.
+__global__ void cast_rows_split3_kernel(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows,
+                                        int cols, uint16_t *y) {
+    const int64_t q = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int cq = cols / 4;
+    if (q >= rows * cq) return;
+    const int64_t r = q / cq;
+    const int c = (int) (q - r * cq) * 4;
+    const int64_t b = r / rows_per_b, i = r - b * rows_per_b;
+    const f32x4 v = *(const f32x4 *) (x + b * ld_b + i * ld_x + c);
+    uint16_t h4[4], l4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h4[e] = f32_to_bf16_bits(v[e]);
+        const float hf = bf16_bits_to_f32(h4[e]);
+        l4[e] = __builtin_isfinite(hf) ? f32_to_bf16_bits(v[e] - hf) : (uint16_t) 0;
+    }
+    u32x2 wh, wl;
+    __builtin_memcpy(&wh, h4, 8);
+    __builtin_memcpy(&wl, l4, 8);
+    uint16_t *yr = y + r * 3 * cols + c;
+    *(u32x2 *) yr = wh;
+    *(u32x2 *) (yr + cols) = wh;
+    *(u32x2 *) (yr + 2 * cols) = wl;
+}
+
 // conv kernel [KW, IC, OC] (element strides s0, s1, s2) -> kw-major rows
 // dst[oc][kw * IC + ic], a bit copy
 template <typename T>
@@ -739,6 +770,30 @@ __global__ void silu_mul_slices_kernel(const float *a, const float *b, int S, in
         g += b[z * stride + i];
     }
     y[i] = v / (1.0f + expf(-v)) * g;
+}
+
+// y[n][m] = (sum of S K-split slices p[z][n][m], slice stride `stride`,
+// rows of M, summed in slice order) + bias[m] (nullable), rows of ld_y
+__global__ void sum_slices_kernel(const float *p, int S, int64_t stride, const float *bias, int64_t N, int M, float *y,
+                                  int64_t ld_y) {
+    const int64_t q = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int mq = M / 4;
+    if (q >= N * mq) return;
+    const int64_t n = q / mq;
+    const int m = (int) (q - n * mq) * 4;
+    const float *src = p + n * M + m;
+    f32x4 v = *(const f32x4 *) src;
+    for (int z = 1; z < S; ++z) {
+        const f32x4 a = *(const f32x4 *) (src + z * stride);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += a[e];
+    }
+    if (bias) {
+        const f32x4 b = *(const f32x4 *) (bias + m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += b[e];
+    }
+    *(f32x4 *) (y + n * ld_y + m) = v;
 }
 
 // Convolution with few output channels (the VAE's final k7, 128 -> 2
@@ -1236,6 +1291,15 @@ hipError_t launch_cast_rows_bf16(const float *x, int64_t ld_x, int64_t ld_b, int
     return hipGetLastError();
 }
 
+hipError_t launch_cast_rows_split3(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows, int cols,
+                                   uint16_t *y, hipStream_t s) {
+    if (rows < 1 || cols < 4 || cols % 4 || rows_per_b < 1 || ld_x % 4 || ld_b % 4) return hipErrorInvalidValue;
+    const int64_t n = rows * (cols / 4);
+    launch_kernel(cast_rows_split3_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, ld_x, ld_b, rows_per_b, rows,
+                  cols, y);
+    return hipGetLastError();
+}
+
 hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
                             hipStream_t s) {
     const int64_t total = (int64_t) KW * IC * OC;
@@ -1282,6 +1346,16 @@ hipError_t launch_silu_mul_slices(const float *a, const float *b, int S, int64_t
                                   hipStream_t s) {
     if (S < 1 || (S > 1 && stride < n)) return hipErrorInvalidValue;
     launch_kernel(silu_mul_slices_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, a, b, S, stride, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_slices(const float *p, int S, int64_t stride, const float *bias, int64_t N, int M, float *y,
+                             int64_t ld_y, hipStream_t s) {
+    if (S < 1 || N < 1 || M < 4 || M % 4 || ld_y % 4 || stride % 4 || (S > 1 && stride < N * M) ||
+        ((uintptr_t) p & 15) || ((uintptr_t) y & 15) || (bias && ((uintptr_t) bias & 15)))
+        return hipErrorInvalidValue;
+    const int64_t n = N * (M / 4);
+    launch_kernel(sum_slices_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, S, stride, bias, N, M, y, ld_y);
     return hipGetLastError();
 }
 

@@ -78,6 +78,8 @@ void read_tuning() {
     t.attn_vrows = env_int("TSK_ATTN_VROWS", 1);
     t.f32_dl = env_int("TSK_F32_DL", 1);
     t.f32_dl_ns = env_int("TSK_F32_DL_NS", 2);
+    t.f32_split = env_int("TSK_F32_SPLIT", 1);
+    t.split_wg = env_int("TSK_SPLIT_WG", 512);
     t.l2_prefetch = env_int("TSK_L2PF", -1);
     // two digits: split-K of linear1 and of ffn.fc2 in the DiT driver
     if (const char *ks = getenv("TSK_KSPLIT"))

@@ -384,6 +384,9 @@ hipError_t launch_im2col_1d(const float *x, int64_t sp, int64_t sc, int64_t sn, 
 // x + b * ld_b + i * ld_x (element strides, multiples of 4; cols % 4 == 0)
 hipError_t launch_cast_rows_bf16(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows, int cols,
                                  uint16_t *y, hipStream_t s);
+// f32 rows as [hi | hi | lo] bf16 planes, 3 cols per row (split products of F32 weights)
+hipError_t launch_cast_rows_split3(const float *x, int64_t ld_x, int64_t ld_b, int rows_per_b, int64_t rows, int cols,
+                                   uint16_t *y, hipStream_t s);
 // conv kernel [KW, IC, OC] of es-byte elements (element strides s0..s2) ->
 // kw-major rows dst[oc][kw * IC + ic]
 hipError_t launch_conv_pack(const void *w, int es, int64_t s0, int64_t s1, int64_t s2, int KW, int IC, int OC, void *dst,
@@ -404,6 +407,10 @@ struct F32Snake {
 hipError_t launch_gemm_f32(const GemmProblem &p, int y_bf16, hipStream_t s, const F32Snake *snake = nullptr);
 // y = silu(a) * b, f32, n elements
 hipError_t launch_silu_mul(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
+// y[n][m] = sum of S K-split slices p[z][n][m] (rows of M, slices `stride` apart, summed in order)
+// + bias[m] (nullable), into rows of ld_y; M, ld_y, stride multiples of 4, 16-byte aligned
+hipError_t launch_sum_slices(const float *p, int S, int64_t stride, const float *bias, int64_t N, int M, float *y,
+                             int64_t ld_y, hipStream_t s);
 // the same with a and b each the sum of S K-split slices (stride elements apart, summed in order)
 hipError_t launch_silu_mul_slices(const float *a, const float *b, int S, int64_t stride, float *y, int64_t n,
                                   hipStream_t s);

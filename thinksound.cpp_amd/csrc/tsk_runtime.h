@@ -40,6 +40,9 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_ATTN_Q8   Q8_0 driver: the attention writes linear1's Q8_0 activations itself (1), or f32 + quantize (0)
 //   TSK_F32_DL / TSK_F32_DL_NS  F32 GEMM with direct global -> LDS loads (1, default; 0 = register staged)
 //                 and its ring depth (2, default; 3)
+//   TSK_F32_SPLIT reference graph: F32 matrices as three bf16 products (1, default; read when a model is
+//                 created, which then holds the split copies) or fp32 MFMA products (0, read on every call)
+//   TSK_SPLIT_WG  most 128 x 128 tiles times K slices of a split product's launch (512)
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
@@ -61,6 +64,8 @@ struct Tuning {
     int q8_qkv_fused = 1;
     int f32_dl = 1;
     int f32_dl_ns = 2;
+    int f32_split = 1;
+    int split_wg = 512;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
     bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:
