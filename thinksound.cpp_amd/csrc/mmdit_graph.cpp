@@ -403,8 +403,12 @@ int conv_splits(const tsk_mmdit *m, const Conv &C, int S) {
     return sp;
 }
 
+int conv_plain(tsk_mmdit *m, const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad,
+               float *y, int64_t ld_y, bool bias, hipStream_t s);
+
 // convmlp / mlp (src/mmdit.cpp:39-52): y = w2(silu(w1 x) * w3 x), the hidden
-// state bf16 in m->hid (the conversion w2's mul_mat applies to it)
+// state bf16 in m->hid (the conversion w2's mul_mat applies to it); w2 into
+// residual slices (splits > 1) or plain rows
 int conv_mlp(tsk_mmdit *m, const Conv &w1, const Conv &w3, const Conv &w2, const uint16_t *x, int64_t ld_x, int64_t xb,
              int IW, int B, float *y, int64_t ld_y, hipStream_t s, int splits = 1) {
     GemmGroup g;
@@ -418,6 +422,7 @@ int conv_mlp(tsk_mmdit *m, const Conv &w1, const Conv &w3, const Conv &w2, const
     q.conv_ic = w1.IC; q.conv_iw = IW; q.conv_ow = IW; q.conv_s = 1; q.conv_p = 1; q.conv_d = 1;
     int rc = hipcheck(launch_gemm_coop(g, EPI_SWIGLU_BF16, s), "mmdit convmlp w1/w3");
     if (rc) return rc;
+    if (splits == 1) return conv_plain(m, w2, m->hid, w1.OC, (int64_t) IW * w1.OC, IW, B, 1, y, ld_y, false, s);
     return conv(w2, m->hid, w1.OC, (int64_t) IW * w1.OC, IW, B, 1, y, ld_y, false, s, true, splits);
 }
 
@@ -495,6 +500,26 @@ int split_slices(const tsk_mmdit *m, int M, int K, int S, int most = PART_SLICES
     return sp;
 }
 constexpr int SPLIT_SUM_MAX = 16;   // slices of a split convolution summed into a plain output
+// A BF16 convolution into plain f32 rows (y = conv(x) + b): over few tiles
+// with a long K (the input projections' convMLP w2, K = 8448 over 112
+// workgroups at 9 s; the final k7 convolution, 64 outputs, 7 workgroups) as
+// K-split slices in m->part, summed with the bias by sum_slices_kernel. Only
+// between blocks: no residual partial sums are pending in m->part then.
+int conv_plain(tsk_mmdit *m, const Conv &C, const uint16_t *x, int64_t ld_x, int64_t xb, int IW, int B, int pad,
+               float *y, int64_t ld_y, bool bias, hipStream_t s) {
+    const int OW = IW + 2 * pad - (C.KW - 1), N = B * OW;
+    const int64_t rows3 = (int64_t) m->cfg.max_batch * (m->cfg.max_latent + m->cfg.max_clip + 2 * m->cfg.text_seq);
+    const size_t cap = (size_t) PART_SLICES * rows3 * m->cfg.hidden;   // floats of m->part
+    const int most = (int) std::min<size_t>(SPLIT_SUM_MAX, cap / ((size_t) m->cfg.max_batch * OW * C.OC));
+    const int sp = C.OC % 4 == 0 && ld_y % 4 == 0 && ((uintptr_t) y & 15) == 0
+                       ? split_slices(m, C.OC, C.KW * C.IC, OW, most) : 1;
+    if (sp == 1) return conv(C, x, ld_x, xb, IW, B, pad, y, ld_y, false, s, !bias);
+    int rc = conv(C, x, ld_x, xb, IW, B, pad, m->part, C.OC, false, s, true, sp);
+    if (rc) return rc;
+    return hipcheck(launch_sum_slices(m->part, sp, (int64_t) N * C.OC, bias ? C.b : nullptr, N, C.OC, y, ld_y, s),
+                    "mmdit conv slices");
+}
+
 // K slices of a residual-branch convolution on the f32 path (summed by the
 // next LayerNorm): F32 kernels as fp32 products by f32_splits, as split
 // products by split_slices; BF16 kernels unsplit
@@ -1500,8 +1525,8 @@ int prep_cond(tsk_mmdit *m, const Call &k, hipStream_t st) {
                            m->clip0, H, st)))
             return rc;
         // sync: conv k7 (padding 3) -> silu -> convMLP (:168-177)
-        if ((rc = conv(conv_of(m, "sync_input_proj.0", true), k.sync16, c.sync_dim, (int64_t) k.sync_S * c.sync_dim,
-                       k.sync_S, B, 3, m->tmp32, H, false, st)) ||
+        if ((rc = conv_plain(m, conv_of(m, "sync_input_proj.0", true), k.sync16, c.sync_dim,
+                             (int64_t) k.sync_S * c.sync_dim, k.sync_S, B, 3, m->tmp32, H, true, st)) ||
             (rc = hipcheck(launch_silu_bf16(m->tmp32, a16, (int64_t) B * k.sync_S * H, st), "silu")) ||
             (rc = conv_mlp(m, conv_of(m, "sync_input_proj.2.w1", false), conv_of(m, "sync_input_proj.2.w3", false),
                            conv_of(m, "sync_input_proj.2.w2", false), a16, H, (int64_t) k.sync_S * H, k.sync_S, B,
@@ -1700,7 +1725,7 @@ int step(tsk_mmdit *m, const Call &k, const float *t, float *flow, hipStream_t s
     if ((rc = run_ln(m, &Ls, 1, B, 0, st)) || (rc = capture())) return rc;
     if ((rc = grab(m, "after_fused", m->lat, (size_t) B * T * H, st))) return rc;
     const Conv fc = conv_of(m, "final_layer.conv", true);
-    if (m->fast) return conv(fc, (const uint16_t *) Ls.xn, H, (int64_t) T * H, T, B, 3, flow, L, false, st);
+    if (m->fast) return conv_plain(m, fc, (const uint16_t *) Ls.xn, H, (int64_t) T * H, T, B, 3, flow, L, true, st);
     return g_conv(m, fc, (const float *) Ls.xn, H, (int64_t) T * H, T, B, 3, flow, L, true, st);
 }
 
