@@ -393,9 +393,10 @@ def vae_bench(tsk, reps=3):
     preserving), latent resident in HBM; HIP events around `reps` decodes"""
     import numpy as np
     v = tsk.Vae(tsk.vae_config(max_latent=646))
-    for k, w in tsk.vae_synthetic_weights(v.tensors(), seed=77, snake_std=0.1).items():
+    weights = tsk.vae_synthetic_weights(v.tensors(), seed=77, snake_std=0.1)
+    for k, w in weights.items():
         v.set_tensor(k, w)
-    out = {}
+    out, ref_audio = {}, {}
     rng = np.random.default_rng(4242)
     for label, T in (("9s", 194), ("30s", 646)):
         lat = tsk.to_device(rng.standard_normal((64, T), dtype=np.float32))
@@ -414,6 +415,38 @@ def vae_bench(tsk, reps=3):
         out[label] = {"ms": round(ms, 3), "latent_frames": T, "samples": T * v.hop,
                       "realtime_factor": round(T * v.hop / 44100.0 / (ms / 1e3), 1),
                       "tflops": round(tf, 1), "frac_of_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4)}
+        ref_audio[label] = (lat, audio.numpy().astype(np.float64))
+    # the opt-in split products (TSK_VAE_SPLIT=1 at creation): the same decode
+    # with every convolution but the output one as three bf16 products
+    os.environ["TSK_VAE_SPLIT"] = "1"
+    tsk.init(0, reread=True)
+    try:
+        vs = tsk.Vae(tsk.vae_config(max_latent=646))
+        for k, w in weights.items():
+            vs.set_tensor(k, w)
+        split = {}
+        for label, T in (("9s", 194), ("30s", 646)):
+            lat, a64 = ref_audio[label]
+            audio = tsk.empty((2, T * vs.hop))
+            vs.decode_device(lat, audio)
+            tsk.synchronize()
+            s, e = tsk.Event(), tsk.Event()
+            s.record()
+            for _ in range(reps):
+                vs.decode_device(lat, audio)
+            e.record()
+            tsk.synchronize()
+            ms = s.elapsed_ms(e) / reps
+            d = audio.numpy().astype(np.float64) - a64
+            split[label] = {"ms": round(ms, 3), "realtime_factor": round(T * vs.hop / 44100.0 / (ms / 1e3), 1),
+                            "rel_l2_vs_fp32_products": float(np.sqrt((d ** 2).sum() / (a64 ** 2).sum()))}
+        split["note"] = ("TSK_VAE_SPLIT=1: F32 products as three bf16 products (weight planes [hi | lo | hi] x "
+                         "input planes [hi | hi | lo]); the default decode above uses fp32 MFMA products")
+        out["split_products"] = split
+        vs.close()
+    finally:
+        os.environ.pop("TSK_VAE_SPLIT", None)
+        tsk.init(0, reread=True)
     v.close()
     return out
 

@@ -85,3 +85,38 @@ def test_vae_reference_channels(env):
     with pytest.raises(tsk.TskError):
         v.decode(np.zeros((64, 17), np.float32))          # beyond max_latent
     v.close()
+
+
+def test_vae_split_products(env, monkeypatch):
+    """The opt-in split products (TSK_VAE_SPLIT=1 when the model is created:
+    every convolution but the output one as three bf16 products over weight
+    planes [hi | lo | hi] and input planes [hi | hi | lo], which the previous
+    convolution's epilogue writes with its SnakeBeta): about 2^-17 of |x w|
+    per term, which the decoder amplifies 50-100 times on its way to the audio
+    (fp32 products: ~6e-5 from the oracle), so the audio is held to 1e-3;
+    TSK_VAE_SPLIT=0 on the same model (read on every call) is the fp32 path
+    again, held to TOL. The split planes' layout is checked by the same
+    comparison: a plane in the wrong place moves the audio by O(1)."""
+    tsk, orc = env
+    monkeypatch.setenv("TSK_VAE_SPLIT", "1")
+    tsk.init(0, reread=True)
+    try:
+        v, ov = build_pair(tsk, orc, max_latent=16)
+        for T, seed in ((3, 3), (16, 4)):
+            lat = np.random.default_rng(seed).standard_normal((64, T)).astype(np.float32)
+            r = ov.decode(lat)
+            a = v.decode(lat)
+            assert np.isfinite(a).all() and np.array_equal(v.decode(lat), a)
+            e = rel_l2(a, r)
+            monkeypatch.setenv("TSK_VAE_SPLIT", "0")
+            tsk.init(0, reread=True)
+            ex = rel_l2(v.decode(lat), r)
+            monkeypatch.setenv("TSK_VAE_SPLIT", "1")
+            tsk.init(0, reread=True)
+            print(f"VAE (reference channels) T={T}: split products rel-L2 {e:.3e}, fp32 products {ex:.3e}",
+                  flush=True)
+            assert e <= 1e-3 and ex <= TOL
+        v.close()
+    finally:
+        monkeypatch.delenv("TSK_VAE_SPLIT", raising=False)
+        tsk.init(0, reread=True)

@@ -812,6 +812,53 @@ __device__ __forceinline__ void gemm_ks_tile(const GemmProblem &p, const Coord t
                 for (int e = 0; e < 4; ++e) { o[e] += b0[e]; o[4 + e] += b1[e]; }
             if constexpr (EPI == EPI_GELU_BF16)
                 for (int e = 0; e < 8; ++e) o[e] = gelu_tanh_f(o[e]);
+            if constexpr (EPI == EPI_F32X) {
+                // + the old y, then the SnakeBeta (the reference's order mul,
+                // sin, sqr, mul, add) into y2, the split planes or y itself
+                float *yr = p.y ? (float *) p.y + (int64_t) n * p.ld_y + m : nullptr;
+                if (p.accumulate) {
+                    const f32x4 a0 = *(const f32x4 *) yr, a1 = *(const f32x4 *) (yr + 4);
+                    for (int e = 0; e < 4; ++e) { o[e] += a0[e]; o[4 + e] += a1[e]; }
+                }
+                if (p.snk_ea) {
+                    const int P = p.snk_period, c0 = m % P;
+                    const f32x4 ea0 = *(const f32x4 *) (p.snk_ea + c0), ea1 = *(const f32x4 *) (p.snk_ea + c0 + 4);
+                    const f32x4 eb0 = *(const f32x4 *) (p.snk_eb + c0), eb1 = *(const f32x4 *) (p.snk_eb + c0 + 4);
+                    const float ea[8] = {ea0[0], ea0[1], ea0[2], ea0[3], ea1[0], ea1[1], ea1[2], ea1[3]};
+                    const float eb[8] = {eb0[0], eb0[1], eb0[2], eb0[3], eb1[0], eb1[1], eb1[2], eb1[3]};
+                    float sv[8];
+                    for (int e = 0; e < 8; ++e) {
+                        const float sn = sinf(o[e] * ea[e]);
+                        sv[e] = o[e] + (sn * sn) * eb[e];
+                    }
+                    if (p.yp) {
+                        uint16_t hi[8], lo[8];
+                        for (int e = 0; e < 8; ++e) {
+                            hi[e] = f32_to_bf16_bits(sv[e]);
+                            const float hf = bf16_bits_to_f32(hi[e]);
+                            lo[e] = __builtin_isfinite(hf) ? f32_to_bf16_bits(sv[e] - hf) : (uint16_t) 0;
+                        }
+                        u32x4 wh, wl;
+                        __builtin_memcpy(&wh, hi, 16);
+                        __builtin_memcpy(&wl, lo, 16);
+                        uint16_t *pr = p.yp + (int64_t) n * 3 * p.ld_y + (int64_t) (m / P) * 3 * P + c0;
+                        *(u32x4 *) pr = wh;
+                        *(u32x4 *) (pr + P) = wh;
+                        *(u32x4 *) (pr + 2 * P) = wl;
+                    } else if (p.y2) {
+                        float *y2r = p.y2 + (int64_t) n * p.ld_y + m;
+                        *(f32x4 *) y2r = f32x4{sv[0], sv[1], sv[2], sv[3]};
+                        *(f32x4 *) (y2r + 4) = f32x4{sv[4], sv[5], sv[6], sv[7]};
+                    } else {
+                        for (int e = 0; e < 8; ++e) o[e] = sv[e];
+                    }
+                }
+                if (yr) {
+                    *(f32x4 *) yr = f32x4{o[0], o[1], o[2], o[3]};
+                    *(f32x4 *) (yr + 4) = f32x4{o[4], o[5], o[6], o[7]};
+                }
+                continue;
+            }
             if constexpr (EPI == EPI_STORE_BF16 || EPI == EPI_GELU_BF16) {
                 uint16_t t8[8];
                 for (int e = 0; e < 8; ++e) t8[e] = f32_to_bf16_bits(o[e]);
@@ -892,6 +939,9 @@ hipError_t conv_epi(GemmGroup &g, int epi, hipStream_t s) {
         case EPI_SWIGLU_F32: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_F32, 1, CONV>(g, s);
         case EPI_SWIGLU_BF16: return ks_launch<TM, TN, R, MODE, EPI_SWIGLU_BF16, 1, CONV>(g, s);
         case EPI_PARTIAL: return ks_launch<TM, TN, R, MODE, EPI_PARTIAL, 1, CONV>(g, s);
+        case EPI_F32X:
+            if constexpr (MODE == MODE_COOP64) return ks_launch<TM, TN, R, MODE, EPI_F32X, 1, CONV>(g, s);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
@@ -913,6 +963,12 @@ hipError_t launch_gemm_coop(GemmGroup &g, int epi, hipStream_t s) {
         if (p.w_tiled && epi_swiglu(epi)) return hipErrorInvalidValue;
         if (epi_swiglu(epi) && (!p.w3 || p.bias || p.M % 8)) return hipErrorInvalidValue;
         if (p.ld_x % 8 || ((uintptr_t) p.x & 15)) return hipErrorInvalidValue;
+        if (epi == EPI_F32X && (p.M % 8 || p.ld_y % 8 || ((uintptr_t) p.y & 15) || (p.bias && ((uintptr_t) p.bias & 15)) ||
+                                (p.accumulate && !p.y) ||
+                                (p.snk_ea && (p.snk_period < 8 || p.snk_period % 8 || !p.snk_eb ||
+                                              ((uintptr_t) p.snk_ea & 15) || ((uintptr_t) p.snk_eb & 15) ||
+                                              ((uintptr_t) p.y2 & 15) || ((uintptr_t) p.yp & 15)))))
+            return hipErrorInvalidValue;
         if (conv && (p.conv_ic % 32 || p.K % p.conv_ic || p.x_group_rows || p.conv_ow < 1 || p.conv_iw < 1 ||
                      p.conv_s < 1 || p.conv_d < 1 || p.conv_p < 0 || p.N % p.conv_ow || p.x_group_stride % 8))
             return hipErrorInvalidValue;

@@ -80,6 +80,7 @@ void read_tuning() {
     t.f32_dl_ns = env_int("TSK_F32_DL_NS", 2);
     t.f32_split = env_int("TSK_F32_SPLIT", 1);
     t.split_wg = env_int("TSK_SPLIT_WG", 512);
+    t.vae_split = env_int("TSK_VAE_SPLIT", 0);
     t.l2_prefetch = env_int("TSK_L2PF", -1);
     // two digits: split-K of linear1 and of ffn.fc2 in the DiT driver
     if (const char *ks = getenv("TSK_KSPLIT"))

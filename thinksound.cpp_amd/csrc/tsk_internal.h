@@ -189,7 +189,8 @@ enum GroupEpi : int {
     // SwiGLU over two weights sharing X: y[n, m] = silu(X W[m]) * (X W3[m]),
     // no bias (convmlp / mlp, src/mmdit.cpp:39-52)
     EPI_SWIGLU_F32 = 15,
-    EPI_SWIGLU_BF16 = 16
+    EPI_SWIGLU_BF16 = 16,
+    EPI_F32X = 17         // y f32 = acc + bias (+ y), SnakeBeta into y / y2 / split planes (see GemmProblem)
 };
 enum GemmFlags : int { GEMM_X_F32 = 1 };
 
@@ -223,6 +224,16 @@ struct GemmProblem {
     float theta_scale, freq_scale, eps;
     float q_scale;                 // q is multiplied by this before its fp16 cast
     const float *rope_cs;          // launch_gemm_ks: (cos, sin) of pair i at position s: [s * 64 + 2 i]
+    // EPI_F32X (split products of F32 weights): y f32 = acc + bias, plus the
+    // old y with accumulate (y nullable: not written), then optionally a
+    // SnakeBeta (snk_ea non-null; channel m % snk_period, ea = exp(alpha),
+    // eb = exp(-beta)) into y2 (f32, row stride ld_y) or yp (bf16 split
+    // planes, rows of 3 ld_y: period group g of a row at 3 g snk_period holds
+    // hi | hi | lo of its channels), else in place of y
+    const float *snk_ea, *snk_eb;
+    int snk_period;
+    float *y2;
+    uint16_t *yp;
     // filled by the launchers
     int tiles_m, tiles_n, block_begin;
     int kt_split;                  // 32-wide k tiles per split (launch_gemm_ks)

@@ -43,6 +43,8 @@ int workspace(hipStream_t s, size_t bytes, void **out);
 //   TSK_F32_SPLIT reference graph: F32 matrices as three bf16 products (1, default; read when a model is
 //                 created, which then holds the split copies) or fp32 MFMA products (0, read on every call)
 //   TSK_SPLIT_WG  most 128 x 128 tiles times K slices of a split product's launch (512)
+//   TSK_VAE_SPLIT VAE decoder: F32 products as three bf16 ones (1; read when a model is created, which then
+//                 holds the split copies) or fp32 MFMA products (0, default; read on every call)
 struct Tuning {
     int q8_cfg = 0;
     bool q8_old = false;
@@ -66,6 +68,7 @@ struct Tuning {
     int f32_dl_ns = 2;
     int f32_split = 1;
     int split_wg = 512;
+    int vae_split = 0;
     int ksplit_out = 2, ksplit_fc2 = 4;   // DiT split-K of linear1 / ffn.fc2 (1..4)
     bool ksplit_set = false;              // TSK_KSPLIT given: the two counts hold at every size
     int l2_prefetch = -1;                 // DiT LN kernels fetch the next projections' weights into L2:

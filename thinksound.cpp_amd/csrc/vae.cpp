@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "../../include/tsk/tsk.h"
+#include "host_convert.h"
 #include "tsk_internal.h"
 #include "tsk_runtime.h"
 
@@ -45,6 +46,7 @@ struct VW {
     int stride;             // ct: the stride s
     size_t offset;          // device float offset of the prepared layout
     size_t count;           // floats stored
+    size_t offset16;        // split products: bf16 offset of the planes (3 count: [hi | lo | hi] per IC group)
 };
 
 }  // namespace
@@ -58,6 +60,14 @@ struct tsk_vae {
     float *lat = nullptr;                          // latent rows [T][latent_dim]
     size_t act_cap = 0;
     int hop = 1;
+    // F32 products as three bf16 ones (opt-in, TSK_VAE_SPLIT=1 when the model
+    // is created; every channel count a multiple of 64): the kernels' split
+    // planes, and the activations the convolutions read as split planes
+    // [T][3 C] (two buffers and the latent)
+    bool split = false;
+    uint16_t *blob16 = nullptr;
+    uint16_t *ap[2] = {nullptr, nullptr};
+    uint16_t *latp = nullptr;
 };
 
 namespace {
@@ -72,7 +82,7 @@ void addv(tsk_vae *v, const std::string &name, int64_t a, int64_t b, int64_t c, 
     x.conv = conv;
     x.ct = ct;
     x.stride = stride;
-    x.offset = 0;
+    x.offset = x.offset16 = 0;
     // prepared layouts: conv kw-major [OC][K * IC]; transposed conv the merged
     // 3-tap kernel [s * OC][3 * IC] and its bias replicated [s * OC]
     x.count = ct ? (size_t) stride * c * 3 * b : (size_t) (a * b * c);
@@ -173,6 +183,94 @@ int conv_t(const tsk_vae *v, const std::string &p, const float *x, int IC, int T
     return TSK_OK;
 }
 
+// ---- split products: the cooperative bf16 GEMM over 3 IC (weight planes
+// [hi | lo | hi] against input planes [hi | hi | lo]: x w up to x_lo w_lo and
+// the lo roundings, ~2^-17 of |x w| per term) with the EPI_F32X epilogue:
+// bias, the residual update, and the SnakeBeta `snake` (parameters of
+// period C) into the split planes yp the next convolution reads, or into an
+// f32 y2 (the final snake, for the fp32 output convolution)
+struct SplitOut {
+    float *y;           // f32 output rows (nullable: not written)
+    bool accumulate;    // y += conv
+    const char *snake;  // SnakeBeta parameters' prefix, or null
+    int C;              // its period (channels)
+    float *y2;          // the snake as f32 rows
+    uint16_t *yp;       // the snake as split planes
+};
+
+void set_out(const tsk_vae *v, GemmProblem &q, const SplitOut &o) {
+    q.y = o.y;
+    q.accumulate = o.accumulate ? 1 : 0;
+    if (o.snake) {
+        q.snk_ea = wp(v, std::string(o.snake) + ".alpha");
+        q.snk_eb = wp(v, std::string(o.snake) + ".beta");
+        q.snk_period = o.C;
+        q.y2 = o.y2;
+        q.yp = o.yp;
+    }
+}
+
+int conv_split(const tsk_vae *v, const std::string &p, const uint16_t *xp, int IC, int T_in, int pad, int dil,
+               const SplitOut &o, hipStream_t s) {
+    const VW &w = wi(v, p + ".weight");
+    const int KW = (int) w.ne[0], OC = (int) w.ne[2];
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = xp; q.ld_x = 3 * IC;
+    q.w = v->blob16 + w.offset16; q.ld_w = (int64_t) KW * 3 * IC;
+    q.bias = wp(v, p + ".bias");
+    q.ld_y = OC;
+    const int T_out = T_in + 2 * pad - dil * (KW - 1);
+    q.M = OC; q.N = T_out; q.K = KW * 3 * IC; q.splits = 1;
+    if (KW > 1 || pad) {
+        q.conv_ic = 3 * IC; q.conv_iw = T_in; q.conv_ow = T_out; q.conv_s = 1; q.conv_p = pad; q.conv_d = dil;
+    }
+    set_out(v, q, o);
+    return hipcheck(launch_gemm_coop(g, EPI_F32X, s), "vae split conv");
+}
+
+// the transposed convolution of conv_t over the split planes: the merged
+// kernel's planes [s OC][3 taps][3 IC], its two-tap phase groups
+int conv_t_split(const tsk_vae *v, const std::string &p, const uint16_t *xp, int IC, int T_in, const SplitOut &o,
+                 hipStream_t s) {
+    const VW &w = wi(v, p + ".weight");
+    const int OC = (int) w.ne[2], st = w.stride;
+    const uint16_t *wq = v->blob16 + w.offset16;
+    const float *bias = wp(v, p + ".bias");
+    const int ra = ct_split_phase(w.ne[0], st);
+    GemmGroup g;
+    memset(&g, 0, sizeof(g));
+    g.nprob = 1;
+    GemmProblem &q = g.p[0];
+    q.x = xp; q.ld_x = 3 * IC;
+    q.ld_w = (int64_t) 9 * IC;
+    q.ld_y = (int64_t) st * OC;
+    q.N = T_in; q.splits = 1;
+    q.conv_ic = 3 * IC; q.conv_iw = T_in; q.conv_ow = T_in; q.conv_s = 1; q.conv_d = 1;
+    set_out(v, q, o);
+    if (ra < 0) {
+        q.w = wq; q.bias = bias;
+        q.M = st * OC; q.K = 9 * IC; q.conv_p = 1;
+        return hipcheck(launch_gemm_coop(g, EPI_F32X, s), "vae split transposed conv");
+    }
+    for (int gi = 0; gi < 2; ++gi) {
+        const int r0 = gi ? ra : 0, r1 = gi ? st : ra;
+        if (r1 <= r0) continue;
+        const int64_t row0 = (int64_t) r0 * OC;
+        q.w = wq + row0 * 9 * IC + (gi ? 3 * IC : 0);   // taps 1, 2 for the second group
+        q.bias = bias + row0;
+        q.y = o.y ? o.y + row0 : nullptr;
+        q.y2 = o.y2 ? o.y2 + row0 : nullptr;
+        q.yp = o.yp ? o.yp + 3 * row0 : nullptr;          // row0 is a multiple of the period OC
+        q.M = (r1 - r0) * OC; q.K = 6 * IC; q.conv_p = gi ? 0 : 1;
+        const int rc = hipcheck(launch_gemm_coop(g, EPI_F32X, s), "vae split transposed conv");
+        if (rc) return rc;
+    }
+    return TSK_OK;
+}
+
 int validate(const tsk_vae_config *c) {
     if (!c) return fail(TSK_ERR_INVALID_ARG, "cfg is NULL");
     if (c->latent_dim < 4 || c->latent_dim % 4 || c->channels < 4 || c->channels % 4 || c->out_channels < 1 ||
@@ -205,6 +303,10 @@ extern "C" void tsk_vae_destroy(tsk_vae *v) {
     for (float *a : v->act)
         if (a) (void) hipFree(a);
     if (v->lat) (void) hipFree(v->lat);
+    if (v->blob16) (void) hipFree(v->blob16);
+    for (uint16_t *a : v->ap)
+        if (a) (void) hipFree(a);
+    if (v->latp) (void) hipFree(v->latp);
     delete v;
 }
 
@@ -260,6 +362,25 @@ extern "C" int tsk_vae_create(const tsk_vae_config *cfg, tsk_vae **out) {
         off += (x.count + 63) & ~(size_t) 63;
     }
     v->act_cap = (size_t) c.max_latent * (size_t) max_ch_t;
+    // split products (opt-in) when every convolution's channels fit the
+    // cooperative bf16 GEMM's 64-wide stages over 3 IC (the final k7 stays
+    // fp32 products). The decoder amplifies a product's relative error about
+    // 50-100 times on its way to the audio: split products (~2^-17 per term)
+    // leave the audio ~5e-4 rel-L2 from fp32 products (fp32 ones: ~6e-5 from
+    // an fp64 decode), 1.6-1.7 times faster
+    v->split = tuning().vae_split && c.latent_dim % 64 == 0;
+    for (int n = 0; n < 5; ++n) {
+        int ci, co, st;
+        block_dims(c, n, &ci, &co, &st);
+        v->split = v->split && ci % 64 == 0 && co % 64 == 0;
+    }
+    size_t off16 = 0;
+    if (v->split)
+        for (auto &x : v->w)
+            if ((x.conv || x.ct) && x.name != "decoder.layers.7.weight") {
+                x.offset16 = off16;
+                off16 += (3 * x.count + 127) & ~(size_t) 127;
+            }
     auto alloc = [&](void **p, size_t bytes) -> int {
         hipError_t e = hipMalloc(p, bytes);
         if (e != hipSuccess) return fail(TSK_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
@@ -269,7 +390,11 @@ extern "C" int tsk_vae_create(const tsk_vae_config *cfg, tsk_vae **out) {
         (rc = alloc((void **) &v->act[0], sizeof(float) * v->act_cap)) ||
         (rc = alloc((void **) &v->act[1], sizeof(float) * v->act_cap)) ||
         (rc = alloc((void **) &v->act[2], sizeof(float) * v->act_cap)) ||
-        (rc = alloc((void **) &v->lat, sizeof(float) * (size_t) c.max_latent * c.latent_dim))) {
+        (rc = alloc((void **) &v->lat, sizeof(float) * (size_t) c.max_latent * c.latent_dim)) ||
+        (v->split && ((rc = alloc((void **) &v->blob16, 2 * off16)) ||
+                      (rc = alloc((void **) &v->ap[0], 6 * v->act_cap)) ||
+                      (rc = alloc((void **) &v->ap[1], 6 * v->act_cap)) ||
+                      (rc = alloc((void **) &v->latp, 6 * (size_t) c.max_latent * c.latent_dim))))) {
         tsk_vae_destroy(v);
         return rc;
     }
@@ -328,8 +453,27 @@ extern "C" int tsk_vae_set_tensor(tsk_vae *v, const char *name, const float *src
     } else {
         for (int64_t i = 0; i < n; ++i) t[i] = is_alpha ? expf(src[i]) : is_beta ? expf(-src[i]) : src[i];
     }
-    return hipcheck(hipMemcpy(v->blob + x.offset, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice),
-                    "vae set_tensor copy");
+    hipError_t e = hipMemcpy(v->blob + x.offset, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && v->split && (x.conv || x.ct) && x.name != "decoder.layers.7.weight") {
+        // the prepared rows in groups of IC -> [hi | lo | hi] per group,
+        // hi = bf16(w), lo = bf16(w - hi)
+        const size_t G = (size_t) x.ne[1];
+        std::vector<uint16_t> sp(3 * x.count);
+        for (size_t g0 = 0; g0 < x.count; g0 += G)
+            for (size_t i = 0; i < G; ++i) {
+                const float w = t[g0 + i];
+                const uint16_t hi = host_bf16_bits(w);
+                const uint32_t hb = (uint32_t) hi << 16;
+                float hf;
+                memcpy(&hf, &hb, 4);
+                uint16_t *d = &sp[3 * g0 + i];
+                d[0] = hi;
+                d[G] = std::isfinite(hf) ? host_bf16_bits(w - hf) : (uint16_t) 0;
+                d[2 * G] = hi;
+            }
+        e = hipMemcpy(v->blob16 + x.offset16, sp.data(), 2 * sp.size(), hipMemcpyHostToDevice);
+    }
+    return hipcheck(e, "vae set_tensor copy");
 }
 
 namespace {
@@ -346,6 +490,52 @@ int decode_impl(tsk_vae *v, int T, const float *latent_d, float *audio_d, hipStr
     float *x = v->act[0], *sx = v->act[1], *t = v->act[2];
     int in0, out0, s0;
     block_dims(c, 0, &in0, &out0, &s0);
+    if (v->split && tuning().vae_split) {
+        // the same chain on split products: each snake written as the split
+        // planes the next convolution reads (sp, then tp), the residual
+        // stream x f32, the final snake f32 (sx) for the output convolution
+        uint16_t *sp = v->ap[0], *tp = v->ap[1];
+        if ((rc = hipcheck(launch_cast_rows_split3(v->lat, c.latent_dim, 0, T, T, c.latent_dim, v->latp, st),
+                           "vae latent planes")) ||
+            (rc = conv_split(v, "decoder.layers.0", v->latp, c.latent_dim, T, 3, 1,
+                             SplitOut{nullptr, false, "decoder.layers.1.layers.0", in0, nullptr, sp}, st)))
+            return rc;
+        int64_t fr = T;
+        int Cs = in0;
+        const int dl[3] = {1, 3, 9};
+        for (int n = 0; n < 5; ++n) {
+            int ci, co, s;
+            block_dims(c, n, &ci, &co, &s);
+            const std::string bp = "decoder.layers." + std::to_string(n + 1);
+            const std::string sn0 = bp + ".layers.2.layers.0";
+            if ((rc = conv_t_split(v, bp + ".layers.1", sp, ci, (int) fr,
+                                   SplitOut{x, false, sn0.c_str(), co, nullptr, tp}, st)))
+                return rc;
+            std::swap(sp, tp);
+            fr *= s;
+            Cs = co;
+            for (int r = 0; r < 3; ++r) {
+                const std::string rp = bp + ".layers." + std::to_string(r + 2), sn = rp + ".layers.2";
+                if ((rc = conv_split(v, rp + ".layers.1", sp, Cs, (int) fr, 3 * dl[r], dl[r],
+                                     SplitOut{nullptr, false, sn.c_str(), Cs, nullptr, tp}, st)))
+                    return rc;
+                const bool last = n == 4 && r == 2;
+                const std::string np = r < 2 ? bp + ".layers." + std::to_string(r + 3) + ".layers.0"
+                                     : n < 4 ? "decoder.layers." + std::to_string(n + 2) + ".layers.0"
+                                             : std::string("decoder.layers.6");
+                if ((rc = conv_split(v, rp + ".layers.3", tp, Cs, (int) fr, 0, 1,
+                                     SplitOut{x, true, np.c_str(), Cs, last ? sx : nullptr, last ? nullptr : sp}, st)))
+                    return rc;
+            }
+        }
+        const VW &wf7 = wi(v, "decoder.layers.7.weight");
+        if (Cs == 128 && wf7.ne[0] == 7 && c.out_channels == 2)
+            return hipcheck(launch_conv_small_oc(sx, (int) fr, Cs, 7, 2, wp(v, "decoder.layers.7.weight"), nullptr, 3,
+                                                 audio_d, fr, st),
+                            "vae final convolution");
+        if ((rc = conv(v, "decoder.layers.7", false, sx, Cs, (int) fr, 3, 1, t, false, st))) return rc;
+        return hipcheck(launch_transpose_ct(t, 1, (int) fr, c.out_channels, audio_d, st), "vae audio");
+    }
     // conv k7 -> snake of block 1 (the conv's own output is not used again)
     F32Snake sk = snake_epi(v, "decoder.layers.1.layers.0", in0, nullptr);
     if ((rc = conv(v, "decoder.layers.0", true, v->lat, c.latent_dim, T, 3, 1, sx, false, st, &sk))) return rc;
