@@ -32,9 +32,11 @@ def test_f32_attention(env, B, H, N):
 
 
 @pytest.mark.parametrize("B,H,N", [(1, 16, 420), (1, 16, 1040), (1, 16, 194), (1, 16, 646),
-                                   (2, 16, 271), (1, 8, 77)])
+                                   (2, 16, 271), (1, 8, 77), (2, 16, 1040)])
 def test_reference_types_f32q_f16kv(env, B, H, N):
-    """the node mmdit.cpp:88-92 emits: Q F32, K/V cast to F16, prec F32."""
+    """the node mmdit.cpp:88-92 emits: Q F32, K/V cast to F16, prec F32; at
+    B = 2, N = 1040 (the graph's 30 s joint attention) on the 2 x 5 launch
+    shape the rule picks there."""
     tsk, orc = env
     rng = np.random.default_rng(N)
     q = rng.standard_normal((B, H, N, 64)).astype(np.float32)

@@ -195,14 +195,14 @@ def test_stream_pairs_change_no_bits(env, monkeypatch):
         dit.close()
 
 
-@pytest.mark.parametrize("T,cfg", [(194, None), (40, "43"), (40, "24"), (40, "14")])
+@pytest.mark.parametrize("T,cfg", [(194, None), (40, "43"), (40, "24"), (40, "14"), (40, "25")])
 def test_attention_q8_output_bits(env, T, cfg):
     """the attention writing linear1's Q8_0 planes itself (the default) gives
     the bits of its f32 output quantized by the separate kernel
     (TSK_ATTN_Q8=0): joint blocks with a pre_only text stream and the
-    automatic 4 x 1 / 4 x 2 launch shapes (T = 194), and forced 4 x 3, 2 x 4
-    and 1 x 4 shapes (key ranges x query blocks: the Q8_0 block's amax across
-    two waves, one wave's lane pair, a lane pair per 32 dims)"""
+    automatic 4 x 1 / 4 x 2 launch shapes (T = 194), and forced 4 x 3, 2 x 4,
+    1 x 4 and 2 x 5 shapes (key ranges x query blocks: the Q8_0 block's amax
+    across two waves, one wave's lane pair, a lane pair per 32 dims)"""
     import os
     tsk, _ = env
     lat, t, txt = inputs(2, T)

@@ -633,6 +633,7 @@ hipError_t launch_cfg(const AttnFastParams &p, int cfg, hipStream_t s) {
         case 21: return launch_ks_qb<KBF16, BOUNDED, 2, 1, VROWS, Q8>(p, s);
         case 22: return launch_ks_qb<KBF16, BOUNDED, 2, 2, VROWS, Q8>(p, s);
         case 24: return launch_ks_qb<KBF16, BOUNDED, 2, 4, VROWS, Q8>(p, s);
+        case 25: return launch_ks_qb<KBF16, BOUNDED, 2, 5, VROWS, Q8>(p, s);
         case 14: return launch_ks_qb<KBF16, BOUNDED, 1, 4, VROWS, Q8>(p, s);
         default: return hipErrorInvalidValue;
     }
@@ -706,10 +707,19 @@ __global__ __launch_bounds__(256) void vt_transpose16_kernel(const void *v, int 
 // (key ranges, query blocks) per workgroup, from MI355X sweeps over the
 // MM-DiT shapes (B=2, 16 heads, N = 194 .. 1040): 32-row query blocks of all
 // (batch, head) pairs spread over the 256 CUs with 2-3 waves per SIMD
-int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16) {
+int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16, int rule_b) {
     const int qblocks = (Nq + 31) / 32 * H * B;
     // bf16 K: the 4 x 3 instance spills a register to scratch (19.3 us at N =
-    // 723, B = 2 against 20.0-20.5 us for 2 x 4), so it keeps 2 x 4
+    // 723, B = 2 against 20.0-20.5 us for 2 x 4), so it keeps 2 x 4. Where the
+    // 4 x 3 workgroups (one per CU) would take a second round and 2 x 5 ones
+    // fit in one (the reference graph's 30 s joint attention, N = 1040: 352
+    // against 224 workgroups), 2 x 5: 27.2 -> 20.1 us per launch. That choice
+    // changes the key ranges, so it counts the drivers' batch capacity
+    // (rule_b) rather than the call's batch; the query-block choices below
+    // leave every query's sums as they are.
+    const int Bk = rule_b > 0 ? rule_b : B, cus = device_info().cus;
+    if (!k_bf16 && (Nq + 31) / 32 * H * Bk >= 640 && (Nq + 95) / 96 * H * Bk > cus && (Nq + 159) / 160 * H * Bk <= cus)
+        return 25;
     if (qblocks >= 640) return k_bf16 ? 24 : 43;
     if (qblocks >= 256) return 42;
     return 41;
@@ -722,7 +732,7 @@ hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s) {
     if ((int64_t) (p.Nkv - 1) * p.k_nb1 + 128 >= ((int64_t) 1 << 31) || p.k_nb1 < 128 ||
         (!p.v_rows && (int64_t) 128 * p.ldv >= ((int64_t) 1 << 31)))
         return hipErrorInvalidValue;
-    const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.k_bf16);
+    const int cfg = p.force_cfg ? p.force_cfg : attn_fast_default_cfg(p.Nq, p.H, p.B, p.k_bf16, p.rule_b);
     if (p.v_rows) {
         // F16 V rows through the transposing LDS reads: fp16 K; 16-byte
         // aligned rows, 31-bit byte range per (batch, head) like K

@@ -1035,6 +1035,7 @@ int attention(tsk_dit *d, const StreamRun *r, int ns, int B, int Ntot, hipStream
     // 1 % margin for the fp16 rounding of q and k
     p.bounded = 1.01f * (float) c.head_dim * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = d->attn_cfg;
+    p.rule_b = d->cfg.max_batch;
     if (tuning().attn_vrows) {
         // the QKV epilogue (BF16 or Q8_0) wrote V as fp16 rows [B][n_head][Ntot][64] into vt
         p.v_rows = 1;

@@ -858,6 +858,7 @@ int run_attention(tsk_mmdit *m, const Stream *r, int ns, int B, int Ntot, hipStr
     // running max below ATTN_LOGIT_BOUND (1 % margin for the fp16 rounding)
     p.bounded = 1.01f * 64.0f * p.c * aq * ak <= ATTN_LOGIT_BOUND;
     p.force_cfg = tuning().attn_cfg;
+    p.rule_b = m->cfg.max_batch;
     if (tuning().attn_vrows) {
         // the QKV epilogue or scatter wrote V as fp16 rows [B][n_head][Ntot][64] into vt
         p.v_rows = 1;

@@ -84,6 +84,8 @@ struct AttnFastParams {
     int bounded;         // fp16 K only: every |q.k| * c <= ATTN_LOGIT_BOUND (no running max)
     int qtiles;          // set by the launcher
     int force_cfg;       // 0: launcher picks; else 10 * key ranges + query blocks
+    int rule_b;          // > 0: the batch the launcher's shape rule counts with (a model's capacity,
+                         // so that a batch row's key ranges, and so its bits, do not depend on the call's B)
     // > 0: workgroups of head h run on XCD (h / xcd_hdiv) % 8, where a QKV
     // GEMM with xcd_hdiv heads per weight tile wrote that head's q / k / V^T
     // (the launcher drops it unless H is a multiple of 8 * xcd_hdiv); 0: the
@@ -104,7 +106,7 @@ struct AttnFastParams {
 // exp2 of it (~6e3) and sums of it over 2^14 keys stay far inside fp16 / fp32.
 constexpr float ATTN_LOGIT_BOUND = 14.0f;
 hipError_t launch_attn_fast(const AttnFastParams &p, hipStream_t s);
-int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16);
+int attn_fast_default_cfg(int Nq, int H, int B, int k_bf16, int rule_b = 0);
 // V (F16/BF16 rows of 64, ggml strides) -> the transposed fp16 layout above
 hipError_t launch_vt_transpose(const void *v, int v_bf16, int64_t nb1, int64_t nb2, int64_t nb3, int Nkv, int H,
                                int B, uint16_t *vt, int ldv, hipStream_t s);
