@@ -488,9 +488,9 @@ int rows_split3(tsk_mmdit *m, const Rows &src, int N, int K, hipStream_t s) {
 // the graph's convolutions): the most, up to `most`, that keep the 128 x 128
 // tiles times slices within TSK_SPLIT_WG (512; swept 256-1536 on the Q8_0
 // graph: 384-512 best, 9 s 7.26 against 7.57-7.80 ms per forward, 30 s
-// 12.24 against 13.05-13.12); every slice an even number of 32-k tiles. Counted from the rows per batch
-// item times the batch capacity, so that a batch row is summed in the same
-// order whatever the call's batch.
+// 12.24 against 13.05-13.12); every slice an even number of 32-k tiles.
+// Counted from the rows per batch item times the batch capacity, so that a
+// batch row is summed in the same order whatever the call's batch.
 int split_slices(const tsk_mmdit *m, int M, int K, int S, int most = PART_SLICES) {
     const int64_t t = (int64_t) ((M + 127) / 128) * ((S * m->cfg.max_batch + 127) / 128);
     const int kt = K / 32;
